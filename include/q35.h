@@ -1,0 +1,164 @@
+/* libq35 — MI355X (gfx950) decode hot path for the Qwen3.5-2B-class text
+ * decoder, as a plain C ABI.
+ *
+ * Conventions for every entry point:
+ *   - pointers are device pointers; bf16 tensors are raw 16-bit patterns;
+ *   - sizes are element counts; tensors are dense row-major unless a stride
+ *     argument says otherwise;
+ *   - all work is enqueued on `stream` (a hipStream_t passed as void*); no
+ *     entry point synchronises, allocates device memory or reads device data
+ *     on the host, so every call can be captured in a hipGraph;
+ *   - the return value is 0 or a hipError_t code; invalid sizes return
+ *     hipErrorInvalidValue (1) before anything is launched.
+ *   - `*_f32` flags say whether a small parameter vector is fp32 (1) or
+ *     bf16 (0).
+ *
+ * Each declaration names the reference interface it replaces
+ * (PingGuoLiZiJvZi/ppu, paths relative to the repository root).
+ */
+#ifndef Q35_H
+#define Q35_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header; q35_abi_version() must return it. */
+#define Q35_ABI_VERSION 1
+int q35_abi_version(void);
+
+/* ---- norms and elementwise ------------------------------------------- */
+
+/* rms_norm: y = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)), rows x width.
+ * Replaces qwen35_fused/kernels.py:44 (rms_norm, kernel :24-53). */
+int q35_rmsnorm(const void* x, const void* w, int w_f32, void* y, int rows, int width, float eps,
+                void* stream);
+
+/* residual_add_rms_norm: r' = bf16(residual + update); y = rms_norm(r').
+ * Replaces qwen35_fused/kernels.py:85 (kernel :56-112). */
+int q35_residual_rmsnorm(const void* residual, const void* update, const void* w, int w_f32,
+                         void* residual_out, void* y, int rows, int width, float eps,
+                         void* stream);
+
+/* gated_rms_norm: y = bf16(bf16(bf16(rms(x)) * bf16(w)) * silu(gate)).
+ * Replaces qwen35_fused/kernels.py:139 (kernel :115-155). */
+int q35_gated_rmsnorm(const void* x, const void* gate, const void* w, int w_f32, void* y,
+                      int rows, int width, float eps, void* stream);
+
+/* silu_and_mul: out[r, c] = bf16(bf16(silu(p[r, c])) * p[r, width + c]).
+ * Replaces qwen35_fused/kernels.py:170 (kernel :158-180). */
+int q35_silu_mul(const void* packed, void* out, long long rows, int width, void* stream);
+
+/* attention_gate_mul: out = bf16(x * bf16(sigmoid(gate))), gate read from the
+ * packed QGKV row. Replaces qwen35_fused/kernels.py:312 (kernel :285-333). */
+int q35_attn_gate_mul(const void* x, const void* packed, void* out, long long tokens, int hidden,
+                      int packed_stride, int head_dim, void* stream);
+
+/* ---- bf16 GEMV (M = 1) ------------------------------------------------- */
+
+/* y[N] = bf16(W[N,K] . xa) where xa depends on `prologue`:
+ *   0: xa = x;  1: xa = rms_norm(x, norm_w);  2: r' = bf16(x + u), xa = rms_norm(r', norm_w).
+ * residual_out / x_norm_out (optional) receive r' and xa.
+ * Replaces the decode F.linear call sites qwen35_fused/integration.py:185,245,272,298-302,359,
+ * fused with the residual_add_rms_norm of integration.py:478-499. */
+int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_w, int norm_w_f32,
+                  float eps, void* residual_out, void* x_norm_out, void* y, int N, int K,
+                  int prologue, void* stream);
+
+/* y[N] = bf16(bf16(silu(bf16(W[n].xa))) * bf16(W[N+n].xa)), W = [gate; up] of [2N, K];
+ * prologue as q35_gemv_bf16. Replaces qwen35_fused/kernels.py:232 (ppu_swiglu_gemv,
+ * kernel :183-263). */
+int q35_swiglu_gemv(const void* W, const void* x, const void* u, const void* norm_w,
+                    int norm_w_f32, float eps, void* residual_out, void* x_norm_out, void* y,
+                    int N, int K, int prologue, void* stream);
+
+/* ---- lm_head GEMV + top-1 -------------------------------------------- */
+
+/* Workspace slots (8 bytes each) for q35_lm_head_top1. */
+long long q35_lm_head_top1_workspace(int V, int K);
+/* out[0] (int64) = argmax_v bf16(W[v] . x), lowest index on ties; no logits stored.
+ * Replaces qwen35_fused/kernels.py:1146 (lm_head_argmax, kernels :1093-1143). */
+int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace,
+                     long long workspace_slots, void* out, void* stream);
+
+/* ---- DeltaNet --------------------------------------------------------- */
+
+/* causal_conv1d_fused for L == 1: state shift, 4-tap conv, bf16 round, SiLU.
+ * x row stride in_stride >= C. Replaces qwen35_fused/kernels.py:659 (kernel :622-656). */
+int q35_conv1d_update(const void* x, const void* w, void* state, void* out, int B, int C,
+                      int in_stride, int kw, void* stream);
+/* causal_conv1d_fused for L > 1 (zero history; last kw inputs saved to state).
+ * Replaces qwen35_fused/kernels.py:659 (kernel :576-619). */
+int q35_conv1d_prefill(const void* x, const void* w, void* state, void* out, int B, int L, int C,
+                       int in_stride, int kw, void* stream);
+
+/* One decode step of the gated delta rule for all heads (D = 128), state fp32
+ * in place. fuse_conv: src is the raw packed projection and conv1d runs first;
+ * fuse_gnorm: out is the gated RMSNorm of the core output (z from packed).
+ * Replaces qwen35_fused/kernels.py:854 (delta_recurrent_fused, kernel :768-851),
+ * fused with :659 and :139 as integration.py:254-271 chains them. */
+int q35_delta_decode(const void* src, int src_stride, const void* packed, int packed_stride,
+                     const void* conv_w, void* conv_state, int kw, const void* a_log,
+                     const void* dt_bias, int params_f32, void* state, const void* norm_w,
+                     int norm_w_f32, float norm_eps, void* out, int B, int H, int D,
+                     int fuse_conv, int fuse_gnorm, void* stream);
+
+/* Workspace floats for q35_delta_prefill. */
+long long q35_delta_prefill_workspace(int B, int L, int H);
+/* Sequential gated delta rule over L tokens (per-token factors precomputed).
+ * Replaces qwen35_fused/kernels.py:854 with precompute_factors (kernels :713-851). */
+int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
+                      const void* a_log, const void* dt_bias, int params_f32, void* state,
+                      void* out, void* workspace, long long workspace_floats, int B, int L, int H,
+                      int D, void* stream);
+
+/* ---- full attention --------------------------------------------------- */
+
+/* qgkv_norm_rope: per-head Q/K RMSNorm (1 + w), partial RoPE, Q to [B,QH,L,D];
+ * K/V to [B,KVH,L,D], or into the static cache at *cache_start + t when
+ * cache_start (int64 device scalar) is given. Positions outside the cache are
+ * not written. Replaces qwen35_fused/kernels.py:507 (kernel :419-505). */
+int q35_qgkv_norm_rope(const void* packed, const void* q_w, const void* k_w, int w_f32,
+                       const void* cos, const void* sin, void* q_out, void* k_out, void* v_out,
+                       const void* cache_start, int B, int L, int QH, int KVH, int D,
+                       int rotary_dim, int cache_len, void* stream);
+
+/* Split count for a cache capacity (chunk length in *chunk_out). */
+int q35_gqa_decode_splits(int cache_len, int kv_heads, int* chunk_out);
+/* Workspace floats for q35_gqa_decode. */
+long long q35_gqa_decode_workspace(int cache_len, int q_heads, int kv_heads, int D);
+/* gqa_decode_attention over a static cache; valid_len is an int64 device
+ * scalar. With packed_gate (the packed QGKV row) the sigmoid gate of
+ * attention_gate_mul is applied to the bf16 output. out [QH*D] bf16.
+ * Replaces qwen35_fused/kernels.py:1031 (kernels :940-1028), optionally fused
+ * with :312 as integration.py:343-358 chains them. */
+int q35_gqa_decode(const void* q, const void* K, const void* V, const void* valid_len, float scale,
+                   const void* packed_gate, void* out, void* workspace, long long workspace_floats,
+                   int QH, int KVH, int D, int cache_len, void* stream);
+
+/* Causal GQA prefill attention: q [B,QH,L,D], K/V [B,KVH,cache_len,D] holding
+ * the prompt at kv_start; out [B,L,QH*D]. Replaces the prefill
+ * ALL_ATTENTION_FUNCTIONS call of qwen35_fused/integration.py:360-372. */
+int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int B, int QH, int KVH,
+                    int D, int L, int cache_len, int kv_start, float scale, void* stream);
+
+/* ---- A8W8 -------------------------------------------------------------- */
+
+/* Per-output-channel weight quantisation (int8 + fp32 scale).
+ * Replaces explore_runtime_quantization.py:142-155 (PPUA8W8Linear.__init__). */
+int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, void* stream);
+/* Per-token dynamic symmetric int8 quantisation (vLLM scaled_int8_quant rule).
+ * Replaces the call at explore_runtime_quantization.py:167-172. */
+int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, void* stream);
+/* y[M,N] = bf16(int32(xq . Wq) * s_x[m] * s_w[n]); with x (bf16) and M == 1 the
+ * activation quantisation is fused (xq/s_x optional outputs), else xq/s_x are
+ * inputs (or filled from x first). acc_out (optional) gets the int32 sums.
+ * Replaces explore_runtime_quantization.py:161-181 (PPUA8W8Linear.forward). */
+int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void* s_w, void* y,
+                  void* acc_out, int M, int N, int K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q35_H */

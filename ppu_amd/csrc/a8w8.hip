@@ -1,0 +1,259 @@
+// A8W8 linear: per-output-channel symmetric int8 weights, per-token dynamic
+// symmetric int8 activations, exact int32 accumulation with packed int8 dot
+// instructions (v_dot4c_i32_i8 via __builtin_amdgcn_sdot4), dequant fused
+// into the store.
+//
+//   weights  : s_w[n] = absmax_n/127 (1 if absmax_n == 0);
+//              Wq = clamp(round_half_even(W/s_w), -127, 127)
+//              [reference explore_runtime_quantization.py:142-155]
+//   tokens   : s_x[m] = absmax_m/127; xq = sat_int8(rint(x * (127/absmax_m)));
+//              an all-zero row gives xq = 0, s_x = 0. This is the published
+//              dynamic per-token rule of vLLM's scaled_int8_quant(symmetric)
+//              that the reference calls [explore_runtime_quantization.py:167-172].
+//   output   : y[m, n] = bf16((float)acc[m, n] * s_x[m] * s_w[n])
+//
+// GEMV work split: one wave64 owns R weight rows; lane l reads 16 int8 at
+// k = c*1024 + 16l of each row for every chunk c (128-bit loads), so the
+// weight stream is read once; activations (L1/L2 resident) are read per chunk.
+// Bytes per launch = N*K + 4N + M*K + 2MN (+4M).
+#include "q35_common.hpp"
+
+namespace {
+
+// One wave per row: absmax, scale and round-half-even quantisation.
+__global__ __launch_bounds__(256) void quant_weight_rows(const uint16_t* __restrict__ W,
+                                                         int8_t* __restrict__ Wq,
+                                                         float* __restrict__ scale, int N, int K) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const uint16_t* row = W + (size_t)n * K;
+  float mx = 0.f;
+  for (int k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(bf2f(row[k])));
+  mx = wave_max(mx);
+  const float s = mx > 0.f ? mx / 127.0f : 1.0f;
+  for (int k = lane; k < K; k += 64) {
+    float q = rintf(bf2f(row[k]) / s);
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    Wq[(size_t)n * K + k] = (int8_t)(int)q;
+  }
+  if (lane == 0) scale[n] = s;
+}
+
+Q35_DEV int8_t sat_i8(float v) {
+  // rint, then saturate; NaN (0 * inf for a zero row) maps to 0.
+  if (v != v) return 0;
+  const float r = rintf(v);
+  return (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
+}
+
+// One wave per token row.
+__global__ __launch_bounds__(256) void quant_act_rows(const uint16_t* __restrict__ x,
+                                                      int8_t* __restrict__ xq,
+                                                      float* __restrict__ scale, int M, int K) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const uint16_t* row = x + (size_t)m * K;
+  float mx = 0.f;
+  for (int k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(bf2f(row[k])));
+  mx = wave_max(mx);
+  const float inv = 127.0f / mx;
+  for (int k = lane; k < K; k += 64) xq[(size_t)m * K + k] = sat_i8(bf2f(row[k]) * inv);
+  if (lane == 0) scale[m] = mx / 127.0f;
+}
+
+Q35_DEV int dot16(const uint4 a, const uint4 b, int acc) {
+  acc = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, acc, false);
+  return acc;
+}
+
+Q35_DEV int wave_sum_i32(int v) {
+  v += dpp_i<Q35_DPP_QUAD_XOR1>(v);
+  v += dpp_i<Q35_DPP_QUAD_XOR2>(v);
+  v += dpp_i<Q35_DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_i<Q35_DPP_ROW_MIRROR>(v);
+  v += __builtin_amdgcn_ds_swizzle(v, Q35_SWZ_XOR16);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
+}
+
+struct A8Args {
+  const int8_t* Wq;       // [N, K]
+  const float* s_w;       // [N]
+  const int8_t* xq;       // [M, K] (input, or written by block 0 when quantising)
+  const float* s_x;       // [M]
+  const uint16_t* x;      // bf16 [1, K] when the M=1 quantisation is fused
+  int8_t* xq_out;         // fused quant: block 0 stores xq (may be null)
+  float* s_x_out;         // fused quant: block 0 stores s_x (may be null)
+  uint16_t* y;            // [M, N] bf16
+  int* acc_out;           // optional int32 [M, N]
+  int M, N, K;
+};
+
+// Fused M=1 path: every wave quantises the (L2-resident) activation row
+// itself, so decode needs one launch per linear.
+template <int R, int NCH>
+__global__ __launch_bounds__(256) void a8w8_gemv_m1(const A8Args a) {
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  const bool writer = blockIdx.x == 0 && threadIdx.x < 64;
+  if (n0 >= a.N && !writer) return;
+  uint4 w[R][NCH];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      w[r][c] = n0 + r < a.N ? ld_stream16(a.Wq + (size_t)(n0 + r) * a.K + c * 1024 + lane * 16)
+                             : make_uint4(0, 0, 0, 0);
+  // Quantise x: lane holds 16 values per chunk.
+  float xf[NCH][16];
+  float mx = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const uint16_t* xp = a.x + c * 1024 + lane * 16;
+    unpack8(*reinterpret_cast<const uint4*>(xp), xf[c]);
+    unpack8(*reinterpret_cast<const uint4*>(xp + 8), xf[c] + 8);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(xf[c][j]));
+  }
+  mx = wave_max(mx);
+  const float inv = 127.0f / mx;
+  const float sx = mx / 127.0f;
+  uint4 xq[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    uint32_t wd[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v |= ((uint32_t)(uint8_t)sat_i8(xf[c][4 * d + j] * inv)) << (8 * j);
+      wd[d] = v;
+    }
+    xq[c] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    if (writer && a.xq_out) *reinterpret_cast<uint4*>(a.xq_out + c * 1024 + lane * 16) = xq[c];
+  }
+  if (writer && a.s_x_out && lane == 0) a.s_x_out[0] = sx;
+  if (n0 >= a.N) return;
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[r] = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc[r] = dot16(w[r][c], xq[c], acc[r]);
+    acc[r] = wave_sum_i32(acc[r]);
+  }
+  if (lane < R && n0 + lane < a.N) {
+    int v = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) v = lane == r ? acc[r] : v;
+    a.y[n0 + lane] = (uint16_t)f2bf((float)v * sx * a.s_w[n0 + lane]);
+    if (a.acc_out) a.acc_out[n0 + lane] = v;
+  }
+}
+
+// General M (pre-quantised activations), any K multiple of 16.
+template <int R, int MT>
+__global__ __launch_bounds__(256) void a8w8_gemv_mt(const A8Args a, int m0) {
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (n0 >= a.N) return;
+  const int mcount = min(MT, a.M - m0);
+  int acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0;
+  for (int k = lane * 16; k < a.K; k += 1024) {
+    uint4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      w[r] = n0 + r < a.N ? ld_stream16(a.Wq + (size_t)(n0 + r) * a.K + k) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < mcount) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(a.xq + (size_t)(m0 + m) * a.K + k);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][m] = dot16(w[r], xv, acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = wave_sum_i32(acc[r][m]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (n0 + r >= a.N) continue;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m < mcount) {
+          const size_t o = (size_t)(m0 + m) * a.N + n0 + r;
+          a.y[o] = (uint16_t)f2bf((float)acc[r][m] * a.s_x[m0 + m] * a.s_w[n0 + r]);
+          if (a.acc_out) a.acc_out[o] = acc[r][m];
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, hipStream_t stream) {
+  Q35_CHECK_ARG(N > 0 && K > 0 && W && Wq && scale);
+  quant_weight_rows<<<(N + 3) / 4, 256, 0, stream>>>((const uint16_t*)W, (int8_t*)Wq,
+                                                    (float*)scale, N, K);
+  return q35_last_error();
+}
+
+int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, hipStream_t stream) {
+  Q35_CHECK_ARG(M >= 0 && K > 0);
+  if (M == 0) return 0;
+  quant_act_rows<<<(M + 3) / 4, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale,
+                                                  M, K);
+  return q35_last_error();
+}
+
+// y[M,N] = bf16(acc * s_x[m] * s_w[n]). When x (bf16) is given and M == 1 the
+// activation quantisation is fused and xq/s_x receive its result (optional);
+// otherwise xq/s_x are inputs. acc_out (optional) receives the int32 sums.
+int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void* s_w, void* y,
+                  void* acc_out, int M, int N, int K, hipStream_t stream) {
+  Q35_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 16 == 0 && Wq && s_w && y);
+  Q35_CHECK_ARG(q35_aligned16(Wq) && q35_aligned16(xq) && q35_aligned16(x));
+  A8Args a{(const int8_t*)Wq, (const float*)s_w, (const int8_t*)xq, (const float*)s_x,
+           (const uint16_t*)x, (int8_t*)xq, (float*)s_x, (uint16_t*)y, (int*)acc_out, M, N, K};
+  if (x && M == 1 && K % 1024 == 0 && (K == 2048 || K == 6144)) {
+    if (K == 2048) {
+      const int R = 2;
+      a8w8_gemv_m1<R, 2><<<(unsigned)((N + 4 * R - 1) / (4 * R)), 256, 0, stream>>>(a);
+    } else {
+      const int R = 1;
+      a8w8_gemv_m1<R, 6><<<(unsigned)((N + 4 * R - 1) / (4 * R)), 256, 0, stream>>>(a);
+    }
+    return q35_last_error();
+  }
+  if (x) {
+    Q35_CHECK_ARG(xq && s_x);
+    const int e = q35_quant_act_i8(x, xq, s_x, M, K, stream);
+    if (e) return e;
+  }
+  Q35_CHECK_ARG(xq && s_x);
+  a.x = nullptr;
+  constexpr int R = 2, MT = 4;
+  const unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
+  for (int m0 = 0; m0 < M; m0 += MT) {
+    a8w8_gemv_mt<R, MT><<<grid, 256, 0, stream>>>(a, m0);
+    const int e = q35_last_error();
+    if (e) return e;
+  }
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,414 @@
+// Gated DeltaNet decode and prefill kernels: depthwise causal conv1d (+SiLU)
+// with its rolling state, the gated delta-rule recurrence and the gated
+// RMSNorm epilogue.
+//
+// Layouts (batch b, head h, token t; H heads of dim D = 128):
+//   packed projection  [B, L, P]  = [q (H*D) | k (H*D) | v (H*D) | z (H*D) | a (H) | b (H) | pad]
+//   qkv after conv     [B, L, 3*H*D]
+//   conv weight        [C, KW] bf16, conv state [B, C, KW] bf16 (last KW inputs)
+//   recurrent state    [B, H, D(k), D(v)] fp32, v contiguous, updated in place
+//   core output        [B, L, H, D] bf16
+//
+// Per token and head (reference kernels.py:768-851, restating the fp32 rule):
+//   q^ = q * rsqrt(sum q^2 + 1e-6) * (1/sqrt(D)),  k^ = k * rsqrt(sum k^2 + 1e-6)
+//   alpha = exp(-exp(A_log) * softplus(a + dt_bias)),  beta = sigmoid(b)
+//   S = alpha*S;  m = S^T k^;  d = beta*(v - m);  S += k^ d^T;  o = S^T q^
+#include "q35_common.hpp"
+
+namespace {
+
+Q35_DEV float ld_param(const void* p, int i, int is_f32) {
+  return is_f32 ? reinterpret_cast<const float*>(p)[i] : bf2f(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+Q35_DEV float softplus20(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+
+// Single-token conv for one channel: window = (state[1..KW-1], x), state
+// shifted in place, returns bf16(silu(bf16(sum_t w[t]*window[t]))) as fp32.
+// [reference kernels.py:622-656]
+Q35_DEV float conv_update_channel(uint16_t* __restrict__ st, const uint16_t* __restrict__ w,
+                                  uint16_t xin, int kw) {
+  float acc = 0.f;
+  for (int t = 0; t < kw - 1; ++t) {
+    const uint16_t s = st[t + 1];
+    st[t] = s;
+    acc = fmaf(bf2f(s), bf2f(w[t]), acc);
+  }
+  st[kw - 1] = xin;
+  acc = fmaf(bf2f(xin), bf2f(w[kw - 1]), acc);
+  return round_bf(silu_f(round_bf(acc)));
+}
+
+// ------------------------------------------------------------------ conv1d
+__global__ __launch_bounds__(256) void conv1d_update(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ w,
+                                                     uint16_t* __restrict__ state,
+                                                     uint16_t* __restrict__ out, int B, int C,
+                                                     int in_stride, int kw) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * C) return;
+  const int b = i / C, c = i - b * C;
+  const float o = conv_update_channel(state + (size_t)i * kw, w + (size_t)c * kw,
+                                      x[(size_t)b * in_stride + c], kw);
+  out[i] = (uint16_t)f2bf(o);
+}
+
+// Prefill conv: zero history before token 0 (the stored state is not read),
+// and the last KW inputs are written to the state [reference kernels.py:576-619].
+__global__ __launch_bounds__(256) void conv1d_prefill(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ w,
+                                                      uint16_t* __restrict__ state,
+                                                      uint16_t* __restrict__ out, int B, int L,
+                                                      int C, int in_stride, int kw) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)B * L * C) return;
+  const int c = (int)(i % C);
+  const long long tf = i / C;
+  const int t = (int)(tf % L);
+  const int b = (int)(tf / L);
+  float acc = 0.f;
+  for (int tap = 0; tap < kw; ++tap) {
+    const int src = t - (kw - 1 - tap);
+    if (src >= 0)
+      acc = fmaf(bf2f(x[((size_t)b * L + src) * in_stride + c]), bf2f(w[(size_t)c * kw + tap]), acc);
+  }
+  out[i] = (uint16_t)f2bf(silu_f(round_bf(acc)));
+  const int pos = t - (L - kw);
+  if (pos >= 0 && pos < kw)
+    state[((size_t)b * C + c) * kw + pos] = x[((size_t)b * L + t) * in_stride + c];
+}
+
+// ------------------------------------------------------------- decode step
+// One 256-thread workgroup per (batch, head); D = 128 fixed. Thread t owns
+// v-columns 4*(t%32)..+3 of k-rows (t/32) + 8*i, i = 0..15: each k-row of the
+// fp32 state is 512 contiguous bytes read by 32 lanes with 16-byte loads, and
+// the state is read once and written once per step.
+constexpr int kD = 128;
+
+struct DeltaArgs {
+  const uint16_t* src;     // FUSE_CONV: packed projection; else post-conv qkv
+  int src_stride;          // elements per token row of src
+  const uint16_t* packed;  // packed projection (a, b, z)
+  int packed_stride;
+  const uint16_t* conv_w;  // [C, kw]
+  uint16_t* conv_state;    // [B, C, kw]
+  int conv_channels;       // C = 3*H*D
+  int kw;
+  const void* a_log;
+  const void* dt_bias;
+  int params_f32;
+  float* state;            // [B, H, D, D]
+  const void* norm_w;      // gated norm weight [D]
+  int norm_w_f32;
+  float norm_eps;
+  uint16_t* out;           // [B, H, D]
+  int H;
+  int z_off, a_off, b_off;
+};
+
+template <bool FUSE_CONV, bool FUSE_GNORM>
+__global__ __launch_bounds__(256) void delta_decode(const DeltaArgs p) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int vq = tid & 31;   // v columns 4*vq .. 4*vq+3
+  const int kg = tid >> 5;   // k rows kg + 8*i
+
+  __shared__ float qs[kD], ks[kD], vs[kD];
+  __shared__ float red[4][kD];
+  __shared__ float sc[4];
+
+  // Issue the state loads first: 16 x 16 B per thread, 64 KiB per head.
+  float* S = p.state + (size_t)bh * kD * kD;
+  float4 st[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    st[i] = *reinterpret_cast<const float4*>(S + (size_t)(kg + 8 * i) * kD + 4 * vq);
+
+  // q, k, v for this head (after conv).
+  const uint16_t* srow = p.src + (size_t)b * p.src_stride;
+  for (int j = tid; j < 3 * kD; j += 256) {
+    const int part = j / kD, i = j - part * kD;
+    const int ch = part * p.H * kD + h * kD + i;
+    float val;
+    if (FUSE_CONV) {
+      val = conv_update_channel(p.conv_state + ((size_t)b * p.conv_channels + ch) * p.kw,
+                                p.conv_w + (size_t)ch * p.kw, srow[ch], p.kw);
+    } else {
+      val = bf2f(srow[ch]);
+    }
+    (part == 0 ? qs : part == 1 ? ks : vs)[i] = val;
+  }
+  __syncthreads();
+
+  // Norm factors (wave 0: q, wave 1: k) and the gates.
+  if (wid < 2) {
+    const float* src = wid == 0 ? qs : ks;
+    const float a0 = src[lane], a1 = src[lane + 64];
+    const float tot = wave_sum(a0 * a0 + a1 * a1);
+    if (lane == 0) sc[wid] = rsqrt_cr(tot + 1e-6f);
+  } else if (tid == 128) {
+    const uint16_t* prow = p.packed + (size_t)b * p.packed_stride;
+    const float a = bf2f(prow[p.a_off + h]) + ld_param(p.dt_bias, h, p.params_f32);
+    const float g = -expf(ld_param(p.a_log, h, p.params_f32)) * softplus20(a);
+    sc[2] = expf(g);
+    sc[3] = 1.0f / (1.0f + expf(-bf2f(prow[p.b_off + h])));
+  }
+  __syncthreads();
+  const float q_inv = sc[0], k_inv = sc[1], alpha = sc[2], beta = sc[3];
+  const float qscale = 0.08838834764831845f;  // fp32(1/sqrt(128))
+
+  // S = alpha*S; partial m = S^T k^ over this thread's rows.
+  float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float kh = ks[kg + 8 * i] * k_inv;
+    st[i].x *= alpha; st[i].y *= alpha; st[i].z *= alpha; st[i].w *= alpha;
+    m.x = fmaf(st[i].x, kh, m.x); m.y = fmaf(st[i].y, kh, m.y);
+    m.z = fmaf(st[i].z, kh, m.z); m.w = fmaf(st[i].w, kh, m.w);
+  }
+  // Reduce over the 8 k-groups: lanes l and l^32 of a wave, then the 4 waves.
+  m.x += __shfl_xor(m.x, 32); m.y += __shfl_xor(m.y, 32);
+  m.z += __shfl_xor(m.z, 32); m.w += __shfl_xor(m.w, 32);
+  if (lane < 32) *reinterpret_cast<float4*>(&red[wid][4 * vq]) = m;
+  __syncthreads();
+  if (tid < kD) {
+    const float mem = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+    vs[tid] = beta * (vs[tid] - mem);   // delta
+  }
+  __syncthreads();
+  const float4 d = *reinterpret_cast<const float4*>(&vs[4 * vq]);
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float kh = ks[kg + 8 * i] * k_inv;
+    const float qh = qs[kg + 8 * i] * q_inv * qscale;
+    st[i].x += kh * d.x; st[i].y += kh * d.y; st[i].z += kh * d.z; st[i].w += kh * d.w;
+    o.x = fmaf(st[i].x, qh, o.x); o.y = fmaf(st[i].y, qh, o.y);
+    o.z = fmaf(st[i].z, qh, o.z); o.w = fmaf(st[i].w, qh, o.w);
+    *reinterpret_cast<float4*>(S + (size_t)(kg + 8 * i) * kD + 4 * vq) = st[i];
+  }
+  o.x += __shfl_xor(o.x, 32); o.y += __shfl_xor(o.y, 32);
+  o.z += __shfl_xor(o.z, 32); o.w += __shfl_xor(o.w, 32);
+  __syncthreads();  // red[] reuse
+  if (lane < 32) *reinterpret_cast<float4*>(&red[wid][4 * vq]) = o;
+  __syncthreads();
+  float core = 0.f;
+  if (tid < kD) core = round_bf((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]));
+  uint16_t* orow = p.out + (size_t)bh * kD;
+  if (!FUSE_GNORM) {
+    if (tid < kD) orow[tid] = (uint16_t)f2bf(core);
+    return;
+  }
+  // Gated RMSNorm over the head [reference kernels.py:115-155].
+  if (wid < 2) {
+    const float ss = wave_sum(core * core);
+    if (lane == 0) sc[wid] = ss;
+  }
+  __syncthreads();
+  if (tid < kD) {
+    const float inv = rsqrt_cr((sc[0] + sc[1]) / (float)kD + p.norm_eps);
+    const float nb = round_bf(core * inv);
+    const float wb = round_bf(ld_param(p.norm_w, tid, p.norm_w_f32));
+    const float weighted = round_bf(nb * wb);
+    const float z = bf2f(p.packed[(size_t)b * p.packed_stride + p.z_off + h * kD + tid]);
+    orow[tid] = (uint16_t)f2bf(weighted * silu_f(z));
+  }
+}
+
+// ------------------------------------------------------------- prefill scan
+// Per (token, head) scalars (q_inv, k_inv, alpha, beta) [reference kernels.py:713-765].
+__global__ __launch_bounds__(256) void delta_factors(const uint16_t* __restrict__ qkv, int qkv_stride,
+                                                     const uint16_t* __restrict__ packed,
+                                                     int packed_stride, const void* a_log,
+                                                     const void* dt_bias, int params_f32,
+                                                     float* __restrict__ factors, int rows, int H,
+                                                     int a_off, int b_off) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);  // r = token_flat * H + h
+  if (r >= rows) return;
+  const int h = r % H;
+  const long long tf = r / H;
+  const uint16_t* row = qkv + (size_t)tf * qkv_stride;
+  const float q0 = bf2f(row[h * kD + lane]), q1 = bf2f(row[h * kD + lane + 64]);
+  const float k0 = bf2f(row[H * kD + h * kD + lane]), k1 = bf2f(row[H * kD + h * kD + lane + 64]);
+  const float qs = wave_sum(q0 * q0 + q1 * q1);
+  const float ks = wave_sum(k0 * k0 + k1 * k1);
+  if (lane == 0) {
+    const uint16_t* prow = packed + (size_t)tf * packed_stride;
+    const float a = bf2f(prow[a_off + h]) + ld_param(dt_bias, h, params_f32);
+    const float alpha = expf(-expf(ld_param(a_log, h, params_f32)) * softplus20(a));
+    const float beta = 1.0f / (1.0f + expf(-bf2f(prow[b_off + h])));
+    float4 f = make_float4(rsqrt_cr(qs + 1e-6f), rsqrt_cr(ks + 1e-6f), alpha, beta);
+    *reinterpret_cast<float4*>(factors + (size_t)r * 4) = f;
+  }
+}
+
+// Sequential scan over L tokens. One wave per (batch, head, 8-column v tile);
+// lane = (k-group kg = lane/4 of 8 rows, v pair vp = lane%4), so the [128 x 8]
+// fp32 state tile lives in registers (16 per lane) for the whole sequence.
+// Reductions over k run across lanes with the same vp (xor 4, 8, 16, 32).
+__global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qkv, int qkv_stride,
+                                                 const float* __restrict__ factors,
+                                                 float* __restrict__ state,
+                                                 uint16_t* __restrict__ out, int L, int H) {
+  const int lane = threadIdx.x;
+  const int tiles = kD / 8;
+  const int tile = blockIdx.x % tiles;
+  const int bh = blockIdx.x / tiles;
+  const int b = bh / H, h = bh - b * H;
+  const int kg = lane >> 2, vp = lane & 3;
+  const int v0 = tile * 8 + 2 * vp;
+  float* S = state + (size_t)bh * kD * kD;
+  float s[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float2 t2 = *reinterpret_cast<const float2*>(S + (size_t)(kg * 8 + i) * kD + v0);
+    s[i][0] = t2.x; s[i][1] = t2.y;
+  }
+  const float qscale = 0.08838834764831845f;
+  for (int t = 0; t < L; ++t) {
+    const uint16_t* row = qkv + ((size_t)b * L + t) * qkv_stride;
+    const uint4 qv = *reinterpret_cast<const uint4*>(row + h * kD + kg * 8);
+    const uint4 kv = *reinterpret_cast<const uint4*>(row + H * kD + h * kD + kg * 8);
+    const uint32_t vv = *reinterpret_cast<const uint32_t*>(row + 2 * H * kD + h * kD + v0);
+    const float4 f = *reinterpret_cast<const float4*>(factors + (((size_t)b * L + t) * H + h) * 4);
+    float q[8], k[8];
+    unpack8(qv, q);
+    unpack8(kv, k);
+    float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      k[i] *= f.y;
+      q[i] = q[i] * f.x * qscale;
+      s[i][0] *= f.z; s[i][1] *= f.z;
+      m0 = fmaf(s[i][0], k[i], m0);
+      m1 = fmaf(s[i][1], k[i], m1);
+    }
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+      m0 += __shfl_xor(m0, off);
+      m1 += __shfl_xor(m1, off);
+    }
+    const float d0 = f.w * (bf_lo(vv) - m0), d1 = f.w * (bf_hi(vv) - m1);
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s[i][0] += k[i] * d0;
+      s[i][1] += k[i] * d1;
+      o0 = fmaf(s[i][0], q[i], o0);
+      o1 = fmaf(s[i][1], q[i], o1);
+    }
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+      o0 += __shfl_xor(o0, off);
+      o1 += __shfl_xor(o1, off);
+    }
+    if (kg == 0)
+      *reinterpret_cast<uint32_t*>(out + (((size_t)b * L + t) * H + h) * kD + v0) = pack_bf2(o0, o1);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    *reinterpret_cast<float2*>(S + (size_t)(kg * 8 + i) * kD + v0) = make_float2(s[i][0], s[i][1]);
+}
+
+}  // namespace
+
+extern "C" {
+
+int q35_conv1d_update(const void* x, const void* w, void* state, void* out, int B, int C,
+                      int in_stride, int kw, hipStream_t stream) {
+  Q35_CHECK_ARG(B >= 0 && C > 0 && kw > 0 && kw <= 16 && in_stride >= C);
+  if (B == 0) return 0;
+  const int total = B * C;
+  conv1d_update<<<(total + 255) / 256, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)w,
+                                                        (uint16_t*)state, (uint16_t*)out, B, C,
+                                                        in_stride, kw);
+  return q35_last_error();
+}
+
+int q35_conv1d_prefill(const void* x, const void* w, void* state, void* out, int B, int L, int C,
+                       int in_stride, int kw, hipStream_t stream) {
+  Q35_CHECK_ARG(B >= 0 && L > 0 && C > 0 && kw > 0 && kw <= 16 && in_stride >= C);
+  const long long total = (long long)B * L * C;
+  if (total == 0) return 0;
+  const long long grid = (total + 255) / 256;
+  Q35_CHECK_ARG(grid < (1ll << 31));
+  conv1d_prefill<<<(unsigned)grid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)w,
+                                                     (uint16_t*)state, (uint16_t*)out, B, L, C,
+                                                     in_stride, kw);
+  return q35_last_error();
+}
+
+// One decode step of the recurrence for all heads. With fuse_conv the input
+// is the raw packed projection and the conv state/weight are applied first;
+// with fuse_gnorm the output is the gated RMSNorm of the core output.
+int q35_delta_decode(const void* src, int src_stride, const void* packed, int packed_stride,
+                     const void* conv_w, void* conv_state, int kw, const void* a_log,
+                     const void* dt_bias, int params_f32, void* state, const void* norm_w,
+                     int norm_w_f32, float norm_eps, void* out, int B, int H, int D,
+                     int fuse_conv, int fuse_gnorm, hipStream_t stream) {
+  Q35_CHECK_ARG(B >= 0 && H > 0 && D == kD);
+  Q35_CHECK_ARG(src_stride >= 3 * H * D && packed_stride >= 4 * H * D + 2 * H);
+  Q35_CHECK_ARG(!fuse_conv || (conv_w && conv_state && kw > 0 && kw <= 16));
+  Q35_CHECK_ARG(!fuse_gnorm || norm_w);
+  Q35_CHECK_ARG(q35_aligned16(state));
+  if (B == 0) return 0;
+  DeltaArgs p;
+  p.src = (const uint16_t*)src;
+  p.src_stride = src_stride;
+  p.packed = (const uint16_t*)packed;
+  p.packed_stride = packed_stride;
+  p.conv_w = (const uint16_t*)conv_w;
+  p.conv_state = (uint16_t*)conv_state;
+  p.conv_channels = 3 * H * D;
+  p.kw = kw;
+  p.a_log = a_log;
+  p.dt_bias = dt_bias;
+  p.params_f32 = params_f32;
+  p.state = (float*)state;
+  p.norm_w = norm_w;
+  p.norm_w_f32 = norm_w_f32;
+  p.norm_eps = norm_eps;
+  p.out = (uint16_t*)out;
+  p.H = H;
+  p.z_off = 3 * H * D;
+  p.a_off = 4 * H * D;
+  p.b_off = 4 * H * D + H;
+  const unsigned grid = (unsigned)(B * H);
+  if (fuse_conv && fuse_gnorm) delta_decode<true, true><<<grid, 256, 0, stream>>>(p);
+  else if (fuse_conv) delta_decode<true, false><<<grid, 256, 0, stream>>>(p);
+  else if (fuse_gnorm) delta_decode<false, true><<<grid, 256, 0, stream>>>(p);
+  else delta_decode<false, false><<<grid, 256, 0, stream>>>(p);
+  return q35_last_error();
+}
+
+// Floats of workspace q35_delta_prefill needs: 4 per (batch, token, head).
+long long q35_delta_prefill_workspace(int B, int L, int H) { return 4ll * B * L * H; }
+
+// Sequential recurrence over L tokens (input: post-conv qkv), state in place.
+int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
+                      const void* a_log, const void* dt_bias, int params_f32, void* state,
+                      void* out, void* workspace, long long workspace_floats, int B, int L, int H,
+                      int D, hipStream_t stream) {
+  Q35_CHECK_ARG(B >= 0 && L > 0 && H > 0 && D == kD);
+  Q35_CHECK_ARG(qkv_stride >= 3 * H * D && qkv_stride % 8 == 0);
+  Q35_CHECK_ARG(packed_stride >= 4 * H * D + 2 * H);
+  Q35_CHECK_ARG(workspace_floats >= q35_delta_prefill_workspace(B, L, H));
+  Q35_CHECK_ARG(q35_aligned16(qkv) && q35_aligned16(workspace) && q35_aligned16(state));
+  if (B == 0) return 0;
+  const long long rows = (long long)B * L * H;
+  Q35_CHECK_ARG(rows < (1ll << 30));
+  delta_factors<<<(unsigned)((rows + 3) / 4), 256, 0, stream>>>(
+      (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
+      params_f32, (float*)workspace, (int)rows, H, 4 * H * D, 4 * H * D + H);
+  int e = q35_last_error();
+  if (e) return e;
+  delta_scan<<<(unsigned)(B * H * (kD / 8)), 64, 0, stream>>>(
+      (const uint16_t*)qkv, qkv_stride, (const float*)workspace, (float*)state, (uint16_t*)out, L, H);
+  return q35_last_error();
+}
+
+}  // extern "C"

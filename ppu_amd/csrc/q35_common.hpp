@@ -1,0 +1,144 @@
+// Shared device helpers for the gfx950 (CDNA4) decode kernels.
+//
+// bf16 values travel as raw 16-bit patterns (uint16_t) so no host or device
+// header type sits in the C ABI. Conversions are explicit: fp32 -> bf16 is
+// round-to-nearest-even, the rounding torch (CPU and GPU) and Triton's
+// `.to(tl.bfloat16)` use, so every rounding point of the reference kernels is
+// reproduced at the same place.
+//
+// Reductions are wave64: quad_perm / row_half_mirror / row_mirror DPP moves
+// reduce each 16-lane row, ds_swizzle (xor 16) joins the two rows of each
+// 32-lane half and v_readlane joins the halves. No LDS allocation is needed.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define Q35_DEV __device__ __forceinline__
+
+typedef uint16_t bf16_t;
+
+// ---------------------------------------------------------------- bf16 <-> f32
+Q35_DEV float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
+Q35_DEV float bf_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+Q35_DEV float bf_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+Q35_DEV uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+Q35_DEV float round_bf(float f) { return bf2f(f2bf(f)); }
+Q35_DEV uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// Unpack 8 bf16 held in a uint4 into fp32.
+Q35_DEV void unpack8(const uint4 v, float* f) {
+  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
+  f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+  f[4] = bf_lo(v.z); f[5] = bf_hi(v.z);
+  f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+}
+Q35_DEV uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = pack_bf2(f[0], f[1]);
+  v.y = pack_bf2(f[2], f[3]);
+  v.z = pack_bf2(f[4], f[5]);
+  v.w = pack_bf2(f[6], f[7]);
+  return v;
+}
+
+// 128-bit streaming load of data read exactly once (weights): non-temporal
+// hint so it does not displace reused lines (activations, KV) from L2/MALL.
+typedef uint32_t q35_u32x4 __attribute__((ext_vector_type(4)));
+Q35_DEV uint4 ld_stream16(const void* p) {
+  const q35_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const q35_u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---------------------------------------------------------------- math
+// 1/sqrt with two correctly rounded steps (sqrt, then divide): the same
+// arithmetic torch's CPU rsqrt performs, so norm factors match the oracle.
+Q35_DEV float rsqrt_cr(float x) { return 1.0f / sqrtf(x); }
+Q35_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
+Q35_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------- DPP moves
+template <int CTRL>
+Q35_DEV float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+Q35_DEV int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+#define Q35_DPP_QUAD_XOR1 0xB1   // quad_perm [1,0,3,2]
+#define Q35_DPP_QUAD_XOR2 0x4E   // quad_perm [2,3,0,1]
+#define Q35_DPP_ROW_HALF_MIRROR 0x141
+#define Q35_DPP_ROW_MIRROR 0x140
+#define Q35_SWZ_XOR16 0x401F     // ds_swizzle bitmask mode: and 0x1f, xor 0x10
+
+Q35_DEV float swz_xor16_f(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), Q35_SWZ_XOR16));
+}
+
+// Sum over each aligned group of 16 lanes; every lane of the row gets it.
+Q35_DEV float row16_sum(float v) {
+  v += dpp_f<Q35_DPP_QUAD_XOR1>(v);
+  v += dpp_f<Q35_DPP_QUAD_XOR2>(v);
+  v += dpp_f<Q35_DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_f<Q35_DPP_ROW_MIRROR>(v);
+  return v;
+}
+
+// Sum over the whole wave64; the result is wave-uniform.
+Q35_DEV float wave_sum(float v) {
+  v = row16_sum(v);
+  v += swz_xor16_f(v);
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  return lo + hi;
+}
+
+Q35_DEV float wave_max(float v) {
+  v = fmaxf(v, dpp_f<Q35_DPP_QUAD_XOR1>(v));
+  v = fmaxf(v, dpp_f<Q35_DPP_QUAD_XOR2>(v));
+  v = fmaxf(v, dpp_f<Q35_DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f<Q35_DPP_ROW_MIRROR>(v));
+  v = fmaxf(v, swz_xor16_f(v));
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  return fmaxf(lo, hi);
+}
+
+// 64-bit max over the wave (used for packed value/index argmax keys).
+Q35_DEV uint64_t u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+Q35_DEV uint64_t wave_max_u64(uint64_t v) {
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64);
+    v = u64_max(v, ((uint64_t)hi << 32) | lo);
+  }
+  return v;
+}
+
+// Order-preserving key for a bf16 value (as fp32 with zero low half) and an
+// index: larger value wins, then the lower index. -0 and +0 compare equal,
+// as float comparison does.
+Q35_DEV uint64_t top1_key(float v_bf16, uint32_t index) {
+  uint32_t b = __float_as_uint(v_bf16) >> 16;
+  if ((b & 0x7fffu) == 0) b = 0;                 // fold -0 onto +0
+  const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - index);
+}
+Q35_DEV uint32_t top1_index(uint64_t key) { return 0xffffffffu - (uint32_t)(key & 0xffffffffu); }
+
+// ---------------------------------------------------------------- launch checks
+#define Q35_CHECK_ARG(cond)                    \
+  do {                                         \
+    if (!(cond)) return (int)hipErrorInvalidValue; \
+  } while (0)
+
+static inline int q35_last_error() { return (int)hipGetLastError(); }
+
+static inline bool q35_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

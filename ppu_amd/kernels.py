@@ -1,0 +1,632 @@
+"""Operator API of the Qwen3.5 decode hot path on MI355X.
+
+Same names, signatures, return shapes/dtypes and ``ValueError`` conditions as
+the reference operator module (qwen35_fused/kernels.py), so the model
+integration and graph runner can call them unchanged. Every operator launches
+hand-written gfx950 kernels from libq35.so on the current torch stream; none
+has a torch or CPU fallback. Outputs and workspaces are allocated with
+``torch.empty`` on the input's device (from the graph pool under capture);
+state tensors (conv state, recurrent state, KV cache) are updated in place.
+
+Tuning keywords of the reference (``block_n``, ``block_v``, ``splits`` ...)
+are accepted and validated as the reference does, but the MI355X kernels pick
+their own decomposition.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+
+
+def _rows_and_width(x: torch.Tensor) -> tuple[int, int]:
+    """reference kernels.py:16-21."""
+    if not x.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    if not x.is_contiguous():
+        raise ValueError("fused kernels require contiguous input")
+    return x.numel() // x.shape[-1], x.shape[-1]
+
+
+def _need_bf16(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t.dtype != _BF16:
+            raise ValueError(f"MI355X kernels take bfloat16 tensors, got {t.dtype}")
+
+
+def _param(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """A small parameter vector as (contiguous tensor, is_fp32 flag)."""
+    if t.dtype == torch.float32:
+        return t.contiguous(), 1
+    if t.dtype == _BF16:
+        return t.contiguous(), 0
+    return t.float().contiguous(), 1
+
+
+def _stream(x: torch.Tensor) -> int:
+    return _lib.stream(x.device)
+
+
+# ------------------------------------------------------------------ norms
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Qwen3.5 RMSNorm ``(1 + w)``: fp32 reduction, bf16 output. reference kernels.py:44."""
+
+    rows, width = _rows_and_width(x)
+    if weight.numel() != width:
+        raise ValueError(f"weight has {weight.numel()} values, expected {width}")
+    _need_bf16(x)
+    w, wf = _param(weight)
+    out = torch.empty_like(x)
+    _lib.call("q35_rmsnorm", x.data_ptr(), w.data_ptr(), wf, out.data_ptr(), rows, width,
+              float(eps), _stream(x))
+    return out
+
+
+def residual_add_rms_norm(
+    residual: torch.Tensor,
+    update: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Return ``(residual + update, RMSNorm(residual + update))``. reference kernels.py:85."""
+
+    if residual.shape != update.shape or residual.dtype != update.dtype:
+        raise ValueError("residual and update must have identical shape and dtype")
+    rows, width = _rows_and_width(residual)
+    if not update.is_contiguous():
+        raise ValueError("update must be contiguous")
+    if weight.numel() != width:
+        raise ValueError(f"weight has {weight.numel()} values, expected {width}")
+    _need_bf16(residual)
+    w, wf = _param(weight)
+    residual_out = torch.empty_like(residual)
+    norm_out = torch.empty_like(residual)
+    _lib.call("q35_residual_rmsnorm", residual.data_ptr(), update.data_ptr(), w.data_ptr(), wf,
+              residual_out.data_ptr(), norm_out.data_ptr(), rows, width, float(eps),
+              _stream(residual))
+    return residual_out, norm_out
+
+
+def gated_rms_norm(
+    x: torch.Tensor,
+    gate: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """Gated RMSNorm with eager rounding points. reference kernels.py:139."""
+
+    if x.shape != gate.shape:
+        raise ValueError("x and gate must have identical shape")
+    rows, width = _rows_and_width(x)
+    if not gate.is_contiguous():
+        raise ValueError("gate must be contiguous")
+    if weight.numel() != width:
+        raise ValueError(f"weight has {weight.numel()} values, expected {width}")
+    _need_bf16(x, gate)
+    w, wf = _param(weight)
+    out = torch.empty_like(x)
+    _lib.call("q35_gated_rmsnorm", x.data_ptr(), gate.data_ptr(), w.data_ptr(), wf, out.data_ptr(),
+              rows, width, float(eps), _stream(x))
+    return out
+
+
+def silu_and_mul(packed: torch.Tensor) -> torch.Tensor:
+    """SiLU of the first half times the second half. reference kernels.py:170."""
+
+    rows, packed_width = _rows_and_width(packed)
+    if packed_width % 2:
+        raise ValueError("packed last dimension must be even")
+    _need_bf16(packed)
+    width = packed_width // 2
+    out = torch.empty((*packed.shape[:-1], width), device=packed.device, dtype=packed.dtype)
+    _lib.call("q35_silu_mul", packed.data_ptr(), out.data_ptr(), rows, width, _stream(packed))
+    return out
+
+
+def attention_gate_mul(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """Multiply attention output by the gate inside the packed QGKV. reference kernels.py:312."""
+
+    if not x.is_contiguous() or not packed_qgkv.is_contiguous():
+        raise ValueError("attention gate tensors must be contiguous")
+    hidden = x.shape[-1]
+    if packed_qgkv.shape[:-1] != x.shape[:-1]:
+        raise ValueError("attention output and packed projection rows do not match")
+    if not x.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    if hidden % head_dim or packed_qgkv.shape[-1] < 2 * hidden:
+        raise ValueError("attention gate layout does not match the packed projection")
+    _need_bf16(x, packed_qgkv)
+    out = torch.empty_like(x)
+    tokens = x.numel() // hidden
+    _lib.call("q35_attn_gate_mul", x.data_ptr(), packed_qgkv.data_ptr(), out.data_ptr(), tokens,
+              hidden, packed_qgkv.shape[-1], head_dim, _stream(x))
+    return out
+
+
+# ------------------------------------------------------------------ GEMV
+def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """Decode ``F.linear(x, W)`` for one token (bf16, fp32 accumulate).
+
+    Replaces the vendor GEMV behind the reference's decode ``F.linear`` call
+    sites (integration.py:185,245,272,298-302,359).
+    """
+
+    k = x.shape[-1]
+    if x.numel() != k:
+        raise ValueError("decode linear expects a single token")
+    if weight.ndim != 2 or weight.shape[1] != k:
+        raise ValueError("linear input and weight dimensions do not match")
+    if not x.is_cuda or not weight.is_contiguous():
+        raise ValueError("decode linear tensors must be contiguous GPU tensors")
+    _need_bf16(x, weight)
+    x = x.contiguous()
+    n = weight.shape[0]
+    out = torch.empty((*x.shape[:-1], n), device=x.device, dtype=x.dtype)
+    _lib.call("q35_gemv_bf16", weight.data_ptr(), x.data_ptr(), None, None, 0, 0.0, None, None,
+              out.data_ptr(), n, k, 0, _stream(x))
+    return out
+
+
+def residual_norm_linear(
+    residual: torch.Tensor,
+    update: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    weight: torch.Tensor,
+    *,
+    swiglu: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``r' = residual + update``; ``y = linear(RMSNorm(r'), W)`` in one launch.
+
+    The residual add and RMSNorm of reference kernels.py:85 run as the GEMV
+    prologue (every wave recomputes the 2048-wide norm from L2); with
+    ``swiglu`` the epilogue of reference kernels.py:232 is applied to a packed
+    [gate; up] weight. Returns ``(r', y)``.
+    """
+
+    k = residual.shape[-1]
+    if residual.numel() != k or update.shape != residual.shape:
+        raise ValueError("fused residual GEMV expects one token")
+    _need_bf16(residual, update, weight)
+    w, wf = _param(norm_weight)
+    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    r_out = torch.empty_like(residual)
+    out = torch.empty((*residual.shape[:-1], n), device=residual.device, dtype=residual.dtype)
+    name = "q35_swiglu_gemv" if swiglu else "q35_gemv_bf16"
+    _lib.call(name, weight.data_ptr(), residual.data_ptr(), update.data_ptr(), w.data_ptr(), wf,
+              float(eps), r_out.data_ptr(), None, out.data_ptr(), n, k, 2, _stream(residual))
+    return r_out, out
+
+
+def ppu_swiglu_gemv(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    *,
+    block_n: int = 8,
+) -> torch.Tensor:
+    """Decode packed gate/up projection with fused SwiGLU. reference kernels.py:232."""
+
+    if x.ndim != 3 or x.shape[:2] != (1, 1) or x.dtype != torch.bfloat16:
+        raise ValueError("SwiGLU GEMV expects BF16 x[1,1,K]")
+    if packed_weight.ndim != 2 or packed_weight.shape[0] % 2:
+        raise ValueError("packed SwiGLU weight must have shape [2N,K]")
+    if packed_weight.shape[1] != x.shape[-1] or packed_weight.dtype != x.dtype:
+        raise ValueError("SwiGLU GEMV input and weight dimensions do not match")
+    if not x.is_contiguous() or not packed_weight.is_contiguous():
+        raise ValueError("SwiGLU GEMV tensors must be contiguous")
+    if block_n not in (2, 4, 8):
+        raise ValueError("SwiGLU GEMV block_n must be 2, 4 or 8")
+    if not x.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    n = packed_weight.shape[0] // 2
+    k = x.shape[-1]
+    out = torch.empty((1, 1, n), device=x.device, dtype=x.dtype)
+    _lib.call("q35_swiglu_gemv", packed_weight.data_ptr(), x.data_ptr(), None, None, 0, 0.0, None,
+              None, out.data_ptr(), n, k, 0, _stream(x))
+    return out
+
+
+def lm_head_argmax(
+    hidden: torch.Tensor,
+    weight: torch.Tensor,
+    *,
+    block_n: int = 16,
+    block_k: int = 128,
+) -> torch.Tensor:
+    """Greedy token id without materialising logits. reference kernels.py:1146."""
+
+    if hidden.shape != (1, weight.shape[1]) or hidden.dtype != torch.bfloat16:
+        raise ValueError("lm_head_argmax supports BF16 batch=1 hidden vectors")
+    if not hidden.is_contiguous() or not weight.is_contiguous():
+        raise ValueError("LM head tensors must be contiguous")
+    if not hidden.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    _need_bf16(weight)
+    vocab, k = weight.shape
+    slots = _lib.load().q35_lm_head_top1_workspace(vocab, k)
+    workspace = torch.empty(slots, device=hidden.device, dtype=torch.int64)
+    output = torch.empty((1, 1), device=hidden.device, dtype=torch.int64)
+    _lib.call("q35_lm_head_top1", weight.data_ptr(), hidden.data_ptr(), vocab, k,
+              workspace.data_ptr(), slots, output.data_ptr(), _stream(hidden))
+    return output
+
+
+# ------------------------------------------------------------------ DeltaNet
+def causal_conv1d_fused(x: torch.Tensor, weight: torch.Tensor, state: torch.Tensor) -> torch.Tensor:
+    """Causal depthwise conv + SiLU, ``state`` updated in place. reference kernels.py:659."""
+
+    if x.ndim != 3 or weight.ndim != 2 or state.ndim != 3:
+        raise ValueError("expected x[B,L,C], weight[C,K], state[B,C,K]")
+    if not x.is_contiguous() or not weight.is_contiguous() or not state.is_contiguous():
+        raise ValueError("causal conv tensors must be contiguous")
+    batch, seq_len, input_stride = x.shape
+    channels, kernel_size = weight.shape
+    if input_stride < channels or state.shape != (batch, channels, kernel_size):
+        raise ValueError("causal conv shapes do not match")
+    if not x.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    _need_bf16(x, weight, state)
+    out = torch.empty((batch, seq_len, channels), device=x.device, dtype=x.dtype)
+    if seq_len == 1:
+        _lib.call("q35_conv1d_update", x.data_ptr(), weight.data_ptr(), state.data_ptr(),
+                  out.data_ptr(), batch, channels, input_stride, kernel_size, _stream(x))
+    else:
+        _lib.call("q35_conv1d_prefill", x.data_ptr(), weight.data_ptr(), state.data_ptr(),
+                  out.data_ptr(), batch, seq_len, channels, input_stride, kernel_size, _stream(x))
+    return out
+
+
+def _delta_params(a_log: torch.Tensor, dt_bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, int]:
+    if a_log.dtype == dt_bias.dtype and a_log.dtype in (torch.float32, _BF16):
+        return a_log.contiguous(), dt_bias.contiguous(), int(a_log.dtype == torch.float32)
+    return a_log.float().contiguous(), dt_bias.float().contiguous(), 1
+
+
+def delta_recurrent_fused(
+    qkv: torch.Tensor,
+    packed_projection: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    state: torch.Tensor,
+    *,
+    block_v: int = 8,
+    precompute_factors: bool = False,
+) -> torch.Tensor:
+    """Sequential gated-delta recurrence; ``state`` updated in place. reference kernels.py:854.
+
+    ``qkv`` is ``[B,L,3*H*D]`` (after conv) and ``packed_projection`` holds
+    ``[qkv,z,a,b]`` in its last dimension. L == 1 runs the one-step decode
+    kernel; L > 1 the per-token factor pass and the sequential scan.
+    """
+
+    if qkv.ndim != 3 or packed_projection.ndim != 3 or state.ndim != 4:
+        raise ValueError("invalid delta recurrent tensor rank")
+    if not qkv.is_contiguous() or not packed_projection.is_contiguous() or not state.is_contiguous():
+        raise ValueError("delta recurrent tensors must be contiguous")
+    batch, seq_len, qkv_width = qkv.shape
+    _, heads, dim, value_dim = state.shape
+    if dim != value_dim or qkv_width != 3 * heads * dim:
+        raise ValueError("delta recurrent dimensions do not match")
+    packed_width = packed_projection.shape[-1]
+    b_offset = qkv_width + heads * dim + heads
+    if packed_width < b_offset + heads:
+        raise ValueError(f"packed projection width {packed_width} is smaller than {b_offset + heads}")
+    if not qkv.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    if dim != 128:
+        raise ValueError("MI355X delta kernels are built for head dim 128")
+    if state.dtype != torch.float32:
+        raise ValueError("delta recurrent state must be float32")
+    _need_bf16(qkv, packed_projection)
+    al, dt, pf = _delta_params(a_log, dt_bias)
+    out = torch.empty((batch, seq_len, heads, dim), device=qkv.device, dtype=qkv.dtype)
+    s = _stream(qkv)
+    if seq_len == 1:
+        _lib.call("q35_delta_decode", qkv.data_ptr(), qkv_width, packed_projection.data_ptr(),
+                  packed_width, None, None, 0, al.data_ptr(), dt.data_ptr(), pf, state.data_ptr(),
+                  None, 0, 0.0, out.data_ptr(), batch, heads, dim, 0, 0, s)
+    else:
+        floats = _lib.load().q35_delta_prefill_workspace(batch, seq_len, heads)
+        workspace = torch.empty(floats, device=qkv.device, dtype=torch.float32)
+        _lib.call("q35_delta_prefill", qkv.data_ptr(), qkv_width, packed_projection.data_ptr(),
+                  packed_width, al.data_ptr(), dt.data_ptr(), pf, state.data_ptr(), out.data_ptr(),
+                  workspace.data_ptr(), floats, batch, seq_len, heads, dim, s)
+    return out
+
+
+def delta_decode_fused(
+    packed_projection: torch.Tensor,
+    conv_weight: torch.Tensor,
+    conv_state: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    state: torch.Tensor,
+    norm_weight: torch.Tensor,
+    norm_eps: float,
+) -> torch.Tensor:
+    """One decode token of a DeltaNet layer in one launch: conv1d update, delta
+    rule and gated RMSNorm (reference kernels.py:659, :854 and :139 as chained
+    by integration.py:254-271). Returns the gated core ``[B*H, D]`` bf16."""
+
+    batch, seq_len, packed_width = packed_projection.shape
+    _, heads, dim, _ = state.shape
+    if seq_len != 1:
+        raise ValueError("fused DeltaNet decode takes one token")
+    _need_bf16(packed_projection, conv_weight, conv_state)
+    al, dt, pf = _delta_params(a_log, dt_bias)
+    nw, nwf = _param(norm_weight)
+    out = torch.empty((batch * heads, dim), device=packed_projection.device, dtype=_BF16)
+    _lib.call("q35_delta_decode", packed_projection.data_ptr(), packed_width,
+              packed_projection.data_ptr(), packed_width, conv_weight.data_ptr(),
+              conv_state.data_ptr(), conv_weight.shape[1], al.data_ptr(), dt.data_ptr(), pf,
+              state.data_ptr(), nw.data_ptr(), nwf, float(norm_eps), out.data_ptr(), batch, heads,
+              dim, 1, 1, _stream(packed_projection))
+    return out
+
+
+# ------------------------------------------------------------------ attention
+def qgkv_norm_rope(
+    packed_qgkv: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    *,
+    q_heads: int,
+    kv_heads: int,
+    dim: int,
+    rotary_dim: int,
+    cache_key: torch.Tensor | None = None,
+    cache_value: torch.Tensor | None = None,
+    cache_start: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Packed Q+gate/K/V layout with Q/K RMSNorm and partial RoPE. reference kernels.py:507."""
+
+    if not packed_qgkv.is_contiguous():
+        raise ValueError("packed QGKV must be contiguous")
+    batch, seq_len, packed_width = packed_qgkv.shape
+    expected = 2 * q_heads * dim + 2 * kv_heads * dim
+    if packed_width != expected:
+        raise ValueError(f"packed QGKV width {packed_width}, expected {expected}")
+    cos = cos.contiguous()
+    sin = sin.contiguous()
+    if cos.shape != (batch, seq_len, rotary_dim) or sin.shape != cos.shape:
+        raise ValueError(f"RoPE shape {tuple(cos.shape)}, expected {(batch, seq_len, rotary_dim)}")
+    if not packed_qgkv.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    _need_bf16(packed_qgkv)
+    if cos.dtype != _BF16:
+        cos = cos.to(_BF16)
+    if sin.dtype != _BF16:
+        sin = sin.to(_BF16)
+    qw, wf = _param(q_weight)
+    kw_, kwf = _param(k_weight)
+    if wf != kwf:
+        qw, kw_, wf = qw.float(), kw_.float(), 1
+    dev = packed_qgkv.device
+    q = torch.empty((batch, q_heads, seq_len, dim), device=dev, dtype=packed_qgkv.dtype)
+    write_cache = cache_key is not None
+    if write_cache:
+        if cache_value is None or cache_start is None:
+            raise ValueError("cache key, value and start must be provided together")
+        if cache_key.shape[:2] != (batch, kv_heads) or cache_key.shape[-1] != dim:
+            raise ValueError("static K cache shape does not match QGKV")
+        if cache_value.shape != cache_key.shape:
+            raise ValueError("static K/V cache shapes must match")
+        if not cache_key.is_contiguous() or not cache_value.is_contiguous():
+            raise ValueError("static K/V cache must be contiguous")
+        if cache_start.dtype != torch.int64 or cache_start.device != dev:
+            raise ValueError("cache_start must be an int64 scalar on the GPU")
+        k, v = cache_key, cache_value
+        cache_len = cache_key.shape[-2]
+        start_ptr = cache_start.data_ptr()
+    else:
+        k = torch.empty((batch, kv_heads, seq_len, dim), device=dev, dtype=packed_qgkv.dtype)
+        v = torch.empty_like(k)
+        cache_len = seq_len
+        start_ptr = None
+    _lib.call("q35_qgkv_norm_rope", packed_qgkv.data_ptr(), qw.data_ptr(), kw_.data_ptr(), wf,
+              cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), start_ptr,
+              batch, seq_len, q_heads, kv_heads, dim, rotary_dim, max(cache_len, 1), _stream(q))
+    return q, k, v
+
+
+def _check_decode_attention(q, cache_keys, cache_values):
+    if q.ndim != 4 or q.shape[0] != 1 or q.shape[2] != 1:
+        raise ValueError("GQA decode attention expects q[1,H,1,D]")
+    if cache_keys.ndim != 4 or cache_keys.shape[0] != 1:
+        raise ValueError("static K cache must be [1,KVH,L,D]")
+    if cache_values.shape != cache_keys.shape:
+        raise ValueError("static K/V cache shapes must match")
+    if not q.is_contiguous() or not cache_keys.is_contiguous() or not cache_values.is_contiguous():
+        raise ValueError("GQA decode attention tensors must be contiguous")
+    heads, head_dim = q.shape[1], q.shape[3]
+    kv_heads = cache_keys.shape[1]
+    if head_dim != cache_keys.shape[3] or heads % kv_heads:
+        raise ValueError("GQA decode attention head layout does not match cache")
+    if not q.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    if head_dim != 256:
+        raise ValueError("MI355X decode attention kernels are built for head_dim 256")
+    _need_bf16(q, cache_keys, cache_values)
+
+
+def gqa_decode_attention(
+    q: torch.Tensor,
+    cache_keys: torch.Tensor,
+    cache_values: torch.Tensor,
+    valid_length: torch.Tensor,
+    scale: float,
+    *,
+    splits: int = 4,
+    block_n: int = 64,
+    packed_gate: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One decode attention step over a static cache. reference kernels.py:1031.
+
+    ``valid_length`` is a device int64 scalar that already includes the
+    current token. With ``packed_gate`` (the packed QGKV row) the output gate
+    of reference kernels.py:312 is fused into the combine. Returns
+    ``[1, 1, H*D]`` bf16.
+    """
+
+    _check_decode_attention(q, cache_keys, cache_values)
+    heads, head_dim = q.shape[1], q.shape[3]
+    kv_heads, cache_len = cache_keys.shape[1], cache_keys.shape[2]
+    if valid_length.dtype != torch.int64 or valid_length.device != q.device:
+        raise ValueError("valid_length must be an int64 tensor on the GPU")
+    floats = _lib.load().q35_gqa_decode_workspace(cache_len, heads, kv_heads, head_dim)
+    workspace = torch.empty(floats, device=q.device, dtype=torch.float32)
+    out = torch.empty((1, 1, heads * head_dim), device=q.device, dtype=q.dtype)
+    gate_ptr = None
+    if packed_gate is not None:
+        if packed_gate.shape[-1] < 2 * heads * head_dim or not packed_gate.is_contiguous():
+            raise ValueError("packed gate does not match the attention heads")
+        gate_ptr = packed_gate.data_ptr()
+    _lib.call("q35_gqa_decode", q.data_ptr(), cache_keys.data_ptr(), cache_values.data_ptr(),
+              valid_length.data_ptr(), float(scale), gate_ptr, out.data_ptr(), workspace.data_ptr(),
+              floats, heads, kv_heads, head_dim, cache_len, _stream(q))
+    return out
+
+
+def gqa_prefill_attention(
+    q: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    scale: float,
+    *,
+    kv_start: int = 0,
+) -> torch.Tensor:
+    """Causal GQA prefill attention: ``q [B,QH,L,D]`` attends to
+    ``keys/values [B,KVH,C,D]`` positions ``[0, kv_start + i]``. Returns
+    ``[B, L, QH*D]`` bf16. Replaces the prefill attention interface call of
+    reference integration.py:360-372."""
+
+    if q.ndim != 4 or keys.ndim != 4 or keys.shape != values.shape:
+        raise ValueError("prefill attention expects q[B,QH,L,D] and K/V[B,KVH,C,D]")
+    batch, heads, seq_len, dim = q.shape
+    kv_heads, cache_len = keys.shape[1], keys.shape[2]
+    if keys.shape[0] != batch or keys.shape[3] != dim or heads % kv_heads:
+        raise ValueError("prefill attention head layout does not match")
+    if kv_start < 0 or kv_start + seq_len > cache_len:
+        raise ValueError("prefill attention range exceeds the key/value length")
+    if not (q.is_contiguous() and keys.is_contiguous() and values.is_contiguous()):
+        raise ValueError("prefill attention tensors must be contiguous")
+    if not q.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    if dim != 256:
+        raise ValueError("MI355X prefill attention kernels are built for head_dim 256")
+    _need_bf16(q, keys, values)
+    out = torch.empty((batch, seq_len, heads * dim), device=q.device, dtype=q.dtype)
+    _lib.call("q35_gqa_prefill", q.data_ptr(), keys.data_ptr(), values.data_ptr(), out.data_ptr(),
+              batch, heads, kv_heads, dim, seq_len, cache_len, kv_start, float(scale), _stream(q))
+    return out
+
+
+# ------------------------------------------------------------------ A8W8
+def quantize_weight_i8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel symmetric int8 weights and fp32 ``[N,1]`` scales.
+    reference explore_runtime_quantization.py:142-155."""
+
+    if weight.ndim != 2 or not weight.is_cuda or not weight.is_contiguous():
+        raise ValueError("weight quantisation expects a contiguous GPU [N,K] tensor")
+    _need_bf16(weight)
+    n, k = weight.shape
+    wq = torch.empty((n, k), device=weight.device, dtype=torch.int8)
+    scale = torch.empty((n, 1), device=weight.device, dtype=torch.float32)
+    _lib.call("q35_quant_weight_i8", weight.data_ptr(), wq.data_ptr(), scale.data_ptr(), n, k,
+              _stream(weight))
+    return wq, scale
+
+
+def quantize_act_i8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-token dynamic symmetric int8 activations and fp32 ``[M,1]`` scales
+    (the scaled_int8_quant call of reference explore_runtime_quantization.py:167-172)."""
+
+    rows, k = _rows_and_width(x)
+    _need_bf16(x)
+    xq = torch.empty(x.shape, device=x.device, dtype=torch.int8)
+    scale = torch.empty((rows, 1), device=x.device, dtype=torch.float32)
+    _lib.call("q35_quant_act_i8", x.data_ptr(), xq.data_ptr(), scale.data_ptr(), rows, k,
+              _stream(x))
+    return xq, scale
+
+
+def a8w8_linear(
+    x: torch.Tensor,
+    weight_q: torch.Tensor,
+    weight_scale: torch.Tensor,
+    *,
+    return_quant: bool = False,
+    return_acc: bool = False,
+):
+    """A8W8 linear: per-token int8 quantisation of ``x``, int32 dot products
+    against per-channel int8 weights, bf16 dequantised output
+    (reference explore_runtime_quantization.py:161-181). For one token the
+    quantisation is fused into the GEMV launch."""
+
+    k = x.shape[-1]
+    if weight_q.ndim != 2 or weight_q.shape[1] != k or weight_q.dtype != torch.int8:
+        raise ValueError("A8W8 weight must be int8 [N,K] matching the input")
+    if k % 16:
+        raise ValueError("A8W8 linear needs K to be a multiple of 16")
+    if not x.is_cuda or not weight_q.is_contiguous():
+        raise ValueError("A8W8 tensors must be contiguous GPU tensors")
+    _need_bf16(x)
+    x2 = x.reshape(-1, k).contiguous()
+    m, n = x2.shape[0], weight_q.shape[0]
+    sw = weight_scale.reshape(-1).float().contiguous()
+    if sw.numel() != n:
+        raise ValueError("A8W8 weight scale must have one value per output channel")
+    xq = torch.empty((m, k), device=x.device, dtype=torch.int8)
+    sx = torch.empty((m, 1), device=x.device, dtype=torch.float32)
+    y = torch.empty((m, n), device=x.device, dtype=_BF16)
+    acc = torch.empty((m, n), device=x.device, dtype=torch.int32) if return_acc else None
+    _lib.call("q35_gemv_a8w8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), weight_q.data_ptr(),
+              sw.data_ptr(), y.data_ptr(), _lib.ptr(acc), m, n, k, _stream(x))
+    y = y.reshape(*x.shape[:-1], n)
+    if not (return_quant or return_acc):
+        return y
+    extra = []
+    if return_quant:
+        extra += [xq, sx]
+    if return_acc:
+        extra.append(acc)
+    return (y, *extra)
+
+
+# ------------------------------------------------------------------ out of scope
+def _vision_out_of_scope(name: str):
+    def fn(*args, **kwargs):
+        raise NotImplementedError(
+            f"{name} belongs to the vision encoder, which this MI355X build does not implement"
+        )
+
+    fn.__name__ = name
+    return fn
+
+
+layer_norm = _vision_out_of_scope("layer_norm")
+residual_add_layer_norm = _vision_out_of_scope("residual_add_layer_norm")
+position_embed_add = _vision_out_of_scope("position_embed_add")
+vision_qkv_rope = _vision_out_of_scope("vision_qkv_rope")
+
+
+def sigmoid_mul(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """``x * bf16(sigmoid(gate))`` (reference kernels.py:266-282; unused by the
+    reference integration). Expressed through the attention-gate kernel with a
+    packed stride of 2*width and the gate in the second half."""
+
+    if x.shape != gate.shape or not x.is_contiguous() or not gate.is_contiguous():
+        raise ValueError("x and gate must be contiguous tensors with identical shape")
+    width = x.shape[-1]
+    packed = torch.cat((gate, gate), dim=-1).contiguous()
+    return attention_gate_mul(x, packed, width)
+
+
+DEFAULT_SCALE = 1.0 / math.sqrt(256)

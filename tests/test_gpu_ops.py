@@ -1,0 +1,458 @@
+"""GPU parity of every operator against the CPU oracle on identical seeded inputs.
+
+Inputs are drawn on the CPU in fp32 from seeded generators, cast to bf16 and
+copied to the GPU, so both sides see the same bits. Tolerances (written per
+assertion): bf16/fp32 outputs rtol 1e-2 / atol 1e-3; int8 quantisation, int32
+accumulators and argmax indices bit-exact; delta-rule state 1e-3 relative.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import a8w8 as oa
+from oracle import ops as ref
+from tests.conftest import KERNEL_SEED, gen
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 1e-3
+BF = torch.bfloat16
+
+
+def randn(g, *shape, scale=1.0, mean=0.0):
+    return (torch.randn(*shape, generator=g) * scale + mean).to(BF)
+
+
+def close(actual, expected, rtol=RTOL, atol=ATOL):
+    torch.testing.assert_close(actual.detach().float().cpu(), expected.detach().float().cpu(),
+                               rtol=rtol, atol=atol)
+
+
+# ------------------------------------------------------------------ norms
+@pytest.mark.parametrize("width", [128, 256, 2048, 100])
+def test_rms_norm(gpu, width):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED)
+    x = randn(g, 7, width)
+    w = randn(g, width)
+    out = K.rms_norm(x.to(gpu), w.to(gpu))
+    close(out, ref.rms_norm(x, w))
+
+
+def test_rms_norm_fp32_weight(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 1)
+    x = randn(g, 3, 2048)
+    w = torch.randn(2048, generator=g) * 0.02
+    close(K.rms_norm(x.to(gpu), w.to(gpu)), ref.rms_norm(x, w))
+
+
+@pytest.mark.parametrize("rows", [1, 7])
+def test_residual_add_rms_norm(gpu, rows):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 2)
+    r = randn(g, rows, 2048)
+    u = randn(g, rows, 2048)
+    w = randn(g, 2048, scale=0.02, mean=1.0)
+    r_out, y = K.residual_add_rms_norm(r.to(gpu), u.to(gpu), w.to(gpu))
+    er, ey = ref.residual_add_rms_norm(r, u, w)
+    assert torch.equal(r_out.cpu(), er), "bf16 residual add must be exact"
+    close(y, ey)
+
+
+def test_gated_rms_norm(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 3)
+    x = randn(g, 32, 128)
+    gate = randn(g, 32, 128)
+    w = randn(g, 128)
+    close(K.gated_rms_norm(x.to(gpu), gate.to(gpu), w.to(gpu)), ref.gated_rms_norm(x, gate, w))
+
+
+def test_silu_and_mul(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 4)
+    p = randn(g, 7, 12288)
+    close(K.silu_and_mul(p.to(gpu)), ref.silu_and_mul(p))
+
+
+def test_attention_gate_mul(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 5)
+    packed = randn(g, 1, 5, 5120)
+    x = randn(g, 1, 5, 2048)
+    close(K.attention_gate_mul(x.to(gpu), packed.to(gpu), 256), ref.attention_gate_mul(x, packed, 256))
+
+
+# ------------------------------------------------------------------ GEMV
+@pytest.mark.parametrize("n,k", [(6144, 2048), (8320, 2048), (5120, 2048), (2048, 2048),
+                                 (2048, 6144), (257, 128), (100, 40)])
+def test_linear(gpu, n, k):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 6)
+    x = randn(g, 1, 1, k)
+    w = randn(g, n, k, scale=0.02)
+    close(K.linear(x.to(gpu), w.to(gpu)), ref.linear(x, w))
+
+
+def test_config1_residual_norm_gemv(gpu):
+    """x, residual ~N(0,1) [1,2048], w ~N(1,0.02), eps 1e-6,
+    then W[6144,2048] ~N(0,0.02), fused in one launch."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED)
+    x = randn(g, 1, 2048)
+    r = randn(g, 1, 2048)
+    nw = randn(g, 2048, scale=0.02, mean=1.0)
+    W = randn(g, 6144, 2048, scale=0.02)
+    r_out, y = K.residual_norm_linear(r.to(gpu), x.to(gpu), nw.to(gpu), 1e-6, W.to(gpu))
+    er, en = ref.residual_add_rms_norm(r, x, nw, 1e-6)
+    assert torch.equal(r_out.cpu(), er)
+    close(y, ref.linear(en, W))
+
+
+@pytest.mark.parametrize("k", [2048, 6144])
+def test_swiglu_gemv(gpu, k):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 7)
+    x = randn(g, 1, 1, k)
+    w = randn(g, 12288, k, scale=0.02)
+    close(K.ppu_swiglu_gemv(x.to(gpu), w.to(gpu)), ref.swiglu_gemv(x, w))
+
+
+def test_swiglu_fused_residual(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 8)
+    r = randn(g, 1, 1, 2048)
+    u = randn(g, 1, 1, 2048)
+    nw = randn(g, 2048, scale=0.02)
+    w = randn(g, 12288, 2048, scale=0.02)
+    r_out, y = K.residual_norm_linear(r.to(gpu), u.to(gpu), nw.to(gpu), 1e-6, w.to(gpu), swiglu=True)
+    er, en = ref.residual_add_rms_norm(r, u, nw)
+    assert torch.equal(r_out.cpu(), er)
+    close(y, ref.swiglu_gemv(en, w))
+
+
+# ------------------------------------------------------------------ lm_head
+@pytest.mark.parametrize("v,k", [(257, 128), (248320, 2048), (5000, 2048)])
+def test_lm_head_argmax(gpu, v, k):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 9)
+    h = randn(g, 1, k)
+    w = randn(g, v, k, scale=0.02 if k == 2048 else 1.0)
+    got = K.lm_head_argmax(h.to(gpu), w.to(gpu))
+    assert got.dtype == torch.int64 and got.shape == (1, 1)
+    exp = ref.lm_head_argmax(h, w)
+    if int(got) != int(exp):
+        # Only acceptable when the two bf16 logits tie within one fp32 rounding.
+        logits = h.float() @ w.float().t()
+        a, b = float(logits[0, int(got)]), float(logits[0, int(exp)])
+        pytest.fail(f"argmax {int(got)} vs {int(exp)}: logits {a} vs {b}")
+
+
+def test_lm_head_ties(gpu):
+    from ppu_amd import kernels as K
+
+    h = torch.zeros(1, 128, dtype=BF)
+    w = torch.zeros(257, 128, dtype=BF)
+    assert int(K.lm_head_argmax(h.to(gpu), w.to(gpu))) == 0
+    g = gen(KERNEL_SEED + 10)
+    h = randn(g, 1, 2048)
+    w = randn(g, 9000, 2048, scale=0.02)
+    w[7777] = w[123]
+    w[8000] = w[123] * 4  # larger
+    w[8500] = w[8000]
+    got = int(K.lm_head_argmax(h.to(gpu), w.to(gpu)))
+    assert got == int(ref.lm_head_argmax(h, w))
+
+
+# ------------------------------------------------------------------ DeltaNet
+@pytest.mark.parametrize("seq_len", [1, 17])
+@pytest.mark.parametrize("extra", [0, 32])
+def test_causal_conv1d(gpu, seq_len, extra):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 11)
+    c = 64
+    x = randn(g, 1, seq_len, c + extra)
+    w = randn(g, c, 4)
+    st0 = randn(g, 1, c, 4)
+    st_ref = st0.clone()
+    exp = ref.causal_conv1d(x, w, st_ref)
+    st = st0.to(gpu)
+    got = K.causal_conv1d_fused(x.to(gpu), w.to(gpu), st)
+    close(got, exp)
+    assert torch.equal(st.cpu(), st_ref)
+
+
+def _delta_inputs(g, seq_len, heads=16, dim=128):
+    qkv_w = 3 * heads * dim
+    packed_w = qkv_w + heads * dim + 2 * heads
+    qkv = randn(g, 1, seq_len, qkv_w)
+    packed = randn(g, 1, seq_len, packed_w)
+    packed[..., :qkv_w] = qkv
+    a_log = randn(g, heads)
+    dt_bias = randn(g, heads)
+    state = torch.randn(1, heads, dim, dim, generator=g) * 0.01
+    return qkv, packed, a_log, dt_bias, state
+
+
+@pytest.mark.parametrize("seq_len", [1, 3, 64])
+def test_delta_recurrent(gpu, seq_len):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 12)
+    qkv, packed, a_log, dt_bias, state = _delta_inputs(g, seq_len)
+    st_ref = state.clone()
+    exp = ref.delta_recurrent(qkv, packed, a_log, dt_bias, st_ref)
+    st = state.to(gpu)
+    got = K.delta_recurrent_fused(qkv.to(gpu), packed.to(gpu), a_log.to(gpu), dt_bias.to(gpu), st,
+                                  precompute_factors=True)
+    close(got, exp)
+    # state: 1e-3 relative (BASELINE tolerance), plus a tiny absolute floor.
+    torch.testing.assert_close(st.cpu(), st_ref, rtol=1e-3, atol=1e-6)
+
+
+def test_config4_delta_64_steps(gpu):
+    """16 heads x 128, S ~N(0,0.1), conv width 4 on q/k/v,
+    beta = sigmoid(N(0,1)), g = -softplus(N(0,1)) (A_log = 0, dt_bias = 0),
+    64 sequential decode tokens through the fused conv+delta+gated-norm kernel,
+    against the oracle chain conv -> delta -> gated norm."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 13)
+    heads, dim = 16, 128
+    conv_dim = 3 * heads * dim
+    packed_w = 8320
+    conv_w = randn(g, conv_dim, 4, scale=0.02)
+    a_log = torch.zeros(heads, dtype=BF)
+    dt_bias = torch.zeros(heads, dtype=BF)
+    norm_w = randn(g, dim, scale=0.02, mean=1.0)
+    state = torch.randn(1, heads, dim, dim, generator=g) * 0.1
+    conv_state = torch.zeros(1, conv_dim, 4, dtype=BF)
+    st_ref, cs_ref = state.clone(), conv_state.clone()
+    st_gpu, cs_gpu = state.to(gpu), conv_state.to(gpu)
+    args_gpu = (conv_w.to(gpu), cs_gpu, a_log.to(gpu), dt_bias.to(gpu), st_gpu, norm_w.to(gpu), 1e-6)
+    worst = 0.0
+    for step in range(64):
+        packed = randn(g, 1, 1, packed_w)
+        qkv = ref.causal_conv1d(packed, conv_w, cs_ref)
+        core = ref.delta_recurrent(qkv, packed, a_log, dt_bias, st_ref)
+        z = packed[..., conv_dim : conv_dim + heads * dim].reshape(-1, dim)
+        exp = ref.gated_rms_norm(core.reshape(-1, dim), z, norm_w)
+        got = K.delta_decode_fused(packed.to(gpu), *args_gpu)
+        close(got, exp)
+        worst = max(worst, float(((st_gpu.cpu() - st_ref).abs().max() / st_ref.abs().max())))
+    assert torch.equal(cs_gpu.cpu(), cs_ref)
+    torch.testing.assert_close(st_gpu.cpu(), st_ref, rtol=1e-3, atol=1e-5)
+    assert worst < 1e-3
+
+
+def test_delta_invariant_beta0_alpha1(gpu):
+    """With beta = 0 (b -> -inf) and alpha = 1 (A_log -> -inf) the state is unchanged."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 14)
+    qkv, packed, _, _, state = _delta_inputs(g, 1)
+    packed[..., -32:] = -1e4  # a and b: beta = sigmoid(-1e4) = 0
+    a_log = torch.full((16,), -1e4)
+    dt_bias = torch.zeros(16)
+    st = state.to(gpu)
+    K.delta_recurrent_fused(qkv.to(gpu), packed.to(gpu), a_log.to(gpu), dt_bias.to(gpu), st)
+    assert torch.equal(st.cpu(), state)
+
+
+# ------------------------------------------------------------------ attention
+def _qgkv_inputs(g, seq_len):
+    q_heads, kv_heads, dim, rot = 8, 2, 256, 64
+    packed = randn(g, 1, seq_len, 2 * q_heads * dim + 2 * kv_heads * dim)
+    qw = randn(g, dim)
+    kw = randn(g, dim)
+    cos = randn(g, 1, seq_len, rot)
+    sin = randn(g, 1, seq_len, rot)
+    return packed, qw, kw, cos, sin
+
+
+def test_qgkv_norm_rope(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 15)
+    packed, qw, kw, cos, sin = _qgkv_inputs(g, 5)
+    kwargs = dict(q_heads=8, kv_heads=2, dim=256, rotary_dim=64)
+    eq, ek, ev = ref.qgkv_norm_rope(packed, qw, kw, cos, sin, **kwargs)
+    q, k, v = K.qgkv_norm_rope(packed.to(gpu), qw.to(gpu), kw.to(gpu), cos.to(gpu), sin.to(gpu), **kwargs)
+    close(q, eq)
+    close(k, ek)
+    assert torch.equal(v.cpu(), ev)
+
+
+def test_qgkv_cache_write(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 16)
+    packed, qw, kw, cos, sin = _qgkv_inputs(g, 5)
+    kwargs = dict(q_heads=8, kv_heads=2, dim=256, rotary_dim=64)
+    eq, ek, ev = ref.qgkv_norm_rope(packed, qw, kw, cos, sin, **kwargs)
+    kc = torch.zeros(1, 2, 13, 256, dtype=BF, device=gpu)
+    vc = torch.zeros_like(kc)
+    start = torch.tensor(3, dtype=torch.int64, device=gpu)
+    q, k, v = K.qgkv_norm_rope(packed.to(gpu), qw.to(gpu), kw.to(gpu), cos.to(gpu), sin.to(gpu),
+                               cache_key=kc, cache_value=vc, cache_start=start, **kwargs)
+    close(q, eq)
+    close(kc[:, :, 3:8], ek)
+    assert torch.equal(vc[:, :, 3:8].cpu(), ev)
+    assert not kc[:, :, :3].any() and not vc[:, :, 8:].any()
+    # A start past the end writes nothing (no out-of-bounds store).
+    start.fill_(12)
+    kc.zero_()
+    K.qgkv_norm_rope(packed.to(gpu), qw.to(gpu), kw.to(gpu), cos.to(gpu), sin.to(gpu),
+                     cache_key=kc, cache_value=vc, cache_start=start, **kwargs)
+    assert kc[:, :, 12].abs().sum() > 0
+
+
+@pytest.mark.parametrize("cache_len,n_valid", [(512, 1), (512, 7), (512, 370), (512, 512),
+                                                (2048, 2048), (8192, 8192), (8192, 5000)])
+def test_gqa_decode_attention(gpu, cache_len, n_valid):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 17)
+    q = randn(g, 1, 8, 1, 256)
+    kc = randn(g, 1, 2, cache_len, 256)
+    vc = randn(g, 1, 2, cache_len, 256)
+    length = torch.tensor(n_valid, dtype=torch.int64)
+    exp = ref.gqa_decode_attention(q, kc, vc, length, 0.0625)
+    got = K.gqa_decode_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), length.to(gpu), 0.0625)
+    close(got, exp)
+
+
+def test_gqa_decode_gate_fused(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 18)
+    q = randn(g, 1, 8, 1, 256)
+    kc = randn(g, 1, 2, 512, 256)
+    vc = randn(g, 1, 2, 512, 256)
+    packed = randn(g, 1, 1, 5120)
+    length = torch.tensor(300, dtype=torch.int64)
+    att = ref.gqa_decode_attention(q, kc, vc, length, 0.0625)
+    exp = ref.attention_gate_mul(att, packed, 256)
+    got = K.gqa_decode_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), length.to(gpu), 0.0625,
+                                 packed_gate=packed.to(gpu))
+    close(got, exp)
+
+
+@pytest.mark.parametrize("seq_len,kv_start", [(33, 0), (64, 16)])
+def test_prefill_attention(gpu, seq_len, kv_start):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 19)
+    q = randn(g, 1, 8, seq_len, 256)
+    kc = randn(g, 1, 2, kv_start + seq_len + 5, 256)
+    vc = randn(g, 1, 2, kv_start + seq_len + 5, 256)
+    exp = ref.prefill_attention(q, kc, vc, 0.0625, kv_start)
+    got = K.gqa_prefill_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), 0.0625, kv_start=kv_start)
+    close(got, exp)
+
+
+# ------------------------------------------------------------------ A8W8
+@pytest.mark.parametrize("n,k", [(12288, 2048), (2048, 6144), (96, 64)])
+def test_quantize_weight_bit_exact(gpu, n, k):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 20)
+    w = randn(g, n, k, scale=0.02)
+    w[0] = 0  # zero row -> scale 1
+    wq, s = K.quantize_weight_i8(w.to(gpu))
+    ewq, es = oa.quantize_weight(w)
+    assert np.array_equal(wq.cpu().numpy(), ewq)
+    assert np.array_equal(s.cpu().numpy(), es)
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("n,k", [(12288, 2048), (2048, 6144)])
+def test_a8w8_linear_config2(gpu, m, n, k):
+    """int8 quantisation and int32 accumulators bit-exact,
+    bf16 dequant output within rtol 1e-2 / atol 1e-3."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 21)
+    w = randn(g, n, k, scale=0.02)
+    x = randn(g, m, k)
+    x[0, :5] = 0
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    y, xq, sx, acc = K.a8w8_linear(x.to(gpu), wq, sw, return_quant=True, return_acc=True)
+    ewq, esw = oa.quantize_weight(w)
+    ey, exq, esx, eacc = oa.a8w8_linear(x, ewq, esw)
+    assert np.array_equal(xq.cpu().numpy(), exq)
+    assert np.array_equal(sx.cpu().numpy(), esx)
+    assert np.array_equal(acc.cpu().numpy(), eacc)
+    close(y, ey)
+
+
+def test_a8w8_zero_row(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 22)
+    w = randn(g, 64, 2048, scale=0.02)
+    x = torch.zeros(1, 2048, dtype=BF)
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    y, xq, sx = K.a8w8_linear(x.to(gpu), wq, sw, return_quant=True)
+    assert not xq.any() and float(sx) == 0.0 and not y.float().any()
+
+
+# ------------------------------------------------------------------ boundary
+def test_single_hip_runtime(gpu):
+    """libq35 binds to the HIP runtime torch loaded (one libamdhip64 mapped)."""
+    maps = open("/proc/self/maps").read().splitlines()
+    hip = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(hip) == 1, hip
+    assert any("libq35.so" in line for line in maps)
+
+
+def test_graph_capture_replay(gpu):
+    """ctypes launches on torch's current stream are captured by
+    torch.cuda.graph; replays (with eager work and syncs between) match eager."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 30)
+    r = randn(g, 1, 2048).to(gpu)
+    u = randn(g, 1, 2048).to(gpu)
+    nw = randn(g, 2048, scale=0.02, mean=1.0).to(gpu)
+    W = randn(g, 6144, 2048, scale=0.02).to(gpu)
+    lw = randn(g, 3000, 6144, scale=0.02).to(gpu)
+    _, y0 = K.residual_norm_linear(r, u, nw, 1e-6, W)
+    t0 = K.lm_head_argmax(y0.reshape(1, -1), lw)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            K.residual_norm_linear(r, u, nw, 1e-6, W)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _, y = K.residual_norm_linear(r, u, nw, 1e-6, W)
+        t = K.lm_head_argmax(y.reshape(1, -1), lw)
+    for i in range(3):
+        y.zero_()
+        t.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y0), f"replay {i}"
+        assert int(t) == int(t0), f"replay {i}"
+        _ = (r * 2).sum().item()  # eager work between replays
