@@ -137,10 +137,14 @@ int q35_gqa_decode(const void* q, const void* K, const void* V, const void* vali
                    int QH, int KVH, int D, int cache_len, void* stream);
 
 /* Causal GQA prefill attention: q [B,QH,L,D], K/V [B,KVH,cache_len,D] holding
- * the prompt at kv_start; out [B,L,QH*D]. Replaces the prefill
- * ALL_ATTENTION_FUNCTIONS call of qwen35_fused/integration.py:360-372. */
+ * the L prompt tokens from position start; query row i attends to keys
+ * [0, start + i]. start = *valid_len - L when valid_len (int64 device scalar,
+ * already including the L tokens) is given, else kv_start. out [B,L,QH*D].
+ * Replaces the prefill ALL_ATTENTION_FUNCTIONS call of
+ * qwen35_fused/integration.py:360-372. */
 int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int B, int QH, int KVH,
-                    int D, int L, int cache_len, int kv_start, float scale, void* stream);
+                    int D, int L, int cache_len, int kv_start, const void* valid_len, float scale,
+                    void* stream);
 
 /* ---- A8W8 -------------------------------------------------------------- */
 

@@ -281,11 +281,17 @@ __global__ __launch_bounds__(256) void gqa_decode_combine(const float* __restric
 // iteration, lane = (key kk = lane/16, 16-dim slice); online softmax in fp32.
 __global__ __launch_bounds__(256) void gqa_prefill_rows(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
-    uint16_t* __restrict__ out, int B, int QH, int KVH, int L, int cache_len, int kv_start,
-    float scale) {
+    uint16_t* __restrict__ out, int B, int QH, int KVH, int L, int cache_len, int kv_start_host,
+    const long long* __restrict__ valid_len, float scale) {
   const int lane = threadIdx.x & 63;
   const long long wv = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wv >= (long long)B * QH * L) return;
+  // With a device length (static cache, already including these L tokens)
+  // the prompt starts at valid_len - L; the bound keeps reads in the cache.
+  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  if (ks < 0) ks = 0;
+  if (ks + L > cache_len) ks = cache_len - L;
+  const int kv_start = (int)ks;
   // Heavy (late) rows first so that the tail of the grid is short.
   const int i = L - 1 - (int)(wv % L);
   const int h = (int)((wv / L) % QH);
@@ -421,16 +427,17 @@ int q35_gqa_decode(const void* q, const void* K, const void* V, const void* vali
 }
 
 int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int B, int QH, int KVH,
-                    int D, int L, int cache_len, int kv_start, float scale, hipStream_t stream) {
+                    int D, int L, int cache_len, int kv_start, const void* valid_len, float scale,
+                    hipStream_t stream) {
   Q35_CHECK_ARG(D == kAD && KVH > 0 && QH % KVH == 0 && B >= 0 && L >= 0);
-  Q35_CHECK_ARG(kv_start >= 0 && kv_start + L <= cache_len);
+  Q35_CHECK_ARG(L <= cache_len && (valid_len || (kv_start >= 0 && kv_start + L <= cache_len)));
   Q35_CHECK_ARG(q35_aligned16(q) && q35_aligned16(K) && q35_aligned16(V) && q35_aligned16(out));
   const long long waves = (long long)B * QH * L;
   if (waves == 0) return 0;
   Q35_CHECK_ARG(waves < (1ll << 31));
   gqa_prefill_rows<<<(unsigned)((waves + 3) / 4), 256, 0, stream>>>(
       (const uint16_t*)q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)out, B, QH, KVH, L,
-      cache_len, kv_start, scale);
+      cache_len, kv_start, (const long long*)valid_len, scale);
   return q35_last_error();
 }
 

@@ -3,28 +3,33 @@
 //
 //   y[n] = bf16( sum_k W[n, k] * x[k] )     W row-major [N, K] bf16, fp32 acc
 //
-// Work split: one wave64 owns R consecutive weight rows. Lane l reads the
-// 16-byte group k = c*512 + 8l of every row for chunk c = 0..NCH-1, so each
-// load instruction of a wave moves one contiguous 1 KiB segment of a row and
-// all R*NCH loads of a lane are issued before the first one is consumed. The
-// activation vector is loaded (or computed by the prologue) after the weight
-// loads are in flight. Per-row partial sums are reduced with the DPP wave
-// reduction. Weights are read exactly once, so the kernel is bound by HBM
-// bandwidth: bytes per launch = 2*N*K (+ 2*K + 2*N).
+// Work split: a workgroup of WV wave64s owns WV*R consecutive weight rows, one
+// wave R rows. Lane l reads the 16-byte group k = c*512 + 8l of each of its
+// rows for chunk c = 0..NCH-1, so every load instruction of a wave moves one
+// contiguous 1 KiB segment of a row, and all R*NCH loads of a lane are in
+// flight before the first is consumed. The activation vector is loaded once
+// per workgroup (16-byte loads issued *before* the weight stream, so the
+// in-order vmcnt lets the prologue run while weights are still arriving),
+// transformed by the prologue and staged in LDS; the barrier between the
+// prologue and the dot product orders LDS only, so the weight loads stay in
+// flight across it. Row sums use the DPP wave reduction. Weights are read
+// exactly once: bytes per launch = 2*N*K + activation + 2*N.
 //
-// Prologues (computed redundantly by every wave from L2-resident vectors):
+// Prologues:
 //   RMSNORM : x = bf16(x * rsqrt(mean(x^2)+eps) * (1+w))          [kernels.py:24-53]
 //   RESNORM : r' = bf16(r+u); x = RMSNorm(r'); block 0 stores r'  [kernels.py:56-112]
 // Epilogues:
 //   STORE   : y[n] = bf16(acc)                                    [F.linear, integration.py:185]
 //   SWIGLU  : rows n and N+n of a packed [gate; up] weight:
 //             y[n] = bf16(bf16(silu(bf16(g))) * bf16(u))          [kernels.py:183-263]
+//   TOP1    : key = (ordered bf16(acc), inverted row); one max key per
+//             workgroup into a candidate array                    [kernels.py:1093-1143]
 #include "q35_common.hpp"
 
 namespace {
 
 enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_RESNORM = 2 };
-enum { EPI_STORE = 0, EPI_SWIGLU = 1 };
+enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_TOP1 = 2 };
 
 struct GemvArgs {
   const uint16_t* W;    // [rows_total, K]
@@ -34,105 +39,55 @@ struct GemvArgs {
   uint16_t* r_out;      // RESNORM: r' written by block 0 (may be null)
   uint16_t* xn_out;     // normalised activation written by block 0 (may be null)
   uint16_t* y;          // output [N]
-  int N;                // output elements
+  unsigned long long* cand;  // TOP1: one key per workgroup
+  int N;                // output elements (TOP1: rows)
   int K;
   int nw_f32;
   float eps;
 };
 
-// Issue the loads of R rows x NCH chunks; rows at or past row_end read as 0.
-template <int R, int NCH>
-Q35_DEV void load_rows(const uint16_t* __restrict__ W, int K, const int* rows, int row_end,
-                       int lane, uint4 (&w)[R][NCH]) {
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int k = c * 512 + lane * 8;
-      if (rows[r] < row_end && k < K) {
-        w[r][c] = ld_stream16(W + (size_t)rows[r] * K + k);
-      } else {
-        w[r][c] = make_uint4(0, 0, 0, 0);
-      }
-    }
+Q35_DEV void load_nw8(const GemvArgs& a, int k, float* w) {
+  if (a.nw_f32) {
+    const float4 lo = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.nw) + k);
+    const float4 hi = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.nw) + k + 4);
+    w[0] = lo.x; w[1] = lo.y; w[2] = lo.z; w[3] = lo.w;
+    w[4] = hi.x; w[5] = hi.y; w[6] = hi.z; w[7] = hi.w;
+  } else {
+    unpack8(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.nw) + k), w);
   }
 }
 
-// Activation chunk c of this lane, after the prologue; packed bf16.
-template <int NCH, int PRO>
-Q35_DEV void load_activation(const GemvArgs& a, int lane, bool writer, uint4 (&xv)[NCH]) {
-  if (PRO == PRO_NONE) {
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int k = c * 512 + lane * 8;
-      xv[c] = k < a.K ? *reinterpret_cast<const uint4*>(a.x + k) : make_uint4(0, 0, 0, 0);
-    }
-    return;
-  }
-  float s[NCH][8];
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int k = c * 512 + lane * 8;
-    if (k < a.K) {
-      unpack8(*reinterpret_cast<const uint4*>(a.x + k), s[c]);
-      if (PRO == PRO_RESNORM) {
-        float b[8];
-        unpack8(*reinterpret_cast<const uint4*>(a.u + k), b);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s[c][j] = round_bf(s[c][j] + b[j]);
-        if (writer && a.r_out) *reinterpret_cast<uint4*>(a.r_out + k) = pack8(s[c]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s[c][j] = 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss += s[c][j] * s[c][j];
-  }
-  const float inv = rsqrt_cr(wave_sum(ss) / (float)a.K + a.eps);
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int k = c * 512 + lane * 8;
-    float o[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float wj = k < a.K ? (a.nw_f32 ? reinterpret_cast<const float*>(a.nw)[k + j]
-                                           : bf2f(reinterpret_cast<const uint16_t*>(a.nw)[k + j]))
-                               : 0.f;
-      o[j] = s[c][j] * inv * (1.0f + wj);
-    }
-    xv[c] = pack8(o);
-    if (writer && a.xn_out && k < a.K) *reinterpret_cast<uint4*>(a.xn_out + k) = xv[c];
-  }
-}
-
-template <int R, int NCH>
-Q35_DEV void dot_rows(const uint4 (&w)[R][NCH], const uint4 (&xv)[NCH], float (&acc)[R]) {
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    float xf[8];
-    unpack8(xv[c], xf);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float wf[8];
-      unpack8(w[r][c], wf);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[r] = fmaf(wf[j], xf[j], acc[r]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-}
-
-template <int R, int NCH, int PRO, int EPI>
-__global__ __launch_bounds__(256) void gemv_bf16(const GemvArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+template <int WV, int R, int NCH, int PRO, int EPI>
+__global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
+  constexpr int NT = WV * 64;
+  constexpr int NV = NCH * 64;                  // activation uint4 groups
+  constexpr int PER = (NV + NT - 1) / NT;       // groups per thread
   constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;  // outputs per wave
-  const int n0 = wave * P;
+  __shared__ uint4 xs[NV];
+  __shared__ float red[WV];
+  __shared__ unsigned long long best_s[WV];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int n0 = (blockIdx.x * WV + wid) * P;
+  const bool writer = blockIdx.x == 0;
+
+  // 1. activation loads (cooperative, before the weight stream).
+  uint4 xa[PER], ua[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = tid + j * NT;
+    if (i < NV && i * 8 < a.K) {
+      xa[j] = *reinterpret_cast<const uint4*>(a.x + i * 8);
+      if (PRO == PRO_RESNORM) ua[j] = *reinterpret_cast<const uint4*>(a.u + i * 8);
+    } else {
+      xa[j] = make_uint4(0, 0, 0, 0);
+      ua[j] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // 2. weight stream.
   int rows[R];
   int row_end;
   if (EPI == EPI_SWIGLU) {
@@ -147,43 +102,131 @@ __global__ __launch_bounds__(256) void gemv_bf16(const GemvArgs a) {
     for (int i = 0; i < R; ++i) rows[i] = n0 + i;
     row_end = a.N;
   }
-  const bool writer = blockIdx.x == 0 && threadIdx.x < 64;
-  if (n0 >= a.N && !writer) return;
-
   uint4 w[R][NCH];
-  load_rows<R, NCH>(a.W, a.K, rows, row_end, lane, w);
-  uint4 xv[NCH];
-  load_activation<NCH, PRO>(a, lane, writer, xv);
-  if (n0 >= a.N) return;
-  float acc[R];
-  dot_rows<R, NCH>(w, xv, acc);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int k = c * 512 + lane * 8;
+      w[r][c] = (rows[r] < row_end && k < a.K) ? ld_stream16(a.W + (size_t)rows[r] * a.K + k)
+                                                : make_uint4(0, 0, 0, 0);
+    }
+  }
 
-  if (lane == 0) {
-    if (EPI == EPI_STORE) {
+  // 3. prologue into LDS.
+  if (PRO == PRO_NONE) {
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (n0 + r < a.N) a.y[n0 + r] = (uint16_t)f2bf(acc[r]);
-    } else {
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid + j * NT;
+      if (i < NV) xs[i] = xa[j];
+    }
+  } else {
+    float s[PER][8];
+    float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < P; ++i) {
-        if (n0 + i < a.N) {
-          const float g = round_bf(acc[i]);
-          const float up = round_bf(acc[P + i]);
-          a.y[n0 + i] = (uint16_t)f2bf(round_bf(silu_f(g)) * up);
+    for (int j = 0; j < PER; ++j) {
+      unpack8(xa[j], s[j]);
+      if (PRO == PRO_RESNORM) {
+        float b[8];
+        unpack8(ua[j], b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[j][e] = round_bf(s[j][e] + b[e]);
+        const int i = tid + j * NT;
+        if (writer && a.r_out && i < NV && i * 8 < a.K)
+          *reinterpret_cast<uint4*>(a.r_out + i * 8) = pack8(s[j]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += s[j][e] * s[j][e];
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[wid] = ss;
+    lds_barrier();
+    float tot = 0.f;
+#pragma unroll
+    for (int v = 0; v < WV; ++v) tot += red[v];
+    const float inv = rsqrt_cr(tot / (float)a.K + a.eps);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid + j * NT;
+      if (i < NV) {
+        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (i * 8 < a.K) {
+          float wn[8];
+          load_nw8(a, i * 8, wn);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = s[j][e] * inv * (1.0f + wn[e]);
         }
+        const uint4 v = pack8(o);
+        xs[i] = v;
+        if (writer && a.xn_out && i * 8 < a.K) *reinterpret_cast<uint4*>(a.xn_out + i * 8) = v;
       }
     }
   }
+  lds_barrier();
+
+  // 4. dot products.
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    float xf[8];
+    unpack8(xs[c * 64 + lane], xf);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float wf[8];
+      unpack8(w[r][c], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[r] = fmaf(wf[e], xf[e], acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+
+  // 5. epilogue.
+  if (EPI == EPI_TOP1) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (n0 + r < a.N) best = u64_max(best, top1_key(round_bf(acc[r]), (uint32_t)(n0 + r)));
+    if (lane == 0) best_s[wid] = best;
+    lds_barrier();
+    if (tid == 0) {
+      uint64_t b = best_s[0];
+#pragma unroll
+      for (int v = 1; v < WV; ++v) b = u64_max(b, best_s[v]);
+      a.cand[blockIdx.x] = b;
+    }
+    return;
+  }
+  if (lane < P && n0 + lane < a.N) {
+    float v;
+    if (EPI == EPI_STORE) {
+      v = acc[0];
+#pragma unroll
+      for (int r = 1; r < R; ++r) v = lane == r ? acc[r] : v;
+    } else {
+      float g = acc[0], up = acc[P];
+#pragma unroll
+      for (int i = 1; i < P; ++i) {
+        g = lane == i ? acc[i] : g;
+        up = lane == i ? acc[P + i] : up;
+      }
+      v = round_bf(silu_f(round_bf(g))) * round_bf(up);
+    }
+    a.y[n0 + lane] = (uint16_t)f2bf(v);
+  }
 }
 
-// Generic fallback for any K (multiple of 8 or not) and unaligned pointers:
-// one wave per output, scalar lane-strided loads. Used by small test shapes.
+// Generic fallback for any K and unaligned pointers: one wave per output,
+// scalar lane-strided loads. Used by small test shapes only.
 template <int PRO, int EPI>
 __global__ __launch_bounds__(256) void gemv_bf16_generic(const GemvArgs a) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const bool writer = blockIdx.x == 0 && threadIdx.x < 64;
-  if (n >= a.N && !writer) return;
+  const int wid = threadIdx.x >> 6;
+  const int n = blockIdx.x * 4 + wid;
+  const bool writer = blockIdx.x == 0 && wid == 0;
+  __shared__ unsigned long long best_s[4];
   float inv = 1.f;
   if (PRO != PRO_NONE) {
     float ss = 0.f;
@@ -208,120 +251,32 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(const GemvArgs a) {
       if (a.xn_out) a.xn_out[k] = (uint16_t)f2bf(xval(k));
     }
   }
-  if (n >= a.N) return;
   float g = 0.f, up = 0.f;
-  for (int k = lane; k < a.K; k += 64) {
-    const float xk = xval(k);
-    g = fmaf(bf2f(a.W[(size_t)n * a.K + k]), xk, g);
-    if (EPI == EPI_SWIGLU) up = fmaf(bf2f(a.W[(size_t)(a.N + n) * a.K + k]), xk, up);
+  if (n < a.N) {
+    for (int k = lane; k < a.K; k += 64) {
+      const float xk = xval(k);
+      g = fmaf(bf2f(a.W[(size_t)n * a.K + k]), xk, g);
+      if (EPI == EPI_SWIGLU) up = fmaf(bf2f(a.W[(size_t)(a.N + n) * a.K + k]), xk, up);
+    }
   }
   g = wave_sum(g);
   if (EPI == EPI_SWIGLU) up = wave_sum(up);
-  if (lane == 0) {
+  if (EPI == EPI_TOP1) {
+    if (lane == 0) best_s[wid] = n < a.N ? top1_key(round_bf(g), (uint32_t)n) : 0ull;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint64_t b = best_s[0];
+      for (int i = 1; i < 4; ++i) b = u64_max(b, best_s[i]);
+      a.cand[blockIdx.x] = b;
+    }
+    return;
+  }
+  if (lane == 0 && n < a.N) {
     if (EPI == EPI_STORE) {
       a.y[n] = (uint16_t)f2bf(g);
     } else {
       a.y[n] = (uint16_t)f2bf(round_bf(silu_f(round_bf(g))) * round_bf(up));
     }
-  }
-}
-
-template <int R, int NCH, int PRO, int EPI>
-int launch_fast(const GemvArgs& a, hipStream_t stream) {
-  constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;
-  const long long waves = (a.N + P - 1) / P;
-  const long long blocks = (waves + 3) / 4;
-  gemv_bf16<R, NCH, PRO, EPI><<<(unsigned)blocks, 256, 0, stream>>>(a);
-  return q35_last_error();
-}
-
-template <int PRO, int EPI>
-int dispatch(const GemvArgs& a, hipStream_t stream) {
-  bool aligned = (a.K % 8 == 0) && q35_aligned16(a.W) && q35_aligned16(a.x) &&
-                 (PRO != PRO_RESNORM || q35_aligned16(a.u)) && q35_aligned16(a.r_out) &&
-                 q35_aligned16(a.xn_out);
-  if (aligned) {
-    const int nch = (a.K + 511) / 512;
-    if constexpr (EPI == EPI_SWIGLU) {
-      if (nch == 4) return launch_fast<2, 4, PRO, EPI>(a, stream);
-      if (nch == 12) return launch_fast<2, 12, PRO, EPI>(a, stream);
-      if (nch == 1) return launch_fast<2, 1, PRO, EPI>(a, stream);
-    } else {
-      const bool wide = a.N >= 8192;
-      if (nch == 4) return wide ? launch_fast<2, 4, PRO, EPI>(a, stream)
-                                : launch_fast<1, 4, PRO, EPI>(a, stream);
-      if (nch == 12) return launch_fast<1, 12, PRO, EPI>(a, stream);
-      if (nch == 1) return launch_fast<2, 1, PRO, EPI>(a, stream);
-      if (nch == 2) return launch_fast<2, 2, PRO, EPI>(a, stream);
-    }
-  }
-  const unsigned blocks = (unsigned)((a.N + 3) / 4);
-  gemv_bf16_generic<PRO, EPI><<<blocks > 0 ? blocks : 1, 256, 0, stream>>>(a);
-  return q35_last_error();
-}
-
-// ------------------------------------------------------------ lm_head top-1
-// Each wave computes R logits, rounds them to bf16 (eager materialises bf16
-// logits before argmax), and folds them into a 64-bit key (ordered bf16
-// value, inverted index) so that one max reduction gives the largest value
-// and, among ties, the lowest index [kernels.py:1093-1143]. Waves reduce in
-// LDS; each workgroup writes one candidate key.
-template <int R, int NCH>
-__global__ __launch_bounds__(256) void lm_head_top1_blocks(const uint16_t* __restrict__ W,
-                                                           const uint16_t* __restrict__ x, int V,
-                                                           int K, unsigned long long* cand) {
-  const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
-  const int n0 = (blockIdx.x * 4 + wid) * R;
-  __shared__ unsigned long long best_s[4];
-  uint64_t best = 0;
-  if (n0 < V) {
-    int rows[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = n0 + r;
-    uint4 w[R][NCH];
-    load_rows<R, NCH>(W, K, rows, V, lane, w);
-    uint4 xv[NCH];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int k = c * 512 + lane * 8;
-      xv[c] = k < K ? *reinterpret_cast<const uint4*>(x + k) : make_uint4(0, 0, 0, 0);
-    }
-    float acc[R];
-    dot_rows<R, NCH>(w, xv, acc);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (n0 + r < V) best = u64_max(best, top1_key(round_bf(acc[r]), (uint32_t)(n0 + r)));
-  }
-  if (lane == 0) best_s[wid] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t b = best_s[0];
-    for (int i = 1; i < 4; ++i) b = u64_max(b, best_s[i]);
-    cand[blockIdx.x] = b;
-  }
-}
-
-__global__ __launch_bounds__(256) void lm_head_top1_generic(const uint16_t* __restrict__ W,
-                                                            const uint16_t* __restrict__ x, int V,
-                                                            int K, unsigned long long* cand) {
-  const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
-  const int n = blockIdx.x * 4 + wid;
-  __shared__ unsigned long long best_s[4];
-  uint64_t best = 0;
-  if (n < V) {
-    float acc = 0.f;
-    for (int k = lane; k < K; k += 64) acc = fmaf(bf2f(W[(size_t)n * K + k]), bf2f(x[k]), acc);
-    acc = wave_sum(acc);
-    best = top1_key(round_bf(acc), (uint32_t)n);
-  }
-  if (lane == 0) best_s[wid] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t b = best_s[0];
-    for (int i = 1; i < 4; ++i) b = u64_max(b, best_s[i]);
-    cand[blockIdx.x] = b;
   }
 }
 
@@ -340,6 +295,45 @@ __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __r
   }
 }
 
+template <int WV, int R, int NCH, int PRO, int EPI>
+long long launch_fast(const GemvArgs& a, hipStream_t stream) {
+  constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;
+  const long long blocks = (a.N + (long long)WV * P - 1) / ((long long)WV * P);
+  gemv_bf16<WV, R, NCH, PRO, EPI><<<(unsigned)blocks, WV * 64, 0, stream>>>(a);
+  return blocks;
+}
+
+bool fast_ok(const GemvArgs& a, int PRO) {
+  return (a.K % 512 == 0) && q35_aligned16(a.W) && q35_aligned16(a.x) &&
+         (PRO != PRO_RESNORM || q35_aligned16(a.u)) && q35_aligned16(a.r_out) &&
+         q35_aligned16(a.xn_out) && (PRO == PRO_NONE || q35_aligned16(a.nw));
+}
+
+// Shape -> tile choice (waves per workgroup, rows per wave), measured on
+// MI355X with rotating weights in a captured graph.
+template <int PRO, int EPI>
+int dispatch(const GemvArgs& a, hipStream_t stream) {
+  if (fast_ok(a, PRO)) {
+    const int nch = a.K / 512;
+    if constexpr (EPI == EPI_SWIGLU) {
+      if (nch == 4) { launch_fast<8, 2, 4, PRO, EPI>(a, stream); return q35_last_error(); }
+      if (nch == 12) { launch_fast<4, 2, 12, PRO, EPI>(a, stream); return q35_last_error(); }
+    } else {
+      if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI>(a, stream); return q35_last_error(); }
+      if (nch == 12) { launch_fast<4, 1, 12, PRO, EPI>(a, stream); return q35_last_error(); }
+      if (nch == 1) { launch_fast<4, 2, 1, PRO, EPI>(a, stream); return q35_last_error(); }
+      if (nch == 2) { launch_fast<4, 2, 2, PRO, EPI>(a, stream); return q35_last_error(); }
+    }
+  }
+  const unsigned blocks = (unsigned)((a.N + 3) / 4);
+  gemv_bf16_generic<PRO, EPI><<<blocks > 0 ? blocks : 1, 256, 0, stream>>>(a);
+  return q35_last_error();
+}
+
+// lm_head tile: 4 waves x 1 row per workgroup (fastest of the swept
+// {2,4,8} waves x {1,2,4,8} rows; a persistent grid-stride variant was slower).
+constexpr int kTopWV = 4, kTopR = 1;
+
 }  // namespace
 
 extern "C" {
@@ -353,7 +347,8 @@ int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_
   Q35_CHECK_ARG(prologue == 0 || norm_w);
   Q35_CHECK_ARG(prologue != 2 || u);
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
-             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, N, K, norm_w_f32, eps};
+             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
+             norm_w_f32, eps};
   if (prologue == 0) return dispatch<PRO_NONE, EPI_STORE>(a, stream);
   if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_STORE>(a, stream);
   return dispatch<PRO_RESNORM, EPI_STORE>(a, stream);
@@ -368,7 +363,8 @@ int q35_swiglu_gemv(const void* W, const void* x, const void* u, const void* nor
   Q35_CHECK_ARG(prologue == 0 || norm_w);
   Q35_CHECK_ARG(prologue != 2 || u);
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
-             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, N, K, norm_w_f32, eps};
+             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
+             norm_w_f32, eps};
   if (prologue == 0) return dispatch<PRO_NONE, EPI_SWIGLU>(a, stream);
   if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_SWIGLU>(a, stream);
   return dispatch<PRO_RESNORM, EPI_SWIGLU>(a, stream);
@@ -384,22 +380,19 @@ long long q35_lm_head_top1_workspace(int V, int K) {
 int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace,
                      long long workspace_slots, void* out, hipStream_t stream) {
   Q35_CHECK_ARG(V > 0 && K > 0 && W && x && workspace && out);
-  const long long need = q35_lm_head_top1_workspace(V, K);
-  Q35_CHECK_ARG(workspace_slots >= need && need < (1ll << 31));
-  unsigned long long* cand = (unsigned long long*)workspace;
-  const bool fast = K == 2048 && q35_aligned16(W) && q35_aligned16(x);
-  // fast: 4 waves x 4 rows per workgroup; generic: 4 waves x 1 row.
-  const long long nc = fast ? (V + 15) / 16 : (V + 3) / 4;
-  if (fast) {
-    lm_head_top1_blocks<4, 4><<<(unsigned)nc, 256, 0, stream>>>(
-        (const uint16_t*)W, (const uint16_t*)x, V, K, cand);
+  Q35_CHECK_ARG(workspace_slots >= q35_lm_head_top1_workspace(V, K) && V < (1 << 30));
+  GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, nullptr,
+             (unsigned long long*)workspace, V, K, 0, 0.f};
+  long long nc;
+  if (K == 2048 && fast_ok(a, PRO_NONE)) {
+    nc = launch_fast<kTopWV, kTopR, 4, PRO_NONE, EPI_TOP1>(a, stream);
   } else {
-    lm_head_top1_generic<<<(unsigned)nc, 256, 0, stream>>>(
-        (const uint16_t*)W, (const uint16_t*)x, V, K, cand);
+    nc = (V + 3) / 4;
+    gemv_bf16_generic<PRO_NONE, EPI_TOP1><<<(unsigned)nc, 256, 0, stream>>>(a);
   }
   const int e = q35_last_error();
   if (e) return e;
-  top1_final<<<1, 1024, 0, stream>>>(cand, (int)nc, (long long*)out);
+  top1_final<<<1, 1024, 0, stream>>>((const unsigned long long*)workspace, (int)nc, (long long*)out);
   return q35_last_error();
 }
 

@@ -142,3 +142,11 @@ Q35_DEV uint32_t top1_index(uint64_t key) { return 0xffffffffu - (uint32_t)(key 
 static inline int q35_last_error() { return (int)hipGetLastError(); }
 
 static inline bool q35_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Workgroup barrier that orders LDS only: outstanding global loads (e.g. a
+// weight stream issued before the barrier) stay in flight across it.
+Q35_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}

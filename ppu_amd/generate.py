@@ -1,0 +1,102 @@
+"""Fused greedy generation with TTFT / decode-throughput timing.
+
+Text-only restatement of the reference's ``VLMModel._generate_fused_greedy``
+(evaluation_wrapper.py:307-441) on the MI355X path: bucketed static cache,
+timer started before the cache reset, prefill through the patched model,
+lm_head top-1, ``token.item()`` ends TTFT, one eager decode step on a fresh
+bucket, then one captured greedy graph replayed per token with one
+device-to-host read per token. Throughput follows the reference formula
+``(tokens - 1) / (elapsed - ttft)`` (benchmark_public.py:148-153).
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from .graph import GreedyDecodeGraph
+from .kernels import lm_head_argmax
+
+
+@dataclass
+class GenerationResult:
+    tokens: list[int]
+    ttft_seconds: float
+    elapsed_seconds: float
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def decode_tokens_per_second(self) -> float:
+        n = len(self.tokens)
+        dt = self.elapsed_seconds - self.ttft_seconds
+        return (n - 1) / dt if n > 1 and dt > 0 else 0.0
+
+
+def cache_bucket(input_len: int, max_new_tokens: int) -> int:
+    """evaluation_wrapper.py:339-341."""
+    required = input_len + max_new_tokens + 1
+    return max(512, ((required + 127) // 128) * 128)
+
+
+class FusedGreedyGenerator:
+    """Keeps one StaticCache and one captured decode graph per cache bucket."""
+
+    def __init__(self, model, eos_ids: set[int] | None = None):
+        self.model = model
+        self.eos_ids = eos_ids or set()
+        self._caches: dict[int, object] = {}
+        self._graphs: dict[int, GreedyDecodeGraph] = {}
+
+    def _cache(self, bucket: int):
+        from transformers.cache_utils import StaticCache
+
+        cache = self._caches.get(bucket)
+        fresh = cache is None
+        if fresh:
+            cache = StaticCache(config=self.model.config, max_cache_len=bucket)
+            self._caches[bucket] = cache
+        return cache, fresh
+
+    @torch.inference_mode()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int) -> GenerationResult:
+        model = self.model
+        input_len = int(input_ids.shape[-1])
+        max_new_tokens = max(1, int(max_new_tokens))
+        bucket = cache_bucket(input_len, max_new_tokens)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        cache, fresh = self._cache(bucket)
+        if not fresh:
+            cache.reset()
+        positions = torch.arange(input_len, device=input_ids.device).view(1, -1)
+        prefill = model.model(input_ids=input_ids, position_ids=positions, past_key_values=cache,
+                              use_cache=True, return_dict=True)
+        token = lm_head_argmax(prefill.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight)
+        generated = [int(token.item())]
+        first_token_at = time.perf_counter()
+        position = torch.full((1, 1), input_len, device=input_ids.device, dtype=torch.long)
+        runner = self._graphs.get(bucket)
+        reused = runner is not None
+        if runner is None and len(generated) < max_new_tokens and generated[-1] not in self.eos_ids:
+            out = model.model(input_ids=token, position_ids=position, past_key_values=cache,
+                              use_cache=True, return_dict=True)
+            token = lm_head_argmax(out.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight)
+            generated.append(int(token.item()))
+            position.add_(1)
+        if len(generated) < max_new_tokens and generated[-1] not in self.eos_ids:
+            if runner is None:
+                runner = GreedyDecodeGraph(model, cache, token, position)
+                self._graphs[bucket] = runner
+            else:
+                runner.set_inputs(token, position)
+            while len(generated) < max_new_tokens and generated[-1] not in self.eos_ids:
+                generated.append(int(runner.replay().reshape(-1)[0].item()))
+        end = time.perf_counter()
+        return GenerationResult(
+            tokens=generated,
+            ttft_seconds=first_token_at - start,
+            elapsed_seconds=end - start,
+            meta={"cache_bucket": bucket, "graph_reused": reused, "cache_reused": not fresh},
+        )

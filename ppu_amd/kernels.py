@@ -15,8 +15,6 @@ their own decomposition.
 
 from __future__ import annotations
 
-import math
-
 import torch
 
 from . import _lib
@@ -201,6 +199,41 @@ def residual_norm_linear(
     _lib.call(name, weight.data_ptr(), residual.data_ptr(), update.data_ptr(), w.data_ptr(), wf,
               float(eps), r_out.data_ptr(), None, out.data_ptr(), n, k, 2, _stream(residual))
     return r_out, out
+
+
+def norm_linear(
+    x: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    weight: torch.Tensor,
+) -> torch.Tensor:
+    """``linear(rms_norm(x), W)`` for one token in one launch: the RMSNorm of
+    reference kernels.py:44 as the GEMV prologue (layer 0's input norm)."""
+
+    k = x.shape[-1]
+    if x.numel() != k or weight.ndim != 2 or weight.shape[1] != k:
+        raise ValueError("fused norm GEMV expects one token matching the weight")
+    _need_bf16(x, weight)
+    w, wf = _param(norm_weight)
+    n = weight.shape[0]
+    out = torch.empty((*x.shape[:-1], n), device=x.device, dtype=x.dtype)
+    _lib.call("q35_gemv_bf16", weight.data_ptr(), x.contiguous().data_ptr(), None, w.data_ptr(), wf,
+              float(eps), None, None, out.data_ptr(), n, k, 1, _stream(x))
+    return out
+
+
+def prefill_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``F.linear(x, W)`` for M > 1 tokens (prefill), bf16 in/out, fp32 accumulate.
+
+    A plain dense GEMM: it runs on the ROCm library GEMM (hipBLASLt/rocBLAS
+    MFMA kernels) behind ``torch.nn.functional.linear`` on the GPU tensor, as
+    the reference's prefill call sites do (integration.py:183,245,298).
+    """
+
+    if not x.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    _need_bf16(x, weight)
+    return torch.nn.functional.linear(x, weight)
 
 
 def ppu_swiglu_gemv(
@@ -501,11 +534,14 @@ def gqa_prefill_attention(
     scale: float,
     *,
     kv_start: int = 0,
+    valid_length: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Causal GQA prefill attention: ``q [B,QH,L,D]`` attends to
-    ``keys/values [B,KVH,C,D]`` positions ``[0, kv_start + i]``. Returns
-    ``[B, L, QH*D]`` bf16. Replaces the prefill attention interface call of
-    reference integration.py:360-372."""
+    """Causal GQA prefill attention: ``q [B,QH,L,D]`` row i attends to
+    ``keys/values [B,KVH,C,D]`` positions ``[0, start + i]``, with
+    ``start = valid_length - L`` when the device scalar ``valid_length``
+    (already including the L tokens, as a static cache's length) is given,
+    else ``kv_start``. Returns ``[B, L, QH*D]`` bf16. Replaces the prefill
+    attention interface call of reference integration.py:360-372."""
 
     if q.ndim != 4 or keys.ndim != 4 or keys.shape != values.shape:
         raise ValueError("prefill attention expects q[B,QH,L,D] and K/V[B,KVH,C,D]")
@@ -513,7 +549,9 @@ def gqa_prefill_attention(
     kv_heads, cache_len = keys.shape[1], keys.shape[2]
     if keys.shape[0] != batch or keys.shape[3] != dim or heads % kv_heads:
         raise ValueError("prefill attention head layout does not match")
-    if kv_start < 0 or kv_start + seq_len > cache_len:
+    if valid_length is None and (kv_start < 0 or kv_start + seq_len > cache_len):
+        raise ValueError("prefill attention range exceeds the key/value length")
+    if seq_len > cache_len:
         raise ValueError("prefill attention range exceeds the key/value length")
     if not (q.is_contiguous() and keys.is_contiguous() and values.is_contiguous()):
         raise ValueError("prefill attention tensors must be contiguous")
@@ -521,10 +559,13 @@ def gqa_prefill_attention(
         raise ValueError("fused kernels require a GPU tensor")
     if dim != 256:
         raise ValueError("MI355X prefill attention kernels are built for head_dim 256")
+    if valid_length is not None and (valid_length.dtype != torch.int64 or valid_length.device != q.device):
+        raise ValueError("valid_length must be an int64 tensor on the GPU")
     _need_bf16(q, keys, values)
     out = torch.empty((batch, seq_len, heads * dim), device=q.device, dtype=q.dtype)
     _lib.call("q35_gqa_prefill", q.data_ptr(), keys.data_ptr(), values.data_ptr(), out.data_ptr(),
-              batch, heads, kv_heads, dim, seq_len, cache_len, kv_start, float(scale), _stream(q))
+              batch, heads, kv_heads, dim, seq_len, cache_len, kv_start, _lib.ptr(valid_length),
+              float(scale), _stream(q))
     return out
 
 
@@ -628,5 +669,3 @@ def sigmoid_mul(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
     packed = torch.cat((gate, gate), dim=-1).contiguous()
     return attention_gate_mul(x, packed, width)
 
-
-DEFAULT_SCALE = 1.0 / math.sqrt(256)
