@@ -1,0 +1,319 @@
+"""Decode tokens/s and TTFT of the synthetic Qwen3.5-2B-shaped decoder on one MI355X.
+
+Workload: the 24-layer 2B-shaped decoder with seeded
+random-init bf16 weights (synthetic; no checkpoint), batch 1, a 1024-token
+prompt of uniform-random token ids, then greedy decode. A "step" is one
+greedy decode token: one replay of the captured decode graph (24 layers +
+lm_head top-1 + token feedback) followed by the host read of the token, as
+the reference's decode loop does (evaluation_wrapper.py:412-419).
+
+Printed (one JSON line on stdout):
+  value        decode tokens/s over the K timed steps (inputs resident in HBM)
+  ttft_ms      prefill (1024 tokens) + first token, timed as the reference
+               does (evaluation_wrapper.py:342-365), median of warm runs
+  roofline     the dominant decode kernel (lm_head GEMV + top-1, 1.017 GB of
+               weights per launch) timed with HIP events on its stream
+  kernels      per-kernel achieved HBM GB/s of the BASELINE configs 1-4
+               (rotating >= 640 MB of distinct buffers so the 256 MB MALL does
+               not serve the weights), in-graph time per launch
+  cpu_baseline the CPU oracle decoder (the reference's PyTorch CPU path,
+               restated) on a bounded sample, same process, host cores
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+PROMPT_LEN = 1024
+NEW_TOKENS = 64
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def graph_time_us(fn, calls: int, reps: int) -> float:
+    """Average time per call of ``fn(i)`` captured ``calls`` times in one graph."""
+    import torch
+
+    for i in range(2):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(calls):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * calls)
+
+
+def lm_head_roofline(model) -> dict:
+    import torch
+
+    from ppu_amd import kernels as K
+
+    w = model.lm_head.weight
+    v, k = w.shape
+    h = torch.randn(1, k, device=w.device, dtype=torch.bfloat16)
+    us = graph_time_us(lambda i: K.lm_head_argmax(h, w), calls=10, reps=10)
+    slots = (v + 3) // 4
+    algo = v * k * 2 + k * 2 + 8  # weights + hidden + index
+    achieved = algo / us / 1e3
+    return {"kernel": "lm_head GEMV + top-1 [248320,2048] bf16", "bound": "hbm",
+            "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+            "us_per_launch": round(us, 2), "algorithmic_bytes": algo,
+            "workspace_bytes": slots * 8}
+
+
+def kernel_table(dev) -> dict:
+    """BASELINE configs 1-4 as individual launches, rotating distinct buffers."""
+    import torch
+
+    from ppu_amd import kernels as K
+
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(20260819)
+    out = {}
+
+    def nbuf(nbytes):
+        return max(2, (640 << 20) // nbytes + 1)
+
+    def rec(name, us, nbytes):
+        gbs = nbytes / us / 1e3
+        out[name] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 3)}
+        log(f"  {name}: {us:.2f} us  {gbs:.0f} GB/s  ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
+
+    # config 1: residual add + RMSNorm + GEMV [6144, 2048]
+    n = nbuf(6144 * 2048 * 2)
+    Ws = [(torch.randn(6144, 2048, device=dev, generator=g) * 0.02).to(bf) for _ in range(n)]
+    x = torch.randn(1, 2048, device=dev, generator=g).to(bf)
+    r = torch.randn(1, 2048, device=dev, generator=g).to(bf)
+    nw = (torch.randn(2048, device=dev, generator=g) * 0.02 + 1).to(bf)
+    us = graph_time_us(lambda i: K.residual_norm_linear(r, x, nw, 1e-6, Ws[i % n]), calls=n, reps=4)
+    rec("cfg1_resnorm_gemv_6144x2048", us, 25_198_592)
+    del Ws
+    # config 2: A8W8 GEMV, M = 1, 4, 16
+    for (nn, kk) in ((12288, 2048), (2048, 6144)):
+        n = nbuf(nn * kk)
+        Wq = [torch.randint(-127, 128, (nn, kk), device=dev, generator=g, dtype=torch.int8)
+              for _ in range(n)]
+        sw = torch.rand(nn, 1, device=dev, generator=g) * 1e-3
+        for m in (1, 4, 16):
+            xm = torch.randn(m, kk, device=dev, generator=g).to(bf)
+            us = graph_time_us(lambda i: K.a8w8_linear(xm, Wq[i % n], sw), calls=n, reps=4)
+            rec(f"cfg2_a8w8_{nn}x{kk}_m{m}", us, nn * kk + 4 * nn + 2 * kk * m + 2 * nn * m)
+        del Wq
+    # config 3: GQA decode attention (8 q / 2 kv heads, D 256)
+    for ctx in (512, 2048, 8192):
+        n = nbuf(2 * 2 * ctx * 256 * 2)
+        Kc = [torch.randn(1, 2, ctx, 256, device=dev, generator=g).to(bf) for _ in range(n)]
+        Vc = [torch.randn(1, 2, ctx, 256, device=dev, generator=g).to(bf) for _ in range(n)]
+        q = torch.randn(1, 8, 1, 256, device=dev, generator=g).to(bf)
+        ln = torch.tensor(ctx, device=dev, dtype=torch.int64)
+        us = graph_time_us(lambda i: K.gqa_decode_attention(q, Kc[i % n], Vc[i % n], ln, 1 / 16),
+                           calls=n, reps=4)
+        rec(f"cfg3_gqa_decode_L{ctx}", us, 2048 * ctx + 8192)
+        del Kc, Vc
+    # config 4: fused conv1d + delta rule + gated RMSNorm, one decode token
+    n = nbuf(16 * 128 * 128 * 4)
+    St = [torch.randn(1, 16, 128, 128, device=dev, generator=g) * 0.1 for _ in range(n)]
+    packed = torch.randn(1, 1, 8320, device=dev, generator=g).to(bf)
+    cw = (torch.randn(6144, 4, device=dev, generator=g) * 0.02).to(bf)
+    cs = torch.zeros(1, 6144, 4, device=dev, dtype=bf)
+    z16 = torch.zeros(16, device=dev, dtype=bf)
+    gw = torch.ones(128, device=dev, dtype=bf)
+    us = graph_time_us(lambda i: K.delta_decode_fused(packed, cw, cs, z16, z16, St[i % n], gw, 1e-6),
+                       calls=n, reps=4)
+    rec("cfg4_delta_decode_step", us, 2_261_120 + 4096)
+    del St
+    return out
+
+
+def cpu_baseline(state, cfg, prompt, decode_steps: int) -> dict:
+    """The oracle decoder on the host cores: a bounded sample of the workload."""
+    import torch
+
+    from oracle.model import OracleDecoder
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    oracle = OracleDecoder(state, cfg)
+    cache = oracle.new_cache(PROMPT_LEN + decode_steps + 8)
+    t0 = time.perf_counter()
+    h = oracle.forward(prompt, cache)
+    tok, _ = oracle.top1(h[:, -1])
+    ttft = time.perf_counter() - t0
+    t1 = time.perf_counter()
+    for _ in range(decode_steps):
+        h = oracle.forward(torch.tensor([[tok]]), cache)
+        tok, _ = oracle.top1(h[:, -1])
+    dt = time.perf_counter() - t1
+    return {"value": round(decode_steps / dt, 3), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port", "ttft_ms": round(ttft * 1e3, 1),
+            "sample": f"oracle decoder (torch CPU, same seeded weights): prefill of the "
+                      f"{prompt.shape[1]}-token prompt, then {decode_steps} greedy decode steps",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--variant", choices=("bf16", "a8w8"), default="bf16")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-decode-steps", type=int, default=8)
+    ap.add_argument("--cpu-prompt", type=int, default=128, help="prompt length of the CPU sample")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (batch-1 decode does not "
+              "shard profitably; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from ppu_amd import synth
+    from ppu_amd.generate import FusedGreedyGenerator, cache_bucket
+    from ppu_amd.graph import GreedyDecodeGraph
+    from ppu_amd.integration import FusionConfig, apply_fusions
+    from ppu_amd.kernels import lm_head_argmax
+
+    dev = torch.device("cuda:0")
+    cfg = synth.config_2b()
+    t0 = time.perf_counter()
+    model = synth.build_model(cfg, device=dev)
+    seen = set()
+    weight_bytes = 0
+    for p in model.parameters():
+        if p.data_ptr() not in seen:
+            seen.add(p.data_ptr())
+            weight_bytes += p.numel() * p.element_size()
+    state = None if args.no_cpu else {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    stats = apply_fusions(model, FusionConfig(a8w8=args.variant == "a8w8"))
+    torch.cuda.synchronize()
+    log(f"model built + fused in {time.perf_counter() - t0:.1f} s: {stats}")
+
+    gen = torch.Generator().manual_seed(synth.MODEL_SEED)
+    prompt_cpu = torch.randint(0, cfg.vocab_size, (1, PROMPT_LEN), generator=gen)
+    prompt = prompt_cpu.to(dev)
+
+    # TTFT and the reference's decode formula through the generation loop.
+    runner = FusedGreedyGenerator(model)
+    first = runner.generate(prompt, NEW_TOKENS)  # builds cache + captures the graph
+    warm = [runner.generate(prompt, NEW_TOKENS) for _ in range(3)]
+    ttft_ms = statistics.median(r.ttft_seconds for r in warm) * 1e3
+    loop_tps = statistics.median(r.decode_tokens_per_second for r in warm)
+    assert all(r.tokens == first.tokens for r in warm), "greedy decode is not deterministic"
+    log(f"TTFT {ttft_ms:.2f} ms (cold {first.ttft_seconds * 1e3:.1f} ms); "
+        f"generate-loop decode {loop_tps:.1f} tok/s; first tokens {first.tokens[:8]}")
+
+    # Timed decode steps: W warmup + K timed replays of the decode graph.
+    bucket = cache_bucket(PROMPT_LEN, args.warmup + args.steps + 2)
+    from transformers.cache_utils import StaticCache
+
+    with torch.inference_mode():
+        cache = StaticCache(config=model.config, max_cache_len=bucket)
+        pos = torch.arange(PROMPT_LEN, device=dev).view(1, -1)
+        out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
+        tok = lm_head_argmax(out.last_hidden_state[:, -1].contiguous(), model.lm_head.weight)
+        graph = GreedyDecodeGraph(model, cache, tok, torch.full((1, 1), PROMPT_LEN, device=dev,
+                                                                dtype=torch.long))
+        tokens = []
+        for _ in range(args.warmup):
+            tokens.append(int(graph.replay().reshape(-1)[0].item()))
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            tokens.append(int(graph.replay().reshape(-1)[0].item()))
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t1
+        # pure device time per replay (no host read between replays)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cache.reset()
+        out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
+        graph.set_inputs(tok, torch.full((1, 1), PROMPT_LEN, device=dev, dtype=torch.long))
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        replay_ms = e0.elapsed_time(e1) / args.steps
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = args.steps / elapsed
+    log(f"decode: {ms_per_step:.3f} ms/token ({value:.1f} tok/s); graph replay alone {replay_ms:.3f} ms")
+
+    with torch.inference_mode():
+        roof = lm_head_roofline(model)
+        log(f"lm_head top-1: {roof['us_per_launch']} us, {roof['achieved']} GB/s "
+            f"({100 * roof['frac']:.1f}%)")
+        kernels = {} if args.no_kernels else kernel_table(dev)
+
+    cpu = None
+    if not args.no_cpu:
+        del model, graph, cache, runner
+        torch.cuda.empty_cache()
+        log("CPU baseline ...")
+        cpu = cpu_baseline(state, cfg, prompt_cpu[:, : args.cpu_prompt], args.cpu_decode_steps)
+        log(f"CPU oracle: {cpu['value']} tok/s decode, TTFT {cpu['ttft_ms']} ms on {cpu['cores']} threads")
+
+    result = {
+        "metric": "decode tokens/s (batch 1, greedy) + TTFT, 1 GPU",
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if args.variant == "bf16" else "int8 (A8W8 linears, bf16 elsewhere)",
+        "data": "synthetic: seeded random-init N(0,0.02) weights, uniform-random token ids",
+        "config": {"workload": "Qwen3.5-2B-shaped decoder (24 layers, 18 DeltaNet + 6 GQA), "
+                               f"{PROMPT_LEN}-token prefill then greedy decode, batch 1, "
+                               f"{args.variant} linears", "cache_bucket": bucket},
+        "ttft_ms": round(ttft_ms, 3),
+        "graph_replay_ms": round(replay_ms, 4),
+        "generate_loop_tokens_per_s": round(loop_tps, 2),
+        "weights_gb_per_token": round(weight_bytes / 1e9, 4),
+        "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "roofline_detail": roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
