@@ -57,13 +57,25 @@ int q35_attn_gate_mul(const void* x, const void* packed, void* out, long long to
 /* ---- bf16 GEMV (M = 1) ------------------------------------------------- */
 
 /* y[N] = bf16(W[N,K] . xa) where xa depends on `prologue`:
- *   0: xa = x;  1: xa = rms_norm(x, norm_w);  2: r' = bf16(x + u), xa = rms_norm(r', norm_w).
+ *   0: xa = x;  1: xa = rms_norm(x, norm_w);  2: r' = bf16(x + u), xa = rms_norm(r', norm_w);
+ *   3: xa = gated_rms_norm(x, gate = u, norm_w) over heads of 128 (K % 512 == 0).
  * residual_out / x_norm_out (optional) receive r' and xa.
  * Replaces the decode F.linear call sites qwen35_fused/integration.py:185,245,272,298-302,359,
- * fused with the residual_add_rms_norm of integration.py:478-499. */
+ * fused with the residual_add_rms_norm of integration.py:478-499 (prologues 1, 2) or the
+ * gated_rms_norm of integration.py:266-271 (prologue 3). */
 int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_w, int norm_w_f32,
                   float eps, void* residual_out, void* x_norm_out, void* y, int N, int K,
                   int prologue, void* stream);
+
+/* q35_gemv_bf16 (prologues 0-2) whose epilogue also runs, for rows n < conv_channels,
+ * the single-token causal conv update on y[n]: conv_out[n] = bf16(silu(bf16(sum_t
+ * conv_w[n,t] * window[t]))), window = (conv_state[n,1:], y[n]), conv_state shifted in
+ * place. Replaces integration.py:245 (packed DeltaNet projection) followed by
+ * qwen35_fused/kernels.py:659 (causal_conv1d_fused at L == 1, kernel :622-656). */
+int q35_gemv_conv(const void* W, const void* x, const void* u, const void* norm_w, int norm_w_f32,
+                  float eps, void* residual_out, void* y, int N, int K, int prologue,
+                  const void* conv_w, void* conv_state, void* conv_out, int conv_channels,
+                  int conv_kw, void* stream);
 
 /* y[N] = bf16(bf16(silu(bf16(W[n].xa))) * bf16(W[N+n].xa)), W = [gate; up] of [2N, K];
  * prologue as q35_gemv_bf16. Replaces qwen35_fused/kernels.py:232 (ppu_swiglu_gemv,
@@ -160,6 +172,12 @@ int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, void* s
  * Replaces explore_runtime_quantization.py:161-181 (PPUA8W8Linear.forward). */
 int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void* s_w, void* y,
                   void* acc_out, int M, int N, int K, void* stream);
+
+/* y[M,N] = bf16(float(acc[m,n]) * s_x[m] * s_w[n]) for int32 accumulators of an
+ * int8 GEMM (the prefill A8W8 path; N % 8 == 0). Same dequant epilogue as
+ * q35_gemv_a8w8, replacing the output stage of explore_runtime_quantization.py:173-180. */
+int q35_dequant_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,
+                    void* stream);
 
 #ifdef __cplusplus
 }

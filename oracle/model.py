@@ -29,6 +29,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import a8w8 as oa
 from . import ops
 
 
@@ -128,10 +129,36 @@ class Cache:
                 self.v[i] = torch.zeros_like(self.k[i])
 
 
+_LINEARS = ("in_proj", "out_proj", "qgkv", "o_proj", "gate_up", "down")
+
+
 class OracleDecoder:
-    def __init__(self, state: dict[str, torch.Tensor], config):
+    """``a8w8``: every linear except the lm_head runs as A8W8 (per-channel int8
+    weights quantised here, per-token int8 activations, exact integer products,
+    fp32 dequant), as the reference applies PPUA8W8Linear to the MLP,
+    attention and DeltaNet projections (explore_runtime_quantization.py:66-84)."""
+
+    def __init__(self, state: dict[str, torch.Tensor], config, *, a8w8: bool = False):
         self.s = Shapes.from_config(config)
         self.w = pack_weights(state, self.s)
+        self.a8w8 = a8w8
+        if a8w8:
+            for lw in self.w["layers"]:
+                for name in _LINEARS:
+                    if name in lw:
+                        q, sc = oa.quantize_weight(lw[name])
+                        lw[name + "_q"] = (torch.from_numpy(q).double(), sc)
+
+    def _lin(self, x: torch.Tensor, lw: dict, name: str) -> torch.Tensor:
+        if not self.a8w8:
+            return F.linear(x, lw[name])
+        wq, sw = lw[name + "_q"]
+        xq, sx = oa.quantize_act(x)
+        # int8 x int8 products summed over K <= 6144 stay below 2^53: fp64 BLAS is exact
+        acc = (torch.from_numpy(xq).double() @ wq.t()).to(torch.int64).numpy()
+        assert abs(acc).max(initial=0) < 2**31
+        y = oa.dequant(acc.astype("int32"), sx, sw)
+        return y.reshape(*x.shape[:-1], -1)
 
     def new_cache(self, max_len: int) -> Cache:
         return Cache(self.s, max_len)
@@ -140,19 +167,19 @@ class OracleDecoder:
     def _delta(self, i, lw, h, cache: Cache):
         s = self.s
         b, l, _ = h.shape
-        packed = F.linear(h, lw["in_proj"])
+        packed = self._lin(h, lw, "in_proj")
         qkv = ops.causal_conv1d(packed, lw["conv_w"], cache.conv[i])
         core = ops.delta_recurrent(qkv, packed, lw["a_log"], lw["dt_bias"], cache.rec[i])
         vd = s.lin_heads * s.lin_dim
         conv_dim = 3 * vd
         z = packed[..., conv_dim : conv_dim + vd].reshape(-1, s.lin_dim)
         core = ops.gated_rms_norm(core.reshape(-1, s.lin_dim), z, lw["gnorm"], s.eps)
-        return F.linear(core.reshape(b, l, vd), lw["out_proj"])
+        return self._lin(core.reshape(b, l, vd), lw, "out_proj")
 
     def _attn(self, i, lw, h, cos, sin, cache: Cache, start: int):
         s = self.s
         l = h.shape[1]
-        packed = F.linear(h, lw["qgkv"])
+        packed = self._lin(h, lw, "qgkv")
         q, kc, vc = ops.qgkv_norm_rope(
             packed, lw["q_norm"], lw["k_norm"], cos, sin, q_heads=s.q_heads, kv_heads=s.kv_heads,
             dim=s.head_dim, rotary_dim=s.rotary_dim, cache_key=cache.k[i], cache_value=cache.v[i],
@@ -164,14 +191,14 @@ class OracleDecoder:
         else:
             o = ops.prefill_attention(q, kc, vc, scale, kv_start=start)
         o = ops.attention_gate_mul(o, packed, s.head_dim)
-        return F.linear(o, lw["o_proj"])
+        return self._lin(o, lw, "o_proj")
 
     def _mlp(self, lw, x):
-        if x.shape[1] == 1:
+        if x.shape[1] == 1 and not self.a8w8:
             act = ops.swiglu_gemv(x, lw["gate_up"])
         else:
-            act = ops.silu_and_mul(F.linear(x, lw["gate_up"]))
-        return F.linear(act, lw["down"])
+            act = ops.silu_and_mul(self._lin(x, lw, "gate_up"))
+        return self._lin(act, lw, "down")
 
     # ------------------------------------------------------------ forward
     @torch.no_grad()
@@ -210,13 +237,17 @@ class OracleDecoder:
         return tok, float(top.values[0] - top.values[1])
 
     @torch.no_grad()
-    def teacher_forced(self, prompt: torch.Tensor, forced: list[int], max_len: int):
+    def teacher_forced(self, prompt: torch.Tensor, forced: list[int], max_len: int,
+                       return_hidden: bool = False):
         """Prefill ``prompt`` then feed ``forced`` tokens one at a time.
-        Returns per step (oracle argmax, top-2 margin), len(forced) + 1 steps."""
+        Returns per step (oracle argmax, top-2 margin), len(forced) + 1 steps,
+        and with ``return_hidden`` also the final-normed hidden state of each step."""
         cache = self.new_cache(max_len)
         h = self.forward(prompt, cache)
         out = [self.top1(h[:, -1])]
+        hidden = [h[:, -1].clone()]
         for tok in forced:
             h = self.forward(torch.tensor([[tok]]), cache)
             out.append(self.top1(h[:, -1]))
-        return out
+            hidden.append(h[:, -1].clone())
+        return (out, hidden) if return_hidden else out

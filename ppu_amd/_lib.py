@@ -31,6 +31,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_attn_gate_mul": (_I, [_P, _P, _P, _L, _I, _I, _I, _P]),
     "q35_gemv_bf16": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _I, _I, _P]),
     "q35_swiglu_gemv": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _I, _I, _P]),
+    "q35_gemv_conv": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
     "q35_lm_head_top1_workspace": (_L, [_I, _I]),
     "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P]),
     "q35_conv1d_update": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
@@ -52,6 +53,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_quant_weight_i8": (_I, [_P, _P, _P, _I, _I, _P]),
     "q35_quant_act_i8": (_I, [_P, _P, _P, _I, _I, _P]),
     "q35_gemv_a8w8": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "q35_dequant_i32": (_I, [_P, _P, _P, _P, _I, _I, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -201,9 +201,41 @@ __global__ __launch_bounds__(256) void a8w8_gemv_mt(const A8Args a, int m0) {
   }
 }
 
+// y[m, n] = bf16((float)acc[m, n] * s_x[m] * s_w[n]); 8 outputs per thread.
+__global__ __launch_bounds__(256) void dequant_rows(const int* __restrict__ acc,
+                                                    const float* __restrict__ s_x,
+                                                    const float* __restrict__ s_w,
+                                                    uint16_t* __restrict__ y, int M, int N) {
+  const long long i = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= (long long)M * N) return;
+  const int m = (int)(i / N);
+  const int n = (int)(i - (long long)m * N);
+  const float sx = s_x[m];
+  const int4 a0 = *reinterpret_cast<const int4*>(acc + i);
+  const int4 a1 = *reinterpret_cast<const int4*>(acc + i + 4);
+  const int av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (float)av[e] * sx * s_w[n + e];
+  *reinterpret_cast<uint4*>(y + i) = pack8(o);
+}
+
 }  // namespace
 
 extern "C" {
+
+// y[M,N] = bf16(acc * s_x[m] * s_w[n]) for int32 accumulators from any int8 GEMM.
+int q35_dequant_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,
+                    hipStream_t stream) {
+  Q35_CHECK_ARG(M > 0 && N > 0 && N % 8 == 0 && acc && s_x && s_w && y);
+  Q35_CHECK_ARG(q35_aligned16(acc) && q35_aligned16(y));
+  const long long groups = (long long)M * N / 8;
+  const long long grid = (groups + 255) / 256;
+  Q35_CHECK_ARG(grid < (1ll << 31));
+  dequant_rows<<<(unsigned)grid, 256, 0, stream>>>((const int*)acc, (const float*)s_x,
+                                                  (const float*)s_w, (uint16_t*)y, M, N);
+  return q35_last_error();
+}
 
 int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, hipStream_t stream) {
   Q35_CHECK_ARG(N > 0 && K > 0 && W && Wq && scale);

@@ -23,22 +23,6 @@ Q35_DEV float ld_param(const void* p, int i, int is_f32) {
 
 Q35_DEV float softplus20(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
 
-// Single-token conv for one channel: window = (state[1..KW-1], x), state
-// shifted in place, returns bf16(silu(bf16(sum_t w[t]*window[t]))) as fp32.
-// [reference kernels.py:622-656]
-Q35_DEV float conv_update_channel(uint16_t* __restrict__ st, const uint16_t* __restrict__ w,
-                                  uint16_t xin, int kw) {
-  float acc = 0.f;
-  for (int t = 0; t < kw - 1; ++t) {
-    const uint16_t s = st[t + 1];
-    st[t] = s;
-    acc = fmaf(bf2f(s), bf2f(w[t]), acc);
-  }
-  st[kw - 1] = xin;
-  acc = fmaf(bf2f(xin), bf2f(w[kw - 1]), acc);
-  return round_bf(silu_f(round_bf(acc)));
-}
-
 // ------------------------------------------------------------------ conv1d
 __global__ __launch_bounds__(256) void conv1d_update(const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ w,
@@ -218,6 +202,104 @@ __global__ __launch_bounds__(256) void delta_decode(const DeltaArgs p) {
   }
 }
 
+// Delta rule only (input already convolved), split over v: one 256-thread
+// workgroup per (batch, head, 32-column v tile), 4 tiles per head, so 4x more
+// CUs stream the state than with one workgroup per head. Thread t owns
+// columns 4*(t%8)..+3 of the tile for rows (t/8) + 32*i, i = 0..3: each row
+// segment of a tile is 128 contiguous bytes read by 8 lanes with 16-byte loads.
+// Every workgroup recomputes the head's norm factors and gates (q, k are 512
+// bytes from L2); the state is read once and written once.
+constexpr int kVT = 32;
+
+__global__ __launch_bounds__(256) void delta_decode_tiled(const DeltaArgs p) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int tiles = kD / kVT;
+  const int tile = blockIdx.x % tiles;
+  const int bh = blockIdx.x / tiles;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int vq = tid & 7;
+  const int kg = tid >> 3;  // 0..31
+  const int c0 = tile * kVT + 4 * vq;
+
+  __shared__ float qs[kD], ks[kD], vs[kVT];
+  __shared__ float red[4][kVT];
+  __shared__ float sc[4];
+
+  float* S = p.state + (size_t)bh * kD * kD;
+  float4 st[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    st[i] = *reinterpret_cast<const float4*>(S + (size_t)(kg + 32 * i) * kD + c0);
+
+  const uint16_t* srow = p.src + (size_t)b * p.src_stride;
+  if (tid < kD) qs[tid] = bf2f(srow[h * kD + tid]);
+  else ks[tid - kD] = bf2f(srow[p.H * kD + h * kD + tid - kD]);
+  if (tid < kVT) vs[tid] = bf2f(srow[2 * p.H * kD + h * kD + tile * kVT + tid]);
+  __syncthreads();
+  if (wid < 2) {
+    const float* src = wid == 0 ? qs : ks;
+    const float a0 = src[lane], a1 = src[lane + 64];
+    const float tot = wave_sum(a0 * a0 + a1 * a1);
+    if (lane == 0) sc[wid] = rsqrt_cr(tot + 1e-6f);
+  } else if (tid == 128) {
+    const uint16_t* prow = p.packed + (size_t)b * p.packed_stride;
+    const float a = bf2f(prow[p.a_off + h]) + ld_param(p.dt_bias, h, p.params_f32);
+    const float g = -expf(ld_param(p.a_log, h, p.params_f32)) * softplus20(a);
+    sc[2] = expf(g);
+    sc[3] = 1.0f / (1.0f + expf(-bf2f(prow[p.b_off + h])));
+  }
+  __syncthreads();
+  const float q_inv = sc[0], k_inv = sc[1], alpha = sc[2], beta = sc[3];
+  const float qscale = 0.08838834764831845f;  // fp32(1/sqrt(128))
+
+  float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float kh = ks[kg + 32 * i] * k_inv;
+    st[i].x *= alpha; st[i].y *= alpha; st[i].z *= alpha; st[i].w *= alpha;
+    m.x = fmaf(st[i].x, kh, m.x); m.y = fmaf(st[i].y, kh, m.y);
+    m.z = fmaf(st[i].z, kh, m.z); m.w = fmaf(st[i].w, kh, m.w);
+  }
+  // reduce over the 8 k-groups of a wave (lane bits 3..5), then the 4 waves
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+    m.x += __shfl_xor(m.x, off); m.y += __shfl_xor(m.y, off);
+    m.z += __shfl_xor(m.z, off); m.w += __shfl_xor(m.w, off);
+  }
+  if (lane < 8) *reinterpret_cast<float4*>(&red[wid][4 * vq]) = m;
+  __syncthreads();
+  if (tid < kVT) {
+    const float mem = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+    vs[tid] = beta * (vs[tid] - mem);
+  }
+  __syncthreads();
+  const float4 d = *reinterpret_cast<const float4*>(&vs[4 * vq]);
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float kh = ks[kg + 32 * i] * k_inv;
+    const float qh = qs[kg + 32 * i] * q_inv * qscale;
+    st[i].x += kh * d.x; st[i].y += kh * d.y; st[i].z += kh * d.z; st[i].w += kh * d.w;
+    o.x = fmaf(st[i].x, qh, o.x); o.y = fmaf(st[i].y, qh, o.y);
+    o.z = fmaf(st[i].z, qh, o.z); o.w = fmaf(st[i].w, qh, o.w);
+    *reinterpret_cast<float4*>(S + (size_t)(kg + 32 * i) * kD + c0) = st[i];
+  }
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+    o.x += __shfl_xor(o.x, off); o.y += __shfl_xor(o.y, off);
+    o.z += __shfl_xor(o.z, off); o.w += __shfl_xor(o.w, off);
+  }
+  __syncthreads();  // red[] reuse
+  if (lane < 8) *reinterpret_cast<float4*>(&red[wid][4 * vq]) = o;
+  __syncthreads();
+  if (tid < kVT) {
+    const float core = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+    p.out[(size_t)bh * kD + tile * kVT + tid] = (uint16_t)f2bf(core);
+  }
+}
+
 // ------------------------------------------------------------- prefill scan
 // Per (token, head) scalars (q_inv, k_inv, alpha, beta) [reference kernels.py:713-765].
 __global__ __launch_bounds__(256) void delta_factors(const uint16_t* __restrict__ qkv, int qkv_stride,
@@ -247,9 +329,29 @@ __global__ __launch_bounds__(256) void delta_factors(const uint16_t* __restrict_
 }
 
 // Sequential scan over L tokens. One wave per (batch, head, 8-column v tile);
-// lane = (k-group kg = lane/4 of 8 rows, v pair vp = lane%4), so the [128 x 8]
-// fp32 state tile lives in registers (16 per lane) for the whole sequence.
-// Reductions over k run across lanes with the same vp (xor 4, 8, 16, 32).
+// lane = (v pair vp = lane/16, k-group kg = lane%16 of 8 rows), so the
+// [128 x 8] fp32 state tile lives in registers (16 per lane) for the whole
+// sequence and every reduction over k is a 16-lane DPP row sum. The next
+// token's q, k, v and factors are loaded one step ahead, so the loop runs at
+// the latency of its arithmetic chain, not of memory.
+struct ScanIn {
+  uint4 q, k;
+  uint32_t v;
+  float4 f;
+};
+
+Q35_DEV ScanIn scan_load(const uint16_t* __restrict__ qkv, int qkv_stride,
+                         const float* __restrict__ factors, int b, int L, int H, int h, int t,
+                         int kg, int v0) {
+  ScanIn in;
+  const uint16_t* row = qkv + ((size_t)b * L + t) * qkv_stride;
+  in.q = *reinterpret_cast<const uint4*>(row + h * kD + kg * 8);
+  in.k = *reinterpret_cast<const uint4*>(row + H * kD + h * kD + kg * 8);
+  in.v = *reinterpret_cast<const uint32_t*>(row + 2 * H * kD + h * kD + v0);
+  in.f = *reinterpret_cast<const float4*>(factors + (((size_t)b * L + t) * H + h) * 4);
+  return in;
+}
+
 __global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qkv, int qkv_stride,
                                                  const float* __restrict__ factors,
                                                  float* __restrict__ state,
@@ -259,7 +361,7 @@ __global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qk
   const int tile = blockIdx.x % tiles;
   const int bh = blockIdx.x / tiles;
   const int b = bh / H, h = bh - b * H;
-  const int kg = lane >> 2, vp = lane & 3;
+  const int kg = lane & 15, vp = lane >> 4;
   const int v0 = tile * 8 + 2 * vp;
   float* S = state + (size_t)bh * kD * kD;
   float s[8][2];
@@ -269,43 +371,44 @@ __global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qk
     s[i][0] = t2.x; s[i][1] = t2.y;
   }
   const float qscale = 0.08838834764831845f;
+  ScanIn nxt = scan_load(qkv, qkv_stride, factors, b, L, H, h, 0, kg, v0);
   for (int t = 0; t < L; ++t) {
-    const uint16_t* row = qkv + ((size_t)b * L + t) * qkv_stride;
-    const uint4 qv = *reinterpret_cast<const uint4*>(row + h * kD + kg * 8);
-    const uint4 kv = *reinterpret_cast<const uint4*>(row + H * kD + h * kD + kg * 8);
-    const uint32_t vv = *reinterpret_cast<const uint32_t*>(row + 2 * H * kD + h * kD + v0);
-    const float4 f = *reinterpret_cast<const float4*>(factors + (((size_t)b * L + t) * H + h) * 4);
+    const ScanIn cur = nxt;
+    if (t + 1 < L) nxt = scan_load(qkv, qkv_stride, factors, b, L, H, h, t + 1, kg, v0);
     float q[8], k[8];
-    unpack8(qv, q);
-    unpack8(kv, k);
-    float m0 = 0.f, m1 = 0.f;
+    unpack8(cur.q, q);
+    unpack8(cur.k, k);
+    const float4 f = cur.f;
+    float ma0 = 0.f, ma1 = 0.f, mb0 = 0.f, mb1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       k[i] *= f.y;
       q[i] = q[i] * f.x * qscale;
       s[i][0] *= f.z; s[i][1] *= f.z;
-      m0 = fmaf(s[i][0], k[i], m0);
-      m1 = fmaf(s[i][1], k[i], m1);
     }
 #pragma unroll
-    for (int off = 4; off < 64; off <<= 1) {
-      m0 += __shfl_xor(m0, off);
-      m1 += __shfl_xor(m1, off);
+    for (int i = 0; i < 4; ++i) {
+      ma0 = fmaf(s[i][0], k[i], ma0);
+      ma1 = fmaf(s[i][1], k[i], ma1);
+      mb0 = fmaf(s[i + 4][0], k[i + 4], mb0);
+      mb1 = fmaf(s[i + 4][1], k[i + 4], mb1);
     }
-    const float d0 = f.w * (bf_lo(vv) - m0), d1 = f.w * (bf_hi(vv) - m1);
-    float o0 = 0.f, o1 = 0.f;
+    const float m0 = row16_sum(ma0 + mb0), m1 = row16_sum(ma1 + mb1);
+    const float d0 = f.w * (bf_lo(cur.v) - m0), d1 = f.w * (bf_hi(cur.v) - m1);
+    float oa0 = 0.f, oa1 = 0.f, ob0 = 0.f, ob1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       s[i][0] += k[i] * d0;
       s[i][1] += k[i] * d1;
-      o0 = fmaf(s[i][0], q[i], o0);
-      o1 = fmaf(s[i][1], q[i], o1);
     }
 #pragma unroll
-    for (int off = 4; off < 64; off <<= 1) {
-      o0 += __shfl_xor(o0, off);
-      o1 += __shfl_xor(o1, off);
+    for (int i = 0; i < 4; ++i) {
+      oa0 = fmaf(s[i][0], q[i], oa0);
+      oa1 = fmaf(s[i][1], q[i], oa1);
+      ob0 = fmaf(s[i + 4][0], q[i + 4], ob0);
+      ob1 = fmaf(s[i + 4][1], q[i + 4], ob1);
     }
+    const float o0 = row16_sum(oa0 + ob0), o1 = row16_sum(oa1 + ob1);
     if (kg == 0)
       *reinterpret_cast<uint32_t*>(out + (((size_t)b * L + t) * H + h) * kD + v0) = pack_bf2(o0, o1);
   }
@@ -381,7 +484,7 @@ int q35_delta_decode(const void* src, int src_stride, const void* packed, int pa
   if (fuse_conv && fuse_gnorm) delta_decode<true, true><<<grid, 256, 0, stream>>>(p);
   else if (fuse_conv) delta_decode<true, false><<<grid, 256, 0, stream>>>(p);
   else if (fuse_gnorm) delta_decode<false, true><<<grid, 256, 0, stream>>>(p);
-  else delta_decode<false, false><<<grid, 256, 0, stream>>>(p);
+  else delta_decode_tiled<<<grid * (kD / kVT), 256, 0, stream>>>(p);
   return q35_last_error();
 }
 

@@ -28,13 +28,13 @@
 
 namespace {
 
-enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_RESNORM = 2 };
-enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_TOP1 = 2 };
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_RESNORM = 2, PRO_GATEDNORM = 3 };
+enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_TOP1 = 2, EPI_CONV = 3 };
 
 struct GemvArgs {
   const uint16_t* W;    // [rows_total, K]
-  const uint16_t* x;    // activation (or residual for RESNORM)
-  const uint16_t* u;    // update (RESNORM)
+  const uint16_t* x;    // activation (residual for RESNORM, core for GATEDNORM)
+  const uint16_t* u;    // update (RESNORM) or gate z (GATEDNORM)
   const void* nw;       // norm weight
   uint16_t* r_out;      // RESNORM: r' written by block 0 (may be null)
   uint16_t* xn_out;     // normalised activation written by block 0 (may be null)
@@ -44,7 +44,16 @@ struct GemvArgs {
   int K;
   int nw_f32;
   float eps;
+  // EPI_CONV: rows n < conv_channels also run the depthwise conv update.
+  const uint16_t* conv_w;  // [conv_channels, conv_kw]
+  uint16_t* conv_state;    // [conv_channels, conv_kw], in place
+  uint16_t* conv_out;      // [conv_channels]
+  int conv_channels;
+  int conv_kw;
 };
+
+// Gated RMSNorm (reference kernels.py:115-155) runs over heads of this width.
+constexpr int kGatedHead = 128;
 
 Q35_DEV void load_nw8(const GemvArgs& a, int k, float* w) {
   if (a.nw_f32) {
@@ -80,7 +89,8 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
     const int i = tid + j * NT;
     if (i < NV && i * 8 < a.K) {
       xa[j] = *reinterpret_cast<const uint4*>(a.x + i * 8);
-      if (PRO == PRO_RESNORM) ua[j] = *reinterpret_cast<const uint4*>(a.u + i * 8);
+      if (PRO == PRO_RESNORM || PRO == PRO_GATEDNORM)
+        ua[j] = *reinterpret_cast<const uint4*>(a.u + i * 8);
     } else {
       xa[j] = make_uint4(0, 0, 0, 0);
       ua[j] = make_uint4(0, 0, 0, 0);
@@ -119,6 +129,37 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
     for (int j = 0; j < PER; ++j) {
       const int i = tid + j * NT;
       if (i < NV) xs[i] = xa[j];
+    }
+  } else if (PRO == PRO_GATEDNORM) {
+    // Group i holds elements 8i..8i+7, so head = i/16: the 16 groups of a head
+    // sit on the 16 lanes of one DPP row (NT is a multiple of 16).
+    static_assert(NT % 16 == 0, "gated norm needs whole heads per row");
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid + j * NT;
+      float s[8], z[8], wn[8];
+      unpack8(xa[j], s);
+      unpack8(ua[j], z);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += s[e] * s[e];
+      ss = row16_sum(ss);
+      const float inv = rsqrt_cr(ss / (float)kGatedHead + a.eps);
+      if (i < NV && i * 8 < a.K) {
+        load_nw8(a, (i * 8) % kGatedHead, wn);
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float nb = round_bf(s[e] * inv);
+          const float weighted = round_bf(nb * round_bf(wn[e]));
+          o[e] = weighted * silu_f(z[e]);
+        }
+        const uint4 v = pack8(o);
+        xs[i] = v;
+        if (writer && a.xn_out) *reinterpret_cast<uint4*>(a.xn_out + i * 8) = v;
+      } else if (i < NV) {
+        xs[i] = make_uint4(0, 0, 0, 0);
+      }
     }
   } else {
     float s[PER][8];
@@ -201,10 +242,19 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
   }
   if (lane < P && n0 + lane < a.N) {
     float v;
-    if (EPI == EPI_STORE) {
+    if (EPI == EPI_STORE || EPI == EPI_CONV) {
       v = acc[0];
 #pragma unroll
       for (int r = 1; r < R; ++r) v = lane == r ? acc[r] : v;
+      if (EPI == EPI_CONV) {
+        const int n = n0 + lane;
+        const uint32_t yb = f2bf(v);
+        if (n < a.conv_channels) {
+          const float c = conv_update_channel(a.conv_state + (size_t)n * a.conv_kw,
+                                              a.conv_w + (size_t)n * a.conv_kw, yb, a.conv_kw);
+          a.conv_out[n] = (uint16_t)f2bf(c);
+        }
+      }
     } else {
       float g = acc[0], up = acc[P];
 #pragma unroll
@@ -272,8 +322,13 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(const GemvArgs a) {
     return;
   }
   if (lane == 0 && n < a.N) {
-    if (EPI == EPI_STORE) {
+    if (EPI == EPI_STORE || EPI == EPI_CONV) {
       a.y[n] = (uint16_t)f2bf(g);
+      if (EPI == EPI_CONV && n < a.conv_channels) {
+        const float c = conv_update_channel(a.conv_state + (size_t)n * a.conv_kw,
+                                            a.conv_w + (size_t)n * a.conv_kw, f2bf(g), a.conv_kw);
+        a.conv_out[n] = (uint16_t)f2bf(c);
+      }
     } else {
       a.y[n] = (uint16_t)f2bf(round_bf(silu_f(round_bf(g))) * round_bf(up));
     }
@@ -284,6 +339,7 @@ __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __r
                                                    int n, long long* out) {
   __shared__ unsigned long long s[16];
   uint64_t b = 0;
+#pragma unroll 8
   for (int i = threadIdx.x; i < n; i += 1024) b = u64_max(b, cand[i]);
   b = wave_max_u64(b);
   if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = b;
@@ -305,7 +361,8 @@ long long launch_fast(const GemvArgs& a, hipStream_t stream) {
 
 bool fast_ok(const GemvArgs& a, int PRO) {
   return (a.K % 512 == 0) && q35_aligned16(a.W) && q35_aligned16(a.x) &&
-         (PRO != PRO_RESNORM || q35_aligned16(a.u)) && q35_aligned16(a.r_out) &&
+         ((PRO != PRO_RESNORM && PRO != PRO_GATEDNORM) || q35_aligned16(a.u)) &&
+         q35_aligned16(a.r_out) &&
          q35_aligned16(a.xn_out) && (PRO == PRO_NONE || q35_aligned16(a.nw));
 }
 
@@ -325,33 +382,65 @@ int dispatch(const GemvArgs& a, hipStream_t stream) {
       if (nch == 2) { launch_fast<4, 2, 2, PRO, EPI>(a, stream); return q35_last_error(); }
     }
   }
-  const unsigned blocks = (unsigned)((a.N + 3) / 4);
-  gemv_bf16_generic<PRO, EPI><<<blocks > 0 ? blocks : 1, 256, 0, stream>>>(a);
-  return q35_last_error();
+  if constexpr (PRO == PRO_GATEDNORM) {
+    return (int)hipErrorInvalidValue;  // gated-norm prologue: fast path only
+  } else {
+    const unsigned blocks = (unsigned)((a.N + 3) / 4);
+    gemv_bf16_generic<PRO, EPI><<<blocks > 0 ? blocks : 1, 256, 0, stream>>>(a);
+    return q35_last_error();
+  }
 }
 
-// lm_head tile: 4 waves x 1 row per workgroup (fastest of the swept
-// {2,4,8} waves x {1,2,4,8} rows; a persistent grid-stride variant was slower).
-constexpr int kTopWV = 4, kTopR = 1;
+// lm_head tile: 4 waves x 4 rows per workgroup, 15520 candidates for the
+// final reduction (one row per wave ran 2% faster but quadrupled the final
+// reduction; a persistent grid-stride variant was slower).
+constexpr int kTopWV = 4, kTopR = 4;
 
 }  // namespace
 
 extern "C" {
 
-// y[N] = W[N,K] . x[K]; optional prologue: mode 0 none, 1 rmsnorm(x), 2 residual add + rmsnorm.
+// y[N] = W[N,K] . xa[K]; prologue: 0 none, 1 rmsnorm(x), 2 residual add + rmsnorm,
+// 3 gated rmsnorm of x (heads of 128) with gate u.
 int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_w, int norm_w_f32,
                   float eps, void* residual_out, void* x_norm_out, void* y, int N, int K,
                   int prologue, hipStream_t stream) {
   Q35_CHECK_ARG(N > 0 && K > 0 && W && x && y);
+  Q35_CHECK_ARG(prologue >= 0 && prologue <= 3);
+  Q35_CHECK_ARG(prologue == 0 || norm_w);
+  Q35_CHECK_ARG(prologue < 2 || u);
+  Q35_CHECK_ARG(prologue != 3 || K % kGatedHead == 0);
+  GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
+             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
+             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0};
+  if (prologue == 0) return dispatch<PRO_NONE, EPI_STORE>(a, stream);
+  if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_STORE>(a, stream);
+  if (prologue == 2) return dispatch<PRO_RESNORM, EPI_STORE>(a, stream);
+  return dispatch<PRO_GATEDNORM, EPI_STORE>(a, stream);
+}
+
+// As q35_gemv_bf16 (prologue 0-2), and rows n < conv_channels also run the
+// single-token depthwise conv update on y[n]: conv_out[n] =
+// bf16(silu(bf16(sum_t w[n,t] * window[t]))), window = (state[n,1:], y[n]),
+// state shifted in place. One wave owns each row, so each conv channel and its
+// state are touched by exactly one wave.
+int q35_gemv_conv(const void* W, const void* x, const void* u, const void* norm_w, int norm_w_f32,
+                  float eps, void* residual_out, void* y, int N, int K, int prologue,
+                  const void* conv_w, void* conv_state, void* conv_out, int conv_channels,
+                  int conv_kw, hipStream_t stream) {
+  Q35_CHECK_ARG(N > 0 && K > 0 && W && x && y);
   Q35_CHECK_ARG(prologue >= 0 && prologue <= 2);
   Q35_CHECK_ARG(prologue == 0 || norm_w);
   Q35_CHECK_ARG(prologue != 2 || u);
+  Q35_CHECK_ARG(conv_channels >= 0 && conv_channels <= N && conv_kw > 0 && conv_kw <= 16);
+  Q35_CHECK_ARG(conv_channels == 0 || (conv_w && conv_state && conv_out));
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
-             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
-             norm_w_f32, eps};
-  if (prologue == 0) return dispatch<PRO_NONE, EPI_STORE>(a, stream);
-  if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_STORE>(a, stream);
-  return dispatch<PRO_RESNORM, EPI_STORE>(a, stream);
+             (uint16_t*)residual_out, nullptr, (uint16_t*)y, nullptr, N, K, norm_w_f32, eps,
+             (const uint16_t*)conv_w, (uint16_t*)conv_state, (uint16_t*)conv_out, conv_channels,
+             conv_kw};
+  if (prologue == 0) return dispatch<PRO_NONE, EPI_CONV>(a, stream);
+  if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_CONV>(a, stream);
+  return dispatch<PRO_RESNORM, EPI_CONV>(a, stream);
 }
 
 // y[N] = bf16(silu(bf16(W[n].x))) * bf16(W[N+n].x) with W = [gate; up] of shape [2N, K].
@@ -364,7 +453,7 @@ int q35_swiglu_gemv(const void* W, const void* x, const void* u, const void* nor
   Q35_CHECK_ARG(prologue != 2 || u);
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
              (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
-             norm_w_f32, eps};
+             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0};
   if (prologue == 0) return dispatch<PRO_NONE, EPI_SWIGLU>(a, stream);
   if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_SWIGLU>(a, stream);
   return dispatch<PRO_RESNORM, EPI_SWIGLU>(a, stream);
@@ -382,7 +471,7 @@ int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace
   Q35_CHECK_ARG(V > 0 && K > 0 && W && x && workspace && out);
   Q35_CHECK_ARG(workspace_slots >= q35_lm_head_top1_workspace(V, K) && V < (1 << 30));
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, nullptr,
-             (unsigned long long*)workspace, V, K, 0, 0.f};
+             (unsigned long long*)workspace, V, K, 0, 0.f, nullptr, nullptr, nullptr, 0, 0};
   long long nc;
   if (K == 2048 && fast_ok(a, PRO_NONE)) {
     nc = launch_fast<kTopWV, kTopR, 4, PRO_NONE, EPI_TOP1>(a, stream);

@@ -150,3 +150,19 @@ Q35_DEV void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+
+// Single-token depthwise causal conv for one channel (reference
+// kernels.py:622-656): window = (state[1..kw-1], x); the state is shifted in
+// place; returns bf16(silu(bf16(sum_t w[t]*window[t]))) as fp32.
+Q35_DEV float conv_update_channel(uint16_t* __restrict__ st, const uint16_t* __restrict__ w,
+                                  uint32_t xin, int kw) {
+  float acc = 0.f;
+  for (int t = 0; t < kw - 1; ++t) {
+    const uint16_t s = st[t + 1];
+    st[t] = s;
+    acc = fmaf(bf2f(s), bf2f(w[t]), acc);
+  }
+  st[kw - 1] = (uint16_t)xin;
+  acc = fmaf(bf2f(xin), bf2f(w[kw - 1]), acc);
+  return round_bf(silu_f(round_bf(acc)));
+}

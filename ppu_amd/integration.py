@@ -342,6 +342,10 @@ def _fused_decode_layers(text_model, residual, config, past_key_values, position
         else:
             mod = layer.self_attn
             lin = mod._q35_qgkv
+        delta = layer.block_type == "linear_attention"
+        if delta:
+            conv_state, rec_state = _delta_cache_tensors(
+                mod, past_key_values, 1, 1, residual.device, residual.dtype)
         # residual add + input RMSNorm fused into the packed projection
         if lin.a8w8:
             if update is None:
@@ -349,16 +353,29 @@ def _fused_decode_layers(text_model, residual, config, past_key_values, position
             else:
                 residual, normalized = K.residual_add_rms_norm(residual, update, ln.weight, ln.eps)
             packed = lin(normalized)
+        elif delta:
+            # ... and the conv1d update in its epilogue
+            r_new, packed, qkv = K.norm_linear_conv(residual, update, ln.weight, ln.eps, lin.weight,
+                                                    mod._q35_conv_w, conv_state)
+            if r_new is not None:
+                residual = r_new
         elif update is None:
             packed = K.norm_linear(residual, ln.weight, ln.eps, lin.weight)
         else:
             residual, packed = K.residual_norm_linear(residual, update, ln.weight, ln.eps, lin.weight)
-        if layer.block_type == "linear_attention":
-            conv_state, rec_state = _delta_cache_tensors(
-                mod, past_key_values, 1, 1, residual.device, residual.dtype)
-            core = K.delta_decode_fused(packed, mod._q35_conv_w, conv_state, mod.A_log, mod.dt_bias,
-                                        rec_state, mod.norm.weight, mod.layer_norm_epsilon)
-            update = mod._q35_out(core.reshape(1, 1, mod.value_dim))
+        if delta:
+            if lin.a8w8 or mod._q35_out.a8w8:
+                core = K.delta_decode_fused(packed, mod._q35_conv_w, conv_state, mod.A_log,
+                                            mod.dt_bias, rec_state, mod.norm.weight,
+                                            mod.layer_norm_epsilon)
+                update = mod._q35_out(core.reshape(1, 1, mod.value_dim))
+            else:
+                # delta rule on the convolved qkv, then gated RMSNorm as the
+                # prologue of the output projection
+                core = K.delta_recurrent_fused(qkv, packed, mod.A_log, mod.dt_bias, rec_state)
+                z = packed[..., mod.conv_dim : mod.conv_dim + mod.value_dim]
+                update = K.gated_norm_linear(core, z, mod.norm.weight, mod.layer_norm_epsilon,
+                                             mod._q35_out.weight)
         else:
             cache_layer = _static_cache_layer(mod, past_key_values, residual)
             q, _, _ = K.qgkv_norm_rope(

@@ -222,6 +222,77 @@ def norm_linear(
     return out
 
 
+def norm_linear_conv(
+    residual: torch.Tensor,
+    update: torch.Tensor | None,
+    norm_weight: torch.Tensor,
+    eps: float,
+    weight: torch.Tensor,
+    conv_weight: torch.Tensor,
+    conv_state: torch.Tensor,
+) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor]:
+    """DeltaNet input projection of one token in one launch.
+
+    Prologue: ``r' = residual + update`` and its RMSNorm (or the RMSNorm of
+    ``residual`` when ``update`` is None, the first layer); GEMV against the
+    packed ``[qkv | z | a | b]`` weight; epilogue: for the first C rows
+    (C = conv channels) the single-token causal conv update of reference
+    kernels.py:622-656, which shifts ``conv_state`` in place. Returns
+    ``(r' or None, packed [1,1,N], qkv [1,1,C])``.
+    """
+
+    k = residual.shape[-1]
+    if residual.numel() != k or weight.ndim != 2 or weight.shape[1] != k:
+        raise ValueError("fused projection expects one token matching the weight")
+    channels, kw = conv_weight.shape
+    if conv_state.shape[-2:] != (channels, kw) or conv_state.numel() != channels * kw:
+        raise ValueError("conv state does not match the conv weight (batch 1)")
+    if not conv_state.is_contiguous() or not conv_weight.is_contiguous():
+        raise ValueError("conv tensors must be contiguous")
+    _need_bf16(residual, weight, conv_weight, conv_state)
+    w, wf = _param(norm_weight)
+    n = weight.shape[0]
+    dev = residual.device
+    packed = torch.empty((1, 1, n), device=dev, dtype=_BF16)
+    qkv = torch.empty((1, 1, channels), device=dev, dtype=_BF16)
+    r_out = None
+    if update is not None:
+        if update.shape != residual.shape:
+            raise ValueError("residual and update must have identical shape")
+        r_out = torch.empty_like(residual)
+    _lib.call("q35_gemv_conv", weight.data_ptr(), residual.data_ptr(), _lib.ptr(update),
+              w.data_ptr(), wf, float(eps), _lib.ptr(r_out), packed.data_ptr(), n, k,
+              2 if update is not None else 1, conv_weight.data_ptr(), conv_state.data_ptr(),
+              qkv.data_ptr(), channels, kw, _stream(residual))
+    return r_out, packed, qkv
+
+
+def gated_norm_linear(
+    core: torch.Tensor,
+    gate: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    weight: torch.Tensor,
+) -> torch.Tensor:
+    """``linear(gated_rms_norm(core, gate), W)`` for one token in one launch:
+    the gated RMSNorm of reference kernels.py:139 (heads of 128, ``w`` used
+    directly) as the prologue of the DeltaNet output projection. ``gate`` may
+    be a contiguous slice of the packed projection."""
+
+    k = core.numel()
+    if gate.numel() != k or weight.ndim != 2 or weight.shape[1] != k or k % 128:
+        raise ValueError("gated norm GEMV expects one token of whole 128-wide heads")
+    if not core.is_contiguous() or not gate.is_contiguous():
+        raise ValueError("gated norm GEMV inputs must be contiguous")
+    _need_bf16(core, gate, weight)
+    w, wf = _param(norm_weight)
+    n = weight.shape[0]
+    out = torch.empty((1, 1, n), device=core.device, dtype=_BF16)
+    _lib.call("q35_gemv_bf16", weight.data_ptr(), core.data_ptr(), gate.data_ptr(), w.data_ptr(),
+              wf, float(eps), None, None, out.data_ptr(), n, k, 3, _stream(core))
+    return out
+
+
 def prefill_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``F.linear(x, W)`` for M > 1 tokens (prefill), bf16 in/out, fp32 accumulate.
 
@@ -570,6 +641,11 @@ def gqa_prefill_attention(
 
 
 # ------------------------------------------------------------------ A8W8
+# Up to this many tokens the A8W8 linear runs on the dot4 GEMV kernel (weights
+# read once per launch); above it, on an int8 GEMM.
+_A8W8_GEMV_MAX_M = 16
+
+
 def quantize_weight_i8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-output-channel symmetric int8 weights and fp32 ``[N,1]`` scales.
     reference explore_runtime_quantization.py:142-155."""
@@ -627,9 +703,19 @@ def a8w8_linear(
     xq = torch.empty((m, k), device=x.device, dtype=torch.int8)
     sx = torch.empty((m, 1), device=x.device, dtype=torch.float32)
     y = torch.empty((m, n), device=x.device, dtype=_BF16)
-    acc = torch.empty((m, n), device=x.device, dtype=torch.int32) if return_acc else None
-    _lib.call("q35_gemv_a8w8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), weight_q.data_ptr(),
-              sw.data_ptr(), y.data_ptr(), _lib.ptr(acc), m, n, k, _stream(x))
+    if m > _A8W8_GEMV_MAX_M and n % 8 == 0 and k % 8 == 0:
+        # Prefill: per-token quantisation (gfx950 kernel), the int8 GEMM on the
+        # ROCm library (hipBLASLt, exact int32 accumulators), dequant kernel.
+        _lib.call("q35_quant_act_i8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), m, k, _stream(x))
+        acc = torch._int_mm(xq, weight_q.t())
+        _lib.call("q35_dequant_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(), m,
+                  n, _stream(x))
+        if not return_acc:
+            acc = None
+    else:
+        acc = torch.empty((m, n), device=x.device, dtype=torch.int32) if return_acc else None
+        _lib.call("q35_gemv_a8w8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), weight_q.data_ptr(),
+                  sw.data_ptr(), y.data_ptr(), _lib.ptr(acc), m, n, k, _stream(x))
     y = y.reshape(*x.shape[:-1], n)
     if not (return_quant or return_acc):
         return y

@@ -3,10 +3,11 @@
 A Transformers Qwen3.5 model (synthetic seeded weights) is patched with
 ``apply_fusions`` and run on the GPU: prefill, then greedy decode through the
 captured graph. The oracle decoder gets the identical weights on the CPU and
-is teacher-forced with the GPU's tokens, so every step compares the GPU token
-with the oracle's argmax on the same history. A step may differ only where
-the oracle's top-2 bf16 logit margin is within the accumulated bf16 rounding
-noise of the two paths (MARGIN); every mismatch is printed with its margin.
+is teacher-forced with the GPU's tokens, so every step compares the two paths
+on the same history: the final hidden states must agree to HIDDEN_RTOL, and a
+token may differ only where the oracle's logit gap between the two tokens is
+within the measured GPU-vs-oracle difference of those two logits (random-init
+logits often tie to the bf16 ulp). Every flip is printed with its numbers.
 """
 
 from __future__ import annotations
@@ -19,9 +20,10 @@ from ppu_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-# Two bf16 ulps at logit magnitude ~4: the largest gap a different fp32
-# summation order can close between otherwise identical paths.
-MARGIN = 0.0625
+# Relative L2 error allowed between the GPU's and the oracle's final hidden
+# state at a teacher-forced step: bf16 rounding noise accumulated through the
+# layers (measured ~0.3-0.6 % on the 2B model), with headroom.
+HIDDEN_RTOL = 2e-2
 
 
 def _build(cfg, gpu, fusion):
@@ -33,34 +35,72 @@ def _build(cfg, gpu, fusion):
     return model, state, stats
 
 
-def _check_teacher_forced(oracle, prompt, tokens, max_len):
-    ref = oracle.teacher_forced(prompt.cpu(), tokens[:-1], max_len)
-    bad = []
+@torch.inference_mode()
+def _gpu_hidden_states(model, prompt, tokens, bucket):
+    """Final-normed hidden state of every step of the GPU path, teacher-forced
+    on ``tokens`` (prefill, then one fused decode step per token)."""
+    from transformers.cache_utils import StaticCache
+
+    dev = prompt.device
+    cache = StaticCache(config=model.config, max_cache_len=bucket)
+    pos = torch.arange(prompt.shape[1], device=dev).view(1, -1)
+    out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
+    hidden = [out.last_hidden_state[:, -1].float().cpu()]
+    p = torch.full((1, 1), prompt.shape[1], device=dev, dtype=torch.long)
+    for tok in tokens[:-1]:
+        out = model.model(input_ids=torch.tensor([[tok]], device=dev), position_ids=p,
+                          past_key_values=cache, use_cache=True)
+        hidden.append(out.last_hidden_state[:, -1].float().cpu())
+        p.add_(1)
+    return hidden
+
+
+def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden):
+    """Every step: the GPU's hidden state within HIDDEN_RTOL of the oracle's;
+    the tokens equal, or the flip explained: the oracle's logit gap between the
+    two tokens is no larger than the measured GPU-vs-oracle difference of
+    those two logits plus one bf16 ulp."""
+    ref, ref_hidden = oracle.teacher_forced(prompt.cpu(), tokens[:-1], max_len, return_hidden=True)
+    emb = oracle.w["embed"].double()
+    bad, errs = [], []
     for step, (tok, (rt, margin)) in enumerate(zip(tokens, ref)):
+        hg, ho = gpu_hidden[step].double(), ref_hidden[step].double()
+        err = float((hg - ho).norm() / ho.norm())
+        errs.append(err)
+        if err > HIDDEN_RTOL:
+            bad.append((step, "hidden", err))
         if tok != rt:
-            print(f"step {step}: gpu {tok} oracle {rt} margin {margin:.4f}", flush=True)
-            if margin > MARGIN:
-                bad.append((step, tok, rt, margin))
-    margins = [m for _, m in ref]
-    print(f"{len(tokens)} steps, {sum(t == r for t, (r, _) in zip(tokens, ref))} identical, "
-          f"min margin {min(margins):.4f}", flush=True)
-    assert not bad, f"mismatches beyond the rounding margin: {bad}"
+            rows = emb[[tok, rt]]
+            lg = (hg @ rows.t()).float().to(torch.bfloat16).double()[0]
+            lo = (ho @ rows.t()).float().to(torch.bfloat16).double()[0]
+            gap = float(lo[1] - lo[0])
+            noise = float((lg - lo).abs().sum())
+            ulp = 2.0 ** (torch.floor(torch.log2(lo.abs().max())).item() - 7)
+            print(f"step {step}: gpu {tok} oracle {rt} oracle margin {margin:.4f} gap {gap:.4f} "
+                  f"logit noise {noise:.4f} hidden err {err:.2e}", flush=True)
+            if gap > noise + ulp:
+                bad.append((step, tok, rt, gap, noise))
+    same = sum(t == r for t, (r, _) in zip(tokens, ref))
+    print(f"{len(tokens)} steps, {same} identical tokens, hidden rel err max {max(errs):.2e} "
+          f"mean {sum(errs) / len(errs):.2e}", flush=True)
+    assert not bad, f"steps outside the parity bound: {bad}"
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_tiny_model_greedy_vs_oracle(gpu, fused):
+@pytest.mark.parametrize("fused,a8w8", [(True, False), (False, False), (True, True)])
+def test_tiny_model_greedy_vs_oracle(gpu, fused, a8w8):
     from ppu_amd.generate import FusedGreedyGenerator
     from ppu_amd.integration import FusionConfig
 
     cfg = synth.config_tiny()
-    model, state, stats = _build(cfg, gpu, FusionConfig(fused_decode=fused))
+    model, state, stats = _build(cfg, gpu, FusionConfig(fused_decode=fused, a8w8=a8w8))
     assert stats["delta"] == 3 and stats["attention"] == 1
     g = torch.Generator().manual_seed(20260625)
     prompt = torch.randint(0, cfg.vocab_size, (1, 70), generator=g).to(gpu)
     res = FusedGreedyGenerator(model).generate(prompt, max_new_tokens=24)
     assert len(res.tokens) == 24
-    oracle = OracleDecoder(state, cfg)
-    _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"])
+    hidden = _gpu_hidden_states(model, prompt, res.tokens, res.meta["cache_bucket"])
+    oracle = OracleDecoder(state, cfg, a8w8=a8w8)
+    _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden)
 
 
 def test_graph_replay_matches_eager_decode(gpu):
@@ -103,3 +143,28 @@ def test_graph_replay_matches_eager_decode(gpu):
             graphed.append(int(runner.replay()))
             torch.cuda.synchronize()
         assert graphed == eager
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("variant", ["bf16", "a8w8"])
+def test_2b_prefill_1024_decode_64_vs_oracle(gpu, variant):
+    """the full 2B-shaped decoder, 1024-token uniform-random
+    prompt, 64 greedy tokens on the GPU (fused decode graph); the CPU oracle
+    decoder is teacher-forced on the same tokens and must agree at every step
+    whose top-2 margin exceeds the bf16 rounding noise."""
+    from ppu_amd.generate import FusedGreedyGenerator
+    from ppu_amd.integration import FusionConfig
+
+    torch.set_num_threads(16)
+    cfg = synth.config_2b()
+    model, state, _ = _build(cfg, gpu, FusionConfig(a8w8=variant == "a8w8"))
+    g = torch.Generator().manual_seed(synth.MODEL_SEED)
+    prompt = torch.randint(0, cfg.vocab_size, (1, 1024), generator=g)
+    res = FusedGreedyGenerator(model).generate(prompt.to(gpu), max_new_tokens=64)
+    print(f"GPU TTFT {res.ttft_seconds * 1e3:.2f} ms, decode {res.decode_tokens_per_second:.1f} tok/s",
+          flush=True)
+    hidden = _gpu_hidden_states(model, prompt.to(gpu), res.tokens, res.meta["cache_bucket"])
+    del model
+    torch.cuda.empty_cache()
+    oracle = OracleDecoder(state, cfg, a8w8=variant == "a8w8")
+    _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden)

@@ -456,3 +456,52 @@ def test_graph_capture_replay(gpu):
         assert torch.equal(y, y0), f"replay {i}"
         assert int(t) == int(t0), f"replay {i}"
         _ = (r * 2).sum().item()  # eager work between replays
+
+
+# ------------------------------------------------------------------ fused DeltaNet decode entries
+@pytest.mark.parametrize("first", [True, False])
+def test_norm_linear_conv(gpu, first):
+    """Input RMSNorm (+ residual add) -> packed projection GEMV -> conv1d update
+    epilogue, against the oracle chain rms_norm/residual_add_rms_norm ->
+    linear -> causal_conv1d."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 40)
+    r = randn(g, 1, 1, 2048)
+    u = randn(g, 1, 1, 2048)
+    nw = randn(g, 2048, scale=0.02)
+    W = randn(g, 8320, 2048, scale=0.02)
+    cw = randn(g, 6144, 4, scale=0.3)
+    cs0 = randn(g, 1, 6144, 4)
+    if first:
+        er, xn = None, ref.rms_norm(r, nw)
+    else:
+        er, xn = ref.residual_add_rms_norm(r, u, nw)
+    ep = ref.linear(xn, W)
+    cs_ref = cs0.clone()
+    eqkv = ref.causal_conv1d(ep, cw, cs_ref)
+    cs = cs0.to(gpu)
+    r_out, packed, qkv = K.norm_linear_conv(r.to(gpu), None if first else u.to(gpu), nw.to(gpu),
+                                            1e-6, W.to(gpu), cw.to(gpu), cs)
+    if not first:
+        assert torch.equal(r_out.cpu(), er)
+    close(packed, ep)
+    close(qkv, eqkv)
+    # state shift is exact; the appended value is this kernel's own bf16 projection
+    assert torch.equal(cs.cpu()[..., :3], cs0[..., 1:])
+    assert torch.equal(cs.cpu()[0, :, 3], packed.cpu()[0, 0, :6144])
+
+
+def test_gated_norm_linear(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 41)
+    core = randn(g, 16, 128)
+    packed = randn(g, 1, 1, 8320)
+    z = packed[..., 6144:8192]
+    nw = randn(g, 128, scale=0.02, mean=1.0)
+    W = randn(g, 2048, 2048, scale=0.02)
+    exp = ref.linear(ref.gated_rms_norm(core, z.reshape(16, 128), nw).reshape(1, 1, 2048), W)
+    pg = packed.to(gpu)
+    got = K.gated_norm_linear(core.to(gpu), pg[..., 6144:8192], nw.to(gpu), 1e-6, W.to(gpu))
+    close(got, exp)

@@ -1,0 +1,72 @@
+"""Pins the oracle decoder's data flow to Transformers' own eager Qwen3.5
+forward (CPU, same weights). The two differ only in rounding points (the
+fused path keeps the delta rule's L2 norms and gates in fp32, Transformers
+rounds some of them to bf16; prefill uses the chunked delta algorithm), so
+logits must agree to within bf16 noise: a missing residual, a swapped gate or
+a wrong packing offset moves them by O(1)."""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from oracle.model import OracleDecoder
+from ppu_amd import synth
+
+
+def _model():
+    cfg = synth.config_tiny()
+    m = synth.build_model(cfg, device="cpu")
+    state = {k: v.detach() for k, v in m.state_dict().items()}
+    return cfg, m, state
+
+
+def test_oracle_decoder_tracks_transformers_eager():
+    from transformers.cache_utils import DynamicCache
+
+    cfg, m, state = _model()
+    o = OracleDecoder(state, cfg)
+    ids = torch.randint(0, cfg.vocab_size, (1, 40), generator=torch.Generator().manual_seed(1))
+    cache = o.new_cache(128)
+    with torch.no_grad():
+        h = o.forward(ids, cache)
+        ol = F.linear(h, state["model.embed_tokens.weight"]).float()
+        pkv = DynamicCache(config=cfg)
+        tl = m(input_ids=ids, past_key_values=pkv, use_cache=True).logits.float()
+        scale = tl.abs().mean()
+        assert (ol - tl).abs().mean() < 0.05 * scale
+        assert (ol - tl).abs().max() < 0.3
+        assert (ol.argmax(-1) == tl.argmax(-1)).float().mean() > 0.8
+        for tok in (5, 17, 300):
+            tl = m(input_ids=torch.tensor([[tok]]), past_key_values=pkv, use_cache=True).logits.float()
+            ol = F.linear(o.forward(torch.tensor([[tok]]), cache), state["model.embed_tokens.weight"]).float()
+            assert (ol - tl).abs().max() < 0.3
+            assert (ol - tl).abs().mean() < 0.05 * tl.abs().mean()
+
+
+def test_oracle_packing_matches_module_weights():
+    cfg, m, state = _model()
+    o = OracleDecoder(state, cfg)
+    lw = o.w["layers"][0]
+    d = m.model.layers[0].linear_attn
+    assert lw["in_proj"].shape == (8320, 2048)
+    assert torch.equal(lw["in_proj"][:6144], d.in_proj_qkv.weight)
+    assert torch.equal(lw["in_proj"][6144:8192], d.in_proj_z.weight)
+    assert torch.equal(lw["in_proj"][8192:8208], d.in_proj_a.weight)
+    assert torch.equal(lw["in_proj"][8208:8224], d.in_proj_b.weight)
+    assert not lw["in_proj"][8224:].any()
+    a = o.w["layers"][3]
+    assert a["qgkv"].shape == (5120, 2048)
+
+
+def test_oracle_a8w8_close_to_bf16():
+    cfg, m, state = _model()
+    ids = torch.randint(0, cfg.vocab_size, (1, 24), generator=torch.Generator().manual_seed(2))
+    outs = []
+    for q in (False, True):
+        o = OracleDecoder(state, cfg, a8w8=q)
+        c = o.new_cache(64)
+        outs.append(F.linear(o.forward(ids, c), state["model.embed_tokens.weight"]).float())
+    # per-channel int8 weights / per-token int8 activations through every linear
+    # of 4 random layers: ~10% of the logit scale (noise, not garbage)
+    assert (outs[0] - outs[1]).abs().mean() < 0.2 * outs[0].abs().mean()
