@@ -67,7 +67,10 @@ int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_
                   float eps, void* residual_out, void* x_norm_out, void* y, int N, int K,
                   int prologue, void* stream);
 
-/* q35_gemv_bf16 (prologues 0-2) whose epilogue also runs, for rows n < conv_channels,
+/* x_row (optional int64 device scalar, prologue 1 only): x is row *x_row of an
+ * [x_rows, K] table (the token embedding lookup of integration.py:402-403) and the raw
+ * row is stored to residual_out.
+ * q35_gemv_bf16 (prologues 0-2) whose epilogue also runs, for rows n < conv_channels,
  * the single-token causal conv update on y[n]: conv_out[n] = bf16(silu(bf16(sum_t
  * conv_w[n,t] * window[t]))), window = (conv_state[n,1:], y[n]), conv_state shifted in
  * place. Replaces integration.py:245 (packed DeltaNet projection) followed by
@@ -75,7 +78,7 @@ int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_
 int q35_gemv_conv(const void* W, const void* x, const void* u, const void* norm_w, int norm_w_f32,
                   float eps, void* residual_out, void* y, int N, int K, int prologue,
                   const void* conv_w, void* conv_state, void* conv_out, int conv_channels,
-                  int conv_kw, void* stream);
+                  int conv_kw, const void* x_row, int x_rows, void* stream);
 
 /* y[N] = bf16(bf16(silu(bf16(W[n].xa))) * bf16(W[N+n].xa)), W = [gate; up] of [2N, K];
  * prologue as q35_gemv_bf16. Replaces qwen35_fused/kernels.py:232 (ppu_swiglu_gemv,
@@ -89,9 +92,12 @@ int q35_swiglu_gemv(const void* W, const void* x, const void* u, const void* nor
 /* Workspace slots (8 bytes each) for q35_lm_head_top1. */
 long long q35_lm_head_top1_workspace(int V, int K);
 /* out[0] (int64) = argmax_v bf16(W[v] . x), lowest index on ties; no logits stored.
+ * With advance (int64 device array of n_advance <= 64) every element is incremented
+ * after the token is written (the token feedback and position += 1 of graph.py:78-79).
  * Replaces qwen35_fused/kernels.py:1146 (lm_head_argmax, kernels :1093-1143). */
 int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace,
-                     long long workspace_slots, void* out, void* stream);
+                     long long workspace_slots, void* out, void* advance, int n_advance,
+                     void* stream);
 
 /* ---- DeltaNet --------------------------------------------------------- */
 
@@ -147,6 +153,21 @@ long long q35_gqa_decode_workspace(int cache_len, int q_heads, int kv_heads, int
 int q35_gqa_decode(const void* q, const void* K, const void* V, const void* valid_len, float scale,
                    const void* packed_gate, void* out, void* workspace, long long workspace_floats,
                    int QH, int KVH, int D, int cache_len, void* stream);
+
+/* One decode token of a full-attention layer after its packed projection: Q/K RMSNorm
+ * (1 + w) and partial RoPE computed in the kernel (cos/sin from the int64 device
+ * positions pos_t/pos_h/pos_w and fp32 inv_freq, interleaved multimodal sections sec_h,
+ * sec_w as Transformers' rotary table), K/V stored into the static cache at index
+ * *cache_len_dev, split-K attention over the cache and the new token, combine, sigmoid
+ * gate, and *cache_len_dev += 1. out [QH*D] bf16. Replaces the chain
+ * integration.py:298-358 (qgkv_norm_rope :507, cumulative_length.add_, gqa_decode_attention
+ * :1031, attention_gate_mul :312) after the packed projection. */
+int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, int w_f32,
+                         const void* inv_freq, const void* pos_t, const void* pos_h,
+                         const void* pos_w, int sec_h, int sec_w, int rotary_dim, void* K, void* V,
+                         void* cache_len_dev, float scale, void* out, void* workspace,
+                         long long workspace_floats, int QH, int KVH, int D, int cache_len,
+                         void* stream);
 
 /* Causal GQA prefill attention: q [B,QH,L,D], K/V [B,KVH,cache_len,D] holding
  * the L prompt tokens from position start; query row i attends to keys

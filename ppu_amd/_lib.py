@@ -31,9 +31,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_attn_gate_mul": (_I, [_P, _P, _P, _L, _I, _I, _I, _P]),
     "q35_gemv_bf16": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _I, _I, _P]),
     "q35_swiglu_gemv": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _I, _I, _P]),
-    "q35_gemv_conv": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "q35_gemv_conv": (
+        _I, [_P, _P, _P, _P, _I, _F, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _I, _P]),
     "q35_lm_head_top1_workspace": (_L, [_I, _I]),
-    "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P]),
+    "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),
     "q35_conv1d_update": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "q35_conv1d_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "q35_delta_decode": (
@@ -50,6 +51,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_gqa_decode_workspace": (_L, [_I, _I, _I, _I]),
     "q35_gqa_decode": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _L, _I, _I, _I, _I, _P]),
     "q35_gqa_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _F, _P]),
+    "q35_gqa_decode_fused": (
+        _I,
+        [_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P, _L, _I, _I, _I, _I,
+         _P],
+    ),
     "q35_quant_weight_i8": (_I, [_P, _P, _P, _I, _I, _P]),
     "q35_quant_act_i8": (_I, [_P, _P, _P, _I, _I, _P]),
     "q35_gemv_a8w8": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),

@@ -116,32 +116,133 @@ __global__ __launch_bounds__(256) void qgkv_norm_rope_k(
 constexpr int kAD = 256;
 constexpr int kMaxG = 8;
 
-template <int G>
+// Extra inputs of the fused decode step: the packed QGKV row of the current
+// token, the Q/K norm weights, the rotary frequencies and positions. The
+// kernel then normalises and rotates q itself (every workgroup, its own G
+// heads), and the workgroup whose chunk holds the new token also computes
+// k, writes k and v into the cache and attends to the new token from LDS.
+struct FusedQ {
+  const uint16_t* packed;      // [2*QH*D + 2*KVH*D]
+  const void* q_w;
+  const void* k_w;
+  int w_f32;
+  const float* inv_freq;       // [rot/2] fp32
+  const long long* pos_t;      // text/temporal position
+  const long long* pos_h;      // multimodal rope rows (may equal pos_t)
+  const long long* pos_w;
+  int sec_h, sec_w;            // interleaved mrope: frequencies taken from H / W rows
+  int rot;                     // rotary dims (64)
+  uint16_t* k_cache;           // written at the new token's position
+  uint16_t* v_cache;
+};
+
+// Q/K RMSNorm (1 + w) + partial RoPE of one 256-wide head held by a wave
+// (lane: dims 4*lane..+3), with cos/sin computed from the positions exactly as
+// Transformers' rotary table does: freq_i = pos * inv_freq[i] (fp32),
+// cos/sin in fp32 rounded to bf16; dims c and c + rot/2 share freq c mod rot/2.
+Q35_DEV void norm_rope_row(const uint16_t* __restrict__ src, const void* w, int w_f32,
+                           const FusedQ& f, int lane, float (&o)[4]) {
+  float x[4], n[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = bf2f(src[lane * 4 + e]);
+    ss += x[e] * x[e];
+  }
+  const float inv = rsqrt_cr(wave_sum(ss) / (float)kAD + 1.0e-6f);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int c = lane * 4 + e;
+    const float wc = w_f32 ? reinterpret_cast<const float*>(w)[c] : bf2f(reinterpret_cast<const uint16_t*>(w)[c]);
+    n[e] = round_bf(x[e] * inv * (1.0f + wc));
+  }
+  const int half = f.rot / 2;
+  const int shift = half / 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int c = lane * 4 + e;
+    const int partner_lane = c < half ? lane + shift : lane - shift;
+    const float pn = __shfl(n[e], partner_lane & 63, 64);
+    if (c < f.rot) {
+      const int i = c < half ? c : c - half;
+      const long long* pp = f.pos_t;
+      if (i % 3 == 1 && i < 3 * f.sec_h) pp = f.pos_h;
+      if (i % 3 == 2 && i < 3 * f.sec_w) pp = f.pos_w;
+      const float ang = (float)pp[0] * f.inv_freq[i];
+      const float cs = round_bf(cosf(ang)), sn = round_bf(sinf(ang));
+      const float qc = round_bf(n[e] * cs);
+      const float rh = c < half ? -pn : pn;
+      o[e] = round_bf(qc + round_bf(rh * sn));
+    } else {
+      o[e] = n[e];
+    }
+  }
+}
+
+template <int G, bool FUSED>
 __global__ __launch_bounds__(256) void gqa_decode_split(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
     const long long* __restrict__ valid_len, float* __restrict__ acc_out, float* __restrict__ ml_out,
-    int cache_len, int chunk, int splits, float scale) {
+    int cache_len, int chunk, int splits, float scale, const FusedQ fq) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int kvh = blockIdx.x;
   const int split = blockIdx.y;
-  const int n_valid = (int)min((long long)cache_len, valid_len[0]);
+  const int QH = G * gridDim.x;
+  // FUSED: valid_len counts the tokens before this one; the new token sits at
+  // index n_old and is attended from LDS by the workgroup that owns it.
+  const long long n_old = FUSED ? valid_len[0] : 0;
+  const int n_cached = FUSED ? (int)min((long long)cache_len, n_old)
+                             : (int)min((long long)cache_len, valid_len[0]);
   const int start = split * chunk;
-  const int end = min(start + chunk, n_valid);
+  const int end = min(start + chunk, n_cached);
+  const bool owns_new = FUSED && n_old >= start && n_old < start + chunk;
+
+  __shared__ float q_s[FUSED ? G : 1][kAD];
+  __shared__ float kn_s[FUSED ? kAD : 1], vn_s[FUSED ? kAD : 1];
+  if (FUSED) {
+    for (int g = wid; g < G; g += 4) {
+      float o[4];
+      norm_rope_row(fq.packed + (size_t)(kvh * G + g) * 2 * kAD, fq.q_w, fq.w_f32, fq, lane, o);
+      *reinterpret_cast<float4*>(&q_s[g][4 * lane]) =
+          make_float4(o[0] * scale, o[1] * scale, o[2] * scale, o[3] * scale);
+    }
+    if (owns_new && wid == 0) {
+      float o[4];
+      const uint16_t* krow = fq.packed + (size_t)2 * QH * kAD + (size_t)kvh * kAD;
+      const uint16_t* vrow = krow + (size_t)gridDim.x * kAD;
+      norm_rope_row(krow, fq.k_w, fq.w_f32, fq, lane, o);
+      const uint2 vraw = *reinterpret_cast<const uint2*>(vrow + 4 * lane);
+      *reinterpret_cast<float4*>(&kn_s[4 * lane]) = make_float4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<float4*>(&vn_s[4 * lane]) =
+          make_float4(bf_lo(vraw.x), bf_hi(vraw.x), bf_lo(vraw.y), bf_hi(vraw.y));
+      if (n_old < cache_len) {
+        const size_t off = ((size_t)kvh * cache_len + (size_t)n_old) * kAD + 4 * lane;
+        *reinterpret_cast<uint2*>(fq.k_cache + off) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+        *reinterpret_cast<uint2*>(fq.v_cache + off) = vraw;
+      }
+    }
+    __syncthreads();
+  }
 
   // q slices for QK (16 dims of the lane's slice, per head), pre-scaled in fp32.
   const int ds = lane & 15;
   float qf[G][16];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const uint16_t* qh = q + (size_t)(kvh * G + g) * kAD + ds * 16;
-    float t8[8];
-    unpack8(*reinterpret_cast<const uint4*>(qh), t8);
+    if (FUSED) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qf[g][j] = t8[j] * scale;
-    unpack8(*reinterpret_cast<const uint4*>(qh + 8), t8);
+      for (int j = 0; j < 16; ++j) qf[g][j] = q_s[g][ds * 16 + j];
+    } else {
+      const uint16_t* qh = q + (size_t)(kvh * G + g) * kAD + ds * 16;
+      float t8[8];
+      unpack8(*reinterpret_cast<const uint4*>(qh), t8);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qf[g][8 + j] = t8[j] * scale;
+      for (int j = 0; j < 8; ++j) qf[g][j] = t8[j] * scale;
+      unpack8(*reinterpret_cast<const uint4*>(qh + 8), t8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[g][8 + j] = t8[j] * scale;
+    }
   }
 
   float m[G], l[G], acc[G][4];
@@ -205,6 +306,29 @@ __global__ __launch_bounds__(256) void gqa_decode_split(
       m[g] = m_new;
     }
   }
+  // The new token (FUSED): wave 0 of the owning workgroup folds it in.
+  if (owns_new && wid == 0) {
+    const float4 kn = *reinterpret_cast<const float4*>(&kn_s[4 * lane]);
+    const float4 vn = *reinterpret_cast<const float4*>(&vn_s[4 * lane]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float4 qv = *reinterpret_cast<const float4*>(&q_s[g][4 * lane]);
+      float sdot = qv.x * kn.x;
+      sdot = fmaf(qv.y, kn.y, sdot);
+      sdot = fmaf(qv.z, kn.z, sdot);
+      sdot = fmaf(qv.w, kn.w, sdot);
+      const float sc = wave_sum(sdot);
+      const float m_new = fmaxf(m[g], sc);
+      const float corr = expf(m[g] - m_new);
+      const float p = expf(sc - m_new);
+      l[g] = l[g] * corr + p;
+      acc[g][0] = fmaf(p, vn.x, acc[g][0] * corr);
+      acc[g][1] = fmaf(p, vn.y, acc[g][1] * corr);
+      acc[g][2] = fmaf(p, vn.z, acc[g][2] * corr);
+      acc[g][3] = fmaf(p, vn.w, acc[g][3] * corr);
+      m[g] = m_new;
+    }
+  }
   // Merge the 4 waves.
   __shared__ float m_s[4][kMaxG], l_s[4][kMaxG];
   __shared__ float a_s[4][kMaxG][kAD];
@@ -241,8 +365,11 @@ __global__ __launch_bounds__(256) void gqa_decode_split(
 __global__ __launch_bounds__(256) void gqa_decode_combine(const float* __restrict__ acc,
                                                           const float* __restrict__ ml,
                                                           const uint16_t* __restrict__ packed_gate,
-                                                          uint16_t* __restrict__ out, int splits) {
+                                                          uint16_t* __restrict__ out, int splits,
+                                                          long long* advance_len) {
   const int h = blockIdx.x;
+  // The split kernel that read the length has completed (stream order).
+  if (advance_len && h == 0 && threadIdx.x == 0) advance_len[0] += 1;
   __shared__ float w_s[1024];
   __shared__ float mx_s, l_s;
   if (threadIdx.x < 64) {
@@ -410,10 +537,12 @@ int q35_gqa_decode(const void* q, const void* K, const void* V, const void* vali
   float* acc = (float*)workspace;
   float* ml = acc + (size_t)QH * splits * D;
   dim3 grid(KVH, splits);
-#define Q35_GQA(GG)                                                                                \
-  gqa_decode_split<GG><<<grid, 256, 0, stream>>>((const uint16_t*)q, (const uint16_t*)K,          \
-                                                 (const uint16_t*)V, (const long long*)valid_len, \
-                                                 acc, ml, cache_len, chunk, splits, scale)
+  const FusedQ none{};
+#define Q35_GQA(GG)                                                                                    \
+  gqa_decode_split<GG, false><<<grid, 256, 0, stream>>>((const uint16_t*)q, (const uint16_t*)K,       \
+                                                        (const uint16_t*)V,                           \
+                                                        (const long long*)valid_len, acc, ml,         \
+                                                        cache_len, chunk, splits, scale, none)
   if (G == 1) Q35_GQA(1);
   else if (G == 2) Q35_GQA(2);
   else if (G == 4) Q35_GQA(4);
@@ -422,7 +551,63 @@ int q35_gqa_decode(const void* q, const void* K, const void* V, const void* vali
   int e = q35_last_error();
   if (e) return e;
   gqa_decode_combine<<<QH, kAD, 0, stream>>>(acc, ml, (const uint16_t*)packed_gate, (uint16_t*)out,
-                                             splits);
+                                             splits, nullptr);
+  return q35_last_error();
+}
+
+// One decode token of a full-attention layer after its packed projection:
+// Q/K RMSNorm + RoPE (cos/sin from the device positions and inv_freq), K/V
+// written into the static cache at index *cache_len_dev, split-K attention
+// over the cache plus the new token, LSE combine, sigmoid gate, and
+// *cache_len_dev += 1. Two launches; nothing is read on the host.
+int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, int w_f32,
+                         const void* inv_freq, const void* pos_t, const void* pos_h,
+                         const void* pos_w, int sec_h, int sec_w, int rotary_dim, void* K, void* V,
+                         void* cache_len_dev, float scale, void* out, void* workspace,
+                         long long workspace_floats, int QH, int KVH, int D, int cache_len,
+                         hipStream_t stream) {
+  Q35_CHECK_ARG(D == kAD && KVH > 0 && QH % KVH == 0 && cache_len > 0);
+  Q35_CHECK_ARG(packed && q_w && k_w && inv_freq && pos_t && K && V && cache_len_dev && out);
+  Q35_CHECK_ARG(rotary_dim > 0 && rotary_dim <= D && rotary_dim % 8 == 0);
+  Q35_CHECK_ARG(sec_h >= 0 && sec_w >= 0 && 3 * sec_h <= rotary_dim && 3 * sec_w <= rotary_dim);
+  const int G = QH / KVH;
+  Q35_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 8);
+  int chunk = 0;
+  const int splits = q35_gqa_decode_splits(cache_len, KVH, &chunk);
+  Q35_CHECK_ARG(splits <= 1024);
+  Q35_CHECK_ARG(workspace_floats >= q35_gqa_decode_workspace(cache_len, QH, KVH, D));
+  Q35_CHECK_ARG(q35_aligned16(K) && q35_aligned16(V) && q35_aligned16(workspace));
+  float* acc = (float*)workspace;
+  float* ml = acc + (size_t)QH * splits * D;
+  FusedQ f;
+  f.packed = (const uint16_t*)packed;
+  f.q_w = q_w;
+  f.k_w = k_w;
+  f.w_f32 = w_f32;
+  f.inv_freq = (const float*)inv_freq;
+  f.pos_t = (const long long*)pos_t;
+  f.pos_h = (const long long*)(pos_h ? pos_h : pos_t);
+  f.pos_w = (const long long*)(pos_w ? pos_w : pos_t);
+  f.sec_h = sec_h;
+  f.sec_w = sec_w;
+  f.rot = rotary_dim;
+  f.k_cache = (uint16_t*)K;
+  f.v_cache = (uint16_t*)V;
+  dim3 grid(KVH, splits);
+#define Q35_GQA(GG)                                                                                 \
+  gqa_decode_split<GG, true><<<grid, 256, 0, stream>>>(nullptr, (const uint16_t*)K,                \
+                                                       (const uint16_t*)V,                         \
+                                                       (const long long*)cache_len_dev, acc, ml,   \
+                                                       cache_len, chunk, splits, scale, f)
+  if (G == 1) Q35_GQA(1);
+  else if (G == 2) Q35_GQA(2);
+  else if (G == 4) Q35_GQA(4);
+  else Q35_GQA(8);
+#undef Q35_GQA
+  int e = q35_last_error();
+  if (e) return e;
+  gqa_decode_combine<<<QH, kAD, 0, stream>>>(acc, ml, (const uint16_t*)packed, (uint16_t*)out,
+                                             splits, (long long*)cache_len_dev);
   return q35_last_error();
 }
 

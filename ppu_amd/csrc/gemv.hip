@@ -50,6 +50,11 @@ struct GemvArgs {
   uint16_t* conv_out;      // [conv_channels]
   int conv_channels;
   int conv_kw;
+  // Optional row gather: x is row *x_row (clamped to [0, x_rows)) of a
+  // [x_rows, K] table (the token embedding); RMSNORM then also stores the raw
+  // row to r_out (the residual stream).
+  const long long* x_row;
+  int x_rows;
 };
 
 // Gated RMSNorm (reference kernels.py:115-155) runs over heads of this width.
@@ -83,12 +88,20 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
   const bool writer = blockIdx.x == 0;
 
   // 1. activation loads (cooperative, before the weight stream).
+  const uint16_t* xsrc = a.x;
+  if (a.x_row) {
+    long long r = a.x_row[0];
+    r = r < 0 ? 0 : (r >= a.x_rows ? a.x_rows - 1 : r);
+    xsrc += (size_t)r * a.K;
+  }
   uint4 xa[PER], ua[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = tid + j * NT;
     if (i < NV && i * 8 < a.K) {
-      xa[j] = *reinterpret_cast<const uint4*>(a.x + i * 8);
+      xa[j] = *reinterpret_cast<const uint4*>(xsrc + i * 8);
+      if (PRO == PRO_RMSNORM && writer && a.r_out)
+        *reinterpret_cast<uint4*>(a.r_out + i * 8) = xa[j];
       if (PRO == PRO_RESNORM || PRO == PRO_GATEDNORM)
         ua[j] = *reinterpret_cast<const uint4*>(a.u + i * 8);
     } else {
@@ -336,7 +349,8 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(const GemvArgs a) {
 }
 
 __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __restrict__ cand,
-                                                   int n, long long* out) {
+                                                   int n, long long* out, long long* advance,
+                                                   int n_advance) {
   __shared__ unsigned long long s[16];
   uint64_t b = 0;
 #pragma unroll 8
@@ -348,6 +362,7 @@ __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __r
     uint64_t m = s[0];
     for (int i = 1; i < 16; ++i) m = u64_max(m, s[i]);
     out[0] = (long long)top1_index(m);
+    for (int i = 0; i < n_advance; ++i) advance[i] += 1;
   }
 }
 
@@ -412,7 +427,7 @@ int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_
   Q35_CHECK_ARG(prologue != 3 || K % kGatedHead == 0);
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
              (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
-             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0};
+             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0, nullptr, 0};
   if (prologue == 0) return dispatch<PRO_NONE, EPI_STORE>(a, stream);
   if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_STORE>(a, stream);
   if (prologue == 2) return dispatch<PRO_RESNORM, EPI_STORE>(a, stream);
@@ -427,17 +442,19 @@ int q35_gemv_bf16(const void* W, const void* x, const void* u, const void* norm_
 int q35_gemv_conv(const void* W, const void* x, const void* u, const void* norm_w, int norm_w_f32,
                   float eps, void* residual_out, void* y, int N, int K, int prologue,
                   const void* conv_w, void* conv_state, void* conv_out, int conv_channels,
-                  int conv_kw, hipStream_t stream) {
+                  int conv_kw, const void* x_row, int x_rows, hipStream_t stream) {
   Q35_CHECK_ARG(N > 0 && K > 0 && W && x && y);
   Q35_CHECK_ARG(prologue >= 0 && prologue <= 2);
   Q35_CHECK_ARG(prologue == 0 || norm_w);
   Q35_CHECK_ARG(prologue != 2 || u);
   Q35_CHECK_ARG(conv_channels >= 0 && conv_channels <= N && conv_kw > 0 && conv_kw <= 16);
   Q35_CHECK_ARG(conv_channels == 0 || (conv_w && conv_state && conv_out));
+  Q35_CHECK_ARG(!x_row || (prologue == 1 && x_rows > 0));
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
              (uint16_t*)residual_out, nullptr, (uint16_t*)y, nullptr, N, K, norm_w_f32, eps,
              (const uint16_t*)conv_w, (uint16_t*)conv_state, (uint16_t*)conv_out, conv_channels,
-             conv_kw};
+             conv_kw, (const long long*)x_row, x_rows};
+  if (x_row && !fast_ok(a, PRO_RMSNORM)) return (int)hipErrorInvalidValue;
   if (prologue == 0) return dispatch<PRO_NONE, EPI_CONV>(a, stream);
   if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_CONV>(a, stream);
   return dispatch<PRO_RESNORM, EPI_CONV>(a, stream);
@@ -453,7 +470,7 @@ int q35_swiglu_gemv(const void* W, const void* x, const void* u, const void* nor
   Q35_CHECK_ARG(prologue != 2 || u);
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
              (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
-             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0};
+             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0, nullptr, 0};
   if (prologue == 0) return dispatch<PRO_NONE, EPI_SWIGLU>(a, stream);
   if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_SWIGLU>(a, stream);
   return dispatch<PRO_RESNORM, EPI_SWIGLU>(a, stream);
@@ -467,11 +484,14 @@ long long q35_lm_head_top1_workspace(int V, int K) {
 
 // out[0] (int64) = argmax_v bf16(W[v].x), lowest index on ties.
 int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace,
-                     long long workspace_slots, void* out, hipStream_t stream) {
+                     long long workspace_slots, void* out, void* advance, int n_advance,
+                     hipStream_t stream) {
+  Q35_CHECK_ARG(!advance || (n_advance >= 0 && n_advance <= 64));
   Q35_CHECK_ARG(V > 0 && K > 0 && W && x && workspace && out);
   Q35_CHECK_ARG(workspace_slots >= q35_lm_head_top1_workspace(V, K) && V < (1 << 30));
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, nullptr,
-             (unsigned long long*)workspace, V, K, 0, 0.f, nullptr, nullptr, nullptr, 0, 0};
+             (unsigned long long*)workspace, V, K, 0, 0.f, nullptr, nullptr, nullptr, 0, 0,
+             nullptr, 0};
   long long nc;
   if (K == 2048 && fast_ok(a, PRO_NONE)) {
     nc = launch_fast<kTopWV, kTopR, 4, PRO_NONE, EPI_TOP1>(a, stream);
@@ -481,7 +501,8 @@ int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace
   }
   const int e = q35_last_error();
   if (e) return e;
-  top1_final<<<1, 1024, 0, stream>>>((const unsigned long long*)workspace, (int)nc, (long long*)out);
+  top1_final<<<1, 1024, 0, stream>>>((const unsigned long long*)workspace, (int)nc, (long long*)out,
+                                     (long long*)advance, advance ? n_advance : 0);
   return q35_last_error();
 }
 

@@ -52,7 +52,12 @@ class GreedyDecodeGraph:
                                                past_key_values=self.cache, use_cache=True,
                                                return_dict=True)
                     hidden = outputs.last_hidden_state[:, -1, :].contiguous()
-                    next_token = lm_head_argmax(hidden, self.model.lm_head.weight)
+                    # top-1, token feedback and position += 1 in the final-reduce launch
+                    lm_head_argmax(hidden, self.model.lm_head.weight, out=self.token,
+                                   advance=self.position_ids)
+                    if self.output_tokens is not None:
+                        self.output_tokens[step].copy_(self.token)
+                    continue
                 else:
                     outputs = self.model(input_ids=self.token, attention_mask=None,
                                          position_ids=self.position_ids, past_key_values=self.cache,

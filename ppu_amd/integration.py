@@ -329,23 +329,45 @@ def _patch_attention(module: torch.nn.Module, config: FusionConfig) -> None:
 
 
 # ----------------------------------------------------------------- text forward
-def _fused_decode_layers(text_model, residual, config, past_key_values, position_embeddings):
-    """One token through all layers with fused launches; returns the final-normed hidden."""
+def _rope_in_kernel(text_model) -> bool:
+    """The fused attention kernel computes cos/sin itself for the default
+    (unscaled) rotary table; other rope types keep Transformers' table."""
+    rot = text_model.rotary_emb
+    return (getattr(rot, "rope_type", "default") == "default"
+            and float(getattr(rot, "attention_scaling", 1.0)) == 1.0
+            and rot.inv_freq.dtype == torch.float32)
+
+
+def _fused_decode_layers(text_model, input_ids, inputs_embeds, config, past_key_values,
+                         rotary_position_ids):
+    """One token through all layers with fused launches; returns the final-normed hidden.
+
+    Per DeltaNet layer: [residual add + RMSNorm -> packed projection -> conv1d
+    update] [delta rule] [gated RMSNorm -> out_proj] [residual add + RMSNorm ->
+    gate/up GEMV -> SwiGLU] [down]. Per attention layer: [residual add +
+    RMSNorm -> packed projection] [Q/K norm + RoPE + cache write + split-K
+    attention] [combine + gate + length += 1] [o_proj] and the same MLP. The
+    embedding row is gathered by the first projection when layer 0 is a bf16
+    DeltaNet layer.
+    """
     layers = text_model.layers[: text_model.config.num_hidden_layers]
-    cos, sin = position_embeddings
+    in_kernel_rope = _rope_in_kernel(text_model)
+    cos = sin = None
+    if not in_kernel_rope:
+        ref = inputs_embeds if inputs_embeds is not None else text_model.embed_tokens.weight[:1]
+        cos, sin = text_model.rotary_emb(ref, rotary_position_ids)
+    residual = inputs_embeds
     update = None
     for index, layer in enumerate(layers):
         ln = layer.input_layernorm
-        if layer.block_type == "linear_attention":
-            mod = layer.linear_attn
-            lin = mod._q35_in
-        else:
-            mod = layer.self_attn
-            lin = mod._q35_qgkv
         delta = layer.block_type == "linear_attention"
+        mod = layer.linear_attn if delta else layer.self_attn
+        lin = mod._q35_in if delta else mod._q35_qgkv
+        if residual is None and not (index == 0 and delta and not lin.a8w8):
+            residual = text_model.embed_tokens(input_ids.view(1, 1))
         if delta:
             conv_state, rec_state = _delta_cache_tensors(
-                mod, past_key_values, 1, 1, residual.device, residual.dtype)
+                mod, past_key_values, 1, 1, lin_device(lin), torch.bfloat16)
         # residual add + input RMSNorm fused into the packed projection
         if lin.a8w8:
             if update is None:
@@ -354,9 +376,14 @@ def _fused_decode_layers(text_model, residual, config, past_key_values, position
                 residual, normalized = K.residual_add_rms_norm(residual, update, ln.weight, ln.eps)
             packed = lin(normalized)
         elif delta:
-            # ... and the conv1d update in its epilogue
-            r_new, packed, qkv = K.norm_linear_conv(residual, update, ln.weight, ln.eps, lin.weight,
-                                                    mod._q35_conv_w, conv_state)
+            # ... and the conv1d update in its epilogue (embedding gather for layer 0)
+            if residual is None:
+                r_new, packed, qkv = K.norm_linear_conv(
+                    text_model.embed_tokens.weight, None, ln.weight, ln.eps, lin.weight,
+                    mod._q35_conv_w, conv_state, token=input_ids)
+            else:
+                r_new, packed, qkv = K.norm_linear_conv(residual, update, ln.weight, ln.eps,
+                                                        lin.weight, mod._q35_conv_w, conv_state)
             if r_new is not None:
                 residual = r_new
         elif update is None:
@@ -378,15 +405,23 @@ def _fused_decode_layers(text_model, residual, config, past_key_values, position
                                              mod._q35_out.weight)
         else:
             cache_layer = _static_cache_layer(mod, past_key_values, residual)
-            q, _, _ = K.qgkv_norm_rope(
-                packed, mod.q_norm.weight, mod.k_norm.weight, cos, sin,
-                q_heads=mod.config.num_attention_heads, kv_heads=mod.config.num_key_value_heads,
-                dim=mod.head_dim, rotary_dim=cos.shape[-1], cache_key=cache_layer.keys,
-                cache_value=cache_layer.values, cache_start=cache_layer.cumulative_length)
-            cache_layer.cumulative_length.add_(1)
-            out = K.gqa_decode_attention(q, cache_layer.keys, cache_layer.values,
-                                         cache_layer.cumulative_length, mod.scaling,
-                                         packed_gate=packed)
+            if in_kernel_rope:
+                out = K.gqa_decode_fused(
+                    packed, mod.q_norm.weight, mod.k_norm.weight, text_model.rotary_emb.inv_freq,
+                    rotary_position_ids, cache_layer.keys, cache_layer.values,
+                    cache_layer.cumulative_length, mod.scaling,
+                    q_heads=mod.config.num_attention_heads,
+                    mrope_section=tuple(text_model.rotary_emb.mrope_section))
+            else:
+                q, _, _ = K.qgkv_norm_rope(
+                    packed, mod.q_norm.weight, mod.k_norm.weight, cos, sin,
+                    q_heads=mod.config.num_attention_heads, kv_heads=mod.config.num_key_value_heads,
+                    dim=mod.head_dim, rotary_dim=cos.shape[-1], cache_key=cache_layer.keys,
+                    cache_value=cache_layer.values, cache_start=cache_layer.cumulative_length)
+                cache_layer.cumulative_length.add_(1)
+                out = K.gqa_decode_attention(q, cache_layer.keys, cache_layer.values,
+                                             cache_layer.cumulative_length, mod.scaling,
+                                             packed_gate=packed)
             update = mod._q35_o(out)
         # post-attention residual + RMSNorm fused into the SwiGLU GEMV
         pln = layer.post_attention_layernorm
@@ -403,6 +438,10 @@ def _fused_decode_layers(text_model, residual, config, past_key_values, position
     return normalized
 
 
+def lin_device(lin: "_Linear") -> torch.device:
+    return (lin.weight if lin.weight is not None else lin.wq).device
+
+
 def _patch_text_model(text_model: torch.nn.Module, config: FusionConfig) -> None:
     """reference integration.py:385-506."""
     if hasattr(text_model, "_fused_original_forward"):
@@ -413,19 +452,22 @@ def _patch_text_model(text_model: torch.nn.Module, config: FusionConfig) -> None
                 inputs_embeds=None, use_cache=None, **kwargs):
         if (input_ids is None) == (inputs_embeds is None):
             raise ValueError("specify exactly one of input_ids and inputs_embeds")
-        if inputs_embeds is None:
-            inputs_embeds = self.embed_tokens(input_ids)
-        if not _is_fast_tensor(inputs_embeds):
+        probe = inputs_embeds if inputs_embeds is not None else self.embed_tokens.weight
+        if not _is_fast_tensor(probe) or (input_ids is not None and not input_ids.is_cuda):
+            if inputs_embeds is None:
+                inputs_embeds = self.embed_tokens(input_ids)
             return self._fused_original_forward(
                 input_ids=None, attention_mask=attention_mask, position_ids=position_ids,
                 past_key_values=past_key_values, inputs_embeds=inputs_embeds, use_cache=use_cache,
                 **kwargs)
         if use_cache and past_key_values is None:
             past_key_values = DynamicCache(config=self.config)
+        src = inputs_embeds if inputs_embeds is not None else input_ids
+        batch, seq_len = src.shape[0], src.shape[1]
         if position_ids is None:
             past_seen = past_key_values.get_seq_length() if past_key_values is not None else 0
-            position_ids = torch.arange(inputs_embeds.shape[1], device=inputs_embeds.device) + past_seen
-            position_ids = position_ids.view(1, 1, -1).expand(4, inputs_embeds.shape[0], -1)
+            position_ids = torch.arange(seq_len, device=src.device) + past_seen
+            position_ids = position_ids.view(1, 1, -1).expand(4, batch, -1)
         elif position_ids.ndim == 2:
             position_ids = position_ids[None, ...].expand(4, position_ids.shape[0], -1)
         if position_ids.ndim == 3 and position_ids.shape[0] == 4:
@@ -437,18 +479,25 @@ def _patch_text_model(text_model: torch.nn.Module, config: FusionConfig) -> None
         if isinstance(attention_mask, torch.Tensor) and not torch.cuda.is_current_stream_capturing():
             if not bool(attention_mask.all()):
                 raise ValueError("the fused MI355X path does not support padded inputs")
-        position_embeddings = self.rotary_emb(inputs_embeds, rotary_position_ids)
-        residual = inputs_embeds.contiguous()
-        seq_len = inputs_embeds.shape[1]
         static = past_key_values is not None and all(
             hasattr(past_key_values.layers[i], "max_cache_len")
             for i, t in enumerate(self.config.layer_types) if t == "full_attention")
-        if (config.fused_decode and seq_len == 1 and inputs_embeds.shape[0] == 1 and static
+        if (config.fused_decode and seq_len == 1 and batch == 1 and static
                 and config.delta and config.attention and config.swiglu):
-            normalized = _fused_decode_layers(self, residual, config, past_key_values,
-                                              position_embeddings)
+            token = None
+            if inputs_embeds is None:
+                token = input_ids.reshape(-1)[:1]
+                if input_ids.dtype != torch.int64:
+                    token = token.to(torch.int64)
+            normalized = _fused_decode_layers(
+                self, token, None if inputs_embeds is None else inputs_embeds.contiguous(), config,
+                past_key_values, rotary_position_ids)
             return qwen_impl.Qwen3_5ModelOutputWithPast(last_hidden_state=normalized,
                                                         past_key_values=past_key_values)
+        if inputs_embeds is None:
+            inputs_embeds = self.embed_tokens(input_ids)
+        position_embeddings = self.rotary_emb(inputs_embeds, rotary_position_ids)
+        residual = inputs_embeds.contiguous()
         normalized = K.rms_norm(residual, self.layers[0].input_layernorm.weight,
                                 self.layers[0].input_layernorm.eps)
         n_layers = self.config.num_hidden_layers

@@ -230,6 +230,8 @@ def norm_linear_conv(
     weight: torch.Tensor,
     conv_weight: torch.Tensor,
     conv_state: torch.Tensor,
+    *,
+    token: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor]:
     """DeltaNet input projection of one token in one launch.
 
@@ -239,10 +241,20 @@ def norm_linear_conv(
     (C = conv channels) the single-token causal conv update of reference
     kernels.py:622-656, which shifts ``conv_state`` in place. Returns
     ``(r' or None, packed [1,1,N], qkv [1,1,C])``.
+
+    With ``token`` (an int64 device scalar) ``residual`` is the embedding table
+    ``[V, K]``: the first layer's input is its row ``token`` (the lookup of
+    integration.py:402-403, done in the prologue), returned as ``r'``.
     """
 
     k = residual.shape[-1]
-    if residual.numel() != k or weight.ndim != 2 or weight.shape[1] != k:
+    rows = residual.numel() // k
+    if token is not None:
+        if update is not None or token.dtype != torch.int64 or token.device != residual.device:
+            raise ValueError("embedding gather takes an int64 GPU token and no update")
+    elif rows != 1:
+        raise ValueError("fused projection expects one token")
+    if weight.ndim != 2 or weight.shape[1] != k:
         raise ValueError("fused projection expects one token matching the weight")
     channels, kw = conv_weight.shape
     if conv_state.shape[-2:] != (channels, kw) or conv_state.numel() != channels * kw:
@@ -260,10 +272,12 @@ def norm_linear_conv(
         if update.shape != residual.shape:
             raise ValueError("residual and update must have identical shape")
         r_out = torch.empty_like(residual)
+    elif token is not None:
+        r_out = torch.empty((1, 1, k), device=dev, dtype=_BF16)
     _lib.call("q35_gemv_conv", weight.data_ptr(), residual.data_ptr(), _lib.ptr(update),
               w.data_ptr(), wf, float(eps), _lib.ptr(r_out), packed.data_ptr(), n, k,
               2 if update is not None else 1, conv_weight.data_ptr(), conv_state.data_ptr(),
-              qkv.data_ptr(), channels, kw, _stream(residual))
+              qkv.data_ptr(), channels, kw, _lib.ptr(token), rows, _stream(residual))
     return r_out, packed, qkv
 
 
@@ -341,8 +355,16 @@ def lm_head_argmax(
     *,
     block_n: int = 16,
     block_k: int = 128,
+    out: torch.Tensor | None = None,
+    advance: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Greedy token id without materialising logits. reference kernels.py:1146."""
+    """Greedy token id without materialising logits. reference kernels.py:1146.
+
+    ``out`` (int64, one element) receives the token instead of a new tensor;
+    ``advance`` (an int64 tensor, e.g. the decode position ids) is incremented
+    by one in the same launch — the token feedback and ``position_ids += 1`` of
+    reference graph.py:78-79 without extra kernels.
+    """
 
     if hidden.shape != (1, weight.shape[1]) or hidden.dtype != torch.bfloat16:
         raise ValueError("lm_head_argmax supports BF16 batch=1 hidden vectors")
@@ -354,9 +376,20 @@ def lm_head_argmax(
     vocab, k = weight.shape
     slots = _lib.load().q35_lm_head_top1_workspace(vocab, k)
     workspace = torch.empty(slots, device=hidden.device, dtype=torch.int64)
-    output = torch.empty((1, 1), device=hidden.device, dtype=torch.int64)
+    if out is None:
+        output = torch.empty((1, 1), device=hidden.device, dtype=torch.int64)
+    else:
+        if out.numel() != 1 or out.dtype != torch.int64 or not out.is_contiguous():
+            raise ValueError("out must be a contiguous one-element int64 tensor")
+        output = out
+    n_adv = 0
+    if advance is not None:
+        if advance.dtype != torch.int64 or not advance.is_contiguous() or advance.numel() > 64:
+            raise ValueError("advance must be a contiguous int64 tensor of at most 64 elements")
+        n_adv = advance.numel()
     _lib.call("q35_lm_head_top1", weight.data_ptr(), hidden.data_ptr(), vocab, k,
-              workspace.data_ptr(), slots, output.data_ptr(), _stream(hidden))
+              workspace.data_ptr(), slots, output.data_ptr(), _lib.ptr(advance), n_adv,
+              _stream(hidden))
     return output
 
 
@@ -595,6 +628,64 @@ def gqa_decode_attention(
     _lib.call("q35_gqa_decode", q.data_ptr(), cache_keys.data_ptr(), cache_values.data_ptr(),
               valid_length.data_ptr(), float(scale), gate_ptr, out.data_ptr(), workspace.data_ptr(),
               floats, heads, kv_heads, head_dim, cache_len, _stream(q))
+    return out
+
+
+def gqa_decode_fused(
+    packed_qgkv: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    inv_freq: torch.Tensor,
+    positions: torch.Tensor,
+    cache_keys: torch.Tensor,
+    cache_values: torch.Tensor,
+    cache_length: torch.Tensor,
+    scale: float,
+    *,
+    q_heads: int,
+    mrope_section: tuple[int, int, int] = (11, 11, 10),
+) -> torch.Tensor:
+    """A full-attention layer's decode token after its packed projection, in
+    two launches: Q/K norm + RoPE (cos/sin from ``positions`` and
+    ``inv_freq``), the K/V cache write at ``cache_length``, split-K attention,
+    combine and sigmoid gate, then ``cache_length += 1`` — the chain
+    qgkv_norm_rope -> cumulative_length.add_ -> gqa_decode_attention ->
+    attention_gate_mul of reference integration.py:298-358.
+
+    ``positions``: int64 device tensor, either one text position or the
+    ``[3, ...]`` multimodal rows (temporal, height, width) of this token.
+    Returns ``[1, 1, QH*D]`` bf16.
+    """
+
+    kv_heads, cache_len, dim = cache_keys.shape[1], cache_keys.shape[2], cache_keys.shape[3]
+    if cache_keys.shape[0] != 1 or cache_values.shape != cache_keys.shape:
+        raise ValueError("static K/V cache must be [1,KVH,L,D]")
+    if packed_qgkv.numel() != 2 * q_heads * dim + 2 * kv_heads * dim or not packed_qgkv.is_contiguous():
+        raise ValueError("packed QGKV does not match the cache heads")
+    if dim != 256:
+        raise ValueError("MI355X decode attention kernels are built for head_dim 256")
+    if inv_freq.dtype != torch.float32 or positions.dtype != torch.int64:
+        raise ValueError("inv_freq must be float32 and positions int64")
+    if cache_length.dtype != torch.int64 or cache_length.numel() != 1:
+        raise ValueError("cache_length must be an int64 scalar")
+    _need_bf16(packed_qgkv, cache_keys, cache_values)
+    qw, wf = _param(q_weight)
+    kw_, kwf = _param(k_weight)
+    if wf != kwf:
+        qw, kw_, wf = qw.float(), kw_.float(), 1
+    # element addresses only (no copy: the rows may be stride-0 expanded views)
+    if positions.dim() >= 2 and positions.shape[0] == 3:
+        p_t, p_h, p_w = (positions[i].data_ptr() for i in range(3))
+    else:
+        p_t = p_h = p_w = positions.data_ptr()
+    floats = _lib.load().q35_gqa_decode_workspace(cache_len, q_heads, kv_heads, dim)
+    workspace = torch.empty(floats, device=packed_qgkv.device, dtype=torch.float32)
+    out = torch.empty((1, 1, q_heads * dim), device=packed_qgkv.device, dtype=_BF16)
+    _lib.call("q35_gqa_decode_fused", packed_qgkv.data_ptr(), qw.data_ptr(), kw_.data_ptr(), wf,
+              inv_freq.data_ptr(), p_t, p_h, p_w, int(mrope_section[1]), int(mrope_section[2]),
+              2 * inv_freq.numel(), cache_keys.data_ptr(), cache_values.data_ptr(),
+              cache_length.data_ptr(), float(scale), out.data_ptr(), workspace.data_ptr(), floats,
+              q_heads, kv_heads, dim, cache_len, _stream(packed_qgkv))
     return out
 
 

@@ -4,7 +4,8 @@ A Transformers Qwen3.5 model (synthetic seeded weights) is patched with
 ``apply_fusions`` and run on the GPU: prefill, then greedy decode through the
 captured graph. The oracle decoder gets the identical weights on the CPU and
 is teacher-forced with the GPU's tokens, so every step compares the two paths
-on the same history: the final hidden states must agree to HIDDEN_RTOL, and a
+on the same history: the final hidden states must agree to HIDDEN_RTOL (set from the measured
+summation-order noise floor of the oracle itself), and a
 token may differ only where the oracle's logit gap between the two tokens is
 within the measured GPU-vs-oracle difference of those two logits (random-init
 logits often tie to the bf16 ulp). Every flip is printed with its numbers.
@@ -21,9 +22,12 @@ from ppu_amd import synth
 pytestmark = pytest.mark.gpu
 
 # Relative L2 error allowed between the GPU's and the oracle's final hidden
-# state at a teacher-forced step: bf16 rounding noise accumulated through the
-# layers (measured ~0.3-0.6 % on the 2B model), with headroom.
-HIDDEN_RTOL = 2e-2
+# state at a teacher-forced step. Two CPU oracle variants that differ only in
+# the fp32 summation order of their linear layers already diverge by 1.1 % (4
+# layers) and 2.4 % (12 layers) on these random-init weights
+# (tests/test_oracle_model.py::test_summation_order_noise_floor); the bounds
+# are about twice that floor at each depth (24 layers extrapolate to ~3.4 %).
+HIDDEN_RTOL = {"tiny": 0.03, "2b": 0.07}
 
 
 def _build(cfg, gpu, fusion):
@@ -55,7 +59,7 @@ def _gpu_hidden_states(model, prompt, tokens, bucket):
     return hidden
 
 
-def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden):
+def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden, rtol):
     """Every step: the GPU's hidden state within HIDDEN_RTOL of the oracle's;
     the tokens equal, or the flip explained: the oracle's logit gap between the
     two tokens is no larger than the measured GPU-vs-oracle difference of
@@ -67,7 +71,7 @@ def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden):
         hg, ho = gpu_hidden[step].double(), ref_hidden[step].double()
         err = float((hg - ho).norm() / ho.norm())
         errs.append(err)
-        if err > HIDDEN_RTOL:
+        if err > rtol:
             bad.append((step, "hidden", err))
         if tok != rt:
             rows = emb[[tok, rt]]
@@ -100,7 +104,8 @@ def test_tiny_model_greedy_vs_oracle(gpu, fused, a8w8):
     assert len(res.tokens) == 24
     hidden = _gpu_hidden_states(model, prompt, res.tokens, res.meta["cache_bucket"])
     oracle = OracleDecoder(state, cfg, a8w8=a8w8)
-    _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden)
+    _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden,
+                          HIDDEN_RTOL["tiny"])
 
 
 def test_graph_replay_matches_eager_decode(gpu):
@@ -167,4 +172,5 @@ def test_2b_prefill_1024_decode_64_vs_oracle(gpu, variant):
     del model
     torch.cuda.empty_cache()
     oracle = OracleDecoder(state, cfg, a8w8=variant == "a8w8")
-    _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden)
+    _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden,
+                          HIDDEN_RTOL["2b"])

@@ -505,3 +505,70 @@ def test_gated_norm_linear(gpu):
     pg = packed.to(gpu)
     got = K.gated_norm_linear(core.to(gpu), pg[..., 6144:8192], nw.to(gpu), 1e-6, W.to(gpu))
     close(got, exp)
+
+
+@pytest.mark.parametrize("positions", [(777, 777, 777), (100, 57, 33)])
+@pytest.mark.parametrize("n_old", [0, 300, 1151])
+def test_gqa_decode_fused_step(gpu, positions, n_old):
+    """Fused attention decode step (Q/K norm + RoPE from device positions, cache
+    write, split-K attention incl. the new token, combine, gate, length += 1)
+    against the oracle chain qgkv_norm_rope -> cache write -> decode attention
+    -> attention gate, with Transformers' rotary table for cos/sin."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding
+
+    from ppu_amd import kernels as K
+    from ppu_amd import synth
+
+    g = gen(KERNEL_SEED + 50)
+    cache_len = 1152
+    packed = randn(g, 1, 1, 5120)
+    qw, kw = randn(g, 256, scale=0.1), randn(g, 256, scale=0.1)
+    kc = randn(g, 1, 2, cache_len, 256)
+    vc = randn(g, 1, 2, cache_len, 256)
+    kc[:, :, n_old:] = 0
+    vc[:, :, n_old:] = 0
+    rot = Qwen3_5TextRotaryEmbedding(synth.config_tiny())
+    pos = torch.tensor(positions, dtype=torch.int64).view(3, 1, 1)
+    cos, sin = rot(torch.zeros(1, 1, 8, dtype=BF), pos)
+    kr, vr = kc.clone(), vc.clone()
+    q, _, _ = ref.qgkv_norm_rope(packed, qw, kw, cos, sin, q_heads=8, kv_heads=2, dim=256,
+                                 rotary_dim=64, cache_key=kr, cache_value=vr, cache_start=n_old)
+    att = ref.gqa_decode_attention(q, kr, vr, n_old + 1, 0.0625)
+    exp = ref.attention_gate_mul(att, packed, 256)
+    kg, vg = kc.to(gpu), vc.to(gpu)
+    length = torch.tensor(n_old, dtype=torch.int64, device=gpu)
+    got = K.gqa_decode_fused(packed.to(gpu), qw.to(gpu), kw.to(gpu), rot.inv_freq.to(gpu),
+                             pos.to(gpu), kg, vg, length, 0.0625, q_heads=8)
+    close(got, exp)
+    assert int(length) == n_old + 1
+    close(kg[:, :, n_old], kr[:, :, n_old])
+    assert torch.equal(vg[:, :, n_old].cpu(), vr[:, :, n_old])
+    assert torch.equal(kg[:, :, :n_old].cpu(), kc[:, :, :n_old])
+
+
+def test_norm_linear_conv_embedding_gather(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 51)
+    table = randn(g, 1000, 2048)
+    nw = randn(g, 2048, scale=0.02)
+    W = randn(g, 8320, 2048, scale=0.02)
+    cw = randn(g, 6144, 4, scale=0.3)
+    cs = torch.zeros(1, 6144, 4, dtype=BF, device=gpu)
+    tok = torch.tensor([737], dtype=torch.int64, device=gpu)
+    r, packed, _ = K.norm_linear_conv(table.to(gpu), None, nw.to(gpu), 1e-6, W.to(gpu), cw.to(gpu), cs,
+                                      token=tok)
+    assert torch.equal(r.cpu().reshape(-1), table[737])
+    close(packed.reshape(1, -1), ref.linear(ref.rms_norm(table[737:738], nw), W))
+
+
+def test_lm_head_feedback(gpu):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 52)
+    h = randn(g, 1, 2048)
+    w = randn(g, 5000, 2048, scale=0.02)
+    tok = torch.zeros(1, 1, dtype=torch.int64, device=gpu)
+    pos = torch.tensor([[41]], dtype=torch.int64, device=gpu)
+    out = K.lm_head_argmax(h.to(gpu), w.to(gpu), out=tok, advance=pos)
+    assert out is tok and int(tok) == int(ref.lm_head_argmax(h, w)) and int(pos) == 42
