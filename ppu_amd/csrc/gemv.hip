@@ -60,23 +60,25 @@ struct GemvArgs {
 // Gated RMSNorm (reference kernels.py:115-155) runs over heads of this width.
 constexpr int kGatedHead = 128;
 
-Q35_DEV void load_nw8(const GemvArgs& a, int k, float* w) {
+// 8 norm weights from the preloaded groups: fp32 (two 16-byte groups) or bf16 (one).
+Q35_DEV void nw8_from(const GemvArgs& a, const uint4 lo, const uint4 hi, float* w) {
   if (a.nw_f32) {
-    const float4 lo = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.nw) + k);
-    const float4 hi = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.nw) + k + 4);
-    w[0] = lo.x; w[1] = lo.y; w[2] = lo.z; w[3] = lo.w;
-    w[4] = hi.x; w[5] = hi.y; w[6] = hi.z; w[7] = hi.w;
+    w[0] = __uint_as_float(lo.x); w[1] = __uint_as_float(lo.y);
+    w[2] = __uint_as_float(lo.z); w[3] = __uint_as_float(lo.w);
+    w[4] = __uint_as_float(hi.x); w[5] = __uint_as_float(hi.y);
+    w[6] = __uint_as_float(hi.z); w[7] = __uint_as_float(hi.w);
   } else {
-    unpack8(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.nw) + k), w);
+    unpack8(lo, w);
   }
 }
 
 template <int WV, int R, int NCH, int PRO, int EPI>
 __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
   constexpr int NT = WV * 64;
-  constexpr int NV = NCH * 64;                  // activation uint4 groups
+  constexpr int NV = NCH * 64;                  // activation uint4 groups (8 bf16 each)
   constexpr int PER = (NV + NT - 1) / NT;       // groups per thread
   constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;  // outputs per wave
+  static_assert(NV % NT == 0 || NT % NV == 0, "activation groups must tile the workgroup");
   __shared__ uint4 xs[NV];
   __shared__ float red[WV];
   __shared__ unsigned long long best_s[WV];
@@ -86,63 +88,70 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
   const int wid = tid >> 6;
   const int n0 = (blockIdx.x * WV + wid) * P;
   const bool writer = blockIdx.x == 0;
+  // Threads past NV (when the workgroup is wider than the vector) own no
+  // activation group; the test is uniform per wave (NV is a multiple of 64).
+  const bool act = NV % NT == 0 || tid < NV;
 
-  // 1. activation loads (cooperative, before the weight stream).
+  // 1. activation, update and norm-weight loads, issued before the weight
+  //    stream so that the in-order vmcnt lets the prologue start while the
+  //    weights are still in flight. No loads below are predicated: predicated
+  //    loads split the code into branches and force a full vmcnt(0) wait.
   const uint16_t* xsrc = a.x;
   if (a.x_row) {
     long long r = a.x_row[0];
     r = r < 0 ? 0 : (r >= a.x_rows ? a.x_rows - 1 : r);
     xsrc += (size_t)r * a.K;
   }
-  uint4 xa[PER], ua[PER];
+  uint4 xa[PER], ua[PER], wa[PER], wb[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int i = tid + j * NT;
-    if (i < NV && i * 8 < a.K) {
-      xa[j] = *reinterpret_cast<const uint4*>(xsrc + i * 8);
-      if (PRO == PRO_RMSNORM && writer && a.r_out)
-        *reinterpret_cast<uint4*>(a.r_out + i * 8) = xa[j];
-      if (PRO == PRO_RESNORM || PRO == PRO_GATEDNORM)
-        ua[j] = *reinterpret_cast<const uint4*>(a.u + i * 8);
-    } else {
-      xa[j] = make_uint4(0, 0, 0, 0);
-      ua[j] = make_uint4(0, 0, 0, 0);
+    const int i = act ? tid + j * NT : 0;
+    xa[j] = *reinterpret_cast<const uint4*>(xsrc + i * 8);
+    if (PRO == PRO_RESNORM || PRO == PRO_GATEDNORM)
+      ua[j] = *reinterpret_cast<const uint4*>(a.u + i * 8);
+    if (PRO != PRO_NONE) {
+      const int kn = PRO == PRO_GATEDNORM ? (i * 8) % kGatedHead : i * 8;
+      if (a.nw_f32) {
+        wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.nw) + kn);
+        wb[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.nw) + kn + 4);
+      } else {
+        wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.nw) + kn);
+      }
     }
   }
 
-  // 2. weight stream.
+  // 2. weight stream: rows past the end read row 0 (valid memory) and are
+  //    never stored.
   int rows[R];
-  int row_end;
   if (EPI == EPI_SWIGLU) {
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      rows[i] = n0 + i < a.N ? n0 + i : 0x7fffffff;
-      rows[P + i] = n0 + i < a.N ? a.N + n0 + i : 0x7fffffff;
+      const bool ok = n0 + i < a.N;
+      rows[i] = ok ? n0 + i : 0;
+      rows[P + i] = ok ? a.N + n0 + i : 0;
     }
-    row_end = 2 * a.N;
   } else {
 #pragma unroll
-    for (int i = 0; i < R; ++i) rows[i] = n0 + i;
-    row_end = a.N;
+    for (int i = 0; i < R; ++i) rows[i] = n0 + i < a.N ? n0 + i : 0;
   }
   uint4 w[R][NCH];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
+    const uint16_t* wrow = a.W + (size_t)rows[r] * a.K + lane * 8;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int k = c * 512 + lane * 8;
-      w[r][c] = (rows[r] < row_end && k < a.K) ? ld_stream16(a.W + (size_t)rows[r] * a.K + k)
-                                                : make_uint4(0, 0, 0, 0);
-    }
+    for (int c = 0; c < NCH; ++c) w[r][c] = ld_stream16(wrow + c * 512);
+  }
+
+  if (PRO == PRO_RMSNORM && writer && a.r_out && act) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) *reinterpret_cast<uint4*>(a.r_out + (tid + j * NT) * 8) = xa[j];
   }
 
   // 3. prologue into LDS.
   if (PRO == PRO_NONE) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = tid + j * NT;
-      if (i < NV) xs[i] = xa[j];
-    }
+    for (int j = 0; j < PER; ++j)
+      if (act) xs[tid + j * NT] = xa[j];
   } else if (PRO == PRO_GATEDNORM) {
     // Group i holds elements 8i..8i+7, so head = i/16: the 16 groups of a head
     // sit on the 16 lanes of one DPP row (NT is a multiple of 16).
@@ -158,8 +167,8 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
       for (int e = 0; e < 8; ++e) ss += s[e] * s[e];
       ss = row16_sum(ss);
       const float inv = rsqrt_cr(ss / (float)kGatedHead + a.eps);
-      if (i < NV && i * 8 < a.K) {
-        load_nw8(a, (i * 8) % kGatedHead, wn);
+      if (act) {
+        nw8_from(a, wa[j], wb[j], wn);
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -170,8 +179,6 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
         const uint4 v = pack8(o);
         xs[i] = v;
         if (writer && a.xn_out) *reinterpret_cast<uint4*>(a.xn_out + i * 8) = v;
-      } else if (i < NV) {
-        xs[i] = make_uint4(0, 0, 0, 0);
       }
     }
   } else {
@@ -186,12 +193,12 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) s[j][e] = round_bf(s[j][e] + b[e]);
         const int i = tid + j * NT;
-        if (writer && a.r_out && i < NV && i * 8 < a.K)
-          *reinterpret_cast<uint4*>(a.r_out + i * 8) = pack8(s[j]);
+        if (writer && a.r_out && act) *reinterpret_cast<uint4*>(a.r_out + i * 8) = pack8(s[j]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += s[j][e] * s[j][e];
     }
+    if (!act) ss = 0.f;  // idle threads loaded group 0; keep it out of the sum
     ss = wave_sum(ss);
     if (lane == 0) red[wid] = ss;
     lds_barrier();
@@ -202,17 +209,14 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = tid + j * NT;
-      if (i < NV) {
-        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (i * 8 < a.K) {
-          float wn[8];
-          load_nw8(a, i * 8, wn);
+      if (act) {
+        float o[8], wn[8];
+        nw8_from(a, wa[j], wb[j], wn);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = s[j][e] * inv * (1.0f + wn[e]);
-        }
+        for (int e = 0; e < 8; ++e) o[e] = s[j][e] * inv * (1.0f + wn[e]);
         const uint4 v = pack8(o);
         xs[i] = v;
-        if (writer && a.xn_out && i * 8 < a.K) *reinterpret_cast<uint4*>(a.xn_out + i * 8) = v;
+        if (writer && a.xn_out) *reinterpret_cast<uint4*>(a.xn_out + i * 8) = v;
       }
     }
   }

@@ -23,14 +23,16 @@ Q35_DEV float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
 Q35_DEV float bf_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
 Q35_DEV float bf_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
 
-Q35_DEV uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
+// fp32 -> bf16 with gfx950's v_cvt_pk_bf16_f32: round to nearest even, NaN
+// stays NaN (the rounding torch's .to(bfloat16) and Triton's casts use).
+typedef float q35_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 q35_bf16x2 __attribute__((ext_vector_type(2)));
+Q35_DEV uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 Q35_DEV float round_bf(float f) { return bf2f(f2bf(f)); }
-Q35_DEV uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+Q35_DEV uint32_t pack_bf2(float lo, float hi) {
+  const q35_f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, q35_bf16x2));
+}
 
 // Unpack 8 bf16 held in a uint4 into fp32.
 Q35_DEV void unpack8(const uint4 v, float* f) {

@@ -22,12 +22,15 @@ from ppu_amd import synth
 pytestmark = pytest.mark.gpu
 
 # Relative L2 error allowed between the GPU's and the oracle's final hidden
-# state at a teacher-forced step. Two CPU oracle variants that differ only in
-# the fp32 summation order of their linear layers already diverge by 1.1 % (4
-# layers) and 2.4 % (12 layers) on these random-init weights
-# (tests/test_oracle_model.py::test_summation_order_noise_floor); the bounds
-# are about twice that floor at each depth (24 layers extrapolate to ~3.4 %).
-HIDDEN_RTOL = {"tiny": 0.03, "2b": 0.07}
+# state at a teacher-forced step, set at about twice the oracle's own noise
+# floor. Two CPU oracle variants that differ only in the fp32 summation order
+# of their linear layers diverge by 1.1 % (4 layers) and 2.4 % (12 layers) on
+# these random-init weights (tests/test_oracle_model.py); on the 24-layer 2B
+# shape a one-ulp change of the RMSNorm variances moves the hidden state by
+# 2.4 % mean / 2.9 % max in bf16 and 8.2 % mean / 10 % max in a8w8, where the
+# per-token int8 quantisation turns ulp changes into whole int8 steps
+# (tests/noise_floor.py).
+HIDDEN_RTOL = {"tiny": 0.03, "2b": 0.07, "2b-a8w8": 0.2}
 
 
 def _build(cfg, gpu, fusion):
@@ -173,4 +176,4 @@ def test_2b_prefill_1024_decode_64_vs_oracle(gpu, variant):
     torch.cuda.empty_cache()
     oracle = OracleDecoder(state, cfg, a8w8=variant == "a8w8")
     _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden,
-                          HIDDEN_RTOL["2b"])
+                          HIDDEN_RTOL["2b" if variant == "bf16" else "2b-a8w8"])
