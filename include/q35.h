@@ -141,7 +141,8 @@ int q35_qgkv_norm_rope(const void* packed, const void* q_w, const void* k_w, int
                        const void* cache_start, int B, int L, int QH, int KVH, int D,
                        int rotary_dim, int cache_len, void* stream);
 
-/* Split count for a cache capacity (chunk length in *chunk_out). */
+/* Split count for a cache capacity (chunk length in *chunk_out): at most 128
+ * splits per KV head, chunks of whole 32-token workgroup iterations. */
 int q35_gqa_decode_splits(int cache_len, int kv_heads, int* chunk_out);
 /* Workspace floats for q35_gqa_decode. */
 long long q35_gqa_decode_workspace(int cache_len, int q_heads, int kv_heads, int D);
@@ -159,7 +160,8 @@ int q35_gqa_decode(const void* q, const void* K, const void* V, const void* vali
  * positions pos_t/pos_h/pos_w and fp32 inv_freq, interleaved multimodal sections sec_h,
  * sec_w as Transformers' rotary table), K/V stored into the static cache at index
  * *cache_len_dev, split-K attention over the cache and the new token, combine, sigmoid
- * gate, and *cache_len_dev += 1. out [QH*D] bf16. Replaces the chain
+ * gate, and *cache_len_dev += 1. out [QH*D] bf16. rotary_dim <= 128 (one
+ * frequency per lane). Replaces the chain
  * integration.py:298-358 (qgkv_norm_rope :507, cumulative_length.add_, gqa_decode_attention
  * :1031, attention_gate_mul :312) after the packed projection. */
 int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, int w_f32,

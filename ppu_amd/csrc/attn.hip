@@ -107,14 +107,25 @@ __global__ __launch_bounds__(256) void qgkv_norm_rope_k(
 // ------------------------------------------------------- GQA split-K decode
 // Grid (KVH, splits): a workgroup reads one contiguous chunk of one KV head
 // once and serves all G = QH/KVH query heads of that head, so K/V bytes are
-// read from HBM exactly once per step. D = 256.
-//   QK: lane = (token tg = lane/16 of a 4-token group, 16-dim slice lane%16);
-//       per-token scores are reduced over the 16-lane DPP row.
+// read from HBM exactly once per step. D = 256. A workgroup of 4 waves covers
+// 32 tokens per iteration, 8 per wave in two groups of 4 (8 waves, two per
+// SIMD, measured no faster: the per-workgroup latency chain dominates):
+//   QK: lane = (token row lane/16 of a group, dims 8*(lane%16) and
+//       128 + 8*(lane%16)); bf16 pair dot products (v_dot2) reduced over the
+//       16-lane DPP row, then times the softmax scale.
 //   PV: lane owns dims 4*lane..4*lane+3; p values are broadcast by readlane.
-// Each wave runs an online softmax over its tokens; the 4 waves are merged in
-// LDS and the workgroup writes (acc[D], m, l) per query head and split.
+// The loads that the Q/K norm + RoPE prologue needs are issued first and the
+// K/V rows of the first iteration right after, so the prologue runs while
+// K/V are in flight (loads retire in order); later iterations are prefetched
+// one ahead. Each wave runs an online softmax over its tokens, the waves are
+// merged in LDS and the workgroup writes (acc[D], m, l) per query head and
+// split; gqa_decode_combine merges the splits.
 constexpr int kAD = 256;
 constexpr int kMaxG = 8;
+constexpr int kSplitWaves = 4;             // waves per split workgroup
+constexpr int kWaveTok = 8;                // tokens per wave per iteration
+constexpr int kIterTok = kSplitWaves * kWaveTok;  // tokens per workgroup iteration
+constexpr int kMaxSplits = 128;            // splits per KV head
 
 // Extra inputs of the fused decode step: the packed QGKV row of the current
 // token, the Q/K norm weights, the rotary frequencies and positions. The
@@ -136,59 +147,126 @@ struct FusedQ {
   uint16_t* v_cache;
 };
 
-// Q/K RMSNorm (1 + w) + partial RoPE of one 256-wide head held by a wave
-// (lane: dims 4*lane..+3), with cos/sin computed from the positions exactly as
-// Transformers' rotary table does: freq_i = pos * inv_freq[i] (fp32),
-// cos/sin in fp32 rounded to bf16; dims c and c + rot/2 share freq c mod rot/2.
-Q35_DEV void norm_rope_row(const uint16_t* __restrict__ src, const void* w, int w_f32,
-                           const FusedQ& f, int lane, float (&o)[4]) {
-  float x[4], n[4];
+// Global loads of one 256-wide head (lane: dims 4*lane..+3) and its norm
+// weights (bf16 in w0, or fp32 in w0:w1).
+struct HeadLoads {
+  uint2 x, w0, w1;
+};
+Q35_DEV HeadLoads load_head(const uint16_t* __restrict__ src, const void* w, int w_f32, int lane) {
+  HeadLoads h;
+  h.x = *reinterpret_cast<const uint2*>(src + 4 * lane);
+  const char* wb = reinterpret_cast<const char*>(w) + (w_f32 ? 16 * lane : 8 * lane);
+  h.w0 = *reinterpret_cast<const uint2*>(wb);
+  h.w1 = *reinterpret_cast<const uint2*>(wb + (w_f32 ? 8 : 0));
+  return h;
+}
+
+// Rotary inputs: lane j owns frequency i = j mod rot/2 (rot/2 <= 64).
+struct RopeLoads {
+  float invf;
+  long long pt, ph, pw;
+};
+Q35_DEV RopeLoads load_rope(const FusedQ& f, int lane) {
+  RopeLoads r;
+  r.invf = f.inv_freq[lane % (f.rot / 2)];
+  r.pt = f.pos_t[0];
+  r.ph = f.pos_h[0];
+  r.pw = f.pos_w[0];
+  return r;
+}
+
+// cos/sin of the lane's 4 dims (bf16-rounded), shared by every head of the
+// token: freq_i = pos * inv_freq[i] in fp32, the position row of frequency i
+// chosen by the interleaved multimodal sections, cos/sin in fp32 rounded to
+// bf16, exactly as Transformers' rotary table; dims c and c + rot/2 share
+// frequency c mod rot/2. Lane j computes frequency j mod rot/2 once and the
+// lanes gather theirs by shuffle.
+struct RopeTable {
+  float cs[4], sn[4];
+};
+Q35_DEV RopeTable rope_table(const RopeLoads& r, const FusedQ& f, int lane) {
+  const int half = f.rot / 2;
+  const int i = lane % half;
+  long long p = r.pt;
+  if (i % 3 == 1 && i < 3 * f.sec_h) p = r.ph;
+  if (i % 3 == 2 && i < 3 * f.sec_w) p = r.pw;
+  float sn, cs;
+  sincosf((float)p * r.invf, &sn, &cs);
+  cs = round_bf(cs);
+  sn = round_bf(sn);
+  RopeTable t;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int src = (lane * 4 + e) % half;
+    t.cs[e] = __shfl(cs, src, 64);
+    t.sn[e] = __shfl(sn, src, 64);
+  }
+  return t;
+}
+
+// Q/K RMSNorm (1 + w) + partial RoPE of one head from its loads. Rounding
+// points follow the reference kernel (kernels.py:419-573):
+//   n = bf16(x * rsqrt(mean(x^2) + 1e-6) * (1 + w))
+//   rot = bf16(bf16(n*cos) + bf16(bf16(+-n_partner) * sin)) for dims < rot
+Q35_DEV void norm_rope(const HeadLoads& h, int w_f32, const RopeTable& t, int rot, int lane,
+                       float (&o)[4]) {
+  const float x[4] = {bf_lo(h.x.x), bf_hi(h.x.x), bf_lo(h.x.y), bf_hi(h.x.y)};
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    x[e] = bf2f(src[lane * 4 + e]);
-    ss += x[e] * x[e];
-  }
+  for (int e = 0; e < 4; ++e) ss += x[e] * x[e];
   const float inv = rsqrt_cr(wave_sum(ss) / (float)kAD + 1.0e-6f);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int c = lane * 4 + e;
-    const float wc = w_f32 ? reinterpret_cast<const float*>(w)[c] : bf2f(reinterpret_cast<const uint16_t*>(w)[c]);
-    n[e] = round_bf(x[e] * inv * (1.0f + wc));
+  float wc[4];
+  if (w_f32) {
+    wc[0] = __uint_as_float(h.w0.x); wc[1] = __uint_as_float(h.w0.y);
+    wc[2] = __uint_as_float(h.w1.x); wc[3] = __uint_as_float(h.w1.y);
+  } else {
+    wc[0] = bf_lo(h.w0.x); wc[1] = bf_hi(h.w0.x); wc[2] = bf_lo(h.w0.y); wc[3] = bf_hi(h.w0.y);
   }
-  const int half = f.rot / 2;
+  float n[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) n[e] = round_bf(x[e] * inv * (1.0f + wc[e]));
+  const int half = rot / 2;
   const int shift = half / 4;
+  // Partner of dim c is c + half (first half) or c - half: lane +- half/4.
+  const bool first = lane * 4 < half;
+  const int partner_lane = (first ? lane + shift : lane - shift) & 63;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int c = lane * 4 + e;
-    const int partner_lane = c < half ? lane + shift : lane - shift;
-    const float pn = __shfl(n[e], partner_lane & 63, 64);
-    if (c < f.rot) {
-      const int i = c < half ? c : c - half;
-      const long long* pp = f.pos_t;
-      if (i % 3 == 1 && i < 3 * f.sec_h) pp = f.pos_h;
-      if (i % 3 == 2 && i < 3 * f.sec_w) pp = f.pos_w;
-      const float ang = (float)pp[0] * f.inv_freq[i];
-      const float cs = round_bf(cosf(ang)), sn = round_bf(sinf(ang));
-      const float qc = round_bf(n[e] * cs);
-      const float rh = c < half ? -pn : pn;
-      o[e] = round_bf(qc + round_bf(rh * sn));
-    } else {
-      o[e] = n[e];
-    }
+    const float pn = __shfl(n[e], partner_lane, 64);
+    const float qc = round_bf(n[e] * t.cs[e]);
+    const float rh = first ? -pn : pn;
+    const float r = round_bf(qc + round_bf(rh * t.sn[e]));
+    o[e] = lane * 4 < rot ? r : n[e];
   }
 }
 
+// Max of a value that is uniform within each 16-lane row, over the 4 rows.
+Q35_DEV float rows4_max(float v) {
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+Q35_DEV float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(q35_bf16x2, a),
+                                         __builtin_bit_cast(q35_bf16x2, b), c, false);
+}
+
 template <int G, bool FUSED>
-__global__ __launch_bounds__(256) void gqa_decode_split(
+__global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
     const long long* __restrict__ valid_len, float* __restrict__ acc_out, float* __restrict__ ml_out,
     int cache_len, int chunk, int splits, float scale, const FusedQ fq) {
+  constexpr int NW = kSplitWaves;
+  constexpr int HPW = (G + NW - 1) / NW;  // query heads per wave in the prologue
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int kvh = blockIdx.x;
   const int split = blockIdx.y;
-  const int QH = G * gridDim.x;
+  const int KVH = gridDim.x;
+  const int QH = G * KVH;
   // FUSED: valid_len counts the tokens before this one; the new token sits at
   // index n_old and is attended from LDS by the workgroup that owns it.
   const long long n_old = FUSED ? valid_len[0] : 0;
@@ -197,54 +275,102 @@ __global__ __launch_bounds__(256) void gqa_decode_split(
   const int start = split * chunk;
   const int end = min(start + chunk, n_cached);
   const bool owns_new = FUSED && n_old >= start && n_old < start + chunk;
+  const int n_iter = end > start ? (end - start + kIterTok - 1) / kIterTok : 0;
 
-  __shared__ float q_s[FUSED ? G : 1][kAD];
-  __shared__ float kn_s[FUSED ? kAD : 1], vn_s[FUSED ? kAD : 1];
-  if (FUSED) {
-    for (int g = wid; g < G; g += 4) {
-      float o[4];
-      norm_rope_row(fq.packed + (size_t)(kvh * G + g) * 2 * kAD, fq.q_w, fq.w_f32, fq, lane, o);
-      *reinterpret_cast<float4*>(&q_s[g][4 * lane]) =
-          make_float4(o[0] * scale, o[1] * scale, o[2] * scale, o[3] * scale);
+  // 1. prologue loads: the wave's query heads, and (FUSED) the new token's k
+  //    and v rows, the norm weights and the rotary inputs.
+  HeadLoads hq[HPW], hk;
+  uint2 vnew = make_uint2(0, 0);
+  RopeLoads rl;
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    const int g = (wid + NW * j) % G;
+    if (FUSED) {
+      hq[j] = load_head(fq.packed + (size_t)(kvh * G + g) * 2 * kAD, fq.q_w, fq.w_f32, lane);
+    } else {
+      hq[j].x = *reinterpret_cast<const uint2*>(q + (size_t)(kvh * G + g) * kAD + 4 * lane);
     }
-    if (owns_new && wid == 0) {
-      float o[4];
-      const uint16_t* krow = fq.packed + (size_t)2 * QH * kAD + (size_t)kvh * kAD;
-      const uint16_t* vrow = krow + (size_t)gridDim.x * kAD;
-      norm_rope_row(krow, fq.k_w, fq.w_f32, fq, lane, o);
-      const uint2 vraw = *reinterpret_cast<const uint2*>(vrow + 4 * lane);
-      *reinterpret_cast<float4*>(&kn_s[4 * lane]) = make_float4(o[0], o[1], o[2], o[3]);
-      *reinterpret_cast<float4*>(&vn_s[4 * lane]) =
-          make_float4(bf_lo(vraw.x), bf_hi(vraw.x), bf_lo(vraw.y), bf_hi(vraw.y));
-      if (n_old < cache_len) {
-        const size_t off = ((size_t)kvh * cache_len + (size_t)n_old) * kAD + 4 * lane;
-        *reinterpret_cast<uint2*>(fq.k_cache + off) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
-        *reinterpret_cast<uint2*>(fq.v_cache + off) = vraw;
+  }
+  if (FUSED) {
+    const uint16_t* krow = fq.packed + (size_t)2 * QH * kAD + (size_t)kvh * kAD;
+    hk = load_head(krow, fq.k_w, fq.w_f32, lane);
+    vnew = *reinterpret_cast<const uint2*>(krow + (size_t)KVH * kAD + 4 * lane);
+    rl = load_rope(fq, lane);
+  }
+
+  // 2. K/V rows of the first iteration. Group gi of a wave holds tokens
+  //    tb + 4*gi + row (K, the lane's 16 dims), V rows tb + i (dims 4*lane..).
+  //    Rows past the valid end are read at the last valid row (in bounds,
+  //    already cached) and masked out of the softmax.
+  const uint16_t* Kh = Kc + (size_t)kvh * cache_len * kAD;
+  const uint16_t* Vh = Vc + (size_t)kvh * cache_len * kAD;
+  const int rw = lane >> 4;
+  const int ds = lane & 15;
+  const int tmax = max(end - 1, 0);
+  uint4 kr[2][2];
+  uint2 vr[kWaveTok];
+  auto load_kv = [&](int it, uint4 (&kd)[2][2], uint2 (&vd)[kWaveTok]) {
+    const int tb = start + it * kIterTok + wid * kWaveTok;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int t = min(tb + 4 * gi + rw, tmax);
+      kd[gi][0] = *reinterpret_cast<const uint4*>(Kh + (size_t)t * kAD + ds * 8);
+      kd[gi][1] = *reinterpret_cast<const uint4*>(Kh + (size_t)t * kAD + 128 + ds * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < kWaveTok; ++i) {
+      const int t = min(tb + i, tmax);
+      vd[i] = *reinterpret_cast<const uint2*>(Vh + (size_t)t * kAD + 4 * lane);
+    }
+  };
+  load_kv(0, kr, vr);
+
+  // 3. prologue: q heads (bf16 pairs, unscaled) into LDS; FUSED also the new
+  //    token's k and v, written into the cache by the owning workgroup.
+  __shared__ uint2 q_s[G][kAD / 4];
+  __shared__ float kn_s[FUSED ? kAD : 1], vn_s[FUSED ? kAD : 1];
+  RopeTable rt;
+  if (FUSED) rt = rope_table(rl, fq, lane);
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    const int g = wid + NW * j;
+    if (g < G) {
+      if (FUSED) {
+        float o[4];
+        norm_rope(hq[j], fq.w_f32, rt, fq.rot, lane, o);
+        q_s[g][lane] = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+      } else {
+        q_s[g][lane] = hq[j].x;
       }
     }
-    __syncthreads();
   }
-
-  // q slices for QK (16 dims of the lane's slice, per head), pre-scaled in fp32.
-  const int ds = lane & 15;
-  float qf[G][16];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (FUSED) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) qf[g][j] = q_s[g][ds * 16 + j];
-    } else {
-      const uint16_t* qh = q + (size_t)(kvh * G + g) * kAD + ds * 16;
-      float t8[8];
-      unpack8(*reinterpret_cast<const uint4*>(qh), t8);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qf[g][j] = t8[j] * scale;
-      unpack8(*reinterpret_cast<const uint4*>(qh + 8), t8);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qf[g][8 + j] = t8[j] * scale;
+  // The new token's k is normalised by the first wave without a q head.
+  constexpr int KW = G % NW;
+  if (owns_new && wid == KW) {
+    float o[4];
+    norm_rope(hk, fq.w_f32, rt, fq.rot, lane, o);
+    *reinterpret_cast<float4*>(&kn_s[4 * lane]) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(&vn_s[4 * lane]) =
+        make_float4(bf_lo(vnew.x), bf_hi(vnew.x), bf_lo(vnew.y), bf_hi(vnew.y));
+    if (n_old < cache_len) {
+      const size_t off = ((size_t)kvh * cache_len + (size_t)n_old) * kAD + 4 * lane;
+      *reinterpret_cast<uint2*>(fq.k_cache + off) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+      *reinterpret_cast<uint2*>(fq.v_cache + off) = vnew;
     }
   }
+  __syncthreads();
 
+  // The lane's q slices as bf16 pairs: dims 8*ds.. and 128 + 8*ds...
+  uint32_t qp[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint2 a = q_s[g][2 * ds], b = q_s[g][2 * ds + 1];
+    const uint2 c = q_s[g][32 + 2 * ds], d = q_s[g][32 + 2 * ds + 1];
+    qp[g][0] = a.x; qp[g][1] = a.y; qp[g][2] = b.x; qp[g][3] = b.y;
+    qp[g][4] = c.x; qp[g][5] = c.y; qp[g][6] = d.x; qp[g][7] = d.y;
+  }
+
+  // 4. online softmax over the wave's tokens (m and l wave-uniform).
   float m[G], l[G], acc[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -252,86 +378,91 @@ __global__ __launch_bounds__(256) void gqa_decode_split(
     l[g] = 0.f;
     acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.f;
   }
-  const uint16_t* Kh = Kc + (size_t)kvh * cache_len * kAD;
-  const uint16_t* Vh = Vc + (size_t)kvh * cache_len * kAD;
-  // Tokens of this wave: groups of 4, interleaved across the 4 waves.
-  for (int t0 = start + wid * 4; t0 < end; t0 += 16) {
-    const int tok = t0 + (lane >> 4);
-    const bool live = tok < end;
-    float kf[16];
-    if (live) {
-      float t8[8];
-      unpack8(*reinterpret_cast<const uint4*>(Kh + (size_t)tok * kAD + ds * 16), t8);
+  for (int it = 0; it < n_iter; ++it) {
+    uint4 kn[2][2];
+    uint2 vn[kWaveTok];
+    load_kv(it + 1, kn, vn);  // past the end this re-reads the last valid row
+    const int tb = start + it * kIterTok + wid * kWaveTok;
+    float vf[kWaveTok][4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) kf[j] = t8[j];
-      unpack8(*reinterpret_cast<const uint4*>(Kh + (size_t)tok * kAD + ds * 16 + 8), t8);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kf[8 + j] = t8[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) kf[j] = 0.f;
+    for (int i = 0; i < kWaveTok; ++i) {
+      vf[i][0] = bf_lo(vr[i].x);
+      vf[i][1] = bf_hi(vr[i].x);
+      vf[i][2] = bf_lo(vr[i].y);
+      vf[i][3] = bf_hi(vr[i].y);
     }
-    // V rows of the 4 tokens, dims 4*lane..+3.
-    uint2 vv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vv[i] = t0 + i < end ? *reinterpret_cast<const uint2*>(Vh + (size_t)(t0 + i) * kAD + 4 * lane)
-                           : make_uint2(0, 0);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float s = 0.f;
+      float s[2];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) s = fmaf(qf[g][j], kf[j], s);
-      s = row16_sum(s);
-      s = live ? s : -INFINITY;
-      float sc[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 16 * i));
-      const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      const float m_new = fmaxf(m[g], mx);
-      const float corr = expf(m[g] - m_new);
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = expf(sc[i] - m_new);
-      l[g] = l[g] * corr + ((p[0] + p[1]) + (p[2] + p[3]));
-#pragma unroll
-      for (int d = 0; d < 4; ++d) acc[g][d] *= corr;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[g][0] = fmaf(p[i], bf_lo(vv[i].x), acc[g][0]);
-        acc[g][1] = fmaf(p[i], bf_hi(vv[i].x), acc[g][1]);
-        acc[g][2] = fmaf(p[i], bf_lo(vv[i].y), acc[g][2]);
-        acc[g][3] = fmaf(p[i], bf_hi(vv[i].y), acc[g][3]);
+      for (int gi = 0; gi < 2; ++gi) {
+        const uint4 k0 = kr[gi][0], k1 = kr[gi][1];
+        float d = dot2_bf16(qp[g][0], k0.x, 0.f);
+        d = dot2_bf16(qp[g][1], k0.y, d);
+        d = dot2_bf16(qp[g][2], k0.z, d);
+        d = dot2_bf16(qp[g][3], k0.w, d);
+        d = dot2_bf16(qp[g][4], k1.x, d);
+        d = dot2_bf16(qp[g][5], k1.y, d);
+        d = dot2_bf16(qp[g][6], k1.z, d);
+        d = dot2_bf16(qp[g][7], k1.w, d);
+        d = row16_sum(d) * scale;
+        s[gi] = tb + 4 * gi + rw < end ? d : -INFINITY;
       }
+      const float m_new = fmaxf(m[g], rows4_max(fmaxf(s[0], s[1])));
+      // A wave whose tokens so far all lie past the valid end keeps m = -inf:
+      // subtract 0 then, so that corr and p are 0 instead of NaN.
+      const float m_sub = m_new == -INFINITY ? 0.f : m_new;
+      const float corr = expf(m[g] - m_sub);
+      const float p0 = expf(s[0] - m_sub), p1 = expf(s[1] - m_sub);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[g][e] *= corr;
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < kWaveTok; ++i) {
+        const float pi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(i < 4 ? p0 : p1), 16 * (i & 3)));
+        psum += pi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
+      }
+      l[g] = l[g] * corr + psum;
       m[g] = m_new;
     }
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      kr[gi][0] = kn[gi][0];
+      kr[gi][1] = kn[gi][1];
+    }
+#pragma unroll
+    for (int i = 0; i < kWaveTok; ++i) vr[i] = vn[i];
   }
-  // The new token (FUSED): wave 0 of the owning workgroup folds it in.
-  if (owns_new && wid == 0) {
-    const float4 kn = *reinterpret_cast<const float4*>(&kn_s[4 * lane]);
-    const float4 vn = *reinterpret_cast<const float4*>(&vn_s[4 * lane]);
+
+  // The new token (FUSED): wave KW of the owning workgroup folds it in.
+  if (owns_new && wid == KW) {
+    const float4 kv = *reinterpret_cast<const float4*>(&kn_s[4 * lane]);
+    const float4 vv = *reinterpret_cast<const float4*>(&vn_s[4 * lane]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float4 qv = *reinterpret_cast<const float4*>(&q_s[g][4 * lane]);
-      float sdot = qv.x * kn.x;
-      sdot = fmaf(qv.y, kn.y, sdot);
-      sdot = fmaf(qv.z, kn.z, sdot);
-      sdot = fmaf(qv.w, kn.w, sdot);
-      const float sc = wave_sum(sdot);
+      const uint2 qv = q_s[g][lane];
+      float sdot = bf_lo(qv.x) * kv.x;
+      sdot = fmaf(bf_hi(qv.x), kv.y, sdot);
+      sdot = fmaf(bf_lo(qv.y), kv.z, sdot);
+      sdot = fmaf(bf_hi(qv.y), kv.w, sdot);
+      const float sc = wave_sum(sdot) * scale;
       const float m_new = fmaxf(m[g], sc);
       const float corr = expf(m[g] - m_new);
       const float p = expf(sc - m_new);
       l[g] = l[g] * corr + p;
-      acc[g][0] = fmaf(p, vn.x, acc[g][0] * corr);
-      acc[g][1] = fmaf(p, vn.y, acc[g][1] * corr);
-      acc[g][2] = fmaf(p, vn.z, acc[g][2] * corr);
-      acc[g][3] = fmaf(p, vn.w, acc[g][3] * corr);
+      acc[g][0] = fmaf(p, vv.x, acc[g][0] * corr);
+      acc[g][1] = fmaf(p, vv.y, acc[g][1] * corr);
+      acc[g][2] = fmaf(p, vv.z, acc[g][2] * corr);
+      acc[g][3] = fmaf(p, vv.w, acc[g][3] * corr);
       m[g] = m_new;
     }
   }
-  // Merge the 4 waves.
-  __shared__ float m_s[4][kMaxG], l_s[4][kMaxG];
-  __shared__ float a_s[4][kMaxG][kAD];
+
+  // 5. merge the waves in LDS; write this split's (acc, m, l) per head.
+  __shared__ float m_s[NW][G], l_s[NW][G], f_s[NW][G];
+  __shared__ float a_s[NW][G][kAD];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if (lane == 0) {
@@ -341,64 +472,123 @@ __global__ __launch_bounds__(256) void gqa_decode_split(
     *reinterpret_cast<float4*>(&a_s[wid][g][4 * lane]) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < G * kAD; idx += 256) {
-    const int g = idx / kAD, d = idx - g * kAD;
+  // Per (wave, head) factor e^(m_w - max_w m_w), 0 for a wave without tokens.
+  if (threadIdx.x < NW * G) {
+    const int w = threadIdx.x / G, g = threadIdx.x % G;
     float mm = -INFINITY;
-    for (int w = 0; w < 4; ++w) mm = fmaxf(mm, m_s[w][g]);
-    float a = 0.f, ll = 0.f;
-    for (int w = 0; w < 4; ++w) {
-      const float f = m_s[w][g] == -INFINITY ? 0.f : expf(m_s[w][g] - mm);
-      a += a_s[w][g][d] * f;
-      ll += l_s[w][g] * f;
-    }
-    const int slot = (kvh * G + g) * splits + split;
-    acc_out[(size_t)slot * kAD + d] = a;
-    if (d == 0) {
+#pragma unroll
+    for (int v = 0; v < NW; ++v) mm = fmaxf(mm, m_s[v][g]);
+    f_s[w][g] = m_s[w][g] == -INFINITY ? 0.f : expf(m_s[w][g] - mm);
+    if (w == 0) {
+      float ll = 0.f;
+#pragma unroll
+      for (int v = 0; v < NW; ++v)
+        ll += l_s[v][g] * (m_s[v][g] == -INFINITY ? 0.f : expf(m_s[v][g] - mm));
+      const int slot = (kvh * G + g) * splits + split;
       ml_out[slot * 2] = mm;
       ml_out[slot * 2 + 1] = ll;
     }
   }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * kAD / 4; idx += NW * 64) {
+    const int g = idx / (kAD / 4), d = (idx % (kAD / 4)) * 4;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = f_s[w][g];
+      const float4 v = *reinterpret_cast<const float4*>(&a_s[w][g][d]);
+      a.x += v.x * f;
+      a.y += v.y * f;
+      a.z += v.z * f;
+      a.w += v.w * f;
+    }
+    const int slot = (kvh * G + g) * splits + split;
+    *reinterpret_cast<float4*>(acc_out + (size_t)slot * kAD + d) = a;
+  }
 }
 
 // Log-sum-exp merge of the splits -> bf16, optionally times bf16(sigmoid(gate))
-// [reference kernels.py:1007-1028 and 285-333]. One workgroup per query head.
+// [reference kernels.py:1007-1028 and 285-333]. One workgroup per query head:
+// thread (part = wave, col = lane) owns dims 4*col..4*col+3 of splits
+// part, part + 4, ... (up to 4*B splits). Every thread requests its partials
+// (clamped indices) before wave 0 reads the (m, l) pairs and turns them into
+// weights in LDS, so the merge is one memory round trip; the four parts are
+// summed in LDS.
+template <int B>
 __global__ __launch_bounds__(256) void gqa_decode_combine(const float* __restrict__ acc,
                                                           const float* __restrict__ ml,
                                                           const uint16_t* __restrict__ packed_gate,
                                                           uint16_t* __restrict__ out, int splits,
                                                           long long* advance_len) {
   const int h = blockIdx.x;
+  const int t = threadIdx.x;
+  const int col = t & 63;
+  const int part = t >> 6;
   // The split kernel that read the length has completed (stream order).
-  if (advance_len && h == 0 && threadIdx.x == 0) advance_len[0] += 1;
-  __shared__ float w_s[1024];
-  __shared__ float mx_s, l_s;
-  if (threadIdx.x < 64) {
+  if (advance_len && h == 0 && t == 0) advance_len[0] += 1;
+  const float* mlh = ml + (size_t)h * splits * 2;
+  const float* acch = acc + (size_t)h * splits * kAD + 4 * col;
+  __shared__ float w_s[kMaxSplits];
+  __shared__ float lt_s;
+  __shared__ float4 red_s[4][kAD / 4];
+  const uint2 graw = packed_gate && part == 0
+                         ? *reinterpret_cast<const uint2*>(packed_gate + h * 2 * kAD + kAD + 4 * col)
+                         : make_uint2(0, 0);
+  float4 a[B];
+#pragma unroll
+  for (int j = 0; j < B; ++j)
+    a[j] = *reinterpret_cast<const float4*>(acch + (size_t)min(part + 4 * j, splits - 1) * kAD);
+  if (t < 64) {
     float mx = -INFINITY;
-    for (int s = threadIdx.x; s < splits; s += 64) mx = fmaxf(mx, ml[(h * splits + s) * 2]);
+    for (int s = t; s < splits; s += 64) mx = fmaxf(mx, mlh[2 * s]);
     mx = wave_max(mx);
     float lt = 0.f;
-    for (int s = threadIdx.x; s < splits; s += 64) {
-      const float ms = ml[(h * splits + s) * 2];
-      const float f = ms == -INFINITY ? 0.f : expf(ms - mx);
-      w_s[s] = f;
-      lt += ml[(h * splits + s) * 2 + 1] * f;
+    for (int s = t; s < splits; s += 64) {
+      const float ms = mlh[2 * s];
+      const float w = ms == -INFINITY ? 0.f : expf(ms - mx);
+      w_s[s] = w;
+      lt += mlh[2 * s + 1] * w;
     }
     lt = wave_sum(lt);
-    if (threadIdx.x == 0) {
-      mx_s = mx;
-      l_s = lt;
-    }
+    if (t == 0) lt_s = lt;
   }
   __syncthreads();
-  const int d = threadIdx.x;
-  float tot = 0.f;
-  for (int s = 0; s < splits; ++s) tot = fmaf(acc[(size_t)(h * splits + s) * kAD + d], w_s[s], tot);
-  float o = round_bf(tot / l_s);
-  if (packed_gate) {
-    const float g = bf2f(packed_gate[h * 2 * kAD + kAD + d]);
-    o = o * round_bf(sigmoid_f(g));
+  float4 tot = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < B; ++j) {
+    const int s = part + 4 * j;
+    const float w = s < splits ? w_s[s] : 0.f;
+    tot.x = fmaf(a[j].x, w, tot.x);
+    tot.y = fmaf(a[j].y, w, tot.y);
+    tot.z = fmaf(a[j].z, w, tot.z);
+    tot.w = fmaf(a[j].w, w, tot.w);
   }
-  out[(size_t)h * kAD + d] = (uint16_t)f2bf(o);
+  red_s[part][col] = tot;
+  __syncthreads();
+  if (part == 0) {
+    const float4 r0 = red_s[0][col], r1 = red_s[1][col], r2 = red_s[2][col], r3 = red_s[3][col];
+    const float lt = lt_s;
+    float o[4] = {round_bf(((r0.x + r1.x) + (r2.x + r3.x)) / lt), round_bf(((r0.y + r1.y) + (r2.y + r3.y)) / lt),
+                  round_bf(((r0.z + r1.z) + (r2.z + r3.z)) / lt), round_bf(((r0.w + r1.w) + (r2.w + r3.w)) / lt)};
+    if (packed_gate) {
+      o[0] *= round_bf(sigmoid_f(bf_lo(graw.x)));
+      o[1] *= round_bf(sigmoid_f(bf_hi(graw.x)));
+      o[2] *= round_bf(sigmoid_f(bf_lo(graw.y)));
+      o[3] *= round_bf(sigmoid_f(bf_hi(graw.y)));
+    }
+    *reinterpret_cast<uint2*>(out + (size_t)h * kAD + 4 * col) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+  }
+}
+
+// Combine launch for a split count (partials per thread = ceil(splits / 4)).
+void launch_combine(const float* acc, const float* ml, const uint16_t* gate, uint16_t* out, int QH,
+                    int splits, long long* advance, hipStream_t stream) {
+  if (splits <= 32)
+    gqa_decode_combine<8><<<QH, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
+  else if (splits <= 64)
+    gqa_decode_combine<16><<<QH, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
+  else
+    gqa_decode_combine<32><<<QH, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
 }
 
 // ---------------------------------------------------------- causal prefill
@@ -506,12 +696,12 @@ int q35_qgkv_norm_rope(const void* packed, const void* q_w, const void* k_w, int
 
 // Split count and chunk length for a cache of cache_len tokens: chosen from
 // the capacity only (never the valid length), so a captured graph stays valid.
+// A chunk is a whole number of 32-token workgroup iterations and there are at
+// most 128 splits per KV head (the combine requests them all at once).
 int q35_gqa_decode_splits(int cache_len, int kv_heads, int* chunk_out) {
   if (cache_len <= 0 || kv_heads <= 0) return 0;
-  long long chunk = ((long long)cache_len * kv_heads + 255) / 256;
-  chunk = (chunk + 15) / 16 * 16;
-  if (chunk < 16) chunk = 16;
-  if (chunk > 1024) chunk = 1024;
+  long long chunk = ((long long)cache_len + kMaxSplits - 1) / kMaxSplits;
+  chunk = (chunk + kIterTok - 1) / kIterTok * kIterTok;
   const int splits = (int)((cache_len + chunk - 1) / chunk);
   if (chunk_out) *chunk_out = (int)chunk;
   return splits;
@@ -531,15 +721,16 @@ int q35_gqa_decode(const void* q, const void* K, const void* V, const void* vali
   Q35_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 8);
   int chunk = 0;
   const int splits = q35_gqa_decode_splits(cache_len, KVH, &chunk);
-  Q35_CHECK_ARG(splits <= 1024);
+  Q35_CHECK_ARG(splits <= kMaxSplits);
   Q35_CHECK_ARG(workspace_floats >= q35_gqa_decode_workspace(cache_len, QH, KVH, D));
   Q35_CHECK_ARG(q35_aligned16(q) && q35_aligned16(K) && q35_aligned16(V) && q35_aligned16(workspace));
+  Q35_CHECK_ARG(q35_aligned8(out) && q35_aligned8(packed_gate));
   float* acc = (float*)workspace;
   float* ml = acc + (size_t)QH * splits * D;
   dim3 grid(KVH, splits);
   const FusedQ none{};
 #define Q35_GQA(GG)                                                                                    \
-  gqa_decode_split<GG, false><<<grid, 256, 0, stream>>>((const uint16_t*)q, (const uint16_t*)K,       \
+  gqa_decode_split<GG, false><<<grid, kSplitWaves * 64, 0, stream>>>((const uint16_t*)q, (const uint16_t*)K,       \
                                                         (const uint16_t*)V,                           \
                                                         (const long long*)valid_len, acc, ml,         \
                                                         cache_len, chunk, splits, scale, none)
@@ -550,8 +741,7 @@ int q35_gqa_decode(const void* q, const void* K, const void* V, const void* vali
 #undef Q35_GQA
   int e = q35_last_error();
   if (e) return e;
-  gqa_decode_combine<<<QH, kAD, 0, stream>>>(acc, ml, (const uint16_t*)packed_gate, (uint16_t*)out,
-                                             splits, nullptr);
+  launch_combine(acc, ml, (const uint16_t*)packed_gate, (uint16_t*)out, QH, splits, nullptr, stream);
   return q35_last_error();
 }
 
@@ -568,15 +758,18 @@ int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, i
                          hipStream_t stream) {
   Q35_CHECK_ARG(D == kAD && KVH > 0 && QH % KVH == 0 && cache_len > 0);
   Q35_CHECK_ARG(packed && q_w && k_w && inv_freq && pos_t && K && V && cache_len_dev && out);
-  Q35_CHECK_ARG(rotary_dim > 0 && rotary_dim <= D && rotary_dim % 8 == 0);
+  // The in-kernel rotary table holds rot/2 <= 64 frequencies, one per lane.
+  Q35_CHECK_ARG(rotary_dim > 0 && rotary_dim <= 128 && rotary_dim % 8 == 0);
   Q35_CHECK_ARG(sec_h >= 0 && sec_w >= 0 && 3 * sec_h <= rotary_dim && 3 * sec_w <= rotary_dim);
   const int G = QH / KVH;
   Q35_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 8);
   int chunk = 0;
   const int splits = q35_gqa_decode_splits(cache_len, KVH, &chunk);
-  Q35_CHECK_ARG(splits <= 1024);
+  Q35_CHECK_ARG(splits <= kMaxSplits);
   Q35_CHECK_ARG(workspace_floats >= q35_gqa_decode_workspace(cache_len, QH, KVH, D));
   Q35_CHECK_ARG(q35_aligned16(K) && q35_aligned16(V) && q35_aligned16(workspace));
+  Q35_CHECK_ARG(q35_aligned4(inv_freq) && q35_aligned8(packed) && q35_aligned8(q_w) && q35_aligned8(k_w));
+  Q35_CHECK_ARG(q35_aligned8(out));
   float* acc = (float*)workspace;
   float* ml = acc + (size_t)QH * splits * D;
   FusedQ f;
@@ -595,7 +788,7 @@ int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, i
   f.v_cache = (uint16_t*)V;
   dim3 grid(KVH, splits);
 #define Q35_GQA(GG)                                                                                 \
-  gqa_decode_split<GG, true><<<grid, 256, 0, stream>>>(nullptr, (const uint16_t*)K,                \
+  gqa_decode_split<GG, true><<<grid, kSplitWaves * 64, 0, stream>>>(nullptr, (const uint16_t*)K,                \
                                                        (const uint16_t*)V,                         \
                                                        (const long long*)cache_len_dev, acc, ml,   \
                                                        cache_len, chunk, splits, scale, f)
@@ -606,8 +799,8 @@ int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, i
 #undef Q35_GQA
   int e = q35_last_error();
   if (e) return e;
-  gqa_decode_combine<<<QH, kAD, 0, stream>>>(acc, ml, (const uint16_t*)packed, (uint16_t*)out,
-                                             splits, (long long*)cache_len_dev);
+  launch_combine(acc, ml, (const uint16_t*)packed, (uint16_t*)out, QH, splits,
+                 (long long*)cache_len_dev, stream);
   return q35_last_error();
 }
 

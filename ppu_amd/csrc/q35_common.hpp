@@ -144,6 +144,8 @@ Q35_DEV uint32_t top1_index(uint64_t key) { return 0xffffffffu - (uint32_t)(key 
 static inline int q35_last_error() { return (int)hipGetLastError(); }
 
 static inline bool q35_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+static inline bool q35_aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
+static inline bool q35_aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 
 // Workgroup barrier that orders LDS only: outstanding global loads (e.g. a
 // weight stream issued before the barrier) stay in flight across it.

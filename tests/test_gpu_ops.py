@@ -340,6 +340,28 @@ def test_gqa_decode_attention(gpu, cache_len, n_valid):
     close(got, exp)
 
 
+@pytest.mark.parametrize("q_heads,kv_heads", [(2, 2), (4, 2), (16, 2), (4, 4), (8, 1)])
+def test_gqa_decode_back_to_back(gpu, q_heads, kv_heads):
+    """Head groupings G = 1, 2, 4, 8 and several launches queued without a host
+    sync in between: the in-kernel split merge keeps per-KV-head arrival
+    counters that each launch must leave at zero for the next one."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 20)
+    cache_len = 1152
+    kc = randn(g, 1, kv_heads, cache_len, 256)
+    vc = randn(g, 1, kv_heads, cache_len, 256)
+    kg, vg = kc.to(gpu), vc.to(gpu)
+    cases = []
+    for n_valid in (1152, 65, 3, 700):
+        q = randn(g, 1, q_heads, 1, 256)
+        length = torch.tensor(n_valid, dtype=torch.int64)
+        got = K.gqa_decode_attention(q.to(gpu), kg, vg, length.to(gpu), 0.0625)
+        cases.append((got, ref.gqa_decode_attention(q, kc, vc, length, 0.0625)))
+    for got, exp in cases:
+        close(got, exp)
+
+
 def test_gqa_decode_gate_fused(gpu):
     from ppu_amd import kernels as K
 
