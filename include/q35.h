@@ -87,6 +87,31 @@ int q35_swiglu_gemv(const void* W, const void* x, const void* u, const void* nor
                     int norm_w_f32, float eps, void* residual_out, void* x_norm_out, void* y,
                     int N, int K, int prologue, void* stream);
 
+/* int8-weight (A8W8) forms of the three GEMVs above, for one token: W is int8
+ * [N, K] (SwiGLU: [2N, K]) with fp32 per-channel scales s_w; the activation
+ * after the prologue (rounded to bf16) is quantised per token inside every
+ * workgroup (s_x = absmax/127, q = sat(rint(x*127/absmax))), int32 dot4
+ * accumulation, y = bf16(float(acc) * s_x * s_w[n]); SwiGLU dequantises gate
+ * and up to bf16 first. K a multiple of 1024 (1, 2, 4 or 6 KiB rows).
+ * Optional acc_out int32 (per output row; SwiGLU [2N]), xq_out int8 [K] and
+ * sx_out fp32 [1] (written by block 0). Each replaces the reference's
+ * norm kernel (kernels.py:44/85/139) followed by PPUA8W8Linear.forward
+ * (explore_runtime_quantization.py:161-181) and, for SwiGLU, silu_and_mul
+ * (kernels.py:158). */
+int q35_gemv_i8(const void* Wq, const void* s_w, const void* x, const void* u, const void* norm_w,
+                int norm_w_f32, float eps, void* residual_out, void* x_norm_out, void* y,
+                void* acc_out, void* xq_out, void* sx_out, int N, int K, int prologue,
+                void* stream);
+int q35_gemv_i8_conv(const void* Wq, const void* s_w, const void* x, const void* u,
+                     const void* norm_w, int norm_w_f32, float eps, void* residual_out, void* y,
+                     int N, int K, int prologue, const void* conv_w, void* conv_state,
+                     void* conv_out, int conv_channels, int conv_kw, const void* x_row, int x_rows,
+                     void* stream);
+int q35_swiglu_gemv_i8(const void* Wq, const void* s_w, const void* x, const void* u,
+                       const void* norm_w, int norm_w_f32, float eps, void* residual_out,
+                       void* x_norm_out, void* y, void* acc_out, int N, int K, int prologue,
+                       void* stream);
+
 /* ---- lm_head GEMV + top-1 -------------------------------------------- */
 
 /* Workspace slots (8 bytes each) for q35_lm_head_top1. */

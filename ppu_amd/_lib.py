@@ -33,6 +33,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_swiglu_gemv": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _I, _I, _P]),
     "q35_gemv_conv": (
         _I, [_P, _P, _P, _P, _I, _F, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _I, _P]),
+    "q35_gemv_i8": (
+        _I, [_P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "q35_gemv_i8_conv": (
+        _I, [_P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _I, _P]),
+    "q35_swiglu_gemv_i8": (
+        _I, [_P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _P]),
     "q35_lm_head_top1_workspace": (_L, [_I, _I]),
     "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),
     "q35_conv1d_update": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),

@@ -12,11 +12,19 @@
 //              that the reference calls [explore_runtime_quantization.py:167-172].
 //   output   : y[m, n] = bf16((float)acc[m, n] * s_x[m] * s_w[n])
 //
-// GEMV work split: one wave64 owns R weight rows; lane l reads 16 int8 at
-// k = c*1024 + 16l of each row for every chunk c (128-bit loads), so the
-// weight stream is read once; activations (L1/L2 resident) are read per chunk.
-// Bytes per launch = N*K + 4N + M*K + 2MN (+4M).
+// One token (M = 1) runs on the tiled GEMV of gemv.hip with int8 weights,
+// which quantises the activation inside every workgroup (q35_gemv_i8). Here:
+// weight/activation quantisation kernels, the skinny M <= 16 GEMV over
+// pre-quantised activations (one wave64 owns R weight rows; lane l reads 16
+// int8 at k = c*1024 + 16l, so the weight stream is read once per launch of
+// MT tokens), and the dequant of a library int32 GEMM for prefill.
 #include "q35_common.hpp"
+
+// The tiled int8-weight GEMV with the activation quantisation fused (gemv.hip).
+extern "C" int q35_gemv_i8(const void* Wq, const void* s_w, const void* x, const void* u,
+                           const void* norm_w, int norm_w_f32, float eps, void* residual_out,
+                           void* x_norm_out, void* y, void* acc_out, void* xq_out, void* sx_out,
+                           int N, int K, int prologue, hipStream_t stream);
 
 namespace {
 
@@ -40,13 +48,6 @@ __global__ __launch_bounds__(256) void quant_weight_rows(const uint16_t* __restr
   if (lane == 0) scale[n] = s;
 }
 
-Q35_DEV int8_t sat_i8(float v) {
-  // rint, then saturate; NaN (0 * inf for a zero row) maps to 0.
-  if (v != v) return 0;
-  const float r = rintf(v);
-  return (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
-}
-
 // One wave per token row.
 __global__ __launch_bounds__(256) void quant_act_rows(const uint16_t* __restrict__ x,
                                                       int8_t* __restrict__ xq,
@@ -63,23 +64,6 @@ __global__ __launch_bounds__(256) void quant_act_rows(const uint16_t* __restrict
   if (lane == 0) scale[m] = mx / 127.0f;
 }
 
-Q35_DEV int dot16(const uint4 a, const uint4 b, int acc) {
-  acc = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, acc, false);
-  acc = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, acc, false);
-  acc = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, acc, false);
-  acc = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, acc, false);
-  return acc;
-}
-
-Q35_DEV int wave_sum_i32(int v) {
-  v += dpp_i<Q35_DPP_QUAD_XOR1>(v);
-  v += dpp_i<Q35_DPP_QUAD_XOR2>(v);
-  v += dpp_i<Q35_DPP_ROW_HALF_MIRROR>(v);
-  v += dpp_i<Q35_DPP_ROW_MIRROR>(v);
-  v += __builtin_amdgcn_ds_swizzle(v, Q35_SWZ_XOR16);
-  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
-}
-
 struct A8Args {
   const int8_t* Wq;       // [N, K]
   const float* s_w;       // [N]
@@ -92,68 +76,6 @@ struct A8Args {
   int* acc_out;           // optional int32 [M, N]
   int M, N, K;
 };
-
-// Fused M=1 path: every wave quantises the (L2-resident) activation row
-// itself, so decode needs one launch per linear.
-template <int R, int NCH>
-__global__ __launch_bounds__(256) void a8w8_gemv_m1(const A8Args a) {
-  const int lane = threadIdx.x & 63;
-  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-  const bool writer = blockIdx.x == 0 && threadIdx.x < 64;
-  if (n0 >= a.N && !writer) return;
-  uint4 w[R][NCH];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      w[r][c] = n0 + r < a.N ? ld_stream16(a.Wq + (size_t)(n0 + r) * a.K + c * 1024 + lane * 16)
-                             : make_uint4(0, 0, 0, 0);
-  // Quantise x: lane holds 16 values per chunk.
-  float xf[NCH][16];
-  float mx = 0.f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const uint16_t* xp = a.x + c * 1024 + lane * 16;
-    unpack8(*reinterpret_cast<const uint4*>(xp), xf[c]);
-    unpack8(*reinterpret_cast<const uint4*>(xp + 8), xf[c] + 8);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(xf[c][j]));
-  }
-  mx = wave_max(mx);
-  const float inv = 127.0f / mx;
-  const float sx = mx / 127.0f;
-  uint4 xq[NCH];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    uint32_t wd[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      uint32_t v = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v |= ((uint32_t)(uint8_t)sat_i8(xf[c][4 * d + j] * inv)) << (8 * j);
-      wd[d] = v;
-    }
-    xq[c] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-    if (writer && a.xq_out) *reinterpret_cast<uint4*>(a.xq_out + c * 1024 + lane * 16) = xq[c];
-  }
-  if (writer && a.s_x_out && lane == 0) a.s_x_out[0] = sx;
-  if (n0 >= a.N) return;
-  int acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    acc[r] = 0;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) acc[r] = dot16(w[r][c], xq[c], acc[r]);
-    acc[r] = wave_sum_i32(acc[r]);
-  }
-  if (lane < R && n0 + lane < a.N) {
-    int v = acc[0];
-#pragma unroll
-    for (int r = 1; r < R; ++r) v = lane == r ? acc[r] : v;
-    a.y[n0 + lane] = (uint16_t)f2bf((float)v * sx * a.s_w[n0 + lane]);
-    if (a.acc_out) a.acc_out[n0 + lane] = v;
-  }
-}
 
 // General M (pre-quantised activations), any K multiple of 16.
 template <int R, int MT>
@@ -177,7 +99,7 @@ __global__ __launch_bounds__(256) void a8w8_gemv_mt(const A8Args a, int m0) {
       if (m < mcount) {
         const uint4 xv = *reinterpret_cast<const uint4*>(a.xq + (size_t)(m0 + m) * a.K + k);
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r][m] = dot16(w[r], xv, acc[r][m]);
+        for (int r = 0; r < R; ++r) acc[r][m] = dot16_i8(w[r], xv, acc[r][m]);
       }
     }
   }
@@ -261,15 +183,10 @@ int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void
   Q35_CHECK_ARG(q35_aligned16(Wq) && q35_aligned16(xq) && q35_aligned16(x));
   A8Args a{(const int8_t*)Wq, (const float*)s_w, (const int8_t*)xq, (const float*)s_x,
            (const uint16_t*)x, (int8_t*)xq, (float*)s_x, (uint16_t*)y, (int*)acc_out, M, N, K};
-  if (x && M == 1 && K % 1024 == 0 && (K == 2048 || K == 6144)) {
-    if (K == 2048) {
-      const int R = 2;
-      a8w8_gemv_m1<R, 2><<<(unsigned)((N + 4 * R - 1) / (4 * R)), 256, 0, stream>>>(a);
-    } else {
-      const int R = 1;
-      a8w8_gemv_m1<R, 6><<<(unsigned)((N + 4 * R - 1) / (4 * R)), 256, 0, stream>>>(a);
-    }
-    return q35_last_error();
+  if (x && M == 1 && (K == 1024 || K == 2048 || K == 4096 || K == 6144)) {
+    // One token: the tiled int8-weight GEMV quantises x in every workgroup.
+    return q35_gemv_i8(Wq, s_w, x, nullptr, nullptr, 0, 0.f, nullptr, nullptr, y, acc_out, xq, s_x,
+                       N, K, 0, stream);
   }
   if (x) {
     Q35_CHECK_ARG(xq && s_x);

@@ -55,6 +55,13 @@ struct GemvArgs {
   // row to r_out (the residual stream).
   const long long* x_row;
   int x_rows;
+  // int8 weights (W is int8 [rows_total, K]): per-channel scales; optional
+  // int32 accumulators [N] (SwiGLU: [2N]) and the quantised activation row
+  // and its scale, written by block 0.
+  const float* s_w;
+  int* acc_out;
+  int8_t* xq_out;
+  float* sx_out;
 };
 
 // Gated RMSNorm (reference kernels.py:115-155) runs over heads of this width.
@@ -72,15 +79,17 @@ Q35_DEV void nw8_from(const GemvArgs& a, const uint4 lo, const uint4 hi, float* 
   }
 }
 
-template <int WV, int R, int NCH, int PRO, int EPI>
-__global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
+template <int WV, int R, int NCH, int PRO, int EPI, bool I8>
+__global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
   constexpr int NT = WV * 64;
-  constexpr int NV = NCH * 64;                  // activation uint4 groups (8 bf16 each)
+  constexpr int NV = NCH * (I8 ? 128 : 64);     // 8-element activation groups
   constexpr int PER = (NV + NT - 1) / NT;       // groups per thread
   constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;  // outputs per wave
   static_assert(NV % NT == 0 || NT % NV == 0, "activation groups must tile the workgroup");
-  __shared__ uint4 xs[NV];
-  __shared__ float red[WV];
+  static_assert(!I8 || EPI != EPI_TOP1, "the top-1 epilogue is bf16 only");
+  __shared__ uint4 xs[I8 ? 1 : NV];             // bf16 activation (8 per group)
+  __shared__ uint2 xq_s[I8 ? NV : 1];           // int8 activation (8 per group)
+  __shared__ float red[WV], redm[WV];
   __shared__ unsigned long long best_s[WV];
 
   const int tid = threadIdx.x;
@@ -119,9 +128,16 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
       }
     }
   }
+  // int8 weights: the per-channel scales of the lane's output rows.
+  float sw_g = 0.f, sw_u = 0.f;
+  if (I8) {
+    const int n = min(n0 + (lane < P ? lane : 0), a.N - 1);
+    sw_g = a.s_w[n];
+    if (EPI == EPI_SWIGLU) sw_u = a.s_w[a.N + n];
+  }
 
-  // 2. weight stream: rows past the end read row 0 (valid memory) and are
-  //    never stored.
+  // 2. weight stream, 16 bytes per lane per 1 KiB chunk of a row: rows past
+  //    the end read row 0 (valid memory) and are never stored.
   int rows[R];
   if (EPI == EPI_SWIGLU) {
 #pragma unroll
@@ -134,12 +150,13 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < R; ++i) rows[i] = n0 + i < a.N ? n0 + i : 0;
   }
+  const size_t row_bytes = (size_t)a.K * (I8 ? 1 : 2);
   uint4 w[R][NCH];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint16_t* wrow = a.W + (size_t)rows[r] * a.K + lane * 8;
+    const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.W) + (size_t)rows[r] * row_bytes + lane * 16;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) w[r][c] = ld_stream16(wrow + c * 512);
+    for (int c = 0; c < NCH; ++c) w[r][c] = ld_stream16(wrow + c * 1024);
   }
 
   if (PRO == PRO_RMSNORM && writer && a.r_out && act) {
@@ -147,18 +164,22 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
     for (int j = 0; j < PER; ++j) *reinterpret_cast<uint4*>(a.r_out + (tid + j * NT) * 8) = xa[j];
   }
 
-  // 3. prologue into LDS.
+  // 3. prologue: the activation values of the thread's groups (0 for idle
+  //    threads); int8 weights need them rounded to bf16 before quantising.
+  float o[PER][8];
   if (PRO == PRO_NONE) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (act) xs[tid + j * NT] = xa[j];
+    for (int j = 0; j < PER; ++j) {
+      unpack8(xa[j], o[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[j][e] = act ? o[j][e] : 0.f;
+    }
   } else if (PRO == PRO_GATEDNORM) {
     // Group i holds elements 8i..8i+7, so head = i/16: the 16 groups of a head
     // sit on the 16 lanes of one DPP row (NT is a multiple of 16).
     static_assert(NT % 16 == 0, "gated norm needs whole heads per row");
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const int i = tid + j * NT;
       float s[8], z[8], wn[8];
       unpack8(xa[j], s);
       unpack8(ua[j], z);
@@ -167,18 +188,13 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
       for (int e = 0; e < 8; ++e) ss += s[e] * s[e];
       ss = row16_sum(ss);
       const float inv = rsqrt_cr(ss / (float)kGatedHead + a.eps);
-      if (act) {
-        nw8_from(a, wa[j], wb[j], wn);
-        float o[8];
+      nw8_from(a, wa[j], wb[j], wn);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float nb = round_bf(s[e] * inv);
-          const float weighted = round_bf(nb * round_bf(wn[e]));
-          o[e] = weighted * silu_f(z[e]);
-        }
-        const uint4 v = pack8(o);
-        xs[i] = v;
-        if (writer && a.xn_out) *reinterpret_cast<uint4*>(a.xn_out + i * 8) = v;
+      for (int e = 0; e < 8; ++e) {
+        const float nb = round_bf(s[e] * inv);
+        const float weighted = round_bf(nb * round_bf(wn[e]));
+        const float v = weighted * silu_f(z[e]);
+        o[j][e] = act ? (I8 ? round_bf(v) : v) : 0.f;
       }
     }
   } else {
@@ -208,40 +224,95 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
     const float inv = rsqrt_cr(tot / (float)a.K + a.eps);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const int i = tid + j * NT;
-      if (act) {
-        float o[8], wn[8];
-        nw8_from(a, wa[j], wb[j], wn);
+      float wn[8];
+      nw8_from(a, wa[j], wb[j], wn);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = s[j][e] * inv * (1.0f + wn[e]);
-        const uint4 v = pack8(o);
-        xs[i] = v;
-        if (writer && a.xn_out) *reinterpret_cast<uint4*>(a.xn_out + i * 8) = v;
+      for (int e = 0; e < 8; ++e) {
+        const float v = s[j][e] * inv * (1.0f + wn[e]);
+        o[j][e] = act ? (I8 ? round_bf(v) : v) : 0.f;
       }
     }
   }
+  if (PRO != PRO_NONE && writer && a.xn_out && act) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) *reinterpret_cast<uint4*>(a.xn_out + (tid + j * NT) * 8) = pack8(o[j]);
+  }
+
+  // 4. stage the activation in LDS: bf16, or (int8 weights) per-token int8
+  //    with s_x = absmax/127, q = sat(rint(x * 127/absmax)) over the whole row.
+  float sx = 0.f;
+  if (!I8) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (act) xs[tid + j * NT] = pack8(o[j]);
+  } else {
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(o[j][e]));
+    mx = wave_max(mx);
+    if (lane == 0) redm[wid] = mx;
+    lds_barrier();
+    mx = redm[0];
+#pragma unroll
+    for (int v = 1; v < WV; ++v) mx = fmaxf(mx, redm[v]);
+    const float inv = 127.0f / mx;
+    sx = mx / 127.0f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid + j * NT;
+      uint32_t q[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[e >> 2] |= (uint32_t)(uint8_t)sat_i8(o[j][e] * inv) << (8 * (e & 3));
+      const uint2 v = make_uint2(q[0], q[1]);
+      if (act) {
+        xq_s[i] = v;
+        if (writer && a.xq_out) *reinterpret_cast<uint2*>(a.xq_out + i * 8) = v;
+      }
+    }
+    if (writer && tid == 0 && a.sx_out) a.sx_out[0] = sx;
+  }
   lds_barrier();
 
-  // 4. dot products.
+  // 5. dot products: fp32 FMA on bf16 pairs, or exact int32 dot4 on int8
+  //    (then acc = float(acc_i32) * s_x; the row scale s_w follows per lane).
   float acc[R];
+  int iacc[R];
+  if (!I8) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    float xf[8];
-    unpack8(xs[c * 64 + lane], xf);
+    for (int c = 0; c < NCH; ++c) {
+      float xf[8];
+      unpack8(xs[c * 64 + lane], xf);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float wf[8];
+        unpack8(w[r][c], wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[r] = fmaf(wf[e], xf[e], acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) iacc[r] = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const uint4 xv = reinterpret_cast<const uint4*>(xq_s)[c * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < R; ++r) iacc[r] = dot16_i8(w[r][c], xv, iacc[r]);
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float wf[8];
-      unpack8(w[r][c], wf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[r] = fmaf(wf[e], xf[e], acc[r]);
+      iacc[r] = wave_sum_i32(iacc[r]);
+      acc[r] = (float)iacc[r] * sx;
     }
   }
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
 
-  // 5. epilogue.
+  // 6. epilogue.
   if (EPI == EPI_TOP1) {
     uint64_t best = 0;
 #pragma unroll
@@ -258,13 +329,22 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
     return;
   }
   if (lane < P && n0 + lane < a.N) {
+    const int n = n0 + lane;
     float v;
     if (EPI == EPI_STORE || EPI == EPI_CONV) {
       v = acc[0];
 #pragma unroll
       for (int r = 1; r < R; ++r) v = lane == r ? acc[r] : v;
+      if (I8) {
+        v *= sw_g;
+        if (a.acc_out) {
+          int iv = iacc[0];
+#pragma unroll
+          for (int r = 1; r < R; ++r) iv = lane == r ? iacc[r] : iv;
+          a.acc_out[n] = iv;
+        }
+      }
       if (EPI == EPI_CONV) {
-        const int n = n0 + lane;
         const uint32_t yb = f2bf(v);
         if (n < a.conv_channels) {
           const float c = conv_update_channel(a.conv_state + (size_t)n * a.conv_kw,
@@ -279,9 +359,23 @@ __global__ __launch_bounds__(WV * 64) void gemv_bf16(const GemvArgs a) {
         g = lane == i ? acc[i] : g;
         up = lane == i ? acc[P + i] : up;
       }
+      if (I8) {
+        g *= sw_g;
+        up *= sw_u;
+        if (a.acc_out) {
+          int ig = iacc[0], iu = iacc[P];
+#pragma unroll
+          for (int i = 1; i < P; ++i) {
+            ig = lane == i ? iacc[i] : ig;
+            iu = lane == i ? iacc[P + i] : iu;
+          }
+          a.acc_out[n] = ig;
+          a.acc_out[a.N + n] = iu;
+        }
+      }
       v = round_bf(silu_f(round_bf(g))) * round_bf(up);
     }
-    a.y[n0 + lane] = (uint16_t)f2bf(v);
+    a.y[n] = (uint16_t)f2bf(v);
   }
 }
 
@@ -370,19 +464,21 @@ __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __r
   }
 }
 
-template <int WV, int R, int NCH, int PRO, int EPI>
+template <int WV, int R, int NCH, int PRO, int EPI, bool I8 = false>
 long long launch_fast(const GemvArgs& a, hipStream_t stream) {
   constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;
   const long long blocks = (a.N + (long long)WV * P - 1) / ((long long)WV * P);
-  gemv_bf16<WV, R, NCH, PRO, EPI><<<(unsigned)blocks, WV * 64, 0, stream>>>(a);
+  gemv_fused<WV, R, NCH, PRO, EPI, I8><<<(unsigned)blocks, WV * 64, 0, stream>>>(a);
   return blocks;
 }
 
-bool fast_ok(const GemvArgs& a, int PRO) {
-  return (a.K % 512 == 0) && q35_aligned16(a.W) && q35_aligned16(a.x) &&
+// The tiled kernel reads 16-byte groups of W, x, u, the norm weight and the
+// outputs, and whole 1 KiB chunks of each weight row.
+bool fast_ok(const GemvArgs& a, int PRO, bool i8 = false) {
+  return (a.K % (i8 ? 1024 : 512) == 0) && q35_aligned16(a.W) && q35_aligned16(a.x) &&
          ((PRO != PRO_RESNORM && PRO != PRO_GATEDNORM) || q35_aligned16(a.u)) &&
-         q35_aligned16(a.r_out) &&
-         q35_aligned16(a.xn_out) && (PRO == PRO_NONE || q35_aligned16(a.nw));
+         q35_aligned16(a.r_out) && q35_aligned16(a.xn_out) && q35_aligned16(a.xq_out) &&
+         (PRO == PRO_NONE || q35_aligned16(a.nw));
 }
 
 // Shape -> tile choice (waves per workgroup, rows per wave), measured on
@@ -408,6 +504,23 @@ int dispatch(const GemvArgs& a, hipStream_t stream) {
     gemv_bf16_generic<PRO, EPI><<<blocks > 0 ? blocks : 1, 256, 0, stream>>>(a);
     return q35_last_error();
   }
+}
+
+// int8 weights: tiled path only (K a multiple of 1024: 1, 2, 4 or 6 chunks).
+template <int PRO, int EPI>
+int dispatch_i8(const GemvArgs& a, hipStream_t stream) {
+  if (!fast_ok(a, PRO, true) || !a.s_w) return (int)hipErrorInvalidValue;
+  const int nch = a.K / 1024;
+  if constexpr (EPI == EPI_SWIGLU) {
+    if (nch == 2) { launch_fast<8, 4, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 6) { launch_fast<4, 2, 6, PRO, EPI, true>(a, stream); return q35_last_error(); }
+  } else {
+    if (nch == 1) { launch_fast<4, 4, 1, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 2) { launch_fast<4, 4, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 6) { launch_fast<4, 2, 6, PRO, EPI, true>(a, stream); return q35_last_error(); }
+  }
+  return (int)hipErrorInvalidValue;
 }
 
 // lm_head tile: 4 waves x 4 rows per workgroup, 15520 candidates for the
@@ -478,6 +591,72 @@ int q35_swiglu_gemv(const void* W, const void* x, const void* u, const void* nor
   if (prologue == 0) return dispatch<PRO_NONE, EPI_SWIGLU>(a, stream);
   if (prologue == 1) return dispatch<PRO_RMSNORM, EPI_SWIGLU>(a, stream);
   return dispatch<PRO_RESNORM, EPI_SWIGLU>(a, stream);
+}
+
+// int8 weights (A8W8): y[N] = bf16(float(Wq[N,K] . xq) * s_x * s_w[n]) with the
+// activation (after the prologue, rounded to bf16) quantised per token inside
+// every workgroup: s_x = absmax/127, xq = sat(rint(x * 127/absmax)). Prologues
+// as q35_gemv_bf16. Optional outputs: acc_out int32 [N], xq_out int8 [K] and
+// sx_out fp32 [1] (the quantised activation, written by block 0).
+int q35_gemv_i8(const void* Wq, const void* s_w, const void* x, const void* u, const void* norm_w,
+                int norm_w_f32, float eps, void* residual_out, void* x_norm_out, void* y,
+                void* acc_out, void* xq_out, void* sx_out, int N, int K, int prologue,
+                hipStream_t stream) {
+  Q35_CHECK_ARG(N > 0 && K > 0 && Wq && s_w && x && y);
+  Q35_CHECK_ARG(prologue >= 0 && prologue <= 3);
+  Q35_CHECK_ARG(prologue == 0 || norm_w);
+  Q35_CHECK_ARG(prologue < 2 || u);
+  Q35_CHECK_ARG(prologue != 3 || K % kGatedHead == 0);
+  GemvArgs a{(const uint16_t*)Wq, (const uint16_t*)x, (const uint16_t*)u, norm_w,
+             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
+             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0, nullptr, 0,
+             (const float*)s_w, (int*)acc_out, (int8_t*)xq_out, (float*)sx_out};
+  if (prologue == 0) return dispatch_i8<PRO_NONE, EPI_STORE>(a, stream);
+  if (prologue == 1) return dispatch_i8<PRO_RMSNORM, EPI_STORE>(a, stream);
+  if (prologue == 2) return dispatch_i8<PRO_RESNORM, EPI_STORE>(a, stream);
+  return dispatch_i8<PRO_GATEDNORM, EPI_STORE>(a, stream);
+}
+
+// q35_gemv_conv with int8 weights (quantisation as q35_gemv_i8).
+int q35_gemv_i8_conv(const void* Wq, const void* s_w, const void* x, const void* u,
+                     const void* norm_w, int norm_w_f32, float eps, void* residual_out, void* y,
+                     int N, int K, int prologue, const void* conv_w, void* conv_state,
+                     void* conv_out, int conv_channels, int conv_kw, const void* x_row, int x_rows,
+                     hipStream_t stream) {
+  Q35_CHECK_ARG(N > 0 && K > 0 && Wq && s_w && x && y);
+  Q35_CHECK_ARG(prologue >= 0 && prologue <= 2);
+  Q35_CHECK_ARG(prologue == 0 || norm_w);
+  Q35_CHECK_ARG(prologue != 2 || u);
+  Q35_CHECK_ARG(conv_channels >= 0 && conv_channels <= N && conv_kw > 0 && conv_kw <= 16);
+  Q35_CHECK_ARG(conv_channels == 0 || (conv_w && conv_state && conv_out));
+  Q35_CHECK_ARG(!x_row || (prologue == 1 && x_rows > 0));
+  GemvArgs a{(const uint16_t*)Wq, (const uint16_t*)x, (const uint16_t*)u, norm_w,
+             (uint16_t*)residual_out, nullptr, (uint16_t*)y, nullptr, N, K, norm_w_f32, eps,
+             (const uint16_t*)conv_w, (uint16_t*)conv_state, (uint16_t*)conv_out, conv_channels,
+             conv_kw, (const long long*)x_row, x_rows, (const float*)s_w, nullptr, nullptr,
+             nullptr};
+  if (prologue == 0) return dispatch_i8<PRO_NONE, EPI_CONV>(a, stream);
+  if (prologue == 1) return dispatch_i8<PRO_RMSNORM, EPI_CONV>(a, stream);
+  return dispatch_i8<PRO_RESNORM, EPI_CONV>(a, stream);
+}
+
+// q35_swiglu_gemv with int8 [gate; up] weights [2N, K] and scales [2N]: gate and
+// up are dequantised to bf16 before the SwiGLU. acc_out (optional) int32 [2N].
+int q35_swiglu_gemv_i8(const void* Wq, const void* s_w, const void* x, const void* u,
+                       const void* norm_w, int norm_w_f32, float eps, void* residual_out,
+                       void* x_norm_out, void* y, void* acc_out, int N, int K, int prologue,
+                       hipStream_t stream) {
+  Q35_CHECK_ARG(N > 0 && K > 0 && Wq && s_w && x && y);
+  Q35_CHECK_ARG(prologue >= 0 && prologue <= 2);
+  Q35_CHECK_ARG(prologue == 0 || norm_w);
+  Q35_CHECK_ARG(prologue != 2 || u);
+  GemvArgs a{(const uint16_t*)Wq, (const uint16_t*)x, (const uint16_t*)u, norm_w,
+             (uint16_t*)residual_out, (uint16_t*)x_norm_out, (uint16_t*)y, nullptr, N, K,
+             norm_w_f32, eps, nullptr, nullptr, nullptr, 0, 0, nullptr, 0,
+             (const float*)s_w, (int*)acc_out, nullptr, nullptr};
+  if (prologue == 0) return dispatch_i8<PRO_NONE, EPI_SWIGLU>(a, stream);
+  if (prologue == 1) return dispatch_i8<PRO_RMSNORM, EPI_SWIGLU>(a, stream);
+  return dispatch_i8<PRO_RESNORM, EPI_SWIGLU>(a, stream);
 }
 
 // Number of 64-bit candidate slots q35_lm_head_top1 needs in its workspace.

@@ -170,3 +170,30 @@ Q35_DEV float conv_update_channel(uint16_t* __restrict__ st, const uint16_t* __r
   acc = fmaf(bf2f(xin), bf2f(w[kw - 1]), acc);
   return round_bf(silu_f(round_bf(acc)));
 }
+
+// ------------------------------------------------------------------ int8
+// Saturating float -> int8 after rint; NaN (0 * inf for a zero row) maps to 0.
+Q35_DEV int8_t sat_i8(float v) {
+  if (v != v) return 0;
+  const float r = rintf(v);
+  return (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
+}
+
+// 16 int8 pairs into an int32 accumulator (v_dot4c_i32_i8).
+Q35_DEV int dot16_i8(const uint4 a, const uint4 b, int acc) {
+  acc = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, acc, false);
+  return acc;
+}
+
+Q35_DEV int wave_sum_i32(int v) {
+  v += dpp_i<Q35_DPP_QUAD_XOR1>(v);
+  v += dpp_i<Q35_DPP_QUAD_XOR2>(v);
+  v += dpp_i<Q35_DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_i<Q35_DPP_ROW_MIRROR>(v);
+  v += __builtin_amdgcn_ds_swizzle(v, Q35_SWZ_XOR16);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
+}
+

@@ -98,6 +98,11 @@ class _Linear:
             self.wq = self.scale = None
         self.out_features = weight.shape[0]
 
+    def gemv_args(self) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """(weight, scale) for the fused decode GEMVs: bf16 weight and None, or
+        int8 weight and its fp32 per-channel scales."""
+        return (self.wq, self.scale) if self.a8w8 else (self.weight, None)
+
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         if self.a8w8:
             return K.a8w8_linear(x.contiguous(), self.wq, self.scale)
@@ -347,8 +352,9 @@ def _fused_decode_layers(text_model, input_ids, inputs_embeds, config, past_key_
     gate/up GEMV -> SwiGLU] [down]. Per attention layer: [residual add +
     RMSNorm -> packed projection] [Q/K norm + RoPE + cache write + split-K
     attention] [combine + gate + length += 1] [o_proj] and the same MLP. The
-    embedding row is gathered by the first projection when layer 0 is a bf16
-    DeltaNet layer.
+    embedding row is gathered by the first projection when layer 0 is a
+    DeltaNet layer. With A8W8 the same launches take int8 weights: each GEMV
+    quantises its (normalised) input row per token inside the launch.
     """
     layers = text_model.layers[: text_model.config.num_hidden_layers]
     in_kernel_rope = _rope_in_kernel(text_model)
@@ -363,47 +369,37 @@ def _fused_decode_layers(text_model, input_ids, inputs_embeds, config, past_key_
         delta = layer.block_type == "linear_attention"
         mod = layer.linear_attn if delta else layer.self_attn
         lin = mod._q35_in if delta else mod._q35_qgkv
-        if residual is None and not (index == 0 and delta and not lin.a8w8):
+        w_in, s_in = lin.gemv_args()
+        if residual is None and not (index == 0 and delta):
             residual = text_model.embed_tokens(input_ids.view(1, 1))
         if delta:
             conv_state, rec_state = _delta_cache_tensors(
                 mod, past_key_values, 1, 1, lin_device(lin), torch.bfloat16)
-        # residual add + input RMSNorm fused into the packed projection
-        if lin.a8w8:
-            if update is None:
-                normalized = K.rms_norm(residual, ln.weight, ln.eps)
-            else:
-                residual, normalized = K.residual_add_rms_norm(residual, update, ln.weight, ln.eps)
-            packed = lin(normalized)
-        elif delta:
-            # ... and the conv1d update in its epilogue (embedding gather for layer 0)
+            # residual add + input RMSNorm in the packed projection's prologue,
+            # the conv1d update in its epilogue (embedding gather for layer 0)
             if residual is None:
                 r_new, packed, qkv = K.norm_linear_conv(
-                    text_model.embed_tokens.weight, None, ln.weight, ln.eps, lin.weight,
-                    mod._q35_conv_w, conv_state, token=input_ids)
+                    text_model.embed_tokens.weight, None, ln.weight, ln.eps, w_in,
+                    mod._q35_conv_w, conv_state, token=input_ids, weight_scale=s_in)
             else:
-                r_new, packed, qkv = K.norm_linear_conv(residual, update, ln.weight, ln.eps,
-                                                        lin.weight, mod._q35_conv_w, conv_state)
+                r_new, packed, qkv = K.norm_linear_conv(residual, update, ln.weight, ln.eps, w_in,
+                                                        mod._q35_conv_w, conv_state,
+                                                        weight_scale=s_in)
             if r_new is not None:
                 residual = r_new
-        elif update is None:
-            packed = K.norm_linear(residual, ln.weight, ln.eps, lin.weight)
+            # delta rule on the convolved qkv, then gated RMSNorm as the
+            # prologue of the output projection
+            core = K.delta_recurrent_fused(qkv, packed, mod.A_log, mod.dt_bias, rec_state)
+            z = packed[..., mod.conv_dim : mod.conv_dim + mod.value_dim]
+            w_out, s_out = mod._q35_out.gemv_args()
+            update = K.gated_norm_linear(core, z, mod.norm.weight, mod.layer_norm_epsilon, w_out,
+                                         weight_scale=s_out)
         else:
-            residual, packed = K.residual_norm_linear(residual, update, ln.weight, ln.eps, lin.weight)
-        if delta:
-            if lin.a8w8 or mod._q35_out.a8w8:
-                core = K.delta_decode_fused(packed, mod._q35_conv_w, conv_state, mod.A_log,
-                                            mod.dt_bias, rec_state, mod.norm.weight,
-                                            mod.layer_norm_epsilon)
-                update = mod._q35_out(core.reshape(1, 1, mod.value_dim))
+            if update is None:
+                packed = K.norm_linear(residual, ln.weight, ln.eps, w_in, weight_scale=s_in)
             else:
-                # delta rule on the convolved qkv, then gated RMSNorm as the
-                # prologue of the output projection
-                core = K.delta_recurrent_fused(qkv, packed, mod.A_log, mod.dt_bias, rec_state)
-                z = packed[..., mod.conv_dim : mod.conv_dim + mod.value_dim]
-                update = K.gated_norm_linear(core, z, mod.norm.weight, mod.layer_norm_epsilon,
-                                             mod._q35_out.weight)
-        else:
+                residual, packed = K.residual_norm_linear(residual, update, ln.weight, ln.eps, w_in,
+                                                          weight_scale=s_in)
             cache_layer = _static_cache_layer(mod, past_key_values, residual)
             if in_kernel_rope:
                 out = K.gqa_decode_fused(
@@ -425,13 +421,9 @@ def _fused_decode_layers(text_model, input_ids, inputs_embeds, config, past_key_
             update = mod._q35_o(out)
         # post-attention residual + RMSNorm fused into the SwiGLU GEMV
         pln = layer.post_attention_layernorm
-        gate_up = layer.mlp._q35_gate_up
-        if gate_up.a8w8:
-            residual, mlp_in = K.residual_add_rms_norm(residual, update, pln.weight, pln.eps)
-            act = K.silu_and_mul(gate_up(mlp_in))
-        else:
-            residual, act = K.residual_norm_linear(residual, update, pln.weight, pln.eps,
-                                                   gate_up.weight, swiglu=True)
+        w_gu, s_gu = layer.mlp._q35_gate_up.gemv_args()
+        residual, act = K.residual_norm_linear(residual, update, pln.weight, pln.eps, w_gu,
+                                               swiglu=True, weight_scale=s_gu)
         update = layer.mlp._q35_down(act)
     _, normalized = K.residual_add_rms_norm(residual, update, text_model.norm.weight,
                                             text_model.norm.eps)

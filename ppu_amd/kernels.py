@@ -147,6 +147,27 @@ def attention_gate_mul(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int
 
 
 # ------------------------------------------------------------------ GEMV
+def _gemv_weight(weight: torch.Tensor, weight_scale: torch.Tensor | None):
+    """A fused GEMV's weight: bf16 ``[N, K]`` (scale None), or int8 ``[N, K]``
+    with its fp32 per-channel scales (A8W8: the activation is quantised per
+    token inside the launch). Returns ``(weight, flat scales or None)``."""
+
+    if weight.ndim != 2 or not weight.is_contiguous():
+        raise ValueError("GEMV weight must be a contiguous [N, K] tensor")
+    if weight.dtype == torch.int8:
+        if weight_scale is None:
+            raise ValueError("int8 weights need their per-channel scales")
+        scale = weight_scale.reshape(-1)
+        if (scale.dtype != torch.float32 or scale.numel() != weight.shape[0]
+                or not scale.is_contiguous() or scale.device != weight.device):
+            raise ValueError("weight_scale must be fp32 with one value per weight row")
+        return weight, scale
+    if weight_scale is not None:
+        raise ValueError("weight_scale is only for int8 weights")
+    _need_bf16(weight)
+    return weight, None
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """Decode ``F.linear(x, W)`` for one token (bf16, fp32 accumulate).
 
@@ -178,26 +199,38 @@ def residual_norm_linear(
     weight: torch.Tensor,
     *,
     swiglu: bool = False,
+    weight_scale: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``r' = residual + update``; ``y = linear(RMSNorm(r'), W)`` in one launch.
 
     The residual add and RMSNorm of reference kernels.py:85 run as the GEMV
-    prologue (every wave recomputes the 2048-wide norm from L2); with
+    prologue (every workgroup recomputes the 2048-wide norm from L2); with
     ``swiglu`` the epilogue of reference kernels.py:232 is applied to a packed
-    [gate; up] weight. Returns ``(r', y)``.
+    [gate; up] weight. An int8 ``weight`` with ``weight_scale`` runs the A8W8
+    linear on the normalised row (quantised per token in the launch).
+    Returns ``(r', y)``.
     """
 
     k = residual.shape[-1]
     if residual.numel() != k or update.shape != residual.shape:
         raise ValueError("fused residual GEMV expects one token")
-    _need_bf16(residual, update, weight)
+    _need_bf16(residual, update)
+    weight, sw = _gemv_weight(weight, weight_scale)
     w, wf = _param(norm_weight)
     n = weight.shape[0] // 2 if swiglu else weight.shape[0]
     r_out = torch.empty_like(residual)
     out = torch.empty((*residual.shape[:-1], n), device=residual.device, dtype=residual.dtype)
-    name = "q35_swiglu_gemv" if swiglu else "q35_gemv_bf16"
-    _lib.call(name, weight.data_ptr(), residual.data_ptr(), update.data_ptr(), w.data_ptr(), wf,
-              float(eps), r_out.data_ptr(), None, out.data_ptr(), n, k, 2, _stream(residual))
+    args = (residual.data_ptr(), update.data_ptr(), w.data_ptr(), wf, float(eps), r_out.data_ptr(),
+            None, out.data_ptr())
+    if sw is None:
+        name = "q35_swiglu_gemv" if swiglu else "q35_gemv_bf16"
+        _lib.call(name, weight.data_ptr(), *args, n, k, 2, _stream(residual))
+    elif swiglu:
+        _lib.call("q35_swiglu_gemv_i8", weight.data_ptr(), sw.data_ptr(), *args, None, n, k, 2,
+                  _stream(residual))
+    else:
+        _lib.call("q35_gemv_i8", weight.data_ptr(), sw.data_ptr(), *args, None, None, None, n, k, 2,
+                  _stream(residual))
     return r_out, out
 
 
@@ -206,19 +239,27 @@ def norm_linear(
     norm_weight: torch.Tensor,
     eps: float,
     weight: torch.Tensor,
+    *,
+    weight_scale: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``linear(rms_norm(x), W)`` for one token in one launch: the RMSNorm of
-    reference kernels.py:44 as the GEMV prologue (layer 0's input norm)."""
+    reference kernels.py:44 as the GEMV prologue (layer 0's input norm); int8
+    ``weight`` + ``weight_scale``: A8W8 as residual_norm_linear."""
 
     k = x.shape[-1]
     if x.numel() != k or weight.ndim != 2 or weight.shape[1] != k:
         raise ValueError("fused norm GEMV expects one token matching the weight")
-    _need_bf16(x, weight)
+    _need_bf16(x)
+    weight, sw = _gemv_weight(weight, weight_scale)
     w, wf = _param(norm_weight)
     n = weight.shape[0]
     out = torch.empty((*x.shape[:-1], n), device=x.device, dtype=x.dtype)
-    _lib.call("q35_gemv_bf16", weight.data_ptr(), x.contiguous().data_ptr(), None, w.data_ptr(), wf,
-              float(eps), None, None, out.data_ptr(), n, k, 1, _stream(x))
+    args = (x.contiguous().data_ptr(), None, w.data_ptr(), wf, float(eps), None, None, out.data_ptr())
+    if sw is None:
+        _lib.call("q35_gemv_bf16", weight.data_ptr(), *args, n, k, 1, _stream(x))
+    else:
+        _lib.call("q35_gemv_i8", weight.data_ptr(), sw.data_ptr(), *args, None, None, None, n, k, 1,
+                  _stream(x))
     return out
 
 
@@ -232,6 +273,7 @@ def norm_linear_conv(
     conv_state: torch.Tensor,
     *,
     token: torch.Tensor | None = None,
+    weight_scale: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor]:
     """DeltaNet input projection of one token in one launch.
 
@@ -244,7 +286,8 @@ def norm_linear_conv(
 
     With ``token`` (an int64 device scalar) ``residual`` is the embedding table
     ``[V, K]``: the first layer's input is its row ``token`` (the lookup of
-    integration.py:402-403, done in the prologue), returned as ``r'``.
+    integration.py:402-403, done in the prologue), returned as ``r'``. An int8
+    ``weight`` with ``weight_scale`` runs the projection as A8W8.
     """
 
     k = residual.shape[-1]
@@ -261,7 +304,8 @@ def norm_linear_conv(
         raise ValueError("conv state does not match the conv weight (batch 1)")
     if not conv_state.is_contiguous() or not conv_weight.is_contiguous():
         raise ValueError("conv tensors must be contiguous")
-    _need_bf16(residual, weight, conv_weight, conv_state)
+    _need_bf16(residual, conv_weight, conv_state)
+    weight, sw = _gemv_weight(weight, weight_scale)
     w, wf = _param(norm_weight)
     n = weight.shape[0]
     dev = residual.device
@@ -274,10 +318,14 @@ def norm_linear_conv(
         r_out = torch.empty_like(residual)
     elif token is not None:
         r_out = torch.empty((1, 1, k), device=dev, dtype=_BF16)
-    _lib.call("q35_gemv_conv", weight.data_ptr(), residual.data_ptr(), _lib.ptr(update),
-              w.data_ptr(), wf, float(eps), _lib.ptr(r_out), packed.data_ptr(), n, k,
-              2 if update is not None else 1, conv_weight.data_ptr(), conv_state.data_ptr(),
-              qkv.data_ptr(), channels, kw, _lib.ptr(token), rows, _stream(residual))
+    args = (residual.data_ptr(), _lib.ptr(update), w.data_ptr(), wf, float(eps), _lib.ptr(r_out),
+            packed.data_ptr(), n, k, 2 if update is not None else 1, conv_weight.data_ptr(),
+            conv_state.data_ptr(), qkv.data_ptr(), channels, kw, _lib.ptr(token), rows,
+            _stream(residual))
+    if sw is None:
+        _lib.call("q35_gemv_conv", weight.data_ptr(), *args)
+    else:
+        _lib.call("q35_gemv_i8_conv", weight.data_ptr(), sw.data_ptr(), *args)
     return r_out, packed, qkv
 
 
@@ -287,23 +335,31 @@ def gated_norm_linear(
     norm_weight: torch.Tensor,
     eps: float,
     weight: torch.Tensor,
+    *,
+    weight_scale: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``linear(gated_rms_norm(core, gate), W)`` for one token in one launch:
     the gated RMSNorm of reference kernels.py:139 (heads of 128, ``w`` used
     directly) as the prologue of the DeltaNet output projection. ``gate`` may
-    be a contiguous slice of the packed projection."""
+    be a contiguous slice of the packed projection. int8 ``weight`` +
+    ``weight_scale``: A8W8 on the normed row."""
 
     k = core.numel()
     if gate.numel() != k or weight.ndim != 2 or weight.shape[1] != k or k % 128:
         raise ValueError("gated norm GEMV expects one token of whole 128-wide heads")
     if not core.is_contiguous() or not gate.is_contiguous():
         raise ValueError("gated norm GEMV inputs must be contiguous")
-    _need_bf16(core, gate, weight)
+    _need_bf16(core, gate)
+    weight, sw = _gemv_weight(weight, weight_scale)
     w, wf = _param(norm_weight)
     n = weight.shape[0]
     out = torch.empty((1, 1, n), device=core.device, dtype=_BF16)
-    _lib.call("q35_gemv_bf16", weight.data_ptr(), core.data_ptr(), gate.data_ptr(), w.data_ptr(),
-              wf, float(eps), None, None, out.data_ptr(), n, k, 3, _stream(core))
+    args = (core.data_ptr(), gate.data_ptr(), w.data_ptr(), wf, float(eps), None, None, out.data_ptr())
+    if sw is None:
+        _lib.call("q35_gemv_bf16", weight.data_ptr(), *args, n, k, 3, _stream(core))
+    else:
+        _lib.call("q35_gemv_i8", weight.data_ptr(), sw.data_ptr(), *args, None, None, None, n, k, 3,
+                  _stream(core))
     return out
 
 

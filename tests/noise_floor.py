@@ -7,7 +7,7 @@ most one fp32 ulp per variance. The relative L2 change of the final hidden
 state per step is the floor the GPU-vs-oracle bounds in test_gpu_model.py are
 set from. Needs about 25 GB of host memory for a8w8 (fp64 integer weights).
 
-    python tests/noise_floor.py bf16|a8w8
+    python tests/noise_floor.py bf16|a8w8 [steps]
 """
 
 from __future__ import annotations
@@ -25,7 +25,7 @@ from oracle.model import OracleDecoder  # noqa: E402
 from ppu_amd import synth  # noqa: E402
 
 
-def main(mode: str) -> None:
+def main(mode: str, steps: int = 64) -> None:
     t0 = time.time()
     cfg = synth.config_2b()
     model = synth.build_model(cfg, device="cpu", seed=1234)
@@ -33,10 +33,11 @@ def main(mode: str) -> None:
     del model
     dec = OracleDecoder(state, cfg, a8w8=mode == "a8w8")
     ids = torch.randint(0, cfg.vocab_size, (1, 1024), generator=torch.Generator().manual_seed(7))
-    forced = torch.randint(0, cfg.vocab_size, (16,), generator=torch.Generator().manual_seed(8)).tolist()
+    forced = torch.randint(0, cfg.vocab_size, (steps - 1,),
+                           generator=torch.Generator().manual_seed(8)).tolist()
 
     def run():
-        cache = dec.new_cache(1100)
+        cache = dec.new_cache(1024 + steps + 8)
         hs = [dec.forward(ids, cache)[:, -1]]
         for t in forced:
             hs.append(dec.forward(torch.tensor([[t]]), cache)[:, -1])
@@ -58,9 +59,11 @@ def main(mode: str) -> None:
         ops.rms_norm = orig
     errs = [float((a.double() - b.double()).norm() / b.double().norm()) for a, b in zip(h1, h2)]
     print(mode, "per step", " ".join(f"{e:.3f}" for e in errs))
-    print(f"{mode} mean {sum(errs) / len(errs):.4f} max {max(errs):.4f}")
+    srt = sorted(errs)
+    print(f"{mode} {len(errs)} steps: mean {sum(errs) / len(errs):.4f} "
+          f"p90 {srt[int(0.9 * (len(srt) - 1))]:.4f} max {srt[-1]:.4f}")
 
 
 if __name__ == "__main__":
     torch.set_num_threads(os.cpu_count() or 1)
-    main(sys.argv[1] if len(sys.argv) > 1 else "bf16")
+    main(sys.argv[1] if len(sys.argv) > 1 else "bf16", int(sys.argv[2]) if len(sys.argv) > 2 else 64)

@@ -4,7 +4,7 @@ A Transformers Qwen3.5 model (synthetic seeded weights) is patched with
 ``apply_fusions`` and run on the GPU: prefill, then greedy decode through the
 captured graph. The oracle decoder gets the identical weights on the CPU and
 is teacher-forced with the GPU's tokens, so every step compares the two paths
-on the same history: the final hidden states must agree to HIDDEN_RTOL (set from the measured
+on the same history: the final hidden states must agree to HIDDEN_BOUNDS (set from the measured
 summation-order noise floor of the oracle itself), and a
 token may differ only where the oracle's logit gap between the two tokens is
 within the measured GPU-vs-oracle difference of those two logits (random-init
@@ -21,16 +21,18 @@ from ppu_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-# Relative L2 error allowed between the GPU's and the oracle's final hidden
-# state at a teacher-forced step, set at about twice the oracle's own noise
-# floor. Two CPU oracle variants that differ only in the fp32 summation order
-# of their linear layers diverge by 1.1 % (4 layers) and 2.4 % (12 layers) on
-# these random-init weights (tests/test_oracle_model.py); on the 24-layer 2B
-# shape a one-ulp change of the RMSNorm variances moves the hidden state by
-# 2.4 % mean / 2.9 % max in bf16 and 8.2 % mean / 10 % max in a8w8, where the
-# per-token int8 quantisation turns ulp changes into whole int8 steps
-# (tests/noise_floor.py).
-HIDDEN_RTOL = {"tiny": 0.03, "2b": 0.07, "2b-a8w8": 0.2}
+# Relative L2 error between the GPU's and the oracle's final hidden state at a
+# teacher-forced step: (bound on the mean over the steps, bound on every
+# step), set from the oracle's own noise floor. Two CPU oracle variants that
+# differ only in the fp32 summation order of their linear layers diverge by
+# 1.1 % (4 layers) and 2.4 % (12 layers) on these random-init weights
+# (tests/test_oracle_model.py). On the 24-layer 2B shape a one-ulp change of the
+# RMSNorm variances moves the hidden state, over 64 steps, by 2.3 % mean /
+# 2.9 % max in bf16 and 8.2 % mean / 10 % max in A8W8, where the per-token int8
+# quantisation turns ulp changes into whole int8 steps (tests/noise_floor.py).
+# The GPU perturbs every reduction, not one: mean bounds are about twice the
+# floor mean, per-step bounds about 2.4x (bf16) and 3x (A8W8) the floor max.
+HIDDEN_BOUNDS = {"tiny": (0.03, 0.03), "2b": (0.05, 0.07), "2b-a8w8": (0.16, 0.30)}
 
 
 def _build(cfg, gpu, fusion):
@@ -62,11 +64,13 @@ def _gpu_hidden_states(model, prompt, tokens, bucket):
     return hidden
 
 
-def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden, rtol):
-    """Every step: the GPU's hidden state within HIDDEN_RTOL of the oracle's;
-    the tokens equal, or the flip explained: the oracle's logit gap between the
-    two tokens is no larger than the measured GPU-vs-oracle difference of
-    those two logits plus one bf16 ulp."""
+def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden, bounds):
+    """The GPU's hidden state within ``bounds`` = (mean, per-step) relative
+    error of the oracle's; at every step the tokens equal, or the flip
+    explained: the oracle's logit gap between the two tokens is no larger than
+    the measured GPU-vs-oracle difference of those two logits plus one bf16
+    ulp."""
+    mean_bound, step_bound = bounds
     ref, ref_hidden = oracle.teacher_forced(prompt.cpu(), tokens[:-1], max_len, return_hidden=True)
     emb = oracle.w["embed"].double()
     bad, errs = [], []
@@ -74,7 +78,7 @@ def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden, rtol):
         hg, ho = gpu_hidden[step].double(), ref_hidden[step].double()
         err = float((hg - ho).norm() / ho.norm())
         errs.append(err)
-        if err > rtol:
+        if err > step_bound:
             bad.append((step, "hidden", err))
         if tok != rt:
             rows = emb[[tok, rt]]
@@ -88,9 +92,11 @@ def _check_teacher_forced(oracle, prompt, tokens, max_len, gpu_hidden, rtol):
             if gap > noise + ulp:
                 bad.append((step, tok, rt, gap, noise))
     same = sum(t == r for t, (r, _) in zip(tokens, ref))
+    mean = sum(errs) / len(errs)
     print(f"{len(tokens)} steps, {same} identical tokens, hidden rel err max {max(errs):.2e} "
-          f"mean {sum(errs) / len(errs):.2e}", flush=True)
+          f"mean {mean:.2e}", flush=True)
     assert not bad, f"steps outside the parity bound: {bad}"
+    assert mean <= mean_bound, f"mean hidden error {mean:.3e} above {mean_bound}"
 
 
 @pytest.mark.parametrize("fused,a8w8", [(True, False), (False, False), (True, True)])
@@ -108,7 +114,7 @@ def test_tiny_model_greedy_vs_oracle(gpu, fused, a8w8):
     hidden = _gpu_hidden_states(model, prompt, res.tokens, res.meta["cache_bucket"])
     oracle = OracleDecoder(state, cfg, a8w8=a8w8)
     _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden,
-                          HIDDEN_RTOL["tiny"])
+                          HIDDEN_BOUNDS["tiny"])
 
 
 def test_graph_replay_matches_eager_decode(gpu):
@@ -176,4 +182,4 @@ def test_2b_prefill_1024_decode_64_vs_oracle(gpu, variant):
     torch.cuda.empty_cache()
     oracle = OracleDecoder(state, cfg, a8w8=variant == "a8w8")
     _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden,
-                          HIDDEN_RTOL["2b" if variant == "bf16" else "2b-a8w8"])
+                          HIDDEN_BOUNDS["2b" if variant == "bf16" else "2b-a8w8"])

@@ -437,6 +437,135 @@ def test_a8w8_zero_row(gpu):
     assert not xq.any() and float(sx) == 0.0 and not y.float().any()
 
 
+def _i8_row(prologue, x, u, nw):
+    """The oracle's normalised activation row for a GEMV prologue."""
+    if prologue == 0:
+        return x
+    if prologue == 1:
+        return ref.rms_norm(x, nw)
+    if prologue == 2:
+        return ref.residual_add_rms_norm(x, u, nw)[1]
+    k = x.shape[-1]
+    return ref.gated_rms_norm(x.reshape(-1, 128), u.reshape(-1, 128), nw).reshape(1, k)
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+@pytest.mark.parametrize("prologue", [0, 1, 2, 3])
+@pytest.mark.parametrize("n,k", [(2048, 2048), (1000, 6144), (4352, 1024)])
+def test_gemv_i8_prologues(gpu, prologue, n, k):
+    """int8-weight GEMV (A8W8, one token) with each prologue. Bit-exact on the
+    kernel's own normalised row (x_norm_out): its quantisation (xq, s_x), the
+    int32 accumulators and the dequantised bf16 output; the normalised row
+    matches the oracle's within rtol 1e-2, and the output the oracle's
+    end-to-end A8W8 linear within 1 % (a one-ulp difference in the row can move
+    an int8 step)."""
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 60 + prologue)
+    w = randn(g, n, k, scale=0.02)
+    x, u = randn(g, 1, k), randn(g, 1, k)
+    nw = randn(g, 128, scale=0.02, mean=1.0) if prologue == 3 else randn(g, k, scale=0.02)
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    xg, ug, nwg = x.to(gpu), u.to(gpu), nw.to(gpu)
+    y = torch.empty(1, n, dtype=BF, device=gpu)
+    acc = torch.empty(n, dtype=torch.int32, device=gpu)
+    xq = torch.empty(k, dtype=torch.int8, device=gpu)
+    sx = torch.empty(1, dtype=torch.float32, device=gpu)
+    xn = torch.empty(1, k, dtype=BF, device=gpu)
+    r = torch.empty(1, k, dtype=BF, device=gpu)
+    _lib.call("q35_gemv_i8", wq.data_ptr(), sw.data_ptr(), xg.data_ptr(),
+              ug.data_ptr() if prologue >= 2 else None, nwg.data_ptr() if prologue else None, 0,
+              1e-6, r.data_ptr() if prologue == 2 else None, xn.data_ptr() if prologue else None,
+              y.data_ptr(), acc.data_ptr(), xq.data_ptr(), sx.data_ptr(), n, k, prologue,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    row = _i8_row(prologue, x, u, nw)
+    got_row = x if prologue == 0 else xn.cpu()
+    if prologue:
+        close(xn, row)
+    if prologue == 2:
+        close(r, ref.residual_add_rms_norm(x, u, nw)[0])
+    exq, esx = oa.quantize_act(got_row)
+    assert np.array_equal(xq.cpu().numpy().reshape(1, -1), exq)
+    assert np.array_equal(sx.cpu().numpy().reshape(1, 1), esx)
+    ewq, esw = wq.cpu().numpy(), sw.cpu().numpy()
+    eacc = oa.int_gemm(exq, ewq)
+    assert np.array_equal(acc.cpu().numpy().reshape(1, -1), eacc)
+    assert torch.equal(y.cpu(), oa.dequant(eacc, esx, esw))
+    assert _rel(y, oa.a8w8_linear(row, ewq, esw)[0]) < 1e-2
+
+
+def test_swiglu_gemv_i8(gpu):
+    """A8W8 [gate; up] GEMV with the residual-norm prologue and SwiGLU
+    epilogue: accumulators exact for both halves, output = silu_and_mul of the
+    dequantised gate and up (bit-exact), and the wrapper's result matches."""
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 65)
+    n, k = 6144, 2048
+    w = randn(g, 2 * n, k, scale=0.02)
+    r, u, nw = randn(g, 1, k), randn(g, 1, k), randn(g, k, scale=0.02)
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    rg, ug, nwg = r.to(gpu), u.to(gpu), nw.to(gpu)
+    y = torch.empty(1, n, dtype=BF, device=gpu)
+    acc = torch.empty(2 * n, dtype=torch.int32, device=gpu)
+    xn = torch.empty(1, k, dtype=BF, device=gpu)
+    r_out = torch.empty(1, k, dtype=BF, device=gpu)
+    _lib.call("q35_swiglu_gemv_i8", wq.data_ptr(), sw.data_ptr(), rg.data_ptr(), ug.data_ptr(),
+              nwg.data_ptr(), 0, 1e-6, r_out.data_ptr(), xn.data_ptr(), y.data_ptr(), acc.data_ptr(),
+              n, k, 2, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    close(xn, ref.residual_add_rms_norm(r, u, nw)[1])
+    exq, esx = oa.quantize_act(xn.cpu())
+    eacc = oa.int_gemm(exq, wq.cpu().numpy())
+    assert np.array_equal(acc.cpu().numpy().reshape(1, -1), eacc)
+    packed = oa.dequant(eacc, esx, sw.cpu().numpy())
+    assert torch.equal(y.cpu(), ref.silu_and_mul(packed))
+    r2, y2 = K.residual_norm_linear(rg, ug, nwg, 1e-6, wq, swiglu=True, weight_scale=sw)
+    assert torch.equal(y2, y) and torch.equal(r2, r_out)
+
+
+def test_norm_linear_conv_i8(gpu):
+    """A8W8 DeltaNet input projection with the conv1d epilogue, including the
+    embedding gather of the first layer: packed output within 1 % of the
+    oracle A8W8 linear, conv output and state exactly the oracle conv of the
+    kernel's own packed output."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 66)
+    table = randn(g, 500, 2048)
+    nw = randn(g, 2048, scale=0.02)
+    w = randn(g, 8320, 2048, scale=0.02)
+    cw = randn(g, 6144, 4, scale=0.3)
+    state0 = randn(g, 1, 6144, 4)
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    ewq, esw = wq.cpu().numpy(), sw.cpu().numpy()
+    cs = state0.to(gpu)
+    tok = torch.tensor([321], dtype=torch.int64, device=gpu)
+    r, packed, qkv = K.norm_linear_conv(table.to(gpu), None, nw.to(gpu), 1e-6, wq, cw.to(gpu), cs,
+                                        token=tok, weight_scale=sw)
+    assert torch.equal(r.cpu().reshape(-1), table[321])
+    row = ref.rms_norm(table[321:322], nw)
+    assert _rel(packed.reshape(1, -1), oa.a8w8_linear(row, ewq, esw)[0]) < 1e-2
+    st = state0.clone()
+    exp = ref.causal_conv1d(packed.cpu()[..., :6144], cw, st)
+    close(qkv, exp)
+    close(cs, st)
+    # second layer form: residual + update prologue
+    res, upd = randn(g, 1, 1, 2048), randn(g, 1, 1, 2048)
+    r2, packed2, _ = K.norm_linear_conv(res.to(gpu), upd.to(gpu), nw.to(gpu), 1e-6, wq, cw.to(gpu),
+                                        cs, weight_scale=sw)
+    er, erow = ref.residual_add_rms_norm(res, upd, nw)
+    close(r2, er)
+    assert _rel(packed2.reshape(1, -1), oa.a8w8_linear(erow.reshape(1, -1), ewq, esw)[0]) < 1e-2
+
+
 # ------------------------------------------------------------------ boundary
 def test_single_hip_runtime(gpu):
     """libq35 binds to the HIP runtime torch loaded (one libamdhip64 mapped)."""
