@@ -16,6 +16,9 @@ Printed (one JSON line on stdout):
   kernels      per-kernel achieved HBM GB/s of the BASELINE configs 1-4
                (rotating >= 640 MB of distinct buffers so the 256 MB MALL does
                not serve the weights), in-graph time per launch
+  variants     the same decode and TTFT measurement for the other linear
+               variant of config 5 (A8W8 when the headline runs bf16), on the
+               same seeded weights
   cpu_baseline the CPU oracle decoder (the reference's PyTorch CPU path,
                restated) on a bounded sample, same process, host cores
 """
@@ -192,6 +195,8 @@ def main() -> None:
     ap.add_argument("--variant", choices=("bf16", "a8w8"), default="bf16")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-other-variant", action="store_true",
+                    help="skip the second (A8W8 or bf16) decode measurement")
     ap.add_argument("--cpu-decode-steps", type=int, default=8)
     ap.add_argument("--cpu-prompt", type=int, default=128, help="prompt length of the CPU sample")
     args = ap.parse_args()
@@ -210,79 +215,101 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     cfg = synth.config_2b()
-    t0 = time.perf_counter()
-    model = synth.build_model(cfg, device=dev)
-    seen = set()
-    weight_bytes = 0
-    for p in model.parameters():
-        if p.data_ptr() not in seen:
-            seen.add(p.data_ptr())
-            weight_bytes += p.numel() * p.element_size()
-    state = None if args.no_cpu else {k: v.detach().cpu() for k, v in model.state_dict().items()}
-    stats = apply_fusions(model, FusionConfig(a8w8=args.variant == "a8w8"))
-    torch.cuda.synchronize()
-    log(f"model built + fused in {time.perf_counter() - t0:.1f} s: {stats}")
-
     gen = torch.Generator().manual_seed(synth.MODEL_SEED)
     prompt_cpu = torch.randint(0, cfg.vocab_size, (1, PROMPT_LEN), generator=gen)
     prompt = prompt_cpu.to(dev)
 
-    # TTFT and the reference's decode formula through the generation loop.
-    runner = FusedGreedyGenerator(model)
-    first = runner.generate(prompt, NEW_TOKENS)  # builds cache + captures the graph
-    warm = [runner.generate(prompt, NEW_TOKENS) for _ in range(3)]
-    ttft_ms = statistics.median(r.ttft_seconds for r in warm) * 1e3
-    loop_tps = statistics.median(r.decode_tokens_per_second for r in warm)
-    assert all(r.tokens == first.tokens for r in warm), "greedy decode is not deterministic"
-    log(f"TTFT {ttft_ms:.2f} ms (cold {first.ttft_seconds * 1e3:.1f} ms); "
-        f"generate-loop decode {loop_tps:.1f} tok/s; first tokens {first.tokens[:8]}")
+    def measure(variant: str, keep_state: bool):
+        """Build the seeded 2B model with ``variant`` linears, then TTFT through
+        the generation loop and K timed decode-graph replays."""
+        t0 = time.perf_counter()
+        model = synth.build_model(cfg, device=dev)
+        seen, weight_bytes = set(), 0
+        for p in model.parameters():
+            if p.data_ptr() not in seen:
+                seen.add(p.data_ptr())
+                weight_bytes += p.numel() * p.element_size()
+        state = {k: v.detach().cpu() for k, v in model.state_dict().items()} if keep_state else None
+        stats = apply_fusions(model, FusionConfig(a8w8=variant == "a8w8"))
+        torch.cuda.synchronize()
+        log(f"[{variant}] model built + fused in {time.perf_counter() - t0:.1f} s: {stats}")
 
-    # Timed decode steps: W warmup + K timed replays of the decode graph.
-    bucket = cache_bucket(PROMPT_LEN, args.warmup + args.steps + 2)
-    from transformers.cache_utils import StaticCache
+        # TTFT and the reference's decode formula through the generation loop.
+        runner = FusedGreedyGenerator(model)
+        first = runner.generate(prompt, NEW_TOKENS)  # builds cache + captures the graph
+        warm = [runner.generate(prompt, NEW_TOKENS) for _ in range(3)]
+        ttft_ms = statistics.median(r.ttft_seconds for r in warm) * 1e3
+        loop_tps = statistics.median(r.decode_tokens_per_second for r in warm)
+        assert all(r.tokens == first.tokens for r in warm), "greedy decode is not deterministic"
+        log(f"[{variant}] TTFT {ttft_ms:.2f} ms (cold {first.ttft_seconds * 1e3:.1f} ms); "
+            f"generate-loop decode {loop_tps:.1f} tok/s; first tokens {first.tokens[:8]}")
+        del runner
 
-    with torch.inference_mode():
-        cache = StaticCache(config=model.config, max_cache_len=bucket)
-        pos = torch.arange(PROMPT_LEN, device=dev).view(1, -1)
-        out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
-        tok = lm_head_argmax(out.last_hidden_state[:, -1].contiguous(), model.lm_head.weight)
-        graph = GreedyDecodeGraph(model, cache, tok, torch.full((1, 1), PROMPT_LEN, device=dev,
-                                                                dtype=torch.long))
-        tokens = []
-        for _ in range(args.warmup):
-            tokens.append(int(graph.replay().reshape(-1)[0].item()))
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(args.steps):
-            tokens.append(int(graph.replay().reshape(-1)[0].item()))
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t1
-        # pure device time per replay (no host read between replays)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        cache.reset()
-        out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
-        graph.set_inputs(tok, torch.full((1, 1), PROMPT_LEN, device=dev, dtype=torch.long))
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(args.steps):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        replay_ms = e0.elapsed_time(e1) / args.steps
-    ms_per_step = elapsed * 1e3 / args.steps
-    value = args.steps / elapsed
-    log(f"decode: {ms_per_step:.3f} ms/token ({value:.1f} tok/s); graph replay alone {replay_ms:.3f} ms")
+        # Timed decode steps: W warmup + K timed replays of the decode graph.
+        bucket = cache_bucket(PROMPT_LEN, args.warmup + args.steps + 2)
+        from transformers.cache_utils import StaticCache
+
+        with torch.inference_mode():
+            cache = StaticCache(config=model.config, max_cache_len=bucket)
+            pos = torch.arange(PROMPT_LEN, device=dev).view(1, -1)
+            out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache,
+                              use_cache=True)
+            tok = lm_head_argmax(out.last_hidden_state[:, -1].contiguous(), model.lm_head.weight)
+            graph = GreedyDecodeGraph(model, cache, tok, torch.full((1, 1), PROMPT_LEN, device=dev,
+                                                                    dtype=torch.long))
+            for _ in range(args.warmup):
+                int(graph.replay().reshape(-1)[0].item())
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(args.steps):
+                int(graph.replay().reshape(-1)[0].item())
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - t1
+            # pure device time per replay (no host read between replays)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            cache.reset()
+            out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache,
+                              use_cache=True)
+            graph.set_inputs(tok, torch.full((1, 1), PROMPT_LEN, device=dev, dtype=torch.long))
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(args.steps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            replay_ms = e0.elapsed_time(e1) / args.steps
+            del graph, cache
+        ms_per_step = elapsed * 1e3 / args.steps
+        log(f"[{variant}] decode: {ms_per_step:.3f} ms/token ({args.steps / elapsed:.1f} tok/s); "
+            f"graph replay alone {replay_ms:.3f} ms")
+        res = {"value": round(args.steps / elapsed, 2), "ms_per_step": round(ms_per_step, 4),
+               "ttft_ms": round(ttft_ms, 3), "graph_replay_ms": round(replay_ms, 4),
+               "generate_loop_tokens_per_s": round(loop_tps, 2),
+               "weights_gb_per_token": round(weight_bytes / 1e9, 4), "cache_bucket": bucket}
+        return model, state, res
+
+    model, state, main_res = measure(args.variant, keep_state=not args.no_cpu)
+    value, ms_per_step, bucket = main_res["value"], main_res["ms_per_step"], main_res["cache_bucket"]
 
     with torch.inference_mode():
         roof = lm_head_roofline(model)
         log(f"lm_head top-1: {roof['us_per_launch']} us, {roof['achieved']} GB/s "
             f"({100 * roof['frac']:.1f}%)")
         kernels = {} if args.no_kernels else kernel_table(dev)
+    del model
+    torch.cuda.empty_cache()
+
+    # The other linear variant of BASELINE config 5 on the same weights.
+    variants = {}
+    if not args.no_other_variant:
+        other = "a8w8" if args.variant == "bf16" else "bf16"
+        m2, _, variants[other] = measure(other, keep_state=False)
+        variants[other].pop("weights_gb_per_token")  # counted before quantisation
+        del m2
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
-        del model, graph, cache, runner
-        torch.cuda.empty_cache()
         log("CPU baseline ...")
         cpu = cpu_baseline(state, cfg, prompt_cpu[:, : args.cpu_prompt], args.cpu_decode_steps)
         log(f"CPU oracle: {cpu['value']} tok/s decode, TTFT {cpu['ttft_ms']} ms on {cpu['cores']} threads")
@@ -303,10 +330,11 @@ def main() -> None:
         "config": {"workload": "Qwen3.5-2B-shaped decoder (24 layers, 18 DeltaNet + 6 GQA), "
                                f"{PROMPT_LEN}-token prefill then greedy decode, batch 1, "
                                f"{args.variant} linears", "cache_bucket": bucket},
-        "ttft_ms": round(ttft_ms, 3),
-        "graph_replay_ms": round(replay_ms, 4),
-        "generate_loop_tokens_per_s": round(loop_tps, 2),
-        "weights_gb_per_token": round(weight_bytes / 1e9, 4),
+        "ttft_ms": main_res["ttft_ms"],
+        "graph_replay_ms": main_res["graph_replay_ms"],
+        "generate_loop_tokens_per_s": main_res["generate_loop_tokens_per_s"],
+        "weights_gb_per_token": main_res["weights_gb_per_token"],
+        "variants": variants,
         "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
         "roofline_detail": roof,
         "kernels": kernels,

@@ -488,7 +488,7 @@ int dispatch(const GemvArgs& a, hipStream_t stream) {
   if (fast_ok(a, PRO)) {
     const int nch = a.K / 512;
     if constexpr (EPI == EPI_SWIGLU) {
-      if (nch == 4) { launch_fast<8, 2, 4, PRO, EPI>(a, stream); return q35_last_error(); }
+      if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI>(a, stream); return q35_last_error(); }
       if (nch == 12) { launch_fast<4, 2, 12, PRO, EPI>(a, stream); return q35_last_error(); }
     } else {
       if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI>(a, stream); return q35_last_error(); }
@@ -507,16 +507,24 @@ int dispatch(const GemvArgs& a, hipStream_t stream) {
 }
 
 // int8 weights: tiled path only (K a multiple of 1024: 1, 2, 4 or 6 chunks).
+// Tiles measured on MI355X with rotating weights in a captured graph: the
+// norm-prologue GEMVs do best with 4 rows per wave (more bytes in flight
+// behind the two workgroup reductions), the others with 2.
 template <int PRO, int EPI>
 int dispatch_i8(const GemvArgs& a, hipStream_t stream) {
   if (!fast_ok(a, PRO, true) || !a.s_w) return (int)hipErrorInvalidValue;
   const int nch = a.K / 1024;
   if constexpr (EPI == EPI_SWIGLU) {
-    if (nch == 2) { launch_fast<8, 4, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 2) { launch_fast<4, 4, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 6) { launch_fast<4, 2, 6, PRO, EPI, true>(a, stream); return q35_last_error(); }
+  } else if constexpr (PRO == PRO_RMSNORM || PRO == PRO_RESNORM) {
+    if (nch == 1) { launch_fast<4, 4, 1, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 2) { launch_fast<4, 4, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI, true>(a, stream); return q35_last_error(); }
     if (nch == 6) { launch_fast<4, 2, 6, PRO, EPI, true>(a, stream); return q35_last_error(); }
   } else {
     if (nch == 1) { launch_fast<4, 4, 1, PRO, EPI, true>(a, stream); return q35_last_error(); }
-    if (nch == 2) { launch_fast<4, 4, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (nch == 2) { launch_fast<4, 2, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
     if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI, true>(a, stream); return q35_last_error(); }
     if (nch == 6) { launch_fast<4, 2, 6, PRO, EPI, true>(a, stream); return q35_last_error(); }
   }
