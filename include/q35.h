@@ -211,8 +211,9 @@ int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int 
 /* Per-output-channel weight quantisation (int8 + fp32 scale).
  * Replaces explore_runtime_quantization.py:142-155 (PPUA8W8Linear.__init__). */
 int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, void* stream);
-/* Per-token dynamic symmetric int8 quantisation (vLLM scaled_int8_quant rule).
- * Replaces the call at explore_runtime_quantization.py:167-172. */
+/* Per-token dynamic symmetric int8 quantisation (vLLM scaled_int8_quant rule),
+ * one workgroup per row: K a multiple of 8 and at most 8192, x 16-byte and xq
+ * 8-byte aligned. Replaces the call at explore_runtime_quantization.py:167-172. */
 int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, void* stream);
 /* y[M,N] = bf16(int32(xq . Wq) * s_x[m] * s_w[n]); with x (bf16) and M == 1 the
  * activation quantisation is fused (xq/s_x optional outputs), else xq/s_x are

@@ -48,20 +48,43 @@ __global__ __launch_bounds__(256) void quant_weight_rows(const uint16_t* __restr
   if (lane == 0) scale[n] = s;
 }
 
-// One wave per token row.
+// One workgroup per token row: 16-byte loads, block absmax, then
+// q = sat(rint(x * 127/absmax)) written as 8-byte groups (K % 8 == 0).
 __global__ __launch_bounds__(256) void quant_act_rows(const uint16_t* __restrict__ x,
                                                       int8_t* __restrict__ xq,
                                                       float* __restrict__ scale, int M, int K) {
-  const int lane = threadIdx.x & 63;
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= M) return;
+  constexpr int PER = 4;  // 8-element groups per thread held in registers (K <= 8192)
+  const int m = blockIdx.x;
+  const int tid = threadIdx.x;
   const uint16_t* row = x + (size_t)m * K;
+  const int groups = K / 8;
+  __shared__ float red[4];
+  float v[PER][8];
   float mx = 0.f;
-  for (int k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(bf2f(row[k])));
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int gidx = tid + j * 256;
+    const uint4 raw = *reinterpret_cast<const uint4*>(row + (size_t)min(gidx, groups - 1) * 8);
+    unpack8(raw, v[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = gidx < groups ? fmaxf(mx, fabsf(v[j][e])) : mx;
+  }
   mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float inv = 127.0f / mx;
-  for (int k = lane; k < K; k += 64) xq[(size_t)m * K + k] = sat_i8(bf2f(row[k]) * inv);
-  if (lane == 0) scale[m] = mx / 127.0f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int gidx = tid + j * 256;
+    if (gidx < groups) {
+      uint32_t q[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[e >> 2] |= (uint32_t)(uint8_t)sat_i8(v[j][e] * inv) << (8 * (e & 3));
+      *reinterpret_cast<uint2*>(xq + (size_t)m * K + gidx * 8) = make_uint2(q[0], q[1]);
+    }
+  }
+  if (tid == 0) scale[m] = mx / 127.0f;
 }
 
 struct A8Args {
@@ -123,6 +146,100 @@ __global__ __launch_bounds__(256) void a8w8_gemv_mt(const A8Args a, int m0) {
   }
 }
 
+// One step of the halving butterfly and the rest by recursion (all indices
+// compile-time, so the values stay in registers): H values are exchanged
+// across lane bit S, or, once one value is left, plain xor-adds finish.
+template <int H, int S, int N>
+Q35_DEV void bfly_reduce(int (&acc)[N], int lane) {
+  if constexpr (S >= 1) {
+    if constexpr (H >= 1) {
+      const bool upper = (lane & S) != 0;
+#pragma unroll
+      for (int j = 0; j < H; ++j) {
+        const int send = upper ? acc[j] : acc[j + H];
+        const int keep = upper ? acc[j + H] : acc[j];
+        acc[j] = keep + __shfl_xor(send, S, 64);
+      }
+      bfly_reduce<H / 2, S / 2, N>(acc, lane);
+    } else {
+      acc[0] += __shfl_xor(acc[0], S, 64);
+      bfly_reduce<0, S / 2, N>(acc, lane);
+    }
+  }
+}
+
+// Skinny A8W8 for 2..MT tokens in one pass over the weights (K = NCH KiB).
+// The workgroup stages the MT pre-quantised rows in LDS (requested before the
+// weight stream, so both are in flight together); lane l owns bytes
+// c*1024 + 16l of each of its R rows and forms R*MT int32 partial sums with
+// v_dot4. The R*MT sums are reduced across the wave by a halving butterfly:
+// at step s (32, 16, ..., 1) each lane keeps the half of its values selected
+// by lane bit s and adds the partner's copy, so after log2(R*MT) steps lane
+// i holds value i summed over the lanes that share its high bits (remaining
+// steps add the rest) -- R*MT - 1 shuffles instead of R*MT full reductions.
+template <int R, int NCH, int MT>
+__global__ __launch_bounds__(256) void a8w8_gemv_skinny(const A8Args a) {
+  constexpr int V = R * MT;  // partial sums per lane (power of two, <= 64)
+  static_assert((V & (V - 1)) == 0 && V <= 64 && V >= 2, "R*MT must be a power of two <= 64");
+  constexpr int KV = NCH * 64;  // uint4 per activation row
+  __shared__ uint4 xs[MT * KV];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int n0 = (blockIdx.x * 4 + (tid >> 6)) * R;
+
+  // 1. activation rows (rows past M read row M-1 and are zeroed), then weights.
+  constexpr int PER = (MT * KV + 255) / 256;
+  uint4 xr[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = min(tid + j * 256, MT * KV - 1);
+    const int m = i / KV;
+    xr[j] = *reinterpret_cast<const uint4*>(a.xq + (size_t)min(m, a.M - 1) * a.K + (i - m * KV) * 16);
+  }
+  uint4 w[R][NCH];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int8_t* wrow = a.Wq + (size_t)min(n0 + r, a.N - 1) * a.K + lane * 16;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) w[r][c] = ld_stream16(wrow + c * 1024);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = tid + j * 256;
+    if (i < MT * KV) xs[i] = i / KV < a.M ? xr[j] : make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+
+  // 2. int32 partial sums, value index v = r * MT + m.
+  int acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const uint4 xv = xs[m * KV + c * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r * MT + m] = dot16_i8(w[r][c], xv, acc[r * MT + m]);
+    }
+  }
+
+  // 3. butterfly reduce-scatter over the wave (integer adds: exact).
+  bfly_reduce<V / 2, 32, V>(acc, lane);
+  // Lane l holds value index l >> (6 - log2 V).
+  constexpr int LOGV = V >= 64 ? 6 : V >= 32 ? 5 : V >= 16 ? 4 : V >= 8 ? 3 : V >= 4 ? 2 : 1;
+  if ((lane & ((1 << (6 - LOGV)) - 1)) == 0) {
+    const int v = lane >> (6 - LOGV);
+    const int r = v / MT, m = v % MT;
+    const int n = n0 + r;
+    if (n < a.N && m < a.M) {
+      const size_t o = (size_t)m * a.N + n;
+      a.y[o] = (uint16_t)f2bf((float)acc[0] * a.s_x[m] * a.s_w[n]);
+      if (a.acc_out) a.acc_out[o] = acc[0];
+    }
+  }
+}
+
 // y[m, n] = bf16((float)acc[m, n] * s_x[m] * s_w[n]); 8 outputs per thread.
 __global__ __launch_bounds__(256) void dequant_rows(const int* __restrict__ acc,
                                                     const float* __restrict__ s_x,
@@ -167,10 +284,11 @@ int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, hipS
 }
 
 int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, hipStream_t stream) {
-  Q35_CHECK_ARG(M >= 0 && K > 0);
+  // One workgroup per row holds the row in registers: K a multiple of 8, at most 8192.
+  Q35_CHECK_ARG(M >= 0 && K > 0 && K % 8 == 0 && K <= 8192);
+  Q35_CHECK_ARG(q35_aligned16(x) && q35_aligned8(xq));
   if (M == 0) return 0;
-  quant_act_rows<<<(M + 3) / 4, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale,
-                                                  M, K);
+  quant_act_rows<<<M, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale, M, K);
   return q35_last_error();
 }
 
@@ -195,6 +313,20 @@ int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void
   }
   Q35_CHECK_ARG(xq && s_x);
   a.x = nullptr;
+  // 2..16 tokens with K = 2 or 6 KiB: one pass over the weights.
+  if (M <= 16 && (K == 2048 || K == 6144) && q35_aligned16(xq)) {
+    const unsigned grid2 = (unsigned)((N + 15) / 16), grid6 = (unsigned)((N + 7) / 8);
+#define Q35_SKINNY(MT)                                                                      \
+  {                                                                                         \
+    if (K == 2048) a8w8_gemv_skinny<4, 2, MT><<<grid2, 256, 0, stream>>>(a);                \
+    else a8w8_gemv_skinny<2, 6, MT><<<grid6, 256, 0, stream>>>(a);                          \
+    return q35_last_error();                                                                \
+  }
+    if (M <= 4) Q35_SKINNY(4)
+    if (M <= 8) Q35_SKINNY(8)
+    Q35_SKINNY(16)
+#undef Q35_SKINNY
+  }
   constexpr int R = 2, MT = 4;
   const unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
   for (int m0 = 0; m0 < M; m0 += MT) {
