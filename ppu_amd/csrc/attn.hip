@@ -591,6 +591,161 @@ void launch_combine(const float* acc, const float* ml, const uint16_t* gate, uin
     gqa_decode_combine<32><<<QH, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
 }
 
+// ------------------------------------------------- causal prefill (MFMA)
+// Flash attention on the matrix cores, v_mfma_f32_16x16x32_bf16. Operand
+// layouts (wave64): A[16 x 32]: lane l holds row l%16, 8 consecutive k at
+// 8*(l/16); B[32 x 16]: lane l holds column l%16, the same 8 k; C[16 x 16]:
+// lane l holds rows 4*(l/16) + i (i = 0..3) of column l%16.
+// Grid (query tiles of 16 rows, KVH, B); the G waves of a workgroup are the G
+// query heads of one KV head over the same 16 rows, so they share the K rows
+// (L1) and the V tile (LDS). Per 32-key iteration and wave:
+//   S = Q K^T: Q (A operand, rows x dims) stays in registers, K rows are the
+//     B operand in their natural layout (16 contiguous bytes per lane);
+//   online softmax on the C layout (row max / sum over the 16 lanes of a DPP
+//     row), scale and causal mask applied to S in fp32;
+//   O += P V: P is split into bf16 hi + lo parts (p - hi rounded again, so P
+//     keeps ~16 mantissa bits: two MFMAs instead of the one of a plain bf16 P)
+//     and moved through a wave-private LDS tile into the A layout; V is staged
+//     transposed in LDS (double-buffered, one barrier per iteration) so the
+//     B operand is again 16 contiguous bytes per lane.
+// Keys past the valid end are masked to -inf and their V rows staged as
+// zeros (the cache beyond the prompt may hold any bits).
+typedef __bf16 q35_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
+
+Q35_DEV q35_f32x4 mfma_16x16x32(const uint4 a, const uint4 b, q35_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(q35_bf16x8, a),
+                                                 __builtin_bit_cast(q35_bf16x8, b), c, 0, 0, 0);
+}
+
+constexpr int kVtStride = 40;  // bf16 per transposed V row: 32 keys + pad
+constexpr int kPStride = 40;   // bf16 per P row: 32 keys + pad
+
+template <int G>
+__global__ __launch_bounds__(G * 64) void gqa_prefill_mfma(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
+    uint16_t* __restrict__ out, int B, int QH, int KVH, int L, int cache_len, int kv_start_host,
+    const long long* __restrict__ valid_len, float scale) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int tile = gridDim.x - 1 - blockIdx.x;  // heavy (late) tiles first
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int h = kvh * G + wid;
+  const int q0 = tile * 16;
+  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  if (ks < 0) ks = 0;
+  if (ks + L > cache_len) ks = cache_len - L;
+  const int kv_start = (int)ks;
+  const int col = lane & 15;  // A row / B column / C column
+  const int kg = lane >> 4;   // k group of 8 / C row group of 4
+
+  // Q operand: row q0 + col (clamped), dims 8*kg + 32t.
+  const uint16_t* qp = q + (((size_t)b * QH + h) * L + min(q0 + col, L - 1)) * kAD + kg * 8;
+  uint4 qa[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) qa[t] = *reinterpret_cast<const uint4*>(qp + 32 * t);
+  int row_abs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) row_abs[i] = kv_start + min(q0 + 4 * kg + i, L - 1);
+  const int n_keys = min(kv_start + min(q0 + 16, L), cache_len);
+  const uint16_t* Kh = Kc + ((size_t)b * KVH + kvh) * cache_len * kAD;
+  const uint16_t* Vh = Vc + ((size_t)b * KVH + kvh) * cache_len * kAD;
+
+  __shared__ alignas(16) uint16_t vt_s[2][kAD * kVtStride];
+  __shared__ alignas(16) uint16_t p_s[G][2][16 * kPStride];
+  q35_f32x4 o[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) o[d] = {0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+  }
+  const int nblk = (n_keys + 31) / 32;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kb = blk * 32;
+    uint16_t* vt = vt_s[blk & 1];
+    // K operand of the two 16-key blocks: key kb + 16*sb + col, dims 8*kg + 32t.
+    uint4 kv[2][8];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const uint16_t* kr = Kh + (size_t)min(kb + 16 * sb + col, n_keys - 1) * kAD + kg * 8;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) kv[sb][t] = *reinterpret_cast<const uint4*>(kr + 32 * t);
+    }
+    // Stage V^T: (key, 8-dim group) pairs, vt[dim][key].
+    for (int pi = threadIdx.x; pi < 32 * (kAD / 8); pi += G * 64) {
+      const int k = pi & 31, dg = pi >> 5;
+      const int key = kb + k;
+      uint4 v = *reinterpret_cast<const uint4*>(Vh + (size_t)min(key, n_keys - 1) * kAD + dg * 8);
+      if (key >= n_keys) v = make_uint4(0, 0, 0, 0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[(dg * 8 + 2 * e) * kVtStride + k] = (uint16_t)(w[e] & 0xffffu);
+        vt[(dg * 8 + 2 * e + 1) * kVtStride + k] = (uint16_t)(w[e] >> 16);
+      }
+    }
+    // S = Q K^T, then scale, causal mask and online softmax per row.
+    q35_f32x4 s[2];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      s[sb] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) s[sb] = mfma_16x16x32(qa[t], kv[sb][t], s[sb]);
+    }
+    float corr[4];
+    uint16_t* ps_hi = p_s[wid][0];
+    uint16_t* ps_lo = p_s[wid][1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sv[2];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int key = kb + 16 * sb + col;
+        sv[sb] = (key <= row_abs[i] && key < n_keys) ? s[sb][i] * scale : -INFINITY;
+      }
+      const float m_new = fmaxf(m[i], row16_max(fmaxf(sv[0], sv[1])));
+      // A row without any valid key so far keeps m = -inf: subtract 0 then.
+      const float m_sub = m_new == -INFINITY ? 0.f : m_new;
+      corr[i] = expf(m[i] - m_sub);
+      const float p0 = expf(sv[0] - m_sub), p1 = expf(sv[1] - m_sub);
+      l[i] = l[i] * corr[i] + row16_sum(p0 + p1);
+      m[i] = m_new;
+      const uint32_t h0 = f2bf(p0), h1 = f2bf(p1);
+      ps_hi[(4 * kg + i) * kPStride + col] = (uint16_t)h0;
+      ps_hi[(4 * kg + i) * kPStride + 16 + col] = (uint16_t)h1;
+      ps_lo[(4 * kg + i) * kPStride + col] = (uint16_t)f2bf(p0 - bf2f(h0));
+      ps_lo[(4 * kg + i) * kPStride + 16 + col] = (uint16_t)f2bf(p1 - bf2f(h1));
+    }
+    __syncthreads();  // V^T staged by every wave; this wave's P tile written
+    // O += P V: A = P rows x keys (row col, keys 8*kg..), B = V^T (dims x keys).
+    const uint4 pa_hi = *reinterpret_cast<const uint4*>(ps_hi + col * kPStride + kg * 8);
+    const uint4 pa_lo = *reinterpret_cast<const uint4*>(ps_lo + col * kPStride + kg * 8);
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[d][i] *= corr[i];
+      const uint4 vb = *reinterpret_cast<const uint4*>(vt + (d * 16 + col) * kVtStride + kg * 8);
+      o[d] = mfma_16x16x32(pa_hi, vb, o[d]);
+      o[d] = mfma_16x16x32(pa_lo, vb, o[d]);
+    }
+  }
+  // out[b, row, h*D + 16d + col] = bf16(O / l) for the valid rows.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = q0 + 4 * kg + i;
+    if (r < L) {
+      const float inv = 1.0f / l[i];
+      uint16_t* orow = out + ((size_t)b * L + r) * QH * kAD + h * kAD + col;
+#pragma unroll
+      for (int d = 0; d < 16; ++d) orow[16 * d] = (uint16_t)f2bf(o[d][i] * inv);
+    }
+  }
+}
+
 // ---------------------------------------------------------- causal prefill
 // q [B, QH, L, D], K/V [B, KVH, cache_len, D] (the prompt at cache offset
 // kv_start), out [B, L, QH*D]. Query row i of a head attends to keys
@@ -810,8 +965,23 @@ int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int 
   Q35_CHECK_ARG(D == kAD && KVH > 0 && QH % KVH == 0 && B >= 0 && L >= 0);
   Q35_CHECK_ARG(L <= cache_len && (valid_len || (kv_start >= 0 && kv_start + L <= cache_len)));
   Q35_CHECK_ARG(q35_aligned16(q) && q35_aligned16(K) && q35_aligned16(V) && q35_aligned16(out));
+  if ((long long)B * QH * L == 0) return 0;
+  const int G = QH / KVH;
+  if ((G == 1 || G == 2 || G == 4 || G == 8) && B < 65536 && KVH < 65536) {
+    dim3 grid((unsigned)((L + 15) / 16), (unsigned)KVH, (unsigned)B);
+#define Q35_PF(GG)                                                                                  \
+  gqa_prefill_mfma<GG><<<grid, GG * 64, 0, stream>>>((const uint16_t*)q, (const uint16_t*)K,       \
+                                                     (const uint16_t*)V, (uint16_t*)out, B, QH, KVH, \
+                                                     L, cache_len, kv_start,                       \
+                                                     (const long long*)valid_len, scale)
+    if (G == 1) Q35_PF(1);
+    else if (G == 2) Q35_PF(2);
+    else if (G == 4) Q35_PF(4);
+    else Q35_PF(8);
+#undef Q35_PF
+    return q35_last_error();
+  }
   const long long waves = (long long)B * QH * L;
-  if (waves == 0) return 0;
   Q35_CHECK_ARG(waves < (1ll << 31));
   gqa_prefill_rows<<<(unsigned)((waves + 3) / 4), 256, 0, stream>>>(
       (const uint16_t*)q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)out, B, QH, KVH, L,

@@ -93,6 +93,15 @@ Q35_DEV float row16_sum(float v) {
   return v;
 }
 
+// Max over the 16 lanes of a DPP row (same exchange pattern as row16_sum).
+Q35_DEV float row16_max(float v) {
+  v = fmaxf(v, dpp_f<Q35_DPP_QUAD_XOR1>(v));
+  v = fmaxf(v, dpp_f<Q35_DPP_QUAD_XOR2>(v));
+  v = fmaxf(v, dpp_f<Q35_DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f<Q35_DPP_ROW_MIRROR>(v));
+  return v;
+}
+
 // Sum over the whole wave64; the result is wave-uniform.
 Q35_DEV float wave_sum(float v) {
   v = row16_sum(v);

@@ -378,8 +378,11 @@ def test_gqa_decode_gate_fused(gpu):
     close(got, exp)
 
 
-@pytest.mark.parametrize("seq_len,kv_start", [(33, 0), (64, 16)])
+@pytest.mark.parametrize("seq_len,kv_start", [(33, 0), (64, 16), (1, 0), (100, 37), (1024, 0)])
 def test_prefill_attention(gpu, seq_len, kv_start):
+    """Causal GQA prefill (MFMA flash attention, P as bf16 hi + lo parts)
+    against the fp64 oracle, rtol 1e-2 / atol 1e-3 on the bf16 output. Cache
+    rows past the prompt hold NaN, which must not reach the output."""
     from ppu_amd import kernels as K
 
     g = gen(KERNEL_SEED + 19)
@@ -387,7 +390,27 @@ def test_prefill_attention(gpu, seq_len, kv_start):
     kc = randn(g, 1, 2, kv_start + seq_len + 5, 256)
     vc = randn(g, 1, 2, kv_start + seq_len + 5, 256)
     exp = ref.prefill_attention(q, kc, vc, 0.0625, kv_start)
-    got = K.gqa_prefill_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), 0.0625, kv_start=kv_start)
+    kg, vg = kc.to(gpu), vc.to(gpu)
+    kg[:, :, kv_start + seq_len:] = float("nan")
+    vg[:, :, kv_start + seq_len:] = float("nan")
+    got = K.gqa_prefill_attention(q.to(gpu), kg, vg, 0.0625, kv_start=kv_start)
+    close(got, exp)
+
+
+@pytest.mark.parametrize("q_heads,kv_heads", [(2, 2), (8, 1), (4, 2)])
+def test_prefill_attention_groupings(gpu, q_heads, kv_heads):
+    """Head groupings G = 1, 8, 2 and the device-length form (start = valid
+    length - L, as the static-cache prefill passes it)."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 23)
+    seq_len, start = 77, 20
+    q = randn(g, 1, q_heads, seq_len, 256)
+    kc = randn(g, 1, kv_heads, 128, 256)
+    vc = randn(g, 1, kv_heads, 128, 256)
+    exp = ref.prefill_attention(q, kc, vc, 0.0625, start)
+    valid = torch.tensor(start + seq_len, dtype=torch.int64, device=gpu)
+    got = K.gqa_prefill_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), 0.0625, valid_length=valid)
     close(got, exp)
 
 
