@@ -610,9 +610,6 @@ void launch_combine(const float* acc, const float* ml, const uint16_t* gate, uin
 //     B operand is again 16 contiguous bytes per lane.
 // Keys past the valid end are masked to -inf and their V rows staged as
 // zeros (the cache beyond the prompt may hold any bits).
-typedef __bf16 q35_bf16x8 __attribute__((ext_vector_type(8)));
-typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
-
 Q35_DEV q35_f32x4 mfma_16x16x32(const uint4 a, const uint4 b, q35_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(q35_bf16x8, a),
                                                  __builtin_bit_cast(q35_bf16x8, b), c, 0, 0, 0);

@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256) void delta_decode_tiled(const DeltaArgs p) {
 }
 
 // ------------------------------------------------------------- prefill scan
-// Per (token, head) scalars (q_inv, k_inv, alpha, beta) [reference kernels.py:713-765].
+// Per (token, head) scalars (q_inv, k_inv, g = log alpha, beta) [reference kernels.py:713-765].
 __global__ __launch_bounds__(256) void delta_factors(const uint16_t* __restrict__ qkv, int qkv_stride,
                                                      const uint16_t* __restrict__ packed,
                                                      int packed_stride, const void* a_log,
@@ -321,9 +321,11 @@ __global__ __launch_bounds__(256) void delta_factors(const uint16_t* __restrict_
   if (lane == 0) {
     const uint16_t* prow = packed + (size_t)tf * packed_stride;
     const float a = bf2f(prow[a_off + h]) + ld_param(dt_bias, h, params_f32);
-    const float alpha = expf(-expf(ld_param(a_log, h, params_f32)) * softplus20(a));
+    // g = log(alpha); the scan applies alpha = exp(g), the value the
+    // reference computes.
+    const float g = -expf(ld_param(a_log, h, params_f32)) * softplus20(a);
     const float beta = 1.0f / (1.0f + expf(-bf2f(prow[b_off + h])));
-    float4 f = make_float4(rsqrt_cr(qs + 1e-6f), rsqrt_cr(ks + 1e-6f), alpha, beta);
+    float4 f = make_float4(rsqrt_cr(qs + 1e-6f), rsqrt_cr(ks + 1e-6f), g, beta);
     *reinterpret_cast<float4*>(factors + (size_t)r * 4) = f;
   }
 }
@@ -331,9 +333,13 @@ __global__ __launch_bounds__(256) void delta_factors(const uint16_t* __restrict_
 // Sequential scan over L tokens. One wave per (batch, head, 8-column v tile);
 // lane = (v pair vp = lane/16, k-group kg = lane%16 of 8 rows), so the
 // [128 x 8] fp32 state tile lives in registers (16 per lane) for the whole
-// sequence and every reduction over k is a 16-lane DPP row sum. The next
-// token's q, k, v and factors are loaded one step ahead, so the loop runs at
-// the latency of its arithmetic chain, not of memory.
+// sequence and every reduction over k is a 16-lane DPP row sum. Tokens are
+// processed in groups of kScanAhead; the next group's inputs (q, k, v,
+// factors) are requested before the current group is processed, so the loop
+// runs at the latency of its arithmetic chain, not of memory. Steps past L
+// read the last token and are no-ops (alpha = 1, beta = 0, no store).
+constexpr int kScanAhead = 8;
+
 struct ScanIn {
   uint4 q, k;
   uint32_t v;
@@ -371,50 +377,374 @@ __global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qk
     s[i][0] = t2.x; s[i][1] = t2.y;
   }
   const float qscale = 0.08838834764831845f;
-  ScanIn nxt = scan_load(qkv, qkv_stride, factors, b, L, H, h, 0, kg, v0);
-  for (int t = 0; t < L; ++t) {
-    const ScanIn cur = nxt;
-    if (t + 1 < L) nxt = scan_load(qkv, qkv_stride, factors, b, L, H, h, t + 1, kg, v0);
-    float q[8], k[8];
-    unpack8(cur.q, q);
-    unpack8(cur.k, k);
-    const float4 f = cur.f;
-    float ma0 = 0.f, ma1 = 0.f, mb0 = 0.f, mb1 = 0.f;
+  ScanIn cur[kScanAhead];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      k[i] *= f.y;
-      q[i] = q[i] * f.x * qscale;
-      s[i][0] *= f.z; s[i][1] *= f.z;
+  for (int j = 0; j < kScanAhead; ++j)
+    cur[j] = scan_load(qkv, qkv_stride, factors, b, L, H, h, min(j, L - 1), kg, v0);
+  for (int t0 = 0; t0 < L; t0 += kScanAhead) {
+    // The next group's inputs are all requested before this group is
+    // processed, so they have landed by the copy at the end of the group.
+    ScanIn nxt[kScanAhead];
+#pragma unroll
+    for (int j = 0; j < kScanAhead; ++j)
+      nxt[j] = scan_load(qkv, qkv_stride, factors, b, L, H, h, min(t0 + kScanAhead + j, L - 1),
+                         kg, v0);
+#pragma unroll
+    for (int j = 0; j < kScanAhead; ++j) {
+      const int t = t0 + j;
+      const ScanIn in = cur[j];
+      const bool live = t < L;
+      float q[8], k[8];
+      unpack8(in.q, q);
+      unpack8(in.k, k);
+      const float4 f = in.f;
+      const float alpha = live ? expf(f.z) : 1.0f;
+      const float beta = live ? f.w : 0.0f;
+      float ma0 = 0.f, ma1 = 0.f, mb0 = 0.f, mb1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        k[i] *= f.y;
+        q[i] = q[i] * f.x * qscale;
+        s[i][0] *= alpha; s[i][1] *= alpha;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ma0 = fmaf(s[i][0], k[i], ma0);
+        ma1 = fmaf(s[i][1], k[i], ma1);
+        mb0 = fmaf(s[i + 4][0], k[i + 4], mb0);
+        mb1 = fmaf(s[i + 4][1], k[i + 4], mb1);
+      }
+      const float m0 = row16_sum(ma0 + mb0), m1 = row16_sum(ma1 + mb1);
+      const float d0 = beta * (bf_lo(in.v) - m0), d1 = beta * (bf_hi(in.v) - m1);
+      float oa0 = 0.f, oa1 = 0.f, ob0 = 0.f, ob1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        s[i][0] += k[i] * d0;
+        s[i][1] += k[i] * d1;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        oa0 = fmaf(s[i][0], q[i], oa0);
+        oa1 = fmaf(s[i][1], q[i], oa1);
+        ob0 = fmaf(s[i + 4][0], q[i + 4], ob0);
+        ob1 = fmaf(s[i + 4][1], q[i + 4], ob1);
+      }
+      const float o0 = row16_sum(oa0 + ob0), o1 = row16_sum(oa1 + ob1);
+      if (live && kg == 0)
+        *reinterpret_cast<uint32_t*>(out + (((size_t)b * L + t) * H + h) * kD + v0) = pack_bf2(o0, o1);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ma0 = fmaf(s[i][0], k[i], ma0);
-      ma1 = fmaf(s[i][1], k[i], ma1);
-      mb0 = fmaf(s[i + 4][0], k[i + 4], mb0);
-      mb1 = fmaf(s[i + 4][1], k[i + 4], mb1);
-    }
-    const float m0 = row16_sum(ma0 + mb0), m1 = row16_sum(ma1 + mb1);
-    const float d0 = f.w * (bf_lo(cur.v) - m0), d1 = f.w * (bf_hi(cur.v) - m1);
-    float oa0 = 0.f, oa1 = 0.f, ob0 = 0.f, ob1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      s[i][0] += k[i] * d0;
-      s[i][1] += k[i] * d1;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      oa0 = fmaf(s[i][0], q[i], oa0);
-      oa1 = fmaf(s[i][1], q[i], oa1);
-      ob0 = fmaf(s[i + 4][0], q[i + 4], ob0);
-      ob1 = fmaf(s[i + 4][1], q[i + 4], ob1);
-    }
-    const float o0 = row16_sum(oa0 + ob0), o1 = row16_sum(oa1 + ob1);
-    if (kg == 0)
-      *reinterpret_cast<uint32_t*>(out + (((size_t)b * L + t) * H + h) * kD + v0) = pack_bf2(o0, o1);
+    for (int j = 0; j < kScanAhead; ++j) cur[j] = nxt[j];
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     *reinterpret_cast<float2*>(S + (size_t)(kg * 8 + i) * kD + v0) = make_float2(s[i][0], s[i][1]);
+}
+
+// ------------------------------------------------------- chunked prefill
+// The recurrence over a chunk of C = 64 tokens in closed form (the UT / WY
+// representation of the delta rule), so that the sequential dependence is
+// over L/64 chunks instead of L tokens and the work is matrix products on
+// the fp32 matrix cores (v_mfma_f32_16x16x4f32). Per head, with k and q the
+// scaled vectors of the recurrence (k*k_inv, q*q_inv/sqrt(D)), G_i the
+// cumulative log-decay inside the chunk and gamma_i = e^{G_i}:
+//   A[i][j] = beta_i e^{G_i-G_j} (k_i . k_j)  (j < i),   T = (I + A)^{-1}
+//   W = T diag(beta gamma) K,   U0 = T diag(beta) V      (independent of S)
+//   U = U0 - W S                                           (the delta vectors)
+//   O = diag(gamma) Q S + P U,  P[i][j] = e^{G_i-G_j} (q_i . k_j)  (j <= i)
+//   S <- gamma_C S + K''^T U,   K''[j] = e^{G_C-G_j} k_j
+// which is the token loop unrolled exactly (every decay factor is e^{a-b}
+// with a <= b, so nothing overflows). Padding tokens past L carry k = q = v =
+// 0, g = 0, beta = 0 and leave S unchanged.
+//   delta_chunk_prep : one workgroup per (chunk, head): A and P from K K^T and
+//     K Q^T, T by forward substitution (one wave, lane = column), W^T and U0,
+//     and Q' = diag(gamma) Q, K''^T, all written in the per-lane order of the
+//     MFMA operands that delta_chunk_scan consumes (coalesced float4 loads).
+//   delta_chunk_scan : one workgroup per (16-column v tile, head): the
+//     [128 x 16] state tile in LDS, the three chunk products per chunk.
+// MFMA 16x16x4 f32 (wave64): A[16x4]: lane l holds row l%16, k l/16;
+// B[4x16]: k l/16, column l%16; C: rows 4*(l/16) + e, column l%16.
+constexpr int kChunk = 64;
+constexpr int kCS = 132;  // fp32 row stride of the K / Q / V chunk tiles in LDS
+constexpr int kAS = 68;   // fp32 row stride of A, then T
+constexpr int kSS = 17;   // fp32 row stride of the state and U tiles in LDS
+// Workspace floats per (batch, head, chunk): W^T, Q', K''^T, P, U0.
+constexpr int kOffWT = 0, kOffQP = 8192, kOffKT = 16384, kOffPQ = 24576, kOffU0 = 28672;
+constexpr int kChunkFloats = 36864;
+
+Q35_DEV q35_f32x4 mfma4(float a, float b, q35_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restrict__ qkv,
+                                                        int qkv_stride,
+                                                        const float* __restrict__ factors,
+                                                        float* __restrict__ ws,
+                                                        float* __restrict__ gc_out, int L, int H,
+                                                        int nC) {
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int col = lane & 15, g4 = lane >> 4;
+  const size_t bhc = ((size_t)b * H + h) * nC + c;
+  __shared__ alignas(16) float Kh[kChunk * kCS];
+  __shared__ alignas(16) float Qh[kChunk * kCS];
+  __shared__ alignas(16) float Vv[kChunk * kCS];
+  __shared__ alignas(16) float Am[kChunk * kAS];
+  __shared__ float G_s[kChunk], gam_s[kChunk], kf_s[kChunk], bg_s[kChunk], b_s[kChunk];
+
+  // 1. the chunk's k, q (scaled as the recurrence scales them) and v in fp32.
+  {
+    const int i = tid >> 2, qq = tid & 3;  // token, 32-dim quarter
+    const int t = c * kChunk + i;
+    const bool live = t < L;
+    const int tc = min(t, L - 1);
+    const uint16_t* row = qkv + ((size_t)b * L + tc) * qkv_stride;
+    const float4 f = *reinterpret_cast<const float4*>(factors + (((size_t)b * L + tc) * H + h) * 4);
+    const float qscale = 0.08838834764831845f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int d = qq * 32 + u * 8;
+      float fq[8], fk[8], fv[8];
+      unpack8(*reinterpret_cast<const uint4*>(row + h * kD + d), fq);
+      unpack8(*reinterpret_cast<const uint4*>(row + H * kD + h * kD + d), fk);
+      unpack8(*reinterpret_cast<const uint4*>(row + 2 * H * kD + h * kD + d), fv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fq[e] = live ? fq[e] * f.x * qscale : 0.f;
+        fk[e] = live ? fk[e] * f.y : 0.f;
+        fv[e] = live ? fv[e] : 0.f;
+      }
+      float* qd = &Qh[i * kCS + d];
+      float* kd = &Kh[i * kCS + d];
+      float* vd = &Vv[i * kCS + d];
+      *reinterpret_cast<float4*>(qd) = make_float4(fq[0], fq[1], fq[2], fq[3]);
+      *reinterpret_cast<float4*>(qd + 4) = make_float4(fq[4], fq[5], fq[6], fq[7]);
+      *reinterpret_cast<float4*>(kd) = make_float4(fk[0], fk[1], fk[2], fk[3]);
+      *reinterpret_cast<float4*>(kd + 4) = make_float4(fk[4], fk[5], fk[6], fk[7]);
+      *reinterpret_cast<float4*>(vd) = make_float4(fv[0], fv[1], fv[2], fv[3]);
+      *reinterpret_cast<float4*>(vd + 4) = make_float4(fv[4], fv[5], fv[6], fv[7]);
+    }
+    if (qq == 0) {
+      G_s[i] = live ? f.z : 0.f;  // g = log alpha, summed below
+      b_s[i] = live ? f.w : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // 2. cumulative log-decay G (inclusive scan over the chunk, wave 0).
+  if (wid == 0) {
+    float gs = G_s[lane];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float up = __shfl_up(gs, o, 64);
+      if (lane >= o) gs += up;
+    }
+    const float glast = __shfl(gs, 63, 64);
+    G_s[lane] = gs;
+    gam_s[lane] = expf(gs);
+    kf_s[lane] = expf(glast - gs);
+    bg_s[lane] = b_s[lane] * expf(gs);
+    if (lane == 0) gc_out[bhc] = expf(glast);
+  }
+  __syncthreads();
+
+  float* wsb = ws + bhc * kChunkFloats;
+  // 3. A (into LDS) and P (to the workspace) for the lower block triangle:
+  //    wave w owns the 16 rows of row tile w.
+  {
+    const int rt = wid;
+    for (int jt = 0; jt <= rt; ++jt) {
+      q35_f32x4 kk = {0.f, 0.f, 0.f, 0.f}, kq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int s = 0; s < 32; ++s) {
+        const int d = 4 * s + g4;
+        const float k_i = Kh[(16 * rt + col) * kCS + d];
+        const float k_j = Kh[(16 * jt + col) * kCS + d];
+        const float q_i = Qh[(16 * rt + col) * kCS + d];
+        kk = mfma4(k_i, k_j, kk);  // (K K^T)[i][j]
+        kq = mfma4(k_j, q_i, kq);  // (K Q^T)[j][i]
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * rt + 4 * g4 + e, j = 16 * jt + col;
+        Am[i * kAS + j] = j < i ? b_s[i] * expf(G_s[i] - G_s[j]) * kk[e] : 0.f;
+      }
+      float4 pq;
+      {
+        const int i = 16 * rt + col;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 16 * jt + 4 * g4 + e;
+          v[e] = j <= i ? expf(G_s[i] - G_s[j]) * kq[e] : 0.f;
+        }
+        pq = make_float4(v[0], v[1], v[2], v[3]);
+      }
+      *reinterpret_cast<float4*>(wsb + kOffPQ + ((rt * 4 + jt) * 64 + lane) * 4) = pq;
+    }
+  }
+  __syncthreads();
+
+  // 4. T = (I + A)^{-1}: forward substitution, lane = column, T column in
+  //    registers; A rows are broadcast LDS reads. T overwrites A.
+  if (wid == 0) {
+    float t[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+      for (int j = 0; j + 3 < i; j += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(&Am[i * kAS + j]);
+        a0 = fmaf(a.x, t[j], a0);
+        a1 = fmaf(a.y, t[j + 1], a1);
+        a2 = fmaf(a.z, t[j + 2], a2);
+        a3 = fmaf(a.w, t[j + 3], a3);
+      }
+#pragma unroll
+      for (int j = i & ~3; j < i; ++j) a0 = fmaf(Am[i * kAS + j], t[j], a0);
+      t[i] = (lane == i ? 1.f : 0.f) - ((a0 + a1) + (a2 + a3));
+    }
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) Am[i * kAS + lane] = t[i];
+  }
+  __syncthreads();
+
+  // 5. W^T = K^T diag(beta gamma) T^T and U0 = T diag(beta) V on the matrix
+  //    cores (row tile rt = wave), Q' and K''^T elementwise.
+  {
+    const int rt = wid;
+    for (int dt = 0; dt < 8; ++dt) {
+      q35_f32x4 w = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int s = 0; s < 16; ++s) {
+        const int j = 4 * s + g4;
+        const float tij = Am[(16 * rt + col) * kAS + j];
+        w = mfma4(bg_s[j] * Kh[j * kCS + 16 * dt + col], tij, w);
+        u = mfma4(tij, b_s[j] * Vv[j * kCS + 16 * dt + col], u);
+      }
+      *reinterpret_cast<float4*>(wsb + kOffWT + ((rt * 8 + dt) * 64 + lane) * 4) =
+          make_float4(w[0], w[1], w[2], w[3]);
+      *reinterpret_cast<float4*>(wsb + kOffU0 + ((rt * 8 + dt) * 64 + lane) * 4) =
+          make_float4(u[0], u[1], u[2], u[3]);
+      const int i = 16 * rt + col;
+      const float gi = gam_s[i];
+      const float* qrow = &Qh[i * kCS + 16 * dt + 4 * g4];
+      *reinterpret_cast<float4*>(wsb + kOffQP + ((rt * 8 + dt) * 64 + lane) * 4) =
+          make_float4(qrow[0] * gi, qrow[1] * gi, qrow[2] * gi, qrow[3] * gi);
+    }
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+      const int dt = 2 * wid + dd;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * (4 * s4 + e) + g4;
+          v[e] = kf_s[j] * Kh[j * kCS + 16 * dt + col];
+        }
+        *reinterpret_cast<float4*>(wsb + kOffKT + ((dt * 4 + s4) * 64 + lane) * 4) =
+            make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict__ ws,
+                                                        const float* __restrict__ gc,
+                                                        float* __restrict__ state,
+                                                        uint16_t* __restrict__ out, int L, int H,
+                                                        int nC) {
+  const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int col = lane & 15, g4 = lane >> 4;
+  const size_t bh = (size_t)b * H + h;
+  __shared__ float S_s[kD * kSS];
+  __shared__ float U_s[kChunk * kSS];
+  float* Sg = state + bh * kD * kD + tile * 16;
+  for (int idx = tid; idx < kD * 16; idx += 256) S_s[(idx >> 4) * kSS + (idx & 15)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
+  __syncthreads();
+  for (int c = 0; c < nC; ++c) {
+    const float* wsb = ws + (bh * nC + c) * kChunkFloats;
+    // This wave's operands: row tile wid of W^T, Q', P and U0, dk tiles
+    // 2*wid and 2*wid+1 of K''^T.
+    float4 wt[8], qp[8], pq[4], kt[2][4];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      wt[dt] = *reinterpret_cast<const float4*>(wsb + kOffWT + ((wid * 8 + dt) * 64 + lane) * 4);
+      qp[dt] = *reinterpret_cast<const float4*>(wsb + kOffQP + ((wid * 8 + dt) * 64 + lane) * 4);
+    }
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+      pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        kt[dd][s4] = *reinterpret_cast<const float4*>(wsb + kOffKT + (((2 * wid + dd) * 4 + s4) * 64 + lane) * 4);
+    const float4 u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
+    const float gC = gc[bh * nC + c];
+
+    // U = U0 - W S (rows 16*wid.., this v tile)
+    q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const float a[4] = {wt[dt].x, wt[dt].y, wt[dt].z, wt[dt].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = mfma4(a[e], S_s[(16 * dt + 4 * g4 + e) * kSS + col], acc);
+    }
+    const float uo[4] = {u0.x - acc[0], u0.y - acc[1], u0.z - acc[2], u0.w - acc[3]};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) U_s[(16 * wid + 4 * g4 + e) * kSS + col] = uo[e];
+    __syncthreads();
+
+    // O = Q' S + P U
+    q35_f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const float a[4] = {qp[dt].x, qp[dt].y, qp[dt].z, qp[dt].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o = mfma4(a[e], S_s[(16 * dt + 4 * g4 + e) * kSS + col], o);
+    }
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      if (jt <= wid) {
+        const float a[4] = {pq[jt].x, pq[jt].y, pq[jt].z, pq[jt].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o = mfma4(a[e], U_s[(16 * jt + 4 * g4 + e) * kSS + col], o);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = c * kChunk + 16 * wid + 4 * g4 + e;
+      if (t < L) out[(((size_t)b * L + t) * H + h) * kD + tile * 16 + col] = (uint16_t)f2bf(o[e]);
+    }
+
+    // S <- gamma_C S + K''^T U (dk tiles 2*wid, 2*wid + 1)
+    q35_f32x4 sn[2];
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+      const int dt = 2 * wid + dd;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sn[dd][e] = gC * S_s[(16 * dt + 4 * g4 + e) * kSS + col];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const float a[4] = {kt[dd][s4].x, kt[dd][s4].y, kt[dd][s4].z, kt[dd][s4].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          sn[dd] = mfma4(a[e], U_s[(4 * (4 * s4 + e) + g4) * kSS + col], sn[dd]);
+      }
+    }
+    __syncthreads();  // every wave has read S and U of this chunk
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S_s[(16 * (2 * wid + dd) + 4 * g4 + e) * kSS + col] = sn[dd][e];
+    __syncthreads();
+  }
+  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = S_s[(idx >> 4) * kSS + (idx & 15)];
 }
 
 }  // namespace
@@ -488,8 +818,16 @@ int q35_delta_decode(const void* src, int src_stride, const void* packed, int pa
   return q35_last_error();
 }
 
-// Floats of workspace q35_delta_prefill needs: 4 per (batch, token, head).
-long long q35_delta_prefill_workspace(int B, int L, int H) { return 4ll * B * L * H; }
+// Prefill runs the chunked form for L >= 64 tokens, the token scan below that.
+constexpr int kChunkMinL = 64;
+
+// Floats of workspace q35_delta_prefill needs: 4 factors per (batch, token,
+// head), and for the chunked form 36864 floats + 1 per (batch, head, chunk).
+long long q35_delta_prefill_workspace(int B, int L, int H) {
+  long long n = 4ll * B * L * H;
+  if (L >= kChunkMinL) n += (long long)B * H * ((L + kChunk - 1) / kChunk) * (kChunkFloats + 1);
+  return n;
+}
 
 // Sequential recurrence over L tokens (input: post-conv qkv), state in place.
 int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
@@ -509,8 +847,23 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
       params_f32, (float*)workspace, (int)rows, H, 4 * H * D, 4 * H * D + H);
   int e = q35_last_error();
   if (e) return e;
-  delta_scan<<<(unsigned)(B * H * (kD / 8)), 64, 0, stream>>>(
-      (const uint16_t*)qkv, qkv_stride, (const float*)workspace, (float*)state, (uint16_t*)out, L, H);
+  if (L < kChunkMinL) {
+    delta_scan<<<(unsigned)(B * H * (kD / 8)), 64, 0, stream>>>(
+        (const uint16_t*)qkv, qkv_stride, (const float*)workspace, (float*)state, (uint16_t*)out, L,
+        H);
+    return q35_last_error();
+  }
+  const int nC = (L + kChunk - 1) / kChunk;
+  Q35_CHECK_ARG(B < 65536 && H < 65536);
+  float* chunk_ws = (float*)workspace + 4ll * B * L * H;
+  float* gc = chunk_ws + (size_t)B * H * nC * kChunkFloats;
+  delta_chunk_prep<<<dim3(nC, H, B), 256, 0, stream>>>((const uint16_t*)qkv, qkv_stride,
+                                                       (const float*)workspace, chunk_ws, gc, L, H,
+                                                       nC);
+  e = q35_last_error();
+  if (e) return e;
+  delta_chunk_scan<<<dim3(kD / 16, H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state,
+                                                            (uint16_t*)out, L, H, nC);
   return q35_last_error();
 }
 

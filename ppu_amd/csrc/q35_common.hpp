@@ -27,6 +27,8 @@ Q35_DEV float bf_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u);
 // stays NaN (the rounding torch's .to(bfloat16) and Triton's casts use).
 typedef float q35_f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 q35_bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 q35_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
 Q35_DEV uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 Q35_DEV float round_bf(float f) { return bf2f(f2bf(f)); }
 Q35_DEV uint32_t pack_bf2(float lo, float hi) {

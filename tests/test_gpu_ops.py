@@ -212,8 +212,11 @@ def _delta_inputs(g, seq_len, heads=16, dim=128):
     return qkv, packed, a_log, dt_bias, state
 
 
-@pytest.mark.parametrize("seq_len", [1, 3, 64])
+@pytest.mark.parametrize("seq_len", [1, 3, 63, 64, 200, 1024])
 def test_delta_recurrent(gpu, seq_len):
+    """Token scan below 64 tokens, the chunked closed form (64-token chunks on
+    the matrix cores, partial last chunk) from 64 on; the incoming state is
+    nonzero, so the carried state enters every chunk."""
     from ppu_amd import kernels as K
 
     g = gen(KERNEL_SEED + 12)
