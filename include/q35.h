@@ -146,10 +146,13 @@ int q35_delta_decode(const void* src, int src_stride, const void* packed, int pa
                      int norm_w_f32, float norm_eps, void* out, int B, int H, int D,
                      int fuse_conv, int fuse_gnorm, void* stream);
 
-/* Workspace floats for q35_delta_prefill. */
+/* Workspace floats for q35_delta_prefill: 4 per (batch, token, head), plus for
+ * L >= 64 36865 per (batch, head, 64-token chunk). */
 long long q35_delta_prefill_workspace(int B, int L, int H);
-/* Sequential gated delta rule over L tokens (per-token factors precomputed).
- * Replaces qwen35_fused/kernels.py:854 with precompute_factors (kernels :713-851). */
+/* Gated delta rule over L tokens (per-token factors precomputed): a token scan
+ * below 64 tokens, the closed form over 64-token chunks on the matrix cores
+ * from 64 on. Replaces qwen35_fused/kernels.py:854 with precompute_factors
+ * (kernels :713-851). */
 int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
                       const void* a_log, const void* dt_bias, int params_f32, void* state,
                       void* out, void* workspace, long long workspace_floats, int B, int L, int H,

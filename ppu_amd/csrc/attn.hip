@@ -661,28 +661,46 @@ __global__ __launch_bounds__(G * 64) void gqa_prefill_mfma(
     l[i] = 0.f;
   }
   const int nblk = (n_keys + 31) / 32;
-  for (int blk = 0; blk < nblk; ++blk) {
+  // Global loads of one 32-key block: the K operand of its two 16-key halves
+  // (key kb + 16*sb + col, dims 8*kg + 32t) and this thread's share of V rows
+  // for the transposed staging. Block blk + 1 is requested before block blk
+  // is computed, so the loop does not wait on memory.
+  constexpr int VPER = (32 * (kAD / 8) + G * 64 - 1) / (G * 64);
+  auto load_block = [&](int blk, uint4 (&kv)[2][8], uint4 (&vr)[VPER]) {
     const int kb = blk * 32;
-    uint16_t* vt = vt_s[blk & 1];
-    // K operand of the two 16-key blocks: key kb + 16*sb + col, dims 8*kg + 32t.
-    uint4 kv[2][8];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       const uint16_t* kr = Kh + (size_t)min(kb + 16 * sb + col, n_keys - 1) * kAD + kg * 8;
 #pragma unroll
       for (int t = 0; t < 8; ++t) kv[sb][t] = *reinterpret_cast<const uint4*>(kr + 32 * t);
     }
-    // Stage V^T: (key, 8-dim group) pairs, vt[dim][key].
-    for (int pi = threadIdx.x; pi < 32 * (kAD / 8); pi += G * 64) {
-      const int k = pi & 31, dg = pi >> 5;
-      const int key = kb + k;
-      uint4 v = *reinterpret_cast<const uint4*>(Vh + (size_t)min(key, n_keys - 1) * kAD + dg * 8);
-      if (key >= n_keys) v = make_uint4(0, 0, 0, 0);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt[(dg * 8 + 2 * e) * kVtStride + k] = (uint16_t)(w[e] & 0xffffu);
-        vt[(dg * 8 + 2 * e + 1) * kVtStride + k] = (uint16_t)(w[e] >> 16);
+    for (int j = 0; j < VPER; ++j) {
+      const int pi = min((int)threadIdx.x + j * G * 64, 32 * (kAD / 8) - 1);
+      const int k = pi & 31, dg = pi >> 5;
+      vr[j] = *reinterpret_cast<const uint4*>(Vh + (size_t)min(kb + k, n_keys - 1) * kAD + dg * 8);
+    }
+  };
+  uint4 kv[2][8], vr[VPER];
+  load_block(0, kv, vr);
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kb = blk * 32;
+    uint16_t* vt = vt_s[blk & 1];
+    uint4 kn[2][8], vn[VPER];
+    load_block(min(blk + 1, nblk - 1), kn, vn);
+    // Stage V^T: (key, 8-dim group) pairs, vt[dim][key]; masked keys as zeros.
+#pragma unroll
+    for (int j = 0; j < VPER; ++j) {
+      const int pi = (int)threadIdx.x + j * G * 64;
+      if (pi < 32 * (kAD / 8)) {
+        const int k = pi & 31, dg = pi >> 5;
+        const uint4 v = kb + k < n_keys ? vr[j] : make_uint4(0, 0, 0, 0);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vt[(dg * 8 + 2 * e) * kVtStride + k] = (uint16_t)(w[e] & 0xffffu);
+          vt[(dg * 8 + 2 * e + 1) * kVtStride + k] = (uint16_t)(w[e] >> 16);
+        }
       }
     }
     // S = Q K^T, then scale, causal mask and online softmax per row.
@@ -729,6 +747,12 @@ __global__ __launch_bounds__(G * 64) void gqa_prefill_mfma(
       o[d] = mfma_16x16x32(pa_hi, vb, o[d]);
       o[d] = mfma_16x16x32(pa_lo, vb, o[d]);
     }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) kv[sb][t] = kn[sb][t];
+#pragma unroll
+    for (int j = 0; j < VPER; ++j) vr[j] = vn[j];
   }
   // out[b, row, h*D + 16d + col] = bf16(O / l) for the valid rows.
 #pragma unroll

@@ -301,32 +301,101 @@ __global__ __launch_bounds__(256) void delta_decode_tiled(const DeltaArgs p) {
 }
 
 // ------------------------------------------------------------- prefill scan
-// Per (token, head) scalars (q_inv, k_inv, g = log alpha, beta) [reference kernels.py:713-765].
-__global__ __launch_bounds__(256) void delta_factors(const uint16_t* __restrict__ qkv, int qkv_stride,
-                                                     const uint16_t* __restrict__ packed,
-                                                     int packed_stride, const void* a_log,
-                                                     const void* dt_bias, int params_f32,
-                                                     float* __restrict__ factors, int rows, int H,
-                                                     int a_off, int b_off) {
+// conv1d_prefill for width-4 filters, 8 channels x 4 tokens per thread: the
+// 7 input rows t0-3 .. t0+3 (16-byte loads, rows before 0 are zero) feed the
+// 4 outputs; taps are summed oldest first as in conv1d_prefill.
+__global__ __launch_bounds__(256) void conv1d_prefill_vec4(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w,
+                                                           uint16_t* __restrict__ state,
+                                                           uint16_t* __restrict__ out, int B, int L,
+                                                           int C, int in_stride) {
+  constexpr int KW = 4, TOK = 4;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cgs = C / 8;
+  const int tgs = (L + TOK - 1) / TOK;
+  if (idx >= (long long)B * tgs * cgs) return;
+  const int cg = (int)(idx % cgs);
+  const long long rest = idx / cgs;
+  const int tg = (int)(rest % tgs);
+  const int b = (int)(rest / tgs);
+  const int c = cg * 8;
+  const int t0 = tg * TOK;
+  float xin[TOK + KW - 1][8];
+#pragma unroll
+  for (int r = 0; r < TOK + KW - 1; ++r) {
+    const int src = t0 - (KW - 1) + r;
+    const int sc = min(max(src, 0), L - 1);
+    unpack8(*reinterpret_cast<const uint4*>(x + ((size_t)b * L + sc) * in_stride + c), xin[r]);
+    if (src < 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xin[r][e] = 0.f;
+    }
+  }
+  float wt[8][KW];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(w + (size_t)c * KW + q * 8), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wt[2 * q + e / 4][e % 4] = f[e];
+  }
+#pragma unroll
+  for (int j = 0; j < TOK; ++j) {
+    const int t = t0 + j;
+    if (t >= L) break;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = 0.f;
+#pragma unroll
+      for (int tap = 0; tap < KW; ++tap) acc = fmaf(xin[j + tap][e], wt[e][tap], acc);
+      o[e] = silu_f(round_bf(acc));
+    }
+    *reinterpret_cast<uint4*>(out + ((size_t)b * L + t) * C + c) = pack8(o);
+    const int pos = t - (L - KW);
+    if (pos >= 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        state[((size_t)b * C + c + e) * KW + pos] = (uint16_t)f2bf(xin[j + KW - 1][e]);
+    }
+  }
+}
+
+// Per (token, head) scalars (q_inv, k_inv, g = log alpha, beta) [reference
+// kernels.py:713-765], 16 lanes per (token, head) row: 4 rows per wave,
+// 16-byte loads of q and k, DPP row sums of squares.
+__global__ __launch_bounds__(256) void delta_factors16(const uint16_t* __restrict__ qkv,
+                                                       int qkv_stride,
+                                                       const uint16_t* __restrict__ packed,
+                                                       int packed_stride, const void* a_log,
+                                                       const void* dt_bias, int params_f32,
+                                                       float* __restrict__ factors, int rows, int H,
+                                                       int a_off, int b_off) {
   const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);  // r = token_flat * H + h
-  if (r >= rows) return;
-  const int h = r % H;
-  const long long tf = r / H;
+  const int r = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const int rc = min(r, rows - 1);
+  const int h = rc % H;
+  const long long tf = rc / H;
+  const int k8 = (lane & 15) * 8;
   const uint16_t* row = qkv + (size_t)tf * qkv_stride;
-  const float q0 = bf2f(row[h * kD + lane]), q1 = bf2f(row[h * kD + lane + 64]);
-  const float k0 = bf2f(row[H * kD + h * kD + lane]), k1 = bf2f(row[H * kD + h * kD + lane + 64]);
-  const float qs = wave_sum(q0 * q0 + q1 * q1);
-  const float ks = wave_sum(k0 * k0 + k1 * k1);
-  if (lane == 0) {
+  float q[8], k[8];
+  unpack8(*reinterpret_cast<const uint4*>(row + h * kD + k8), q);
+  unpack8(*reinterpret_cast<const uint4*>(row + H * kD + h * kD + k8), k);
+  float qs = 0.f, ks = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    qs += q[e] * q[e];
+    ks += k[e] * k[e];
+  }
+  qs = row16_sum(qs);
+  ks = row16_sum(ks);
+  if ((lane & 15) == 0 && r < rows) {
     const uint16_t* prow = packed + (size_t)tf * packed_stride;
     const float a = bf2f(prow[a_off + h]) + ld_param(dt_bias, h, params_f32);
-    // g = log(alpha); the scan applies alpha = exp(g), the value the
-    // reference computes.
     const float g = -expf(ld_param(a_log, h, params_f32)) * softplus20(a);
     const float beta = 1.0f / (1.0f + expf(-bf2f(prow[b_off + h])));
-    float4 f = make_float4(rsqrt_cr(qs + 1e-6f), rsqrt_cr(ks + 1e-6f), g, beta);
-    *reinterpret_cast<float4*>(factors + (size_t)r * 4) = f;
+    *reinterpret_cast<float4*>(factors + (size_t)r * 4) =
+        make_float4(rsqrt_cr(qs + 1e-6f), rsqrt_cr(ks + 1e-6f), g, beta);
   }
 }
 
@@ -666,26 +735,42 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   float* Sg = state + bh * kD * kD + tile * 16;
   for (int idx = tid; idx < kD * 16; idx += 256) S_s[(idx >> 4) * kSS + (idx & 15)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
   __syncthreads();
-  for (int c = 0; c < nC; ++c) {
+  // This wave's operands of one chunk: row tile wid of W^T, Q', P and U0, dk
+  // tiles 2*wid and 2*wid+1 of K''^T. Chunk c + 1 is requested before chunk c
+  // is computed.
+  struct ChunkOps {
+    float4 wt[8], qp[8], pq[4], kt[2][4], u0;
+    float gC;
+  };
+  auto load_ops = [&](int c, ChunkOps& op) {
     const float* wsb = ws + (bh * nC + c) * kChunkFloats;
-    // This wave's operands: row tile wid of W^T, Q', P and U0, dk tiles
-    // 2*wid and 2*wid+1 of K''^T.
-    float4 wt[8], qp[8], pq[4], kt[2][4];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      wt[dt] = *reinterpret_cast<const float4*>(wsb + kOffWT + ((wid * 8 + dt) * 64 + lane) * 4);
-      qp[dt] = *reinterpret_cast<const float4*>(wsb + kOffQP + ((wid * 8 + dt) * 64 + lane) * 4);
+      op.wt[dt] = *reinterpret_cast<const float4*>(wsb + kOffWT + ((wid * 8 + dt) * 64 + lane) * 4);
+      op.qp[dt] = *reinterpret_cast<const float4*>(wsb + kOffQP + ((wid * 8 + dt) * 64 + lane) * 4);
     }
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
-      pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
+      op.pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd)
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
-        kt[dd][s4] = *reinterpret_cast<const float4*>(wsb + kOffKT + (((2 * wid + dd) * 4 + s4) * 64 + lane) * 4);
-    const float4 u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
-    const float gC = gc[bh * nC + c];
+        op.kt[dd][s4] =
+            *reinterpret_cast<const float4*>(wsb + kOffKT + (((2 * wid + dd) * 4 + s4) * 64 + lane) * 4);
+    op.u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
+    op.gC = gc[bh * nC + c];
+  };
+  ChunkOps cur;
+  load_ops(0, cur);
+  for (int c = 0; c < nC; ++c) {
+    ChunkOps nxt;
+    load_ops(min(c + 1, nC - 1), nxt);
+    const float4* wt = cur.wt;
+    const float4* qp = cur.qp;
+    const float4* pq = cur.pq;
+    const float4 u0 = cur.u0;
+    const float gC = cur.gC;
 
     // U = U0 - W S (rows 16*wid.., this v tile)
     q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -731,7 +816,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
       for (int e = 0; e < 4; ++e) sn[dd][e] = gC * S_s[(16 * dt + 4 * g4 + e) * kSS + col];
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const float a[4] = {kt[dd][s4].x, kt[dd][s4].y, kt[dd][s4].z, kt[dd][s4].w};
+        const float a[4] = {cur.kt[dd][s4].x, cur.kt[dd][s4].y, cur.kt[dd][s4].z, cur.kt[dd][s4].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           sn[dd] = mfma4(a[e], U_s[(4 * (4 * s4 + e) + g4) * kSS + col], sn[dd]);
@@ -743,6 +828,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
 #pragma unroll
       for (int e = 0; e < 4; ++e) S_s[(16 * (2 * wid + dd) + 4 * g4 + e) * kSS + col] = sn[dd][e];
     __syncthreads();
+    cur = nxt;
   }
   for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = S_s[(idx >> 4) * kSS + (idx & 15)];
 }
@@ -767,6 +853,16 @@ int q35_conv1d_prefill(const void* x, const void* w, void* state, void* out, int
   Q35_CHECK_ARG(B >= 0 && L > 0 && C > 0 && kw > 0 && kw <= 16 && in_stride >= C);
   const long long total = (long long)B * L * C;
   if (total == 0) return 0;
+  if (kw == 4 && C % 8 == 0 && in_stride % 8 == 0 && q35_aligned16(x) && q35_aligned16(w) &&
+      q35_aligned16(out)) {
+    const long long threads = (long long)B * ((L + 3) / 4) * (C / 8);
+    const long long g = (threads + 255) / 256;
+    Q35_CHECK_ARG(g < (1ll << 31));
+    conv1d_prefill_vec4<<<(unsigned)g, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)w,
+                                                         (uint16_t*)state, (uint16_t*)out, B, L, C,
+                                                         in_stride);
+    return q35_last_error();
+  }
   const long long grid = (total + 255) / 256;
   Q35_CHECK_ARG(grid < (1ll << 31));
   conv1d_prefill<<<(unsigned)grid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)w,
@@ -842,7 +938,7 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
   if (B == 0) return 0;
   const long long rows = (long long)B * L * H;
   Q35_CHECK_ARG(rows < (1ll << 30));
-  delta_factors<<<(unsigned)((rows + 3) / 4), 256, 0, stream>>>(
+  delta_factors16<<<(unsigned)((rows + 15) / 16), 256, 0, stream>>>(
       (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
       params_f32, (float*)workspace, (int)rows, H, 4 * H * D, 4 * H * D + H);
   int e = q35_last_error();

@@ -1,12 +1,12 @@
 // Row-wise decode kernels: RMSNorm, residual-add + RMSNorm, gated RMSNorm,
 // SiLU-and-mul and the attention output gate.
 //
-// One wave64 owns one row. Rows whose width is a multiple of 8 are streamed
-// with 128-bit loads (8 bf16 per lane per step); other widths take a scalar
-// lane-strided path. Sums of squares are reduced with the DPP/swizzle wave
-// reduction from q35_common.hpp. The norm kernels make two passes over a row:
-// the second pass re-reads it from L1/L2 instead of holding it in registers,
-// so any width works.
+// One wave64 owns one row. Widths of 512/1024/2048/4096 keep the row in
+// registers between the two passes (one memory round trip per row); other
+// widths that are a multiple of 8 stream the row twice with 128-bit loads, and
+// the rest take a scalar lane-strided path. Gated RMSNorm over 128-wide heads
+// packs 4 rows per wave (16 lanes x 8 elements). Sums of squares are reduced
+// with the DPP/swizzle reductions from q35_common.hpp.
 #include "q35_common.hpp"
 
 namespace {
@@ -82,6 +82,107 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const uint16_t* __restrict__
   }
 }
 
+// rmsnorm_rows for widths of NPER * 512: the row stays in registers between
+// the two passes (lane l holds elements 512*j + 8*l .. +7), and every load
+// (x, u, w) is issued before the reduction, so a row costs one round trip.
+template <bool RESIDUAL, int NPER>
+__global__ __launch_bounds__(256) void rmsnorm_rows_reg(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ u,
+                                                        const void* __restrict__ w, int w_f32,
+                                                        uint16_t* __restrict__ r_out,
+                                                        uint16_t* __restrict__ y, int rows, float eps) {
+  constexpr int width = NPER * 512;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const size_t base = (size_t)row * width;
+  uint4 xa[NPER], ua[NPER], wa[NPER], wb[NPER];
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    const int k = j * 512 + lane * 8;
+    xa[j] = *reinterpret_cast<const uint4*>(x + base + k);
+    if (RESIDUAL) ua[j] = *reinterpret_cast<const uint4*>(u + base + k);
+    if (w_f32) {
+      wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + k);
+      wb[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + k + 4);
+    } else {
+      wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + k);
+    }
+  }
+  float a[NPER][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    unpack8(xa[j], a[j]);
+    if (RESIDUAL) {
+      float b[8];
+      unpack8(ua[j], b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[j][e] = round_bf(a[j][e] + b[e]);
+      *reinterpret_cast<uint4*>(r_out + base + j * 512 + lane * 8) = pack8(a[j]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += a[j][e] * a[j][e];
+  }
+  const float inv = rsqrt_cr(wave_sum(ss) / (float)width + eps);
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    float wf[8];
+    if (w_f32) {
+      wf[0] = __uint_as_float(wa[j].x); wf[1] = __uint_as_float(wa[j].y);
+      wf[2] = __uint_as_float(wa[j].z); wf[3] = __uint_as_float(wa[j].w);
+      wf[4] = __uint_as_float(wb[j].x); wf[5] = __uint_as_float(wb[j].y);
+      wf[6] = __uint_as_float(wb[j].z); wf[7] = __uint_as_float(wb[j].w);
+    } else {
+      unpack8(wa[j], wf);
+    }
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = a[j][e] * inv * (1.0f + wf[e]);
+    *reinterpret_cast<uint4*>(y + base + j * 512 + lane * 8) = pack8(o);
+  }
+}
+
+// Gated RMSNorm over rows of exactly 128 (one head): 16 lanes per row, 8
+// elements per lane, 4 rows per wave; the sum of squares is a DPP row sum.
+__global__ __launch_bounds__(256) void gated_rmsnorm_rows128(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ gate,
+                                                             const void* __restrict__ w, int w_f32,
+                                                             uint16_t* __restrict__ y, int rows,
+                                                             float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const int k = (lane & 15) * 8;
+  const int rc = min(row, rows - 1);
+  const size_t base = (size_t)rc * 128 + k;
+  const uint4 xr = *reinterpret_cast<const uint4*>(x + base);
+  const uint4 gr = *reinterpret_cast<const uint4*>(gate + base);
+  float wf[8];
+  if (w_f32) {
+    const float4 w0 = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + k);
+    const float4 w1 = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + k + 4);
+    wf[0] = w0.x; wf[1] = w0.y; wf[2] = w0.z; wf[3] = w0.w;
+    wf[4] = w1.x; wf[5] = w1.y; wf[6] = w1.z; wf[7] = w1.w;
+  } else {
+    unpack8(*reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + k), wf);
+  }
+  float a[8], g[8];
+  unpack8(xr, a);
+  unpack8(gr, g);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += a[e] * a[e];
+  const float inv = rsqrt_cr(row16_sum(ss) / 128.0f + eps);
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float nb = round_bf(a[e] * inv);
+    const float weighted = round_bf(nb * round_bf(wf[e]));
+    o[e] = weighted * silu_f(g[e]);
+  }
+  if (row < rows) *reinterpret_cast<uint4*>(y + base) = pack8(o);
+}
+
 // y = bf16( bf16(bf16(x * rsqrt(mean(x^2)+eps)) * bf16(w)) * silu(gate) )
 // [reference kernels.py:115-155]; the weight is used directly (no 1 + w).
 __global__ __launch_bounds__(256) void gated_rmsnorm_rows(const uint16_t* __restrict__ x,
@@ -121,6 +222,23 @@ __global__ __launch_bounds__(256) void silu_mul_elems(const uint16_t* __restrict
   out[i] = (uint16_t)f2bf(round_bf(silu_f(g)) * up);
 }
 
+// silu_mul_elems with 8 elements per thread (width a multiple of 8).
+__global__ __launch_bounds__(256) void silu_mul_vec(const uint16_t* __restrict__ packed,
+                                                    uint16_t* __restrict__ out, long long groups,
+                                                    int width) {
+  const long long gi = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gi >= groups) return;
+  const int gpr = width / 8;
+  const long long row = gi / gpr;
+  const int col = (int)(gi - row * gpr) * 8;
+  float g[8], up[8], o[8];
+  unpack8(*reinterpret_cast<const uint4*>(packed + row * 2 * width + col), g);
+  unpack8(*reinterpret_cast<const uint4*>(packed + row * 2 * width + width + col), up);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = round_bf(silu_f(g[e])) * up[e];
+  *reinterpret_cast<uint4*>(out + row * width + col) = pack8(o);
+}
+
 // out = bf16( x * bf16(sigmoid(gate)) ); the gate of head h sits at
 // packed[token, h*2*head_dim + head_dim + col] [reference kernels.py:285-333].
 __global__ __launch_bounds__(256) void attn_gate_elems(const uint16_t* __restrict__ x,
@@ -148,6 +266,17 @@ int q35_rmsnorm(const void* x, const void* w, int w_f32, void* y, int rows, int 
   if (rows == 0) return 0;
   const int grid = (rows + kWaves - 1) / kWaves;
   const int vec = (width % 8 == 0) && q35_aligned16(x) && q35_aligned16(y);
+  if (vec && q35_aligned16(w) && (width == 512 || width == 1024 || width == 2048 || width == 4096)) {
+#define Q35_RMS(NP)                                                                               \
+  rmsnorm_rows_reg<false, NP><<<grid, 256, 0, stream>>>((const uint16_t*)x, nullptr, w, w_f32,  \
+                                                        nullptr, (uint16_t*)y, rows, eps)
+    if (width == 512) Q35_RMS(1);
+    else if (width == 1024) Q35_RMS(2);
+    else if (width == 2048) Q35_RMS(4);
+    else Q35_RMS(8);
+#undef Q35_RMS
+    return q35_last_error();
+  }
   rmsnorm_rows<false><<<grid, 256, 0, stream>>>((const uint16_t*)x, nullptr, w, w_f32, nullptr,
                                                 (uint16_t*)y, rows, width, eps, vec);
   return q35_last_error();
@@ -161,6 +290,18 @@ int q35_residual_rmsnorm(const void* residual, const void* update, const void* w
   const int grid = (rows + kWaves - 1) / kWaves;
   const int vec = (width % 8 == 0) && q35_aligned16(residual) && q35_aligned16(update) &&
                   q35_aligned16(residual_out) && q35_aligned16(y);
+  if (vec && q35_aligned16(w) && (width == 512 || width == 1024 || width == 2048 || width == 4096)) {
+#define Q35_RMS(NP)                                                                               \
+  rmsnorm_rows_reg<true, NP><<<grid, 256, 0, stream>>>(                                          \
+      (const uint16_t*)residual, (const uint16_t*)update, w, w_f32, (uint16_t*)residual_out,     \
+      (uint16_t*)y, rows, eps)
+    if (width == 512) Q35_RMS(1);
+    else if (width == 1024) Q35_RMS(2);
+    else if (width == 2048) Q35_RMS(4);
+    else Q35_RMS(8);
+#undef Q35_RMS
+    return q35_last_error();
+  }
   rmsnorm_rows<true><<<grid, 256, 0, stream>>>((const uint16_t*)residual, (const uint16_t*)update,
                                                w, w_f32, (uint16_t*)residual_out, (uint16_t*)y,
                                                rows, width, eps, vec);
@@ -171,6 +312,13 @@ int q35_gated_rmsnorm(const void* x, const void* gate, const void* w, int w_f32,
                       int width, float eps, hipStream_t stream) {
   Q35_CHECK_ARG(rows >= 0 && width > 0);
   if (rows == 0) return 0;
+  if (width == 128 && q35_aligned16(x) && q35_aligned16(gate) && q35_aligned16(y) &&
+      q35_aligned16(w)) {
+    const int grid4 = (rows + 4 * kWaves - 1) / (4 * kWaves);
+    gated_rmsnorm_rows128<<<grid4, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)gate, w,
+                                                     w_f32, (uint16_t*)y, rows, eps);
+    return q35_last_error();
+  }
   const int grid = (rows + kWaves - 1) / kWaves;
   gated_rmsnorm_rows<<<grid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)gate, w, w_f32,
                                                (uint16_t*)y, rows, width, eps);
@@ -181,6 +329,14 @@ int q35_silu_mul(const void* packed, void* out, long long rows, int width, hipSt
   Q35_CHECK_ARG(rows >= 0 && width > 0);
   const long long total = rows * (long long)width;
   if (total == 0) return 0;
+  if (width % 8 == 0 && q35_aligned16(packed) && q35_aligned16(out)) {
+    const long long groups = total / 8;
+    const long long g8 = (groups + 255) / 256;
+    Q35_CHECK_ARG(g8 < (1ll << 31));
+    silu_mul_vec<<<(unsigned)g8, 256, 0, stream>>>((const uint16_t*)packed, (uint16_t*)out, groups,
+                                                   width);
+    return q35_last_error();
+  }
   const long long grid = (total + 255) / 256;
   Q35_CHECK_ARG(grid < (1ll << 31));
   silu_mul_elems<<<(unsigned)grid, 256, 0, stream>>>((const uint16_t*)packed, (uint16_t*)out, total,
