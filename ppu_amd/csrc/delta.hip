@@ -710,7 +710,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int j = 4 * (4 * s4 + e) + g4;
+          const int j = 16 * s4 + 4 * g4 + e;
           v[e] = kf_s[j] * Kh[j * kCS + 16 * dt + col];
         }
         *reinterpret_cast<float4*>(wsb + kOffKT + ((dt * 4 + s4) * 64 + lane) * 4) =
@@ -720,21 +720,38 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   }
 }
 
+// State and U tiles are kept transposed in LDS ([column][row]) so that the
+// four k values a lane feeds to four consecutive MFMAs are one float4 read;
+// MFMA chains alternate between two accumulators.
+constexpr int kST = kD + 4;      // fp32 per transposed state column
+constexpr int kUT = kChunk + 4;  // fp32 per transposed U column
+
 __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict__ ws,
                                                         const float* __restrict__ gc,
                                                         float* __restrict__ state,
                                                         uint16_t* __restrict__ out, int L, int H,
                                                         int nC) {
-  const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // Workgroups are dispatched to the 8 XCDs round-robin by linear id; the 8
+  // v tiles of a head read the same chunk operands, so they are placed on one
+  // XCD (one L2 fill serves all 8): id = xcd + 8*slot, head = xcd + 8*(slot/8).
+  const int id = blockIdx.x, b = blockIdx.y;
+  int tile, h;
+  if (H % 8 == 0) {
+    const int slot = id >> 3;
+    h = (id & 7) + 8 * (slot >> 3);
+    tile = slot & 7;
+  } else {
+    tile = id & 7;
+    h = id >> 3;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g4 = lane >> 4;
   const size_t bh = (size_t)b * H + h;
-  __shared__ float S_s[kD * kSS];
-  __shared__ float U_s[kChunk * kSS];
+  __shared__ alignas(16) float St[16 * kST];
+  __shared__ alignas(16) float Ut[16 * kUT];
   float* Sg = state + bh * kD * kD + tile * 16;
-  for (int idx = tid; idx < kD * 16; idx += 256) S_s[(idx >> 4) * kSS + (idx & 15)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
-  __syncthreads();
+  for (int idx = tid; idx < kD * 16; idx += 256) St[(idx & 15) * kST + (idx >> 4)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
   // This wave's operands of one chunk: row tile wid of W^T, Q', P and U0, dk
   // tiles 2*wid and 2*wid+1 of K''^T. Chunk c + 1 is requested before chunk c
   // is computed.
@@ -761,50 +778,54 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
     op.u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
     op.gC = gc[bh * nC + c];
   };
+  auto mma4 = [](const float4 a, const float4 bv, q35_f32x4 c0, q35_f32x4 c1, q35_f32x4& o0,
+                 q35_f32x4& o1) {
+    c0 = mfma4(a.x, bv.x, c0);
+    c1 = mfma4(a.y, bv.y, c1);
+    c0 = mfma4(a.z, bv.z, c0);
+    c1 = mfma4(a.w, bv.w, c1);
+    o0 = c0;
+    o1 = c1;
+  };
   ChunkOps cur;
   load_ops(0, cur);
+  __syncthreads();
+  const float* scol = &St[col * kST + 4 * g4];
+  float* ucol = &Ut[col * kUT + 4 * g4];
   for (int c = 0; c < nC; ++c) {
     ChunkOps nxt;
     load_ops(min(c + 1, nC - 1), nxt);
-    const float4* wt = cur.wt;
-    const float4* qp = cur.qp;
-    const float4* pq = cur.pq;
-    const float4 u0 = cur.u0;
-    const float gC = cur.gC;
 
     // U = U0 - W S (rows 16*wid.., this v tile)
-    q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    q35_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const float a[4] = {wt[dt].x, wt[dt].y, wt[dt].z, wt[dt].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc = mfma4(a[e], S_s[(16 * dt + 4 * g4 + e) * kSS + col], acc);
+      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);
+      mma4(cur.wt[dt], sv, a0, a1, a0, a1);
     }
-    const float uo[4] = {u0.x - acc[0], u0.y - acc[1], u0.z - acc[2], u0.w - acc[3]};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) U_s[(16 * wid + 4 * g4 + e) * kSS + col] = uo[e];
+    const float4 uo = make_float4(cur.u0.x - (a0[0] + a1[0]), cur.u0.y - (a0[1] + a1[1]),
+                                  cur.u0.z - (a0[2] + a1[2]), cur.u0.w - (a0[3] + a1[3]));
+    *reinterpret_cast<float4*>(ucol + 16 * wid) = uo;
     __syncthreads();
 
     // O = Q' S + P U
-    q35_f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    q35_f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const float a[4] = {qp[dt].x, qp[dt].y, qp[dt].z, qp[dt].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o = mfma4(a[e], S_s[(16 * dt + 4 * g4 + e) * kSS + col], o);
+      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);
+      mma4(cur.qp[dt], sv, o0, o1, o0, o1);
     }
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
       if (jt <= wid) {
-        const float a[4] = {pq[jt].x, pq[jt].y, pq[jt].z, pq[jt].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o = mfma4(a[e], U_s[(16 * jt + 4 * g4 + e) * kSS + col], o);
+        const float4 uv = *reinterpret_cast<const float4*>(ucol + 16 * jt);
+        mma4(cur.pq[jt], uv, o0, o1, o0, o1);
       }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = c * kChunk + 16 * wid + 4 * g4 + e;
-      if (t < L) out[(((size_t)b * L + t) * H + h) * kD + tile * 16 + col] = (uint16_t)f2bf(o[e]);
+      if (t < L) out[(((size_t)b * L + t) * H + h) * kD + tile * 16 + col] = (uint16_t)f2bf(o0[e] + o1[e]);
     }
 
     // S <- gamma_C S + K''^T U (dk tiles 2*wid, 2*wid + 1)
@@ -812,25 +833,25 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd) {
       const int dt = 2 * wid + dd;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sn[dd][e] = gC * S_s[(16 * dt + 4 * g4 + e) * kSS + col];
+      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);
+      q35_f32x4 s0 = {cur.gC * sv.x, cur.gC * sv.y, cur.gC * sv.z, cur.gC * sv.w};
+      q35_f32x4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const float a[4] = {cur.kt[dd][s4].x, cur.kt[dd][s4].y, cur.kt[dd][s4].z, cur.kt[dd][s4].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          sn[dd] = mfma4(a[e], U_s[(4 * (4 * s4 + e) + g4) * kSS + col], sn[dd]);
+        const float4 uv = *reinterpret_cast<const float4*>(ucol + 16 * s4);
+        mma4(cur.kt[dd][s4], uv, s0, s1, s0, s1);
       }
+      sn[dd] = s0 + s1;
     }
     __syncthreads();  // every wave has read S and U of this chunk
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) S_s[(16 * (2 * wid + dd) + 4 * g4 + e) * kSS + col] = sn[dd][e];
+      *reinterpret_cast<float4*>(&St[col * kST + 16 * (2 * wid + dd) + 4 * g4]) =
+          make_float4(sn[dd][0], sn[dd][1], sn[dd][2], sn[dd][3]);
     __syncthreads();
     cur = nxt;
   }
-  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = S_s[(idx >> 4) * kSS + (idx & 15)];
+  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = St[(idx & 15) * kST + (idx >> 4)];
 }
 
 }  // namespace
@@ -958,8 +979,8 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
                                                        nC);
   e = q35_last_error();
   if (e) return e;
-  delta_chunk_scan<<<dim3(kD / 16, H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state,
-                                                            (uint16_t*)out, L, H, nC);
+  delta_chunk_scan<<<dim3((kD / 16) * H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state,
+                                                              (uint16_t*)out, L, H, nC);
   return q35_last_error();
 }
 
