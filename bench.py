@@ -12,8 +12,11 @@ Printed (one JSON line on stdout):
   ttft_ms      prefill (1024 tokens) + first token, timed as the reference
                does (evaluation_wrapper.py:342-365), median of warm runs
   roofline     the dominant decode kernel (lm_head GEMV + top-1, 1.017 GB of
-               weights per launch) timed with HIP events on its stream
-  kernels      per-kernel achieved HBM GB/s of the BASELINE configs 1-4
+               weights per launch) timed with HIP events on its stream;
+               traffic = its HBM bytes per launch from the committed
+               rocprofv3 --pmc summary profiles/lm_head_top1_traffic_pmc.txt
+               (made from ``bench.py --counter-probe`` runs)
+  kernels     per-kernel achieved HBM GB/s of the BASELINE configs 1-4
                (rotating >= 640 MB of distinct buffers so the 256 MB MALL does
                not serve the weights), in-graph time per launch
   variants     the same decode and TTFT measurement for the other linear
@@ -69,6 +72,19 @@ def graph_time_us(fn, calls: int, reps: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * calls)
 
 
+def pmc_traffic(name: str):
+    """HBM bytes per launch read from a committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a copy kernel of known size),
+    or None when the summary is absent."""
+    try:
+        for line in (ROOT / "profiles" / name).read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def lm_head_roofline(model) -> dict:
     import torch
 
@@ -83,7 +99,8 @@ def lm_head_roofline(model) -> dict:
     achieved = algo / us / 1e3
     return {"kernel": "lm_head GEMV + top-1 [248320,2048] bf16", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": pmc_traffic("lm_head_top1_traffic_pmc.txt"),
             "us_per_launch": round(us, 2), "algorithmic_bytes": algo,
             "workspace_bytes": slots * 8}
 
@@ -152,6 +169,45 @@ def kernel_table(dev) -> dict:
     return out
 
 
+def counter_probe(dev) -> None:
+    """A short fixed workload for ``rocprofv3 --pmc`` passes (one counter set
+    per run), so that per-dispatch counters can be read for:
+
+    * 5 launches of the lm_head GEMV + top-1 on a [248320, 2048] bf16 weight;
+    * 5 calibration launches of a plain elementwise kernel (``neg``) that reads
+      exactly 1 GiB and writes exactly 1 GiB, the yardstick that turns the
+      FETCH_SIZE / WRITE_SIZE counters into bytes;
+    * 3 launches of each prefill GEMM shape (M = 1024 tokens) of the 2B
+      decoder, for MFMA counters.
+    """
+    import torch
+    import torch.nn.functional as F
+
+    from ppu_amd import kernels as K
+
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(20260819)
+    w = (torch.randn(248320, 2048, device=dev, generator=g) * 0.02).to(bf)
+    h = torch.randn(1, 2048, device=dev, generator=g).to(bf)
+    for _ in range(5):
+        K.lm_head_argmax(h, w)
+    torch.cuda.synchronize()
+    del w
+    src = torch.randn(1 << 28, device=dev, generator=g)  # 2^28 fp32 = 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    for (n, k) in ((8320, 2048), (2048, 2048), (5120, 2048), (12288, 2048), (2048, 6144)):
+        x = torch.randn(1024, k, device=dev, generator=g).to(bf)
+        wt = (torch.randn(n, k, device=dev, generator=g) * 0.02).to(bf)
+        for _ in range(3):
+            F.linear(x, wt)
+    torch.cuda.synchronize()
+    log("counter probe done")
+
+
 def cpu_baseline(state, cfg, prompt, decode_steps: int) -> dict:
     """The oracle decoder on the host cores: a bounded sample of the workload."""
     import torch
@@ -199,6 +255,8 @@ def main() -> None:
                     help="skip the second (A8W8 or bf16) decode measurement")
     ap.add_argument("--cpu-decode-steps", type=int, default=8)
     ap.add_argument("--cpu-prompt", type=int, default=128, help="prompt length of the CPU sample")
+    ap.add_argument("--counter-probe", action="store_true",
+                    help="only run the short workload profiled with rocprofv3 --pmc, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (batch-1 decode does not "
@@ -206,6 +264,10 @@ def main() -> None:
         sys.exit(2)
 
     import torch
+
+    if args.counter_probe:
+        counter_probe(torch.device("cuda:0"))
+        return
 
     from ppu_amd import synth
     from ppu_amd.generate import FusedGreedyGenerator, cache_bucket
