@@ -767,6 +767,231 @@ __global__ __launch_bounds__(G * 64) void gqa_prefill_mfma(
   }
 }
 
+// ------------------------------------------ causal prefill, 64-key blocks
+// Grid (query tiles of 16 rows, heavy first; KVH; B). A workgroup has 2G
+// waves: wave w serves query head g = w % G of the KV head over key half
+// kh = w / G (keys 32kh..32kh+31 of every 64-key block), with its own online
+// softmax; the two halves of a head are merged in LDS at the end. Per block
+// the K and V rows are staged once for all waves in their natural [key][dim]
+// layout (16-byte stores, double-buffered, one barrier per block; the next
+// block is loaded to registers before the current one is computed).
+//   S = Q K^T: Q rows (A operand) stay in registers, K rows are read from LDS
+//     as the B operand (16 contiguous bytes per lane);
+//   O += P V: P is kept as bf16 hi + lo (~16 mantissa bits, two MFMAs); the
+//     wave writes P^T [key][row] (4 rows = 8 bytes per lane) and reads the A
+//     operand back with the gfx950 transpose read ds_read_b64_tr_b16, which
+//     also turns row-major V into the B operand. Within each 16-lane group g
+//     the read returns to lane 16g + i, element e, the 16-bit word at
+//     address(lane 16g + 4e + i/4) + (i % 4); so lane 16g + 4e + q pointing at
+//     row 8g + 4h + e, column 16t + 4q gives lane 16g + i the 4 rows
+//     8g + 4h .. 8g + 4h + 3 of column 16t + i: read h = 0, 1 fill the 8
+//     consecutive k of an MFMA operand.
+// Keys past the valid end are clamped to the last valid row on load (finite
+// values) and masked to -inf in S, so they add exact zeros.
+typedef short q35_i16x4 __attribute__((ext_vector_type(4)));
+Q35_DEV uint2 lds_read_tr16(const uint16_t* p) {
+  const q35_i16x4 v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) q35_i16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+constexpr int kFaKeys = 64;         // keys per block
+constexpr int kFaRow = kAD + 16;    // padded K/V row in LDS (elements)
+constexpr int kFaPt = 16 + 4;       // padded P^T row (16 query rows)
+
+template <int G>
+__global__ __launch_bounds__(2 * G * 64) void gqa_prefill_fa(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
+    uint16_t* __restrict__ out, int B, int QH, int KVH, int L, int cache_len, int kv_start_host,
+    const long long* __restrict__ valid_len, float scale) {
+  constexpr int NW = 2 * G;
+  constexpr int NT = NW * 64;
+  constexpr int PER = kFaKeys * (kAD / 8) / NT;  // 16-byte K (and V) groups per thread
+  static_assert(PER * NT == kFaKeys * (kAD / 8), "block must split evenly");
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int g = wid % G, kh = wid / G;
+  const int tile = gridDim.x - 1 - blockIdx.x;  // heavy (late) tiles first
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int h = kvh * G + g;
+  const int q0 = tile * 16;
+  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  if (ks < 0) ks = 0;
+  if (ks + L > cache_len) ks = cache_len - L;
+  const int kv_start = (int)ks;
+  const int col = lane & 15;  // A row / B column / C column
+  const int kg = lane >> 4;   // k group of 8 / C row group of 4
+  // transpose-read addressing: lane 16*kg + 4e + tq reads row 4e-offset, column 4tq
+  const int te = (lane & 15) >> 2, tq = lane & 3;
+
+  const uint16_t* qp = q + (((size_t)b * QH + h) * L + min(q0 + col, L - 1)) * kAD + kg * 8;
+  uint4 qa[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) qa[t] = *reinterpret_cast<const uint4*>(qp + 32 * t);
+  int row_abs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) row_abs[i] = kv_start + min(q0 + 4 * kg + i, L - 1);
+  const int n_keys = min(kv_start + min(q0 + 16, L), cache_len);
+  const int nblk = (n_keys + kFaKeys - 1) / kFaKeys;
+  const uint16_t* Kh = Kc + ((size_t)b * KVH + kvh) * cache_len * kAD;
+  const uint16_t* Vh = Vc + ((size_t)b * KVH + kvh) * cache_len * kAD;
+
+  __shared__ alignas(16) uint16_t kv_s[2][2][kFaKeys * kFaRow];  // [buf][K, V][key][dim]
+  __shared__ alignas(16) uint16_t pt_s[NW][2][32 * kFaPt];       // [wave][hi, lo][key][row]
+
+  uint4 kr[PER], vr[PER];
+#define Q35_FA_LOAD(blk)                                                                 \
+  do {                                                                                   \
+    _Pragma("unroll") for (int j = 0; j < PER; ++j) {                                     \
+      const int gi = (int)threadIdx.x + j * NT;                                           \
+      const int key = min((blk) * kFaKeys + (gi >> 5), n_keys - 1);                       \
+      const size_t off = (size_t)key * kAD + (gi & 31) * 8;                               \
+      kr[j] = *reinterpret_cast<const uint4*>(Kh + off);                                  \
+      vr[j] = *reinterpret_cast<const uint4*>(Vh + off);                                  \
+    }                                                                                     \
+  } while (0)
+#define Q35_FA_STORE(buf)                                                                \
+  do {                                                                                   \
+    _Pragma("unroll") for (int j = 0; j < PER; ++j) {                                     \
+      const int gi = (int)threadIdx.x + j * NT;                                           \
+      const int off = (gi >> 5) * kFaRow + (gi & 31) * 8;                                 \
+      *reinterpret_cast<uint4*>(&kv_s[buf][0][off]) = kr[j];                              \
+      *reinterpret_cast<uint4*>(&kv_s[buf][1][off]) = vr[j];                              \
+    }                                                                                     \
+  } while (0)
+
+  q35_f32x4 o[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) o[d] = {0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+  }
+  uint16_t* pt_hi = pt_s[wid][0];
+  uint16_t* pt_lo = pt_s[wid][1];
+
+  Q35_FA_LOAD(0);
+  Q35_FA_STORE(0);
+  __syncthreads();
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int buf = blk & 1;
+    Q35_FA_LOAD(min(blk + 1, nblk - 1));  // in flight while this block is computed
+    const uint16_t* Ks = kv_s[buf][0] + 32 * kh * kFaRow;
+    const uint16_t* Vs = kv_s[buf][1] + 32 * kh * kFaRow;
+    const int kb = blk * kFaKeys + 32 * kh;  // first key of this wave's half
+    // S = Q K^T over the wave's 32 keys (two 16-key column tiles).
+    q35_f32x4 s[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      s[st] = {0.f, 0.f, 0.f, 0.f};
+      const uint16_t* krow = Ks + (16 * st + col) * kFaRow + 8 * kg;
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        s[st] = mfma_16x16x32(qa[t], *reinterpret_cast<const uint4*>(krow + 32 * t), s[st]);
+    }
+    // Online softmax per row; P^T as bf16 hi + lo, 4 rows (8 bytes) per store.
+    float corr[4], p[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sv[2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int key = kb + 16 * st + col;
+        sv[st] = (key <= row_abs[i] && key < n_keys) ? s[st][i] * scale : -INFINITY;
+      }
+      const float m_new = fmaxf(m[i], row16_max(fmaxf(sv[0], sv[1])));
+      // A row without any valid key so far keeps m = -inf: subtract 0 then.
+      const float m_sub = m_new == -INFINITY ? 0.f : m_new;
+      corr[i] = expf(m[i] - m_sub);
+      p[0][i] = expf(sv[0] - m_sub);
+      p[1][i] = expf(sv[1] - m_sub);
+      l[i] = l[i] * corr[i] + row16_sum(p[0][i] + p[1][i]);
+      m[i] = m_new;
+    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      float hi[4], lo[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        hi[i] = round_bf(p[st][i]);
+        lo[i] = p[st][i] - hi[i];
+      }
+      const int off = (16 * st + col) * kFaPt + 4 * kg;
+      *reinterpret_cast<uint2*>(pt_hi + off) = make_uint2(pack_bf2(hi[0], hi[1]), pack_bf2(hi[2], hi[3]));
+      *reinterpret_cast<uint2*>(pt_lo + off) = make_uint2(pack_bf2(lo[0], lo[1]), pack_bf2(lo[2], lo[3]));
+    }
+    // P operand (rows x 32 keys) back through the transpose read; the wave's
+    // own LDS stores above complete before its later reads (in-order LDS).
+    uint4 pa_hi, pa_lo;
+    {
+      const int off0 = (8 * kg + te) * kFaPt + 4 * tq;
+      const int off1 = (8 * kg + 4 + te) * kFaPt + 4 * tq;
+      const uint2 h0 = lds_read_tr16(pt_hi + off0), h1 = lds_read_tr16(pt_hi + off1);
+      const uint2 l0 = lds_read_tr16(pt_lo + off0), l1 = lds_read_tr16(pt_lo + off1);
+      pa_hi = make_uint4(h0.x, h0.y, h1.x, h1.y);
+      pa_lo = make_uint4(l0.x, l0.y, l1.x, l1.y);
+    }
+    // O += P V; V rows 8kg + 4h + te of the wave's half, dims 16d + 4tq.
+    const uint16_t* v0 = Vs + (8 * kg + te) * kFaRow + 4 * tq;
+    const uint16_t* v1 = Vs + (8 * kg + 4 + te) * kFaRow + 4 * tq;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[d][i] *= corr[i];
+      const uint2 a = lds_read_tr16(v0 + 16 * d), c = lds_read_tr16(v1 + 16 * d);
+      const uint4 vb = make_uint4(a.x, a.y, c.x, c.y);
+      o[d] = mfma_16x16x32(pa_hi, vb, o[d]);
+      o[d] = mfma_16x16x32(pa_lo, vb, o[d]);
+    }
+    Q35_FA_STORE(buf ^ 1);
+    __syncthreads();
+  }
+#undef Q35_FA_LOAD
+#undef Q35_FA_STORE
+
+  // Merge the two key halves of each head: half 1 leaves (O, m, l) in LDS
+  // (the K/V buffers are free after the last barrier), half 0 combines and
+  // writes out[b, row, h*D + 16d + col] = bf16(O / l) for the valid rows.
+  float* mo = reinterpret_cast<float*>(&kv_s[0][0][0]);  // [G][16 rows][kAD]
+  float* ml = mo + G * 16 * kAD;                           // [G][16 rows][2]
+  if (kh == 1) {
+#pragma unroll
+    for (int d = 0; d < 16; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mo[(g * 16 + 4 * kg + i) * kAD + 16 * d + col] = o[d][i];
+    if (col == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ml[(g * 16 + 4 * kg + i) * 2] = m[i];
+        ml[(g * 16 + 4 * kg + i) * 2 + 1] = l[i];
+      }
+    }
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = q0 + 4 * kg + i;
+      const float m1 = ml[(g * 16 + 4 * kg + i) * 2], l1 = ml[(g * 16 + 4 * kg + i) * 2 + 1];
+      const float mm = fmaxf(m[i], m1);
+      const float f0 = m[i] == -INFINITY ? 0.f : expf(m[i] - mm);
+      const float f1 = m1 == -INFINITY ? 0.f : expf(m1 - mm);
+      const float inv = 1.0f / (l[i] * f0 + l1 * f1);
+      if (r < L) {
+        uint16_t* orow = out + ((size_t)b * L + r) * QH * kAD + h * kAD + col;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+          const float v = o[d][i] * f0 + mo[(g * 16 + 4 * kg + i) * kAD + 16 * d + col] * f1;
+          orow[16 * d] = (uint16_t)f2bf(v * inv);
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------- causal prefill
 // q [B, QH, L, D], K/V [B, KVH, cache_len, D] (the prompt at cache offset
 // kv_start), out [B, L, QH*D]. Query row i of a head attends to keys
@@ -995,11 +1220,17 @@ int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int 
                                                      (const uint16_t*)V, (uint16_t*)out, B, QH, KVH, \
                                                      L, cache_len, kv_start,                       \
                                                      (const long long*)valid_len, scale)
+#define Q35_FA(GG)                                                                                \
+  gqa_prefill_fa<GG><<<grid, 2 * GG * 64, 0, stream>>>((const uint16_t*)q, (const uint16_t*)K,     \
+                                                       (const uint16_t*)V, (uint16_t*)out, B, QH,    \
+                                                       KVH, L, cache_len, kv_start,                  \
+                                                       (const long long*)valid_len, scale)
     if (G == 1) Q35_PF(1);
-    else if (G == 2) Q35_PF(2);
-    else if (G == 4) Q35_PF(4);
+    else if (G == 2) Q35_FA(2);
+    else if (G == 4) Q35_FA(4);
     else Q35_PF(8);
 #undef Q35_PF
+#undef Q35_FA
     return q35_last_error();
   }
   const long long waves = (long long)B * QH * L;
