@@ -526,16 +526,17 @@ __global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qk
 // with a <= b, so nothing overflows). Padding tokens past L carry k = q = v =
 // 0, g = 0, beta = 0 and leave S unchanged.
 //   delta_chunk_prep : one workgroup per (chunk, head): A and P from K K^T and
-//     K Q^T, T by forward substitution (one wave, lane = column), W^T and U0,
-//     and Q' = diag(gamma) Q, K''^T, all written in the per-lane order of the
-//     MFMA operands that delta_chunk_scan consumes (coalesced float4 loads).
+//     K Q^T, T by 16 x 16 blocks (diagonal blocks by forward substitution,
+//     the rest as MFMA products), W^T and U0, and Q' = diag(gamma) Q, K''^T,
+//     all written in the per-lane order of the MFMA operands that
+//     delta_chunk_scan consumes (coalesced float4 loads).
 //   delta_chunk_scan : one workgroup per (16-column v tile, head): the
 //     [128 x 16] state tile in LDS, the three chunk products per chunk.
 // MFMA 16x16x4 f32 (wave64): A[16x4]: lane l holds row l%16, k l/16;
 // B[4x16]: k l/16, column l%16; C: rows 4*(l/16) + e, column l%16.
 constexpr int kChunk = 64;
 constexpr int kCS = 132;  // fp32 row stride of the K / Q / V chunk tiles in LDS
-constexpr int kAS = 68;   // fp32 row stride of A, then T
+constexpr int kAS = 68;   // fp32 row stride of A and of T
 constexpr int kSS = 17;   // fp32 row stride of the state and U tiles in LDS
 // Workspace floats per (batch, head, chunk): W^T, Q', K''^T, P, U0.
 constexpr int kOffWT = 0, kOffQP = 8192, kOffKT = 16384, kOffPQ = 24576, kOffU0 = 28672;
@@ -559,7 +560,9 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   __shared__ alignas(16) float Kh[kChunk * kCS];
   __shared__ alignas(16) float Qh[kChunk * kCS];
   __shared__ alignas(16) float Vv[kChunk * kCS];
-  __shared__ alignas(16) float Am[kChunk * kAS];
+  __shared__ alignas(16) float Am[kChunk * kAS];  // A (strictly lower)
+  __shared__ alignas(16) float Tm[kChunk * kAS];  // T = (I + A)^{-1} (lower)
+  __shared__ alignas(16) float Xs[4][16 * 17];     // per-wave 16 x 16 scratch
   __shared__ float G_s[kChunk], gam_s[kChunk], kf_s[kChunk], bg_s[kChunk], b_s[kChunk];
 
   // 1. the chunk's k, q (scaled as the recurrence scales them) and v in fp32.
@@ -619,21 +622,35 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   __syncthreads();
 
   float* wsb = ws + bhc * kChunkFloats;
-  // 3. A (into LDS) and P (to the workspace) for the lower block triangle:
-  //    wave w owns the 16 rows of row tile w.
+  // 3. A (into LDS) and P (to the workspace) on the 10 tiles (rt, jt <= rt)
+  //    of the lower block triangle, 3/3/2/2 tiles per wave. Operands are
+  //    float4 reads of 4 consecutive dims: lane (col, g4) feeds dims
+  //    16s + 4g4 + e to MFMA e of step s, for both operands.
   {
-    const int rt = wid;
-    for (int jt = 0; jt <= rt; ++jt) {
-      q35_f32x4 kk = {0.f, 0.f, 0.f, 0.f}, kq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-      for (int s = 0; s < 32; ++s) {
-        const int d = 4 * s + g4;
-        const float k_i = Kh[(16 * rt + col) * kCS + d];
-        const float k_j = Kh[(16 * jt + col) * kCS + d];
-        const float q_i = Qh[(16 * rt + col) * kCS + d];
-        kk = mfma4(k_i, k_j, kk);  // (K K^T)[i][j]
-        kq = mfma4(k_j, q_i, kq);  // (K Q^T)[j][i]
+    const unsigned packed = wid == 0 ? 0x540u : (wid == 1 ? 0xA98u : (wid == 2 ? 0x0DCu : 0x0FEu));
+    const int count = wid < 2 ? 3 : 2;
+    for (int n = 0; n < count; ++n) {
+      const int tj = (packed >> (4 * n)) & 15;
+      const int rt = tj >> 2, jt = tj & 3;
+      q35_f32x4 kk0 = {0.f, 0.f, 0.f, 0.f}, kk1 = kk0, kq0 = kk0, kq1 = kk0;
+      const float* ki = &Kh[(16 * rt + col) * kCS + 4 * g4];
+      const float* kj = &Kh[(16 * jt + col) * kCS + 4 * g4];
+      const float* qi = &Qh[(16 * rt + col) * kCS + 4 * g4];
+#pragma unroll 4
+      for (int st = 0; st < 8; ++st) {
+        const float4 x = *reinterpret_cast<const float4*>(ki + 16 * st);
+        const float4 y = *reinterpret_cast<const float4*>(kj + 16 * st);
+        const float4 z = *reinterpret_cast<const float4*>(qi + 16 * st);
+        kk0 = mfma4(x.x, y.x, kk0);  // (K K^T)[i][j]
+        kq0 = mfma4(y.x, z.x, kq0);  // (K Q^T)[j][i]
+        kk1 = mfma4(x.y, y.y, kk1);
+        kq1 = mfma4(y.y, z.y, kq1);
+        kk0 = mfma4(x.z, y.z, kk0);
+        kq0 = mfma4(y.z, z.z, kq0);
+        kk1 = mfma4(x.w, y.w, kk1);
+        kq1 = mfma4(y.w, z.w, kq1);
       }
+      const q35_f32x4 kk = kk0 + kk1, kq = kq0 + kq1;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 16 * rt + 4 * g4 + e, j = 16 * jt + col;
@@ -655,56 +672,84 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   }
   __syncthreads();
 
-  // 4. T = (I + A)^{-1}: forward substitution, lane = column, T column in
-  //    registers; A rows are broadcast LDS reads. T overwrites A.
-  if (wid == 0) {
-    float t[kChunk];
+  // 4. T = (I + A)^{-1} by 16 x 16 blocks (A strictly lower triangular):
+  //    T_II = (I + A_II)^{-1} by forward substitution (wave I, lane = column),
+  //    then T_IJ = -T_II sum_{K=J}^{I-1} A_IK T_KJ level by level (I - J =
+  //    1, 2, 3) as 16 x 16 x 16 MFMA products, one block per wave.
+  {
+    const int I = wid, j = lane & 15;
+    float t[16];
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (int i = 0; i < 16; ++i) {
+      float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-      for (int j = 0; j + 3 < i; j += 4) {
-        const float4 a = *reinterpret_cast<const float4*>(&Am[i * kAS + j]);
-        a0 = fmaf(a.x, t[j], a0);
-        a1 = fmaf(a.y, t[j + 1], a1);
-        a2 = fmaf(a.z, t[j + 2], a2);
-        a3 = fmaf(a.w, t[j + 3], a3);
+      for (int k = 0; k + 1 < i; k += 2) {
+        a0 = fmaf(Am[(16 * I + i) * kAS + 16 * I + k], t[k], a0);
+        a1 = fmaf(Am[(16 * I + i) * kAS + 16 * I + k + 1], t[k + 1], a1);
       }
-#pragma unroll
-      for (int j = i & ~3; j < i; ++j) a0 = fmaf(Am[i * kAS + j], t[j], a0);
-      t[i] = (lane == i ? 1.f : 0.f) - ((a0 + a1) + (a2 + a3));
+      if (i & 1) a0 = fmaf(Am[(16 * I + i) * kAS + 16 * I + i - 1], t[i - 1], a0);
+      t[i] = (i == j ? 1.f : 0.f) - (a0 + a1);
     }
+    if (lane < 16) {
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) Am[i * kAS + lane] = t[i];
+      for (int i = 0; i < 16; ++i) Tm[(16 * I + i) * kAS + 16 * I + j] = t[i];
+    }
   }
   __syncthreads();
+  // C += A B for 16 x 16 tiles in LDS (A row stride kAS, B row stride sb).
+  auto mm16 = [&](const float* at, const float* bt, int sb, q35_f32x4 c) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) c = mfma4(at[col * kAS + 4 * st + g4], bt[(4 * st + g4) * sb + col], c);
+    return c;
+  };
+  for (int d = 1; d < 4; ++d) {
+    if (wid < 4 - d) {
+      const int J = wid, I = wid + d;
+      q35_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      for (int K = J; K < I; ++K) x = mm16(&Am[16 * I * kAS + 16 * K], &Tm[16 * K * kAS + 16 * J], kAS, x);
+      float* xs = Xs[wid];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xs[(4 * g4 + e) * 17 + col] = x[e];
+      // the wave's own LDS stores complete before its later reads (in-order LDS)
+      const q35_f32x4 tt = mm16(&Tm[16 * I * kAS + 16 * I], xs, 17, q35_f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Tm[(16 * I + 4 * g4 + e) * kAS + 16 * J + col] = -tt[e];
+    }
+    __syncthreads();
+  }
 
   // 5. W^T = K^T diag(beta gamma) T^T and U0 = T diag(beta) V on the matrix
-  //    cores (row tile rt = wave), Q' and K''^T elementwise.
+  //    cores for every (row tile rt, dim tile dt), wave w taking dt = 2w and
+  //    2w + 1 (T is lower triangular: only j < 16(rt + 1) contribute, so the
+  //    work per wave is equal); Q' and K''^T elementwise.
   {
-    const int rt = wid;
-    for (int dt = 0; dt < 8; ++dt) {
-      q35_f32x4 w = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int s = 0; s < 16; ++s) {
-        const int j = 4 * s + g4;
-        const float tij = Am[(16 * rt + col) * kAS + j];
-        w = mfma4(bg_s[j] * Kh[j * kCS + 16 * dt + col], tij, w);
-        u = mfma4(tij, b_s[j] * Vv[j * kCS + 16 * dt + col], u);
-      }
-      *reinterpret_cast<float4*>(wsb + kOffWT + ((rt * 8 + dt) * 64 + lane) * 4) =
-          make_float4(w[0], w[1], w[2], w[3]);
-      *reinterpret_cast<float4*>(wsb + kOffU0 + ((rt * 8 + dt) * 64 + lane) * 4) =
-          make_float4(u[0], u[1], u[2], u[3]);
-      const int i = 16 * rt + col;
-      const float gi = gam_s[i];
-      const float* qrow = &Qh[i * kCS + 16 * dt + 4 * g4];
-      *reinterpret_cast<float4*>(wsb + kOffQP + ((rt * 8 + dt) * 64 + lane) * 4) =
-          make_float4(qrow[0] * gi, qrow[1] * gi, qrow[2] * gi, qrow[3] * gi);
-    }
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd) {
       const int dt = 2 * wid + dd;
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        q35_f32x4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = w0, u0 = w0, u1 = w0;
+#pragma unroll
+        for (int st = 0; st < 4 * (rt + 1); st += 2) {
+          const int j0 = 4 * st + g4, j1 = j0 + 4;
+          const float t0 = Tm[(16 * rt + col) * kAS + j0];
+          const float t1 = Tm[(16 * rt + col) * kAS + j1];
+          w0 = mfma4(bg_s[j0] * Kh[j0 * kCS + 16 * dt + col], t0, w0);
+          u0 = mfma4(t0, b_s[j0] * Vv[j0 * kCS + 16 * dt + col], u0);
+          w1 = mfma4(bg_s[j1] * Kh[j1 * kCS + 16 * dt + col], t1, w1);
+          u1 = mfma4(t1, b_s[j1] * Vv[j1 * kCS + 16 * dt + col], u1);
+        }
+        const q35_f32x4 w = w0 + w1, u = u0 + u1;
+        *reinterpret_cast<float4*>(wsb + kOffWT + ((rt * 8 + dt) * 64 + lane) * 4) =
+            make_float4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<float4*>(wsb + kOffU0 + ((rt * 8 + dt) * 64 + lane) * 4) =
+            make_float4(u[0], u[1], u[2], u[3]);
+        const int i = 16 * rt + col;
+        const float gi = gam_s[i];
+        const float* qrow = &Qh[i * kCS + 16 * dt + 4 * g4];
+        *reinterpret_cast<float4*>(wsb + kOffQP + ((rt * 8 + dt) * 64 + lane) * 4) =
+            make_float4(qrow[0] * gi, qrow[1] * gi, qrow[2] * gi, qrow[3] * gi);
+      }
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         float v[4];
