@@ -45,6 +45,14 @@ int q35_residual_rmsnorm(const void* residual, const void* update, const void* w
 int q35_gated_rmsnorm(const void* x, const void* gate, const void* w, int w_f32, void* y,
                       int rows, int width, float eps, void* stream);
 
+/* Gated RMSNorm over 128-wide rows whose gate sits inside a wider packed row:
+ * gate row r at gate + (r / group_rows) * group_stride + (r % group_rows) * 128
+ * (elements). The prefill form of the call at qwen35_fused/integration.py:264-271,
+ * where z is a slice of the packed projection (no copy of z). */
+int q35_gated_rmsnorm_grouped(const void* x, const void* gate, int group_rows,
+                              long long group_stride, const void* w, int w_f32, void* y, int rows,
+                              float eps, void* stream);
+
 /* silu_and_mul: out[r, c] = bf16(bf16(silu(p[r, c])) * p[r, width + c]).
  * Replaces qwen35_fused/kernels.py:170 (kernel :158-180). */
 int q35_silu_mul(const void* packed, void* out, long long rows, int width, void* stream);

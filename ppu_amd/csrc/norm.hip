@@ -145,18 +145,23 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_reg(const uint16_t* __restri
 
 // Gated RMSNorm over rows of exactly 128 (one head): 16 lanes per row, 8
 // elements per lane, 4 rows per wave; the sum of squares is a DPP row sum.
+// The gate of row r is read at (r / group_rows) * group_stride +
+// (r % group_rows) * 128, so a gate that sits inside a wider packed row per
+// token (group_rows heads per token) is read in place.
 __global__ __launch_bounds__(256) void gated_rmsnorm_rows128(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ gate,
                                                              const void* __restrict__ w, int w_f32,
                                                              uint16_t* __restrict__ y, int rows,
-                                                             float eps) {
+                                                             float eps, int group_rows,
+                                                             long long group_stride) {
   const int lane = threadIdx.x & 63;
   const int row = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * 4 + (lane >> 4);
   const int k = (lane & 15) * 8;
   const int rc = min(row, rows - 1);
   const size_t base = (size_t)rc * 128 + k;
+  const size_t gbase = (size_t)(rc / group_rows) * group_stride + (size_t)(rc % group_rows) * 128 + k;
   const uint4 xr = *reinterpret_cast<const uint4*>(x + base);
-  const uint4 gr = *reinterpret_cast<const uint4*>(gate + base);
+  const uint4 gr = *reinterpret_cast<const uint4*>(gate + gbase);
   float wf[8];
   if (w_f32) {
     const float4 w0 = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + k);
@@ -316,12 +321,27 @@ int q35_gated_rmsnorm(const void* x, const void* gate, const void* w, int w_f32,
       q35_aligned16(w)) {
     const int grid4 = (rows + 4 * kWaves - 1) / (4 * kWaves);
     gated_rmsnorm_rows128<<<grid4, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)gate, w,
-                                                     w_f32, (uint16_t*)y, rows, eps);
+                                                     w_f32, (uint16_t*)y, rows, eps, rows,
+                                                     (long long)rows * 128);
     return q35_last_error();
   }
   const int grid = (rows + kWaves - 1) / kWaves;
   gated_rmsnorm_rows<<<grid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)gate, w, w_f32,
                                                (uint16_t*)y, rows, width, eps);
+  return q35_last_error();
+}
+
+int q35_gated_rmsnorm_grouped(const void* x, const void* gate, int group_rows,
+                              long long group_stride, const void* w, int w_f32, void* y, int rows,
+                              float eps, hipStream_t stream) {
+  Q35_CHECK_ARG(rows >= 0 && group_rows > 0 && group_stride >= (long long)group_rows * 128);
+  Q35_CHECK_ARG(group_stride % 8 == 0 && q35_aligned16(x) && q35_aligned16(gate) &&
+                q35_aligned16(y) && q35_aligned16(w));
+  if (rows == 0) return 0;
+  const int grid4 = (rows + 4 * kWaves - 1) / (4 * kWaves);
+  gated_rmsnorm_rows128<<<grid4, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)gate, w,
+                                                   w_f32, (uint16_t*)y, rows, eps, group_rows,
+                                                   group_stride);
   return q35_last_error();
 }
 

@@ -266,10 +266,17 @@ def _patch_delta(module: torch.nn.Module, config: FusionConfig) -> None:
         core = K.delta_recurrent_fused(qkv, packed, self.A_log, self.dt_bias, recurrent_state,
                                        block_v=config.delta_block_v,
                                        precompute_factors=config.delta_precompute_factors)
-        z_start = self.conv_dim
-        z = packed[..., z_start : z_start + self.value_dim].reshape(-1, self.head_v_dim).contiguous()
-        core = K.gated_rms_norm(core.reshape(-1, self.head_v_dim), z, self.norm.weight,
-                                self.layer_norm_epsilon)
+        core = core.reshape(-1, self.head_v_dim)
+        if self.head_v_dim == 128:
+            # z read in place from the packed projection (no copy)
+            core = K.gated_rms_norm_packed(core, packed, self.conv_dim,
+                                           self.value_dim // self.head_v_dim, self.norm.weight,
+                                           self.layer_norm_epsilon)
+        else:
+            z_start = self.conv_dim
+            z = packed[..., z_start : z_start + self.value_dim].reshape(-1, self.head_v_dim)
+            core = K.gated_rms_norm(core, z.contiguous(), self.norm.weight,
+                                    self.layer_norm_epsilon)
         return self._q35_out(core.reshape(batch, seq_len, self.value_dim))
 
     module.forward = types.MethodType(forward, module)

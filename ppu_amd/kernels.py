@@ -113,6 +113,39 @@ def gated_rms_norm(
     return out
 
 
+def gated_rms_norm_packed(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    gate_offset: int,
+    heads: int,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """Gated RMSNorm of ``x`` [tokens * heads, 128] whose gate of (token, head)
+    is ``packed[token, gate_offset + head * 128 : ... + 128]``, read in place
+    from the packed projection (the prefill form of reference
+    integration.py:264-271, without the copy of z)."""
+
+    rows, width = _rows_and_width(x)
+    if width != 128:
+        raise ValueError("the packed gated norm runs over 128-wide heads")
+    if not x.is_contiguous() or not packed.is_contiguous():
+        raise ValueError("x and packed must be contiguous")
+    stride = packed.shape[-1]
+    tokens = packed.numel() // stride
+    if rows != tokens * heads or gate_offset < 0 or gate_offset + heads * 128 > stride:
+        raise ValueError("gate slice does not match the packed rows")
+    if weight.numel() != width:
+        raise ValueError(f"weight has {weight.numel()} values, expected {width}")
+    _need_bf16(x, packed)
+    w, wf = _param(weight)
+    out = torch.empty_like(x)
+    gate = packed.reshape(-1)[gate_offset:]
+    _lib.call("q35_gated_rmsnorm_grouped", x.data_ptr(), gate.data_ptr(), heads, stride,
+              w.data_ptr(), wf, out.data_ptr(), rows, float(eps), _stream(x))
+    return out
+
+
 def silu_and_mul(packed: torch.Tensor) -> torch.Tensor:
     """SiLU of the first half times the second half. reference kernels.py:170."""
 

@@ -78,6 +78,24 @@ def test_gated_rms_norm(gpu):
     close(K.gated_rms_norm(x.to(gpu), gate.to(gpu), w.to(gpu)), ref.gated_rms_norm(x, gate, w))
 
 
+def test_gated_rms_norm_packed(gpu):
+    """The prefill form reads z in place from the packed projection [L, 8320]
+    (z = columns 6144..8191, 16 heads of 128): same bits as the copied z."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 6)
+    tokens, heads = 37, 16
+    core = randn(g, tokens * heads, 128)
+    packed = randn(g, 1, tokens, 8320)
+    w = randn(g, 128, scale=0.02, mean=1.0)
+    z = packed[..., 6144:8192].reshape(tokens * heads, 128)
+    exp = ref.gated_rms_norm(core, z, w)
+    got = K.gated_rms_norm_packed(core.to(gpu), packed.to(gpu), 6144, heads, w.to(gpu))
+    close(got, exp)
+    copied = K.gated_rms_norm(core.to(gpu), z.contiguous().to(gpu), w.to(gpu))
+    assert torch.equal(got, copied)
+
+
 def test_silu_and_mul(gpu):
     from ppu_amd import kernels as K
 
