@@ -202,102 +202,97 @@ __global__ __launch_bounds__(256) void delta_decode(const DeltaArgs p) {
   }
 }
 
-// Delta rule only (input already convolved), split over v: one 256-thread
-// workgroup per (batch, head, 32-column v tile), 4 tiles per head, so 4x more
-// CUs stream the state than with one workgroup per head. Thread t owns
-// columns 4*(t%8)..+3 of the tile for rows (t/8) + 32*i, i = 0..3: each row
-// segment of a tile is 128 contiguous bytes read by 8 lanes with 16-byte loads.
-// Every workgroup recomputes the head's norm factors and gates (q, k are 512
-// bytes from L2); the state is read once and written once.
-constexpr int kVT = 32;
+// Delta rule only (input already convolved), one wave64 per (batch, head,
+// 8-column v tile): 16 waves per head, 256 for the 2B shape, so the whole chip
+// streams the state. Lane (rg = lane/2, cq = lane%2) owns state rows rg + 32i
+// (i < 4), columns 8*tile + 4cq .. +3 (16-byte loads; a row segment of the
+// tile is 32 contiguous bytes). Every reduction over the 128 k rows is
+// in-thread (4 rows) plus the 32 lanes of equal cq (xor shuffles over lane
+// bits 1..5), so the kernel has no barrier and no LDS. Each wave recomputes
+// the head's norm factors and gates (q, k are 512 bytes from L2); the state
+// is read once and written once.
+constexpr int kWT = 8;  // v columns per wave
 
-__global__ __launch_bounds__(256) void delta_decode_tiled(const DeltaArgs p) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wid = tid >> 6;
-  const int tiles = kD / kVT;
+Q35_DEV float4 xor_sum_rows(float4 v) {
+#pragma unroll
+  for (int off = 2; off < 64; off <<= 1) {
+    v.x += __shfl_xor(v.x, off);
+    v.y += __shfl_xor(v.y, off);
+    v.z += __shfl_xor(v.z, off);
+    v.w += __shfl_xor(v.w, off);
+  }
+  return v;
+}
+
+template <bool PF32>  // gate parameters (A_log, dt_bias) fp32, else bf16
+__global__ __launch_bounds__(64) void delta_decode_wave(const DeltaArgs p) {
+  const int lane = threadIdx.x;
+  const int tiles = kD / kWT;
   const int tile = blockIdx.x % tiles;
   const int bh = blockIdx.x / tiles;
   const int b = bh / p.H, h = bh - b * p.H;
-  const int vq = tid & 7;
-  const int kg = tid >> 3;  // 0..31
-  const int c0 = tile * kVT + 4 * vq;
+  const int rg = lane >> 1, cq = lane & 1;
+  const int c0 = tile * kWT + 4 * cq;
 
-  __shared__ float qs[kD], ks[kD], vs[kVT];
-  __shared__ float red[4][kVT];
-  __shared__ float sc[4];
-
+  // The small loads (q, k, v, gate inputs) are issued before the state: loads
+  // retire in order, so the norms and gates are computed while the state is
+  // still in flight.
+  const uint16_t* srow = p.src + (size_t)b * p.src_stride;
+  const float q0 = bf2f(srow[h * kD + lane]), q1 = bf2f(srow[h * kD + 64 + lane]);
+  const float k0 = bf2f(srow[p.H * kD + h * kD + lane]), k1 = bf2f(srow[p.H * kD + h * kD + 64 + lane]);
+  const uint16_t* vsrc = srow + 2 * p.H * kD + h * kD + c0;
+  const float v0 = bf2f(vsrc[0]), v1 = bf2f(vsrc[1]), v2 = bf2f(vsrc[2]), v3 = bf2f(vsrc[3]);
+  const uint16_t* prow = p.packed + (size_t)b * p.packed_stride;
+  const float a_in = bf2f(prow[p.a_off + h]), b_in = bf2f(prow[p.b_off + h]);
+  const float a_log = ld_param(p.a_log, h, PF32), dt_b = ld_param(p.dt_bias, h, PF32);
   float* S = p.state + (size_t)bh * kD * kD;
   float4 st[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    st[i] = *reinterpret_cast<const float4*>(S + (size_t)(kg + 32 * i) * kD + c0);
-
-  const uint16_t* srow = p.src + (size_t)b * p.src_stride;
-  if (tid < kD) qs[tid] = bf2f(srow[h * kD + tid]);
-  else ks[tid - kD] = bf2f(srow[p.H * kD + h * kD + tid - kD]);
-  if (tid < kVT) vs[tid] = bf2f(srow[2 * p.H * kD + h * kD + tile * kVT + tid]);
-  __syncthreads();
-  if (wid < 2) {
-    const float* src = wid == 0 ? qs : ks;
-    const float a0 = src[lane], a1 = src[lane + 64];
-    const float tot = wave_sum(a0 * a0 + a1 * a1);
-    if (lane == 0) sc[wid] = rsqrt_cr(tot + 1e-6f);
-  } else if (tid == 128) {
-    const uint16_t* prow = p.packed + (size_t)b * p.packed_stride;
-    const float a = bf2f(prow[p.a_off + h]) + ld_param(p.dt_bias, h, p.params_f32);
-    const float g = -expf(ld_param(p.a_log, h, p.params_f32)) * softplus20(a);
-    sc[2] = expf(g);
-    sc[3] = 1.0f / (1.0f + expf(-bf2f(prow[p.b_off + h])));
+  for (int i = 0; i < 4; ++i) {
+    const q35_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const q35_f32x4*>(S + (size_t)(rg + 32 * i) * kD + c0));
+    st[i] = make_float4(v.x, v.y, v.z, v.w);
   }
-  __syncthreads();
-  const float q_inv = sc[0], k_inv = sc[1], alpha = sc[2], beta = sc[3];
+  __builtin_amdgcn_sched_barrier(0);  // keep every load above the math below
+  const float g = -expf(a_log) * softplus20(a_in + dt_b);
+  const float alpha = expf(g);
+  const float beta = 1.0f / (1.0f + expf(-b_in));
+  const float q_inv = rsqrt_cr(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
+  const float k_inv = rsqrt_cr(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
   const float qscale = 0.08838834764831845f;  // fp32(1/sqrt(128))
+  // row r of q / k sits in lane r % 64, element r / 64
+  float kh[4], qh[4];
+  kh[0] = __shfl(k0, rg) * k_inv;
+  kh[1] = __shfl(k0, rg + 32) * k_inv;
+  kh[2] = __shfl(k1, rg) * k_inv;
+  kh[3] = __shfl(k1, rg + 32) * k_inv;
+  qh[0] = __shfl(q0, rg) * q_inv * qscale;
+  qh[1] = __shfl(q0, rg + 32) * q_inv * qscale;
+  qh[2] = __shfl(q1, rg) * q_inv * qscale;
+  qh[3] = __shfl(q1, rg + 32) * q_inv * qscale;
 
+  // decay, then m = (alpha S)^T k_hat over the 128 rows
   float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float kh = ks[kg + 32 * i] * k_inv;
     st[i].x *= alpha; st[i].y *= alpha; st[i].z *= alpha; st[i].w *= alpha;
-    m.x = fmaf(st[i].x, kh, m.x); m.y = fmaf(st[i].y, kh, m.y);
-    m.z = fmaf(st[i].z, kh, m.z); m.w = fmaf(st[i].w, kh, m.w);
+    m.x = fmaf(st[i].x, kh[i], m.x); m.y = fmaf(st[i].y, kh[i], m.y);
+    m.z = fmaf(st[i].z, kh[i], m.z); m.w = fmaf(st[i].w, kh[i], m.w);
   }
-  // reduce over the 8 k-groups of a wave (lane bits 3..5), then the 4 waves
-#pragma unroll
-  for (int off = 8; off < 64; off <<= 1) {
-    m.x += __shfl_xor(m.x, off); m.y += __shfl_xor(m.y, off);
-    m.z += __shfl_xor(m.z, off); m.w += __shfl_xor(m.w, off);
-  }
-  if (lane < 8) *reinterpret_cast<float4*>(&red[wid][4 * vq]) = m;
-  __syncthreads();
-  if (tid < kVT) {
-    const float mem = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
-    vs[tid] = beta * (vs[tid] - mem);
-  }
-  __syncthreads();
-  const float4 d = *reinterpret_cast<const float4*>(&vs[4 * vq]);
+  m = xor_sum_rows(m);
+  const float4 d = make_float4(beta * (v0 - m.x), beta * (v1 - m.y), beta * (v2 - m.z), beta * (v3 - m.w));
+  // S += k_hat delta^T, o = S^T q_hat
   float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float kh = ks[kg + 32 * i] * k_inv;
-    const float qh = qs[kg + 32 * i] * q_inv * qscale;
-    st[i].x += kh * d.x; st[i].y += kh * d.y; st[i].z += kh * d.z; st[i].w += kh * d.w;
-    o.x = fmaf(st[i].x, qh, o.x); o.y = fmaf(st[i].y, qh, o.y);
-    o.z = fmaf(st[i].z, qh, o.z); o.w = fmaf(st[i].w, qh, o.w);
-    *reinterpret_cast<float4*>(S + (size_t)(kg + 32 * i) * kD + c0) = st[i];
+    st[i].x += kh[i] * d.x; st[i].y += kh[i] * d.y; st[i].z += kh[i] * d.z; st[i].w += kh[i] * d.w;
+    o.x = fmaf(st[i].x, qh[i], o.x); o.y = fmaf(st[i].y, qh[i], o.y);
+    o.z = fmaf(st[i].z, qh[i], o.z); o.w = fmaf(st[i].w, qh[i], o.w);
+    __builtin_nontemporal_store(q35_f32x4{st[i].x, st[i].y, st[i].z, st[i].w},
+                                reinterpret_cast<q35_f32x4*>(S + (size_t)(rg + 32 * i) * kD + c0));
   }
-#pragma unroll
-  for (int off = 8; off < 64; off <<= 1) {
-    o.x += __shfl_xor(o.x, off); o.y += __shfl_xor(o.y, off);
-    o.z += __shfl_xor(o.z, off); o.w += __shfl_xor(o.w, off);
-  }
-  __syncthreads();  // red[] reuse
-  if (lane < 8) *reinterpret_cast<float4*>(&red[wid][4 * vq]) = o;
-  __syncthreads();
-  if (tid < kVT) {
-    const float core = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
-    p.out[(size_t)bh * kD + tile * kVT + tid] = (uint16_t)f2bf(core);
-  }
+  o = xor_sum_rows(o);
+  if (rg == 0)
+    *reinterpret_cast<uint2*>(p.out + (size_t)bh * kD + c0) = make_uint2(pack_bf2(o.x, o.y), pack_bf2(o.z, o.w));
 }
 
 // ------------------------------------------------------------- prefill scan
@@ -976,7 +971,11 @@ int q35_delta_decode(const void* src, int src_stride, const void* packed, int pa
   if (fuse_conv && fuse_gnorm) delta_decode<true, true><<<grid, 256, 0, stream>>>(p);
   else if (fuse_conv) delta_decode<true, false><<<grid, 256, 0, stream>>>(p);
   else if (fuse_gnorm) delta_decode<false, true><<<grid, 256, 0, stream>>>(p);
-  else delta_decode_tiled<<<grid * (kD / kVT), 256, 0, stream>>>(p);
+  else {
+    Q35_CHECK_ARG(q35_aligned8(out));
+    if (params_f32) delta_decode_wave<true><<<grid * (kD / kWT), 64, 0, stream>>>(p);
+    else delta_decode_wave<false><<<grid * (kD / kWT), 64, 0, stream>>>(p);
+  }
   return q35_last_error();
 }
 
