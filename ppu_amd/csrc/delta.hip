@@ -305,32 +305,42 @@ __global__ __launch_bounds__(256) void conv1d_prefill_vec4(const uint16_t* __res
                                                            uint16_t* __restrict__ out, int B, int L,
                                                            int C, int in_stride) {
   constexpr int KW = 4, TOK = 4;
-  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const int cgs = C / 8;
-  const int tgs = (L + TOK - 1) / TOK;
-  if (idx >= (long long)B * tgs * cgs) return;
+  // 32-bit index arithmetic: the host limits the grid to fewer than 2^31 threads.
+  const unsigned idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const unsigned cgs = C / 8;
+  const unsigned tgs = (L + TOK - 1) / TOK;
+  if (idx >= (unsigned)B * tgs * cgs) return;
   const int cg = (int)(idx % cgs);
-  const long long rest = idx / cgs;
+  const unsigned rest = idx / cgs;
   const int tg = (int)(rest % tgs);
   const int b = (int)(rest / tgs);
   const int c = cg * 8;
   const int t0 = tg * TOK;
+  // Every row and tap load is issued before any is used (rows before token 0
+  // are read at row 0 and zeroed by a select): a branch per row would make
+  // the compiler wait for each load in turn.
+  uint4 raw[TOK + KW - 1], wraw[4];
+#pragma unroll
+  for (int r = 0; r < TOK + KW - 1; ++r) {
+    const int sc = min(max(t0 - (KW - 1) + r, 0), L - 1);
+    raw[r] = *reinterpret_cast<const uint4*>(x + ((size_t)b * L + sc) * in_stride + c);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) wraw[q] = *reinterpret_cast<const uint4*>(w + (size_t)c * KW + q * 8);
+  __builtin_amdgcn_sched_barrier(0);  // keep every load above the arithmetic
   float xin[TOK + KW - 1][8];
 #pragma unroll
   for (int r = 0; r < TOK + KW - 1; ++r) {
-    const int src = t0 - (KW - 1) + r;
-    const int sc = min(max(src, 0), L - 1);
-    unpack8(*reinterpret_cast<const uint4*>(x + ((size_t)b * L + sc) * in_stride + c), xin[r]);
-    if (src < 0) {
+    const bool before = t0 - (KW - 1) + r < 0;
+    unpack8(raw[r], xin[r]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xin[r][e] = 0.f;
-    }
+    for (int e = 0; e < 8; ++e) xin[r][e] = before ? 0.f : xin[r][e];
   }
   float wt[8][KW];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     float f[8];
-    unpack8(*reinterpret_cast<const uint4*>(w + (size_t)c * KW + q * 8), f);
+    unpack8(wraw[q], f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) wt[2 * q + e / 4][e % 4] = f[e];
   }
@@ -344,7 +354,7 @@ __global__ __launch_bounds__(256) void conv1d_prefill_vec4(const uint16_t* __res
       float acc = 0.f;
 #pragma unroll
       for (int tap = 0; tap < KW; ++tap) acc = fmaf(xin[j + tap][e], wt[e][tap], acc);
-      o[e] = silu_f(round_bf(acc));
+      o[e] = silu_fast(round_bf(acc));
     }
     *reinterpret_cast<uint4*>(out + ((size_t)b * L + t) * C + c) = pack8(o);
     const int pos = t - (L - KW);
@@ -914,11 +924,10 @@ int q35_conv1d_prefill(const void* x, const void* w, void* state, void* out, int
   Q35_CHECK_ARG(B >= 0 && L > 0 && C > 0 && kw > 0 && kw <= 16 && in_stride >= C);
   const long long total = (long long)B * L * C;
   if (total == 0) return 0;
+  const long long vthreads = (long long)B * ((L + 3) / 4) * (C / 8);
   if (kw == 4 && C % 8 == 0 && in_stride % 8 == 0 && q35_aligned16(x) && q35_aligned16(w) &&
-      q35_aligned16(out)) {
-    const long long threads = (long long)B * ((L + 3) / 4) * (C / 8);
-    const long long g = (threads + 255) / 256;
-    Q35_CHECK_ARG(g < (1ll << 31));
+      q35_aligned16(out) && vthreads < (1ll << 31) - 256) {
+    const long long g = (vthreads + 255) / 256;
     conv1d_prefill_vec4<<<(unsigned)g, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)w,
                                                          (uint16_t*)state, (uint16_t*)out, B, L, C,
                                                          in_stride);

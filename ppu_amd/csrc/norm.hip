@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void silu_mul_vec(const uint16_t* __restrict__
   unpack8(*reinterpret_cast<const uint4*>(packed + row * 2 * width + col), g);
   unpack8(*reinterpret_cast<const uint4*>(packed + row * 2 * width + width + col), up);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = round_bf(silu_f(g[e])) * up[e];
+  for (int e = 0; e < 8; ++e) o[e] = round_bf(silu_fast(g[e])) * up[e];
   *reinterpret_cast<uint4*>(out + row * width + col) = pack8(o);
 }
 

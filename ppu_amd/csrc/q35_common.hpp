@@ -65,6 +65,11 @@ Q35_DEV uint4 ld_stream16(const void* p) {
 // arithmetic torch's CPU rsqrt performs, so norm factors match the oracle.
 Q35_DEV float rsqrt_cr(float x) { return 1.0f / sqrtf(x); }
 Q35_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// SiLU from the hardware exp2 and reciprocal (a few fp32 ulp from silu_f), for
+// the VALU-bound prefill elementwise kernels whose result is rounded to bf16
+// immediately: the fp32 difference moves that rounding only for values within
+// a few ulp of a bf16 rounding boundary.
+Q35_DEV float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 Q35_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // ---------------------------------------------------------------- DPP moves
