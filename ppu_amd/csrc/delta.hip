@@ -798,10 +798,13 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   const int lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g4 = lane >> 4;
   const size_t bh = (size_t)b * H + h;
-  __shared__ alignas(16) float St[16 * kST];
+  // The state tile is double-buffered (chunk c reads St[c & 1] and writes the
+  // new state into the other half), so a chunk needs two barriers: after U is
+  // written and after the new state is written.
+  __shared__ alignas(16) float St2[2][16 * kST];
   __shared__ alignas(16) float Ut[16 * kUT];
   float* Sg = state + bh * kD * kD + tile * 16;
-  for (int idx = tid; idx < kD * 16; idx += 256) St[(idx & 15) * kST + (idx >> 4)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
+  for (int idx = tid; idx < kD * 16; idx += 256) St2[0][(idx & 15) * kST + (idx >> 4)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
   // This wave's operands of one chunk: row tile wid of W^T, Q', P and U0, dk
   // tiles 2*wid and 2*wid+1 of K''^T. Chunk c + 1 is requested before chunk c
   // is computed.
@@ -840,11 +843,13 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   ChunkOps cur;
   load_ops(0, cur);
   __syncthreads();
-  const float* scol = &St[col * kST + 4 * g4];
   float* ucol = &Ut[col * kUT + 4 * g4];
   for (int c = 0; c < nC; ++c) {
     ChunkOps nxt;
     load_ops(min(c + 1, nC - 1), nxt);
+    float* St = St2[c & 1];
+    float* Sn = St2[(c & 1) ^ 1];
+    const float* scol = &St[col * kST + 4 * g4];
 
     // U = U0 - W S (rows 16*wid.., this v tile)
     q35_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
@@ -856,15 +861,16 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
     const float4 uo = make_float4(cur.u0.x - (a0[0] + a1[0]), cur.u0.y - (a0[1] + a1[1]),
                                   cur.u0.z - (a0[2] + a1[2]), cur.u0.w - (a0[3] + a1[3]));
     *reinterpret_cast<float4*>(ucol + 16 * wid) = uo;
-    __syncthreads();
 
-    // O = Q' S + P U
+    // O = Q' S + P U; Q' S needs only S, so it runs before the barrier that
+    // waits for every wave's U.
     q35_f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);
       mma4(cur.qp[dt], sv, o0, o1, o0, o1);
     }
+    __syncthreads();
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
       if (jt <= wid) {
@@ -893,15 +899,15 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
       }
       sn[dd] = s0 + s1;
     }
-    __syncthreads();  // every wave has read S and U of this chunk
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd)
-      *reinterpret_cast<float4*>(&St[col * kST + 16 * (2 * wid + dd) + 4 * g4]) =
+      *reinterpret_cast<float4*>(&Sn[col * kST + 16 * (2 * wid + dd) + 4 * g4]) =
           make_float4(sn[dd][0], sn[dd][1], sn[dd][2], sn[dd][3]);
-    __syncthreads();
+    __syncthreads();  // the new state is complete; U and the old state are free
     cur = nxt;
   }
-  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = St[(idx & 15) * kST + (idx >> 4)];
+  const float* Sf = St2[nC & 1];
+  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = Sf[(idx & 15) * kST + (idx >> 4)];
 }
 
 }  // namespace
