@@ -215,7 +215,12 @@ int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, i
  * qwen35_fused/integration.py:360-372. */
 int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int B, int QH, int KVH,
                     int D, int L, int cache_len, int kv_start, const void* valid_len, float scale,
-                    void* stream);
+                    void* workspace, long long workspace_floats, void* stream);
+
+/* Floats of workspace q35_gqa_prefill uses to split the key range of long
+ * query tiles across workgroups (0: no split applies). With a smaller or
+ * null workspace the call still runs, without splitting. */
+long long q35_gqa_prefill_workspace(int B, int QH, int KVH, int L, int cache_len);
 
 /* ---- A8W8 -------------------------------------------------------------- */
 

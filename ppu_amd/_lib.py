@@ -57,7 +57,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_gqa_decode_splits": (_I, [_I, _I, ctypes.POINTER(_I)]),
     "q35_gqa_decode_workspace": (_L, [_I, _I, _I, _I]),
     "q35_gqa_decode": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _L, _I, _I, _I, _I, _P]),
-    "q35_gqa_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _F, _P]),
+    "q35_gqa_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _F, _P, _L, _P]),
+    "q35_gqa_prefill_workspace": (_L, [_I, _I, _I, _I, _I]),
     "q35_gqa_decode_fused": (
         _I,
         [_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P, _L, _I, _I, _I, _I,

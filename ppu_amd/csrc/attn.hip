@@ -803,7 +803,8 @@ template <int G>
 __global__ __launch_bounds__(2 * G * 64) void gqa_prefill_fa(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
     uint16_t* __restrict__ out, int B, int QH, int KVH, int L, int cache_len, int kv_start_host,
-    const long long* __restrict__ valid_len, float scale) {
+    const long long* __restrict__ valid_len, float scale, int sb, int smax,
+    float* __restrict__ part) {
   constexpr int NW = 2 * G;
   constexpr int NT = NW * 64;
   constexpr int PER = kFaKeys * (kAD / 8) / NT;  // 16-byte K (and V) groups per thread
@@ -811,7 +812,9 @@ __global__ __launch_bounds__(2 * G * 64) void gqa_prefill_fa(
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int g = wid % G, kh = wid / G;
-  const int tile = gridDim.x - 1 - blockIdx.x;  // heavy (late) tiles first
+  const int ntiles = gridDim.x / smax;
+  const int tile = ntiles - 1 - (int)blockIdx.x / smax;  // heavy (late) tiles first
+  const int split = (int)blockIdx.x % smax;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
   const int h = kvh * G + g;
@@ -834,6 +837,10 @@ __global__ __launch_bounds__(2 * G * 64) void gqa_prefill_fa(
   for (int i = 0; i < 4; ++i) row_abs[i] = kv_start + min(q0 + 4 * kg + i, L - 1);
   const int n_keys = min(kv_start + min(q0 + 16, L), cache_len);
   const int nblk = (n_keys + kFaKeys - 1) / kFaKeys;
+  // This workgroup's key blocks [b0, b1) of the tile (sb blocks per split).
+  const int nsplit = (nblk + sb - 1) / sb;
+  if (split >= nsplit) return;  // whole workgroup: no barrier is skipped
+  const int b0 = split * sb, b1 = min(b0 + sb, nblk);
   const uint16_t* Kh = Kc + ((size_t)b * KVH + kvh) * cache_len * kAD;
   const uint16_t* Vh = Vc + ((size_t)b * KVH + kvh) * cache_len * kAD;
 
@@ -873,12 +880,12 @@ __global__ __launch_bounds__(2 * G * 64) void gqa_prefill_fa(
   uint16_t* pt_hi = pt_s[wid][0];
   uint16_t* pt_lo = pt_s[wid][1];
 
-  Q35_FA_LOAD(0);
+  Q35_FA_LOAD(b0);
   Q35_FA_STORE(0);
   __syncthreads();
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk & 1;
-    Q35_FA_LOAD(min(blk + 1, nblk - 1));  // in flight while this block is computed
+  for (int blk = b0; blk < b1; ++blk) {
+    const int buf = (blk - b0) & 1;
+    Q35_FA_LOAD(min(blk + 1, b1 - 1));  // in flight while this block is computed
     const uint16_t* Ks = kv_s[buf][0] + 32 * kh * kFaRow;
     const uint16_t* Vs = kv_s[buf][1] + 32 * kh * kFaRow;
     const int kb = blk * kFaKeys + 32 * kh;  // first key of this wave's half
@@ -972,24 +979,90 @@ __global__ __launch_bounds__(2 * G * 64) void gqa_prefill_fa(
   }
   __syncthreads();
   if (kh == 0) {
+    // One split: the final rows. Several: this split's (O, m, l) record, O
+    // relative to m and not yet divided by l; gqa_prefill_merge combines them.
+    float* rec = nsplit > 1 ? part + ((((size_t)b * KVH + kvh) * ntiles + tile) * smax + split) *
+                                         (size_t)(G * 16 * (kAD + 2))
+                            : nullptr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = q0 + 4 * kg + i;
-      const float m1 = ml[(g * 16 + 4 * kg + i) * 2], l1 = ml[(g * 16 + 4 * kg + i) * 2 + 1];
+      const int rr = g * 16 + 4 * kg + i;
+      const float m1 = ml[rr * 2], l1 = ml[rr * 2 + 1];
       const float mm = fmaxf(m[i], m1);
       const float f0 = m[i] == -INFINITY ? 0.f : expf(m[i] - mm);
       const float f1 = m1 == -INFINITY ? 0.f : expf(m1 - mm);
-      const float inv = 1.0f / (l[i] * f0 + l1 * f1);
-      if (r < L) {
+      const float lt = l[i] * f0 + l1 * f1;
+      if (rec) {
+#pragma unroll
+        for (int d = 0; d < 16; ++d)
+          rec[rr * kAD + 16 * d + col] = o[d][i] * f0 + mo[rr * kAD + 16 * d + col] * f1;
+        if (col == 0) {
+          rec[G * 16 * kAD + rr * 2] = mm;
+          rec[G * 16 * kAD + rr * 2 + 1] = lt;
+        }
+      } else if (r < L) {
+        const float inv = 1.0f / lt;
         uint16_t* orow = out + ((size_t)b * L + r) * QH * kAD + h * kAD + col;
 #pragma unroll
         for (int d = 0; d < 16; ++d) {
-          const float v = o[d][i] * f0 + mo[(g * 16 + 4 * kg + i) * kAD + 16 * d + col] * f1;
+          const float v = o[d][i] * f0 + mo[rr * kAD + 16 * d + col] * f1;
           orow[16 * d] = (uint16_t)f2bf(v * inv);
         }
       }
     }
   }
+}
+
+// Merge of the split records of the query tiles with more than one split:
+// one thread per (query head g, row r, 16 dims), G*256 threads per (tile, KV
+// head); O = sum_s O_s e^{m_s - M} / sum_s l_s e^{m_s - M}, M = max_s m_s.
+template <int G>
+__global__ __launch_bounds__(G * 256) void gqa_prefill_merge(
+    const float* __restrict__ part, uint16_t* __restrict__ out, int B, int QH, int KVH, int L,
+    int cache_len, int kv_start_host, const long long* __restrict__ valid_len, int sb, int smax) {
+  const int t = threadIdx.x;
+  const int g = t >> 8, r = (t >> 4) & 15, dq = t & 15;
+  const int tile = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int ntiles = gridDim.x;
+  const int q0 = tile * 16;
+  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  if (ks < 0) ks = 0;
+  if (ks + L > cache_len) ks = cache_len - L;
+  const int n_keys = min((int)ks + min(q0 + 16, L), cache_len);
+  const int nblk = (n_keys + kFaKeys - 1) / kFaKeys;
+  const int nsplit = (nblk + sb - 1) / sb;
+  if (nsplit <= 1 || q0 + r >= L) return;  // no barrier in this kernel
+  const size_t rs = (size_t)G * 16 * (kAD + 2);
+  const float* rec0 = part + (((size_t)b * KVH + kvh) * ntiles + tile) * smax * rs;
+  const int rr = g * 16 + r;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, rec0[sp * rs + G * 16 * kAD + rr * 2]);
+  float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  float lt = 0.f;
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float* rec = rec0 + sp * rs;
+    const float ms = rec[G * 16 * kAD + rr * 2];
+    const float f = ms == -INFINITY ? 0.f : expf(ms - mx);
+    lt += rec[G * 16 * kAD + rr * 2 + 1] * f;
+    const float4* v = reinterpret_cast<const float4*>(rec + rr * kAD + 16 * dq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 x = v[j];
+      acc[4 * j] = fmaf(x.x, f, acc[4 * j]);
+      acc[4 * j + 1] = fmaf(x.y, f, acc[4 * j + 1]);
+      acc[4 * j + 2] = fmaf(x.z, f, acc[4 * j + 2]);
+      acc[4 * j + 3] = fmaf(x.w, f, acc[4 * j + 3]);
+    }
+  }
+  const float inv = 1.0f / lt;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] *= inv;
+  uint4* o = reinterpret_cast<uint4*>(out + ((size_t)b * L + q0 + r) * QH * kAD + (kvh * G + g) * kAD + 16 * dq);
+  o[0] = pack8(acc);
+  o[1] = pack8(acc + 8);
 }
 
 // ---------------------------------------------------------- causal prefill
@@ -1205,9 +1278,56 @@ int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, i
   return q35_last_error();
 }
 
+// Split plan of the 64-key-block prefill kernel: query tile t (16 rows) has
+// nblk(t) key blocks and splits them into ranges of sb blocks, one workgroup
+// each. sb starts at 4 and grows until the workgroups of a prompt that starts
+// at key 0 fit one round on the device's CUs (one workgroup per CU: the
+// kernel takes 156 KB of LDS); smax = the splits of a tile covering the whole
+// cache sizes the grid and the workspace. The plan depends only on
+// (B, KVH, L, cache_len), so q35_gqa_prefill_workspace sees the same one.
+constexpr int kFaSplitBlocks = 4;
+static int fa_device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+static void fa_plan(int B, int KVH, int L, int cache_len, int* sb_out, int* smax_out) {
+  const int nblk_max = (cache_len + kFaKeys - 1) / kFaKeys;
+  const int ntiles = (L + 15) / 16;
+  const long long budget = fa_device_cus();
+  int sb = kFaSplitBlocks;
+  for (; sb < nblk_max; ++sb) {
+    long long wgs = 0;
+    for (int t = 0; t < ntiles; ++t) {
+      const int nb = (min(16 * t + 16, L) + kFaKeys - 1) / kFaKeys;
+      wgs += (nb + sb - 1) / sb;
+    }
+    if (wgs * B * KVH <= budget) break;
+  }
+  *sb_out = sb;
+  *smax_out = (nblk_max + sb - 1) / sb;
+}
+
+long long q35_gqa_prefill_workspace(int B, int QH, int KVH, int L, int cache_len) {
+  if (B <= 0 || KVH <= 0 || QH <= 0 || QH % KVH || L <= 0 || cache_len <= 0) return 0;
+  const int G = QH / KVH;
+  if (G != 2 && G != 4) return 0;
+  int sb, smax;
+  fa_plan(B, KVH, L, cache_len, &sb, &smax);
+  if (smax <= 1) return 0;
+  return (long long)B * KVH * ((L + 15) / 16) * smax * G * 16 * (kAD + 2);
+}
+
 int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int B, int QH, int KVH,
                     int D, int L, int cache_len, int kv_start, const void* valid_len, float scale,
-                    hipStream_t stream) {
+                    void* workspace, long long workspace_floats, hipStream_t stream) {
   Q35_CHECK_ARG(D == kAD && KVH > 0 && QH % KVH == 0 && B >= 0 && L >= 0);
   Q35_CHECK_ARG(L <= cache_len && (valid_len || (kv_start >= 0 && kv_start + L <= cache_len)));
   Q35_CHECK_ARG(q35_aligned16(q) && q35_aligned16(K) && q35_aligned16(V) && q35_aligned16(out));
@@ -1220,17 +1340,39 @@ int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int 
                                                      (const uint16_t*)V, (uint16_t*)out, B, QH, KVH, \
                                                      L, cache_len, kv_start,                       \
                                                      (const long long*)valid_len, scale)
-#define Q35_FA(GG)                                                                                \
-  gqa_prefill_fa<GG><<<grid, 2 * GG * 64, 0, stream>>>((const uint16_t*)q, (const uint16_t*)K,     \
-                                                       (const uint16_t*)V, (uint16_t*)out, B, QH,    \
-                                                       KVH, L, cache_len, kv_start,                  \
-                                                       (const long long*)valid_len, scale)
-    if (G == 1) Q35_PF(1);
-    else if (G == 2) Q35_FA(2);
-    else if (G == 4) Q35_FA(4);
-    else Q35_PF(8);
-#undef Q35_PF
+    if (G == 2 || G == 4) {
+      // Long query tiles split their key range over workgroups of at most
+      // kFaSplitBlocks blocks when the workspace holds the split records.
+      const int ntiles = (L + 15) / 16;
+      int sb, smax;
+      fa_plan(B, KVH, L, cache_len, &sb, &smax);
+      const long long need = q35_gqa_prefill_workspace(B, QH, KVH, L, cache_len);
+      if (smax <= 1 || !workspace || workspace_floats < need) {
+        smax = 1;
+        sb = (cache_len + kFaKeys - 1) / kFaKeys;
+      }
+      Q35_CHECK_ARG((long long)ntiles * smax < (1ll << 31));
+      dim3 fgrid((unsigned)(ntiles * smax), (unsigned)KVH, (unsigned)B);
+#define Q35_FA(GG)                                                                               \
+  do {                                                                                         \
+    gqa_prefill_fa<GG><<<fgrid, 2 * GG * 64, 0, stream>>>(                                     \
+        (const uint16_t*)q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)out, B, QH, KVH,  \
+        L, cache_len, kv_start, (const long long*)valid_len, scale, sb, smax,                    \
+        (float*)workspace);                                                                      \
+    if (smax > 1)                                                                              \
+      gqa_prefill_merge<GG><<<grid, GG * 256, 0, stream>>>(                                    \
+          (const float*)workspace, (uint16_t*)out, B, QH, KVH, L, cache_len, kv_start,           \
+          (const long long*)valid_len, sb, smax);                                                \
+  } while (0)
+      if (G == 2) Q35_FA(2);
+      else Q35_FA(4);
 #undef Q35_FA
+    } else if (G == 1) {
+      Q35_PF(1);
+    } else {
+      Q35_PF(8);
+    }
+#undef Q35_PF
     return q35_last_error();
   }
   const long long waves = (long long)B * QH * L;

@@ -814,9 +814,11 @@ def gqa_prefill_attention(
         raise ValueError("valid_length must be an int64 tensor on the GPU")
     _need_bf16(q, keys, values)
     out = torch.empty((batch, seq_len, heads * dim), device=q.device, dtype=q.dtype)
+    floats = _lib.load().q35_gqa_prefill_workspace(batch, heads, kv_heads, seq_len, cache_len)
+    ws = torch.empty(max(floats, 1), device=q.device, dtype=torch.float32) if floats > 0 else None
     _lib.call("q35_gqa_prefill", q.data_ptr(), keys.data_ptr(), values.data_ptr(), out.data_ptr(),
               batch, heads, kv_heads, dim, seq_len, cache_len, kv_start, _lib.ptr(valid_length),
-              float(scale), _stream(q))
+              float(scale), _lib.ptr(ws), floats, _stream(q))
     return out
 
 

@@ -399,7 +399,8 @@ def test_gqa_decode_gate_fused(gpu):
     close(got, exp)
 
 
-@pytest.mark.parametrize("seq_len,kv_start", [(33, 0), (64, 16), (1, 0), (100, 37), (1024, 0)])
+@pytest.mark.parametrize("seq_len,kv_start", [(33, 0), (64, 16), (1, 0), (100, 37), (1024, 0),
+                                             (300, 500)])
 def test_prefill_attention(gpu, seq_len, kv_start):
     """Causal GQA prefill (MFMA flash attention, P as bf16 hi + lo parts)
     against the fp64 oracle, rtol 1e-2 / atol 1e-3 on the bf16 output. Cache
@@ -433,6 +434,35 @@ def test_prefill_attention_groupings(gpu, q_heads, kv_heads):
     valid = torch.tensor(start + seq_len, dtype=torch.int64, device=gpu)
     got = K.gqa_prefill_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), 0.0625, valid_length=valid)
     close(got, exp)
+
+
+@pytest.mark.parametrize("q_heads,kv_heads", [(8, 2), (4, 2)])
+def test_prefill_attention_split_keys(gpu, q_heads, kv_heads):
+    """Query tiles with more than 4 key blocks of 64 split their key range over
+    workgroups and are merged by a second launch; with no workspace the same
+    call runs unsplit. Device length with a prompt that starts at 600 of a
+    1024-row cache (tiles cover 10-13 key blocks)."""
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 24)
+    seq_len, start, cache = 200, 600, 1024
+    q = randn(g, 1, q_heads, seq_len, 256)
+    kc = randn(g, 1, kv_heads, cache, 256)
+    vc = randn(g, 1, kv_heads, cache, 256)
+    exp = ref.prefill_attention(q, kc, vc, 0.0625, start)
+    valid = torch.tensor(start + seq_len, dtype=torch.int64, device=gpu)
+    qg, kg, vg = q.to(gpu), kc.to(gpu), vc.to(gpu)
+    kg[:, :, start + seq_len:] = float("nan")
+    vg[:, :, start + seq_len:] = float("nan")
+    assert _lib.load().q35_gqa_prefill_workspace(1, q_heads, kv_heads, seq_len, cache) > 0
+    got = K.gqa_prefill_attention(qg, kg, vg, 0.0625, valid_length=valid)
+    close(got, exp)
+    unsplit = torch.empty_like(got)
+    _lib.call("q35_gqa_prefill", qg.data_ptr(), kg.data_ptr(), vg.data_ptr(), unsplit.data_ptr(),
+              1, q_heads, kv_heads, 256, seq_len, cache, 0, valid.data_ptr(), 0.0625, None, 0,
+              torch.cuda.current_stream().cuda_stream)
+    close(unsplit, exp)
 
 
 # ------------------------------------------------------------------ A8W8
