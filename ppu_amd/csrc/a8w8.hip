@@ -48,12 +48,13 @@ __global__ __launch_bounds__(256) void quant_weight_rows(const uint16_t* __restr
   if (lane == 0) scale[n] = s;
 }
 
-// One workgroup per token row: 16-byte loads, block absmax, then
-// q = sat(rint(x * 127/absmax)) written as 8-byte groups (K % 8 == 0).
+// One workgroup per token row: 16-byte loads (PER groups of 8 per thread,
+// K <= PER * 2048), block absmax, then q = sat(rint(x * 127/absmax)) written
+// as 8-byte groups (K % 8 == 0).
+template <int PER>
 __global__ __launch_bounds__(256) void quant_act_rows(const uint16_t* __restrict__ x,
                                                       int8_t* __restrict__ xq,
                                                       float* __restrict__ scale, int M, int K) {
-  constexpr int PER = 4;  // 8-element groups per thread held in registers (K <= 8192)
   const int m = blockIdx.x;
   const int tid = threadIdx.x;
   const uint16_t* row = x + (size_t)m * K;
@@ -241,22 +242,28 @@ __global__ __launch_bounds__(256) void a8w8_gemv_skinny(const A8Args a) {
 }
 
 // y[m, n] = bf16((float)acc[m, n] * s_x[m] * s_w[n]); 8 outputs per thread.
+// y[m, n..n+7] = bf16(acc * s_x[m] * s_w[n..]) (that multiplication order):
+// grid (column blocks of 2048, rows), every load issued before use.
 __global__ __launch_bounds__(256) void dequant_rows(const int* __restrict__ acc,
                                                     const float* __restrict__ s_x,
                                                     const float* __restrict__ s_w,
                                                     uint16_t* __restrict__ y, int M, int N) {
-  const long long i = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-  if (i >= (long long)M * N) return;
-  const int m = (int)(i / N);
-  const int n = (int)(i - (long long)m * N);
-  const float sx = s_x[m];
-  const int4 a0 = *reinterpret_cast<const int4*>(acc + i);
-  const int4 a1 = *reinterpret_cast<const int4*>(acc + i + 4);
-  const int av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-  float o[8];
+  const int n = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (n >= N) return;
+  const float4 w0 = *reinterpret_cast<const float4*>(s_w + n);
+  const float4 w1 = *reinterpret_cast<const float4*>(s_w + n + 4);
+  const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const size_t i = (size_t)m * N + n;
+    const int4 a0 = *reinterpret_cast<const int4*>(acc + i);
+    const int4 a1 = *reinterpret_cast<const int4*>(acc + i + 4);
+    const float sx = s_x[m];
+    const int av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    float o[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = (float)av[e] * sx * s_w[n + e];
-  *reinterpret_cast<uint4*>(y + i) = pack8(o);
+    for (int e = 0; e < 8; ++e) o[e] = (float)av[e] * sx * w[e];
+    *reinterpret_cast<uint4*>(y + i) = pack8(o);
+  }
 }
 
 }  // namespace
@@ -267,12 +274,10 @@ extern "C" {
 int q35_dequant_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,
                     hipStream_t stream) {
   Q35_CHECK_ARG(M > 0 && N > 0 && N % 8 == 0 && acc && s_x && s_w && y);
-  Q35_CHECK_ARG(q35_aligned16(acc) && q35_aligned16(y));
-  const long long groups = (long long)M * N / 8;
-  const long long grid = (groups + 255) / 256;
-  Q35_CHECK_ARG(grid < (1ll << 31));
-  dequant_rows<<<(unsigned)grid, 256, 0, stream>>>((const int*)acc, (const float*)s_x,
-                                                  (const float*)s_w, (uint16_t*)y, M, N);
+  Q35_CHECK_ARG(q35_aligned16(acc) && q35_aligned16(y) && q35_aligned16(s_w));
+  const dim3 grid((unsigned)((N / 8 + 255) / 256), (unsigned)min(M, 65535));
+  dequant_rows<<<grid, 256, 0, stream>>>((const int*)acc, (const float*)s_x, (const float*)s_w,
+                                         (uint16_t*)y, M, N);
   return q35_last_error();
 }
 
@@ -288,7 +293,15 @@ int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, hipStre
   Q35_CHECK_ARG(M >= 0 && K > 0 && K % 8 == 0 && K <= 8192);
   Q35_CHECK_ARG(q35_aligned16(x) && q35_aligned8(xq));
   if (M == 0) return 0;
-  quant_act_rows<<<M, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale, M, K);
+  const int per = (K / 8 + 255) / 256;
+  if (per == 1)
+    quant_act_rows<1><<<M, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale, M, K);
+  else if (per == 2)
+    quant_act_rows<2><<<M, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale, M, K);
+  else if (per == 3)
+    quant_act_rows<3><<<M, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale, M, K);
+  else
+    quant_act_rows<4><<<M, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale, M, K);
   return q35_last_error();
 }
 
