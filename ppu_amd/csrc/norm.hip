@@ -227,21 +227,23 @@ __global__ __launch_bounds__(256) void silu_mul_elems(const uint16_t* __restrict
   out[i] = (uint16_t)f2bf(round_bf(silu_f(g)) * up);
 }
 
-// silu_mul_elems with 8 elements per thread (width a multiple of 8).
+// silu_mul_elems with 8 elements per thread (width a multiple of 8), grid
+// (column blocks of 2048, rows) so no thread divides its index.
 __global__ __launch_bounds__(256) void silu_mul_vec(const uint16_t* __restrict__ packed,
-                                                    uint16_t* __restrict__ out, long long groups,
+                                                    uint16_t* __restrict__ out, long long rows,
                                                     int width) {
-  const long long gi = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gi >= groups) return;
-  const int gpr = width / 8;
-  const long long row = gi / gpr;
-  const int col = (int)(gi - row * gpr) * 8;
-  float g[8], up[8], o[8];
-  unpack8(*reinterpret_cast<const uint4*>(packed + row * 2 * width + col), g);
-  unpack8(*reinterpret_cast<const uint4*>(packed + row * 2 * width + width + col), up);
+  const int col = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (col >= width) return;
+  for (long long row = blockIdx.y; row < rows; row += gridDim.y) {
+    const uint4 graw = *reinterpret_cast<const uint4*>(packed + row * 2 * width + col);
+    const uint4 uraw = *reinterpret_cast<const uint4*>(packed + row * 2 * width + width + col);
+    float g[8], up[8], o[8];
+    unpack8(graw, g);
+    unpack8(uraw, up);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = round_bf(silu_fast(g[e])) * up[e];
-  *reinterpret_cast<uint4*>(out + row * width + col) = pack8(o);
+    for (int e = 0; e < 8; ++e) o[e] = round_bf(silu_fast(g[e])) * up[e];
+    *reinterpret_cast<uint4*>(out + row * width + col) = pack8(o);
+  }
 }
 
 // out = bf16( x * bf16(sigmoid(gate)) ); the gate of head h sits at
@@ -261,6 +263,28 @@ __global__ __launch_bounds__(256) void attn_gate_elems(const uint16_t* __restric
   out[i] = (uint16_t)f2bf(bf2f(x[i]) * round_bf(sigmoid_f(g)));
 }
 
+
+// attn_gate_elems with 8 columns per thread (16-byte loads; head_dim,
+// hidden and packed_stride multiples of 8), grid (column blocks, tokens).
+__global__ __launch_bounds__(256) void attn_gate_vec(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ packed,
+                                                     uint16_t* __restrict__ out, long long tokens,
+                                                     int hidden, int packed_stride, int head_dim) {
+  const int col = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (col >= hidden) return;
+  const int head = col / head_dim;
+  const int hc = col - head * head_dim;
+  for (long long t = blockIdx.y; t < tokens; t += gridDim.y) {
+    const uint4 xr = *reinterpret_cast<const uint4*>(x + t * hidden + col);
+    const uint4 gr = *reinterpret_cast<const uint4*>(packed + t * packed_stride + head * 2 * head_dim + head_dim + hc);
+    float xv[8], gv[8], o[8];
+    unpack8(xr, xv);
+    unpack8(gr, gv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = xv[e] * round_bf(sigmoid_f(gv[e]));
+    *reinterpret_cast<uint4*>(out + t * hidden + col) = pack8(o);
+  }
+}
 }  // namespace
 
 extern "C" {
@@ -350,11 +374,8 @@ int q35_silu_mul(const void* packed, void* out, long long rows, int width, hipSt
   const long long total = rows * (long long)width;
   if (total == 0) return 0;
   if (width % 8 == 0 && q35_aligned16(packed) && q35_aligned16(out)) {
-    const long long groups = total / 8;
-    const long long g8 = (groups + 255) / 256;
-    Q35_CHECK_ARG(g8 < (1ll << 31));
-    silu_mul_vec<<<(unsigned)g8, 256, 0, stream>>>((const uint16_t*)packed, (uint16_t*)out, groups,
-                                                   width);
+    const dim3 grid((unsigned)((width / 8 + 255) / 256), (unsigned)min(rows, 65535ll));
+    silu_mul_vec<<<grid, 256, 0, stream>>>((const uint16_t*)packed, (uint16_t*)out, rows, width);
     return q35_last_error();
   }
   const long long grid = (total + 255) / 256;
@@ -370,6 +391,13 @@ int q35_attn_gate_mul(const void* x, const void* packed, void* out, long long to
   Q35_CHECK_ARG(packed_stride >= 2 * hidden);
   const long long total = tokens * (long long)hidden;
   if (total == 0) return 0;
+  if (head_dim % 8 == 0 && packed_stride % 8 == 0 && q35_aligned16(x) && q35_aligned16(packed) &&
+      q35_aligned16(out)) {
+    const dim3 vgrid((unsigned)((hidden / 8 + 255) / 256), (unsigned)min(tokens, 65535ll));
+    attn_gate_vec<<<vgrid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)packed,
+                                             (uint16_t*)out, tokens, hidden, packed_stride, head_dim);
+    return q35_last_error();
+  }
   const long long grid = (total + 255) / 256;
   Q35_CHECK_ARG(grid < (1ll << 31));
   attn_gate_elems<<<(unsigned)grid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)packed,
