@@ -231,9 +231,11 @@ int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, void
  * one workgroup per row: K a multiple of 8 and at most 8192, x 16-byte and xq
  * 8-byte aligned. Replaces the call at explore_runtime_quantization.py:167-172. */
 int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, void* stream);
-/* y[M,N] = bf16(int32(xq . Wq) * s_x[m] * s_w[n]); with x (bf16) and M == 1 the
- * activation quantisation is fused (xq/s_x optional outputs), else xq/s_x are
- * inputs (or filled from x first). acc_out (optional) gets the int32 sums.
+/* y[M,N] = bf16(int32(xq . Wq) * s_x[m] * s_w[n]). With x (bf16) the per-token
+ * quantisation is done here and xq/s_x receive it (fused into the GEMV launch
+ * for M == 1 and for small M*K at K = 2048/6144, where they are optional);
+ * with x == NULL, xq/s_x are inputs. 2..16 tokens at K = 2048/6144 run on the
+ * int8 matrix cores. acc_out (optional) gets the int32 sums.
  * Replaces explore_runtime_quantization.py:161-181 (PPUA8W8Linear.forward). */
 int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void* s_w, void* y,
                   void* acc_out, int M, int N, int K, void* stream);

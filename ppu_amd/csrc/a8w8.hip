@@ -14,10 +14,10 @@
 //
 // One token (M = 1) runs on the tiled GEMV of gemv.hip with int8 weights,
 // which quantises the activation inside every workgroup (q35_gemv_i8). Here:
-// weight/activation quantisation kernels, the skinny M <= 16 GEMV over
-// pre-quantised activations (one wave64 owns R weight rows; lane l reads 16
-// int8 at k = c*1024 + 16l, so the weight stream is read once per launch of
-// MT tokens), and the dequant of a library int32 GEMM for prefill.
+// weight/activation quantisation kernels, the skinny 2..16-token GEMM on the
+// int8 matrix cores (the weight stream is read once per launch; the per-token
+// quantisation fused while M*K is small), a dot4 GEMV for other shapes, and
+// the dequant of a library int32 GEMM for prefill.
 #include "q35_common.hpp"
 
 // The tiled int8-weight GEMV with the activation quantisation fused (gemv.hip).
@@ -79,10 +79,7 @@ __global__ __launch_bounds__(256) void quant_act_rows(const uint16_t* __restrict
   for (int j = 0; j < PER; ++j) {
     const int gidx = tid + j * 256;
     if (gidx < groups) {
-      uint32_t q[2] = {0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q[e >> 2] |= (uint32_t)(uint8_t)sat_i8(v[j][e] * inv) << (8 * (e & 3));
-      *reinterpret_cast<uint2*>(xq + (size_t)m * K + gidx * 8) = make_uint2(q[0], q[1]);
+      *reinterpret_cast<uint2*>(xq + (size_t)m * K + gidx * 8) = quant8_i8(v[j], inv);
     }
   }
   if (tid == 0) scale[m] = mx / 127.0f;
@@ -147,96 +144,134 @@ __global__ __launch_bounds__(256) void a8w8_gemv_mt(const A8Args a, int m0) {
   }
 }
 
-// One step of the halving butterfly and the rest by recursion (all indices
-// compile-time, so the values stay in registers): H values are exchanged
-// across lane bit S, or, once one value is left, plain xor-adds finish.
-template <int H, int S, int N>
-Q35_DEV void bfly_reduce(int (&acc)[N], int lane) {
-  if constexpr (S >= 1) {
-    if constexpr (H >= 1) {
-      const bool upper = (lane & S) != 0;
-#pragma unroll
-      for (int j = 0; j < H; ++j) {
-        const int send = upper ? acc[j] : acc[j + H];
-        const int keep = upper ? acc[j + H] : acc[j];
-        acc[j] = keep + __shfl_xor(send, S, 64);
-      }
-      bfly_reduce<H / 2, S / 2, N>(acc, lane);
-    } else {
-      acc[0] += __shfl_xor(acc[0], S, 64);
-      bfly_reduce<0, S / 2, N>(acc, lane);
-    }
-  }
-}
+// Skinny A8W8 for 2..MT tokens (MT = 4, 8 or 16) in one pass over the
+// weights, on the int8 matrix cores (v_mfma_i32_16x16x64_i8): the tokens fill
+// the 16 columns of the B operand, 16 weight rows the A operand, so a wave
+// forms a 16 x 16 int32 tile per 64 k with one instruction and the dot4 work
+// of the M tokens (the VALU bound of a dot4 skinny GEMV at M = 16) vanishes.
+// Operand layout (wave64): lane l supplies row l%16 of A and column l%16 of
+// B, 16 consecutive k at 16*(l/16) of the 64-k block; lane l receives C rows
+// 4*(l/16)+e, column l%16. Both operands use the same k order, and integer
+// sums are exact in any order, so any such k assignment gives the same acc.
+//
+// Workgroup: RT row tiles of 16 weight rows x KS slices of K, one wave per
+// (tile, slice); lane l of a wave streams 16 bytes at k = k0 + 64c + 16(l/16)
+// of row l%16, KB = K/(KS*64) loads, all in flight before the first MFMA.
+// QUANT: the MT bf16 activation rows are read by every workgroup (requested
+// before the weight stream: loads retire in order, so the quantisation runs
+// while the weights arrive) and quantised per token in LDS with the rule of
+// quant_act_rows; workgroup 0 stores xq and s_x when asked. Otherwise the
+// int8 rows and s_x are inputs. Rows past M read row M-1 and are never
+// stored; B columns past MT repeat a staged row and are dropped. The KS
+// partial tiles are summed in LDS, then one thread per output dequantises.
+template <int MT, int RT, int KS, int K, bool QUANT>
+__global__ __launch_bounds__(RT * KS * 64) void a8w8_skinny_mfma(const A8Args a) {
+  constexpr int NW = RT * KS;
+  constexpr int KB = K / (KS * 64);          // MFMAs (16-byte loads) per lane
+  constexpr int XS = K + 16;                 // LDS row stride: rows 16 bytes apart in the banks
+  constexpr int RPW = (MT + NW - 1) / NW;    // activation rows per wave
+  constexpr int XV = QUANT ? K / 512 : K / 1024;  // 16-byte activation loads per lane and row
+  static_assert(K % (KS * 64) == 0 && KS >= 4 && (MT & (MT - 1)) == 0 && MT <= 16, "tile shape");
+  static_assert(XV >= 1, "K too small for the activation tiling");
+  // MT staged rows plus one discard row for waves whose row index passes MT.
+  __shared__ __attribute__((aligned(16))) int8_t xq_s[(MT + 1) * XS];
+  __shared__ float sx_s[MT + 1];
+  __shared__ int4 red[NW][64];
 
-// Skinny A8W8 for 2..MT tokens in one pass over the weights (K = NCH KiB).
-// The workgroup stages the MT pre-quantised rows in LDS (requested before the
-// weight stream, so both are in flight together); lane l owns bytes
-// c*1024 + 16l of each of its R rows and forms R*MT int32 partial sums with
-// v_dot4. The R*MT sums are reduced across the wave by a halving butterfly:
-// at step s (32, 16, ..., 1) each lane keeps the half of its values selected
-// by lane bit s and adds the partner's copy, so after log2(R*MT) steps lane
-// i holds value i summed over the lanes that share its high bits (remaining
-// steps add the rest) -- R*MT - 1 shuffles instead of R*MT full reductions.
-template <int R, int NCH, int MT>
-__global__ __launch_bounds__(256) void a8w8_gemv_skinny(const A8Args a) {
-  constexpr int V = R * MT;  // partial sums per lane (power of two, <= 64)
-  static_assert((V & (V - 1)) == 0 && V <= 64 && V >= 2, "R*MT must be a power of two <= 64");
-  constexpr int KV = NCH * 64;  // uint4 per activation row
-  __shared__ uint4 xs[MT * KV];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int n0 = (blockIdx.x * 4 + (tid >> 6)) * R;
+  const int wid = tid >> 6;
+  const int nb = blockIdx.x * RT * 16;
 
-  // 1. activation rows (rows past M read row M-1 and are zeroed), then weights.
-  constexpr int PER = (MT * KV + 255) / 256;
-  uint4 xr[PER];
+  // 1. activation rows (bf16 or int8), the output thread's weight scale, then
+  //    the weight stream (unpredicated: rows past N read row N-1).
+  uint4 xr[RPW][XV];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = min(tid + j * 256, MT * KV - 1);
-    const int m = i / KV;
-    xr[j] = *reinterpret_cast<const uint4*>(a.xq + (size_t)min(m, a.M - 1) * a.K + (i - m * KV) * 16);
-  }
-  uint4 w[R][NCH];
+  for (int j = 0; j < RPW; ++j) {
+    const int m = min(wid + NW * j, a.M - 1);
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int8_t* wrow = a.Wq + (size_t)min(n0 + r, a.N - 1) * a.K + lane * 16;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) w[r][c] = ld_stream16(wrow + c * 1024);
-  }
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = tid + j * 256;
-    if (i < MT * KV) xs[i] = i / KV < a.M ? xr[j] : make_uint4(0, 0, 0, 0);
-  }
-  __syncthreads();
-
-  // 2. int32 partial sums, value index v = r * MT + m.
-  int acc[V];
-#pragma unroll
-  for (int v = 0; v < V; ++v) acc[v] = 0;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const uint4 xv = xs[m * KV + c * 64 + lane];
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r * MT + m] = dot16_i8(w[r][c], xv, acc[r * MT + m]);
+    for (int t = 0; t < XV; ++t) {
+      const int q = lane + 64 * t;
+      xr[j][t] = QUANT ? *reinterpret_cast<const uint4*>(a.x + (size_t)m * K + q * 8)
+                       : *reinterpret_cast<const uint4*>(a.xq + (size_t)m * K + q * 16);
     }
   }
+  // Output thread t < RT*256: tile t/256, token m = (t%256)/16, row n = t%16.
+  const int o_rt = tid >> 8, o_m = (tid >> 4) & 15, o_n = tid & 15;
+  const int o_row = nb + o_rt * 16 + o_n;
+  const float sw = a.s_w[min(o_row, a.N - 1)];
+  const float sx_in = QUANT ? 0.f : a.s_x[min(o_m, a.M - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const int rt = wid / KS, ks = wid % KS;
+  const int wrow = min(nb + rt * 16 + (lane & 15), a.N - 1);
+  const int8_t* wp = a.Wq + (size_t)wrow * K + ks * (K / KS) + 16 * (lane >> 4);
+  uint4 w[KB];
+#pragma unroll
+  for (int c = 0; c < KB; ++c) w[c] = ld_stream16(wp + 64 * c);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // 3. butterfly reduce-scatter over the wave (integer adds: exact).
-  bfly_reduce<V / 2, 32, V>(acc, lane);
-  // Lane l holds value index l >> (6 - log2 V).
-  constexpr int LOGV = V >= 64 ? 6 : V >= 32 ? 5 : V >= 16 ? 4 : V >= 8 ? 3 : V >= 4 ? 2 : 1;
-  if ((lane & ((1 << (6 - LOGV)) - 1)) == 0) {
-    const int v = lane >> (6 - LOGV);
-    const int r = v / MT, m = v % MT;
-    const int n = n0 + r;
-    if (n < a.N && m < a.M) {
-      const size_t o = (size_t)m * a.N + n;
-      a.y[o] = (uint16_t)f2bf((float)acc[0] * a.s_x[m] * a.s_w[n]);
-      if (a.acc_out) a.acc_out[o] = acc[0];
+  // 2. stage the int8 rows in LDS (quantising bf16 rows per token).
+  const bool writer = blockIdx.x == 0;
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int m = min(wid + NW * j, MT);  // MT: the discard row (no branch around the loads)
+    if (QUANT) {
+      float v[XV][8];
+      float mx = 0.f;
+#pragma unroll
+      for (int t = 0; t < XV; ++t) {
+        unpack8(xr[j][t], v[t]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[t][e]));
+      }
+      mx = wave_max(mx);
+      const float inv = 127.0f / mx;
+#pragma unroll
+      for (int t = 0; t < XV; ++t) {
+        const int q = lane + 64 * t;
+        const uint2 pv = quant8_i8(v[t], inv);
+        *reinterpret_cast<uint2*>(xq_s + m * XS + q * 8) = pv;
+        if (writer && a.xq_out && m < a.M) *reinterpret_cast<uint2*>(a.xq_out + (size_t)m * K + q * 8) = pv;
+      }
+      if (lane == 0) {
+        sx_s[m] = mx / 127.0f;
+        if (writer && a.s_x_out && m < a.M) a.s_x_out[m] = mx / 127.0f;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < XV; ++t) {
+        // Field-wise vector store (a struct copy here becomes a private-memory memcpy).
+        const q35_u32x4 v = {xr[j][t].x, xr[j][t].y, xr[j][t].z, xr[j][t].w};
+        *reinterpret_cast<q35_u32x4*>(xq_s + m * XS + (lane + 64 * t) * 16) = v;
+      }
+    }
+  }
+  lds_barrier();
+
+  // 3. KB int8 MFMAs over the wave's k slice.
+  typedef int q35_i32x4 __attribute__((ext_vector_type(4)));
+  q35_i32x4 acc = {0, 0, 0, 0};
+  const int8_t* bp = xq_s + (lane & 15 & (MT - 1)) * XS + ks * (K / KS) + 16 * (lane >> 4);
+#pragma unroll
+  for (int c = 0; c < KB; ++c) {
+    const q35_i32x4 bv = *reinterpret_cast<const q35_i32x4*>(bp + 64 * c);
+    const q35_i32x4 av = {(int)w[c].x, (int)w[c].y, (int)w[c].z, (int)w[c].w};
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc, 0, 0, 0);
+  }
+
+  // 4. sum the KS slices of each tile; output (m, n) sits at lane 16(n/4)+m, element n%4.
+  red[wid][lane] = make_int4(acc[0], acc[1], acc[2], acc[3]);
+  lds_barrier();
+  if (tid < RT * 256) {
+    const int* rp = reinterpret_cast<const int*>(&red[o_rt * KS][0]) + (16 * (o_n >> 2) + o_m) * 4 + (o_n & 3);
+    int s = 0;
+#pragma unroll
+    for (int k2 = 0; k2 < KS; ++k2) s += rp[k2 * 256];
+    if (o_m < a.M && o_row < a.N) {
+      const size_t o = (size_t)o_m * a.N + o_row;
+      const float sx = QUANT ? sx_s[o_m] : sx_in;
+      a.y[o] = (uint16_t)f2bf((float)s * sx * sw);
+      if (a.acc_out) a.acc_out[o] = s;
     }
   }
 }
@@ -264,6 +299,15 @@ __global__ __launch_bounds__(256) void dequant_rows(const int* __restrict__ acc,
     for (int e = 0; e < 8; ++e) o[e] = (float)av[e] * sx * w[e];
     *reinterpret_cast<uint4*>(y + i) = pack8(o);
   }
+}
+
+template <int MT, int RT, int KS, int K, bool QUANT>
+int launch_skinny(const A8Args& a, hipStream_t stream) {
+  // QUANT needs the bf16 rows; otherwise the int8 rows and their scales.
+  if (QUANT ? !a.x : (!a.xq || !a.s_x)) return (int)hipErrorInvalidValue;
+  const unsigned grid = (unsigned)((a.N + 16 * RT - 1) / (16 * RT));
+  a8w8_skinny_mfma<MT, RT, KS, K, QUANT><<<grid, RT * KS * 64, 0, stream>>>(a);
+  return q35_last_error();
 }
 
 }  // namespace
@@ -319,6 +363,36 @@ int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void
     return q35_gemv_i8(Wq, s_w, x, nullptr, nullptr, 0, 0.f, nullptr, nullptr, y, acc_out, xq, s_x,
                        N, K, 0, stream);
   }
+  // 2..16 tokens with K = 2 or 6 KiB: one pass over the weights on the int8
+  // matrix cores. Tiles and the fused quantisation per (K, MT) from a measured
+  // sweep (MI355X, rotating 640 MB of weights): every workgroup of the fused
+  // form quantises all MT rows itself, which stops paying at MT*K = 96 Ki.
+  if (M <= 16 && (K == 2048 || K == 6144)) {
+    const int mt = M <= 4 ? 4 : M <= 8 ? 8 : 16;
+    const bool fuse = x && mt * K <= 49152;
+    if (x && !fuse) {
+      Q35_CHECK_ARG(xq && s_x);
+      const int e = q35_quant_act_i8(x, xq, s_x, M, K, stream);
+      if (e) return e;
+    }
+    if (!fuse) Q35_CHECK_ARG(xq && s_x);
+    a.x = fuse ? (const uint16_t*)x : nullptr;
+    a.xq_out = fuse ? (int8_t*)xq : nullptr;
+    a.s_x_out = fuse ? (float*)s_x : nullptr;
+    if (K == 2048) {  // 48 rows x 4 K slices per workgroup (256 workgroups at N = 12288)
+      if (mt == 4) return fuse ? launch_skinny<4, 3, 4, 2048, true>(a, stream)
+                               : launch_skinny<4, 3, 4, 2048, false>(a, stream);
+      if (mt == 8) return fuse ? launch_skinny<8, 3, 4, 2048, true>(a, stream)
+                               : launch_skinny<8, 3, 4, 2048, false>(a, stream);
+      return fuse ? launch_skinny<16, 3, 4, 2048, true>(a, stream)
+                  : launch_skinny<16, 3, 4, 2048, false>(a, stream);
+    }
+    if (mt == 4) return fuse ? launch_skinny<4, 1, 4, 6144, true>(a, stream)
+                             : launch_skinny<4, 1, 4, 6144, false>(a, stream);
+    if (mt == 8) return fuse ? launch_skinny<8, 1, 8, 6144, true>(a, stream)
+                             : launch_skinny<8, 1, 8, 6144, false>(a, stream);
+    return launch_skinny<16, 1, 4, 6144, false>(a, stream);
+  }
   if (x) {
     Q35_CHECK_ARG(xq && s_x);
     const int e = q35_quant_act_i8(x, xq, s_x, M, K, stream);
@@ -326,20 +400,6 @@ int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void
   }
   Q35_CHECK_ARG(xq && s_x);
   a.x = nullptr;
-  // 2..16 tokens with K = 2 or 6 KiB: one pass over the weights.
-  if (M <= 16 && (K == 2048 || K == 6144) && q35_aligned16(xq)) {
-    const unsigned grid2 = (unsigned)((N + 15) / 16), grid6 = (unsigned)((N + 7) / 8);
-#define Q35_SKINNY(MT)                                                                      \
-  {                                                                                         \
-    if (K == 2048) a8w8_gemv_skinny<4, 2, MT><<<grid2, 256, 0, stream>>>(a);                \
-    else a8w8_gemv_skinny<2, 6, MT><<<grid6, 256, 0, stream>>>(a);                          \
-    return q35_last_error();                                                                \
-  }
-    if (M <= 4) Q35_SKINNY(4)
-    if (M <= 8) Q35_SKINNY(8)
-    Q35_SKINNY(16)
-#undef Q35_SKINNY
-  }
   constexpr int R = 2, MT = 4;
   const unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
   for (int m0 = 0; m0 < M; m0 += MT) {

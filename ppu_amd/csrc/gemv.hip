@@ -262,10 +262,7 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = tid + j * NT;
-      uint32_t q[2] = {0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q[e >> 2] |= (uint32_t)(uint8_t)sat_i8(o[j][e] * inv) << (8 * (e & 3));
-      const uint2 v = make_uint2(q[0], q[1]);
+      const uint2 v = quant8_i8(o[j], inv);
       if (act) {
         xq_s[i] = v;
         if (writer && a.xq_out) *reinterpret_cast<uint2*>(a.xq_out + i * 8) = v;

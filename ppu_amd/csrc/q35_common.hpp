@@ -188,11 +188,28 @@ Q35_DEV float conv_update_channel(uint16_t* __restrict__ st, const uint16_t* __r
 }
 
 // ------------------------------------------------------------------ int8
-// Saturating float -> int8 after rint; NaN (0 * inf for a zero row) maps to 0.
-Q35_DEV int8_t sat_i8(float v) {
-  if (v != v) return 0;
-  const float r = rintf(v);
-  return (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
+// Four quantised bytes packed little-endian: q = sat_int8(rint(v * inv)) with
+// NaN -> 0 (the same map as sat_i8, in fewer instructions): v_rndne_f32, then
+// v_cvt_i32_f32 (NaN -> 0, +-inf saturate to the int32 range), v_med3_i32 to
+// [-128, 127], and two byte permutes per pair.
+Q35_DEV int cvt_i32_sat(float r) {
+  int i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(r));
+  return i;
+}
+Q35_DEV uint32_t quant4_i8(float a, float b, float c, float d, float inv) {
+  const int ia = min(max(cvt_i32_sat(__builtin_rintf(a * inv)), -128), 127);
+  const int ib = min(max(cvt_i32_sat(__builtin_rintf(b * inv)), -128), 127);
+  const int ic = min(max(cvt_i32_sat(__builtin_rintf(c * inv)), -128), 127);
+  const int id = min(max(cvt_i32_sat(__builtin_rintf(d * inv)), -128), 127);
+  // perm(S0, S1, sel): selector byte 0-3 picks a byte of S1, 4-7 of S0, 0x0c gives 0.
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)ib, (uint32_t)ia, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)id, (uint32_t)ic, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+// Eight consecutive values into two packed words.
+Q35_DEV uint2 quant8_i8(const float* v, float inv) {
+  return make_uint2(quant4_i8(v[0], v[1], v[2], v[3], inv), quant4_i8(v[4], v[5], v[6], v[7], inv));
 }
 
 // 16 int8 pairs into an int32 accumulator (v_dot4c_i32_i8).

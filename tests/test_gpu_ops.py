@@ -500,15 +500,48 @@ def test_a8w8_linear_config2(gpu, m, n, k):
     close(y, ey)
 
 
-def test_a8w8_zero_row(gpu):
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_a8w8_zero_row(gpu, m):
+    """An all-zero token row quantises to 0 with scale 0 (0 * inf -> NaN -> 0)."""
     from ppu_amd import kernels as K
 
     g = gen(KERNEL_SEED + 22)
     w = randn(g, 64, 2048, scale=0.02)
-    x = torch.zeros(1, 2048, dtype=BF)
+    x = randn(g, m, 2048)
+    x[m - 1] = 0
     wq, sw = K.quantize_weight_i8(w.to(gpu))
     y, xq, sx = K.a8w8_linear(x.to(gpu), wq, sw, return_quant=True)
-    assert not xq.any() and float(sx) == 0.0 and not y.float().any()
+    assert not xq[m - 1].any() and float(sx[m - 1]) == 0.0 and not y[m - 1].float().any()
+    if m > 1:
+        assert xq[0].any() and float(sx[0]) > 0.0
+
+
+@pytest.mark.parametrize("m", [3, 8, 16])
+@pytest.mark.parametrize("n,k", [(12288, 2048), (2048, 6144)])
+def test_a8w8_prequantised_abi(gpu, m, n, k):
+    """q35_gemv_a8w8 with x = NULL: the int8 rows and their scales are inputs
+    (the skinny matrix-core path without the fused quantisation); int32
+    accumulators bit-exact, one all-zero token row included."""
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 23)
+    w = randn(g, n, k, scale=0.02)
+    x = randn(g, m, k)
+    x[1] = 0
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    ewq, esw = oa.quantize_weight(w)
+    ey, exq, esx, eacc = oa.a8w8_linear(x, ewq, esw)
+    xq = torch.from_numpy(exq).to(gpu)
+    sx = torch.from_numpy(esx).reshape(m, 1).to(gpu)
+    swf = sw.reshape(-1).float().contiguous()
+    y = torch.empty(m, n, dtype=BF, device=gpu)
+    acc = torch.empty(m, n, dtype=torch.int32, device=gpu)
+    _lib.call("q35_gemv_a8w8", None, xq.data_ptr(), sx.data_ptr(), wq.data_ptr(), swf.data_ptr(),
+              y.data_ptr(), acc.data_ptr(), m, n, k, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(acc.cpu().numpy(), eacc)
+    close(y, ey)
 
 
 def _i8_row(prologue, x, u, nw):
