@@ -240,6 +240,16 @@ int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, void* s
 int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void* s_w, void* y,
                   void* acc_out, int M, int N, int K, void* stream);
 
+/* Prefill GEMM on the matrix cores: C[M,N] = bf16(A[M,K] . B[N,K]^T), bf16 in,
+ * fp32 accumulate. K a multiple of 128, A and B 16-byte aligned, M*K and N*K
+ * below 2^32. Replaces F.linear at the prefill sites integration.py:183,245,298. */
+int q35_gemm_bf16(const void* A, const void* B, void* C, int M, int N, int K, void* stream);
+/* Packed gate/up projection with SwiGLU in the epilogue: B = [gate; up] is
+ * [2N, K]; C[M,N] = bf16(bf16(silu(bf16(A.Bg^T))) * bf16(A.Bu^T)). Replaces
+ * F.linear on the packed weight followed by silu_and_mul (integration.py:183-185,
+ * kernels.py:158-180) for prefill. Same constraints as q35_gemm_bf16. */
+int q35_gemm_swiglu_bf16(const void* A, const void* B, void* C, int M, int N, int K, void* stream);
+
 /* y[M,N] = bf16(float(acc[m,n]) * s_x[m] * s_w[n]) for int32 accumulators of an
  * int8 GEMM (the prefill A8W8 path; N % 8 == 0). Same dequant epilogue as
  * q35_gemv_a8w8, replacing the output stage of explore_runtime_quantization.py:173-180. */

@@ -68,6 +68,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_quant_act_i8": (_I, [_P, _P, _P, _I, _I, _P]),
     "q35_gemv_a8w8": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "q35_dequant_i32": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "q35_gemm_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "q35_gemm_swiglu_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -410,6 +410,35 @@ def prefill_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(x, weight)
 
 
+def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False) -> torch.Tensor:
+    """The hand-written matrix-core prefill GEMM: ``F.linear(x, W)`` (bf16 in
+    and out, fp32 accumulate) or, with ``swiglu``, ``silu_and_mul(F.linear(x,
+    W))`` for a packed ``[gate; up]`` weight in one launch (reference
+    integration.py:183-185, kernels.py:158-180). K must be a multiple of 128.
+    ``prefill_linear`` uses the ROCm library GEMM instead, which measured
+    faster at the model's prefill shapes."""
+
+    k = x.shape[-1]
+    if weight.ndim != 2 or weight.shape[1] != k:
+        raise ValueError("GEMM weight must be [N, K] matching the input")
+    if k % 128:
+        raise ValueError("the matrix-core GEMM needs K to be a multiple of 128")
+    if swiglu and weight.shape[0] % 2:
+        raise ValueError("packed SwiGLU weight must have an even number of rows")
+    if not x.is_cuda or not weight.is_contiguous():
+        raise ValueError("GEMM tensors must be contiguous GPU tensors")
+    _need_bf16(x, weight)
+    x2 = x.reshape(-1, k).contiguous()
+    m = x2.shape[0]
+    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    y = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_BF16)
+    if m == 0:
+        return y
+    name = "q35_gemm_swiglu_bf16" if swiglu else "q35_gemm_bf16"
+    _lib.call(name, x2.data_ptr(), weight.data_ptr(), y.data_ptr(), m, n, k, _stream(x))
+    return y
+
+
 def ppu_swiglu_gemv(
     x: torch.Tensor,
     packed_weight: torch.Tensor,

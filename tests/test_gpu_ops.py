@@ -516,6 +516,44 @@ def test_a8w8_zero_row(gpu, m):
         assert xq[0].any() and float(sx[0]) > 0.0
 
 
+@pytest.mark.parametrize("m,n,k", [(1024, 12288, 2048), (300, 1000, 2048), (64, 2048, 6144),
+                                   (1, 200, 128)])
+def test_gemm_bf16(gpu, m, n, k):
+    """Matrix-core GEMM vs the fp32 product, rounded once to bf16: rtol 1e-2 /
+    atol 1e-3 against the bf16-rounded reference (ragged M and N tiles)."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 90)
+    x, w = randn(g, m, k), randn(g, n, k, scale=0.02)
+    y = K.gemm_bf16(x.to(gpu), w.to(gpu))
+    close(y, (x.float() @ w.float().t()).to(BF))
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 6144, 2048), (200, 500, 2048)])
+def test_gemm_swiglu_bf16(gpu, m, n, k):
+    """Packed gate/up GEMM with the SwiGLU epilogue vs F.linear + silu_and_mul
+    rounding points on the fp32 product. g and u are each rounded to bf16 from
+    fp32 sums taken in another order, so a one-ulp flip in g and in u can
+    compound with the final rounding: every element within rtol 2e-2 /
+    atol 2e-3, and all but 1e-5 of them within the rtol 1e-2 / atol 1e-3 bar."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 91)
+    x, w = randn(g, m, k), randn(g, 2 * n, k, scale=0.02)
+    y = K.gemm_bf16(x.to(gpu), w.to(gpu), swiglu=True).float().cpu()
+    exp = ref.silu_and_mul((x.float() @ w.float().t()).to(BF)).float()
+    close(y, exp, rtol=2e-2, atol=2e-3)
+    outside = ((y - exp).abs() > 1e-3 + 1e-2 * exp.abs()).sum().item()
+    assert outside <= 1e-5 * exp.numel()
+
+
+def test_gemm_bf16_rejects_k():
+    from ppu_amd import kernels as K
+
+    with pytest.raises(ValueError):
+        K.gemm_bf16(torch.zeros(4, 96, dtype=BF), torch.zeros(8, 96, dtype=BF))
+
+
 @pytest.mark.parametrize("m", [3, 8, 16])
 @pytest.mark.parametrize("n,k", [(12288, 2048), (2048, 6144)])
 def test_a8w8_prequantised_abi(gpu, m, n, k):
