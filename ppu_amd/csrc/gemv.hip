@@ -24,6 +24,9 @@
 //             y[n] = bf16(bf16(silu(bf16(g))) * bf16(u))          [kernels.py:183-263]
 //   TOP1    : key = (ordered bf16(acc), inverted row); one max key per
 //             workgroup into a candidate array                    [kernels.py:1093-1143]
+//             (lm_head_top1_persist and the generic fallback)
+#include <algorithm>
+
 #include "q35_common.hpp"
 
 namespace {
@@ -86,11 +89,10 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
   constexpr int PER = (NV + NT - 1) / NT;       // groups per thread
   constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;  // outputs per wave
   static_assert(NV % NT == 0 || NT % NV == 0, "activation groups must tile the workgroup");
-  static_assert(!I8 || EPI != EPI_TOP1, "the top-1 epilogue is bf16 only");
+  static_assert(EPI != EPI_TOP1, "the lm_head top-1 runs in lm_head_top1_persist");
   __shared__ uint4 xs[I8 ? 1 : NV];             // bf16 activation (8 per group)
   __shared__ uint2 xq_s[I8 ? NV : 1];           // int8 activation (8 per group)
   __shared__ float red[WV], redm[WV];
-  __shared__ unsigned long long best_s[WV];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -310,21 +312,6 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
   }
 
   // 6. epilogue.
-  if (EPI == EPI_TOP1) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (n0 + r < a.N) best = u64_max(best, top1_key(round_bf(acc[r]), (uint32_t)(n0 + r)));
-    if (lane == 0) best_s[wid] = best;
-    lds_barrier();
-    if (tid == 0) {
-      uint64_t b = best_s[0];
-#pragma unroll
-      for (int v = 1; v < WV; ++v) b = u64_max(b, best_s[v]);
-      a.cand[blockIdx.x] = b;
-    }
-    return;
-  }
   if (lane < P && n0 + lane < a.N) {
     const int n = n0 + lane;
     float v;
@@ -461,6 +448,75 @@ __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __r
   }
 }
 
+// lm_head GEMV + top-1 as a persistent grid (a few workgroups per CU): wave w
+// of the grid takes row groups w, w + G, w + 2G, ... (G = waves in the grid,
+// R rows per group) and keeps its best (value, index) key in a register.
+// The hidden vector is held in registers (lane l owns k = c*512 + 8l), the
+// next group's rows are requested before the current group is reduced, and
+// no workgroup prologue repeats per row group; one key per workgroup goes to
+// top1_final. Group indices past the wave's last are clamped to it (the
+// repeated rows are re-reads of lines just fetched and change no key).
+template <int WV, int R, int NCH>
+__global__ __launch_bounds__(WV * 64) void lm_head_top1_persist(const GemvArgs a) {
+  __shared__ unsigned long long best_s[WV];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int G = gridDim.x * WV;
+  const int wg = blockIdx.x * WV + wid;
+  const int ngroups = (a.N + R - 1) / R;
+  const int niter = wg < ngroups ? (ngroups - 1 - wg) / G + 1 : 0;
+  float xf[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) unpack8(*reinterpret_cast<const uint4*>(a.x + c * 512 + 8 * lane), xf[c]);
+  const size_t row_bytes = (size_t)a.K * 2;
+  const uint8_t* wbase = reinterpret_cast<const uint8_t*>(a.W) + lane * 16;
+  uint64_t best = 0;
+  uint4 w0[R][NCH], w1[R][NCH];
+#define Q35_LM_LOAD(WB, IT)                                                           \
+  do {                                                                                \
+    const int grp = wg + min((IT), max(niter - 1, 0)) * G;                            \
+    _Pragma("unroll") for (int r = 0; r < R; ++r) {                                   \
+      const int row = min(grp * R + r, a.N - 1);                                      \
+      const uint8_t* wr = wbase + (size_t)row * row_bytes;                            \
+      _Pragma("unroll") for (int c = 0; c < NCH; ++c) WB[r][c] = ld_stream16(wr + c * 1024); \
+    }                                                                                 \
+  } while (0)
+#define Q35_LM_REDUCE(WB, IT)                                                         \
+  do {                                                                                \
+    const int grp = wg + (IT) * G;                                                    \
+    _Pragma("unroll") for (int r = 0; r < R; ++r) {                                   \
+      float acc = 0.f;                                                                \
+      _Pragma("unroll") for (int c = 0; c < NCH; ++c) {                               \
+        float wf[8];                                                                  \
+        unpack8(WB[r][c], wf);                                                        \
+        _Pragma("unroll") for (int e = 0; e < 8; ++e) acc = fmaf(wf[e], xf[c][e], acc); \
+      }                                                                               \
+      acc = wave_sum(acc);                                                            \
+      const int row = grp * R + r;                                                    \
+      if (row < a.N) best = u64_max(best, top1_key(round_bf(acc), (uint32_t)row));    \
+    }                                                                                 \
+  } while (0)
+  if (niter > 0) {
+    Q35_LM_LOAD(w0, 0);
+    for (int it = 0; it < niter; it += 2) {
+      Q35_LM_LOAD(w1, it + 1);
+      Q35_LM_REDUCE(w0, it);
+      if (it + 1 >= niter) break;
+      Q35_LM_LOAD(w0, it + 2);
+      Q35_LM_REDUCE(w1, it + 1);
+    }
+  }
+#undef Q35_LM_LOAD
+#undef Q35_LM_REDUCE
+  if (lane == 0) best_s[wid] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = best_s[0];
+#pragma unroll
+    for (int v = 1; v < WV; ++v) b = u64_max(b, best_s[v]);
+    a.cand[blockIdx.x] = b;
+  }
+}
+
 template <int WV, int R, int NCH, int PRO, int EPI, bool I8 = false>
 long long launch_fast(const GemvArgs& a, hipStream_t stream) {
   constexpr int P = EPI == EPI_SWIGLU ? R / 2 : R;
@@ -528,10 +584,23 @@ int dispatch_i8(const GemvArgs& a, hipStream_t stream) {
   return (int)hipErrorInvalidValue;
 }
 
-// lm_head tile: 4 waves x 4 rows per workgroup, 15520 candidates for the
-// final reduction (one row per wave ran 2% faster but quadrupled the final
-// reduction; a persistent grid-stride variant was slower).
-constexpr int kTopWV = 4, kTopR = 4;
+// Persistent lm_head grid, from a sweep (MI355X, 1.017 GB of weights): 4
+// waves per workgroup, one row per group, 2 workgroups per CU (512 keys for
+// top1_final); 143.6 us against 160.6 us for the one-workgroup-per-16-rows
+// grid of gemv_fused. 6-8 waves per CU measured best; 4 per CU or 16 per CU
+// lost 5-20 %.
+constexpr int kLmWV = 4, kLmR = 1, kLmBlocksPerCU = 2;
+static int lm_device_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+      cus = prop.multiProcessorCount;
+    if (cus <= 0) cus = 256;
+  }
+  return cus;
+}
 
 }  // namespace
 
@@ -682,7 +751,8 @@ int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace
              nullptr, 0};
   long long nc;
   if (K == 2048 && fast_ok(a, PRO_NONE)) {
-    nc = launch_fast<kTopWV, kTopR, 4, PRO_NONE, EPI_TOP1>(a, stream);
+    nc = std::min<long long>((long long)lm_device_cus() * kLmBlocksPerCU, workspace_slots);
+    lm_head_top1_persist<kLmWV, kLmR, 4><<<(unsigned)nc, kLmWV * 64, 0, stream>>>(a);
   } else {
     nc = (V + 3) / 4;
     gemv_bf16_generic<PRO_NONE, EPI_TOP1><<<(unsigned)nc, 256, 0, stream>>>(a);
