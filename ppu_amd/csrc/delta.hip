@@ -536,7 +536,12 @@ __global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qk
 //     all written in the per-lane order of the MFMA operands that
 //     delta_chunk_scan consumes (coalesced float4 loads).
 //   delta_chunk_scan : one workgroup per (16-column v tile, head): the
-//     [128 x 16] state tile in LDS, the three chunk products per chunk.
+//     [128 x 16] state tile in LDS and only the recurrence (U = U0 - W S,
+//     S <- gamma_C S + K''^T U) per chunk; the state entering each chunk and
+//     U are stored as snapshots.
+//   delta_chunk_out  : one workgroup per (chunk, head), all in parallel:
+//     O = Q' S + P U from the snapshots (the output products do not feed
+//     the next chunk, so they leave the sequential loop).
 // MFMA 16x16x4 f32 (wave64): A[16x4]: lane l holds row l%16, k l/16;
 // B[4x16]: k l/16, column l%16; C: rows 4*(l/16) + e, column l%16.
 constexpr int kChunk = 64;
@@ -546,9 +551,26 @@ constexpr int kSS = 17;   // fp32 row stride of the state and U tiles in LDS
 // Workspace floats per (batch, head, chunk): W^T, Q', K''^T, P, U0.
 constexpr int kOffWT = 0, kOffQP = 8192, kOffKT = 16384, kOffPQ = 24576, kOffU0 = 28672;
 constexpr int kChunkFloats = 36864;
+// Snapshot floats per (batch, head, chunk): for each 16-column v tile the
+// state entering the chunk and U, both transposed ([column][row]): S^T at
+// tile*3072, U^T at tile*3072 + 2048.
+constexpr int kSnapTile = 3072, kSnapU = 2048;
+constexpr int kSnapFloats = 8 * kSnapTile;
 
 Q35_DEV q35_f32x4 mfma4(float a, float b, q35_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Four consecutive 4-k MFMA steps with the lane's float4 operands, alternating
+// between two accumulators (c0 takes steps 0 and 2, c1 steps 1 and 3).
+Q35_DEV void mma4(const float4 a, const float4 bv, q35_f32x4 c0, q35_f32x4 c1, q35_f32x4& o0,
+                  q35_f32x4& o1) {
+  c0 = mfma4(a.x, bv.x, c0);
+  c1 = mfma4(a.y, bv.y, c1);
+  c0 = mfma4(a.z, bv.z, c0);
+  c1 = mfma4(a.w, bv.w, c1);
+  o0 = c0;
+  o1 = c1;
 }
 
 __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restrict__ qkv,
@@ -779,8 +801,7 @@ constexpr int kUT = kChunk + 4;  // fp32 per transposed U column
 __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict__ ws,
                                                         const float* __restrict__ gc,
                                                         float* __restrict__ state,
-                                                        uint16_t* __restrict__ out, int L, int H,
-                                                        int nC) {
+                                                        float* __restrict__ snap, int H, int nC) {
   // Workgroups are dispatched to the 8 XCDs round-robin by linear id; the 8
   // v tiles of a head read the same chunk operands, so they are placed on one
   // XCD (one L2 fill serves all 8): id = xcd + 8*slot, head = xcd + 8*(slot/8).
@@ -805,23 +826,18 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   __shared__ alignas(16) float Ut[16 * kUT];
   float* Sg = state + bh * kD * kD + tile * 16;
   for (int idx = tid; idx < kD * 16; idx += 256) St2[0][(idx & 15) * kST + (idx >> 4)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
-  // This wave's operands of one chunk: row tile wid of W^T, Q', P and U0, dk
-  // tiles 2*wid and 2*wid+1 of K''^T. Chunk c + 1 is requested before chunk c
-  // is computed.
+  // This wave's operands of one chunk: row tile wid of W^T and U0, dk tiles
+  // 2*wid and 2*wid+1 of K''^T. Chunk c + 1 is requested before chunk c is
+  // computed.
   struct ChunkOps {
-    float4 wt[8], qp[8], pq[4], kt[2][4], u0;
+    float4 wt[8], kt[2][4], u0;
     float gC;
   };
   auto load_ops = [&](int c, ChunkOps& op) {
     const float* wsb = ws + (bh * nC + c) * kChunkFloats;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < 8; ++dt)
       op.wt[dt] = *reinterpret_cast<const float4*>(wsb + kOffWT + ((wid * 8 + dt) * 64 + lane) * 4);
-      op.qp[dt] = *reinterpret_cast<const float4*>(wsb + kOffQP + ((wid * 8 + dt) * 64 + lane) * 4);
-    }
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-      op.pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd)
 #pragma unroll
@@ -831,83 +847,127 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
     op.u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
     op.gC = gc[bh * nC + c];
   };
-  auto mma4 = [](const float4 a, const float4 bv, q35_f32x4 c0, q35_f32x4 c1, q35_f32x4& o0,
-                 q35_f32x4& o1) {
-    c0 = mfma4(a.x, bv.x, c0);
-    c1 = mfma4(a.y, bv.y, c1);
-    c0 = mfma4(a.z, bv.z, c0);
-    c1 = mfma4(a.w, bv.w, c1);
-    o0 = c0;
-    o1 = c1;
-  };
-  ChunkOps cur;
-  load_ops(0, cur);
+  // Two operand sets alternate (chunk c computes from one while chunk c + 1
+  // loads into the other): copying a set whose loads are still in flight
+  // would wait for them.
+  ChunkOps opa, opb;
+  load_ops(0, opa);
   __syncthreads();
   float* ucol = &Ut[col * kUT + 4 * g4];
-  for (int c = 0; c < nC; ++c) {
-    ChunkOps nxt;
-    load_ops(min(c + 1, nC - 1), nxt);
-    float* St = St2[c & 1];
-    float* Sn = St2[(c & 1) ^ 1];
-    const float* scol = &St[col * kST + 4 * g4];
+#define Q35_SCAN_CHUNK(CUR, NXT, C)                                                           \
+  do {                                                                                        \
+    const int ci = (C); /* not named c: the argument is an expression in the loop's c */     \
+    load_ops(min(ci + 1, nC - 1), NXT);                                                        \
+    float* St = St2[ci & 1];                                                                   \
+    float* Sn = St2[(ci & 1) ^ 1];                                                             \
+    const float* scol = &St[col * kST + 4 * g4];                                              \
+    float* sp = snap + (bh * nC + ci) * kSnapFloats + tile * kSnapTile;                        \
+    /* Snapshot of the state entering the chunk ([column][row], 2 float4 per thread). */      \
+    _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                           \
+      const int q = tid + 256 * i; /* 512 float4: column q / 32, rows 4 * (q % 32) */         \
+      *reinterpret_cast<float4*>(sp + q * 4) =                                                \
+          *reinterpret_cast<const float4*>(&St[(q >> 5) * kST + 4 * (q & 31)]);               \
+    }                                                                                         \
+    /* U = U0 - W S (rows 16*wid.., this v tile) */                                           \
+    q35_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};                           \
+    _Pragma("unroll") for (int dt = 0; dt < 8; ++dt) {                                        \
+      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);                     \
+      mma4(CUR.wt[dt], sv, a0, a1, a0, a1);                                                   \
+    }                                                                                         \
+    const float4 uo = make_float4(CUR.u0.x - (a0[0] + a1[0]), CUR.u0.y - (a0[1] + a1[1]),     \
+                                  CUR.u0.z - (a0[2] + a1[2]), CUR.u0.w - (a0[3] + a1[3]));    \
+    *reinterpret_cast<float4*>(ucol + 16 * wid) = uo;                                         \
+    *reinterpret_cast<float4*>(sp + kSnapU + col * kChunk + 16 * wid + 4 * g4) = uo;          \
+    __syncthreads();                                                                          \
+    /* S <- gamma_C S + K''^T U (dk tiles 2*wid, 2*wid + 1) */                                \
+    q35_f32x4 sn[2];                                                                          \
+    _Pragma("unroll") for (int dd = 0; dd < 2; ++dd) {                                        \
+      const int dt = 2 * wid + dd;                                                            \
+      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);                     \
+      q35_f32x4 s0 = {CUR.gC * sv.x, CUR.gC * sv.y, CUR.gC * sv.z, CUR.gC * sv.w};            \
+      q35_f32x4 s1 = {0.f, 0.f, 0.f, 0.f};                                                    \
+      _Pragma("unroll") for (int s4 = 0; s4 < 4; ++s4) {                                      \
+        const float4 uv = *reinterpret_cast<const float4*>(ucol + 16 * s4);                   \
+        mma4(CUR.kt[dd][s4], uv, s0, s1, s0, s1);                                             \
+      }                                                                                       \
+      sn[dd] = s0 + s1;                                                                       \
+    }                                                                                         \
+    _Pragma("unroll") for (int dd = 0; dd < 2; ++dd)                                          \
+      *reinterpret_cast<float4*>(&Sn[col * kST + 16 * (2 * wid + dd) + 4 * g4]) =             \
+          make_float4(sn[dd][0], sn[dd][1], sn[dd][2], sn[dd][3]);                            \
+    __syncthreads(); /* the new state is complete; U and the old state are free */            \
+  } while (0)
+  for (int c = 0; c < nC; c += 2) {
+    Q35_SCAN_CHUNK(opa, opb, c);
+    if (c + 1 >= nC) break;
+    Q35_SCAN_CHUNK(opb, opa, c + 1);
+  }
+#undef Q35_SCAN_CHUNK
+  const float* Sf = St2[nC & 1];
+  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = Sf[(idx & 15) * kST + (idx >> 4)];
+}
 
-    // U = U0 - W S (rows 16*wid.., this v tile)
-    q35_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+// O = Q' S + P U for one (chunk, head) from the snapshots: the chunk's S and
+// U (all 8 v tiles, 96 KB) are staged once in LDS with padded column strides;
+// wave w (8 per workgroup, two per SIMD) takes a row tile of 16 tokens (w for
+// w < 4, 7 - w above) and column tiles 4 (w / 4) .. +3, with Q' and P loaded
+// once, and runs the
+// same MFMA chains (two alternating accumulators, Q' S first, then the causal
+// P U tiles) as the recurrence kernel's layout, so O is the token loop's
+// output in closed form.
+__global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__ ws,
+                                                       const float* __restrict__ snap,
+                                                       uint16_t* __restrict__ out, int L, int H,
+                                                       int nC) {
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // Waves w and w + 4 share a SIMD: pairing row tile w with row tile 3 - w
+  // gives every SIMD the same causal P U work.
+  const int tid = threadIdx.x, lane = tid & 63, half = tid >> 8;
+  const int wid = half ? 3 - ((tid >> 6) & 3) : (tid >> 6) & 3;
+  const int col = lane & 15, g4 = lane >> 4;
+  const size_t bhc = ((size_t)b * H + h) * nC + c;
+  const float* wsb = ws + bhc * kChunkFloats;
+  const float* sp = snap + bhc * kSnapFloats;
+  __shared__ alignas(16) float Ss[8 * 16 * kST];
+  __shared__ alignas(16) float Us[8 * 16 * kUT];
+  // Snapshot: per tile 512 float4 of S^T (column q/32, rows 4(q%32)) and 256 of U^T.
+  float4 st[12];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);
-      mma4(cur.wt[dt], sv, a0, a1, a0, a1);
-    }
-    const float4 uo = make_float4(cur.u0.x - (a0[0] + a1[0]), cur.u0.y - (a0[1] + a1[1]),
-                                  cur.u0.z - (a0[2] + a1[2]), cur.u0.w - (a0[3] + a1[3]));
-    *reinterpret_cast<float4*>(ucol + 16 * wid) = uo;
-
-    // O = Q' S + P U; Q' S needs only S, so it runs before the barrier that
-    // waits for every wave's U.
+  for (int i = 0; i < 12; ++i) st[i] = *reinterpret_cast<const float4*>(sp + (tid + 512 * i) * 4);
+  float4 qp[8], pq[4];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+    qp[dt] = *reinterpret_cast<const float4*>(wsb + kOffQP + ((wid * 8 + dt) * 64 + lane) * 4);
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)  // tiles above the diagonal are never used: read tile wid
+    pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
+#pragma unroll
+  for (int i = 0; i < 12; ++i) {
+    const int q = tid + 512 * i;          // float4 index in the snapshot
+    const int tile = q / 768, r = q % 768;
+    float* dst = r < 512 ? &Ss[(tile * 16 + (r >> 5)) * kST + 4 * (r & 31)]
+                         : &Us[(tile * 16 + ((r - 512) >> 4)) * kUT + 4 * ((r - 512) & 15)];
+    *reinterpret_cast<float4*>(dst) = st[i];
+  }
+  __syncthreads();
+#pragma unroll 2
+  for (int tt = 0; tt < 4; ++tt) {
+    const int tile = 4 * half + tt;
+    const float* scol = &Ss[(tile * 16 + col) * kST + 4 * g4];
+    const float* ucol = &Us[(tile * 16 + col) * kUT + 4 * g4];
     q35_f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);
-      mma4(cur.qp[dt], sv, o0, o1, o0, o1);
-    }
-    __syncthreads();
+    for (int dt = 0; dt < 8; ++dt)
+      mma4(qp[dt], *reinterpret_cast<const float4*>(scol + 16 * dt), o0, o1, o0, o1);
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      if (jt <= wid) {
-        const float4 uv = *reinterpret_cast<const float4*>(ucol + 16 * jt);
-        mma4(cur.pq[jt], uv, o0, o1, o0, o1);
-      }
-    }
+    for (int jt = 0; jt < 4; ++jt)
+      if (jt <= wid) mma4(pq[jt], *reinterpret_cast<const float4*>(ucol + 16 * jt), o0, o1, o0, o1);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = c * kChunk + 16 * wid + 4 * g4 + e;
       if (t < L) out[(((size_t)b * L + t) * H + h) * kD + tile * 16 + col] = (uint16_t)f2bf(o0[e] + o1[e]);
     }
-
-    // S <- gamma_C S + K''^T U (dk tiles 2*wid, 2*wid + 1)
-    q35_f32x4 sn[2];
-#pragma unroll
-    for (int dd = 0; dd < 2; ++dd) {
-      const int dt = 2 * wid + dd;
-      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);
-      q35_f32x4 s0 = {cur.gC * sv.x, cur.gC * sv.y, cur.gC * sv.z, cur.gC * sv.w};
-      q35_f32x4 s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const float4 uv = *reinterpret_cast<const float4*>(ucol + 16 * s4);
-        mma4(cur.kt[dd][s4], uv, s0, s1, s0, s1);
-      }
-      sn[dd] = s0 + s1;
-    }
-#pragma unroll
-    for (int dd = 0; dd < 2; ++dd)
-      *reinterpret_cast<float4*>(&Sn[col * kST + 16 * (2 * wid + dd) + 4 * g4]) =
-          make_float4(sn[dd][0], sn[dd][1], sn[dd][2], sn[dd][3]);
-    __syncthreads();  // the new state is complete; U and the old state are free
-    cur = nxt;
   }
-  const float* Sf = St2[nC & 1];
-  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = Sf[(idx & 15) * kST + (idx >> 4)];
 }
 
 }  // namespace
@@ -998,10 +1058,12 @@ int q35_delta_decode(const void* src, int src_stride, const void* packed, int pa
 constexpr int kChunkMinL = 64;
 
 // Floats of workspace q35_delta_prefill needs: 4 factors per (batch, token,
-// head), and for the chunked form 36864 floats + 1 per (batch, head, chunk).
+// head), and for the chunked form 36864 operand floats, 1 decay and 24576
+// snapshot floats per (batch, head, chunk).
 long long q35_delta_prefill_workspace(int B, int L, int H) {
   long long n = 4ll * B * L * H;
-  if (L >= kChunkMinL) n += (long long)B * H * ((L + kChunk - 1) / kChunk) * (kChunkFloats + 1);
+  if (L >= kChunkMinL)  // + 3: the snapshots start at the next 16-byte boundary
+    n += (long long)B * H * ((L + kChunk - 1) / kChunk) * (kChunkFloats + 1 + kSnapFloats) + 3;
   return n;
 }
 
@@ -1033,13 +1095,18 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
   Q35_CHECK_ARG(B < 65536 && H < 65536);
   float* chunk_ws = (float*)workspace + 4ll * B * L * H;
   float* gc = chunk_ws + (size_t)B * H * nC * kChunkFloats;
+  // Snapshots start 16-byte aligned after the B*H*nC chunk decays.
+  float* snap = gc + (((size_t)B * H * nC + 3) & ~(size_t)3);
   delta_chunk_prep<<<dim3(nC, H, B), 256, 0, stream>>>((const uint16_t*)qkv, qkv_stride,
                                                        (const float*)workspace, chunk_ws, gc, L, H,
                                                        nC);
   e = q35_last_error();
   if (e) return e;
-  delta_chunk_scan<<<dim3((kD / 16) * H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state,
-                                                              (uint16_t*)out, L, H, nC);
+  delta_chunk_scan<<<dim3((kD / 16) * H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state, snap,
+                                                              H, nC);
+  e = q35_last_error();
+  if (e) return e;
+  delta_chunk_out<<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L, H, nC);
   return q35_last_error();
 }
 
