@@ -847,6 +847,27 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
     op.u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
     op.gC = gc[bh * nC + c];
   };
+  // The same loads in two halves, issued between the MFMAs of the two phases
+  // of the previous chunk (the K''^T half during the U phase, the W^T half
+  // during the state update): 17 back-to-back 1 KiB loads per wave otherwise
+  // hold the wave ~0.5 us in the texture unit between chunks.
+  auto load_k = [&](int c, ChunkOps& op) {
+    const float* wsb = ws + (bh * nC + c) * kChunkFloats;
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        op.kt[dd][s4] =
+            *reinterpret_cast<const float4*>(wsb + kOffKT + (((2 * wid + dd) * 4 + s4) * 64 + lane) * 4);
+    op.gC = gc[bh * nC + c];
+  };
+  auto load_w = [&](int c, ChunkOps& op) {
+    const float* wsb = ws + (bh * nC + c) * kChunkFloats;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      op.wt[dt] = *reinterpret_cast<const float4*>(wsb + kOffWT + ((wid * 8 + dt) * 64 + lane) * 4);
+    op.u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
+  };
   // Two operand sets alternate (chunk c computes from one while chunk c + 1
   // loads into the other): copying a set whose loads are still in flight
   // would wait for them.
@@ -857,7 +878,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
 #define Q35_SCAN_CHUNK(CUR, NXT, C)                                                           \
   do {                                                                                        \
     const int ci = (C); /* not named c: the argument is an expression in the loop's c */     \
-    load_ops(min(ci + 1, nC - 1), NXT);                                                        \
+    const int cn = min(ci + 1, nC - 1);                                                       \
     float* St = St2[ci & 1];                                                                   \
     float* Sn = St2[(ci & 1) ^ 1];                                                             \
     const float* scol = &St[col * kST + 4 * g4];                                              \
@@ -878,6 +899,11 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
                                   CUR.u0.z - (a0[2] + a1[2]), CUR.u0.w - (a0[3] + a1[3]));    \
     *reinterpret_cast<float4*>(ucol + 16 * wid) = uo;                                         \
     *reinterpret_cast<float4*>(sp + kSnapU + col * kChunk + 16 * wid + 4 * g4) = uo;          \
+    load_k(cn, NXT);                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                           \
+      __builtin_amdgcn_sched_group_barrier(0x8, 2, 0);                                        \
+      __builtin_amdgcn_sched_group_barrier(0x20, 1, 0);                                       \
+    }                                                                                         \
     __syncthreads();                                                                          \
     /* S <- gamma_C S + K''^T U (dk tiles 2*wid, 2*wid + 1) */                                \
     q35_f32x4 sn[2];                                                                          \
@@ -895,13 +921,21 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
     _Pragma("unroll") for (int dd = 0; dd < 2; ++dd)                                          \
       *reinterpret_cast<float4*>(&Sn[col * kST + 16 * (2 * wid + dd) + 4 * g4]) =             \
           make_float4(sn[dd][0], sn[dd][1], sn[dd][2], sn[dd][3]);                            \
+    load_w(cn, NXT);                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 9; ++i) {                                           \
+      __builtin_amdgcn_sched_group_barrier(0x8, 2, 0);                                        \
+      __builtin_amdgcn_sched_group_barrier(0x20, 1, 0);                                       \
+    }                                                                                         \
     __syncthreads(); /* the new state is complete; U and the old state are free */            \
   } while (0)
-  for (int c = 0; c < nC; c += 2) {
+  // Pairs of chunks with no branch between them (a conditional second half
+  // let the compiler sink the prefetch into it, next to its use).
+  int c = 0;
+  for (; c + 1 < nC; c += 2) {
     Q35_SCAN_CHUNK(opa, opb, c);
-    if (c + 1 >= nC) break;
     Q35_SCAN_CHUNK(opb, opa, c + 1);
   }
+  if (c < nC) Q35_SCAN_CHUNK(opa, opb, c);
 #undef Q35_SCAN_CHUNK
   const float* Sf = St2[nC & 1];
   for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = Sf[(idx & 15) * kST + (idx >> 4)];
