@@ -378,63 +378,65 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
     l[g] = 0.f;
     acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.f;
   }
-  for (int it = 0; it < n_iter; ++it) {
-    uint4 kn[2][2];
-    uint2 vn[kWaveTok];
-    load_kv(it + 1, kn, vn);  // past the end this re-reads the last valid row
-    const int tb = start + it * kIterTok + wid * kWaveTok;
-    float vf[kWaveTok][4];
-#pragma unroll
-    for (int i = 0; i < kWaveTok; ++i) {
-      vf[i][0] = bf_lo(vr[i].x);
-      vf[i][1] = bf_hi(vr[i].x);
-      vf[i][2] = bf_lo(vr[i].y);
-      vf[i][3] = bf_hi(vr[i].y);
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float s[2];
-#pragma unroll
-      for (int gi = 0; gi < 2; ++gi) {
-        const uint4 k0 = kr[gi][0], k1 = kr[gi][1];
-        float d = dot2_bf16(qp[g][0], k0.x, 0.f);
-        d = dot2_bf16(qp[g][1], k0.y, d);
-        d = dot2_bf16(qp[g][2], k0.z, d);
-        d = dot2_bf16(qp[g][3], k0.w, d);
-        d = dot2_bf16(qp[g][4], k1.x, d);
-        d = dot2_bf16(qp[g][5], k1.y, d);
-        d = dot2_bf16(qp[g][6], k1.z, d);
-        d = dot2_bf16(qp[g][7], k1.w, d);
-        d = row16_sum(d) * scale;
-        s[gi] = tb + 4 * gi + rw < end ? d : -INFINITY;
-      }
-      const float m_new = fmaxf(m[g], rows4_max(fmaxf(s[0], s[1])));
-      // A wave whose tokens so far all lie past the valid end keeps m = -inf:
-      // subtract 0 then, so that corr and p are 0 instead of NaN.
-      const float m_sub = m_new == -INFINITY ? 0.f : m_new;
-      const float corr = expf(m[g] - m_sub);
-      const float p0 = expf(s[0] - m_sub), p1 = expf(s[1] - m_sub);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[g][e] *= corr;
-      float psum = 0.f;
-#pragma unroll
-      for (int i = 0; i < kWaveTok; ++i) {
-        const float pi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(i < 4 ? p0 : p1), 16 * (i & 3)));
-        psum += pi;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
-      }
-      l[g] = l[g] * corr + psum;
-      m[g] = m_new;
-    }
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      kr[gi][0] = kn[gi][0];
-      kr[gi][1] = kn[gi][1];
-    }
-#pragma unroll
-    for (int i = 0; i < kWaveTok; ++i) vr[i] = vn[i];
+  // One 32-token step of the workgroup from the registers KR / VR.
+#define Q35_ATT_STEP(KR, VR, IT)                                                                \
+  do {                                                                                          \
+    const int tb = start + (IT) * kIterTok + wid * kWaveTok;                                    \
+    float vf[kWaveTok][4];                                                                      \
+    _Pragma("unroll") for (int i = 0; i < kWaveTok; ++i) {                                      \
+      vf[i][0] = bf_lo(VR[i].x);                                                                \
+      vf[i][1] = bf_hi(VR[i].x);                                                                \
+      vf[i][2] = bf_lo(VR[i].y);                                                                \
+      vf[i][3] = bf_hi(VR[i].y);                                                                \
+    }                                                                                           \
+    _Pragma("unroll") for (int g = 0; g < G; ++g) {                                             \
+      float s[2];                                                                               \
+      _Pragma("unroll") for (int gi = 0; gi < 2; ++gi) {                                        \
+        const uint4 k0 = KR[gi][0], k1 = KR[gi][1];                                             \
+        float d = dot2_bf16(qp[g][0], k0.x, 0.f);                                               \
+        d = dot2_bf16(qp[g][1], k0.y, d);                                                       \
+        d = dot2_bf16(qp[g][2], k0.z, d);                                                       \
+        d = dot2_bf16(qp[g][3], k0.w, d);                                                       \
+        d = dot2_bf16(qp[g][4], k1.x, d);                                                       \
+        d = dot2_bf16(qp[g][5], k1.y, d);                                                       \
+        d = dot2_bf16(qp[g][6], k1.z, d);                                                       \
+        d = dot2_bf16(qp[g][7], k1.w, d);                                                       \
+        d = row16_sum(d) * scale;                                                               \
+        s[gi] = tb + 4 * gi + rw < end ? d : -INFINITY;                                         \
+      }                                                                                         \
+      const float m_new = fmaxf(m[g], rows4_max(fmaxf(s[0], s[1])));                           \
+      /* A wave whose tokens so far all lie past the valid end keeps m = -inf:              */  \
+      /* subtract 0 then, so that corr and p are 0 instead of NaN.                          */  \
+      const float m_sub = m_new == -INFINITY ? 0.f : m_new;                                     \
+      const float corr = expf(m[g] - m_sub);                                                    \
+      const float p0 = expf(s[0] - m_sub), p1 = expf(s[1] - m_sub);                             \
+      _Pragma("unroll") for (int e = 0; e < 4; ++e) acc[g][e] *= corr;                          \
+      float psum = 0.f;                                                                         \
+      _Pragma("unroll") for (int i = 0; i < kWaveTok; ++i) {                                    \
+        const float pi = __int_as_float(                                                        \
+            __builtin_amdgcn_readlane(__float_as_int(i < 4 ? p0 : p1), 16 * (i & 3)));          \
+        psum += pi;                                                                             \
+        _Pragma("unroll") for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]); \
+      }                                                                                         \
+      l[g] = l[g] * corr + psum;                                                                \
+      m[g] = m_new;                                                                             \
+    }                                                                                           \
+  } while (0)
+  // Two register sets alternate over pairs of steps, the next step's rows
+  // requested before the current one is reduced; nothing copies a set whose
+  // loads are in flight, and a single step (the decode shape) issues no
+  // prefetch at all.
+  uint4 kb[2][2];
+  uint2 vb[kWaveTok];
+  int it = 0;
+  for (; it + 1 < n_iter; it += 2) {
+    load_kv(it + 1, kb, vb);
+    Q35_ATT_STEP(kr, vr, it);
+    if (it + 2 < n_iter) load_kv(it + 2, kr, vr);
+    Q35_ATT_STEP(kb, vb, it + 1);
   }
+  if (it < n_iter) Q35_ATT_STEP(kr, vr, it);
+#undef Q35_ATT_STEP
 
   // The new token (FUSED): wave KW of the owning workgroup folds it in.
   if (owns_new && wid == KW) {
@@ -508,36 +510,38 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
 }
 
 // Log-sum-exp merge of the splits -> bf16, optionally times bf16(sigmoid(gate))
-// [reference kernels.py:1007-1028 and 285-333]. One workgroup per query head:
-// thread (part = wave, col = lane) owns dims 4*col..4*col+3 of splits
-// part, part + 4, ... (up to 4*B splits). Every thread requests its partials
-// (clamped indices) before wave 0 reads the (m, l) pairs and turns them into
-// weights in LDS, so the merge is one memory round trip; the four parts are
-// summed in LDS.
+// [reference kernels.py:1007-1028 and 285-333]. Grid (query head, quarter of
+// the 256 dims): thread (part = t/16, col = t%16) owns dims 64*quarter +
+// 4*col .. +3 of splits part, part + 16, ... (up to 16*B splits). Every
+// thread requests its partials (clamped indices) before wave 0 reads the
+// (m, l) pairs and turns them into weights in LDS, so the merge is one
+// memory round trip; the 16 parts are summed in LDS. Four workgroups per
+// head keep each thread's share of a 128-split merge at 8 loads.
 template <int B>
 __global__ __launch_bounds__(256) void gqa_decode_combine(const float* __restrict__ acc,
                                                           const float* __restrict__ ml,
                                                           const uint16_t* __restrict__ packed_gate,
                                                           uint16_t* __restrict__ out, int splits,
                                                           long long* advance_len) {
-  const int h = blockIdx.x;
+  const int h = blockIdx.x >> 2, qd = blockIdx.x & 3;
   const int t = threadIdx.x;
-  const int col = t & 63;
-  const int part = t >> 6;
+  const int col = t & 15;
+  const int part = t >> 4;
+  const int d0 = 64 * qd + 4 * col;
   // The split kernel that read the length has completed (stream order).
-  if (advance_len && h == 0 && t == 0) advance_len[0] += 1;
+  if (advance_len && blockIdx.x == 0 && t == 0) advance_len[0] += 1;
   const float* mlh = ml + (size_t)h * splits * 2;
-  const float* acch = acc + (size_t)h * splits * kAD + 4 * col;
+  const float* acch = acc + (size_t)h * splits * kAD + d0;
   __shared__ float w_s[kMaxSplits];
   __shared__ float lt_s;
-  __shared__ float4 red_s[4][kAD / 4];
+  __shared__ float4 red_s[16][16];
   const uint2 graw = packed_gate && part == 0
-                         ? *reinterpret_cast<const uint2*>(packed_gate + h * 2 * kAD + kAD + 4 * col)
+                         ? *reinterpret_cast<const uint2*>(packed_gate + h * 2 * kAD + kAD + d0)
                          : make_uint2(0, 0);
   float4 a[B];
 #pragma unroll
   for (int j = 0; j < B; ++j)
-    a[j] = *reinterpret_cast<const float4*>(acch + (size_t)min(part + 4 * j, splits - 1) * kAD);
+    a[j] = *reinterpret_cast<const float4*>(acch + (size_t)min(part + 16 * j, splits - 1) * kAD);
   if (t < 64) {
     float mx = -INFINITY;
     for (int s = t; s < splits; s += 64) mx = fmaxf(mx, mlh[2 * s]);
@@ -556,7 +560,7 @@ __global__ __launch_bounds__(256) void gqa_decode_combine(const float* __restric
   float4 tot = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < B; ++j) {
-    const int s = part + 4 * j;
+    const int s = part + 16 * j;
     const float w = s < splits ? w_s[s] : 0.f;
     tot.x = fmaf(a[j].x, w, tot.x);
     tot.y = fmaf(a[j].y, w, tot.y);
@@ -566,29 +570,37 @@ __global__ __launch_bounds__(256) void gqa_decode_combine(const float* __restric
   red_s[part][col] = tot;
   __syncthreads();
   if (part == 0) {
-    const float4 r0 = red_s[0][col], r1 = red_s[1][col], r2 = red_s[2][col], r3 = red_s[3][col];
+    float4 r = red_s[0][col];
+#pragma unroll
+    for (int p = 1; p < 16; ++p) {
+      const float4 v = red_s[p][col];
+      r.x += v.x;
+      r.y += v.y;
+      r.z += v.z;
+      r.w += v.w;
+    }
     const float lt = lt_s;
-    float o[4] = {round_bf(((r0.x + r1.x) + (r2.x + r3.x)) / lt), round_bf(((r0.y + r1.y) + (r2.y + r3.y)) / lt),
-                  round_bf(((r0.z + r1.z) + (r2.z + r3.z)) / lt), round_bf(((r0.w + r1.w) + (r2.w + r3.w)) / lt)};
+    float o[4] = {round_bf(r.x / lt), round_bf(r.y / lt), round_bf(r.z / lt), round_bf(r.w / lt)};
     if (packed_gate) {
       o[0] *= round_bf(sigmoid_f(bf_lo(graw.x)));
       o[1] *= round_bf(sigmoid_f(bf_hi(graw.x)));
       o[2] *= round_bf(sigmoid_f(bf_lo(graw.y)));
       o[3] *= round_bf(sigmoid_f(bf_hi(graw.y)));
     }
-    *reinterpret_cast<uint2*>(out + (size_t)h * kAD + 4 * col) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+    *reinterpret_cast<uint2*>(out + (size_t)h * kAD + d0) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
   }
 }
 
-// Combine launch for a split count (partials per thread = ceil(splits / 4)).
+// Combine launch for a split count (partials per thread = ceil(splits / 16)).
 void launch_combine(const float* acc, const float* ml, const uint16_t* gate, uint16_t* out, int QH,
                     int splits, long long* advance, hipStream_t stream) {
+  const unsigned grid = (unsigned)(4 * QH);
   if (splits <= 32)
-    gqa_decode_combine<8><<<QH, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
+    gqa_decode_combine<2><<<grid, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
   else if (splits <= 64)
-    gqa_decode_combine<16><<<QH, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
+    gqa_decode_combine<4><<<grid, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
   else
-    gqa_decode_combine<32><<<QH, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
+    gqa_decode_combine<8><<<grid, 256, 0, stream>>>(acc, ml, gate, out, splits, advance);
 }
 
 // ------------------------------------------------- causal prefill (MFMA)
