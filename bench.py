@@ -299,7 +299,7 @@ def main() -> None:
         # TTFT and the reference's decode formula through the generation loop.
         runner = FusedGreedyGenerator(model)
         first = runner.generate(prompt, NEW_TOKENS)  # builds cache + captures the graph
-        warm = [runner.generate(prompt, NEW_TOKENS) for _ in range(3)]
+        warm = [runner.generate(prompt, NEW_TOKENS) for _ in range(7)]  # median of 7 warm runs
         ttft_ms = statistics.median(r.ttft_seconds for r in warm) * 1e3
         loop_tps = statistics.median(r.decode_tokens_per_second for r in warm)
         assert all(r.tokens == first.tokens for r in warm), "greedy decode is not deterministic"

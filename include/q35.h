@@ -27,6 +27,12 @@ extern "C" {
 #define Q35_ABI_VERSION 1
 int q35_abi_version(void);
 
+/* Zero n device buffers in one launch: ptrs[i] (16-byte aligned) holds
+ * nbytes[i] bytes; ptrs and nbytes are host arrays. Replaces the per-tensor
+ * zero_() calls of Transformers' Cache.reset() on a reused generation cache
+ * (evaluation_wrapper.py:350-352). */
+int q35_zero_buffers(void* const* ptrs, const long long* nbytes, int n, void* stream);
+
 /* ---- norms and elementwise ------------------------------------------- */
 
 /* rms_norm: y = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)), rows x width.
@@ -239,6 +245,14 @@ int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, void* s
  * Replaces explore_runtime_quantization.py:161-181 (PPUA8W8Linear.forward). */
 int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void* s_w, void* y,
                   void* acc_out, int M, int N, int K, void* stream);
+
+/* Prefill SwiGLU of the packed [gate; up] A8W8 GEMM on its int32 accumulators
+ * acc[M, 2N]: y[M,N] = bf16(bf16(silu(g)) * u), g and u dequantised as in
+ * q35_dequant_i32 (N % 8 == 0, acc/s_w/y 16-byte aligned). Replaces the
+ * dequant of explore_runtime_quantization.py:173-180 followed by silu_and_mul
+ * (kernels.py:158-180) at integration.py:183-185. */
+int q35_dequant_swiglu_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,
+                           void* stream);
 
 /* Prefill GEMM on the matrix cores: C[M,N] = bf16(A[M,K] . B[N,K]^T), bf16 in,
  * fp32 accumulate. K a multiple of 128, A and B 16-byte aligned, M*K and N*K

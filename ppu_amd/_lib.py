@@ -24,6 +24,7 @@ _F = ctypes.c_float
 # name -> (restype, argtypes); mirrors include/q35.h (checked by the CPU tests).
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_abi_version": (_I, []),
+    "q35_zero_buffers": (_I, [_P, _P, _I, _P]),
     "q35_rmsnorm": (_I, [_P, _P, _I, _P, _I, _I, _F, _P]),
     "q35_residual_rmsnorm": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P]),
     "q35_gated_rmsnorm": (_I, [_P, _P, _P, _I, _P, _I, _I, _F, _P]),
@@ -68,6 +69,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_quant_act_i8": (_I, [_P, _P, _P, _I, _I, _P]),
     "q35_gemv_a8w8": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "q35_dequant_i32": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "q35_dequant_swiglu_i32": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "q35_gemm_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "q35_gemm_swiglu_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
 }

@@ -310,9 +310,61 @@ int launch_skinny(const A8Args& a, hipStream_t stream) {
   return q35_last_error();
 }
 
+// Prefill SwiGLU on the int32 accumulators of the packed [gate; up] int8
+// GEMM: g = bf16(acc[m, n] * s_x[m] * s_w[n]), u = bf16(acc[m, N+n] * s_x[m] *
+// s_w[N+n]) (the dequant of q35_dequant_i32), y[m, n] = bf16(bf16(silu(g)) *
+// u) (silu_and_mul's rounding points, the hardware exp/reciprocal SiLU of the
+// prefill SiLU-mul) -- the dequantised gate/up rows are never stored. Grid
+// (column blocks of 2048 outputs, rows); 8 outputs per thread.
+__global__ __launch_bounds__(256) void dequant_swiglu_rows(const int* __restrict__ acc,
+                                                           const float* __restrict__ s_x,
+                                                           const float* __restrict__ s_w,
+                                                           uint16_t* __restrict__ y, int M, int N) {
+  const int n = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (n >= N) return;
+  const float4 g0 = *reinterpret_cast<const float4*>(s_w + n);
+  const float4 g1 = *reinterpret_cast<const float4*>(s_w + n + 4);
+  const float4 u0 = *reinterpret_cast<const float4*>(s_w + N + n);
+  const float4 u1 = *reinterpret_cast<const float4*>(s_w + N + n + 4);
+  const float wg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const float wu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const int* row = acc + (size_t)m * 2 * N;
+    const int4 a0 = *reinterpret_cast<const int4*>(row + n);
+    const int4 a1 = *reinterpret_cast<const int4*>(row + n + 4);
+    const int4 b0 = *reinterpret_cast<const int4*>(row + N + n);
+    const int4 b1 = *reinterpret_cast<const int4*>(row + N + n + 4);
+    const float sx = s_x[m];
+    const int ag[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const int au[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float g = round_bf((float)ag[e] * sx * wg[e]);
+      const float u = round_bf((float)au[e] * sx * wu[e]);
+      o[e] = round_bf(silu_fast(g)) * u;
+    }
+    *reinterpret_cast<uint4*>(y + (size_t)m * N + n) = pack8(o);
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+// y[M,N] = bf16(bf16(silu(g)) * u) with g, u the dequantised columns n and
+// N + n of the int32 accumulators acc[M, 2N] of a packed [gate; up] A8W8
+// GEMM (N % 8 == 0, 16-byte aligned acc, s_w and y).
+int q35_dequant_swiglu_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,
+                           hipStream_t stream) {
+  Q35_CHECK_ARG(M > 0 && N > 0 && N % 8 == 0 && acc && s_x && s_w && y);
+  Q35_CHECK_ARG(q35_aligned16(acc) && q35_aligned16(y) && q35_aligned16(s_w));
+  const dim3 grid((unsigned)((N / 8 + 255) / 256), (unsigned)min(M, 65535));
+  dequant_swiglu_rows<<<grid, 256, 0, stream>>>((const int*)acc, (const float*)s_x,
+                                                (const float*)s_w, (uint16_t*)y, M, N);
+  return q35_last_error();
+}
+
 
 // y[M,N] = bf16(acc * s_x[m] * s_w[n]) for int32 accumulators from any int8 GEMM.
 int q35_dequant_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,

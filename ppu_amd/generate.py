@@ -17,7 +17,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .graph import GreedyDecodeGraph
-from .kernels import lm_head_argmax
+from .kernels import lm_head_argmax, zero_tensors
 
 
 @dataclass
@@ -38,6 +38,33 @@ def cache_bucket(input_len: int, max_new_tokens: int) -> int:
     """evaluation_wrapper.py:339-341."""
     required = input_len + max_new_tokens + 1
     return max(512, ((required + 127) // 128) * 128)
+
+
+def reset_cache(cache) -> None:
+    """Transformers' ``Cache.reset()`` (cache_utils: StaticLayer.reset and
+    LinearAttentionCacheLayerMixin.reset) with every tensor it zeroes cleared
+    by one kernel launch: the K/V of initialised attention layers, the
+    initialised conv and recurrent states of linear-attention layers and the
+    static layers' cumulative-length tensors; ``has_previous_state`` flags are
+    cleared and integer cumulative lengths set to 0 as there."""
+
+    tensors = []
+    for layer in cache.layers:
+        if hasattr(layer, "number_of_states"):
+            for i in range(layer.number_of_states):
+                if layer.is_conv_states_initialized[i]:
+                    tensors.append(layer.conv_states[i])
+                if layer.is_recurrent_states_initialized[i]:
+                    tensors.append(layer.recurrent_states[i])
+                layer.has_previous_state[i] = False
+        if getattr(layer, "is_initialized", False) and getattr(layer, "keys", None) is not None:
+            tensors += [layer.keys, layer.values]
+        if hasattr(layer, "cumulative_length"):
+            if isinstance(layer.cumulative_length, int):
+                layer.cumulative_length = 0
+            else:
+                tensors.append(layer.cumulative_length)
+    zero_tensors(tensors)
 
 
 class FusedGreedyGenerator:
@@ -69,7 +96,7 @@ class FusedGreedyGenerator:
         start = time.perf_counter()
         cache, fresh = self._cache(bucket)
         if not fresh:
-            cache.reset()
+            reset_cache(cache)
         positions = torch.arange(input_len, device=input_ids.device).view(1, -1)
         prefill = model.model(input_ids=input_ids, position_ids=positions, past_key_values=cache,
                               use_cache=True, return_dict=True)

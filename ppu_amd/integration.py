@@ -216,6 +216,8 @@ def _patch_mlp(module: torch.nn.Module, config: FusionConfig) -> None:
         if (config.ppu_swiglu_gemv and x.shape[:2] == (1, 1) and not gate_up.a8w8):
             activated = K.ppu_swiglu_gemv(x.contiguous(), gate_up.weight,
                                           block_n=config.ppu_swiglu_block_n)
+        elif gate_up.a8w8:
+            activated = K.a8w8_swiglu(x.contiguous(), gate_up.wq, gate_up.scale)
         else:
             activated = K.silu_and_mul(gate_up(x.contiguous()))
         return self._q35_down(activated)

@@ -938,6 +938,60 @@ def a8w8_linear(
     return (y, *extra)
 
 
+def a8w8_swiglu(x: torch.Tensor, weight_q: torch.Tensor, weight_scale: torch.Tensor) -> torch.Tensor:
+    """``silu_and_mul(a8w8_linear(x, Wq, s_w))`` for a packed ``[gate; up]``
+    int8 weight (reference integration.py:183-185 with PPUA8W8Linear,
+    explore_runtime_quantization.py:161-181): for prefill the int32
+    accumulators go straight into a fused dequant + SwiGLU kernel, so the
+    dequantised gate/up rows are never written; one token or a few use the
+    A8W8 GEMV and ``silu_and_mul``. Same values as the two-step form."""
+
+    k = x.shape[-1]
+    n2 = weight_q.shape[0]
+    if weight_q.ndim != 2 or weight_q.shape[1] != k or weight_q.dtype != torch.int8 or n2 % 2:
+        raise ValueError("packed A8W8 SwiGLU weight must be int8 [2N, K] matching the input")
+    x2 = x.reshape(-1, k)
+    m, n = x2.shape[0], n2 // 2
+    if m <= _A8W8_GEMV_MAX_M or n % 8 or k % 8:
+        return silu_and_mul(a8w8_linear(x, weight_q, weight_scale))
+    if not x.is_cuda or not weight_q.is_contiguous():
+        raise ValueError("A8W8 tensors must be contiguous GPU tensors")
+    _need_bf16(x)
+    x2 = x2.contiguous()
+    sw = weight_scale.reshape(-1).float().contiguous()
+    if sw.numel() != n2:
+        raise ValueError("A8W8 weight scale must have one value per output channel")
+    xq = torch.empty((m, k), device=x.device, dtype=torch.int8)
+    sx = torch.empty((m, 1), device=x.device, dtype=torch.float32)
+    _lib.call("q35_quant_act_i8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), m, k, _stream(x))
+    acc = torch._int_mm(xq, weight_q.t())
+    y = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_BF16)
+    _lib.call("q35_dequant_swiglu_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(), m,
+              n, _stream(x))
+    return y
+
+
+def zero_tensors(tensors) -> None:
+    """Zero a list of GPU tensors with one kernel launch (16-byte aligned
+    contiguous ones; any other is cleared with ``zero_()``)."""
+
+    fused = []
+    for t in tensors:
+        if t.is_cuda and t.is_contiguous() and t.data_ptr() % 16 == 0:
+            fused.append(t)
+        else:
+            t.zero_()
+    if not fused:
+        return
+    import ctypes
+
+    n = len(fused)
+    ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() for t in fused])
+    sizes = (ctypes.c_longlong * n)(*[t.numel() * t.element_size() for t in fused])
+    _lib.call("q35_zero_buffers", ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(sizes, ctypes.c_void_p),
+              n, _stream(fused[0]))
+
+
 # ------------------------------------------------------------------ out of scope
 def _vision_out_of_scope(name: str):
     def fn(*args, **kwargs):

@@ -117,6 +117,57 @@ def test_tiny_model_greedy_vs_oracle(gpu, fused, a8w8):
                           HIDDEN_BOUNDS["tiny"])
 
 
+def test_fused_cache_reset_matches_transformers(gpu):
+    """reset_cache (one zeroing launch) leaves a used cache exactly as
+    Transformers' Cache.reset() does, and a generator reusing its cache
+    reproduces the first run's tokens."""
+    from transformers.cache_utils import StaticCache
+
+    from ppu_amd.generate import FusedGreedyGenerator, reset_cache
+
+    cfg = synth.config_tiny()
+    model, _, _ = _build(cfg, gpu, None)
+    g = torch.Generator().manual_seed(11)
+    prompt = torch.randint(0, cfg.vocab_size, (1, 70), generator=g).to(gpu)
+
+    def used_cache():
+        cache = StaticCache(config=cfg, max_cache_len=512)
+        with torch.inference_mode():
+            pos = torch.arange(70, device=gpu).view(1, -1)
+            model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
+        return cache
+
+    def snapshot(cache):
+        out = []
+        for layer in cache.layers:
+            for name in ("keys", "values", "cumulative_length"):
+                v = getattr(layer, name, None)
+                out.append(v.clone() if isinstance(v, torch.Tensor) else v)
+            for d in ("conv_states", "recurrent_states", "has_previous_state"):
+                v = getattr(layer, d, None)
+                if isinstance(v, dict):
+                    out += [x.clone() if isinstance(x, torch.Tensor) else x for x in v.values()]
+        return out
+
+    ca, cb = used_cache(), used_cache()
+    assert any(isinstance(t, torch.Tensor) and t.any() for t in snapshot(cb))
+    with torch.inference_mode():  # the states are inference tensors, as in generate()
+        ca.reset()
+        reset_cache(cb)
+    torch.cuda.synchronize()
+    sa, sb = snapshot(ca), snapshot(cb)
+    assert len(sa) == len(sb)
+    for a, b in zip(sa, sb):
+        if isinstance(a, torch.Tensor):
+            assert torch.equal(a, b) and not b.any()
+        else:
+            assert a == b
+    gen_ = FusedGreedyGenerator(model)
+    first = gen_.generate(prompt, max_new_tokens=12)
+    again = gen_.generate(prompt, max_new_tokens=12)
+    assert again.meta["cache_reused"] and again.tokens == first.tokens
+
+
 def test_graph_replay_matches_eager_decode(gpu):
     """Graph replays advance the cache exactly as eager decode steps do."""
     from transformers.cache_utils import StaticCache

@@ -500,6 +500,25 @@ def test_a8w8_linear_config2(gpu, m, n, k):
     close(y, ey)
 
 
+@pytest.mark.parametrize("m", [4, 300])
+def test_a8w8_swiglu_prefill(gpu, m):
+    """Fused int32 dequant + SwiGLU equals a8w8_linear followed by silu_and_mul
+    bit for bit, and the oracle's A8W8 linear + SiLU-mul within tolerance."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 24)
+    n, k = 6144, 2048
+    w = randn(g, 2 * n, k, scale=0.02)
+    x = randn(g, m, k)
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    xg = x.to(gpu)
+    y = K.a8w8_swiglu(xg, wq, sw)
+    two_step = K.silu_and_mul(K.a8w8_linear(xg, wq, sw))
+    assert torch.equal(y, two_step)
+    ewq, esw = oa.quantize_weight(w)
+    close(y, ref.silu_and_mul(oa.a8w8_linear(x, ewq, esw)[0]))
+
+
 @pytest.mark.parametrize("m", [1, 4, 16])
 def test_a8w8_zero_row(gpu, m):
     """An all-zero token row quantises to 0 with scale 0 (0 * inf -> NaN -> 0)."""
