@@ -575,7 +575,10 @@ Q35_DEV void mma4(const float4 a, const float4 bv, q35_f32x4 c0, q35_f32x4 c1, q
 
 __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restrict__ qkv,
                                                         int qkv_stride,
-                                                        const float* __restrict__ factors,
+                                                        const uint16_t* __restrict__ packed,
+                                                        int packed_stride, const void* a_log,
+                                                        const void* dt_bias, int params_f32,
+                                                        int a_off, int b_off,
                                                         float* __restrict__ ws,
                                                         float* __restrict__ gc_out, int L, int H,
                                                         int nC) {
@@ -592,26 +595,53 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   __shared__ alignas(16) float Xs[4][16 * 17];     // per-wave 16 x 16 scratch
   __shared__ float G_s[kChunk], gam_s[kChunk], kf_s[kChunk], bg_s[kChunk], b_s[kChunk];
 
-  // 1. the chunk's k, q (scaled as the recurrence scales them) and v in fp32.
+  // 1. the chunk's k, q (scaled as the recurrence scales them) and v in fp32,
+  //    with the per-token factors of the token loop computed here: q_inv,
+  //    k_inv = rsqrt(sum of squares + 1e-6) over the head (the 4 threads of a
+  //    token hold 32 dims each: quad sum), g = -e^{A_log} softplus(a +
+  //    dt_bias), beta = sigmoid(b) [reference kernels.py:713-765].
   {
     const int i = tid >> 2, qq = tid & 3;  // token, 32-dim quarter
     const int t = c * kChunk + i;
     const bool live = t < L;
     const int tc = min(t, L - 1);
     const uint16_t* row = qkv + ((size_t)b * L + tc) * qkv_stride;
-    const float4 f = *reinterpret_cast<const float4*>(factors + (((size_t)b * L + tc) * H + h) * 4);
+    const uint16_t* prow = packed + ((size_t)b * L + tc) * packed_stride;
+    const float a_raw = bf2f(prow[a_off + h]), b_raw = bf2f(prow[b_off + h]);
+    const float alog = ld_param(a_log, h, params_f32), dtb = ld_param(dt_bias, h, params_f32);
+    float rq[4][8], rk[4][8];
+    uint4 rv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int d = qq * 32 + u * 8;
+      unpack8(*reinterpret_cast<const uint4*>(row + h * kD + d), rq[u]);
+      unpack8(*reinterpret_cast<const uint4*>(row + H * kD + h * kD + d), rk[u]);
+      rv[u] = *reinterpret_cast<const uint4*>(row + 2 * H * kD + h * kD + d);
+    }
+    float qs = 0.f, ks = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qs += rq[u][e] * rq[u][e];
+        ks += rk[u][e] * rk[u][e];
+      }
+    qs += __shfl_xor(qs, 1, 64);
+    ks += __shfl_xor(ks, 1, 64);
+    qs += __shfl_xor(qs, 2, 64);
+    ks += __shfl_xor(ks, 2, 64);
+    const float4 f = make_float4(rsqrt_cr(qs + 1e-6f), rsqrt_cr(ks + 1e-6f),
+                                 -expf(alog) * softplus20(a_raw + dtb), 1.0f / (1.0f + expf(-b_raw)));
     const float qscale = 0.08838834764831845f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int d = qq * 32 + u * 8;
       float fq[8], fk[8], fv[8];
-      unpack8(*reinterpret_cast<const uint4*>(row + h * kD + d), fq);
-      unpack8(*reinterpret_cast<const uint4*>(row + H * kD + h * kD + d), fk);
-      unpack8(*reinterpret_cast<const uint4*>(row + 2 * H * kD + h * kD + d), fv);
+      unpack8(rv[u], fv);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        fq[e] = live ? fq[e] * f.x * qscale : 0.f;
-        fk[e] = live ? fk[e] * f.y : 0.f;
+        fq[e] = live ? rq[u][e] * f.x * qscale : 0.f;
+        fk[e] = live ? rk[u][e] * f.y : 0.f;
         fv[e] = live ? fv[e] : 0.f;
       }
       float* qd = &Qh[i * kCS + d];
@@ -1114,12 +1144,13 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
   if (B == 0) return 0;
   const long long rows = (long long)B * L * H;
   Q35_CHECK_ARG(rows < (1ll << 30));
-  delta_factors16<<<(unsigned)((rows + 15) / 16), 256, 0, stream>>>(
-      (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
-      params_f32, (float*)workspace, (int)rows, H, 4 * H * D, 4 * H * D + H);
-  int e = q35_last_error();
-  if (e) return e;
+  int e = 0;
   if (L < kChunkMinL) {
+    delta_factors16<<<(unsigned)((rows + 15) / 16), 256, 0, stream>>>(
+        (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
+        params_f32, (float*)workspace, (int)rows, H, 4 * H * D, 4 * H * D + H);
+    e = q35_last_error();
+    if (e) return e;
     delta_scan<<<(unsigned)(B * H * (kD / 8)), 64, 0, stream>>>(
         (const uint16_t*)qkv, qkv_stride, (const float*)workspace, (float*)state, (uint16_t*)out, L,
         H);
@@ -1131,9 +1162,9 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
   float* gc = chunk_ws + (size_t)B * H * nC * kChunkFloats;
   // Snapshots start 16-byte aligned after the B*H*nC chunk decays.
   float* snap = gc + (((size_t)B * H * nC + 3) & ~(size_t)3);
-  delta_chunk_prep<<<dim3(nC, H, B), 256, 0, stream>>>((const uint16_t*)qkv, qkv_stride,
-                                                       (const float*)workspace, chunk_ws, gc, L, H,
-                                                       nC);
+  delta_chunk_prep<<<dim3(nC, H, B), 256, 0, stream>>>(
+      (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
+      params_f32, 4 * H * D, 4 * H * D + H, chunk_ws, gc, L, H, nC);
   e = q35_last_error();
   if (e) return e;
   delta_chunk_scan<<<dim3((kD / 16) * H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state, snap,
