@@ -172,6 +172,19 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
                       void* out, void* workspace, long long workspace_floats, int B, int L, int H,
                       int D, void* stream);
 
+/* q35_delta_prefill followed by the gated RMSNorm of every (token, head) row:
+ * y[b, t, h, :] = bf16(bf16(bf16(o * rsqrt(mean(o^2) + eps)) * bf16(norm_w)) *
+ * silu(z)), o the core output and z = packed[token, 3*H*D + h*D ...]. For L >=
+ * 64 the norm runs inside the chunked output kernel (out is not written);
+ * below, out receives the core output and a norm launch follows. Replaces
+ * the delta_recurrent_fused + gated_rms_norm pair at integration.py:255-271
+ * (kernels.py:854 and :139) for prefill. */
+int q35_delta_prefill_gated(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
+                            const void* a_log, const void* dt_bias, int params_f32, void* state,
+                            void* out, void* workspace, long long workspace_floats, int B, int L,
+                            int H, int D, const void* norm_w, int norm_w_f32, float eps, void* y,
+                            void* stream);
+
 /* ---- full attention --------------------------------------------------- */
 
 /* qgkv_norm_rope: per-head Q/K RMSNorm (1 + w), partial RoPE, Q to [B,QH,L,D];

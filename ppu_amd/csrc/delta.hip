@@ -971,18 +971,33 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = Sf[(idx & 15) * kST + (idx >> 4)];
 }
 
+// Gated RMSNorm fused into the output kernel (optional): with the core row
+// of a token spread over the lanes of two waves, y = bf16(bf16(bf16(o *
+// rsqrt(mean(o^2) + eps)) * bf16(w)) * silu(z)) with o the bf16 core output
+// and z the gate slice of the packed projection [reference kernels.py:115-155].
+struct GatedNormArgs {
+  const uint16_t* z;   // packed + z offset; gate of (token, head) at z + token*stride + head*128
+  long long z_stride;  // elements per token row of the packed projection
+  const void* w;       // [128] bf16 or fp32
+  int w_f32;
+  float eps;
+  uint16_t* y;         // [B, L, H, 128]
+};
+
 // O = Q' S + P U for one (chunk, head) from the snapshots: the chunk's S and
 // U (all 8 v tiles, 96 KB) are staged once in LDS with padded column strides;
 // wave w (8 per workgroup, two per SIMD) takes a row tile of 16 tokens (w for
 // w < 4, 7 - w above) and column tiles 4 (w / 4) .. +3, with Q' and P loaded
-// once, and runs the
-// same MFMA chains (two alternating accumulators, Q' S first, then the causal
-// P U tiles) as the recurrence kernel's layout, so O is the token loop's
-// output in closed form.
+// once, and runs the same MFMA chains (two alternating accumulators, Q' S
+// first, then the causal P U tiles) as the recurrence kernel's layout, so O
+// is the token loop's output in closed form. GN: the gated RMSNorm of each
+// token row is applied before the store (the two column halves of a row
+// meet in LDS for the sum of squares); otherwise the core output is stored.
+template <bool GN>
 __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__ ws,
                                                        const float* __restrict__ snap,
                                                        uint16_t* __restrict__ out, int L, int H,
-                                                       int nC) {
+                                                       int nC, const GatedNormArgs gn) {
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   // Waves w and w + 4 share a SIMD: pairing row tile w with row tile 3 - w
   // gives every SIMD the same causal P U work.
@@ -994,6 +1009,7 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
   const float* sp = snap + bhc * kSnapFloats;
   __shared__ alignas(16) float Ss[8 * 16 * kST];
   __shared__ alignas(16) float Us[8 * 16 * kUT];
+  __shared__ float ss_s[GN ? 2 : 1][kChunk];
   // Snapshot: per tile 512 float4 of S^T (column q/32, rows 4(q%32)) and 256 of U^T.
   float4 st[12];
 #pragma unroll
@@ -1005,6 +1021,22 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)  // tiles above the diagonal are never used: read tile wid
     pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
+  // GN: the lane's gate values and norm weights (4 tiles x 4 rows).
+  uint16_t zr[4][4];
+  float wn[4];
+  if (GN) {
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int cabs = (4 * half + tt) * 16 + col;
+      wn[tt] = gn.w_f32 ? reinterpret_cast<const float*>(gn.w)[cabs]
+                        : bf2f(reinterpret_cast<const uint16_t*>(gn.w)[cabs]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = min(c * kChunk + 16 * wid + 4 * g4 + e, L - 1);
+        zr[tt][e] = gn.z[((size_t)b * L + t) * gn.z_stride + (size_t)h * kD + cabs];
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 12; ++i) {
     const int q = tid + 512 * i;          // float4 index in the snapshot
@@ -1014,6 +1046,7 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
     *reinterpret_cast<float4*>(dst) = st[i];
   }
   __syncthreads();
+  float ob[4][4];
 #pragma unroll 2
   for (int tt = 0; tt < 4; ++tt) {
     const int tile = 4 * half + tt;
@@ -1028,8 +1061,38 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
       if (jt <= wid) mma4(pq[jt], *reinterpret_cast<const float4*>(ucol + 16 * jt), o0, o1, o0, o1);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int t = c * kChunk + 16 * wid + 4 * g4 + e;
-      if (t < L) out[(((size_t)b * L + t) * H + h) * kD + tile * 16 + col] = (uint16_t)f2bf(o0[e] + o1[e]);
+      if (GN) {
+        ob[tt][e] = round_bf(o0[e] + o1[e]);
+      } else {
+        const int t = c * kChunk + 16 * wid + 4 * g4 + e;
+        if (t < L) out[(((size_t)b * L + t) * H + h) * kD + tile * 16 + col] = (uint16_t)f2bf(o0[e] + o1[e]);
+      }
+    }
+  }
+  if (GN) {
+    // Sum of squares of each row: 4 tiles in the lane, the 16 column lanes
+    // (one DPP row), then the two halves through LDS.
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float ss = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) ss += ob[tt][e] * ob[tt][e];
+      ss = row16_sum(ss);
+      if (col == 0) ss_s[half][16 * wid + 4 * g4 + e] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 16 * wid + 4 * g4 + e;
+      const int t = c * kChunk + r;
+      const float inv = rsqrt_cr((ss_s[0][r] + ss_s[1][r]) / (float)kD + gn.eps);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float nb = round_bf(ob[tt][e] * inv);
+        const float weighted = round_bf(nb * round_bf(wn[tt]));
+        const float v = weighted * silu_f(bf2f(zr[tt][e]));
+        if (t < L) gn.y[(((size_t)b * L + t) * H + h) * kD + (4 * half + tt) * 16 + col] = (uint16_t)f2bf(v);
+      }
     }
   }
 }
@@ -1131,11 +1194,16 @@ long long q35_delta_prefill_workspace(int B, int L, int H) {
   return n;
 }
 
-// Sequential recurrence over L tokens (input: post-conv qkv), state in place.
-int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
-                      const void* a_log, const void* dt_bias, int params_f32, void* state,
-                      void* out, void* workspace, long long workspace_floats, int B, int L, int H,
-                      int D, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The prefill recurrence (token scan below 64 tokens, chunked form above);
+// with gn the chunked output kernel also applies the gated RMSNorm into gn->y.
+int delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
+                  const void* a_log, const void* dt_bias, int params_f32, void* state, void* out,
+                  void* workspace, long long workspace_floats, int B, int L, int H, int D,
+                  const GatedNormArgs* gn, hipStream_t stream) {
   Q35_CHECK_ARG(B >= 0 && L > 0 && H > 0 && D == kD);
   Q35_CHECK_ARG(qkv_stride >= 3 * H * D && qkv_stride % 8 == 0);
   Q35_CHECK_ARG(packed_stride >= 4 * H * D + 2 * H);
@@ -1171,8 +1239,52 @@ int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int p
                                                               H, nC);
   e = q35_last_error();
   if (e) return e;
-  delta_chunk_out<<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L, H, nC);
+  if (gn && gn->y)
+    delta_chunk_out<true><<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L, H,
+                                                             nC, *gn);
+  else
+    delta_chunk_out<false><<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L, H,
+                                                              nC, GatedNormArgs{});
   return q35_last_error();
+}
+
+}  // namespace
+
+// gated_rmsnorm of norm.hip, for the token-scan path of the fused entry point.
+extern "C" int q35_gated_rmsnorm_grouped(const void* x, const void* gate, int group_rows,
+                                         long long group_stride, const void* w, int w_f32, void* y,
+                                         int rows, float eps, hipStream_t stream);
+
+extern "C" {
+
+// Sequential recurrence over L tokens (input: post-conv qkv), state in place.
+int q35_delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
+                      const void* a_log, const void* dt_bias, int params_f32, void* state,
+                      void* out, void* workspace, long long workspace_floats, int B, int L, int H,
+                      int D, hipStream_t stream) {
+  return delta_prefill(qkv, qkv_stride, packed, packed_stride, a_log, dt_bias, params_f32, state,
+                       out, workspace, workspace_floats, B, L, H, D, nullptr, stream);
+}
+
+// The same recurrence followed by the gated RMSNorm of every (token, head)
+// row with the gate z = packed[token, 3*H*D + h*D ...] and weight norm_w:
+// y receives the normalised output ([B, L, H, D] bf16); out is the core
+// output (written by the token-scan path only).
+int q35_delta_prefill_gated(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
+                            const void* a_log, const void* dt_bias, int params_f32, void* state,
+                            void* out, void* workspace, long long workspace_floats, int B, int L,
+                            int H, int D, const void* norm_w, int norm_w_f32, float eps, void* y,
+                            hipStream_t stream) {
+  Q35_CHECK_ARG(norm_w && y && out && D == kD && packed_stride % 8 == 0);
+  Q35_CHECK_ARG(q35_aligned16(norm_w) && q35_aligned16(y) && q35_aligned16(packed));
+  const GatedNormArgs gn{(const uint16_t*)packed + 3ll * H * D, packed_stride, norm_w, norm_w_f32,
+                         eps, (uint16_t*)y};
+  const int e = delta_prefill(qkv, qkv_stride, packed, packed_stride, a_log, dt_bias, params_f32,
+                              state, out, workspace, workspace_floats, B, L, H, D,
+                              L >= kChunkMinL ? &gn : nullptr, stream);
+  if (e || L >= kChunkMinL) return e;
+  return q35_gated_rmsnorm_grouped(out, (const uint16_t*)packed + 3ll * H * D, H, packed_stride,
+                                   norm_w, norm_w_f32, y, B * L * H, eps, stream);
 }
 
 }  // extern "C"

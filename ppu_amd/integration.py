@@ -265,6 +265,11 @@ def _patch_delta(module: torch.nn.Module, config: FusionConfig) -> None:
         conv_state, recurrent_state = _delta_cache_tensors(
             self, cache_params, batch, seq_len, hidden_states.device, hidden_states.dtype)
         qkv = K.causal_conv1d_fused(packed, self._q35_conv_w, conv_state)
+        if self.head_v_dim == 128 and seq_len > 1 and self.conv_dim == 3 * self.value_dim:
+            # prefill: recurrence and gated norm (z read in place) in one call
+            core = K.delta_prefill_gated(qkv, packed, self.A_log, self.dt_bias, recurrent_state,
+                                         self.norm.weight, self.layer_norm_epsilon)
+            return self._q35_out(core.reshape(batch, seq_len, self.value_dim))
         core = K.delta_recurrent_fused(qkv, packed, self.A_log, self.dt_bias, recurrent_state,
                                        block_v=config.delta_block_v,
                                        precompute_factors=config.delta_precompute_factors)

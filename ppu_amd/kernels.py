@@ -594,6 +594,53 @@ def delta_recurrent_fused(
     return out
 
 
+def delta_prefill_gated(
+    qkv: torch.Tensor,
+    packed_projection: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    state: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """Prefill recurrence (``delta_recurrent_fused``, L > 1) followed by the
+    gated RMSNorm of every (token, head) row with the gate z read in place
+    from ``packed_projection`` (reference integration.py:255-271 with
+    kernels.py:115-155); for 64 or more tokens the norm runs inside the
+    chunked output kernel. Returns ``[B, L, H, D]`` bf16; ``state`` updated in
+    place."""
+
+    if qkv.ndim != 3 or packed_projection.ndim != 3 or state.ndim != 4:
+        raise ValueError("invalid delta recurrent tensor rank")
+    if not qkv.is_contiguous() or not packed_projection.is_contiguous() or not state.is_contiguous():
+        raise ValueError("delta recurrent tensors must be contiguous")
+    batch, seq_len, qkv_width = qkv.shape
+    _, heads, dim, value_dim = state.shape
+    if dim != value_dim or qkv_width != 3 * heads * dim or dim != 128 or seq_len < 2:
+        raise ValueError("delta prefill dimensions do not match (head dim 128, L > 1)")
+    packed_width = packed_projection.shape[-1]
+    if packed_width < qkv_width + heads * dim + 2 * heads or packed_width % 8:
+        raise ValueError("packed projection does not hold [qkv | z | a | b]")
+    if norm_weight.numel() != dim:
+        raise ValueError(f"norm weight has {norm_weight.numel()} values, expected {dim}")
+    if not qkv.is_cuda:
+        raise ValueError("fused kernels require a GPU tensor")
+    if state.dtype != torch.float32:
+        raise ValueError("delta recurrent state must be float32")
+    _need_bf16(qkv, packed_projection)
+    al, dt, pf = _delta_params(a_log, dt_bias)
+    w, wf = _param(norm_weight)
+    out = torch.empty((batch, seq_len, heads, dim), device=qkv.device, dtype=qkv.dtype)
+    y = torch.empty_like(out)
+    floats = _lib.load().q35_delta_prefill_workspace(batch, seq_len, heads)
+    workspace = torch.empty(floats, device=qkv.device, dtype=torch.float32)
+    _lib.call("q35_delta_prefill_gated", qkv.data_ptr(), qkv_width, packed_projection.data_ptr(),
+              packed_width, al.data_ptr(), dt.data_ptr(), pf, state.data_ptr(), out.data_ptr(),
+              workspace.data_ptr(), floats, batch, seq_len, heads, dim, w.data_ptr(), wf, float(eps),
+              y.data_ptr(), _stream(qkv))
+    return y
+
+
 def delta_decode_fused(
     packed_projection: torch.Tensor,
     conv_weight: torch.Tensor,

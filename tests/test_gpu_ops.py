@@ -249,6 +249,36 @@ def test_delta_recurrent(gpu, seq_len):
     torch.testing.assert_close(st.cpu(), st_ref, rtol=1e-3, atol=1e-6)
 
 
+@pytest.mark.parametrize("seq_len", [3, 63, 200, 1024])
+def test_delta_prefill_gated(gpu, seq_len):
+    """Prefill recurrence + gated RMSNorm in one call (the norm is fused into
+    the chunked output kernel from 64 tokens on). The core output of the
+    unfused call is checked against the oracle recurrence, and the fused
+    result against the oracle norm of that same core: the chain has four bf16
+    roundings, so comparing it end to end against an oracle core that differs
+    by one ulp in a few places would test the rounding chain, not the kernel.
+    The final state equals the unfused call's bit for bit."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 14)
+    heads, dim = 16, 128
+    qkv, packed, a_log, dt_bias, state = _delta_inputs(g, seq_len)
+    norm_w = randn(g, dim, scale=0.02, mean=1.0)
+    st_ref = state.clone()
+    core_ref = ref.delta_recurrent(qkv, packed, a_log, dt_bias, st_ref)
+    args = (qkv.to(gpu), packed.to(gpu), a_log.to(gpu), dt_bias.to(gpu))
+    st2 = state.to(gpu)
+    core = K.delta_recurrent_fused(*args, st2)
+    close(core, core_ref)
+    st = state.to(gpu)
+    got = K.delta_prefill_gated(*args, st, norm_w.to(gpu), 1e-6)
+    z = packed[..., 3 * heads * dim : 4 * heads * dim].reshape(-1, dim)
+    exp = ref.gated_rms_norm(core.cpu().reshape(-1, dim), z, norm_w).reshape(1, seq_len, heads, dim)
+    close(got, exp)
+    assert torch.equal(st, st2)
+    torch.testing.assert_close(st.cpu(), st_ref, rtol=1e-3, atol=1e-6)
+
+
 def test_config4_delta_64_steps(gpu):
     """16 heads x 128, S ~N(0,0.1), conv width 4 on q/k/v,
     beta = sigmoid(N(0,1)), g = -softplus(N(0,1)) (A_log = 0, dt_bias = 0),
