@@ -15,7 +15,9 @@ Printed (one JSON line on stdout):
                weights per launch) timed with HIP events on its stream;
                traffic = its HBM bytes per launch from the committed
                rocprofv3 --pmc summary profiles/lm_head_top1_traffic_pmc.txt
-               (made from ``bench.py --counter-probe`` runs)
+               (made from ``bench.py --counter-probe`` runs); read_ceiling
+               is a plain streaming read of the same weight bytes
+               (kernels.stream_read), the device's achievable read rate
   kernels     per-kernel achieved HBM GB/s of the BASELINE configs 1-4
                (rotating >= 640 MB of distinct buffers so the 256 MB MALL does
                not serve the weights), in-graph time per launch
@@ -97,12 +99,21 @@ def lm_head_roofline(model) -> dict:
     slots = (v + 3) // 4
     algo = v * k * 2 + k * 2 + 8  # weights + hidden + index
     achieved = algo / us / 1e3
+    # the device's achievable read rate: the same weight bytes read once by
+    # the plain streaming-read probe (same loads, no arithmetic)
+    read_us = graph_time_us(lambda i: K.stream_read(w), calls=10, reps=10)
+    read_gbs = v * k * 2 / read_us / 1e3
+    log(f"lm_head top-1: {us:.1f} us, {achieved:.0f} GB/s; plain read of the same bytes "
+        f"{read_us:.1f} us, {read_gbs:.0f} GB/s ({100 * achieved / read_gbs:.1f}% of it)")
     return {"kernel": "lm_head GEMV + top-1 [248320,2048] bf16", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": pmc_traffic("lm_head_top1_traffic_pmc.txt"),
             "us_per_launch": round(us, 2), "algorithmic_bytes": algo,
-            "workspace_bytes": slots * 8}
+            "workspace_bytes": slots * 8,
+            "read_ceiling": {"GB/s": round(read_gbs, 1), "us": round(read_us, 2),
+                             "frac_of_peak": round(read_gbs / PEAK_HBM_GBS, 4),
+                             "lm_head_frac_of_ceiling": round(achieved / read_gbs, 4)}}
 
 
 def kernel_table(dev) -> dict:

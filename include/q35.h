@@ -33,6 +33,15 @@ int q35_abi_version(void);
  * (evaluation_wrapper.py:350-352). */
 int q35_zero_buffers(void* const* ptrs, const long long* nbytes, int n, void* stream);
 
+/* Measurement utility with no counterpart in the reference: read nbytes
+ * (multiple of 16; p 16-byte aligned) once with the non-temporal 16-byte
+ * loads of the GEMV weight stream, one workgroup per CU, and write one XOR
+ * word per thread to out (out_words >= 256 * CUs; the workgroup count goes
+ * to *workgroups_out when not null). Timing it gives the HBM read rate the
+ * decode GEMVs can reach on this device. */
+int q35_stream_read(const void* p, long long nbytes, void* out, long long out_words, int* workgroups_out,
+                    void* stream);
+
 /* ---- norms and elementwise ------------------------------------------- */
 
 /* rms_norm: y = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)), rows x width.

@@ -25,6 +25,7 @@ _F = ctypes.c_float
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_abi_version": (_I, []),
     "q35_zero_buffers": (_I, [_P, _P, _I, _P]),
+    "q35_stream_read": (_I, [_P, _L, _P, _L, _P, _P]),
     "q35_rmsnorm": (_I, [_P, _P, _I, _P, _I, _I, _F, _P]),
     "q35_residual_rmsnorm": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P]),
     "q35_gated_rmsnorm": (_I, [_P, _P, _P, _I, _P, _I, _I, _F, _P]),

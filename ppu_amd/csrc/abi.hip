@@ -1,6 +1,7 @@
-// ABI version query (the value must match Q35_ABI_VERSION in include/q35.h)
-// and the cache reset: every state tensor of a reused KV / linear-attention
-// cache zeroed by one launch instead of one fill kernel per tensor.
+// ABI version query (the value must match Q35_ABI_VERSION in include/q35.h),
+// the cache reset (every state tensor of a reused KV / linear-attention cache
+// zeroed by one launch instead of one fill kernel per tensor) and the HBM
+// read-rate probe that the decode GEMVs are measured against.
 #include "q35_common.hpp"
 
 namespace {
@@ -24,6 +25,40 @@ __global__ __launch_bounds__(256) void zero_buffers(const ZeroArgs a) {
        off += (long long)gridDim.x * 256 * 16)
     *reinterpret_cast<q35_u32x4*>(p + off) = z;
   if (blockIdx.x == 0 && threadIdx.x < n - n16) p[n16 + threadIdx.x] = 0;
+}
+
+// Read-rate probe: every 16-byte group of p read once with non-temporal
+// loads (the GEMV weight-stream load), grid-stride over a persistent grid,
+// 8 loads per lane in flight, an XOR fold so no load is dead; one word per
+// thread. 8 loads per lane on one workgroup of 4 waves per CU was the
+// fastest of 36 shapes (grid size x loads in flight x row-chunked order)
+// over the 1 GB lm_head weight.
+constexpr int kReadU = 8;
+__global__ __launch_bounds__(256) void stream_read(const uint8_t* __restrict__ p, long long n16,
+                                                   uint32_t* __restrict__ out) {
+  const long long stride = (long long)gridDim.x * 256;
+  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + (kReadU - 1) * stride < n16; i += kReadU * stride) {
+    uint4 v[kReadU];
+#pragma unroll
+    for (int u = 0; u < kReadU; ++u) v[u] = ld_stream16(p + (i + u * stride) * 16);
+#pragma unroll
+    for (int u = 0; u < kReadU; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 v = ld_stream16(p + i * 16);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
 }
 
 }  // namespace
@@ -56,6 +91,19 @@ int q35_zero_buffers(void* const* ptrs, const long long* nbytes, int n, hipStrea
     if (e) return e;
   }
   return 0;
+}
+
+// Read nbytes (a multiple of 16, p 16-byte aligned) once; out receives one
+// XOR word per thread (out_words >= 256 * workgroups; workgroups = the CU
+// count, written to *workgroups_out when it is not null).
+int q35_stream_read(const void* p, long long nbytes, void* out, long long out_words, int* workgroups_out,
+                    hipStream_t stream) {
+  Q35_CHECK_ARG(p && out && nbytes > 0 && nbytes % 16 == 0 && q35_aligned16(p));
+  const int blocks = device_cus();
+  Q35_CHECK_ARG(out_words >= (long long)blocks * 256);
+  if (workgroups_out) *workgroups_out = blocks;
+  stream_read<<<blocks, 256, 0, stream>>>((const uint8_t*)p, nbytes / 16, (uint32_t*)out);
+  return q35_last_error();
 }
 
 }  // extern "C"

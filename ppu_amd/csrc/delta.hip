@@ -551,11 +551,13 @@ constexpr int kSS = 17;   // fp32 row stride of the state and U tiles in LDS
 // Workspace floats per (batch, head, chunk): W^T, Q', K''^T, P, U0.
 constexpr int kOffWT = 0, kOffQP = 8192, kOffKT = 16384, kOffPQ = 24576, kOffU0 = 28672;
 constexpr int kChunkFloats = 36864;
-// Snapshot floats per (batch, head, chunk): for each 16-column v tile the
-// state entering the chunk and U, both transposed ([column][row]): S^T at
-// tile*3072, U^T at tile*3072 + 2048.
-constexpr int kSnapTile = 3072, kSnapU = 2048;
-constexpr int kSnapFloats = 8 * kSnapTile;
+// Snapshot floats per (batch, head, chunk), in the B-operand order of the
+// output kernel's MFMAs (lane (col, g4) of 16x16x4 step group s reads the
+// float4 of rows 16s + 4g4 .. +3, column col): the state entering the chunk
+// as [v tile][k tile][lane] float4 (2048 floats per v tile), then U as
+// [v tile][token tile][lane] float4 (1024 floats per v tile) from kSnapU.
+constexpr int kSnapSTile = 2048, kSnapU = 8 * kSnapSTile, kSnapUTile = 1024;
+constexpr int kSnapFloats = kSnapU + 8 * kSnapUTile;
 
 Q35_DEV q35_f32x4 mfma4(float a, float b, q35_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -912,12 +914,14 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
     float* St = St2[ci & 1];                                                                   \
     float* Sn = St2[(ci & 1) ^ 1];                                                             \
     const float* scol = &St[col * kST + 4 * g4];                                              \
-    float* sp = snap + (bh * nC + ci) * kSnapFloats + tile * kSnapTile;                        \
-    /* Snapshot of the state entering the chunk ([column][row], 2 float4 per thread). */      \
+    float* sp = snap + (bh * nC + ci) * kSnapFloats;                                          \
+    /* Snapshot of the state entering the chunk in operand order (2 float4 per thread): */    \
+    /* float4 q = (k tile q / 64, lane q % 64) holds rows 16(q/64) + 4(lane/16) .. +3 of */   \
+    /* column lane % 16. */                                                                   \
     _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                           \
-      const int q = tid + 256 * i; /* 512 float4: column q / 32, rows 4 * (q % 32) */         \
-      *reinterpret_cast<float4*>(sp + q * 4) =                                                \
-          *reinterpret_cast<const float4*>(&St[(q >> 5) * kST + 4 * (q & 31)]);               \
+      const int q = tid + 256 * i, ln = q & 63;                                               \
+      *reinterpret_cast<float4*>(sp + tile * kSnapSTile + q * 4) = *reinterpret_cast<const float4*>( \
+          &St[(ln & 15) * kST + 16 * (q >> 6) + 4 * (ln >> 4)]);                              \
     }                                                                                         \
     /* U = U0 - W S (rows 16*wid.., this v tile) */                                           \
     q35_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};                           \
@@ -928,7 +932,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
     const float4 uo = make_float4(CUR.u0.x - (a0[0] + a1[0]), CUR.u0.y - (a0[1] + a1[1]),     \
                                   CUR.u0.z - (a0[2] + a1[2]), CUR.u0.w - (a0[3] + a1[3]));    \
     *reinterpret_cast<float4*>(ucol + 16 * wid) = uo;                                         \
-    *reinterpret_cast<float4*>(sp + kSnapU + col * kChunk + 16 * wid + 4 * g4) = uo;          \
+    *reinterpret_cast<float4*>(sp + kSnapU + tile * kSnapUTile + (wid * 64 + lane) * 4) = uo;  \
     load_k(cn, NXT);                                                                          \
     _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                           \
       __builtin_amdgcn_sched_group_barrier(0x8, 2, 0);                                        \
@@ -984,15 +988,18 @@ struct GatedNormArgs {
   uint16_t* y;         // [B, L, H, 128]
 };
 
-// O = Q' S + P U for one (chunk, head) from the snapshots: the chunk's S and
-// U (all 8 v tiles, 96 KB) are staged once in LDS with padded column strides;
-// wave w (8 per workgroup, two per SIMD) takes a row tile of 16 tokens (w for
-// w < 4, 7 - w above) and column tiles 4 (w / 4) .. +3, with Q' and P loaded
-// once, and runs the same MFMA chains (two alternating accumulators, Q' S
-// first, then the causal P U tiles) as the recurrence kernel's layout, so O
-// is the token loop's output in closed form. GN: the gated RMSNorm of each
-// token row is applied before the store (the two column halves of a row
-// meet in LDS for the sum of squares); otherwise the core output is stored.
+// O = Q' S + P U for one (chunk, head) from the snapshots, which the scan
+// stores in this kernel's B-operand order: nothing is staged in LDS, every
+// operand is one coalesced 1 KiB float4 read per wave. Wave w (8 per
+// workgroup, two per SIMD) takes a row tile of 16 tokens (w for w < 4, 7 - w
+// above) and column tiles 4 (w / 4) .. +3, with Q' and P loaded once; the S
+// and U operands of column tile t + 1 are requested before tile t is
+// computed (two register sets alternate), so the snapshot stream overlaps the
+// MFMA chains (two alternating accumulators, Q' S first, then the causal
+// P U tiles) of the recurrence kernel's layout: O is the token loop's output
+// in closed form. GN: the gated RMSNorm of each token row is applied before
+// the store (the two column halves of a row meet in LDS for the sum of
+// squares); otherwise the core output is stored.
 template <bool GN>
 __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__ ws,
                                                        const float* __restrict__ snap,
@@ -1007,20 +1014,29 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
   const size_t bhc = ((size_t)b * H + h) * nC + c;
   const float* wsb = ws + bhc * kChunkFloats;
   const float* sp = snap + bhc * kSnapFloats;
-  __shared__ alignas(16) float Ss[8 * 16 * kST];
-  __shared__ alignas(16) float Us[8 * 16 * kUT];
   __shared__ float ss_s[GN ? 2 : 1][kChunk];
-  // Snapshot: per tile 512 float4 of S^T (column q/32, rows 4(q%32)) and 256 of U^T.
-  float4 st[12];
+  struct TileOps {
+    float4 s[8], u[4];
+  };
+  // U tiles above the diagonal are never used: they re-read tile wid.
+  auto load_tile = [&](int tile, TileOps& t) {
+    const float* st = sp + tile * kSnapSTile + lane * 4;
 #pragma unroll
-  for (int i = 0; i < 12; ++i) st[i] = *reinterpret_cast<const float4*>(sp + (tid + 512 * i) * 4);
+    for (int dt = 0; dt < 8; ++dt) t.s[dt] = *reinterpret_cast<const float4*>(st + dt * 256);
+    const float* ut = sp + kSnapU + tile * kSnapUTile + lane * 4;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) t.u[jt] = *reinterpret_cast<const float4*>(ut + min(jt, wid) * 256);
+  };
   float4 qp[8], pq[4];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
     qp[dt] = *reinterpret_cast<const float4*>(wsb + kOffQP + ((wid * 8 + dt) * 64 + lane) * 4);
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)  // tiles above the diagonal are never used: read tile wid
+  for (int jt = 0; jt < 4; ++jt)
     pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
+  TileOps ta, tb;
+  load_tile(4 * half, ta);
+  load_tile(4 * half + 1, tb);
   // GN: the lane's gate values and norm weights (4 tiles x 4 rows).
   uint16_t zr[4][4];
   float wn[4];
@@ -1037,38 +1053,31 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
       }
     }
   }
-#pragma unroll
-  for (int i = 0; i < 12; ++i) {
-    const int q = tid + 512 * i;          // float4 index in the snapshot
-    const int tile = q / 768, r = q % 768;
-    float* dst = r < 512 ? &Ss[(tile * 16 + (r >> 5)) * kST + 4 * (r & 31)]
-                         : &Us[(tile * 16 + ((r - 512) >> 4)) * kUT + 4 * ((r - 512) & 15)];
-    *reinterpret_cast<float4*>(dst) = st[i];
-  }
-  __syncthreads();
   float ob[4][4];
-#pragma unroll 2
-  for (int tt = 0; tt < 4; ++tt) {
-    const int tile = 4 * half + tt;
-    const float* scol = &Ss[(tile * 16 + col) * kST + 4 * g4];
-    const float* ucol = &Us[(tile * 16 + col) * kUT + 4 * g4];
+  auto compute = [&](int tt, const TileOps& t) {
     q35_f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      mma4(qp[dt], *reinterpret_cast<const float4*>(scol + 16 * dt), o0, o1, o0, o1);
+    for (int dt = 0; dt < 8; ++dt) mma4(qp[dt], t.s[dt], o0, o1, o0, o1);
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
-      if (jt <= wid) mma4(pq[jt], *reinterpret_cast<const float4*>(ucol + 16 * jt), o0, o1, o0, o1);
+      if (jt <= wid) mma4(pq[jt], t.u[jt], o0, o1, o0, o1);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if (GN) {
         ob[tt][e] = round_bf(o0[e] + o1[e]);
       } else {
-        const int t = c * kChunk + 16 * wid + 4 * g4 + e;
-        if (t < L) out[(((size_t)b * L + t) * H + h) * kD + tile * 16 + col] = (uint16_t)f2bf(o0[e] + o1[e]);
+        const int tok = c * kChunk + 16 * wid + 4 * g4 + e;
+        if (tok < L)
+          out[(((size_t)b * L + tok) * H + h) * kD + (4 * half + tt) * 16 + col] = (uint16_t)f2bf(o0[e] + o1[e]);
       }
     }
-  }
+  };
+  compute(0, ta);
+  load_tile(4 * half + 2, ta);
+  compute(1, tb);
+  load_tile(4 * half + 3, tb);
+  compute(2, ta);
+  compute(3, tb);
   if (GN) {
     // Sum of squares of each row: 4 tiles in the lane, the 16 column lanes
     // (one DPP row), then the two halves through LDS.

@@ -1039,6 +1039,27 @@ def zero_tensors(tensors) -> None:
               n, _stream(fused[0]))
 
 
+def stream_read(buf: torch.Tensor) -> torch.Tensor:
+    """Read every byte of a contiguous GPU tensor once with the GEMV weight
+    stream's loads (one workgroup per CU) and return one int32 XOR word per
+    thread. A measurement utility (no counterpart in the reference): timing
+    it gives the achievable HBM read rate the decode GEMVs are compared to."""
+
+    import ctypes
+
+    if not buf.is_cuda or not buf.is_contiguous():
+        raise ValueError("stream_read needs a contiguous GPU tensor")
+    nbytes = buf.numel() * buf.element_size()
+    if nbytes == 0 or nbytes % 16 or buf.data_ptr() % 16:
+        raise ValueError("stream_read needs a 16-byte aligned size and address")
+    props = torch.cuda.get_device_properties(buf.device)
+    out = torch.empty(props.multi_processor_count * 256, device=buf.device, dtype=torch.int32)
+    blocks = ctypes.c_int(0)
+    _lib.call("q35_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), out.numel(),
+              ctypes.addressof(blocks), _stream(buf))
+    return out[: blocks.value * 256]
+
+
 # ------------------------------------------------------------------ out of scope
 def _vision_out_of_scope(name: str):
     def fn(*args, **kwargs):

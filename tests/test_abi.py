@@ -69,6 +69,7 @@ def test_invalid_sizes_rejected_before_launch():
     assert lib.q35_gqa_decode(None, None, None, None, 1.0, None, None, None, 0, 8, 2, 128, 512, None) == 1
     assert lib.q35_delta_decode(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, 0.0,
                                 None, 1, 16, 64, 0, 0, None) == 1
+    assert lib.q35_stream_read(None, 16, None, 1 << 20, None, None) == 1
 
 
 def test_wrappers_reject_cpu_tensors():
@@ -90,6 +91,8 @@ def test_wrappers_reject_cpu_tensors():
         K.ppu_swiglu_gemv(x.view(1, 1, -1), torch.zeros(16, 2048, dtype=torch.bfloat16))
     with pytest.raises(ValueError):
         K.ppu_swiglu_gemv(x.view(1, 1, -1), torch.zeros(16, 2048, dtype=torch.bfloat16), block_n=3)
+    with pytest.raises(ValueError):
+        K.stream_read(x)
 
 
 def test_reference_import_names():

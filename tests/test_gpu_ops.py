@@ -596,6 +596,23 @@ def test_gemm_swiglu_bf16(gpu, m, n, k):
     assert outside <= 1e-5 * exp.numel()
 
 
+@pytest.mark.parametrize("nbytes", [16, 1 << 20, (9 << 20) + 48])
+def test_stream_read(gpu, nbytes):
+    """The read-rate probe reads every 16-byte group exactly once: the XOR of
+    its per-thread words is the XOR of all words of the buffer (sizes below,
+    above and past one full 8-load sweep of the grid, with a tail)."""
+    import numpy as np
+
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 15)
+    words = torch.randint(-(2**31), 2**31 - 1, (nbytes // 4,), generator=g, dtype=torch.int32)
+    out = K.stream_read(words.to(gpu))
+    torch.cuda.synchronize()
+    got = np.bitwise_xor.reduce(out.cpu().numpy())
+    assert got == np.bitwise_xor.reduce(words.numpy())
+
+
 def test_gemm_bf16_rejects_k():
     from ppu_amd import kernels as K
 
