@@ -999,8 +999,9 @@ struct GatedNormArgs {
 // P U tiles) of the recurrence kernel's layout: O is the token loop's output
 // in closed form. GN: the gated RMSNorm of each token row is applied before
 // the store (the two column halves of a row meet in LDS for the sum of
-// squares); otherwise the core output is stored.
-template <bool GN>
+// squares; WF32: the norm weight is fp32, else bf16); otherwise the core
+// output is stored.
+template <bool GN, bool WF32>
 __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__ ws,
                                                        const float* __restrict__ snap,
                                                        uint16_t* __restrict__ out, int L, int H,
@@ -1009,7 +1010,9 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
   // Waves w and w + 4 share a SIMD: pairing row tile w with row tile 3 - w
   // gives every SIMD the same causal P U work.
   const int tid = threadIdx.x, lane = tid & 63, half = tid >> 8;
-  const int wid = half ? 3 - ((tid >> 6) & 3) : (tid >> 6) & 3;
+  // wave-uniform (readfirstlane): the causal P U tests below are scalar
+  // branches, not exec-mask branches that would drain the loads in flight
+  const int wid = __builtin_amdgcn_readfirstlane(half ? 3 - ((tid >> 6) & 3) : (tid >> 6) & 3);
   const int col = lane & 15, g4 = lane >> 4;
   const size_t bhc = ((size_t)b * H + h) * nC + c;
   const float* wsb = ws + bhc * kChunkFloats;
@@ -1044,8 +1047,10 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const int cabs = (4 * half + tt) * 16 + col;
-      wn[tt] = gn.w_f32 ? reinterpret_cast<const float*>(gn.w)[cabs]
-                        : bf2f(reinterpret_cast<const uint16_t*>(gn.w)[cabs]);
+      // The weight type is a template parameter: a run-time branch between
+      // two load forms would make the compiler drain every load in flight.
+      wn[tt] = WF32 ? reinterpret_cast<const float*>(gn.w)[cabs]
+                    : bf2f(reinterpret_cast<const uint16_t*>(gn.w)[cabs]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = min(c * kChunk + 16 * wid + 4 * g4 + e, L - 1);
@@ -1053,6 +1058,9 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
       }
     }
   }
+  // Every load above the first MFMA (the scheduler would otherwise start the
+  // chains after the first few loads and wait on each in turn).
+  __builtin_amdgcn_sched_barrier(0);
   float ob[4][4];
   auto compute = [&](int tt, const TileOps& t) {
     q35_f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
@@ -1248,12 +1256,15 @@ int delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packe
                                                               H, nC);
   e = q35_last_error();
   if (e) return e;
-  if (gn && gn->y)
-    delta_chunk_out<true><<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L, H,
-                                                             nC, *gn);
+  if (gn && gn->y && gn->w_f32)
+    delta_chunk_out<true, true><<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L,
+                                                                   H, nC, *gn);
+  else if (gn && gn->y)
+    delta_chunk_out<true, false><<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L,
+                                                                    H, nC, *gn);
   else
-    delta_chunk_out<false><<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L, H,
-                                                              nC, GatedNormArgs{});
+    delta_chunk_out<false, false><<<dim3(nC, H, B), 512, 0, stream>>>(chunk_ws, snap, (uint16_t*)out, L,
+                                                                     H, nC, GatedNormArgs{});
   return q35_last_error();
 }
 
