@@ -240,6 +240,52 @@ Q35_DEV void norm_rope(const HeadLoads& h, int w_f32, const RopeTable& t, int ro
   }
 }
 
+// Prefill Q/K norm + RoPE for 256-wide heads (the qgkv_norm_rope_k contract,
+// same arithmetic as norm_rope): one wave per (token, query head), lane dims
+// 4*lane .. +3. Every load (the q head and its norm weights, the token's
+// cos/sin, and the k and v heads with the k weights, read by every wave and
+// used by waves of heads < KVH) is an 8-byte vector load issued before any
+// arithmetic; the weight type is chosen by address, so no branch separates
+// the loads. rot > 0, rot % 8 == 0 (checked on the host).
+__global__ __launch_bounds__(256) void qgkv_norm_rope_256(
+    const uint16_t* __restrict__ packed, const void* qw, const void* kw, int w_f32,
+    const uint16_t* __restrict__ cos, const uint16_t* __restrict__ sin, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out, const long long* cache_start,
+    int B, int L, int QH, int KVH, int rot, int cache_len) {
+  const int lane = threadIdx.x & 63;
+  const int pid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pid >= B * L * QH) return;
+  const int head = pid % QH;
+  const int tf = pid / QH;  // b*L + t
+  const int t = tf % L, b = tf / L;
+  const uint16_t* row = packed + (size_t)tf * (2 * QH * kAD + 2 * KVH * kAD);
+  const int kh = min(head, KVH - 1);
+  const HeadLoads hq = load_head(row + head * 2 * kAD, qw, w_f32, lane);
+  const HeadLoads hk = load_head(row + 2 * QH * kAD + kh * kAD, kw, w_f32, lane);
+  const uint2 vv = *reinterpret_cast<const uint2*>(row + 2 * QH * kAD + KVH * kAD + kh * kAD + 4 * lane);
+  const int rc = (4 * lane) % rot;  // lanes past rot/4 read valid, unused entries
+  const uint2 cr = *reinterpret_cast<const uint2*>(cos + (size_t)tf * rot + rc);
+  const uint2 sr = *reinterpret_cast<const uint2*>(sin + (size_t)tf * rot + rc);
+  const long long start = cache_start ? cache_start[0] : 0;
+  RopeTable tab;
+  tab.cs[0] = bf_lo(cr.x); tab.cs[1] = bf_hi(cr.x); tab.cs[2] = bf_lo(cr.y); tab.cs[3] = bf_hi(cr.y);
+  tab.sn[0] = bf_lo(sr.x); tab.sn[1] = bf_hi(sr.x); tab.sn[2] = bf_lo(sr.y); tab.sn[3] = bf_hi(sr.y);
+  float o[4];
+  norm_rope(hq, w_f32, tab, rot, lane, o);
+  uint16_t* qo = q_out + (((size_t)b * QH + head) * L + t) * kAD + 4 * lane;
+  *reinterpret_cast<uint2*>(qo) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+  if (head < KVH) {
+    norm_rope(hk, w_f32, tab, rot, lane, o);
+    const long long pos = t + start;
+    const int len = cache_start ? cache_len : L;
+    if (pos >= 0 && pos < len) {  // never write outside the cache
+      const size_t off = (((size_t)b * KVH + head) * len + pos) * kAD + 4 * lane;
+      *reinterpret_cast<uint2*>(k_out + off) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+      *reinterpret_cast<uint2*>(v_out + off) = vv;
+    }
+  }
+}
+
 // Max of a value that is uniform within each 16-lane row, over the 4 rows.
 Q35_DEV float rows4_max(float v) {
   const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
@@ -1168,6 +1214,14 @@ int q35_qgkv_norm_rope(const void* packed, const void* q_w, const void* k_w, int
   Q35_CHECK_ARG(waves < (1ll << 31));
   const unsigned grid = (unsigned)((waves + 3) / 4);
   const long long* cs = (const long long*)cache_start;
+  if (D == kAD && rotary_dim > 0 && rotary_dim % 8 == 0 && q35_aligned8(packed) && q35_aligned8(q_w) &&
+      q35_aligned8(k_w) && q35_aligned8(cos) && q35_aligned8(sin) && q35_aligned8(q_out) &&
+      q35_aligned8(k_out) && q35_aligned8(v_out)) {
+    qgkv_norm_rope_256<<<grid, 256, 0, stream>>>(
+        (const uint16_t*)packed, q_w, k_w, w_f32, (const uint16_t*)cos, (const uint16_t*)sin,
+        (uint16_t*)q_out, (uint16_t*)k_out, (uint16_t*)v_out, cs, B, L, QH, KVH, rotary_dim, cache_len);
+    return q35_last_error();
+  }
 #define Q35_QGKV(EE)                                                                          \
   qgkv_norm_rope_k<EE><<<grid, 256, 0, stream>>>(                                             \
       (const uint16_t*)packed, q_w, k_w, w_f32, (const uint16_t*)cos, (const uint16_t*)sin,   \

@@ -575,6 +575,9 @@ Q35_DEV void mma4(const float4 a, const float4 bv, q35_f32x4 c0, q35_f32x4 c1, q
   o1 = c1;
 }
 
+// PF32: A_log and dt_bias are fp32 (else bf16); a template parameter, since a
+// run-time branch between two load forms makes the compiler wait for each.
+template <bool PF32>
 __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restrict__ qkv,
                                                         int qkv_stride,
                                                         const uint16_t* __restrict__ packed,
@@ -610,7 +613,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
     const uint16_t* row = qkv + ((size_t)b * L + tc) * qkv_stride;
     const uint16_t* prow = packed + ((size_t)b * L + tc) * packed_stride;
     const float a_raw = bf2f(prow[a_off + h]), b_raw = bf2f(prow[b_off + h]);
-    const float alog = ld_param(a_log, h, params_f32), dtb = ld_param(dt_bias, h, params_f32);
+    const float alog = ld_param(a_log, h, PF32), dtb = ld_param(dt_bias, h, PF32);
     float rq[4][8], rk[4][8];
     uint4 rv[4];
 #pragma unroll
@@ -856,8 +859,26 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   // written and after the new state is written.
   __shared__ alignas(16) float St2[2][16 * kST];
   __shared__ alignas(16) float Ut[16 * kUT];
+  // The state tile (128 rows x 16 columns): float4 q = (row q / 4, columns
+  // 4(q % 4) .. +3), two per thread, both loads issued before the transposed
+  // LDS writes.
   float* Sg = state + bh * kD * kD + tile * 16;
-  for (int idx = tid; idx < kD * 16; idx += 256) St2[0][(idx & 15) * kST + (idx >> 4)] = Sg[(size_t)(idx >> 4) * kD + (idx & 15)];
+  {
+    float4 sv[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = tid + 256 * i;
+      sv[i] = *reinterpret_cast<const float4*>(Sg + (size_t)(q >> 2) * kD + 4 * (q & 3));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = tid + 256 * i, r = q >> 2, c0 = 4 * (q & 3);
+      St2[0][(c0 + 0) * kST + r] = sv[i].x;
+      St2[0][(c0 + 1) * kST + r] = sv[i].y;
+      St2[0][(c0 + 2) * kST + r] = sv[i].z;
+      St2[0][(c0 + 3) * kST + r] = sv[i].w;
+    }
+  }
   // This wave's operands of one chunk: row tile wid of W^T and U0, dk tiles
   // 2*wid and 2*wid+1 of K''^T. Chunk c + 1 is requested before chunk c is
   // computed.
@@ -972,7 +993,12 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   if (c < nC) Q35_SCAN_CHUNK(opa, opb, c);
 #undef Q35_SCAN_CHUNK
   const float* Sf = St2[nC & 1];
-  for (int idx = tid; idx < kD * 16; idx += 256) Sg[(size_t)(idx >> 4) * kD + (idx & 15)] = Sf[(idx & 15) * kST + (idx >> 4)];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = tid + 256 * i, r = q >> 2, c0 = 4 * (q & 3);
+    *reinterpret_cast<float4*>(Sg + (size_t)r * kD + c0) =
+        make_float4(Sf[c0 * kST + r], Sf[(c0 + 1) * kST + r], Sf[(c0 + 2) * kST + r], Sf[(c0 + 3) * kST + r]);
+  }
 }
 
 // Gated RMSNorm fused into the output kernel (optional): with the core row
@@ -1247,9 +1273,14 @@ int delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packe
   float* gc = chunk_ws + (size_t)B * H * nC * kChunkFloats;
   // Snapshots start 16-byte aligned after the B*H*nC chunk decays.
   float* snap = gc + (((size_t)B * H * nC + 3) & ~(size_t)3);
-  delta_chunk_prep<<<dim3(nC, H, B), 256, 0, stream>>>(
-      (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
-      params_f32, 4 * H * D, 4 * H * D + H, chunk_ws, gc, L, H, nC);
+  if (params_f32)
+    delta_chunk_prep<true><<<dim3(nC, H, B), 256, 0, stream>>>(
+        (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
+        params_f32, 4 * H * D, 4 * H * D + H, chunk_ws, gc, L, H, nC);
+  else
+    delta_chunk_prep<false><<<dim3(nC, H, B), 256, 0, stream>>>(
+        (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
+        params_f32, 4 * H * D, 4 * H * D + H, chunk_ws, gc, L, H, nC);
   e = q35_last_error();
   if (e) return e;
   delta_chunk_scan<<<dim3((kD / 16) * H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state, snap,

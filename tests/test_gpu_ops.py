@@ -339,11 +339,15 @@ def _qgkv_inputs(g, seq_len):
     return packed, qw, kw, cos, sin
 
 
-def test_qgkv_norm_rope(gpu):
+@pytest.mark.parametrize("seq_len,w_dtype", [(5, torch.float32), (70, torch.bfloat16)])
+def test_qgkv_norm_rope(gpu, seq_len, w_dtype):
+    """Prefill Q/K norm + RoPE (the 256-wide vector path) against the oracle,
+    with fp32 and bf16 norm weights."""
     from ppu_amd import kernels as K
 
     g = gen(KERNEL_SEED + 15)
-    packed, qw, kw, cos, sin = _qgkv_inputs(g, 5)
+    packed, qw, kw, cos, sin = _qgkv_inputs(g, seq_len)
+    qw, kw = qw.to(w_dtype), kw.to(w_dtype)
     kwargs = dict(q_heads=8, kv_heads=2, dim=256, rotary_dim=64)
     eq, ek, ev = ref.qgkv_norm_rope(packed, qw, kw, cos, sin, **kwargs)
     q, k, v = K.qgkv_norm_rope(packed.to(gpu), qw.to(gpu), kw.to(gpu), cos.to(gpu), sin.to(gpu), **kwargs)
