@@ -130,6 +130,17 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
       }
     }
   }
+  // EPI_CONV with width-4 filters: the lane's conv state and taps (4 bf16
+  // each, one 8-byte load) are requested with the activation, so the
+  // epilogue's conv update has no memory round trip; without conv channels or
+  // for other widths the (unused) loads read the activation instead.
+  uint2 cst = make_uint2(0u, 0u), cwt = make_uint2(0u, 0u);
+  if (EPI == EPI_CONV) {
+    const bool fast = a.conv_channels > 0 && a.conv_kw == 4;
+    const int nc = max(min(n0 + (lane < P ? lane : 0), a.conv_channels - 1), 0);
+    cst = *reinterpret_cast<const uint2*>(fast ? a.conv_state + (size_t)nc * 4 : a.x);
+    cwt = *reinterpret_cast<const uint2*>(fast ? a.conv_w + (size_t)nc * 4 : a.x);
+  }
   // int8 weights: the per-channel scales of the lane's output rows.
   float sw_g = 0.f, sw_u = 0.f;
   if (I8) {
@@ -331,8 +342,20 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
       if (EPI == EPI_CONV) {
         const uint32_t yb = f2bf(v);
         if (n < a.conv_channels) {
-          const float c = conv_update_channel(a.conv_state + (size_t)n * a.conv_kw,
-                                              a.conv_w + (size_t)n * a.conv_kw, yb, a.conv_kw);
+          float c;
+          if (a.conv_kw == 4) {
+            // window (state[1..3], y), taps oldest first, as conv_update_channel
+            float cacc = fmaf(bf_hi(cst.x), bf_lo(cwt.x), 0.f);
+            cacc = fmaf(bf_lo(cst.y), bf_hi(cwt.x), cacc);
+            cacc = fmaf(bf_hi(cst.y), bf_lo(cwt.y), cacc);
+            cacc = fmaf(bf2f(yb), bf_hi(cwt.y), cacc);
+            *reinterpret_cast<uint2*>(a.conv_state + (size_t)n * 4) =
+                make_uint2((cst.x >> 16) | (cst.y << 16), (cst.y >> 16) | (yb << 16));
+            c = round_bf(silu_f(round_bf(cacc)));
+          } else {
+            c = conv_update_channel(a.conv_state + (size_t)n * a.conv_kw,
+                                    a.conv_w + (size_t)n * a.conv_kw, yb, a.conv_kw);
+          }
           a.conv_out[n] = (uint16_t)f2bf(c);
         }
       }
@@ -640,6 +663,7 @@ int q35_gemv_conv(const void* W, const void* x, const void* u, const void* norm_
   Q35_CHECK_ARG(prologue != 2 || u);
   Q35_CHECK_ARG(conv_channels >= 0 && conv_channels <= N && conv_kw > 0 && conv_kw <= 16);
   Q35_CHECK_ARG(conv_channels == 0 || (conv_w && conv_state && conv_out));
+  Q35_CHECK_ARG(conv_channels == 0 || conv_kw != 4 || (q35_aligned8(conv_w) && q35_aligned8(conv_state)));
   Q35_CHECK_ARG(!x_row || (prologue == 1 && x_rows > 0));
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, (const uint16_t*)u, norm_w,
              (uint16_t*)residual_out, nullptr, (uint16_t*)y, nullptr, N, K, norm_w_f32, eps,
@@ -703,6 +727,7 @@ int q35_gemv_i8_conv(const void* Wq, const void* s_w, const void* x, const void*
   Q35_CHECK_ARG(prologue != 2 || u);
   Q35_CHECK_ARG(conv_channels >= 0 && conv_channels <= N && conv_kw > 0 && conv_kw <= 16);
   Q35_CHECK_ARG(conv_channels == 0 || (conv_w && conv_state && conv_out));
+  Q35_CHECK_ARG(conv_channels == 0 || conv_kw != 4 || (q35_aligned8(conv_w) && q35_aligned8(conv_state)));
   Q35_CHECK_ARG(!x_row || (prologue == 1 && x_rows > 0));
   GemvArgs a{(const uint16_t*)Wq, (const uint16_t*)x, (const uint16_t*)u, norm_w,
              (uint16_t*)residual_out, nullptr, (uint16_t*)y, nullptr, N, K, norm_w_f32, eps,
