@@ -270,8 +270,9 @@ def main() -> None:
                     help="only run the short workload profiled with rocprofv3 --pmc, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (batch-1 decode does not "
-              "shard profitably; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (a batch-1 decode step "
+              "is bound by per-launch latency, which sharding adds to). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
