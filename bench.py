@@ -11,13 +11,18 @@ Printed (one JSON line on stdout):
   value        decode tokens/s over the K timed steps (inputs resident in HBM)
   ttft_ms      prefill (1024 tokens) + first token, timed as the reference
                does (evaluation_wrapper.py:342-365), median of warm runs
-  roofline     the dominant decode kernel (lm_head GEMV + top-1, 1.017 GB of
-               weights per launch) timed with HIP events on its stream;
+  roofline     the decode kernel with the largest share of the step: the
+               residual add + RMSNorm + SwiGLU GEMV [12288, 2048] (24 per
+               token), timed with HIP events on its stream over the model's
+               own 24 layer weights (1.2 GB, rotated in one graph);
                traffic = its HBM bytes per launch from the committed
-               rocprofv3 --pmc summary profiles/lm_head_top1_traffic_pmc.txt
-               (made from ``bench.py --counter-probe`` runs); read_ceiling
-               is a plain streaming read of the same weight bytes
-               (kernels.stream_read), the device's achievable read rate
+               rocprofv3 --pmc summary profiles/decode_step_traffic_pmc.txt
+               (``bench.py --counter-probe`` runs); roofline_detail adds a
+               plain streaming read of the same byte count rotated the same
+               way (the launch-size ceiling), and the lm_head GEMV + top-1
+  step_roofline  the whole decode step: HBM bytes one token needs (packed
+               weights, lm_head, recurrent/conv state read + write, K/V read
+               at the mean context of the timed steps) / ms_per_step
   kernels     per-kernel achieved HBM GB/s of the BASELINE configs 1-4
                (rotating >= 640 MB of distinct buffers so the 256 MB MALL does
                not serve the weights), in-graph time per launch
@@ -25,7 +30,12 @@ Printed (one JSON line on stdout):
                variant of config 5 (A8W8 when the headline runs bf16), on the
                same seeded weights
   cpu_baseline the CPU oracle decoder (the reference's PyTorch CPU path,
-               restated) on a bounded sample, same process, host cores
+               restated) on the config-5 prompt: the full 1024-token prefill
+               then 16 greedy decode steps, same process, host cores; beside
+               it Transformers' own eager forward (what the reference runs for
+               CPU tensors) on the same weights and threads
+  inputs_sha256  SHA-256 of the prompt and of the generated weights, with
+               whether they equal the committed tests/golden/digests.json
 """
 
 from __future__ import annotations
@@ -74,15 +84,18 @@ def graph_time_us(fn, calls: int, reps: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * calls)
 
 
-def pmc_traffic(name: str):
+def pmc_traffic(name: str, kernel: str | None = None):
     """HBM bytes per launch read from a committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE passes scaled by a copy kernel of known size),
-    or None when the summary is absent."""
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a copy kernel of known size):
+    the ``traffic_bytes_per_launch`` line, or with ``kernel`` the summary row
+    whose first field starts with that kernel name; None when absent."""
     try:
         for line in (ROOT / "profiles" / name).read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
+            if kernel is None and line.startswith("traffic_bytes_per_launch:"):
                 return int(line.split(":", 1)[1])
-    except (OSError, ValueError):
+            if kernel is not None and line.startswith(kernel + " |"):
+                return int(line.split("|")[3])
+    except (OSError, ValueError, IndexError):
         pass
     return None
 
@@ -114,6 +127,78 @@ def lm_head_roofline(model) -> dict:
             "read_ceiling": {"GB/s": round(read_gbs, 1), "us": round(read_us, 2),
                              "frac_of_peak": round(read_gbs / PEAK_HBM_GBS, 4),
                              "lm_head_frac_of_ceiling": round(achieved / read_gbs, 4)}}
+
+
+def swiglu_roofline(model, variant: str) -> dict:
+    """The residual add + RMSNorm + SwiGLU GEMV ``[2*6144, 2048]`` of the
+    decode step (the kernel with the largest share of it: 24 launches per
+    token), launched over the model's own 24 layer weights in one graph, and a
+    plain streaming read of the same bytes rotated the same way."""
+    import torch
+
+    from ppu_amd import kernels as K
+    from ppu_amd.integration import text_stack
+
+    layers = text_stack(model).layers
+    dev = layers[0].mlp.q35_gate_up.w.device
+    g = torch.Generator(device=dev).manual_seed(20260819)
+    r = torch.randn(1, 1, 2048, device=dev, generator=g).to(torch.bfloat16)
+    u = torch.randn(1, 1, 2048, device=dev, generator=g).to(torch.bfloat16)
+    ops = [(l.mlp.q35_gate_up.w, l.mlp.q35_gate_up.s, l.post_attention_layernorm) for l in layers]
+    n = len(ops)
+
+    def launch(i):
+        w, sc, ln = ops[i % n]
+        return K.residual_norm_linear(r, u, ln.weight, ln.eps, w, swiglu=True, weight_scale=sc)
+
+    us = graph_time_us(launch, calls=n, reps=10)
+    w0, s0, _ = ops[0]
+    n_rows, k = w0.shape
+    wbytes = w0.numel() * w0.element_size() + (0 if s0 is None else s0.numel() * 4)
+    algo = wbytes + 3 * k * 2 + k * 2 + (n_rows // 2) * 2  # W (+scales), r, u, norm w, r', y
+    achieved = algo / us / 1e3
+    read_us = graph_time_us(lambda i: K.stream_read(ops[i % n][0]), calls=n, reps=10)
+    read_gbs = w0.numel() * w0.element_size() / read_us / 1e3
+    kname = f"gemv_fused<4, {4 if variant == 'a8w8' else 2}, {2 if variant == 'a8w8' else 4}, 2, 1, " \
+            f"{'true' if variant == 'a8w8' else 'false'}>"
+    log(f"SwiGLU GEMV [{n_rows},{k}] ({variant}): {us:.2f} us, {achieved:.0f} GB/s "
+        f"({100 * achieved / PEAK_HBM_GBS:.1f}% of 8 TB/s); plain read of the same bytes "
+        f"{read_us:.2f} us ({100 * read_us / us:.1f}% of the GEMV time)")
+    return {"kernel": f"residual add + RMSNorm + SwiGLU GEMV [{n_rows},{k}] {variant} ({kname})",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": pmc_traffic("decode_step_traffic_pmc.txt", kname) if variant == "bf16" else None,
+            "us_per_launch": round(us, 3), "algorithmic_bytes": algo, "launches_per_token": n,
+            "same_size_read": {"us": round(read_us, 3), "GB/s": round(read_gbs, 1),
+                               "gemv_frac_of_read_rate": round(achieved / read_gbs, 4)}}
+
+
+def step_bytes(model, context: float) -> int:
+    """HBM bytes one decode token needs: every packed weight (and int8 scale)
+    once, the lm_head (tied embedding) once, the small per-layer parameters,
+    the embedding row, the recurrent and conv states read and written, and
+    the K/V cache read over ``context`` positions plus the new row written."""
+    from ppu_amd.integration import _Weight, text_stack
+
+    stack = text_stack(model)
+    total = 0
+    for m in model.modules():
+        if isinstance(m, _Weight):
+            total += m.w.numel() * m.w.element_size() + (0 if m.s is None else m.s.numel() * 4)
+    total += model.lm_head.weight.numel() * 2 + stack.config.hidden_size * 2
+    for name, p in stack.named_parameters():
+        if p is not None and "embed_tokens" not in name:
+            total += p.numel() * p.element_size()  # norms, conv taps, A_log, dt_bias
+    for layer in stack.layers:
+        if hasattr(layer, "linear_attn"):
+            m = layer.linear_attn
+            total += 2 * m.num_v_heads * m.head_k_dim * m.head_v_dim * 4
+            total += 2 * m.conv_dim * m.conv_kernel_size * 2
+        else:
+            a = layer.self_attn
+            kv = a.config.num_key_value_heads * a.head_dim * 2
+            total += int(2 * kv * context) + 2 * kv
+    return total
 
 
 def kernel_table(dev) -> dict:
@@ -165,7 +250,9 @@ def kernel_table(dev) -> dict:
                            calls=n, reps=4)
         rec(f"cfg3_gqa_decode_L{ctx}", us, 2048 * ctx + 8192)
         del Kc, Vc
-    # config 4: fused conv1d + delta rule + gated RMSNorm, one decode token
+    # config 4: one decode token of a DeltaNet layer through the kernels the
+    # model runs (conv update, the 256-wave delta step, packed gated norm),
+    # and the delta step alone
     n = nbuf(16 * 128 * 128 * 4)
     St = [torch.randn(1, 16, 128, 128, device=dev, generator=g) * 0.1 for _ in range(n)]
     packed = torch.randn(1, 1, 8320, device=dev, generator=g).to(bf)
@@ -173,9 +260,18 @@ def kernel_table(dev) -> dict:
     cs = torch.zeros(1, 6144, 4, device=dev, dtype=bf)
     z16 = torch.zeros(16, device=dev, dtype=bf)
     gw = torch.ones(128, device=dev, dtype=bf)
-    us = graph_time_us(lambda i: K.delta_decode_fused(packed, cw, cs, z16, z16, St[i % n], gw, 1e-6),
+
+    def chain(i):
+        qkv = K.causal_conv1d_fused(packed, cw, cs)
+        core = K.delta_recurrent_fused(qkv, packed, z16, z16, St[i % n])
+        return K.gated_rms_norm_packed(core.reshape(-1, 128), packed, 6144, 16, gw, 1e-6)
+
+    us = graph_time_us(chain, calls=n, reps=4)
+    rec("cfg4_delta_decode_chain_3_launches", us, 2_265_216)
+    qkv = K.causal_conv1d_fused(packed, cw, cs)
+    us = graph_time_us(lambda i: K.delta_recurrent_fused(qkv, packed, z16, z16, St[i % n]),
                        calls=n, reps=4)
-    rec("cfg4_delta_decode_step", us, 2_261_120 + 4096)
+    rec("cfg4_delta_step_kernel", us, 2 * 16 * 128 * 128 * 4 + 6144 * 2 + 64 + 4096)
     del St
     return out
 
@@ -184,32 +280,58 @@ def counter_probe(dev) -> None:
     """A short fixed workload for ``rocprofv3 --pmc`` passes (one counter set
     per run), so that per-dispatch counters can be read for:
 
-    * 5 launches of the lm_head GEMV + top-1 on a [248320, 2048] bf16 weight;
     * 5 calibration launches of a plain elementwise kernel (``neg``) that reads
       exactly 1 GiB and writes exactly 1 GiB, the yardstick that turns the
       FETCH_SIZE / WRITE_SIZE counters into bytes;
-    * 3 launches of each prefill GEMM shape (M = 1024 tokens) of the 2B
-      decoder, for MFMA counters.
+    * 5 launches of the lm_head GEMV + top-1 on a [248320, 2048] bf16 weight;
+    * 4 replays of the captured decode step of the seeded 2B decoder (bf16
+      linears, 1024-token context): every decode kernel with its real
+      weights, 129 dispatches per replay;
+    * 3 launches of each prefill GEMM shape (M = 1024 tokens), for MFMA
+      counters.
     """
     import torch
     import torch.nn.functional as F
 
     from ppu_amd import kernels as K
+    from ppu_amd import synth
+    from ppu_amd.graph import GreedyDecodeGraph
+    from ppu_amd.integration import apply_fusions
 
     bf = torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(20260819)
-    w = (torch.randn(248320, 2048, device=dev, generator=g) * 0.02).to(bf)
-    h = torch.randn(1, 2048, device=dev, generator=g).to(bf)
-    for _ in range(5):
-        K.lm_head_argmax(h, w)
-    torch.cuda.synchronize()
-    del w
     src = torch.randn(1 << 28, device=dev, generator=g)  # 2^28 fp32 = 1 GiB
     dst = torch.empty_like(src)
     for _ in range(5):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
     del src, dst
+    w = (torch.randn(248320, 2048, device=dev, generator=g) * 0.02).to(bf)
+    h = torch.randn(1, 2048, device=dev, generator=g).to(bf)
+    for _ in range(5):
+        K.lm_head_argmax(h, w)
+    torch.cuda.synchronize()
+    del w
+    log("counter probe: calibration + lm_head done; decode step ...")
+    cfg = synth.config_2b()
+    model = synth.build_model(cfg, device=dev)
+    apply_fusions(model)
+    from transformers.cache_utils import StaticCache
+
+    prompt = synth.prompt_ids(PROMPT_LEN, cfg.vocab_size).to(dev)
+    with torch.inference_mode():
+        cache = StaticCache(config=cfg, max_cache_len=1152)
+        pos = torch.arange(PROMPT_LEN, device=dev).view(1, -1)
+        out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
+        tok = K.lm_head_argmax(out.last_hidden_state[:, -1].contiguous(), model.lm_head.weight)
+        graph = GreedyDecodeGraph(model, cache, tok, torch.full((1, 1), PROMPT_LEN, device=dev,
+                                                                dtype=torch.long))
+        for _ in range(4):
+            graph.replay()
+        torch.cuda.synchronize()
+    del graph, cache, model
+    torch.cuda.empty_cache()
+    log("counter probe: decode step done; prefill GEMMs ...")
     for (n, k) in ((8320, 2048), (2048, 2048), (5120, 2048), (12288, 2048), (2048, 6144)):
         x = torch.randn(1024, k, device=dev, generator=g).to(bf)
         wt = (torch.randn(n, k, device=dev, generator=g) * 0.02).to(bf)
@@ -219,29 +341,155 @@ def counter_probe(dev) -> None:
     log("counter probe done")
 
 
-def cpu_baseline(state, cfg, prompt, decode_steps: int) -> dict:
-    """The oracle decoder on the host cores: a bounded sample of the workload."""
+# Algorithmic bytes per launch of the decode-step kernels (2B shape, bf16,
+# 1024-token context), by the kernel names rocprofv3 reports.
+DECODE_ALGO_BYTES = {
+    "gemv_fused<4, 2, 4, 2, 1, false>": 2 * 6144 * 2048 * 2 + 4 * 2048 * 2 + 6144 * 2,
+    "gemv_fused<4, 1, 12, 0, 0, false>": 2048 * 6144 * 2 + 6144 * 2 + 2048 * 2,
+    "gemv_fused<4, 2, 4, 2, 3, false>": 8320 * 2048 * 2 + 4 * 2048 * 2 + 8320 * 2
+    + 6144 * 4 * 2 * 3 + 6144 * 2,
+    "gemv_fused<4, 2, 4, 3, 0, false>": 2048 * 2048 * 2 + 2 * 2048 * 2 + 128 * 2 + 2048 * 2,
+    "gemv_fused<4, 2, 4, 2, 0, false>": 5120 * 2048 * 2 + 4 * 2048 * 2 + 5120 * 2,
+    "gemv_fused<4, 2, 4, 0, 0, false>": 2048 * 2048 * 2 + 2 * 2048 * 2,
+    "delta_decode_wave<false>": 2 * 16 * 128 * 128 * 4 + 6144 * 2 + 64 + 16 * 128 * 2,
+    "lm_head_top1_persist<4, 1, 4>": 248320 * 2048 * 2 + 2048 * 2 + 8,
+}
+
+
+def pmc_summary(fetch_csv: str, write_csv: str) -> None:
+    """Print the HBM-traffic summary of two ``rocprofv3 --pmc`` runs of
+    ``--counter-probe`` (FETCH_SIZE, then WRITE_SIZE; their
+    ``*_counter_collection.csv`` files): mean KiB per dispatch per kernel,
+    scaled by what the counters read for the 1 GiB in / 1 GiB out ``neg``
+    calibration kernel, against the kernel's algorithmic bytes."""
+    import csv
+    from collections import defaultdict
+
+    def load(path, counter):
+        per, raw_names = defaultdict(list), {}
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name", counter) != counter:
+                    continue
+                raw = row["Kernel_Name"].replace("(anonymous namespace)::", "")
+                raw = raw[5:] if raw.startswith("void ") else raw
+                name = raw.split("(")[0].strip()
+                per[name].append(float(row["Counter_Value"]))
+                raw_names[name] = raw
+        return {k: sum(v) / len(v) for k, v in per.items()}, raw_names
+
+    (fetch, raw), (write, _) = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+    neg = [k for k in fetch if "neg_kernel" in raw[k]]
+    if not neg:
+        raise SystemExit("no calibration (neg) kernel in the FETCH_SIZE run")
+    f_scale = (1 << 20) / fetch[neg[0]]
+    w_scale = (1 << 20) / write[neg[0]]
+    print(f"calibration kernel {neg[0]}: FETCH_SIZE {fetch[neg[0]]:.1f} KiB, WRITE_SIZE "
+          f"{write[neg[0]]:.1f} KiB per dispatch for 1 GiB in / 1 GiB out -> scale "
+          f"fetch x{f_scale:.4f}, write x{w_scale:.4f}")
+    print("kernel | fetch KiB | write KiB | traffic bytes per launch | algorithmic bytes | ratio")
+    for name in sorted(fetch, key=lambda k: -fetch[k]):
+        if name not in write:
+            continue
+        traffic = int((fetch[name] * f_scale + write[name] * w_scale) * 1024)
+        algo = DECODE_ALGO_BYTES.get(name)
+        ratio = f"{traffic / algo:.4f}" if algo else "-"
+        print(f"{name} | {fetch[name]:.1f} | {write[name]:.1f} | {traffic} | {algo or '-'} | {ratio}")
+
+
+def cpu_baseline(state, cfg, prompt, decode_steps: int, eager: bool = True) -> dict:
+    """The reference's PyTorch CPU path on the host cores, on the config-5
+    prompt: the oracle decoder (the reference's fused data flow restated,
+    ``kind: port``) prefills the whole prompt and decodes ``decode_steps``
+    greedy tokens; beside it Transformers' own eager Qwen3.5 forward, which
+    the reference runs for CPU tensors (integration.py:51-52), on the same
+    weights and thread count (prefill, then cached decode steps)."""
     import torch
 
     from oracle.model import OracleDecoder
 
-    torch.set_num_threads(os.cpu_count() or 1)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
     oracle = OracleDecoder(state, cfg)
-    cache = oracle.new_cache(PROMPT_LEN + decode_steps + 8)
+    cache = oracle.new_cache(prompt.shape[1] + decode_steps + 8)
     t0 = time.perf_counter()
     h = oracle.forward(prompt, cache)
     tok, _ = oracle.top1(h[:, -1])
     ttft = time.perf_counter() - t0
+    tokens = [tok]
     t1 = time.perf_counter()
     for _ in range(decode_steps):
         h = oracle.forward(torch.tensor([[tok]]), cache)
         tok, _ = oracle.top1(h[:, -1])
+        tokens.append(tok)
     dt = time.perf_counter() - t1
-    return {"value": round(decode_steps / dt, 3), "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port", "ttft_ms": round(ttft * 1e3, 1),
-            "sample": f"oracle decoder (torch CPU, same seeded weights): prefill of the "
-                      f"{prompt.shape[1]}-token prompt, then {decode_steps} greedy decode steps",
-            "cpu_model": _cpu_model()}
+    del oracle, cache
+    out = {"value": round(decode_steps / dt, 3), "unit": "tokens/s", "cores": torch.get_num_threads(),
+           "kind": "port", "ttft_ms": round(ttft * 1e3, 1),
+           "sample": f"oracle decoder (torch CPU, same seeded weights): prefill of the full "
+                     f"{prompt.shape[1]}-token config-5 prompt, then {decode_steps} greedy decode "
+                     f"steps (of the 64 the GPU workload decodes)",
+           "cpu_model": _cpu_model()}
+    log(f"CPU oracle: TTFT {ttft * 1e3:.0f} ms, decode {decode_steps / dt:.2f} tok/s on "
+        f"{threads} threads; tokens {tokens[:6]}")
+    if eager:
+        out["transformers_eager"] = _eager_cpu(state, cfg, prompt, decode_steps)
+    return out
+
+
+def _eager_cpu(state, cfg, prompt, decode_steps: int) -> dict:
+    import torch
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5ForCausalLM
+
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("meta"):
+            model = Qwen3_5ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(old)
+    model.load_state_dict(state, assign=True, strict=False)
+    model.tie_weights()
+    rot = model.model.rotary_emb
+    inv_freq, _ = rot.compute_default_rope_parameters(cfg, "cpu")
+    rot.inv_freq = inv_freq
+    rot.original_inv_freq = inv_freq
+    model.eval()
+    with torch.inference_mode():
+        cache = DynamicCache(config=cfg)
+        t0 = time.perf_counter()
+        out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        tok = int(out.logits[0, -1].argmax())
+        ttft = time.perf_counter() - t0
+        tokens = [tok]
+        t1 = time.perf_counter()
+        for _ in range(decode_steps):
+            out = model(input_ids=torch.tensor([[tok]]), past_key_values=cache, use_cache=True,
+                        logits_to_keep=1)
+            tok = int(out.logits[0, -1].argmax())
+            tokens.append(tok)
+        dt = time.perf_counter() - t1
+    log(f"CPU Transformers eager: TTFT {ttft * 1e3:.0f} ms, decode {decode_steps / dt:.2f} tok/s; "
+        f"tokens {tokens[:6]}")
+    return {"value": round(decode_steps / dt, 3), "unit": "tokens/s", "ttft_ms": round(ttft * 1e3, 1),
+            "cores": torch.get_num_threads(),
+            "sample": f"Transformers 5.15 eager Qwen3_5ForCausalLM (bf16, CPU, DynamicCache), same "
+                      f"weights: {prompt.shape[1]}-token prefill, then {decode_steps} greedy steps"}
+
+
+def _digest_report(digests: dict) -> dict:
+    """The run's input digests and whether they equal the committed ones."""
+    try:
+        golden = json.loads((ROOT / "tests" / "golden" / "digests.json").read_text())
+    except (OSError, ValueError):
+        golden = {}
+    out = dict(digests)
+    if "prompt" in digests:
+        out["prompt_matches_golden"] = digests["prompt"] == golden.get("prompt_1024")
+    if "weights" in digests:
+        out["weights_match_golden"] = digests["weights"] == golden.get("weights_2b")
+    return out
 
 
 def _cpu_model() -> str:
@@ -264,11 +512,17 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-other-variant", action="store_true",
                     help="skip the second (A8W8 or bf16) decode measurement")
-    ap.add_argument("--cpu-decode-steps", type=int, default=8)
-    ap.add_argument("--cpu-prompt", type=int, default=128, help="prompt length of the CPU sample")
+    ap.add_argument("--cpu-decode-steps", type=int, default=16)
+    ap.add_argument("--cpu-prompt", type=int, default=PROMPT_LEN, help="prompt length of the CPU sample")
+    ap.add_argument("--no-eager", action="store_true", help="skip the Transformers-eager CPU timing")
     ap.add_argument("--counter-probe", action="store_true",
                     help="only run the short workload profiled with rocprofv3 --pmc, then exit")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the HBM-traffic table of two --counter-probe pmc runs, then exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (a batch-1 decode step "
               "is bound by per-launch latency, which sharding adds to). Run with --gpus 1.",
@@ -289,15 +543,18 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     cfg = synth.config_2b()
-    gen = torch.Generator().manual_seed(synth.MODEL_SEED)
-    prompt_cpu = torch.randint(0, cfg.vocab_size, (1, PROMPT_LEN), generator=gen)
+    prompt_cpu = synth.prompt_ids(PROMPT_LEN, cfg.vocab_size)
     prompt = prompt_cpu.to(dev)
+    digests = {"prompt": synth.tensor_sha256(prompt_cpu)}
 
     def measure(variant: str, keep_state: bool):
         """Build the seeded 2B model with ``variant`` linears, then TTFT through
         the generation loop and K timed decode-graph replays."""
         t0 = time.perf_counter()
-        model = synth.build_model(cfg, device=dev)
+        wd = []
+        model = synth.build_model(cfg, device=dev, digest=wd if keep_state else None)
+        if wd:
+            digests["weights"] = wd[0]
         seen, weight_bytes = set(), 0
         for p in model.parameters():
             if p.data_ptr() not in seen:
@@ -356,19 +613,28 @@ def main() -> None:
         ms_per_step = elapsed * 1e3 / args.steps
         log(f"[{variant}] decode: {ms_per_step:.3f} ms/token ({args.steps / elapsed:.1f} tok/s); "
             f"graph replay alone {replay_ms:.3f} ms")
+        context = PROMPT_LEN + 1 + args.warmup + (args.steps + 1) / 2
+        nbytes = step_bytes(model, context)
+        gbs = nbytes / (ms_per_step * 1e-3) / 1e9
         res = {"value": round(args.steps / elapsed, 2), "ms_per_step": round(ms_per_step, 4),
                "ttft_ms": round(ttft_ms, 3), "graph_replay_ms": round(replay_ms, 4),
                "generate_loop_tokens_per_s": round(loop_tps, 2),
-               "weights_gb_per_token": round(weight_bytes / 1e9, 4), "cache_bucket": bucket}
+               "weights_gb_per_token": round(weight_bytes / 1e9, 4), "cache_bucket": bucket,
+               "step_roofline": {"bytes_per_token": nbytes, "mean_context": context,
+                                 "achieved_GB/s": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                 "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                 "frac_replay_only": round(nbytes / (replay_ms * 1e-3) / 1e9
+                                                           / PEAK_HBM_GBS, 4)}}
+        log(f"[{variant}] step: {nbytes / 1e9:.4f} GB/token -> {gbs:.0f} GB/s "
+            f"({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
         return model, state, res
 
     model, state, main_res = measure(args.variant, keep_state=not args.no_cpu)
     value, ms_per_step, bucket = main_res["value"], main_res["ms_per_step"], main_res["cache_bucket"]
 
     with torch.inference_mode():
-        roof = lm_head_roofline(model)
-        log(f"lm_head top-1: {roof['us_per_launch']} us, {roof['achieved']} GB/s "
-            f"({100 * roof['frac']:.1f}%)")
+        roof = swiglu_roofline(model, args.variant)
+        lm = lm_head_roofline(model)
         kernels = {} if args.no_kernels else kernel_table(dev)
     del model
     torch.cuda.empty_cache()
@@ -379,14 +645,16 @@ def main() -> None:
         other = "a8w8" if args.variant == "bf16" else "bf16"
         m2, _, variants[other] = measure(other, keep_state=False)
         variants[other].pop("weights_gb_per_token")  # counted before quantisation
+        with torch.inference_mode():
+            variants[other]["swiglu_gemv"] = swiglu_roofline(m2, other)
         del m2
         torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
         log("CPU baseline ...")
-        cpu = cpu_baseline(state, cfg, prompt_cpu[:, : args.cpu_prompt], args.cpu_decode_steps)
-        log(f"CPU oracle: {cpu['value']} tok/s decode, TTFT {cpu['ttft_ms']} ms on {cpu['cores']} threads")
+        cpu = cpu_baseline(state, cfg, prompt_cpu[:, : args.cpu_prompt], args.cpu_decode_steps,
+                           eager=not args.no_eager)
 
     result = {
         "metric": "decode tokens/s (batch 1, greedy) + TTFT, 1 GPU",
@@ -410,9 +678,11 @@ def main() -> None:
         "weights_gb_per_token": main_res["weights_gb_per_token"],
         "variants": variants,
         "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
-        "roofline_detail": roof,
+        "roofline_detail": {"swiglu_gemv": roof, "lm_head": lm},
+        "step_roofline": main_res["step_roofline"],
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "inputs_sha256": _digest_report(digests),
     }
     print(json.dumps(result), flush=True)
 

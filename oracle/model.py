@@ -47,6 +47,7 @@ class Shapes:
     conv_k: int
     eps: float
     vocab: int
+    mrope_section: tuple = (11, 11, 10)
 
     @classmethod
     def from_config(cls, cfg):
@@ -64,6 +65,7 @@ class Shapes:
             conv_k=cfg.linear_conv_kernel_dim,
             eps=cfg.rms_norm_eps,
             vocab=cfg.vocab_size,
+            mrope_section=tuple(rp.get("mrope_section", (11, 11, 10))),
         )
 
 
@@ -201,21 +203,39 @@ class OracleDecoder:
         return self._lin(act, lw, "down")
 
     # ------------------------------------------------------------ forward
+    def _layer_states(self, i: int, cache: Cache) -> dict:
+        if i in cache.rec:
+            return {"conv": cache.conv[i].clone(), "rec": cache.rec[i].clone()}
+        return {"k": cache.k[i].clone(), "v": cache.v[i].clone()}
+
     @torch.no_grad()
-    def forward(self, ids: torch.Tensor, cache: Cache) -> torch.Tensor:
-        """ids [1, L] at positions cache.length ...; returns the final-normed
-        hidden states [1, L, hidden] and advances the cache."""
+    def forward(self, ids: torch.Tensor | None, cache: Cache, trace: list | None = None, *,
+                embeds: torch.Tensor | None = None,
+                rope_positions: torch.Tensor | None = None) -> torch.Tensor:
+        """ids [1, L] (or ``embeds`` [1, L, hidden], the input embeddings of a
+        multimodal prompt) written at cache slots cache.length ...; returns the
+        final-normed hidden states [1, L, hidden] and advances the cache.
+        ``rope_positions`` ([1, L] or multimodal [3, 1, L]) default to the
+        cache slots (text-only positions).
+
+        ``trace`` (a list) receives one dict per layer for layer-wise checks:
+        ``residual_in`` / ``normalized_in`` (the layer's input stream and its
+        input-normed row), ``update`` (mixer output), ``residual_mid`` (stream
+        after the mixer add), ``mlp_out``, ``normalized_out`` (the next
+        layer's normed input, or the final norm) and ``states`` (the layer's
+        conv/recurrent or K/V cache after the layer, cloned)."""
         s = self.s
-        l = ids.shape[1]
+        l = ids.shape[1] if ids is not None else embeds.shape[1]
         start = cache.length
         if start + l > cache.max_len:
             raise ValueError("cache too short")
-        positions = torch.arange(start, start + l).view(1, l)
-        cos, sin = ops.rotary_cos_sin(positions, s.rotary_dim, s.rope_theta)
-        residual = self.w["embed"][ids]
+        positions = torch.arange(start, start + l).view(1, l) if rope_positions is None else rope_positions
+        cos, sin = ops.rotary_cos_sin(positions, s.rotary_dim, s.rope_theta, s.mrope_section)
+        residual = self.w["embed"][ids] if ids is not None else embeds.to(torch.bfloat16)
         layers = self.w["layers"]
         normalized = ops.rms_norm(residual, layers[0]["in_norm"], s.eps)
         for i, lw in enumerate(layers):
+            rec = {"residual_in": residual, "normalized_in": normalized} if trace is not None else None
             if lw["kind"] == "linear_attention":
                 upd = self._delta(i, lw, normalized, cache)
             else:
@@ -224,6 +244,10 @@ class OracleDecoder:
             mlp_out = self._mlp(lw, mlp_in)
             nxt = layers[i + 1]["in_norm"] if i + 1 < len(layers) else self.w["final_norm"]
             residual_new, normalized = ops.residual_add_rms_norm(residual, mlp_out, nxt, s.eps)
+            if rec is not None:
+                rec.update(update=upd, residual_mid=residual, mlp_out=mlp_out,
+                           normalized_out=normalized, states=self._layer_states(i, cache))
+                trace.append(rec)
             if i + 1 < len(layers):
                 residual = residual_new
         cache.length = start + l

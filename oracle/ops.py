@@ -264,12 +264,25 @@ def prefill_attention(q, keys, values, scale, kv_start: int = 0):
 
 
 # ---------------------------------------------------------------- rotary
-def rotary_cos_sin(positions: torch.Tensor, rotary_dim: int = 64, theta: float = 1e7):
-    """Text-only Qwen3.5 rotary table (Transformers Qwen3_5TextRotaryEmbedding
-    with identical T/H/W positions, where interleaved mrope is the identity):
-    inv_freq = 1/theta^(2i/R) in fp32; freqs = pos * inv_freq (fp32);
-    emb = [freqs, freqs]; cos/sin -> bf16. positions [B,L] int64."""
+def rotary_cos_sin(positions: torch.Tensor, rotary_dim: int = 64, theta: float = 1e7,
+                   mrope_section=(11, 11, 10)):
+    """Qwen3.5 rotary table (Transformers Qwen3_5TextRotaryEmbedding, default
+    rope): inv_freq = 1/theta^(2i/R) in fp32; freqs = pos * inv_freq (fp32);
+    emb = [freqs, freqs]; cos/sin -> bf16.
+
+    ``positions`` [B, L] int64 (text: the same position on the temporal,
+    height and width rows) or [3, B, L] multimodal rows, combined by the
+    interleaved mrope rule: frequency j takes row 1 when j % 3 == 1 and
+    j < 3 * section[1], row 2 when j % 3 == 2 and j < 3 * section[2], else
+    row 0 (modeling_qwen3_5.py apply_interleaved_mrope)."""
     inv_freq = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, dtype=torch.int64).float() / rotary_dim))
-    freqs = positions.float()[..., None] * inv_freq
+    if positions.ndim == 2:
+        positions = positions[None].expand(3, *positions.shape)
+    freqs = positions.float()[..., None] * inv_freq  # [3, B, L, R/2]
+    j = torch.arange(rotary_dim // 2)
+    row = torch.zeros_like(j)
+    row[(j % 3 == 1) & (j < 3 * mrope_section[1])] = 1
+    row[(j % 3 == 2) & (j < 3 * mrope_section[2])] = 2
+    freqs = torch.gather(freqs, 0, row.view(1, 1, 1, -1).expand(1, *freqs.shape[1:]))[0]
     emb = torch.cat((freqs, freqs), dim=-1)
     return _bf(emb.cos()), _bf(emb.sin())

@@ -1,11 +1,23 @@
-"""hipGraph runner for the single-token greedy Qwen3.5 decode step.
+"""Captured greedy decode for the Qwen3.5 hot path (hipGraph via torch.cuda.graph).
 
-Drop-in for reference qwen35_fused/graph.py:10-94: captures one (or
-``steps``) greedy decode step(s) — the patched text forward, the fused
-lm_head top-1, the token feedback and ``position_ids += 1`` — with
-``torch.cuda.graph`` (a hipGraph on ROCm) and replays it once per token. All
-kernels read the valid cache length and the position from device memory, so a
-replay needs no host work besides the launch.
+Interface of reference qwen35_fused/graph.py:10-94 (``GreedyDecodeGraph`` with
+``set_inputs`` and ``replay``; ``replay`` returns the next token ``[1, 1]`` for
+one step per replay, or ``[steps, 1, 1]``), built around a token ring instead
+of separate input/output buffers:
+
+* ``_ring`` holds ``steps`` token slots. Captured step ``s`` reads its input
+  token from slot ``s - 1`` (step 0 from the last slot, which holds the
+  previous replay's final token or the token given to ``set_inputs``) and its
+  greedy token lands in slot ``s``. Consecutive replays therefore continue the
+  sequence with no copy node and no host work, and with one step per replay
+  the single slot is both the input and the output token.
+* With ``fused_lm_head`` the lm_head top-1 launch writes the token straight
+  into its ring slot and advances the position tensor in the same launch
+  (``lm_head_argmax(..., out=, advance=)``); otherwise the logits path of the
+  model runs and the argmax and ``position += 1`` are separate captured ops.
+
+Everything the captured kernels read between replays (token, position, cache
+length) lives in device memory, so ``replay`` is one graph launch.
 """
 
 from __future__ import annotations
@@ -16,69 +28,75 @@ from .kernels import lm_head_argmax
 
 
 class GreedyDecodeGraph:
-    """Capture model decode, LM head argmax and autoregressive token feedback.
+    """One capture of ``steps`` greedy decode steps of ``model`` over ``cache``.
 
-    The supplied cache must already hold the prefill state and use static
-    full-attention layers. ``position_ids`` is the first decode token's
-    position tensor (``[1, 1]`` text positions, or the multimodal layout).
+    ``cache`` must hold the prefill state (static full-attention layers);
+    ``token`` is the first decode input ``[1, 1]`` int64 and ``position_ids``
+    its position tensor (``[1, 1]`` text positions or a multimodal
+    ``[k, 1, 1]`` tensor), both on the GPU.
     """
 
     def __init__(self, model, cache, token, position_ids, *, fused_lm_head: bool = True,
                  steps: int = 1) -> None:
-        if token.shape[-1] != 1 or token.dtype != torch.long or not token.is_cuda:
-            raise ValueError("token must be a GPU int64 tensor with sequence length 1")
-        if not position_ids.is_cuda:
-            raise ValueError("position_ids must be on the GPU")
-        if steps < 1:
-            raise ValueError("steps must be positive")
+        if not (isinstance(token, torch.Tensor) and token.is_cuda and token.dtype == torch.long
+                and token.shape[-1] == 1):
+            raise ValueError("token must be an int64 GPU tensor whose last dimension is 1")
+        if not (isinstance(position_ids, torch.Tensor) and position_ids.is_cuda):
+            raise ValueError("position_ids must be a GPU tensor")
+        if int(steps) < 1:
+            raise ValueError("steps must be at least 1")
         self.model = model
         self.cache = cache
-        self.token = token.clone()
-        self.position_ids = position_ids.clone()
-        self.graph = torch.cuda.CUDAGraph()
+        self.fused_lm_head = bool(fused_lm_head)
+        self.steps = int(steps)
+        self._ring = torch.empty((self.steps, *token.shape), dtype=torch.long, device=token.device)
+        self._ring[-1].copy_(token)
+        self._positions = position_ids.clone()
         self.logits = None
-        self.fused_lm_head = fused_lm_head
-        self.steps = steps
-        self.output_tokens = None
-        if steps > 1:
-            self.output_tokens = torch.empty((steps, *self.token.shape), device=self.token.device,
-                                             dtype=self.token.dtype)
-        torch.cuda.synchronize()
+        torch.cuda.synchronize(token.device)
+        self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            for step in range(self.steps):
-                if self.fused_lm_head:
-                    outputs = self.model.model(input_ids=self.token, attention_mask=None,
-                                               position_ids=self.position_ids,
-                                               past_key_values=self.cache, use_cache=True,
-                                               return_dict=True)
-                    hidden = outputs.last_hidden_state[:, -1, :].contiguous()
-                    # top-1, token feedback and position += 1 in the final-reduce launch
-                    lm_head_argmax(hidden, self.model.lm_head.weight, out=self.token,
-                                   advance=self.position_ids)
-                    if self.output_tokens is not None:
-                        self.output_tokens[step].copy_(self.token)
-                    continue
-                else:
-                    outputs = self.model(input_ids=self.token, attention_mask=None,
-                                         position_ids=self.position_ids, past_key_values=self.cache,
-                                         use_cache=True, logits_to_keep=1, return_dict=True)
-                    self.logits = outputs.logits
-                    next_token = self.logits[:, -1, :].argmax(dim=-1, keepdim=True)
-                if self.output_tokens is not None:
-                    self.output_tokens[step].copy_(next_token)
-                self.token.copy_(next_token)
-                self.position_ids.add_(1)
+            for s in range(self.steps):
+                self._record_step(self._ring[s - 1], self._ring[s])
+
+    def _record_step(self, token_in: torch.Tensor, token_out: torch.Tensor) -> None:
+        model, positions = self.model, self._positions
+        if self.fused_lm_head:
+            state = model.model(input_ids=token_in, attention_mask=None, position_ids=positions,
+                                past_key_values=self.cache, use_cache=True, return_dict=True)
+            last = state.last_hidden_state[:, -1, :].contiguous()
+            lm_head_argmax(last, model.lm_head.weight, out=token_out, advance=positions)
+            return
+        state = model(input_ids=token_in, attention_mask=None, position_ids=positions,
+                      past_key_values=self.cache, use_cache=True, logits_to_keep=1,
+                      return_dict=True)
+        self.logits = state.logits
+        token_out.copy_(state.logits[:, -1, :].argmax(dim=-1, keepdim=True).view_as(token_out))
+        positions.add_(1)
+
+    @property
+    def token(self) -> torch.Tensor:
+        """The most recent greedy token (the next replay's input)."""
+        return self._ring[-1]
+
+    @property
+    def position_ids(self) -> torch.Tensor:
+        """The position tensor the next replay decodes at."""
+        return self._positions
+
+    @property
+    def output_tokens(self) -> torch.Tensor | None:
+        return self._ring if self.steps > 1 else None
 
     def set_inputs(self, token: torch.Tensor, position_ids: torch.Tensor) -> None:
-        """Set the first token and position for the next replay."""
-        if token.shape != self.token.shape or position_ids.shape != self.position_ids.shape:
+        """Start the next replay from ``token`` at ``position_ids``."""
+        if tuple(token.shape) != tuple(self._ring.shape[1:]) or position_ids.shape != self._positions.shape:
             raise ValueError("graph input shapes do not match the captured buffers")
-        self.token.copy_(token)
-        self.position_ids.copy_(position_ids)
+        self._ring[-1].copy_(token)
+        self._positions.copy_(position_ids)
 
     def replay(self) -> torch.Tensor:
+        """Run the captured steps; the token ``[1, 1]`` (one step) or the
+        ``[steps, 1, 1]`` tokens of this replay, in order."""
         self.graph.replay()
-        if self.steps == 1:
-            return self.token
-        assert self.output_tokens is not None
-        return self.output_tokens
+        return self._ring[0] if self.steps == 1 else self._ring

@@ -1,36 +1,39 @@
-"""Install the MI355X fused Qwen3.5 inference path on a Transformers model.
+"""Install the MI355X Qwen3.5 fast path on a Transformers model.
 
-Drop-in for the reference's qwen35_fused/integration.py: the same
-``FusionConfig`` fields, ``apply_fusions(model, config) -> stats`` and
-``precompute_vision_kwargs``, the same weight packing and the same patched
-module forwards, with every decode and prefill operator running on the
-gfx950 kernels of ``ppu_amd.kernels``. Fields added for MI355X:
+Public interface of reference qwen35_fused/integration.py (``FusionConfig``
+:32-48, ``apply_fusions(model, config) -> stats`` :778-814,
+``precompute_vision_kwargs`` :738-775): the same config fields and stats keys,
+the same packed weight layouts and the same module forwards taking over, with
+every decode and prefill operator on the gfx950 kernels of ``ppu_amd.kernels``.
 
-  fused_decode : at L == 1 the patched text forward runs each layer as a few
-                 fused launches (residual add + RMSNorm in the prologue of the
-                 next GEMV, conv1d + delta rule + gated RMSNorm in one kernel,
-                 attention combine + sigmoid gate in one kernel) instead of the
-                 reference's per-op sequence;
-  a8w8         : the packed projections and the other linears run as A8W8
-                 (per-channel int8 weights quantised once here, per-token int8
-                 activations), as reference explore_runtime_quantization.py
-                 applies PPUA8W8Linear to the M, F and L module groups. The
-                 lm_head stays bf16.
+How it is put together here:
 
-Patched forwards fall back to the original Transformers forward for inputs
-that are not GPU bf16 tensors, as the reference does (integration.py:51-52);
-with ``release_original_weights`` that fallback cannot run (the reference has
-the same limitation).
+* Each packed projection is a ``_Weight`` submodule (bf16 ``[N, K]``, or with
+  A8W8 an int8 ``[N, K]`` + fp32 per-row scales) attached to the module that
+  owns it, so the packed tensors follow ``model.to()`` and stay out of the
+  state dict.
+* ``_take_over`` routes a module's ``forward`` through a fast function that
+  answers ``NotImplemented`` for inputs it does not handle (CPU or non-bf16
+  tensors, as reference integration.py:51-52); the original forward then runs.
+* The decoder stack is driven layer by layer by ``prefill_layer`` and
+  ``decode_layer``; ``decode_layer`` is the fused batch-1 decode of one layer
+  (residual add + RMSNorm in the prologue of the layer's first GEMV, the conv
+  update in its epilogue, the gated norm in the output projection's prologue,
+  Q/K norm + RoPE + cache write + split-K attention in one launch and the
+  combine + gate in another, the post-attention norm in the SwiGLU GEMV).
+
+Fields added for MI355X: ``fused_decode`` (use ``decode_layer`` for batch-1
+single-token steps over a static cache) and ``a8w8`` (the packed projections
+and the other linears as A8W8, as reference explore_runtime_quantization.py
+applies PPUA8W8Linear; the lm_head stays bf16).
 """
 
 from __future__ import annotations
 
-import types
 from dataclasses import dataclass
-from typing import Any
+from typing import Any, Callable
 
 import torch
-import torch.nn.functional as F
 from transformers.cache_utils import DynamicCache
 from transformers.models.qwen3_5 import modeling_qwen3_5 as qwen_impl
 
@@ -39,7 +42,7 @@ from . import kernels as K
 
 @dataclass(frozen=True)
 class FusionConfig:
-    """reference integration.py:32-48, plus ``fused_decode`` and ``a8w8``."""
+    """Switches of reference integration.py:32-48, plus ``fused_decode`` and ``a8w8``."""
 
     delta: bool = True
     rms_norm: bool = True
@@ -60,509 +63,497 @@ class FusionConfig:
     a8w8: bool = False
 
 
-def _is_fast_tensor(x: torch.Tensor) -> bool:
-    return x.is_cuda and x.dtype == torch.bfloat16
+def _gpu_bf16(t: Any) -> bool:
+    return isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.bfloat16
 
 
-def _register_buffer(module: torch.nn.Module, name: str, value: torch.Tensor | None) -> None:
-    if hasattr(module, name):
-        setattr(module, name, value)
-    else:
-        module.register_buffer(name, value, persistent=False)
-
-
-def _release_linear_weight(module: torch.nn.Module) -> int:
-    weight = module.weight
-    released = weight.numel() * weight.element_size()
-    module.register_parameter("weight", None)
-    return released
-
-
-def _text_model(model: torch.nn.Module) -> torch.nn.Module:
+def text_stack(model: torch.nn.Module) -> torch.nn.Module:
+    """The decoder stack: ``model.model.language_model`` (VLM) or ``model.model``."""
     inner = model.model
     return getattr(inner, "language_model", inner)
 
 
-# ----------------------------------------------------------------- linears
-class _Linear:
-    """A projection weight as the decode/prefill kernels consume it: bf16
-    [N, K], or int8 [N, K] + fp32 [N, 1] scales when A8W8 is on."""
+# ----------------------------------------------------------------- weights
+class _Weight(torch.nn.Module):
+    """A projection weight in the form the kernels read."""
 
-    def __init__(self, weight: torch.Tensor, a8w8: bool):
-        self.a8w8 = a8w8
-        if a8w8:
-            self.wq, self.scale = K.quantize_weight_i8(weight.contiguous())
-            self.weight = None
+    def __init__(self, weight: torch.Tensor, int8: bool) -> None:
+        super().__init__()
+        weight = weight.detach().contiguous()
+        if int8:
+            q, scale = K.quantize_weight_i8(weight)
+            self.register_buffer("w", q, persistent=False)
+            self.register_buffer("s", scale.reshape(-1).contiguous(), persistent=False)
         else:
-            self.weight = weight.contiguous()
-            self.wq = self.scale = None
-        self.out_features = weight.shape[0]
+            self.register_buffer("w", weight, persistent=False)
+            self.s = None
 
-    def gemv_args(self) -> tuple[torch.Tensor, torch.Tensor | None]:
-        """(weight, scale) for the fused decode GEMVs: bf16 weight and None, or
-        int8 weight and its fp32 per-channel scales."""
-        return (self.wq, self.scale) if self.a8w8 else (self.weight, None)
+    @property
+    def int8(self) -> bool:
+        return self.w.dtype == torch.int8
 
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        if self.a8w8:
-            return K.a8w8_linear(x.contiguous(), self.wq, self.scale)
+    @property
+    def out_features(self) -> int:
+        return self.w.shape[0]
+
+    def operands(self) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """(weight, per-row scales or None) for the fused decode GEMVs."""
+        return self.w, self.s
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.int8:
+            return K.a8w8_linear(x.contiguous(), self.w, self.s)
         if x.numel() == x.shape[-1]:
-            return K.linear(x, self.weight)
-        return K.prefill_linear(x, self.weight)
+            return K.linear(x.contiguous(), self.w)
+        return K.prefill_linear(x, self.w)
 
 
-def _pack_linear_weights(model: torch.nn.Module, config: FusionConfig) -> dict[str, int]:
-    """reference integration.py:69-140: packed [qkv|z|a|b] (padded), [gate; up]
-    and [q; k; v] projections; originals released when configured."""
-    text_model = _text_model(model)
-    stats = {"delta": 0, "mlp": 0, "attention": 0, "vision": 0, "released_weight_bytes": 0}
-    q8 = config.a8w8
-    for layer in text_model.layers:
-        if hasattr(layer, "linear_attn") and config.delta:
-            delta = layer.linear_attn
-            packed = torch.cat(
-                (delta.in_proj_qkv.weight, delta.in_proj_z.weight, delta.in_proj_a.weight,
-                 delta.in_proj_b.weight),
-                dim=0,
-            ).contiguous().detach()
-            if config.delta_projection_padding:
-                pad_rows = (-packed.shape[0]) % config.delta_projection_padding
-                if pad_rows:
-                    packed = F.pad(packed, (0, 0, 0, pad_rows))
-            _register_buffer(delta, "_fused_in_proj_weight", packed)
-            delta._q35_in = _Linear(packed, q8)
-            delta._q35_out = _Linear(delta.out_proj.weight.detach(), q8)
-            delta._q35_conv_w = delta.conv1d.weight.detach().squeeze(1).contiguous()
-            if q8:
-                _register_buffer(delta, "_fused_in_proj_weight", None)
-            if config.release_original_weights:
-                stats["released_weight_bytes"] += sum(
-                    _release_linear_weight(p)
-                    for p in (delta.in_proj_qkv, delta.in_proj_z, delta.in_proj_a, delta.in_proj_b)
-                )
-            stats["delta"] += 1
-
-        if config.swiglu:
-            mlp = layer.mlp
-            gate_up = torch.cat((mlp.gate_proj.weight, mlp.up_proj.weight), dim=0).contiguous().detach()
-            _register_buffer(mlp, "_fused_gate_up_weight", gate_up)
-            mlp._q35_gate_up = _Linear(gate_up, q8)
-            mlp._q35_down = _Linear(mlp.down_proj.weight.detach(), q8)
-            if q8:
-                _register_buffer(mlp, "_fused_gate_up_weight", None)
-            if config.release_original_weights:
-                stats["released_weight_bytes"] += _release_linear_weight(mlp.gate_proj)
-                stats["released_weight_bytes"] += _release_linear_weight(mlp.up_proj)
-            stats["mlp"] += 1
-
-        if hasattr(layer, "self_attn") and config.attention:
-            attn = layer.self_attn
-            qgkv = torch.cat(
-                (attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight), dim=0
-            ).contiguous().detach()
-            biases = (attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias)
-            if any(b is not None for b in biases):
-                raise ValueError("the MI355X path supports bias-free Qwen3.5 attention projections only")
-            _register_buffer(attn, "_fused_qgkv_weight", qgkv)
-            attn._q35_qgkv = _Linear(qgkv, q8)
-            attn._q35_o = _Linear(attn.o_proj.weight.detach(), q8)
-            if q8:
-                _register_buffer(attn, "_fused_qgkv_weight", None)
-            if config.release_original_weights:
-                for p in (attn.q_proj, attn.k_proj, attn.v_proj):
-                    stats["released_weight_bytes"] += _release_linear_weight(p)
-            stats["attention"] += 1
-    return stats
+def _stack_rows(parts: list[torch.Tensor], multiple: int) -> torch.Tensor:
+    """Concatenate weights along the output dimension, zero rows appended up
+    to a multiple of ``multiple`` (reference integration.py:78-97)."""
+    rows = sum(p.shape[0] for p in parts)
+    total = -(-rows // multiple) * multiple if multiple else rows
+    out = parts[0].new_zeros((total, parts[0].shape[1]))
+    at = 0
+    for p in parts:
+        out[at : at + p.shape[0]].copy_(p.detach())
+        at += p.shape[0]
+    return out
 
 
-# ----------------------------------------------------------------- module patches
-def _patch_norm_module(module: torch.nn.Module) -> None:
-    if hasattr(module, "_fused_original_forward"):
+def _free_linears(*linears: torch.nn.Module) -> int:
+    """Drop the original projection weights; returns the bytes given back."""
+    freed = 0
+    for lin in linears:
+        freed += lin.weight.numel() * lin.weight.element_size()
+        lin.weight = None
+    return freed
+
+
+def _pack_layer(layer: torch.nn.Module, config: FusionConfig, stats: dict[str, int]) -> None:
+    int8 = config.a8w8
+    free = config.release_original_weights
+    if hasattr(layer, "linear_attn") and config.delta:
+        m = layer.linear_attn
+        projections = (m.in_proj_qkv, m.in_proj_z, m.in_proj_a, m.in_proj_b)
+        m.q35_in = _Weight(_stack_rows([p.weight for p in projections],
+                                       config.delta_projection_padding), int8)
+        m.q35_out = _Weight(m.out_proj.weight, int8)
+        m.q35_conv_w = m.conv1d.weight.detach().reshape(m.conv_dim, -1).contiguous()
+        if free:
+            stats["released_weight_bytes"] += _free_linears(*projections)
+        stats["delta"] += 1
+    if config.swiglu:
+        mlp = layer.mlp
+        mlp.q35_gate_up = _Weight(_stack_rows([mlp.gate_proj.weight, mlp.up_proj.weight], 0), int8)
+        mlp.q35_down = _Weight(mlp.down_proj.weight, int8)
+        if free:
+            stats["released_weight_bytes"] += _free_linears(mlp.gate_proj, mlp.up_proj)
+        stats["mlp"] += 1
+    if hasattr(layer, "self_attn") and config.attention:
+        a = layer.self_attn
+        projections = (a.q_proj, a.k_proj, a.v_proj)
+        if any(p.bias is not None for p in projections):
+            raise ValueError("the MI355X path supports bias-free Qwen3.5 attention projections only")
+        a.q35_qgkv = _Weight(_stack_rows([p.weight for p in projections], 0), int8)
+        a.q35_o = _Weight(a.o_proj.weight, int8)
+        if free:
+            stats["released_weight_bytes"] += _free_linears(*projections)
+        stats["attention"] += 1
+
+
+# ----------------------------------------------------------------- forwards
+def _take_over(module: torch.nn.Module, fast: Callable[..., Any]) -> None:
+    """Route ``module.forward`` through ``fast``; when ``fast`` returns
+    ``NotImplemented`` the module's original forward handles the call."""
+    if getattr(module, "_q35_original_forward", None) is not None:
         return
-    module._fused_original_forward = module.forward
+    original = module.forward
 
-    def forward(self, x: torch.Tensor):
-        if _is_fast_tensor(x) and x.is_contiguous():
-            return K.rms_norm(x, self.weight, self.eps)
-        return self._fused_original_forward(x)
+    def forward(*args, **kwargs):
+        out = fast(*args, **kwargs)
+        return original(*args, **kwargs) if out is NotImplemented else out
 
-    module.forward = types.MethodType(forward, module)
-
-
-def _patch_gated_norm_module(module: torch.nn.Module) -> None:
-    if hasattr(module, "_fused_original_forward"):
-        return
-    module._fused_original_forward = module.forward
-
-    def forward(self, hidden_states: torch.Tensor, gate: torch.Tensor | None = None):
-        if gate is not None and _is_fast_tensor(hidden_states):
-            return K.gated_rms_norm(hidden_states.contiguous(), gate.contiguous(), self.weight,
-                                    self.variance_epsilon)
-        return self._fused_original_forward(hidden_states, gate)
-
-    module.forward = types.MethodType(forward, module)
+    module._q35_original_forward = original
+    module.forward = forward
 
 
-def _patch_mlp(module: torch.nn.Module, config: FusionConfig) -> None:
-    """reference integration.py:169-187."""
-    if hasattr(module, "_fused_original_forward"):
-        return
-    module._fused_original_forward = module.forward
-
-    def forward(self, x: torch.Tensor):
-        if not _is_fast_tensor(x):
-            return self._fused_original_forward(x)
-        gate_up = self._q35_gate_up
-        if (config.ppu_swiglu_gemv and x.shape[:2] == (1, 1) and not gate_up.a8w8):
-            activated = K.ppu_swiglu_gemv(x.contiguous(), gate_up.weight,
-                                          block_n=config.ppu_swiglu_block_n)
-        elif gate_up.a8w8:
-            activated = K.a8w8_swiglu(x.contiguous(), gate_up.wq, gate_up.scale)
-        else:
-            activated = K.silu_and_mul(gate_up(x.contiguous()))
-        return self._q35_down(activated)
-
-    module.forward = types.MethodType(forward, module)
+def _norm_fast(module):
+    def fast(x, *args, **kwargs):
+        if args or kwargs or not _gpu_bf16(x) or not x.is_contiguous():
+            return NotImplemented
+        return K.rms_norm(x, module.weight, module.eps)
+    return fast
 
 
-def _delta_cache_tensors(module, cache_params, batch, seq_len, device, dtype):
-    """reference integration.py:191-217: conv and recurrent state tensors of a
-    DeltaNet layer (lazily initialised in the Transformers cache layer)."""
-    conv_shape = (batch, module.conv_dim, module.conv_kernel_size)
-    recurrent_shape = (batch, module.num_v_heads, module.head_k_dim, module.head_v_dim)
-    if cache_params is None:
-        return (
-            torch.zeros(conv_shape, device=device, dtype=dtype),
-            torch.zeros(recurrent_shape, device=device, dtype=torch.float32),
-        )
-    cache_layer = cache_params.layers[module.layer_idx]
-    if cache_layer.record_past:
-        raise RuntimeError("fused DeltaNet does not support rollback cache recording")
-    if not cache_layer.is_conv_states_initialized[0]:
-        example = torch.empty((batch, module.conv_dim, seq_len), device=device, dtype=dtype)
-        cache_layer.lazy_initialization(conv_states=example, conv_kernel_size=module.conv_kernel_size)
-    if not cache_layer.is_recurrent_states_initialized[0]:
-        example = torch.empty(recurrent_shape, device=device, dtype=torch.float32)
-        cache_layer.lazy_initialization(recurrent_states=example)
-    cache_layer.has_previous_state[0] = True
-    return cache_layer.conv_states[0], cache_layer.recurrent_states[0]
+def _gated_norm_fast(module):
+    def fast(hidden_states, gate=None, *args, **kwargs):
+        if gate is None or args or kwargs or not _gpu_bf16(hidden_states):
+            return NotImplemented
+        return K.gated_rms_norm(hidden_states.contiguous(), gate.contiguous(), module.weight,
+                                module.variance_epsilon)
+    return fast
 
 
-def _patch_delta(module: torch.nn.Module, config: FusionConfig) -> None:
-    """reference integration.py:220-274."""
-    if hasattr(module, "_fused_original_forward"):
-        return
-    module._fused_original_forward = module.forward
+def _mlp_fast(module, config: FusionConfig):
+    def fast(x, *args, **kwargs):
+        if args or kwargs or not _gpu_bf16(x):
+            return NotImplemented
+        return _mlp_apply(module, x.contiguous(), config)
+    return fast
 
-    def forward(self, hidden_states, cache_params=None, attention_mask=None, **kwargs):
-        if not _is_fast_tensor(hidden_states):
-            return self._fused_original_forward(hidden_states, cache_params=cache_params,
-                                                attention_mask=attention_mask, **kwargs)
-        if attention_mask is not None:
-            hidden_states = qwen_impl.apply_mask_to_padding_states(hidden_states, attention_mask)
-        batch, seq_len, _ = hidden_states.shape
-        packed = self._q35_in(hidden_states.contiguous())
-        conv_state, recurrent_state = _delta_cache_tensors(
-            self, cache_params, batch, seq_len, hidden_states.device, hidden_states.dtype)
-        qkv = K.causal_conv1d_fused(packed, self._q35_conv_w, conv_state)
-        if self.head_v_dim == 128 and seq_len > 1 and self.conv_dim == 3 * self.value_dim:
-            # prefill: recurrence and gated norm (z read in place) in one call
-            core = K.delta_prefill_gated(qkv, packed, self.A_log, self.dt_bias, recurrent_state,
-                                         self.norm.weight, self.layer_norm_epsilon)
-            return self._q35_out(core.reshape(batch, seq_len, self.value_dim))
-        core = K.delta_recurrent_fused(qkv, packed, self.A_log, self.dt_bias, recurrent_state,
+
+def _mlp_apply(mlp, x: torch.Tensor, config: FusionConfig) -> torch.Tensor:
+    """SwiGLU MLP (reference integration.py:169-187): decode one token through
+    the SwiGLU GEMV, prefill through the GEMM and ``silu_and_mul``."""
+    gate_up = mlp.q35_gate_up
+    if gate_up.int8:
+        act = K.a8w8_swiglu(x, gate_up.w, gate_up.s)
+    elif config.ppu_swiglu_gemv and x.shape[:-1] == (1, 1):
+        act = K.ppu_swiglu_gemv(x, gate_up.w, block_n=config.ppu_swiglu_block_n)
+    else:
+        act = K.silu_and_mul(gate_up(x))
+    return mlp.q35_down(act)
+
+
+# ----------------------------------------------------------------- cache state
+def _delta_state(mixer, cache, batch: int, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """Conv state ``[B, C, kw]`` bf16 and recurrent state ``[B, H, Dk, Dv]``
+    fp32 of a DeltaNet layer: the cache layer's own tensors (created on first
+    use, as Transformers' LinearAttentionLayer does), or fresh zeros without a
+    cache (reference integration.py:191-217)."""
+    conv_shape = (batch, mixer.conv_dim, mixer.conv_kernel_size)
+    rec_shape = (batch, mixer.num_v_heads, mixer.head_k_dim, mixer.head_v_dim)
+    if cache is None:
+        return (torch.zeros(conv_shape, device=device, dtype=torch.bfloat16),
+                torch.zeros(rec_shape, device=device, dtype=torch.float32))
+    slot = cache.layers[mixer.layer_idx]
+    if slot.record_past:
+        raise RuntimeError("the fused DeltaNet path keeps no rollback history (record_past)")
+    if not slot.is_conv_states_initialized[0]:
+        slot.lazy_initialization(conv_states=torch.empty(conv_shape, device=device,
+                                                         dtype=torch.bfloat16))
+    if not slot.is_recurrent_states_initialized[0]:
+        slot.lazy_initialization(recurrent_states=torch.empty(rec_shape, device=device,
+                                                              dtype=torch.float32))
+    slot.has_previous_state[0] = True
+    return slot.conv_states[0], slot.recurrent_states[0]
+
+
+def _kv_slot(attn, cache, like: torch.Tensor):
+    """The static cache layer of an attention module (allocated on first use),
+    or None for a dynamic cache / no cache."""
+    if cache is None:
+        return None
+    slot = cache.layers[attn.layer_idx]
+    if not hasattr(slot, "max_cache_len"):
+        return None
+    if not slot.is_initialized:
+        shape = (like.shape[0], attn.config.num_key_value_heads, like.shape[1], attn.head_dim)
+        probe = torch.empty(shape, device=like.device, dtype=like.dtype)
+        slot.lazy_initialization(probe, probe)
+    return slot
+
+
+# ----------------------------------------------------------------- mixers
+def _delta_prefill(mixer, hidden: torch.Tensor, cache, config: FusionConfig) -> torch.Tensor:
+    """DeltaNet mixer on the GPU (reference integration.py:220-274)."""
+    batch, length, _ = hidden.shape
+    packed = mixer.q35_in(hidden.contiguous())
+    conv_state, rec_state = _delta_state(mixer, cache, batch, hidden.device)
+    qkv = K.causal_conv1d_fused(packed, mixer.q35_conv_w, conv_state)
+    dv = mixer.head_v_dim
+    if dv == 128 and length > 1 and mixer.conv_dim == 3 * mixer.value_dim:
+        core = K.delta_prefill_gated(qkv, packed, mixer.A_log, mixer.dt_bias, rec_state,
+                                     mixer.norm.weight, mixer.layer_norm_epsilon)
+    else:
+        core = K.delta_recurrent_fused(qkv, packed, mixer.A_log, mixer.dt_bias, rec_state,
                                        block_v=config.delta_block_v,
                                        precompute_factors=config.delta_precompute_factors)
-        core = core.reshape(-1, self.head_v_dim)
-        if self.head_v_dim == 128:
-            # z read in place from the packed projection (no copy)
-            core = K.gated_rms_norm_packed(core, packed, self.conv_dim,
-                                           self.value_dim // self.head_v_dim, self.norm.weight,
-                                           self.layer_norm_epsilon)
+        core = core.reshape(-1, dv)
+        if dv == 128:
+            core = K.gated_rms_norm_packed(core, packed, mixer.conv_dim, mixer.value_dim // dv,
+                                           mixer.norm.weight, mixer.layer_norm_epsilon)
         else:
-            z_start = self.conv_dim
-            z = packed[..., z_start : z_start + self.value_dim].reshape(-1, self.head_v_dim)
-            core = K.gated_rms_norm(core, z.contiguous(), self.norm.weight,
-                                    self.layer_norm_epsilon)
-        return self._q35_out(core.reshape(batch, seq_len, self.value_dim))
-
-    module.forward = types.MethodType(forward, module)
+            z = packed[..., mixer.conv_dim : mixer.conv_dim + mixer.value_dim]
+            core = K.gated_rms_norm(core, z.reshape(-1, dv).contiguous(), mixer.norm.weight,
+                                    mixer.layer_norm_epsilon)
+    return mixer.q35_out(core.reshape(batch, length, mixer.value_dim))
 
 
-def _static_cache_layer(module, past_key_values, hidden_states):
-    if past_key_values is None:
-        return None
-    candidate = past_key_values.layers[module.layer_idx]
-    if not hasattr(candidate, "max_cache_len"):
-        return None
-    if not candidate.is_initialized:
-        batch, seq_len = hidden_states.shape[:2]
-        shape = (batch, module.config.num_key_value_heads, seq_len, module.head_dim)
-        initial_key = torch.empty(shape, device=hidden_states.device, dtype=hidden_states.dtype)
-        candidate.lazy_initialization(initial_key, torch.empty_like(initial_key))
-    return candidate
+def _delta_fast(mixer, config: FusionConfig):
+    def fast(hidden_states, cache_params=None, attention_mask=None, **kwargs):
+        if not _gpu_bf16(hidden_states):
+            return NotImplemented
+        if attention_mask is not None:
+            hidden_states = qwen_impl.apply_mask_to_padding_states(hidden_states, attention_mask)
+        return _delta_prefill(mixer, hidden_states, cache_params, config)
+    return fast
 
 
-def _patch_attention(module: torch.nn.Module, config: FusionConfig) -> None:
-    """reference integration.py:277-382; prefill attention runs on the gfx950
-    causal GQA kernel instead of the attention interface."""
-    if hasattr(module, "_fused_original_forward"):
-        return
-    module._fused_original_forward = module.forward
-
-    def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
-                **kwargs):
-        if not _is_fast_tensor(hidden_states):
-            return self._fused_original_forward(hidden_states, position_embeddings, attention_mask,
-                                                past_key_values=past_key_values, **kwargs)
-        packed = self._q35_qgkv(hidden_states.contiguous())
-        cos, sin = position_embeddings
-        cache_layer = _static_cache_layer(self, past_key_values, hidden_states)
-        seq_len = hidden_states.shape[1]
-        q, k, v = K.qgkv_norm_rope(
-            packed, self.q_norm.weight, self.k_norm.weight, cos, sin,
-            q_heads=self.config.num_attention_heads, kv_heads=self.config.num_key_value_heads,
-            dim=self.head_dim, rotary_dim=cos.shape[-1],
-            cache_key=None if cache_layer is None else cache_layer.keys,
-            cache_value=None if cache_layer is None else cache_layer.values,
-            cache_start=None if cache_layer is None else cache_layer.cumulative_length,
-        )
-        valid = None
-        kv_start = 0
-        if cache_layer is not None:
-            cache_layer.cumulative_length.add_(seq_len)
-            valid = cache_layer.cumulative_length
-        elif past_key_values is not None:
-            k, v = past_key_values.update(k, v, self.layer_idx)
-            kv_start = k.shape[2] - seq_len
-        if config.gqa_decode_attention and cache_layer is not None and seq_len == 1:
-            out = K.gqa_decode_attention(q, cache_layer.keys, cache_layer.values, valid,
-                                         self.scaling, packed_gate=packed)
-            return self._q35_o(out), None
-        out = K.gqa_prefill_attention(q, k.contiguous(), v.contiguous(), self.scaling,
+def _attention_prefill(attn, hidden: torch.Tensor, position_embeddings, cache,
+                       config: FusionConfig) -> torch.Tensor:
+    """Attention mixer on the GPU (reference integration.py:277-382): packed
+    projection, Q/K norm + RoPE with the static-cache write, decode attention
+    for one token or causal GQA prefill attention, sigmoid gate, o_proj."""
+    length = hidden.shape[1]
+    packed = attn.q35_qgkv(hidden.contiguous())
+    cos, sin = position_embeddings
+    slot = _kv_slot(attn, cache, hidden)
+    q, k, v = K.qgkv_norm_rope(
+        packed, attn.q_norm.weight, attn.k_norm.weight, cos, sin,
+        q_heads=attn.config.num_attention_heads, kv_heads=attn.config.num_key_value_heads,
+        dim=attn.head_dim, rotary_dim=cos.shape[-1],
+        cache_key=None if slot is None else slot.keys,
+        cache_value=None if slot is None else slot.values,
+        cache_start=None if slot is None else slot.cumulative_length,
+    )
+    kv_start, valid = 0, None
+    if slot is not None:
+        slot.cumulative_length.add_(length)
+        valid = slot.cumulative_length
+    elif cache is not None:
+        k, v = cache.update(k, v, attn.layer_idx)
+        kv_start = k.shape[2] - length
+    if slot is not None and length == 1 and config.gqa_decode_attention:
+        out = K.gqa_decode_attention(q, slot.keys, slot.values, valid, attn.scaling,
+                                     packed_gate=packed)
+    else:
+        out = K.gqa_prefill_attention(q, k.contiguous(), v.contiguous(), attn.scaling,
                                       kv_start=kv_start, valid_length=valid)
-        out = K.attention_gate_mul(out, packed, self.head_dim)
-        return self._q35_o(out), None
-
-    module.forward = types.MethodType(forward, module)
+        out = K.attention_gate_mul(out, packed, attn.head_dim)
+    return attn.q35_o(out)
 
 
-# ----------------------------------------------------------------- text forward
-def _rope_in_kernel(text_model) -> bool:
-    """The fused attention kernel computes cos/sin itself for the default
-    (unscaled) rotary table; other rope types keep Transformers' table."""
-    rot = text_model.rotary_emb
+def _attention_fast(attn, config: FusionConfig):
+    def fast(hidden_states, position_embeddings, attention_mask, past_key_values=None, **kwargs):
+        if not _gpu_bf16(hidden_states):
+            return NotImplemented
+        return _attention_prefill(attn, hidden_states, position_embeddings, past_key_values,
+                                  config), None
+    return fast
+
+
+# ----------------------------------------------------------------- layers
+@dataclass
+class DecodeContext:
+    """What every layer of one fused decode step shares: the cache, the rope
+    positions of the token and, when the rotary table is not computed inside
+    the attention kernel, the token's cos/sin."""
+
+    cache: Any
+    rope_positions: torch.Tensor
+    in_kernel_rope: bool
+    cos: torch.Tensor | None = None
+    sin: torch.Tensor | None = None
+
+
+def _rope_in_kernel(stack) -> bool:
+    """The fused attention kernel builds cos/sin itself for the default
+    (unscaled, fp32 inverse-frequency) rotary table."""
+    rot = stack.rotary_emb
     return (getattr(rot, "rope_type", "default") == "default"
             and float(getattr(rot, "attention_scaling", 1.0)) == 1.0
             and rot.inv_freq.dtype == torch.float32)
 
 
-def _fused_decode_layers(text_model, input_ids, inputs_embeds, config, past_key_values,
-                         rotary_position_ids):
-    """One token through all layers with fused launches; returns the final-normed hidden.
+def decode_layer(stack, index: int, residual: torch.Tensor | None, update: torch.Tensor | None,
+                 ctx: DecodeContext, token: torch.Tensor | None = None, trace: dict | None = None):
+    """One decoder layer of a batch-1 decode step in fused launches.
 
-    Per DeltaNet layer: [residual add + RMSNorm -> packed projection -> conv1d
-    update] [delta rule] [gated RMSNorm -> out_proj] [residual add + RMSNorm ->
-    gate/up GEMV -> SwiGLU] [down]. Per attention layer: [residual add +
-    RMSNorm -> packed projection] [Q/K norm + RoPE + cache write + split-K
-    attention] [combine + gate + length += 1] [o_proj] and the same MLP. The
-    embedding row is gathered by the first projection when layer 0 is a
-    DeltaNet layer. With A8W8 the same launches take int8 weights: each GEMV
-    quantises its (normalised) input row per token inside the launch.
+    The layer's input is the pending pair ``(residual, update)``: its input
+    RMSNorm runs on ``residual + update`` inside the first GEMV (``update`` is
+    None for the first layer; with ``token`` given, ``residual`` is None and
+    the first layer gathers the embedding row itself). Returns the pending pair
+    after the layer: ``(residual after the mixer, MLP output)``. ``trace`` (a
+    dict) receives the mixer output as ``update``.
     """
-    layers = text_model.layers[: text_model.config.num_hidden_layers]
-    in_kernel_rope = _rope_in_kernel(text_model)
-    cos = sin = None
-    if not in_kernel_rope:
-        ref = inputs_embeds if inputs_embeds is not None else text_model.embed_tokens.weight[:1]
-        cos, sin = text_model.rotary_emb(ref, rotary_position_ids)
-    residual = inputs_embeds
-    update = None
-    for index, layer in enumerate(layers):
-        ln = layer.input_layernorm
-        delta = layer.block_type == "linear_attention"
-        mod = layer.linear_attn if delta else layer.self_attn
-        lin = mod._q35_in if delta else mod._q35_qgkv
-        w_in, s_in = lin.gemv_args()
-        if residual is None and not (index == 0 and delta):
-            residual = text_model.embed_tokens(input_ids.view(1, 1))
-        if delta:
-            conv_state, rec_state = _delta_cache_tensors(
-                mod, past_key_values, 1, 1, lin_device(lin), torch.bfloat16)
-            # residual add + input RMSNorm in the packed projection's prologue,
-            # the conv1d update in its epilogue (embedding gather for layer 0)
-            if residual is None:
-                r_new, packed, qkv = K.norm_linear_conv(
-                    text_model.embed_tokens.weight, None, ln.weight, ln.eps, w_in,
-                    mod._q35_conv_w, conv_state, token=input_ids, weight_scale=s_in)
-            else:
-                r_new, packed, qkv = K.norm_linear_conv(residual, update, ln.weight, ln.eps, w_in,
-                                                        mod._q35_conv_w, conv_state,
-                                                        weight_scale=s_in)
-            if r_new is not None:
-                residual = r_new
-            # delta rule on the convolved qkv, then gated RMSNorm as the
-            # prologue of the output projection
-            core = K.delta_recurrent_fused(qkv, packed, mod.A_log, mod.dt_bias, rec_state)
-            z = packed[..., mod.conv_dim : mod.conv_dim + mod.value_dim]
-            w_out, s_out = mod._q35_out.gemv_args()
-            update = K.gated_norm_linear(core, z, mod.norm.weight, mod.layer_norm_epsilon, w_out,
-                                         weight_scale=s_out)
+    layer = stack.layers[index]
+    ln = layer.input_layernorm
+    if hasattr(layer, "linear_attn"):
+        m = layer.linear_attn
+        w_in, s_in = m.q35_in.operands()
+        conv_state, rec_state = _delta_state(m, ctx.cache, 1, w_in.device)
+        if residual is None:
+            r_new, packed, qkv = K.norm_linear_conv(
+                stack.embed_tokens.weight, None, ln.weight, ln.eps, w_in, m.q35_conv_w, conv_state,
+                token=token, weight_scale=s_in)
         else:
-            if update is None:
-                packed = K.norm_linear(residual, ln.weight, ln.eps, w_in, weight_scale=s_in)
-            else:
-                residual, packed = K.residual_norm_linear(residual, update, ln.weight, ln.eps, w_in,
-                                                          weight_scale=s_in)
-            cache_layer = _static_cache_layer(mod, past_key_values, residual)
-            if in_kernel_rope:
-                out = K.gqa_decode_fused(
-                    packed, mod.q_norm.weight, mod.k_norm.weight, text_model.rotary_emb.inv_freq,
-                    rotary_position_ids, cache_layer.keys, cache_layer.values,
-                    cache_layer.cumulative_length, mod.scaling,
-                    q_heads=mod.config.num_attention_heads,
-                    mrope_section=tuple(text_model.rotary_emb.mrope_section))
-            else:
-                q, _, _ = K.qgkv_norm_rope(
-                    packed, mod.q_norm.weight, mod.k_norm.weight, cos, sin,
-                    q_heads=mod.config.num_attention_heads, kv_heads=mod.config.num_key_value_heads,
-                    dim=mod.head_dim, rotary_dim=cos.shape[-1], cache_key=cache_layer.keys,
-                    cache_value=cache_layer.values, cache_start=cache_layer.cumulative_length)
-                cache_layer.cumulative_length.add_(1)
-                out = K.gqa_decode_attention(q, cache_layer.keys, cache_layer.values,
-                                             cache_layer.cumulative_length, mod.scaling,
-                                             packed_gate=packed)
-            update = mod._q35_o(out)
-        # post-attention residual + RMSNorm fused into the SwiGLU GEMV
-        pln = layer.post_attention_layernorm
-        w_gu, s_gu = layer.mlp._q35_gate_up.gemv_args()
-        residual, act = K.residual_norm_linear(residual, update, pln.weight, pln.eps, w_gu,
-                                               swiglu=True, weight_scale=s_gu)
-        update = layer.mlp._q35_down(act)
-    _, normalized = K.residual_add_rms_norm(residual, update, text_model.norm.weight,
-                                            text_model.norm.eps)
-    return normalized
+            r_new, packed, qkv = K.norm_linear_conv(residual, update, ln.weight, ln.eps, w_in,
+                                                    m.q35_conv_w, conv_state, weight_scale=s_in)
+        residual = residual if r_new is None else r_new
+        core = K.delta_recurrent_fused(qkv, packed, m.A_log, m.dt_bias, rec_state)
+        z = packed[..., m.conv_dim : m.conv_dim + m.value_dim]
+        w_out, s_out = m.q35_out.operands()
+        update = K.gated_norm_linear(core, z, m.norm.weight, m.layer_norm_epsilon, w_out,
+                                     weight_scale=s_out)
+    else:
+        a = layer.self_attn
+        w_in, s_in = a.q35_qgkv.operands()
+        if residual is None:
+            residual = stack.embed_tokens(token.view(1, 1))
+        if update is None:
+            packed = K.norm_linear(residual, ln.weight, ln.eps, w_in, weight_scale=s_in)
+        else:
+            residual, packed = K.residual_norm_linear(residual, update, ln.weight, ln.eps, w_in,
+                                                      weight_scale=s_in)
+        slot = _kv_slot(a, ctx.cache, residual)
+        if ctx.in_kernel_rope:
+            rot = stack.rotary_emb
+            out = K.gqa_decode_fused(
+                packed, a.q_norm.weight, a.k_norm.weight, rot.inv_freq, ctx.rope_positions,
+                slot.keys, slot.values, slot.cumulative_length, a.scaling,
+                q_heads=a.config.num_attention_heads, mrope_section=tuple(rot.mrope_section))
+        else:
+            q, _, _ = K.qgkv_norm_rope(
+                packed, a.q_norm.weight, a.k_norm.weight, ctx.cos, ctx.sin,
+                q_heads=a.config.num_attention_heads, kv_heads=a.config.num_key_value_heads,
+                dim=a.head_dim, rotary_dim=ctx.cos.shape[-1], cache_key=slot.keys,
+                cache_value=slot.values, cache_start=slot.cumulative_length)
+            slot.cumulative_length.add_(1)
+            out = K.gqa_decode_attention(q, slot.keys, slot.values, slot.cumulative_length,
+                                         a.scaling, packed_gate=packed)
+        update = a.q35_o(out)
+    if trace is not None:
+        trace["update"] = update
+    pln = layer.post_attention_layernorm
+    w_gu, s_gu = layer.mlp.q35_gate_up.operands()
+    residual, act = K.residual_norm_linear(residual, update, pln.weight, pln.eps, w_gu, swiglu=True,
+                                           weight_scale=s_gu)
+    return residual, layer.mlp.q35_down(act)
 
 
-def lin_device(lin: "_Linear") -> torch.device:
-    return (lin.weight if lin.weight is not None else lin.wq).device
+def prefill_layer(stack, index: int, residual: torch.Tensor, normalized: torch.Tensor, cache,
+                  position_embeddings, config: FusionConfig, trace: dict | None = None):
+    """One decoder layer of the unfused-decode / prefill text forward
+    (reference integration.py:456-499): mixer on the normalised input, residual
+    add + post-attention RMSNorm, MLP, residual add + the next layer's input
+    RMSNorm (the final norm after the last layer). Returns ``(residual,
+    normalised)`` for the next layer; after the last layer ``residual`` is the
+    stream before the final add. ``trace`` (a dict) receives ``update`` (mixer
+    output), ``residual_mid`` and ``mlp_out``."""
+    layer = stack.layers[index]
+    if hasattr(layer, "linear_attn"):
+        update = layer.linear_attn(hidden_states=normalized, cache_params=cache,
+                                   attention_mask=None)
+    else:
+        update, _ = layer.self_attn(hidden_states=normalized, position_embeddings=position_embeddings,
+                                    attention_mask=None, past_key_values=cache)
+    residual, mlp_in = K.residual_add_rms_norm(residual, update.contiguous(),
+                                               layer.post_attention_layernorm.weight,
+                                               layer.post_attention_layernorm.eps)
+    mlp_out = layer.mlp(mlp_in)
+    if trace is not None:
+        trace.update(update=update, residual_mid=residual, mlp_out=mlp_out)
+    last = index + 1 == stack.config.num_hidden_layers
+    norm = stack.norm if last else stack.layers[index + 1].input_layernorm
+    summed, normalized = K.residual_add_rms_norm(residual, mlp_out.contiguous(), norm.weight, norm.eps)
+    return (residual if last else summed), normalized
 
 
-def _patch_text_model(text_model: torch.nn.Module, config: FusionConfig) -> None:
-    """reference integration.py:385-506."""
-    if hasattr(text_model, "_fused_original_forward"):
-        return
-    text_model._fused_original_forward = text_model.forward
+def _rope_positions(position_ids, past_seen: int, batch: int, length: int, device) -> torch.Tensor:
+    """Positions the rotary embedding takes: Transformers' Qwen3.5 text model
+    accepts ``[B, L]`` text positions, ``[3, B, L]`` rope rows or ``[4, B, L]``
+    with the text row first (reference integration.py:409-418)."""
+    if position_ids is None:
+        return torch.arange(past_seen, past_seen + length, device=device).expand(batch, length)
+    if position_ids.ndim == 3 and position_ids.shape[0] == 4:
+        return position_ids[1:]
+    return position_ids
 
-    def forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
-                inputs_embeds=None, use_cache=None, **kwargs):
+
+def _static_cache(stack, cache) -> bool:
+    return cache is not None and all(
+        hasattr(cache.layers[i], "max_cache_len")
+        for i, kind in enumerate(stack.config.layer_types) if kind == "full_attention")
+
+
+def _text_fast(stack, config: FusionConfig):
+    def fast(input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
+             inputs_embeds=None, use_cache=None, **kwargs):
         if (input_ids is None) == (inputs_embeds is None):
             raise ValueError("specify exactly one of input_ids and inputs_embeds")
-        probe = inputs_embeds if inputs_embeds is not None else self.embed_tokens.weight
-        if not _is_fast_tensor(probe) or (input_ids is not None and not input_ids.is_cuda):
-            if inputs_embeds is None:
-                inputs_embeds = self.embed_tokens(input_ids)
-            return self._fused_original_forward(
-                input_ids=None, attention_mask=attention_mask, position_ids=position_ids,
-                past_key_values=past_key_values, inputs_embeds=inputs_embeds, use_cache=use_cache,
-                **kwargs)
-        if use_cache and past_key_values is None:
-            past_key_values = DynamicCache(config=self.config)
-        src = inputs_embeds if inputs_embeds is not None else input_ids
-        batch, seq_len = src.shape[0], src.shape[1]
-        if position_ids is None:
-            past_seen = past_key_values.get_seq_length() if past_key_values is not None else 0
-            position_ids = torch.arange(seq_len, device=src.device) + past_seen
-            position_ids = position_ids.view(1, 1, -1).expand(4, batch, -1)
-        elif position_ids.ndim == 2:
-            position_ids = position_ids[None, ...].expand(4, position_ids.shape[0], -1)
-        if position_ids.ndim == 3 and position_ids.shape[0] == 4:
-            text_position_ids = position_ids[0]
-            rotary_position_ids = position_ids[1:]
+        if inputs_embeds is not None:
+            if not _gpu_bf16(inputs_embeds):
+                return NotImplemented
+            device, (batch, length) = inputs_embeds.device, inputs_embeds.shape[:2]
         else:
-            text_position_ids = None
-            rotary_position_ids = position_ids
-        if isinstance(attention_mask, torch.Tensor) and not torch.cuda.is_current_stream_capturing():
-            if not bool(attention_mask.all()):
-                raise ValueError("the fused MI355X path does not support padded inputs")
-        static = past_key_values is not None and all(
-            hasattr(past_key_values.layers[i], "max_cache_len")
-            for i, t in enumerate(self.config.layer_types) if t == "full_attention")
-        if (config.fused_decode and seq_len == 1 and batch == 1 and static
+            if not (input_ids.is_cuda and _gpu_bf16(stack.embed_tokens.weight)):
+                return NotImplemented
+            device, (batch, length) = input_ids.device, input_ids.shape[:2]
+        if position_ids is not None and position_ids.device != device:
+            raise ValueError(f"position_ids are on {position_ids.device}, the inputs on {device}")
+        if (isinstance(attention_mask, torch.Tensor) and not torch.cuda.is_current_stream_capturing()
+                and not bool(attention_mask.all())):
+            raise ValueError("the fused MI355X path does not support padded inputs")
+        cache = past_key_values
+        if use_cache and cache is None:
+            cache = DynamicCache(config=stack.config)
+        past = cache.get_seq_length() if cache is not None else 0
+        rope_pos = _rope_positions(position_ids, past, batch, length, device)
+        n = stack.config.num_hidden_layers
+        if (config.fused_decode and length == 1 and batch == 1 and _static_cache(stack, cache)
                 and config.delta and config.attention and config.swiglu):
+            ctx = DecodeContext(cache, rope_pos, _rope_in_kernel(stack))
+            if not ctx.in_kernel_rope:
+                ref = inputs_embeds if inputs_embeds is not None else stack.embed_tokens.weight[:1]
+                ctx.cos, ctx.sin = stack.rotary_emb(ref, rope_pos)
             token = None
-            if inputs_embeds is None:
-                token = input_ids.reshape(-1)[:1]
-                if input_ids.dtype != torch.int64:
-                    token = token.to(torch.int64)
-            normalized = _fused_decode_layers(
-                self, token, None if inputs_embeds is None else inputs_embeds.contiguous(), config,
-                past_key_values, rotary_position_ids)
-            return qwen_impl.Qwen3_5ModelOutputWithPast(last_hidden_state=normalized,
-                                                        past_key_values=past_key_values)
-        if inputs_embeds is None:
-            inputs_embeds = self.embed_tokens(input_ids)
-        position_embeddings = self.rotary_emb(inputs_embeds, rotary_position_ids)
-        residual = inputs_embeds.contiguous()
-        normalized = K.rms_norm(residual, self.layers[0].input_layernorm.weight,
-                                self.layers[0].input_layernorm.eps)
-        n_layers = self.config.num_hidden_layers
-        for index, layer in enumerate(self.layers[:n_layers]):
-            if layer.block_type == "linear_attention":
-                update = layer.linear_attn(hidden_states=normalized, cache_params=past_key_values,
-                                           attention_mask=None, **kwargs)
-            else:
-                update, _ = layer.self_attn(hidden_states=normalized, attention_mask=None,
-                                            position_ids=text_position_ids,
-                                            past_key_values=past_key_values,
-                                            position_embeddings=position_embeddings, **kwargs)
-            residual, mlp_in = K.residual_add_rms_norm(residual, update.contiguous(),
-                                                       layer.post_attention_layernorm.weight,
-                                                       layer.post_attention_layernorm.eps)
-            mlp_out = layer.mlp(mlp_in)
-            nxt = self.layers[index + 1].input_layernorm if index + 1 < n_layers else self.norm
-            res_next, normalized = K.residual_add_rms_norm(residual, mlp_out.contiguous(),
-                                                           nxt.weight, nxt.eps)
-            if index + 1 < n_layers:
-                residual = res_next
-        return qwen_impl.Qwen3_5ModelOutputWithPast(last_hidden_state=normalized,
-                                                    past_key_values=past_key_values)
-
-    text_model.forward = types.MethodType(forward, text_model)
+            residual = inputs_embeds.contiguous() if inputs_embeds is not None else None
+            if residual is None:
+                token = input_ids.reshape(-1)[:1].to(torch.int64)
+            update = None
+            for i in range(n):
+                residual, update = decode_layer(stack, i, residual, update, ctx, token)
+            _, hidden = K.residual_add_rms_norm(residual, update, stack.norm.weight, stack.norm.eps)
+        else:
+            embeds = inputs_embeds if inputs_embeds is not None else stack.embed_tokens(input_ids)
+            rope = stack.rotary_emb(embeds, rope_pos)
+            residual = embeds.contiguous()
+            hidden = K.rms_norm(residual, stack.layers[0].input_layernorm.weight,
+                                stack.layers[0].input_layernorm.eps)
+            for i in range(n):
+                residual, hidden = prefill_layer(stack, i, residual, hidden, cache, rope, config)
+        return qwen_impl.Qwen3_5ModelOutputWithPast(last_hidden_state=hidden, past_key_values=cache)
+    return fast
 
 
+# ----------------------------------------------------------------- entry points
 def precompute_vision_kwargs(model: torch.nn.Module, inputs: Any) -> Any:
     """reference integration.py:738-775. The vision encoder is outside this
-    build; for text-only inputs (no ``image_grid_thw``) the mapping is returned
-    unchanged, and image inputs are passed through for Transformers' own
-    vision path."""
+    build: for text-only inputs (no ``image_grid_thw``) the mapping is returned
+    unchanged, and image inputs go to Transformers' own vision path, which
+    computes these tensors itself."""
     return inputs
 
 
 def apply_fusions(model: torch.nn.Module, config: FusionConfig | None = None) -> dict[str, int]:
-    """Pack weights and install the enabled fast paths (reference integration.py:778-814)."""
+    """Pack the projection weights and take over the enabled module forwards
+    (reference integration.py:778-814). Returns the packing statistics."""
     config = config or FusionConfig()
     if model.training:
         raise ValueError("apply_fusions requires model.eval()")
-    stats = _pack_linear_weights(model, config)
-    text_model = _text_model(model)
-    for layer in text_model.layers:
+    stack = text_stack(model)
+    stats = {"delta": 0, "mlp": 0, "attention": 0, "vision": 0, "released_weight_bytes": 0}
+    for layer in stack.layers:
+        _pack_layer(layer, config, stats)
+    for layer in stack.layers:
         if config.rms_norm:
-            _patch_norm_module(layer.input_layernorm)
-            _patch_norm_module(layer.post_attention_layernorm)
+            _take_over(layer.input_layernorm, _norm_fast(layer.input_layernorm))
+            _take_over(layer.post_attention_layernorm, _norm_fast(layer.post_attention_layernorm))
         if config.swiglu:
-            _patch_mlp(layer.mlp, config)
+            _take_over(layer.mlp, _mlp_fast(layer.mlp, config))
         if hasattr(layer, "linear_attn") and config.delta:
-            _patch_gated_norm_module(layer.linear_attn.norm)
-            _patch_delta(layer.linear_attn, config)
+            _take_over(layer.linear_attn.norm, _gated_norm_fast(layer.linear_attn.norm))
+            _take_over(layer.linear_attn, _delta_fast(layer.linear_attn, config))
         if hasattr(layer, "self_attn") and config.attention:
-            _patch_norm_module(layer.self_attn.q_norm)
-            _patch_norm_module(layer.self_attn.k_norm)
-            _patch_attention(layer.self_attn, config)
+            _take_over(layer.self_attn.q_norm, _norm_fast(layer.self_attn.q_norm))
+            _take_over(layer.self_attn.k_norm, _norm_fast(layer.self_attn.k_norm))
+            _take_over(layer.self_attn, _attention_fast(layer.self_attn, config))
     if config.rms_norm:
-        _patch_norm_module(text_model.norm)
+        _take_over(stack.norm, _norm_fast(stack.norm))
     if config.residual_norm:
-        _patch_text_model(text_model, config)
+        _take_over(stack, _text_fast(stack, config))
     model._qwen35_fusion_config = config
     stats["delta_precompute_factors"] = int(config.delta and config.delta_precompute_factors)
     stats["ppu_swiglu_gemv"] = int(config.swiglu and config.ppu_swiglu_gemv)

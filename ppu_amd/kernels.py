@@ -15,11 +15,44 @@ their own decomposition.
 
 from __future__ import annotations
 
+import functools
+import itertools
+
 import torch
 
 from . import _lib
 
 _BF16 = torch.bfloat16
+
+
+
+def _device_checked(fn):
+    """Validate the device of every tensor argument before the wrapper runs.
+
+    Each tensor an operator receives reaches a kernel as a raw address, so all
+    of them (inputs, weights, states, ``out``/``advance`` targets, positions)
+    must be GPU tensors on one device; a CPU tensor would otherwise become a
+    host address inside a kernel. Raises ``ValueError`` before any launch.
+    """
+
+    code = fn.__code__
+    names = code.co_varnames[: code.co_argcount + code.co_kwonlyargcount]
+
+    @functools.wraps(fn)
+    def checked(*args, **kwargs):
+        device = None
+        for name, value in itertools.chain(zip(names, args), kwargs.items()):
+            if not isinstance(value, torch.Tensor):
+                continue
+            if not value.is_cuda:
+                raise ValueError(f"fused kernels require GPU tensors: {name} is on {value.device}")
+            if device is None:
+                device = value.device
+            elif value.device != device:
+                raise ValueError(f"{name} is on {value.device}, the other operands on {device}")
+        return fn(*args, **kwargs)
+
+    return checked
 
 
 def _rows_and_width(x: torch.Tensor) -> tuple[int, int]:
@@ -51,6 +84,7 @@ def _stream(x: torch.Tensor) -> int:
 
 
 # ------------------------------------------------------------------ norms
+@_device_checked
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """Qwen3.5 RMSNorm ``(1 + w)``: fp32 reduction, bf16 output. reference kernels.py:44."""
 
@@ -65,6 +99,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
     return out
 
 
+@_device_checked
 def residual_add_rms_norm(
     residual: torch.Tensor,
     update: torch.Tensor,
@@ -90,6 +125,7 @@ def residual_add_rms_norm(
     return residual_out, norm_out
 
 
+@_device_checked
 def gated_rms_norm(
     x: torch.Tensor,
     gate: torch.Tensor,
@@ -113,6 +149,7 @@ def gated_rms_norm(
     return out
 
 
+@_device_checked
 def gated_rms_norm_packed(
     x: torch.Tensor,
     packed: torch.Tensor,
@@ -146,6 +183,7 @@ def gated_rms_norm_packed(
     return out
 
 
+@_device_checked
 def silu_and_mul(packed: torch.Tensor) -> torch.Tensor:
     """SiLU of the first half times the second half. reference kernels.py:170."""
 
@@ -159,6 +197,7 @@ def silu_and_mul(packed: torch.Tensor) -> torch.Tensor:
     return out
 
 
+@_device_checked
 def attention_gate_mul(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int) -> torch.Tensor:
     """Multiply attention output by the gate inside the packed QGKV. reference kernels.py:312."""
 
@@ -201,6 +240,7 @@ def _gemv_weight(weight: torch.Tensor, weight_scale: torch.Tensor | None):
     return weight, None
 
 
+@_device_checked
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """Decode ``F.linear(x, W)`` for one token (bf16, fp32 accumulate).
 
@@ -224,6 +264,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+@_device_checked
 def residual_norm_linear(
     residual: torch.Tensor,
     update: torch.Tensor,
@@ -267,6 +308,7 @@ def residual_norm_linear(
     return r_out, out
 
 
+@_device_checked
 def norm_linear(
     x: torch.Tensor,
     norm_weight: torch.Tensor,
@@ -296,6 +338,7 @@ def norm_linear(
     return out
 
 
+@_device_checked
 def norm_linear_conv(
     residual: torch.Tensor,
     update: torch.Tensor | None,
@@ -362,6 +405,7 @@ def norm_linear_conv(
     return r_out, packed, qkv
 
 
+@_device_checked
 def gated_norm_linear(
     core: torch.Tensor,
     gate: torch.Tensor,
@@ -396,6 +440,7 @@ def gated_norm_linear(
     return out
 
 
+@_device_checked
 def prefill_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``F.linear(x, W)`` for M > 1 tokens (prefill), bf16 in/out, fp32 accumulate.
 
@@ -410,6 +455,7 @@ def prefill_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(x, weight)
 
 
+@_device_checked
 def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False) -> torch.Tensor:
     """The hand-written matrix-core prefill GEMM: ``F.linear(x, W)`` (bf16 in
     and out, fp32 accumulate) or, with ``swiglu``, ``silu_and_mul(F.linear(x,
@@ -439,6 +485,7 @@ def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False) ->
     return y
 
 
+@_device_checked
 def ppu_swiglu_gemv(
     x: torch.Tensor,
     packed_weight: torch.Tensor,
@@ -467,6 +514,7 @@ def ppu_swiglu_gemv(
     return out
 
 
+@_device_checked
 def lm_head_argmax(
     hidden: torch.Tensor,
     weight: torch.Tensor,
@@ -512,6 +560,7 @@ def lm_head_argmax(
 
 
 # ------------------------------------------------------------------ DeltaNet
+@_device_checked
 def causal_conv1d_fused(x: torch.Tensor, weight: torch.Tensor, state: torch.Tensor) -> torch.Tensor:
     """Causal depthwise conv + SiLU, ``state`` updated in place. reference kernels.py:659."""
 
@@ -542,6 +591,7 @@ def _delta_params(a_log: torch.Tensor, dt_bias: torch.Tensor) -> tuple[torch.Ten
     return a_log.float().contiguous(), dt_bias.float().contiguous(), 1
 
 
+@_device_checked
 def delta_recurrent_fused(
     qkv: torch.Tensor,
     packed_projection: torch.Tensor,
@@ -594,6 +644,7 @@ def delta_recurrent_fused(
     return out
 
 
+@_device_checked
 def delta_prefill_gated(
     qkv: torch.Tensor,
     packed_projection: torch.Tensor,
@@ -641,6 +692,7 @@ def delta_prefill_gated(
     return y
 
 
+@_device_checked
 def delta_decode_fused(
     packed_projection: torch.Tensor,
     conv_weight: torch.Tensor,
@@ -655,10 +707,25 @@ def delta_decode_fused(
     rule and gated RMSNorm (reference kernels.py:659, :854 and :139 as chained
     by integration.py:254-271). Returns the gated core ``[B*H, D]`` bf16."""
 
+    if packed_projection.ndim != 3 or state.ndim != 4 or conv_weight.ndim != 2 or conv_state.ndim != 3:
+        raise ValueError("expected packed[B,1,W], conv_weight[C,K], conv_state[B,C,K], state[B,H,D,D]")
+    for name, t in (("packed_projection", packed_projection), ("conv_weight", conv_weight),
+                    ("conv_state", conv_state), ("state", state)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
     batch, seq_len, packed_width = packed_projection.shape
-    _, heads, dim, _ = state.shape
+    _, heads, dim, value_dim = state.shape
     if seq_len != 1:
         raise ValueError("fused DeltaNet decode takes one token")
+    if state.shape[0] != batch or dim != value_dim or dim != 128 or state.dtype != torch.float32:
+        raise ValueError("delta state must be float32 [B, H, 128, 128]")
+    channels, kernel_size = conv_weight.shape
+    if channels != 3 * heads * dim or conv_state.shape != (batch, channels, kernel_size):
+        raise ValueError("conv weight/state do not match the 3*H*D convolved channels")
+    if packed_width < channels + heads * dim + 2 * heads:
+        raise ValueError("packed projection does not hold [qkv | z | a | b]")
+    if norm_weight.numel() != dim or a_log.numel() != heads or dt_bias.numel() != heads:
+        raise ValueError("norm weight, A_log and dt_bias do not match the heads")
     _need_bf16(packed_projection, conv_weight, conv_state)
     al, dt, pf = _delta_params(a_log, dt_bias)
     nw, nwf = _param(norm_weight)
@@ -672,6 +739,7 @@ def delta_decode_fused(
 
 
 # ------------------------------------------------------------------ attention
+@_device_checked
 def qgkv_norm_rope(
     packed_qgkv: torch.Tensor,
     q_weight: torch.Tensor,
@@ -758,6 +826,7 @@ def _check_decode_attention(q, cache_keys, cache_values):
     _need_bf16(q, cache_keys, cache_values)
 
 
+@_device_checked
 def gqa_decode_attention(
     q: torch.Tensor,
     cache_keys: torch.Tensor,
@@ -796,6 +865,7 @@ def gqa_decode_attention(
     return out
 
 
+@_device_checked
 def gqa_decode_fused(
     packed_qgkv: torch.Tensor,
     q_weight: torch.Tensor,
@@ -854,6 +924,7 @@ def gqa_decode_fused(
     return out
 
 
+@_device_checked
 def gqa_prefill_attention(
     q: torch.Tensor,
     keys: torch.Tensor,
@@ -904,6 +975,7 @@ def gqa_prefill_attention(
 _A8W8_GEMV_MAX_M = 16
 
 
+@_device_checked
 def quantize_weight_i8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-output-channel symmetric int8 weights and fp32 ``[N,1]`` scales.
     reference explore_runtime_quantization.py:142-155."""
@@ -919,6 +991,7 @@ def quantize_weight_i8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor
     return wq, scale
 
 
+@_device_checked
 def quantize_act_i8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-token dynamic symmetric int8 activations and fp32 ``[M,1]`` scales
     (the scaled_int8_quant call of reference explore_runtime_quantization.py:167-172)."""
@@ -932,6 +1005,7 @@ def quantize_act_i8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return xq, scale
 
 
+@_device_checked
 def a8w8_linear(
     x: torch.Tensor,
     weight_q: torch.Tensor,
@@ -985,6 +1059,7 @@ def a8w8_linear(
     return (y, *extra)
 
 
+@_device_checked
 def a8w8_swiglu(x: torch.Tensor, weight_q: torch.Tensor, weight_scale: torch.Tensor) -> torch.Tensor:
     """``silu_and_mul(a8w8_linear(x, Wq, s_w))`` for a packed ``[gate; up]``
     int8 weight (reference integration.py:183-185 with PPUA8W8Linear,
@@ -1039,6 +1114,7 @@ def zero_tensors(tensors) -> None:
               n, _stream(fused[0]))
 
 
+@_device_checked
 def stream_read(buf: torch.Tensor) -> torch.Tensor:
     """Read every byte of a contiguous GPU tensor once with the GEMV weight
     stream's loads (one workgroup per CU) and return one int32 XOR word per
@@ -1077,6 +1153,7 @@ position_embed_add = _vision_out_of_scope("position_embed_add")
 vision_qkv_rope = _vision_out_of_scope("vision_qkv_rope")
 
 
+@_device_checked
 def sigmoid_mul(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
     """``x * bf16(sigmoid(gate))`` (reference kernels.py:266-282; unused by the
     reference integration). Expressed through the attention-gate kernel with a

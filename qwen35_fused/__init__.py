@@ -5,6 +5,7 @@
 (reference qwen35_fused/__init__.py:1-40, evaluation_wrapper.py:115-117,317-318).
 """
 
+from ppu_amd.integration import precompute_vision_kwargs  # noqa: F401
 from ppu_amd.kernels import (  # noqa: F401
     attention_gate_mul,
     causal_conv1d_fused,
@@ -39,4 +40,5 @@ __all__ = [
     "sigmoid_mul",
     "silu_and_mul",
     "vision_qkv_rope",
+    "precompute_vision_kwargs",
 ]

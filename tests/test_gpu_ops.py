@@ -314,6 +314,51 @@ def test_config4_delta_64_steps(gpu):
     assert worst < 1e-3
 
 
+def test_config4_delta_64_steps_production_chain(gpu):
+    """BASELINE config 4 through the kernels the model's decode step runs: the
+    single-token conv update (``causal_conv1d_fused``, L = 1) then the
+    256-wave delta step (``delta_recurrent_fused``, L = 1) and the packed gated
+    norm, 64 sequential tokens. Each step's core output within the bf16
+    tolerance of the oracle's, and the recurrent state within 1e-3 relative
+    (max-abs over max-abs, and L2) after every step, not only the last."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 23)
+    heads, dim = 16, 128
+    conv_dim = 3 * heads * dim
+    packed_w = 8320
+    conv_w = randn(g, conv_dim, 4, scale=0.02)
+    a_log = torch.zeros(heads, dtype=BF)
+    dt_bias = torch.zeros(heads, dtype=BF)
+    norm_w = randn(g, dim, scale=0.02, mean=1.0)
+    state = torch.randn(1, heads, dim, dim, generator=g) * 0.1
+    conv_state = torch.zeros(1, conv_dim, 4, dtype=BF)
+    st_ref, cs_ref = state.clone(), conv_state.clone()
+    st_gpu, cs_gpu = state.to(gpu), conv_state.to(gpu)
+    conv_w_gpu, a_gpu, dt_gpu, nw_gpu = conv_w.to(gpu), a_log.to(gpu), dt_bias.to(gpu), norm_w.to(gpu)
+    worst_max = worst_l2 = 0.0
+    for step in range(64):
+        packed = randn(g, 1, 1, packed_w)
+        qkv = ref.causal_conv1d(packed, conv_w, cs_ref)
+        core = ref.delta_recurrent(qkv, packed, a_log, dt_bias, st_ref)
+        z = packed[..., conv_dim : conv_dim + heads * dim].reshape(-1, dim)
+        exp = ref.gated_rms_norm(core.reshape(-1, dim), z, norm_w)
+        pg = packed.to(gpu)
+        qkv_g = K.causal_conv1d_fused(pg, conv_w_gpu, cs_gpu)
+        core_g = K.delta_recurrent_fused(qkv_g, pg, a_gpu, dt_gpu, st_gpu)
+        close(qkv_g, qkv)
+        close(core_g, core)
+        got = K.gated_rms_norm_packed(core_g.reshape(-1, dim), pg, conv_dim, heads, nw_gpu, 1e-6)
+        close(got, exp)
+        d = st_gpu.cpu() - st_ref
+        worst_max = max(worst_max, float(d.abs().max() / st_ref.abs().max()))
+        worst_l2 = max(worst_l2, float(d.norm() / st_ref.norm()))
+    print(f"state after 64 steps: worst max-abs rel {worst_max:.2e}, worst L2 rel {worst_l2:.2e}")
+    assert torch.equal(cs_gpu.cpu(), cs_ref)
+    torch.testing.assert_close(st_gpu.cpu(), st_ref, rtol=1e-3, atol=1e-5)
+    assert worst_max < 1e-3 and worst_l2 < 1e-3
+
+
 def test_delta_invariant_beta0_alpha1(gpu):
     """With beta = 0 (b -> -inf) and alpha = 1 (A_log -> -inf) the state is unchanged."""
     from ppu_amd import kernels as K

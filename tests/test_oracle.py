@@ -261,6 +261,25 @@ def test_rotary_table_matches_transformers():
     assert torch.equal(cos, cos_tf) and torch.equal(sin, sin_tf)
 
 
+def test_multimodal_rotary_table_matches_transformers():
+    """Distinct temporal / height / width rows (an image's 2-D positions):
+    the interleaved mrope row choice must match Transformers bit for bit, and
+    a plan that ignores the rows (text table of row 0) must not."""
+    from ppu_amd import synth
+
+    m = tf_impl()
+    cfg = synth.config_tiny()
+    rot = m.Qwen3_5TextRotaryEmbedding(cfg)
+    g = gen(KERNEL_SEED + 21)
+    pos = torch.randint(0, 5000, (3, 1, 40), generator=g)
+    x = torch.zeros(1, 40, 8, dtype=BF)
+    cos_tf, sin_tf = rot(x, pos)
+    cos, sin = ref.rotary_cos_sin(pos, 64, 1e7, (11, 11, 10))
+    assert torch.equal(cos, cos_tf) and torch.equal(sin, sin_tf)
+    cos0, _ = ref.rotary_cos_sin(pos[0], 64, 1e7)
+    assert not torch.equal(cos0, cos_tf)
+
+
 # ---------------------------------------------------------------- attention
 def test_decode_attention_matches_sdpa_and_split_invariance():
     g = gen(KERNEL_SEED + 13)
