@@ -122,43 +122,69 @@ def _stack_rows(parts: list[torch.Tensor], multiple: int) -> torch.Tensor:
 
 
 def _free_linears(*linears: torch.nn.Module) -> int:
-    """Drop the original projection weights; returns the bytes given back."""
+    """Drop the original projection weights; returns the bytes given back
+    (weights never materialised, on the meta device, count as zero)."""
     freed = 0
     for lin in linears:
-        freed += lin.weight.numel() * lin.weight.element_size()
+        if lin.weight is not None and not lin.weight.is_meta:
+            freed += lin.weight.numel() * lin.weight.element_size()
         lin.weight = None
     return freed
 
 
-def _pack_layer(layer: torch.nn.Module, config: FusionConfig, stats: dict[str, int]) -> None:
-    int8 = config.a8w8
-    free = config.release_original_weights
+def layer_projections(layer: torch.nn.Module, config: FusionConfig) -> dict[str, torch.Tensor]:
+    """The packed projection weights of one decoder layer, from its modules
+    (reference integration.py:69-140): ``in`` = DeltaNet ``[qkv | z | a | b]``
+    zero-padded to a multiple of ``delta_projection_padding`` rows, ``out``;
+    ``qgkv`` = attention ``[q (+gate); k; v]``, ``o``; ``gate_up`` = MLP
+    ``[gate; up]``, ``down``."""
+    out: dict[str, torch.Tensor] = {}
     if hasattr(layer, "linear_attn") and config.delta:
         m = layer.linear_attn
-        projections = (m.in_proj_qkv, m.in_proj_z, m.in_proj_a, m.in_proj_b)
-        m.q35_in = _Weight(_stack_rows([p.weight for p in projections],
-                                       config.delta_projection_padding), int8)
-        m.q35_out = _Weight(m.out_proj.weight, int8)
+        parts = [m.in_proj_qkv.weight, m.in_proj_z.weight, m.in_proj_a.weight, m.in_proj_b.weight]
+        out["in"] = _stack_rows(parts, config.delta_projection_padding)
+        out["out"] = m.out_proj.weight.detach()
+    if config.swiglu:
+        out["gate_up"] = _stack_rows([layer.mlp.gate_proj.weight, layer.mlp.up_proj.weight], 0)
+        out["down"] = layer.mlp.down_proj.weight.detach()
+    if hasattr(layer, "self_attn") and config.attention:
+        a = layer.self_attn
+        if any(p.bias is not None for p in (a.q_proj, a.k_proj, a.v_proj)):
+            raise ValueError("the MI355X path supports bias-free Qwen3.5 attention projections only")
+        out["qgkv"] = _stack_rows([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0)
+        out["o"] = a.o_proj.weight.detach()
+    return out
+
+
+def attach_layer(layer: torch.nn.Module, config: FusionConfig, stats: dict[str, int],
+                 packed: dict[str, torch.Tensor]) -> None:
+    """Give one layer its packed weights (``layer_projections`` layout; A8W8
+    quantises them here) and, with ``release_original_weights``, drop the
+    original projection weights."""
+    int8 = config.a8w8
+    free = config.release_original_weights
+    if "in" in packed:
+        m = layer.linear_attn
+        m.q35_in = _Weight(packed["in"], int8)
+        m.q35_out = _Weight(packed["out"], int8)
         m.q35_conv_w = m.conv1d.weight.detach().reshape(m.conv_dim, -1).contiguous()
         if free:
-            stats["released_weight_bytes"] += _free_linears(*projections)
+            stats["released_weight_bytes"] += _free_linears(m.in_proj_qkv, m.in_proj_z,
+                                                            m.in_proj_a, m.in_proj_b)
         stats["delta"] += 1
-    if config.swiglu:
+    if "gate_up" in packed:
         mlp = layer.mlp
-        mlp.q35_gate_up = _Weight(_stack_rows([mlp.gate_proj.weight, mlp.up_proj.weight], 0), int8)
-        mlp.q35_down = _Weight(mlp.down_proj.weight, int8)
+        mlp.q35_gate_up = _Weight(packed["gate_up"], int8)
+        mlp.q35_down = _Weight(packed["down"], int8)
         if free:
             stats["released_weight_bytes"] += _free_linears(mlp.gate_proj, mlp.up_proj)
         stats["mlp"] += 1
-    if hasattr(layer, "self_attn") and config.attention:
+    if "qgkv" in packed:
         a = layer.self_attn
-        projections = (a.q_proj, a.k_proj, a.v_proj)
-        if any(p.bias is not None for p in projections):
-            raise ValueError("the MI355X path supports bias-free Qwen3.5 attention projections only")
-        a.q35_qgkv = _Weight(_stack_rows([p.weight for p in projections], 0), int8)
-        a.q35_o = _Weight(a.o_proj.weight, int8)
+        a.q35_qgkv = _Weight(packed["qgkv"], int8)
+        a.q35_o = _Weight(packed["o"], int8)
         if free:
-            stats["released_weight_bytes"] += _free_linears(*projections)
+            stats["released_weight_bytes"] += _free_linears(a.q_proj, a.k_proj, a.v_proj)
         stats["attention"] += 1
 
 
@@ -534,9 +560,20 @@ def apply_fusions(model: torch.nn.Module, config: FusionConfig | None = None) ->
     if model.training:
         raise ValueError("apply_fusions requires model.eval()")
     stack = text_stack(model)
+    return install(model, config, [layer_projections(layer, config) for layer in stack.layers])
+
+
+def install(model: torch.nn.Module, config: FusionConfig,
+            packed: list[dict[str, torch.Tensor]]) -> dict[str, int]:
+    """``apply_fusions`` with the packed weights given (one
+    ``layer_projections``-layout dict per layer), as the checkpoint loader
+    builds them straight from the files."""
+    if model.training:
+        raise ValueError("apply_fusions requires model.eval()")
+    stack = text_stack(model)
     stats = {"delta": 0, "mlp": 0, "attention": 0, "vision": 0, "released_weight_bytes": 0}
-    for layer in stack.layers:
-        _pack_layer(layer, config, stats)
+    for layer, weights in zip(stack.layers, packed):
+        attach_layer(layer, config, stats, weights)
     for layer in stack.layers:
         if config.rms_norm:
             _take_over(layer.input_layernorm, _norm_fast(layer.input_layernorm))

@@ -232,3 +232,25 @@ def test_wrappers_reject_wrong_device_before_launch(gpu):
                              torch.zeros(1, 8, 128, 128, device=gpu),
                              torch.ones(128, device=gpu, dtype=bf), 1e-6)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("a8w8", [False, True])
+def test_checkpoint_loader_generates_like_the_built_model(gpu, tmp_path, a8w8):
+    """A checkpoint written from the seeded model and read back by the
+    loader (packed at load, int8-quantised at load with ``a8w8``) generates
+    the same greedy tokens as the same model built in memory and packed by
+    ``apply_fusions``."""
+    from ppu_amd.checkpoint import load_checkpoint
+    from ppu_amd.generate import FusedGreedyGenerator
+    from ppu_amd.integration import FusionConfig, apply_fusions
+    from tests.test_checkpoint import write_checkpoint
+
+    cfg = synth.config_tiny()
+    built = synth.build_model(cfg, device=gpu)
+    write_checkpoint(built, cfg, tmp_path)
+    apply_fusions(built, FusionConfig(a8w8=a8w8))
+    loaded, _ = load_checkpoint(tmp_path, device=gpu, fusion=FusionConfig(a8w8=a8w8))
+    prompt = synth.prompt_ids(50, cfg.vocab_size, seed=synth.MODEL_SEED + 9).to(gpu)
+    a = FusedGreedyGenerator(built).generate(prompt, max_new_tokens=16).tokens
+    b = FusedGreedyGenerator(loaded).generate(prompt, max_new_tokens=16).tokens
+    assert a == b
