@@ -146,6 +146,18 @@ long long q35_lm_head_top1_workspace(int V, int K);
 int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace,
                      long long workspace_slots, void* out, void* advance, int n_advance,
                      void* stream);
+/* No counterpart in the reference: q35_lm_head_top1 for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same result and arguments minus the
+ * workspace: the candidate keys go to a fixed array in the library's device
+ * memory (65,536 8-byte slots, one copy per GPU, kept until the process
+ * ends). Limit: the K = 2048 path (16-byte aligned W and x) takes any
+ * V < 2^30; other shapes need (V + 3) / 4 slots, so V <= 262,141, and larger
+ * V returns hipErrorInvalidValue before any launch. Allocates nothing. All
+ * calls on one GPU share the array: calls that overlap on one GPU (two
+ * streams at once) race. */
+int q35_lm_head_top1_noalloc(const void* W, const void* x, int V, int K, void* out,
+                             void* advance, int n_advance, void* stream);
 
 /* ---- DeltaNet --------------------------------------------------------- */
 

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I, [_P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _P]),
     "q35_lm_head_top1_workspace": (_L, [_I, _I]),
     "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),
+    "q35_lm_head_top1_noalloc": (_I, [_P, _P, _I, _I, _P, _P, _I, _P]),
     "q35_conv1d_update": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "q35_conv1d_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "q35_delta_decode": (

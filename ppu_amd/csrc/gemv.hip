@@ -26,6 +26,7 @@
 //             workgroup into a candidate array                    [kernels.py:1093-1143]
 //             (lm_head_top1_persist and the generic fallback)
 #include <algorithm>
+#include <mutex>
 
 #include "q35_common.hpp"
 
@@ -625,6 +626,63 @@ static int lm_device_cus() {
   return cus;
 }
 
+// Shared by q35_lm_head_top1 and q35_lm_head_top1_noalloc: the top-1 GEMV
+// writes one candidate key per workgroup to `workspace`, top1_final reduces
+// them. Every slot the final reduction reads is written by the same call, so
+// the workspace needs no clearing.
+int lm_head_top1_launch(const void* W, const void* x, int V, int K, void* workspace,
+                        long long workspace_slots, void* out, void* advance, int n_advance,
+                        hipStream_t stream) {
+  GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, nullptr,
+             (unsigned long long*)workspace, V, K, 0, 0.f, nullptr, nullptr, nullptr, 0, 0,
+             nullptr, 0};
+  long long nc;
+  if (K == 2048 && fast_ok(a, PRO_NONE)) {
+    nc = std::min<long long>((long long)lm_device_cus() * kLmBlocksPerCU, workspace_slots);
+    lm_head_top1_persist<kLmWV, kLmR, 4><<<(unsigned)nc, kLmWV * 64, 0, stream>>>(a);
+  } else {
+    nc = (V + 3) / 4;
+    gemv_bf16_generic<PRO_NONE, EPI_TOP1><<<(unsigned)nc, 256, 0, stream>>>(a);
+  }
+  const int e = q35_last_error();
+  if (e) return e;
+  top1_final<<<1, 1024, 0, stream>>>((const unsigned long long*)workspace, (int)nc, (long long*)out,
+                                     (long long*)advance, advance ? n_advance : 0);
+  return q35_last_error();
+}
+
+// Scratch of q35_lm_head_top1_noalloc: the candidate keys of one top-1 call
+// (512 slots for the persistent 2-workgroups-per-CU grid; the one-key-per-4-
+// rows fallback grid needs (V + 3) / 4). It lives in the library's device
+// memory, one copy per GPU the library runs on, held until the process ends.
+// All calls on one GPU share it, so calls that overlap on one GPU race.
+constexpr long long kTop1ScratchSlots = 65536;  // 512 KiB
+}  // namespace
+static __device__ __align__(256) unsigned long long scratch[kTop1ScratchSlots];
+namespace {
+
+// Device address of this GPU's copy of `scratch`, resolved once per
+// device with that device current (the array's name is only a host-side
+// stand-in; kernels must receive this address).
+int top1_scratch(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -771,22 +829,26 @@ int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace
   Q35_CHECK_ARG(!advance || (n_advance >= 0 && n_advance <= 64));
   Q35_CHECK_ARG(V > 0 && K > 0 && W && x && workspace && out);
   Q35_CHECK_ARG(workspace_slots >= q35_lm_head_top1_workspace(V, K) && V < (1 << 30));
-  GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, nullptr,
-             (unsigned long long*)workspace, V, K, 0, 0.f, nullptr, nullptr, nullptr, 0, 0,
-             nullptr, 0};
-  long long nc;
-  if (K == 2048 && fast_ok(a, PRO_NONE)) {
-    nc = std::min<long long>((long long)lm_device_cus() * kLmBlocksPerCU, workspace_slots);
-    lm_head_top1_persist<kLmWV, kLmR, 4><<<(unsigned)nc, kLmWV * 64, 0, stream>>>(a);
-  } else {
-    nc = (V + 3) / 4;
-    gemv_bf16_generic<PRO_NONE, EPI_TOP1><<<(unsigned)nc, 256, 0, stream>>>(a);
-  }
-  const int e = q35_last_error();
+  return lm_head_top1_launch(W, x, V, K, workspace, workspace_slots, out, advance, n_advance,
+                             stream);
+}
+
+// q35_lm_head_top1 without a workspace argument: the candidate keys go to
+// this library's `scratch` array on the current device (see top1_scratch).
+int q35_lm_head_top1_noalloc(const void* W, const void* x, int V, int K, void* out, void* advance,
+                             int n_advance, hipStream_t stream) {
+  Q35_CHECK_ARG(!advance || (n_advance >= 0 && n_advance <= 64));
+  Q35_CHECK_ARG(V > 0 && K > 0 && W && x && out && V < (1 << 30));
+  GemvArgs probe{(const uint16_t*)W, (const uint16_t*)x};
+  const long long need = (K == 2048 && fast_ok(probe, PRO_NONE))
+                             ? (long long)lm_device_cus() * kLmBlocksPerCU
+                             : (long long)(V + 3) / 4;
+  if (need > kTop1ScratchSlots) return (int)hipErrorInvalidValue;  // beyond the scratch array
+  void* scratch = nullptr;
+  const int e = top1_scratch(&scratch);
   if (e) return e;
-  top1_final<<<1, 1024, 0, stream>>>((const unsigned long long*)workspace, (int)nc, (long long*)out,
-                                     (long long*)advance, advance ? n_advance : 0);
-  return q35_last_error();
+  return lm_head_top1_launch(W, x, V, K, scratch, kTop1ScratchSlots, out, advance, n_advance,
+                             stream);
 }
 
 }  // extern "C"
