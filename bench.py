@@ -175,20 +175,38 @@ def swiglu_roofline(model, variant: str) -> dict:
 
 def step_bytes(model, context: float) -> int:
     """HBM bytes one decode token needs: every packed weight (and int8 scale)
-    once, the lm_head (tied embedding) once, the small per-layer parameters,
+    once, the lm_head (tied embedding) once, the small per-layer parameters
+    the decode kernels read (norm weights, conv taps, ``A_log``, ``dt_bias``),
     the embedding row, the recurrent and conv states read and written, and
-    the K/V cache read over ``context`` positions plus the new row written."""
+    the K/V cache read over ``context`` positions plus the new row written.
+    Each storage is counted once (a bf16 packed weight may share the storage
+    of the original parameter); nn.Linear weights are read only through their
+    packed form."""
+    import torch
+
     from ppu_amd.integration import _Weight, text_stack
 
     stack = text_stack(model)
+    seen: set[int] = set()
     total = 0
+
+    def add(t):
+        nonlocal total
+        if t is not None and t.data_ptr() not in seen:
+            seen.add(t.data_ptr())
+            total += t.numel() * t.element_size()
+
     for m in model.modules():
         if isinstance(m, _Weight):
-            total += m.w.numel() * m.w.element_size() + (0 if m.s is None else m.s.numel() * 4)
-    total += model.lm_head.weight.numel() * 2 + stack.config.hidden_size * 2
-    for name, p in stack.named_parameters():
-        if p is not None and "embed_tokens" not in name:
-            total += p.numel() * p.element_size()  # norms, conv taps, A_log, dt_bias
+            add(m.w)
+            add(m.s)
+    add(model.lm_head.weight)
+    total += stack.config.hidden_size * 2  # the embedding row of the token
+    for mod in stack.modules():
+        if isinstance(mod, torch.nn.Linear) or mod is stack.embed_tokens:
+            continue
+        for p in mod.parameters(recurse=False):
+            add(p)
     for layer in stack.layers:
         if hasattr(layer, "linear_attn"):
             m = layer.linear_attn

@@ -456,13 +456,14 @@ def prefill_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 
 
 @_device_checked
-def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False) -> torch.Tensor:
+def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
+              plan: tuple[int, int] | None = None) -> torch.Tensor:
     """The hand-written matrix-core prefill GEMM: ``F.linear(x, W)`` (bf16 in
     and out, fp32 accumulate) or, with ``swiglu``, ``silu_and_mul(F.linear(x,
     W))`` for a packed ``[gate; up]`` weight in one launch (reference
     integration.py:183-185, kernels.py:158-180). K must be a multiple of 128.
-    ``prefill_linear`` uses the ROCm library GEMM instead, which measured
-    faster at the model's prefill shapes."""
+    ``plan`` = (tile shape 0-3, K splits) overrides the library's choice (for
+    measurement)."""
 
     k = x.shape[-1]
     if weight.ndim != 2 or weight.shape[1] != k:
@@ -471,7 +472,7 @@ def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False) ->
         raise ValueError("the matrix-core GEMM needs K to be a multiple of 128")
     if swiglu and weight.shape[0] % 2:
         raise ValueError("packed SwiGLU weight must have an even number of rows")
-    if not x.is_cuda or not weight.is_contiguous():
+    if not weight.is_contiguous():
         raise ValueError("GEMM tensors must be contiguous GPU tensors")
     _need_bf16(x, weight)
     x2 = x.reshape(-1, k).contiguous()
@@ -480,8 +481,21 @@ def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False) ->
     y = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_BF16)
     if m == 0:
         return y
-    name = "q35_gemm_swiglu_bf16" if swiglu else "q35_gemm_bf16"
-    _lib.call(name, x2.data_ptr(), weight.data_ptr(), y.data_ptr(), m, n, k, _stream(x))
+    lib = _lib.load()
+    if plan is None:
+        nbytes = lib.q35_gemm_workspace(m, n, k, int(swiglu))
+    else:
+        nbytes = lib.q35_gemm_plan_workspace(m, n, plan[0], plan[1], int(swiglu))
+        if nbytes < 0:
+            raise ValueError(f"invalid GEMM plan {plan}")
+    ws = torch.empty(nbytes // 4, device=x.device, dtype=torch.float32) if nbytes > 0 else None
+    if plan is None:
+        name = "q35_gemm_swiglu_bf16" if swiglu else "q35_gemm_bf16"
+        _lib.call(name, x2.data_ptr(), weight.data_ptr(), y.data_ptr(), m, n, k, _lib.ptr(ws),
+                  nbytes, _stream(x))
+    else:
+        _lib.call("q35_gemm_bf16_plan", x2.data_ptr(), weight.data_ptr(), y.data_ptr(), m, n, k,
+                  plan[0], plan[1], int(swiglu), _lib.ptr(ws), nbytes, _stream(x))
     return y
 
 
@@ -1016,8 +1030,9 @@ def a8w8_linear(
 ):
     """A8W8 linear: per-token int8 quantisation of ``x``, int32 dot products
     against per-channel int8 weights, bf16 dequantised output
-    (reference explore_runtime_quantization.py:161-181). For one token the
-    quantisation is fused into the GEMV launch."""
+    (reference explore_runtime_quantization.py:161-181). Up to 16 tokens run
+    on the int8 GEMV (for one token with the quantisation fused into the
+    launch); prefill on the ROCm library's int8 GEMM and the dequant kernel."""
 
     k = x.shape[-1]
     if weight_q.ndim != 2 or weight_q.shape[1] != k or weight_q.dtype != torch.int8:
@@ -1036,8 +1051,11 @@ def a8w8_linear(
     sx = torch.empty((m, 1), device=x.device, dtype=torch.float32)
     y = torch.empty((m, n), device=x.device, dtype=_BF16)
     if m > _A8W8_GEMV_MAX_M and n % 8 == 0 and k % 8 == 0:
-        # Prefill: per-token quantisation (gfx950 kernel), the int8 GEMM on the
+        # Prefill: per-token quantisation (gfx950 kernel), the int8 GEMM of the
         # ROCm library (hipBLASLt, exact int32 accumulators), dequant kernel.
+        # (gemm_a8w8, the hand-written int8 GEMM with the dequant in its
+        # epilogue, gives the same bits but measured 8-75% slower at M = 1024
+        # on the 2B shapes, dequant included.)
         _lib.call("q35_quant_act_i8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), m, k, _stream(x))
         acc = torch._int_mm(xq, weight_q.t())
         _lib.call("q35_dequant_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(), m,
@@ -1086,10 +1104,54 @@ def a8w8_swiglu(x: torch.Tensor, weight_q: torch.Tensor, weight_scale: torch.Ten
     xq = torch.empty((m, k), device=x.device, dtype=torch.int8)
     sx = torch.empty((m, 1), device=x.device, dtype=torch.float32)
     _lib.call("q35_quant_act_i8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), m, k, _stream(x))
-    acc = torch._int_mm(xq, weight_q.t())
     y = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_BF16)
+    acc = torch._int_mm(xq, weight_q.t())
     _lib.call("q35_dequant_swiglu_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(), m,
               n, _stream(x))
+    return y
+
+
+def _gemm_a8w8_into(xq, sx, weight_q, sw, y, *, swiglu, plan) -> None:
+    m, k = xq.shape
+    n = weight_q.shape[0] // 2 if swiglu else weight_q.shape[0]
+    tile, splits = plan if plan is not None else (-1, 1)
+    lib = _lib.load()
+    nbytes = lib.q35_gemm_a8w8_workspace(m, n, k, int(swiglu), tile, splits)
+    if nbytes < 0:
+        raise ValueError(f"invalid GEMM plan {plan}")
+    ws = torch.empty(nbytes // 4, device=xq.device, dtype=torch.float32) if nbytes > 0 else None
+    _lib.call("q35_gemm_a8w8", xq.data_ptr(), sx.data_ptr(), weight_q.data_ptr(), sw.data_ptr(),
+              y.data_ptr(), m, n, k, int(swiglu), tile, splits, _lib.ptr(ws), nbytes, _stream(xq))
+
+
+@_device_checked
+def gemm_a8w8(xq: torch.Tensor, x_scale: torch.Tensor, weight_q: torch.Tensor,
+              weight_scale: torch.Tensor, *, swiglu: bool = False,
+              plan: tuple[int, int] | None = None) -> torch.Tensor:
+    """The int8 matrix-core prefill GEMM on already quantised operands:
+    ``bf16(float(xq . Wq^T) * s_x[m] * s_w[n])`` (exact int32 accumulators,
+    the dequant of reference explore_runtime_quantization.py:173-180), or with
+    ``swiglu`` the SwiGLU of a packed ``[gate; up]`` int8 weight on the
+    dequantised bf16 gate and up. K must be a multiple of 256. ``plan`` =
+    (tile shape 0-3, K splits) overrides the library's choice."""
+
+    if xq.dtype != torch.int8 or weight_q.dtype != torch.int8 or xq.ndim != 2 or weight_q.ndim != 2:
+        raise ValueError("int8 GEMM operands must be int8 [M,K] and [N,K]")
+    m, k = xq.shape
+    if weight_q.shape[1] != k or k % 256:
+        raise ValueError("int8 GEMM needs matching K, a multiple of 256")
+    if swiglu and weight_q.shape[0] % 2:
+        raise ValueError("packed SwiGLU weight must have an even number of rows")
+    if not (xq.is_contiguous() and weight_q.is_contiguous()):
+        raise ValueError("int8 GEMM operands must be contiguous")
+    sx = x_scale.reshape(-1).float().contiguous()
+    sw = weight_scale.reshape(-1).float().contiguous()
+    if sx.numel() != m or sw.numel() != weight_q.shape[0]:
+        raise ValueError("int8 GEMM scales: one per token row and one per weight row")
+    n = weight_q.shape[0] // 2 if swiglu else weight_q.shape[0]
+    y = torch.empty((m, n), device=xq.device, dtype=_BF16)
+    if m:
+        _gemm_a8w8_into(xq, sx, weight_q, sw, y, swiglu=swiglu, plan=plan)
     return y
 
 

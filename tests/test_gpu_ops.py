@@ -577,6 +577,10 @@ def test_a8w8_linear_config2(gpu, m, n, k):
     assert np.array_equal(sx.cpu().numpy(), esx)
     assert np.array_equal(acc.cpu().numpy(), eacc)
     close(y, ey)
+    # the dequant is the oracle's expression on exact accumulators: bit-exact
+    assert torch.equal(y.cpu(), ey)
+    if m > 16 and k % 256 == 0:  # the hand-written int8 GEMM: the same bits
+        assert torch.equal(K.gemm_a8w8(xq, sx, wq, sw).cpu(), ey)
 
 
 @pytest.mark.parametrize("m", [4, 300])
@@ -625,6 +629,98 @@ def test_gemm_bf16(gpu, m, n, k):
     x, w = randn(g, m, k), randn(g, n, k, scale=0.02)
     y = K.gemm_bf16(x.to(gpu), w.to(gpu))
     close(y, (x.float() @ w.float().t()).to(BF))
+
+
+@pytest.mark.parametrize("tile,splits", [(0, 1), (1, 1), (1, 2), (1, 3), (2, 1), (2, 2), (3, 1),
+                                         (3, 4), (1, 6)])
+@pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (300, 700, 1536)])
+def test_gemm_bf16_split_plans(gpu, tile, splits, m, n, k):
+    """Every tile shape with K split over workgroups (the last one to finish a
+    tile sums the partials): the fp32 product within the bf16 bar, ragged
+    tiles included; the same launch twice in a row and three graph replays
+    give identical bits (the arrival counters reset themselves and the split
+    order of the sum is fixed)."""
+    from ppu_amd import kernels as K
+
+    if (k // 64) % (2 * splits):
+        pytest.skip("K / 64 must split into pairs of stages")
+    g = gen(KERNEL_SEED + 92)
+    x, w = randn(g, m, k), randn(g, n, k, scale=0.02)
+    xg, wg = x.to(gpu), w.to(gpu)
+    y1 = K.gemm_bf16(xg, wg, plan=(tile, splits))
+    y2 = K.gemm_bf16(xg, wg, plan=(tile, splits))
+    close(y1, (x.float() @ w.float().t()).to(BF))
+    assert torch.equal(y1, y2)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y3 = K.gemm_bf16(xg, wg, plan=(tile, splits))
+    for _ in range(3):
+        y3.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y3, y1)
+
+
+def _exact_i8_product(xq, wq):
+    """int8 x int8 dot products summed exactly (|sum| < 2^53 in float64)."""
+    return (xq.cpu().double() @ wq.cpu().double().t()).to(torch.int64)
+
+
+@pytest.mark.parametrize("plan", [None, (0, 1), (1, 1), (1, 2), (2, 1), (2, 2), (3, 1), (3, 4)])
+@pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (300, 1000, 2048), (17, 200, 256)])
+def test_gemm_a8w8(gpu, plan, m, n, k):
+    """int8 matrix-core GEMM with the dequant epilogue: bit-exact against the
+    oracle's dequant of the exact integer product, for every tile shape and
+    K split (ragged tiles included); repeated launches and three graph
+    replays give the same bits."""
+    from ppu_amd import kernels as K
+
+    if plan is not None and (k // 128) % (2 * plan[1]):
+        pytest.skip("K / 128 must split into pairs of stages")
+    g = gen(KERNEL_SEED + 93)
+    w, x = randn(g, n, k, scale=0.02), randn(g, m, k)
+    x[m // 2] = 0  # a zero row: scale 0, output 0
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    xq, sx = K.quantize_act_i8(x.to(gpu))
+    y1 = K.gemm_a8w8(xq, sx, wq, sw, plan=plan)
+    y2 = K.gemm_a8w8(xq, sx, wq, sw, plan=plan)
+    acc = _exact_i8_product(xq, wq)
+    assert int(acc.abs().max()) < 2**31
+    exp = oa.dequant(acc.numpy().astype(np.int32), sx.cpu().numpy(), sw.cpu().numpy())
+    assert torch.equal(y1.cpu(), exp)
+    assert torch.equal(y1, y2)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y3 = K.gemm_a8w8(xq, sx, wq, sw, plan=plan)
+    for _ in range(3):
+        y3.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y3, y1)
+
+
+@pytest.mark.parametrize("plan", [None, (0, 1), (2, 1), (3, 1)])
+@pytest.mark.parametrize("m,n,k", [(1024, 6144, 2048), (200, 504, 2048)])
+def test_gemm_a8w8_swiglu(gpu, plan, m, n, k):
+    """Packed gate/up int8 GEMM with dequant + SwiGLU in the epilogue: the same
+    bits as the exact integer product put through q35_dequant_swiglu_i32 (the
+    separate dequant + SwiGLU kernel), which a8w8_swiglu runs for prefill."""
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 94)
+    w, x = randn(g, 2 * n, k, scale=0.02), randn(g, m, k)
+    wq, sw = K.quantize_weight_i8(w.to(gpu))
+    xq, sx = K.quantize_act_i8(x.to(gpu))
+    y = K.gemm_a8w8(xq, sx, wq, sw, swiglu=True, plan=plan)
+    acc = _exact_i8_product(xq, wq).to(torch.int32).to(gpu)
+    exp = torch.empty((m, n), device=gpu, dtype=BF)
+    _lib.call("q35_dequant_swiglu_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(),
+              exp.data_ptr(), m, n, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(y, exp)
+    if plan is None:
+        assert torch.equal(K.a8w8_swiglu(x.to(gpu), wq, sw), exp)
 
 
 @pytest.mark.parametrize("m,n,k", [(1024, 6144, 2048), (200, 500, 2048)])
@@ -695,6 +791,10 @@ def test_a8w8_prequantised_abi(gpu, m, n, k):
     torch.cuda.synchronize()
     assert np.array_equal(acc.cpu().numpy(), eacc)
     close(y, ey)
+    # the dequant is the oracle's expression on exact accumulators: bit-exact
+    assert torch.equal(y.cpu(), ey)
+    if m > 16 and k % 256 == 0:  # the hand-written int8 GEMM: the same bits
+        assert torch.equal(K.gemm_a8w8(xq, sx, wq, sw).cpu(), ey)
 
 
 def _i8_row(prologue, x, u, nw):
