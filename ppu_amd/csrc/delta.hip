@@ -211,6 +211,12 @@ __global__ __launch_bounds__(256) void delta_decode(const DeltaArgs p) {
 // bits 1..5), so the kernel has no barrier and no LDS. Each wave recomputes
 // the head's norm factors and gates (q, k are 512 bytes from L2); the state
 // is read once and written once.
+// Tile placement: four tiles share each 128-byte line of a state row, and
+// workgroups are dispatched to the 8 XCDs (each with its own L2) round-robin
+// by linear id, so with tile = id % 16 every line was fetched by four L2s
+// (FETCH_SIZE 2.6x the state). When B*H is a multiple of 8 the 16 tiles of
+// a head are given ids of one residue mod 8 (one XCD): id = xcd + 8*slot,
+// head = xcd + 8*(slot / 16), tile = slot % 16.
 constexpr int kWT = 8;  // v columns per wave
 
 Q35_DEV float4 xor_sum_rows(float4 v) {
@@ -227,9 +233,17 @@ Q35_DEV float4 xor_sum_rows(float4 v) {
 template <bool PF32>  // gate parameters (A_log, dt_bias) fp32, else bf16
 __global__ __launch_bounds__(64) void delta_decode_wave(const DeltaArgs p) {
   const int lane = threadIdx.x;
-  const int tiles = kD / kWT;
-  const int tile = blockIdx.x % tiles;
-  const int bh = blockIdx.x / tiles;
+  constexpr int tiles = kD / kWT;
+  const int id = blockIdx.x;
+  int tile, bh;
+  if ((gridDim.x / tiles) % 8 == 0) {
+    const int slot = id >> 3;
+    tile = slot % tiles;
+    bh = (id & 7) + 8 * (slot / tiles);
+  } else {
+    tile = id % tiles;
+    bh = id / tiles;
+  }
   const int b = bh / p.H, h = bh - b * p.H;
   const int rg = lane >> 1, cq = lane & 1;
   const int c0 = tile * kWT + 4 * cq;

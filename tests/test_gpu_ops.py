@@ -1018,9 +1018,10 @@ def test_gated_norm_linear(gpu):
     close(got, exp)
 
 
+@pytest.mark.parametrize("cache_len", [1152, 4096])
 @pytest.mark.parametrize("positions", [(777, 777, 777), (100, 57, 33)])
 @pytest.mark.parametrize("n_old", [0, 300, 1151])
-def test_gqa_decode_fused_step(gpu, positions, n_old):
+def test_gqa_decode_fused_step(gpu, positions, n_old, cache_len):
     """Fused attention decode step (Q/K norm + RoPE from device positions, cache
     write, split-K attention incl. the new token, combine, gate, length += 1)
     against the oracle chain qgkv_norm_rope -> cache write -> decode attention
@@ -1031,7 +1032,6 @@ def test_gqa_decode_fused_step(gpu, positions, n_old):
     from ppu_amd import synth
 
     g = gen(KERNEL_SEED + 50)
-    cache_len = 1152
     packed = randn(g, 1, 1, 5120)
     qw, kw = randn(g, 256, scale=0.1), randn(g, 256, scale=0.1)
     kc = randn(g, 1, 2, cache_len, 256)
@@ -1055,6 +1055,49 @@ def test_gqa_decode_fused_step(gpu, positions, n_old):
     close(kg[:, :, n_old], kr[:, :, n_old])
     assert torch.equal(vg[:, :, n_old].cpu(), vr[:, :, n_old])
     assert torch.equal(kg[:, :, :n_old].cpu(), kc[:, :, :n_old])
+
+
+@pytest.mark.parametrize("cache_len", [1152, 4096])
+def test_gqa_decode_fused_graph_replays(gpu, cache_len):
+    """The fused decode step (split kernel + combine) captured in a graph:
+    every replay appends one cache row, advances the length by exactly one
+    and gives the same bits as the same sequence of eager calls on a copy of
+    the cache, with eager work and host syncs between the replays."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding
+
+    from ppu_amd import kernels as K
+    from ppu_amd import synth
+
+    g = gen(KERNEL_SEED + 53)
+    n_old = 700
+    packed = randn(g, 1, 1, 5120).to(gpu)
+    qw, kw = randn(g, 256, scale=0.1).to(gpu), randn(g, 256, scale=0.1).to(gpu)
+    kc = randn(g, 1, 2, cache_len, 256).to(gpu)
+    vc = randn(g, 1, 2, cache_len, 256).to(gpu)
+    rot = Qwen3_5TextRotaryEmbedding(synth.config_tiny())
+    inv = rot.inv_freq.to(gpu)
+    pos = torch.tensor((900, 900, 900), dtype=torch.int64, device=gpu).view(3, 1, 1)
+    ke, ve = kc.clone(), vc.clone()
+    le = torch.tensor(n_old, dtype=torch.int64, device=gpu)
+    eager = [K.gqa_decode_fused(packed, qw, kw, inv, pos, ke, ve, le, 0.0625, q_heads=8)
+             for _ in range(4)]
+    assert int(le) == n_old + 4
+    length = torch.tensor(n_old, dtype=torch.int64, device=gpu)
+    K.gqa_decode_fused(packed, qw, kw, inv, pos, kc.clone(), vc.clone(), length.clone(), 0.0625,
+                       q_heads=8)  # warm the allocator outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = K.gqa_decode_fused(packed, qw, kw, inv, pos, kc, vc, length, 0.0625, q_heads=8)
+    assert int(length) == n_old  # capture ran nothing
+    for r in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(length) == n_old + r + 1
+        assert torch.equal(out, eager[r])
+        K.gqa_decode_attention(packed[..., :2048].reshape(1, 8, 1, 256).contiguous(), ke, ve,
+                               le, 0.0625)  # eager work between the replays
+    assert torch.equal(kc[:, :, : n_old + 4], ke[:, :, : n_old + 4])
 
 
 def test_norm_linear_conv_embedding_gather(gpu):
