@@ -294,6 +294,63 @@ def kernel_table(dev) -> dict:
     return out
 
 
+def gemm_sweep(dev) -> None:
+    """The prefill GEMM shapes of the 2B decoder at M = 1024: the ROCm library
+    (F.linear bf16; torch._int_mm + the dequant kernel for int8) against the
+    hand-written matrix-core GEMMs for every tile plan, each graph-timed over
+    rotating weights (>= 512 MB, so the MALL does not serve them). Prints one
+    table row per (shape, implementation, plan) on stdout."""
+    import torch
+    import torch.nn.functional as F
+
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=dev).manual_seed(1)
+    m = PROMPT_LEN
+    stream = torch.cuda.current_stream().cuda_stream
+    shapes = [(8320, 2048, 18), (2048, 2048, 24), (5120, 2048, 6), (12288, 2048, 24), (2048, 6144, 24)]
+    print("# N x K (per prefill) | implementation | plan (tile, K splits) | us | TFLOP/s (TOP/s)")
+    for n, k, count in shapes:
+        flops = 2 * m * n * k
+        nset = max(2, (512 << 20) // (n * k * 2) + 1)
+        w = [(torch.randn(n, k, device=dev, generator=g) * 0.02).to(torch.bfloat16) for _ in range(nset)]
+        x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+
+        def row(impl, plan, us):
+            print(f"{n} x {k} ({count}) | {impl} | {plan} | {us:.2f} | {flops / us / 1e6:.0f}",
+                  flush=True)
+
+        row("library bf16 (F.linear)", "-", graph_time_us(lambda i: F.linear(x, w[i % nset]), nset, 5))
+        plans = [None, (0, 1), (1, 1), (2, 1), (3, 1), (1, 2), (1, 3)]
+        for plan in plans:
+            if plan and (k // 64) % (2 * plan[1]):
+                continue
+            us = graph_time_us(lambda i: K.gemm_bf16(x, w[i % nset], plan=plan), nset, 5)
+            row("own bf16 (q35_gemm_bf16)", plan or "default plan", us)
+        del w
+        nset8 = max(2, (512 << 20) // (n * k) + 1)
+        wq = [torch.randint(-127, 128, (n, k), device=dev, dtype=torch.int8, generator=g)
+              for _ in range(nset8)]
+        sw = torch.rand(n, device=dev, generator=g) * 1e-3
+        xq, sx = K.quantize_act_i8(x)
+        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+        def lib_i8(i):
+            acc = torch._int_mm(xq, wq[i % nset8].t())
+            _lib.call("q35_dequant_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(),
+                      m, n, stream)
+
+        row("library int8 (_int_mm) + dequant", "-", graph_time_us(lib_i8, nset8, 5))
+        for plan in [None, (0, 1), (1, 1), (2, 1), (1, 2)]:
+            if plan and (k // 128) % (2 * plan[1]):
+                continue
+            us = graph_time_us(lambda i: K.gemm_a8w8(xq, sx, wq[i % nset8], sw, plan=plan), nset8, 5)
+            row("own int8 + fused dequant (q35_gemm_a8w8)", plan or "default plan", us)
+        del wq
+        torch.cuda.empty_cache()
+
+
 def counter_probe(dev) -> None:
     """A short fixed workload for ``rocprofv3 --pmc`` passes (one counter set
     per run), so that per-dispatch counters can be read for:
@@ -533,6 +590,8 @@ def main() -> None:
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     ap.add_argument("--cpu-prompt", type=int, default=PROMPT_LEN, help="prompt length of the CPU sample")
     ap.add_argument("--no-eager", action="store_true", help="skip the Transformers-eager CPU timing")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="prefill GEMM shapes: ROCm library vs the hand-written GEMMs, then exit")
     ap.add_argument("--counter-probe", action="store_true",
                     help="only run the short workload profiled with rocprofv3 --pmc, then exit")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -551,6 +610,9 @@ def main() -> None:
 
     if args.counter_probe:
         counter_probe(torch.device("cuda:0"))
+        return
+    if args.gemm_sweep:
+        gemm_sweep(torch.device("cuda:0"))
         return
 
     from ppu_amd import synth

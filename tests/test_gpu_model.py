@@ -30,7 +30,8 @@ pytestmark = pytest.mark.gpu
 # (tests/test_oracle_model.py). On the 24-layer 2B shape a one-ulp change of the
 # RMSNorm variances moves the hidden state, over 64 steps, by 2.3 % mean /
 # 2.9 % max in bf16 and 8.2 % mean / 10 % max in A8W8, where the per-token int8
-# quantisation turns ulp changes into whole int8 steps (tests/noise_floor.py).
+# quantisation turns ulp changes into whole int8 steps (the perturbation of
+# tests/test_oracle_model.py::_variance_order_noise run once at the 2B shape).
 # The GPU perturbs every reduction, not one: mean bounds are about twice the
 # floor mean, per-step bounds about 2.4x (bf16) and 3x (A8W8) the floor max.
 HIDDEN_BOUNDS = {"tiny": (0.03, 0.03), "2b": (0.05, 0.07), "2b-a8w8": (0.16, 0.30)}

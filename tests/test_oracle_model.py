@@ -126,9 +126,10 @@ def test_a8w8_noise_floor_exceeds_bf16():
     change into whole int8 steps, so the a8w8 path's noise floor is several
     times the bf16 path's; the GPU-vs-oracle bound of each variant is set from
     its own floor. Here (4 layers, 64 tokens) about 0.6 % bf16 and 1.7 % a8w8;
-    on the 24-layer 2B shape with a 1024-token prompt, summing the variances
-    in fp64 instead gives 2.3 % (max 2.9 %) bf16 and 8.2 % (max 10 %) a8w8
-    over 64 steps (tests/noise_floor.py)."""
+    on the 24-layer 2B shape with a 1024-token prompt the same perturbation
+    (this function's, run at that shape once on the host; too slow for the CPU
+    suite) measured 2.3 % (max 2.9 %) bf16 and 8.2 % (max 10 %) a8w8 over 64
+    steps."""
     nb = _variance_order_noise(False)
     nq = _variance_order_noise(True)
     print(f"variance-order noise: bf16 {nb:.4f} a8w8 {nq:.4f}")
