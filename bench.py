@@ -118,6 +118,19 @@ def lm_head_roofline(model) -> dict:
     read_gbs = v * k * 2 / read_us / 1e3
     log(f"lm_head top-1: {us:.1f} us, {achieved:.0f} GB/s; plain read of the same bytes "
         f"{read_us:.1f} us, {read_gbs:.0f} GB/s ({100 * achieved / read_gbs:.1f}% of it)")
+    from ppu_amd.integration import lm_head_screen
+
+    screened = None
+    screen = lm_head_screen(model)
+    if screen is not None:
+        hs = [torch.randn(1, k, device=w.device, dtype=torch.bfloat16) for _ in range(10)]
+        s_us = graph_time_us(lambda i: K.lm_head_argmax(hs[i], w, screen=screen), calls=10, reps=10)
+        same = all(int(K.lm_head_argmax(x, w, screen=screen)) == int(K.lm_head_argmax(x, w))
+                   for x in hs)
+        screened = {"us_per_call": round(s_us, 2), "same_index_as_full": same,
+                    "int8_bytes": v * k + 8 * v,
+                    "speedup_vs_full": round(us / s_us, 3)}
+        log(f"screened lm_head top-1: {s_us:.1f} us ({us / s_us:.2f}x), same index: {same}")
     return {"kernel": "lm_head GEMV + top-1 [248320,2048] bf16", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
@@ -126,7 +139,8 @@ def lm_head_roofline(model) -> dict:
             "workspace_bytes": slots * 8,
             "read_ceiling": {"GB/s": round(read_gbs, 1), "us": round(read_us, 2),
                              "frac_of_peak": round(read_gbs / PEAK_HBM_GBS, 4),
-                             "lm_head_frac_of_ceiling": round(achieved / read_gbs, 4)}}
+                             "lm_head_frac_of_ceiling": round(achieved / read_gbs, 4)},
+            "screened": screened}
 
 
 def swiglu_roofline(model, variant: str) -> dict:

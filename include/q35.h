@@ -158,6 +158,21 @@ int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace
  * streams at once) race. */
 int q35_lm_head_top1_noalloc(const void* W, const void* x, int V, int K, void* out,
                              void* advance, int n_advance, void* stream);
+/* The same index as q35_lm_head_top1 (replaces the same reference call,
+ * qwen35_fused/kernels.py:1146), found with half the weight bytes: an int8
+ * copy of W screens every row with a rigorous bound on the difference to the
+ * row's bf16 logit, and only the rows the bound cannot exclude are recomputed
+ * with q35_lm_head_top1's arithmetic (bit-identical result for any weights;
+ * the number of recomputed rows sets the cost). K = 2048; W, Wq, x and the
+ * workspace 16-byte aligned. q35_lm_head_screen_prep makes Wq [V, K] int8 and
+ * s, c [V] fp32 from W once; workspace of
+ * q35_lm_head_top1_screened_workspace(V, K) bytes. */
+int q35_lm_head_screen_prep(const void* W, int V, int K, void* Wq, void* s, void* c, void* stream);
+long long q35_lm_head_top1_screened_workspace(int V, int K);
+int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, const void* c,
+                              const void* x, int V, int K, void* workspace,
+                              long long workspace_bytes, void* out, void* advance, int n_advance,
+                              void* stream);
 
 /* ---- DeltaNet --------------------------------------------------------- */
 

@@ -651,6 +651,251 @@ int lm_head_top1_launch(const void* W, const void* x, int V, int K, void* worksp
   return q35_last_error();
 }
 
+// ------------------------------------------------ screened exact lm_head top-1
+// The lm_head GEMV reads 1 GB of bf16 weights per token to find one index.
+// The screened form reads an int8 copy of them (half the bytes) and recomputes
+// exactly only the rows that can still be the answer:
+//   screen    Q_r = s_r * sum_i x_i q_ri in fp32, q_r = rint(w_r / s_r), s_r =
+//             absmax_r / 127, and a bound eps_r >= |B_r - Q_r|, where B_r is
+//             the bf16 logit the full kernel computes for row r (its fp32 sum
+//             rounded to bf16). With e_r = w_r - s_r q_r, by Cauchy-Schwarz
+//             |x.w_r - Q_r| <= |x| |e_r| + (fp32 error of the screen), the
+//             full kernel's fp32 sum is within n u |x| |w_r| of x.w_r
+//             (n = 2048 terms, u = 2^-24), and its bf16 rounding moves it by at
+//             most 2^-8 of its magnitude; with c_r = |e_r| (1 + 2^-10) +
+//             2 gamma (|w_r| + |e_r|), gamma = 2.5e-4 (twice n u):
+//             eps_r = |x| c_r (1 + 2^-7) + 2^-7 |Q_r|, every term at least
+//             twice what it covers. U_r = Q_r + eps_r >= B_r >= Q_r - eps_r.
+//   rescore   L* = max_r (Q_r - eps_r) <= max_r B_r, so every row whose B_r is
+//             the maximum has U_r >= L*; only rows with !(U_r < L*) (NaN rows
+//             included) are recomputed, with the full kernel's arithmetic for
+//             a row (same lane layout, fmaf order and wave reduction), and the
+//             usual (value, lowest index) key picks among them. The result is
+//             the full kernel's, bit for bit, whatever the weights; the number
+//             of recomputed rows (a few percent for random N(0, 0.02) weights,
+//             where the screen's bound is about one logit standard deviation)
+//             only sets the cost.
+constexpr float kScreenGamma = 2.5e-4f;
+
+// One wave per row (4 per workgroup), K = 512 * NCH: lane l holds elements
+// c*512 + 8l .. +7. Writes the int8 row (natural k order), s_r and c_r.
+template <int NCH>
+__global__ __launch_bounds__(256) void lm_screen_prep(const uint16_t* __restrict__ W,
+                                                      int8_t* __restrict__ Wq,
+                                                      float* __restrict__ s_out,
+                                                      float* __restrict__ c_out, int V) {
+  constexpr int K = 512 * NCH;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= V) return;
+  const uint16_t* wr = W + (size_t)row * K;
+  float w[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) unpack8(*reinterpret_cast<const uint4*>(wr + c * 512 + 8 * lane), w[c]);
+  float am = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(w[c][e]));
+  am = wave_max(am);
+  const float sc = am > 0.f ? am / 127.f : 1.f;
+  const float inv = am > 0.f ? 127.f / am : 0.f;
+  float se = 0.f, sw = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float q = fminf(fmaxf(rintf(w[c][e] * inv), -127.f), 127.f);
+      const float d = w[c][e] - sc * q;
+      se = fmaf(d, d, se);
+      sw = fmaf(w[c][e], w[c][e], sw);
+      const uint32_t b = (uint32_t)((int)q & 0xff);
+      if (e < 4) lo |= b << (8 * e);
+      else hi |= b << (8 * (e - 4));
+    }
+    *reinterpret_cast<uint2*>(Wq + (size_t)row * K + c * 512 + 8 * lane) = make_uint2(lo, hi);
+  }
+  se = wave_sum(se);
+  sw = wave_sum(sw);
+  if (lane == 0) {
+    const float ne = sqrtf(se), nw = sqrtf(sw);
+    s_out[row] = sc;
+    c_out[row] = ne * (1.0f + 0x1p-10f) + 2.0f * kScreenGamma * (nw + ne);
+  }
+}
+
+// The int8 screen as a persistent grid (the lm_head top-1 layout): wave w
+// takes row groups w, w + G, ... of R rows, K = 1024 * NCH8; lane l holds x
+// elements c*1024 + 16l .. +15 (the bytes of its 16-byte weight load); the
+// next group's rows and their s_r, c_r are requested before the current group
+// is reduced. Writes U_r and one max_r (Q_r - eps_r) per workgroup.
+template <int WV, int R, int NCH8>
+__global__ __launch_bounds__(WV * 64) void lm_head_screen(const int8_t* __restrict__ Wq,
+                                                          const float* __restrict__ s_w,
+                                                          const float* __restrict__ c_r,
+                                                          const uint16_t* __restrict__ x, int V,
+                                                          float* __restrict__ U,
+                                                          float* __restrict__ lpart) {
+  constexpr int K = 1024 * NCH8;
+  __shared__ float best_s[WV];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int G = gridDim.x * WV;
+  const int wg = blockIdx.x * WV + wid;
+  const int ngroups = (V + R - 1) / R;
+  const int niter = wg < ngroups ? (ngroups - 1 - wg) / G + 1 : 0;
+  float xf[NCH8][16];
+  float nx2 = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH8; ++c) {
+    unpack8(*reinterpret_cast<const uint4*>(x + c * 1024 + 16 * lane), xf[c]);
+    unpack8(*reinterpret_cast<const uint4*>(x + c * 1024 + 16 * lane + 8), xf[c] + 8);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) nx2 = fmaf(xf[c][e], xf[c][e], nx2);
+  }
+  const float nx = sqrtf(wave_sum(nx2)) * (1.0f + 0x1p-10f);
+  float best = -INFINITY;
+  uint4 q0[R][NCH8], q1[R][NCH8];
+  float s0[R], s1[R], e0[R], e1[R];
+#define Q35_SC_LOAD(QB, SB, EB, IT)                                                   \
+  do {                                                                                \
+    const int grp = wg + min((IT), max(niter - 1, 0)) * G;                            \
+    _Pragma("unroll") for (int r = 0; r < R; ++r) {                                   \
+      const int row = min(grp * R + r, V - 1);                                        \
+      const int8_t* wr = Wq + (size_t)row * K + 16 * lane;                            \
+      _Pragma("unroll") for (int c = 0; c < NCH8; ++c) QB[r][c] = ld_stream16(wr + c * 1024); \
+      SB[r] = s_w[row];                                                               \
+      EB[r] = c_r[row];                                                               \
+    }                                                                                 \
+  } while (0)
+#define Q35_SC_REDUCE(QB, SB, EB, IT)                                                 \
+  do {                                                                                \
+    const int grp = wg + (IT) * G;                                                    \
+    _Pragma("unroll") for (int r = 0; r < R; ++r) {                                   \
+      float acc = 0.f;                                                                \
+      _Pragma("unroll") for (int c = 0; c < NCH8; ++c) {                              \
+        const uint32_t wd[4] = {QB[r][c].x, QB[r][c].y, QB[r][c].z, QB[r][c].w};      \
+        _Pragma("unroll") for (int e = 0; e < 16; ++e) {                              \
+          const float q = (float)(int)(int8_t)(wd[e >> 2] >> (8 * (e & 3)));          \
+          acc = fmaf(q, xf[c][e], acc);                                               \
+        }                                                                             \
+      }                                                                               \
+      acc = wave_sum(acc);                                                            \
+      const int row = grp * R + r;                                                    \
+      if (row < V) {                                                                  \
+        const float qv = acc * SB[r];                                                 \
+        const float eps = nx * EB[r] * (1.0f + 0x1p-7f) + 0x1p-7f * fabsf(qv);        \
+        if (lane == 0) U[row] = qv + eps;                                             \
+        best = fmaxf(best, qv - eps);                                                 \
+      }                                                                               \
+    }                                                                                 \
+  } while (0)
+  if (niter > 0) {
+    Q35_SC_LOAD(q0, s0, e0, 0);
+    for (int it = 0; it < niter; it += 2) {
+      Q35_SC_LOAD(q1, s1, e1, it + 1);
+      Q35_SC_REDUCE(q0, s0, e0, it);
+      if (it + 1 >= niter) break;
+      Q35_SC_LOAD(q0, s0, e0, it + 2);
+      Q35_SC_REDUCE(q1, s1, e1, it + 1);
+    }
+  }
+#undef Q35_SC_LOAD
+#undef Q35_SC_REDUCE
+  if (lane == 0) best_s[wid] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = best_s[0];
+#pragma unroll
+    for (int v = 1; v < WV; ++v) b = fmaxf(b, best_s[v]);
+    lpart[blockIdx.x] = b;
+  }
+}
+
+// Exact recomputation of the rows the screen left: each wave takes a
+// contiguous slice of rows, tests 64 at a time (!(U_r < L*)) and recomputes
+// its candidates four at a time (missing ones repeat the last candidate, so
+// the loads carry no branch) with lm_head_top1_persist's arithmetic for one
+// row (K = 2048: lane l holds k = c*512 + 8l, fmaf in (c, e) order,
+// wave_sum, bf16 rounding). One key per workgroup for top1_final.
+template <int WV>
+__global__ __launch_bounds__(WV * 64) void lm_head_rescore(const uint16_t* __restrict__ W,
+                                                           const uint16_t* __restrict__ x,
+                                                           const float* __restrict__ U,
+                                                           const float* __restrict__ lpart,
+                                                           int nparts, int V,
+                                                           unsigned long long* __restrict__ cand) {
+  constexpr int NCH = 4, K = 2048;
+  __shared__ unsigned long long best_s[WV];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  float xf[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) unpack8(*reinterpret_cast<const uint4*>(x + c * 512 + 8 * lane), xf[c]);
+  float lstar = -INFINITY;
+  for (int i = lane; i < nparts; i += 64) lstar = fmaxf(lstar, lpart[i]);
+  lstar = wave_max(lstar);
+  const int nw = gridDim.x * WV;
+  const int w = blockIdx.x * WV + wid;
+  const int per = (V + nw - 1) / nw;
+  const int r0 = min(V, w * per), r1 = min(V, r0 + per);
+  uint64_t best = 0;
+  const uint8_t* wbase = reinterpret_cast<const uint8_t*>(W) + lane * 16;
+  for (int base = r0; base < r1; base += 64) {
+    const int row = base + lane;
+    const bool is_cand = row < r1 && !(U[min(row, V - 1)] < lstar);
+    uint64_t mask = __ballot(is_cand);
+    while (mask) {
+      int rows[4];
+      int last = base;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (mask) {
+          last = base + (int)__builtin_ctzll(mask);
+          mask &= mask - 1;
+        }
+        rows[j] = last;
+      }
+      uint4 wv[4][NCH];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          wv[j][c] = ld_stream16(wbase + (size_t)rows[j] * K * 2 + c * 1024);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          float wf[8];
+          unpack8(wv[j][c], wf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc = fmaf(wf[e], xf[c][e], acc);
+        }
+        acc = wave_sum(acc);
+        best = u64_max(best, top1_key(round_bf(acc), (uint32_t)rows[j]));
+      }
+    }
+  }
+  if (lane == 0) best_s[wid] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = best_s[0];
+#pragma unroll
+    for (int v = 1; v < WV; ++v) b = u64_max(b, best_s[v]);
+    cand[blockIdx.x] = b;
+  }
+}
+
+constexpr int kScWV = 4, kScR = 2;
+// Workspace of the screened top-1: U [V] floats, then per workgroup one
+// float (max lower bound) and one 64-bit key, 256-byte aligned sections.
+long long screened_parts() { return (long long)lm_device_cus() * kLmBlocksPerCU; }
+long long align256(long long b) { return (b + 255) / 256 * 256; }
+long long screened_bytes(int V) {
+  const long long nb = screened_parts();
+  return align256((long long)V * 4) + align256(nb * 4) + nb * 8;
+}
+
 // Scratch of q35_lm_head_top1_noalloc: the candidate keys of one top-1 call
 // (512 slots for the persistent 2-workgroups-per-CU grid; the one-key-per-4-
 // rows fallback grid needs (V + 3) / 4). It lives in the library's device
@@ -831,6 +1076,51 @@ int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace
   Q35_CHECK_ARG(workspace_slots >= q35_lm_head_top1_workspace(V, K) && V < (1 << 30));
   return lm_head_top1_launch(W, x, V, K, workspace, workspace_slots, out, advance, n_advance,
                              stream);
+}
+
+// Screen operands of an lm_head weight W [V, K] (bf16, K = 2048): the int8
+// copy Wq [V, K], s [V] and c [V] fp32 (see lm_head_screen).
+int q35_lm_head_screen_prep(const void* W, int V, int K, void* Wq, void* s, void* c,
+                            hipStream_t stream) {
+  Q35_CHECK_ARG(W && Wq && s && c && V > 0 && K == 2048 && V < (1 << 30));
+  Q35_CHECK_ARG(q35_aligned16(W) && q35_aligned16(Wq));
+  lm_screen_prep<4><<<(unsigned)((V + 3) / 4), 256, 0, stream>>>(
+      (const uint16_t*)W, (int8_t*)Wq, (float*)s, (float*)c, V);
+  return q35_last_error();
+}
+
+long long q35_lm_head_top1_screened_workspace(int V, int K) {
+  if (V <= 0 || K != 2048) return 0;
+  return screened_bytes(V);
+}
+
+// out[0] = the index q35_lm_head_top1 returns for (W, x), found through the
+// int8 screen (Wq, s, c from q35_lm_head_screen_prep of this W) and the exact
+// recomputation of the rows it cannot exclude; `advance` as there.
+int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, const void* c,
+                              const void* x, int V, int K, void* workspace,
+                              long long workspace_bytes, void* out, void* advance, int n_advance,
+                              hipStream_t stream) {
+  Q35_CHECK_ARG(!advance || (n_advance >= 0 && n_advance <= 64));
+  Q35_CHECK_ARG(W && Wq && s && c && x && workspace && out && V > 0 && K == 2048 && V < (1 << 30));
+  Q35_CHECK_ARG(q35_aligned16(W) && q35_aligned16(Wq) && q35_aligned16(x) && q35_aligned16(workspace));
+  Q35_CHECK_ARG(workspace_bytes >= screened_bytes(V));
+  const long long nb = screened_parts();
+  float* U = (float*)workspace;
+  float* lpart = (float*)((char*)workspace + align256((long long)V * 4));
+  unsigned long long* cand =
+      (unsigned long long*)((char*)workspace + align256((long long)V * 4) + align256(nb * 4));
+  lm_head_screen<kScWV, kScR, 2><<<(unsigned)nb, kScWV * 64, 0, stream>>>(
+      (const int8_t*)Wq, (const float*)s, (const float*)c, (const uint16_t*)x, V, U, lpart);
+  int e = q35_last_error();
+  if (e) return e;
+  lm_head_rescore<kScWV><<<(unsigned)nb, kScWV * 64, 0, stream>>>(
+      (const uint16_t*)W, (const uint16_t*)x, U, lpart, (int)nb, V, cand);
+  e = q35_last_error();
+  if (e) return e;
+  top1_final<<<1, 1024, 0, stream>>>(cand, (int)nb, (long long*)out, (long long*)advance,
+                                     advance ? n_advance : 0);
+  return q35_last_error();
 }
 
 // q35_lm_head_top1 without a workspace argument: the candidate keys go to

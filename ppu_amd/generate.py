@@ -17,6 +17,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .graph import GreedyDecodeGraph
+from .integration import lm_head_screen
 from .kernels import lm_head_argmax, zero_tensors
 
 
@@ -100,7 +101,9 @@ class FusedGreedyGenerator:
         positions = torch.arange(input_len, device=input_ids.device).view(1, -1)
         prefill = model.model(input_ids=input_ids, position_ids=positions, past_key_values=cache,
                               use_cache=True, return_dict=True)
-        token = lm_head_argmax(prefill.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight)
+        screen = lm_head_screen(model)
+        token = lm_head_argmax(prefill.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight,
+                               screen=screen)
         generated = [int(token.item())]
         first_token_at = time.perf_counter()
         position = torch.full((1, 1), input_len, device=input_ids.device, dtype=torch.long)
@@ -109,7 +112,8 @@ class FusedGreedyGenerator:
         if runner is None and len(generated) < max_new_tokens and generated[-1] not in self.eos_ids:
             out = model.model(input_ids=token, position_ids=position, past_key_values=cache,
                               use_cache=True, return_dict=True)
-            token = lm_head_argmax(out.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight)
+            token = lm_head_argmax(out.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight,
+                                   screen=screen)
             generated.append(int(token.item()))
             position.add_(1)
         if len(generated) < max_new_tokens and generated[-1] not in self.eos_ids:

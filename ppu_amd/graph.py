@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import torch
 
+from .integration import lm_head_screen
 from .kernels import lm_head_argmax
 
 
@@ -65,7 +66,8 @@ class GreedyDecodeGraph:
             state = model.model(input_ids=token_in, attention_mask=None, position_ids=positions,
                                 past_key_values=self.cache, use_cache=True, return_dict=True)
             last = state.last_hidden_state[:, -1, :].contiguous()
-            lm_head_argmax(last, model.lm_head.weight, out=token_out, advance=positions)
+            lm_head_argmax(last, model.lm_head.weight, out=token_out, advance=positions,
+                           screen=lm_head_screen(model))
             return
         state = model(input_ids=token_in, attention_mask=None, position_ids=positions,
                       past_key_values=self.cache, use_cache=True, logits_to_keep=1,

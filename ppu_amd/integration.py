@@ -61,6 +61,10 @@ class FusionConfig:
     vision_graph_max_entries: int = 48
     fused_decode: bool = True
     a8w8: bool = False
+    # greedy top-1 through an int8 screen of the lm_head plus an exact
+    # recomputation of the rows it cannot exclude (same token, about half the
+    # bytes; 0.5 GB more device memory for the 2B vocabulary)
+    lm_head_screen: bool = True
 
 
 def _gpu_bf16(t: Any) -> bool:
@@ -553,6 +557,37 @@ def precompute_vision_kwargs(model: torch.nn.Module, inputs: Any) -> Any:
     return inputs
 
 
+def attach_lm_head_screen(model: torch.nn.Module) -> bool:
+    """Give ``model.lm_head`` the operands of the screened greedy top-1 (an
+    int8 copy of its weight and per-row scale / error-bound factors), keyed
+    to the weight's storage and version; False where the weight does not fit
+    the kernel (not a contiguous bf16 GPU [V, 2048] tensor)."""
+    lm = getattr(model, "lm_head", None)
+    w = getattr(lm, "weight", None)
+    if w is None or w.dim() != 2 or w.shape[1] != 2048 or not _gpu_bf16(w) or not w.is_contiguous():
+        return False
+    wq, sw, cr = K.lm_head_screen_prep(w)
+    lm.register_buffer("q35_screen_wq", wq, persistent=False)
+    lm.register_buffer("q35_screen_s", sw, persistent=False)
+    lm.register_buffer("q35_screen_c", cr, persistent=False)
+    lm._q35_screen_of = (w.data_ptr(), w._version)
+    return True
+
+
+def lm_head_screen(model: torch.nn.Module):
+    """The screen operands for ``lm_head_argmax(..., screen=)``, or None when
+    there are none or the weight changed (storage or in-place version) since
+    they were made; the full top-1 kernel then runs."""
+    lm = getattr(model, "lm_head", None)
+    wq = getattr(lm, "q35_screen_wq", None)
+    if wq is None:
+        return None
+    w = lm.weight
+    if (w.data_ptr(), w._version) != getattr(lm, "_q35_screen_of", None) or wq.device != w.device:
+        return None
+    return wq, lm.q35_screen_s, lm.q35_screen_c
+
+
 def apply_fusions(model: torch.nn.Module, config: FusionConfig | None = None) -> dict[str, int]:
     """Pack the projection weights and take over the enabled module forwards
     (reference integration.py:778-814). Returns the packing statistics."""
@@ -592,6 +627,7 @@ def install(model: torch.nn.Module, config: FusionConfig,
     if config.residual_norm:
         _take_over(stack, _text_fast(stack, config))
     model._qwen35_fusion_config = config
+    stats["lm_head_screen"] = int(config.lm_head_screen and attach_lm_head_screen(model))
     stats["delta_precompute_factors"] = int(config.delta and config.delta_precompute_factors)
     stats["ppu_swiglu_gemv"] = int(config.swiglu and config.ppu_swiglu_gemv)
     stats["fused_decode"] = int(config.fused_decode)

@@ -41,7 +41,13 @@ def _device_checked(fn):
     @functools.wraps(fn)
     def checked(*args, **kwargs):
         device = None
+        flat = []
         for name, value in itertools.chain(zip(names, args), kwargs.items()):
+            if isinstance(value, (tuple, list)):
+                flat.extend((name, v) for v in value)
+            else:
+                flat.append((name, value))
+        for name, value in flat:
             if not isinstance(value, torch.Tensor):
                 continue
             if not value.is_cuda:
@@ -537,13 +543,17 @@ def lm_head_argmax(
     block_k: int = 128,
     out: torch.Tensor | None = None,
     advance: torch.Tensor | None = None,
+    screen: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """Greedy token id without materialising logits. reference kernels.py:1146.
 
     ``out`` (int64, one element) receives the token instead of a new tensor;
     ``advance`` (an int64 tensor, e.g. the decode position ids) is incremented
     by one in the same launch — the token feedback and ``position_ids += 1`` of
-    reference graph.py:78-79 without extra kernels.
+    reference graph.py:78-79 without extra kernels. ``screen`` (the tensors
+    ``lm_head_screen_prep`` made from this ``weight``) finds the same index
+    through an int8 copy of the weight and an exact recomputation of the rows
+    the screen cannot exclude (about half the bytes read).
     """
 
     if hidden.shape != (1, weight.shape[1]) or hidden.dtype != torch.bfloat16:
@@ -554,8 +564,19 @@ def lm_head_argmax(
         raise ValueError("fused kernels require a GPU tensor")
     _need_bf16(weight)
     vocab, k = weight.shape
-    slots = _lib.load().q35_lm_head_top1_workspace(vocab, k)
-    workspace = torch.empty(slots, device=hidden.device, dtype=torch.int64)
+    if screen is not None:
+        wq, sw, cr = screen
+        if (wq.shape != weight.shape or wq.dtype != torch.int8 or sw.shape != (vocab,)
+                or cr.shape != (vocab,) or sw.dtype != torch.float32 or cr.dtype != torch.float32
+                or not (wq.is_contiguous() and sw.is_contiguous() and cr.is_contiguous())):
+            raise ValueError("screen must be lm_head_screen_prep(weight)")
+        if k != 2048:
+            raise ValueError("the screened lm_head top-1 is built for K = 2048")
+        nbytes = _lib.load().q35_lm_head_top1_screened_workspace(vocab, k)
+        workspace = torch.empty(nbytes, device=hidden.device, dtype=torch.uint8)
+    else:
+        slots = _lib.load().q35_lm_head_top1_workspace(vocab, k)
+        workspace = torch.empty(slots, device=hidden.device, dtype=torch.int64)
     if out is None:
         output = torch.empty((1, 1), device=hidden.device, dtype=torch.int64)
     else:
@@ -567,10 +588,34 @@ def lm_head_argmax(
         if advance.dtype != torch.int64 or not advance.is_contiguous() or advance.numel() > 64:
             raise ValueError("advance must be a contiguous int64 tensor of at most 64 elements")
         n_adv = advance.numel()
-    _lib.call("q35_lm_head_top1", weight.data_ptr(), hidden.data_ptr(), vocab, k,
-              workspace.data_ptr(), slots, output.data_ptr(), _lib.ptr(advance), n_adv,
-              _stream(hidden))
+    if screen is not None:
+        _lib.call("q35_lm_head_top1_screened", weight.data_ptr(), wq.data_ptr(), sw.data_ptr(),
+                  cr.data_ptr(), hidden.data_ptr(), vocab, k, workspace.data_ptr(), nbytes,
+                  output.data_ptr(), _lib.ptr(advance), n_adv, _stream(hidden))
+    else:
+        _lib.call("q35_lm_head_top1", weight.data_ptr(), hidden.data_ptr(), vocab, k,
+                  workspace.data_ptr(), slots, output.data_ptr(), _lib.ptr(advance), n_adv,
+                  _stream(hidden))
     return output
+
+
+@_device_checked
+def lm_head_screen_prep(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The operands of the screened lm_head top-1 for ``weight`` [V, 2048]
+    bf16: an int8 copy (per-row absmax / 127 scale) and per-row fp32 scale
+    and error-bound factor. Made once per weight; 0.5 bytes per weight
+    element plus 8 bytes per row."""
+
+    if weight.ndim != 2 or weight.shape[1] != 2048 or not weight.is_contiguous():
+        raise ValueError("screen operands are built for a contiguous [V, 2048] weight")
+    _need_bf16(weight)
+    vocab, k = weight.shape
+    wq = torch.empty((vocab, k), device=weight.device, dtype=torch.int8)
+    sw = torch.empty(vocab, device=weight.device, dtype=torch.float32)
+    cr = torch.empty(vocab, device=weight.device, dtype=torch.float32)
+    _lib.call("q35_lm_head_screen_prep", weight.data_ptr(), vocab, k, wq.data_ptr(),
+              sw.data_ptr(), cr.data_ptr(), _stream(weight))
+    return wq, sw, cr
 
 
 # ------------------------------------------------------------------ DeltaNet

@@ -199,6 +199,129 @@ def test_lm_head_ties(gpu):
     assert got == int(ref.lm_head_argmax(h, w))
 
 
+def _screened(gpu, h, w, **kw):
+    from ppu_amd import kernels as K
+
+    return K.lm_head_argmax(h, w, screen=K.lm_head_screen_prep(w), **kw)
+
+
+@pytest.mark.parametrize("v", [248320, 50000, 1, 63, 4099])
+def test_lm_head_screened_equals_full(gpu, v):
+    """The int8-screened top-1 returns the full kernel's index, for the 2B
+    vocabulary and ragged small ones, over hidden vectors of several scales
+    (the screen's bound grows with |x|), and the oracle's index where the
+    full kernel's is checked against it."""
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 60)
+    w = (torch.randn(v, 2048, device=gpu, generator=g) * 0.02).to(BF)
+    screen = K.lm_head_screen_prep(w)
+    for scale in (0.25, 1.0, 4.0, 30.0):
+        for _ in range(3):
+            h = (torch.randn(1, 2048, device=gpu, generator=g) * scale).to(BF)
+            full = int(K.lm_head_argmax(h, w))
+            assert int(K.lm_head_argmax(h, w, screen=screen)) == full
+    if v <= 50000:
+        h = (torch.randn(1, 2048, device=gpu, generator=g)).to(BF)
+        assert int(K.lm_head_argmax(h, w, screen=screen)) == int(ref.lm_head_argmax(h.cpu(), w.cpu()))
+
+
+def test_lm_head_screened_ties_and_adversarial(gpu):
+    """Planted exact ties (lowest index wins), a larger copy of a row, rows
+    one bf16 ulp apart, all rows equal (every row a candidate), an all-zero
+    hidden vector, a row far outside the others' range (an outlier scale) and
+    an inf row (NaN bound: always recomputed): the same index as the full
+    kernel every time."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 61)
+    h = randn(g, 1, 2048)
+    w = randn(g, 9000, 2048, scale=0.02)
+    w[7777] = w[123]
+    w[8000] = w[123] * 4
+    w[8500] = w[8000]
+    hg, wg = h.to(gpu), w.to(gpu)
+    assert int(_screened(gpu, hg, wg)) == int(K.lm_head_argmax(hg, wg)) == int(ref.lm_head_argmax(h, w))
+    # rows one ulp apart around the current winner
+    best = int(K.lm_head_argmax(hg, wg))
+    w2 = w.clone()
+    w2[4000] = w[best]
+    w2[4000, 0] = torch.nextafter(w[best, 0].float(), torch.tensor(1e9)).to(BF)
+    w2g = w2.to(gpu)
+    assert int(_screened(gpu, hg, w2g)) == int(K.lm_head_argmax(hg, w2g))
+    same = w[5].expand(3000, 2048).contiguous().to(gpu)
+    assert int(_screened(gpu, hg, same)) == 0 == int(K.lm_head_argmax(hg, same))
+    zero_h = torch.zeros(1, 2048, dtype=BF, device=gpu)
+    assert int(_screened(gpu, zero_h, wg)) == 0 == int(K.lm_head_argmax(zero_h, wg))
+    w3 = w.clone()
+    w3[17] = w[17] * 300
+    w3g = w3.to(gpu)
+    assert int(_screened(gpu, hg, w3g)) == int(K.lm_head_argmax(hg, w3g))
+    w4 = w.clone()
+    w4[29, 7] = float("inf")
+    w4g = w4.to(gpu)
+    assert int(_screened(gpu, hg, w4g)) == int(K.lm_head_argmax(hg, w4g))
+
+
+def test_lm_head_screen_bound_holds(gpu):
+    """The screen's upper bounds (left in the workspace) are at least every
+    row's exact logit plus the bf16 rounding, and the largest lower bound is
+    at most the largest logit: checked against fp64 dot products."""
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 62)
+    v = 60000
+    w = (torch.randn(v, 2048, device=gpu, generator=g) * 0.02).to(BF)
+    h = torch.randn(1, 2048, device=gpu, generator=g).to(BF)
+    wq, sw, cr = K.lm_head_screen_prep(w)
+    nbytes = _lib.load().q35_lm_head_top1_screened_workspace(v, 2048)
+    ws = torch.empty(nbytes, device=gpu, dtype=torch.uint8)
+    out = torch.empty(1, 1, device=gpu, dtype=torch.int64)
+    _lib.call("q35_lm_head_top1_screened", w.data_ptr(), wq.data_ptr(), sw.data_ptr(), cr.data_ptr(),
+              h.data_ptr(), v, 2048, ws.data_ptr(), nbytes, out.data_ptr(), None, 0,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    upper = ws[: v * 4].view(torch.float32).double().cpu()
+    exact = (w.double() @ h.double().t()).reshape(-1).cpu()
+    assert bool((upper >= exact + exact.abs() * 2.0**-8).all())
+    # per-workgroup largest lower bounds follow U (256-byte aligned), one per
+    # workgroup of the persistent grid (2 per CU)
+    nb = 2 * torch.cuda.get_device_properties(gpu).multi_processor_count
+    at = (v * 4 + 255) // 256 * 256
+    lower_max = float(ws[at : at + 4 * nb].view(torch.float32).max())
+    assert lower_max <= float(exact.max()) * (1 - 2.0**-8 * (1 if exact.max() > 0 else -1))
+    # candidates: a few percent of the rows for these random weights
+    frac = float((upper >= lower_max).double().mean())
+    print(f"candidate fraction {frac:.4f}")
+    assert frac < 0.2
+    assert int(out) == int(K.lm_head_argmax(h, w))
+
+
+def test_lm_head_screened_in_graph_with_feedback(gpu):
+    """Captured in a graph with the token written to ``out`` and positions
+    advanced: every replay equals the eager full kernel on the same input."""
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 63)
+    w = (torch.randn(20000, 2048, device=gpu, generator=g) * 0.02).to(BF)
+    screen = K.lm_head_screen_prep(w)
+    h = torch.randn(1, 2048, device=gpu, generator=g).to(BF)
+    tok = torch.zeros(1, 1, dtype=torch.int64, device=gpu)
+    pos = torch.tensor([[7]], dtype=torch.int64, device=gpu)
+    K.lm_head_argmax(h, w, out=tok, advance=pos, screen=screen)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        K.lm_head_argmax(h, w, out=tok, advance=pos, screen=screen)
+    for r in range(3):
+        h.copy_(torch.randn(1, 2048, device=gpu, generator=g).to(BF))
+        tok.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(tok) == int(K.lm_head_argmax(h, w)) and int(pos) == 9 + r
+
+
 # ------------------------------------------------------------------ DeltaNet
 @pytest.mark.parametrize("seq_len", [1, 17])
 @pytest.mark.parametrize("extra", [0, 32])
