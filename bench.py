@@ -189,7 +189,10 @@ def swiglu_roofline(model, variant: str) -> dict:
 
 def step_bytes(model, context: float) -> int:
     """HBM bytes one decode token needs: every packed weight (and int8 scale)
-    once, the lm_head (tied embedding) once, the small per-layer parameters
+    once, the lm_head (tied embedding) once (with the screened top-1
+    installed: its int8 copy, per-row scale and bound factor and the per-row
+    upper bounds written and read back, in place of the bf16 weight; the
+    recomputed rows are not counted), the small per-layer parameters
     the decode kernels read (norm weights, conv taps, ``A_log``, ``dt_bias``),
     the embedding row, the recurrent and conv states read and written, and
     the K/V cache read over ``context`` positions plus the new row written.
@@ -214,7 +217,16 @@ def step_bytes(model, context: float) -> int:
         if isinstance(m, _Weight):
             add(m.w)
             add(m.s)
-    add(model.lm_head.weight)
+    from ppu_amd.integration import lm_head_screen
+
+    screen = lm_head_screen(model)
+    if screen is None:
+        add(model.lm_head.weight)
+    else:
+        for t in screen:
+            add(t)
+        total += 2 * 4 * screen[1].numel()  # per-row upper bounds written and read
+        seen.add(model.lm_head.weight.data_ptr())  # the tied embedding is not re-counted below
     total += stack.config.hidden_size * 2  # the embedding row of the token
     for mod in stack.modules():
         if isinstance(mod, torch.nn.Linear) or mod is stack.embed_tokens:

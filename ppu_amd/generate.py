@@ -7,6 +7,12 @@ lm_head top-1, ``token.item()`` ends TTFT, one eager decode step on a fresh
 bucket, then one captured greedy graph replayed per token with one
 device-to-host read per token. Throughput follows the reference formula
 ``(tokens - 1) / (elapsed - ttft)`` (benchmark_public.py:148-153).
+
+Prefill is captured too, per (cache bucket, prompt length): a length seen
+before runs the cache reset, the ~290 prefill launches and the first token's
+top-1 as one graph replay (``PrefillGraph``), so the host issues one launch
+instead of running the integration's Python per op. The graph is captured at
+the end of the first call with that length, outside its timed region.
 """
 
 from __future__ import annotations
@@ -68,14 +74,74 @@ def reset_cache(cache) -> None:
     zero_tensors(tensors)
 
 
-class FusedGreedyGenerator:
-    """Keeps one StaticCache and one captured decode graph per cache bucket."""
+_FLAG_ATTRS = ("has_previous_state", "is_conv_states_initialized", "is_recurrent_states_initialized",
+               "is_initialized", "cumulative_length")
 
-    def __init__(self, model, eos_ids: set[int] | None = None):
+
+def _cache_flags(cache) -> list:
+    """The host-side state of a cache's layers (flags and integer lengths)
+    that the Python of a prefill sets; device tensors are left out."""
+    state = []
+    for layer in cache.layers:
+        for name in _FLAG_ATTRS:
+            value = getattr(layer, name, None)
+            if isinstance(value, (bool, int)):
+                state.append((layer, name, value))
+            elif isinstance(value, list) and all(isinstance(v, (bool, int)) for v in value):
+                state.append((layer, name, list(value)))
+    return state
+
+
+def _restore_flags(state: list) -> None:
+    for layer, name, value in state:
+        setattr(layer, name, list(value) if isinstance(value, list) else value)
+
+
+class PrefillGraph:
+    """The prefill of one prompt length over one static cache, captured once:
+    the cache reset (one zeroing kernel), the patched model's prefill and the
+    first token's lm_head top-1 into a static token tensor. ``run`` copies the
+    prompt ids into the captured input buffer, replays, and sets the cache's
+    host-side flags to what the eager prefill leaves. The cache's tensors must
+    already exist (one eager prefill over it first)."""
+
+    def __init__(self, model, cache, input_ids: torch.Tensor) -> None:
+        device = input_ids.device
+        self.ids = input_ids.clone()
+        self.positions = torch.arange(int(input_ids.shape[-1]), device=device).view(1, -1)
+        self.token = torch.zeros((1, 1), device=device, dtype=torch.long)
+        saved = _cache_flags(cache)
+        screen = lm_head_screen(model)
+        torch.cuda.synchronize(device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            reset_cache(cache)
+            out = model.model(input_ids=self.ids, position_ids=self.positions, past_key_values=cache,
+                              use_cache=True, return_dict=True)
+            lm_head_argmax(out.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight,
+                           out=self.token, screen=screen)
+        self.flags = _cache_flags(cache)  # host state after a prefill
+        _restore_flags(saved)  # the capture ran no kernel: the cache is as it was
+
+    def run(self, input_ids: torch.Tensor) -> torch.Tensor:
+        self.ids.copy_(input_ids)
+        self.graph.replay()
+        _restore_flags(self.flags)
+        return self.token
+
+
+class FusedGreedyGenerator:
+    """Keeps one StaticCache and one captured decode graph per cache bucket,
+    and one captured prefill per (bucket, prompt length) seen (at most
+    ``max_prefill_graphs``, the oldest dropped first)."""
+
+    def __init__(self, model, eos_ids: set[int] | None = None, max_prefill_graphs: int = 4):
         self.model = model
         self.eos_ids = eos_ids or set()
         self._caches: dict[int, object] = {}
         self._graphs: dict[int, GreedyDecodeGraph] = {}
+        self._prefills: dict[tuple[int, int], PrefillGraph] = {}
+        self.max_prefill_graphs = int(max_prefill_graphs)
 
     def _cache(self, bucket: int):
         from transformers.cache_utils import StaticCache
@@ -96,14 +162,18 @@ class FusedGreedyGenerator:
         torch.cuda.synchronize()
         start = time.perf_counter()
         cache, fresh = self._cache(bucket)
-        if not fresh:
-            reset_cache(cache)
-        positions = torch.arange(input_len, device=input_ids.device).view(1, -1)
-        prefill = model.model(input_ids=input_ids, position_ids=positions, past_key_values=cache,
-                              use_cache=True, return_dict=True)
         screen = lm_head_screen(model)
-        token = lm_head_argmax(prefill.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight,
-                               screen=screen)
+        captured = self._prefills.get((bucket, input_len))
+        if captured is not None:
+            token = captured.run(input_ids)
+        else:
+            if not fresh:
+                reset_cache(cache)
+            positions = torch.arange(input_len, device=input_ids.device).view(1, -1)
+            prefill = model.model(input_ids=input_ids, position_ids=positions, past_key_values=cache,
+                                  use_cache=True, return_dict=True)
+            token = lm_head_argmax(prefill.last_hidden_state[:, -1, :].contiguous(),
+                                   model.lm_head.weight, screen=screen)
         generated = [int(token.item())]
         first_token_at = time.perf_counter()
         position = torch.full((1, 1), input_len, device=input_ids.device, dtype=torch.long)
@@ -125,9 +195,15 @@ class FusedGreedyGenerator:
             while len(generated) < max_new_tokens and generated[-1] not in self.eos_ids:
                 generated.append(int(runner.replay().reshape(-1)[0].item()))
         end = time.perf_counter()
+        if captured is None:
+            # outside the timed region: capture this length's prefill for next time
+            while len(self._prefills) >= max(self.max_prefill_graphs, 1):
+                self._prefills.pop(next(iter(self._prefills)))
+            self._prefills[(bucket, input_len)] = PrefillGraph(model, cache, input_ids)
         return GenerationResult(
             tokens=generated,
             ttft_seconds=first_token_at - start,
             elapsed_seconds=end - start,
-            meta={"cache_bucket": bucket, "graph_reused": reused, "cache_reused": not fresh},
+            meta={"cache_bucket": bucket, "graph_reused": reused, "cache_reused": not fresh,
+                  "prefill_graph": captured is not None},
         )

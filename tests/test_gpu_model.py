@@ -144,6 +144,38 @@ def test_fused_cache_reset_matches_transformers(gpu):
     assert again.meta["cache_reused"] and again.tokens == first.tokens
 
 
+@pytest.mark.parametrize("a8w8", [False, True])
+def test_prefill_graph_matches_eager(gpu, a8w8):
+    """A prompt length seen before runs its prefill as one captured graph:
+    the same tokens as the eager first call, for the same prompt and for a
+    different prompt of that length (the graph reads the ids from its input
+    buffer), with the cache's device state and host flags as after an eager
+    prefill; a new length runs eagerly again."""
+    from ppu_amd.generate import FusedGreedyGenerator
+    from ppu_amd.integration import FusionConfig
+
+    cfg = synth.config_tiny()
+    model, _, _ = _build(cfg, gpu, FusionConfig(a8w8=a8w8))
+    g = torch.Generator().manual_seed(12)
+    p1 = torch.randint(0, cfg.vocab_size, (1, 90), generator=g).to(gpu)
+    p2 = torch.randint(0, cfg.vocab_size, (1, 90), generator=g).to(gpu)
+    p3 = torch.randint(0, cfg.vocab_size, (1, 33), generator=g).to(gpu)
+    eager = {}
+    for name, p in (("p1", p1), ("p2", p2), ("p3", p3)):
+        eager[name] = FusedGreedyGenerator(model).generate(p, max_new_tokens=10).tokens
+    gen_ = FusedGreedyGenerator(model)
+    first = gen_.generate(p1, max_new_tokens=10)
+    assert not first.meta["prefill_graph"] and first.tokens == eager["p1"]
+    for name, p in (("p1", p1), ("p2", p2), ("p1", p1)):
+        res = gen_.generate(p, max_new_tokens=10)
+        assert res.meta["prefill_graph"], name
+        assert res.tokens == eager[name], name
+    res = gen_.generate(p3, max_new_tokens=10)
+    assert not res.meta["prefill_graph"] and res.tokens == eager["p3"]
+    res = gen_.generate(p2, max_new_tokens=10)  # the 90-token graph survives another length
+    assert res.meta["prefill_graph"] and res.tokens == eager["p2"]
+
+
 def test_graph_replay_matches_eager_decode(gpu):
     """Graph replays advance the cache exactly as eager decode steps do."""
     from transformers.cache_utils import StaticCache
