@@ -457,6 +457,86 @@ DECODE_ALGO_BYTES = {
 }
 
 
+def trace_summary(kind: str, trace_csv: str, bench_json: str) -> None:
+    """Print the per-kernel anatomy of a ``rocprofv3 --kernel-trace`` run of
+    ``bench.py --no-cpu --no-kernels``: ``decode`` = one graph-replayed decode
+    step per linear variant (the second-to-last replay of each), ``prefill``
+    = one warm prefill + first token per variant (the last of each); with the
+    unprofiled figures of the same run's JSON line."""
+    import collections
+    import csv
+    import re
+
+    d = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+
+    def short(n):
+        n = n.replace("(anonymous namespace)::", "").replace("void ", "")
+        m = re.match(r"([\w:]+)(<[^(]*>)?", n)
+        return ((m.group(1).split("::")[-1] + (m.group(2) or "")) if m else n)[:58]
+
+    def dur(r):
+        return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+    def int8(a, b):
+        return any(("gemv_fused" in rows[i]["Kernel_Name"] and ", true>" in rows[i]["Kernel_Name"])
+                   or "I8II" in rows[i]["Kernel_Name"] for i in range(a, b))
+
+    def table(seg, grid, top=None):
+        t0, t1 = int(seg[0]["Start_Timestamp"]), int(seg[-1]["End_Timestamp"])
+        agg = collections.OrderedDict()
+        for r in seg:
+            k = short(r["Kernel_Name"]) + (f" g{r['Grid_Size_X']}" if grid else "")
+            x = agg.setdefault(k, [0, 0.0])
+            x[0] += 1
+            x[1] += dur(r)
+        busy = sum(v[1] for v in agg.values())
+        out = [f"#   {len(seg)} kernels, wall {(t1 - t0) / 1e3:.1f} us, sum of kernel durations {busy:.1f} us"]
+        items = sorted(agg.items(), key=lambda kv: -kv[1][1])
+        for k, (n, t) in items[:top] if top else items:
+            out.append(f"#   {k:72s} n={n:3d} total {t:8.1f} us  avg {t / n:7.2f} us")
+        return out
+
+    ends = [i for i, r in enumerate(rows) if "top1_final" in r["Kernel_Name"]]
+    v = d.get("variants", {}).get("a8w8", {})
+    lines = []
+    if kind == "decode":
+        steps = [(a + 1, b + 1) for a, b in zip(ends, ends[1:]) if 60 < b - a < 400]
+        for name, pick in (("bf16", False), ("A8W8", True)):
+            sel = [s for s in steps if int8(*s) == pick]
+            if len(sel) >= 2:
+                lines.append(f"# {name} decode step (second-to-last {name} replay in the trace):")
+                lines += table(rows[sel[-2][0]:sel[-2][1]], True)
+                lines.append("#")
+    else:
+        preps = [i for i, r in enumerate(rows) if "delta_chunk_prep" in r["Kernel_Name"]]
+        wins = []
+        for k in range(0, len(preps), 18):
+            w = preps[k:k + 18]
+            a = max([e for e in ends if e < w[0]], default=-1) + 1
+            b = min([e for e in ends if e > w[-1]], default=len(rows) - 1) + 1
+            # a generate() prefill: its first top-1 (the screened one, when the
+            # model has it) follows the prefill directly, with no decode GEMV
+            # in between as in the bench's separate eager setup
+            tail = [rows[i]["Kernel_Name"] for i in range(w[-1], b)]
+            if not any("gemv_fused" in n for n in tail) and (
+                    any("lm_head_screen" in n for n in tail) or not any(
+                        "lm_head_screen" in r["Kernel_Name"] for r in rows)):
+                wins.append((a, b))
+        for name, pick in (("bf16", False), ("A8W8", True)):
+            sel = [w for w in wins if int8(*w) == pick]
+            if sel:
+                lines.append(f"# {name}: one warm prefill (1024 tokens) + first token, the last in the trace:")
+                lines += table(rows[sel[-1][0]:sel[-1][1]], False, top=24)
+                lines.append("#")
+    lines.append(f"# bench.py JSON given ({Path(bench_json).name}): bf16 decode {d['ms_per_step']} ms/token = "
+                 f"{d['value']} tok/s (graph replay alone {d['graph_replay_ms']} ms), TTFT {d['ttft_ms']} ms;")
+    if v:
+        lines.append(f"#   A8W8 decode {v.get('ms_per_step')} ms/token = {v.get('value')} tok/s "
+                     f"(replay {v.get('graph_replay_ms')} ms), TTFT {v.get('ttft_ms')} ms.")
+    print("\n".join(lines))
+
+
 def pmc_summary(fetch_csv: str, write_csv: str) -> None:
     """Print the HBM-traffic summary of two ``rocprofv3 --pmc`` runs of
     ``--counter-probe`` (FETCH_SIZE, then WRITE_SIZE; their
@@ -616,6 +696,8 @@ def main() -> None:
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     ap.add_argument("--cpu-prompt", type=int, default=PROMPT_LEN, help="prompt length of the CPU sample")
     ap.add_argument("--no-eager", action="store_true", help="skip the Transformers-eager CPU timing")
+    ap.add_argument("--trace-summary", nargs=3, metavar=("decode|prefill", "TRACE_CSV", "BENCH_JSON"),
+                    help="per-kernel anatomy of a rocprofv3 kernel trace of this bench, then exit")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="prefill GEMM shapes: ROCm library vs the hand-written GEMMs, then exit")
     ap.add_argument("--counter-probe", action="store_true",
@@ -625,6 +707,9 @@ def main() -> None:
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.trace_summary:
+        trace_summary(*args.trace_summary)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (a batch-1 decode step "
