@@ -350,6 +350,28 @@ int q35_gemm_a8w8(const void* Aq, const void* s_x, const void* Bq, const void* s
                   long long workspace_bytes, void* stream);
 long long q35_gemm_a8w8_workspace(int M, int N, int K, int swiglu, int tile, int splits);
 
+/* A8W8 prefill between the int8 GEMMs of a layer: residual add of the
+ * dequantised accumulators of the previous GEMM (q35_dequant_i32's values) +
+ * RMSNorm (width 2048, (1 + w) weight) with the normalised rows quantised per
+ * token for the next GEMM (q35_quant_act_i8's rule): the same bits as
+ * q35_dequant_i32 -> q35_residual_rmsnorm -> q35_quant_act_i8 in one launch.
+ * y (bf16 normalised rows) and yq/s_y may each be null, not both. Replaces
+ * the dequant of explore_runtime_quantization.py:173-180, the residual norm of
+ * integration.py:456-499 and the activation quant of
+ * explore_runtime_quantization.py:167-172 at the A8W8 prefill sites. */
+int q35_residual_rmsnorm_dequant_quant(const void* x, const void* acc, const void* s_x,
+                                       const void* s_w, const void* w, int w_f32, void* r_out,
+                                       void* y, void* yq, void* s_y, int rows, int width, float eps,
+                                       void* stream);
+/* A8W8 prefill MLP: q35_dequant_swiglu_i32's SwiGLU of the packed [gate; up]
+ * accumulators acc[M, 2N], quantised per token into yq[M, N] int8 and s_y[M]
+ * (q35_quant_act_i8's rule) for the down projection; the bf16 activation is
+ * never stored. N % 8 == 0, N <= 6144. Replaces silu_and_mul
+ * (kernels.py:158-180) + the activation quant of the down projection's
+ * PPUA8W8Linear at integration.py:183-187. */
+int q35_dequant_swiglu_quant(const void* acc, const void* s_x, const void* s_w, void* yq, void* s_y,
+                             int M, int N, void* stream);
+
 /* y[M,N] = bf16(float(acc[m,n]) * s_x[m] * s_w[n]) for int32 accumulators of an
  * int8 GEMM (the prefill A8W8 path; N % 8 == 0). Same dequant epilogue as
  * q35_gemv_a8w8, replacing the output stage of explore_runtime_quantization.py:173-180. */

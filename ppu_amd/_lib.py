@@ -81,6 +81,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_gemm_plan_workspace": (_L, [_I, _I, _I, _I, _I]),
     "q35_gemm_a8w8": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
     "q35_gemm_a8w8_workspace": (_L, [_I, _I, _I, _I, _I, _I]),
+    "q35_residual_rmsnorm_dequant_quant": (
+        _I, [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P]),
+    "q35_dequant_swiglu_quant": (_I, [_P, _P, _P, _P, _P, _I, _I, _P]),
     "q35_lm_head_screen_prep": (_I, [_P, _I, _I, _P, _P, _P, _P]),
     "q35_lm_head_top1_screened_workspace": (_L, [_I, _I]),
     "q35_lm_head_top1_screened": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),

@@ -348,6 +348,144 @@ __global__ __launch_bounds__(256) void dequant_swiglu_rows(const int* __restrict
   }
 }
 
+// ---------------------------------------------------------- A8W8 prefill rows
+// The prefill of an A8W8 layer hands int8 activations and int32 accumulators
+// between its GEMMs. These kernels fuse the steps around them, each with the
+// arithmetic of the separate kernels it replaces, so the values are the same
+// bits:
+//   resnorm_dequant_quant_rows  update = bf16(float(acc) * s_x[m] * s_w[k])
+//     (q35_dequant_i32), r = bf16(x + update), y = bf16(r * rsqrt(mean(r^2) +
+//     eps) * (1 + w)) (q35_residual_rmsnorm, width 2048), and optionally y
+//     quantised per token (q35_quant_act_i8: s = absmax/127, q = sat(rint(y *
+//     127/absmax))). One wave per row; lane l holds k = 512j + 8l .. +7; every
+//     load is issued before the reduction.
+//   swiglu_quant_rows  act = bf16(bf16(silu(g)) * u) from the [gate; up]
+//     accumulators (q35_dequant_swiglu_i32), quantised per token; the bf16
+//     act is never stored. One workgroup per row (N / 8 <= 3 * 256).
+template <bool QUANT, bool YOUT>
+__global__ __launch_bounds__(256) void resnorm_dequant_quant_rows(
+    const uint16_t* __restrict__ x, const int* __restrict__ acc, const float* __restrict__ s_x,
+    const float* __restrict__ s_w, const void* __restrict__ w, int w_f32,
+    uint16_t* __restrict__ r_out, uint16_t* __restrict__ y, int8_t* __restrict__ yq,
+    float* __restrict__ s_y, int rows, float eps) {
+  constexpr int NPER = 4, width = 2048;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const size_t base = (size_t)row * width;
+  uint4 xa[NPER], wa[NPER], wb[NPER];
+  int4 c0[NPER], c1[NPER];
+  float4 s0[NPER], s1[NPER];
+  const float sx = s_x[row];
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    const int k = j * 512 + lane * 8;
+    xa[j] = *reinterpret_cast<const uint4*>(x + base + k);
+    c0[j] = *reinterpret_cast<const int4*>(acc + base + k);
+    c1[j] = *reinterpret_cast<const int4*>(acc + base + k + 4);
+    s0[j] = *reinterpret_cast<const float4*>(s_w + k);
+    s1[j] = *reinterpret_cast<const float4*>(s_w + k + 4);
+    if (w_f32) {
+      wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + k);
+      wb[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + k + 4);
+    } else {
+      wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + k);
+    }
+  }
+  float a[NPER][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    unpack8(xa[j], a[j]);
+    const int av[8] = {c0[j].x, c0[j].y, c0[j].z, c0[j].w, c1[j].x, c1[j].y, c1[j].z, c1[j].w};
+    const float sv[8] = {s0[j].x, s0[j].y, s0[j].z, s0[j].w, s1[j].x, s1[j].y, s1[j].z, s1[j].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[j][e] = round_bf(a[j][e] + round_bf((float)av[e] * sx * sv[e]));
+    *reinterpret_cast<uint4*>(r_out + base + j * 512 + lane * 8) = pack8(a[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += a[j][e] * a[j][e];
+  }
+  const float inv = rsqrt_cr(wave_sum(ss) / (float)width + eps);
+  float o[NPER][8];
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPER; ++j) {
+    float wf[8];
+    if (w_f32) {
+      wf[0] = __uint_as_float(wa[j].x); wf[1] = __uint_as_float(wa[j].y);
+      wf[2] = __uint_as_float(wa[j].z); wf[3] = __uint_as_float(wa[j].w);
+      wf[4] = __uint_as_float(wb[j].x); wf[5] = __uint_as_float(wb[j].y);
+      wf[6] = __uint_as_float(wb[j].z); wf[7] = __uint_as_float(wb[j].w);
+    } else {
+      unpack8(wa[j], wf);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o[j][e] = round_bf(a[j][e] * inv * (1.0f + wf[e]));
+      mx = fmaxf(mx, fabsf(o[j][e]));
+    }
+    if (YOUT) *reinterpret_cast<uint4*>(y + base + j * 512 + lane * 8) = pack8(o[j]);
+  }
+  if (QUANT) {
+    mx = wave_max(mx);
+    const float qinv = 127.0f / mx;
+#pragma unroll
+    for (int j = 0; j < NPER; ++j)
+      *reinterpret_cast<uint2*>(yq + base + j * 512 + lane * 8) = quant8_i8(o[j], qinv);
+    if (lane == 0) s_y[row] = mx / 127.0f;
+  }
+}
+
+__global__ __launch_bounds__(256) void swiglu_quant_rows(const int* __restrict__ acc,
+                                                         const float* __restrict__ s_x,
+                                                         const float* __restrict__ s_w,
+                                                         int8_t* __restrict__ yq,
+                                                         float* __restrict__ s_y, int N) {
+  constexpr int PER = 3;
+  const int m = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int groups = N / 8;
+  const int* row = acc + (size_t)m * 2 * N;
+  const float sx = s_x[m];
+  __shared__ float red[4];
+  float o[PER][8];
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int gi = min(tid + 256 * j, groups - 1);
+    const int n = gi * 8;
+    const int4 a0 = *reinterpret_cast<const int4*>(row + n);
+    const int4 a1 = *reinterpret_cast<const int4*>(row + n + 4);
+    const int4 b0 = *reinterpret_cast<const int4*>(row + N + n);
+    const int4 b1 = *reinterpret_cast<const int4*>(row + N + n + 4);
+    const float4 g0 = *reinterpret_cast<const float4*>(s_w + n);
+    const float4 g1 = *reinterpret_cast<const float4*>(s_w + n + 4);
+    const float4 u0 = *reinterpret_cast<const float4*>(s_w + N + n);
+    const float4 u1 = *reinterpret_cast<const float4*>(s_w + N + n + 4);
+    const int ag[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const int au[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float wg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float wu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float g = round_bf((float)ag[e] * sx * wg[e]);
+      const float u = round_bf((float)au[e] * sx * wu[e]);
+      o[j][e] = round_bf(round_bf(silu_fast(g)) * u);
+      mx = tid + 256 * j < groups ? fmaxf(mx, fabsf(o[j][e])) : mx;
+    }
+  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float qinv = 127.0f / mx;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (tid + 256 * j < groups)
+      *reinterpret_cast<uint2*>(yq + (size_t)m * N + (tid + 256 * j) * 8) = quant8_i8(o[j], qinv);
+  if (tid == 0) s_y[m] = mx / 127.0f;
+}
+
 }  // namespace
 
 extern "C" {
@@ -365,6 +503,43 @@ int q35_dequant_swiglu_i32(const void* acc, const void* s_x, const void* s_w, vo
   return q35_last_error();
 }
 
+
+// A8W8 prefill: residual add of a dequantised int8-GEMM output + RMSNorm
+// (width 2048) with the normalised rows optionally quantised per token; the
+// same bits as q35_dequant_i32 -> q35_residual_rmsnorm -> q35_quant_act_i8.
+// y and (yq, s_y) may each be null (not both); acc, x, r_out, y, s_w, w
+// 16-byte aligned.
+int q35_residual_rmsnorm_dequant_quant(const void* x, const void* acc, const void* s_x,
+                                       const void* s_w, const void* w, int w_f32, void* r_out,
+                                       void* y, void* yq, void* s_y, int rows, int width, float eps,
+                                       hipStream_t stream) {
+  Q35_CHECK_ARG(rows > 0 && width == 2048 && x && acc && s_x && s_w && w && r_out);
+  Q35_CHECK_ARG((y || yq) && (!yq || s_y));
+  Q35_CHECK_ARG(q35_aligned16(x) && q35_aligned16(acc) && q35_aligned16(s_w) && q35_aligned16(w) &&
+                q35_aligned16(r_out) && (!y || q35_aligned16(y)) && (!yq || q35_aligned8(yq)));
+  const unsigned grid = (unsigned)((rows + 3) / 4);
+#define Q35_RDQ(Q, Y)                                                                               \
+  resnorm_dequant_quant_rows<Q, Y><<<grid, 256, 0, stream>>>(                                      \
+      (const uint16_t*)x, (const int*)acc, (const float*)s_x, (const float*)s_w, w, w_f32,          \
+      (uint16_t*)r_out, (uint16_t*)y, (int8_t*)yq, (float*)s_y, rows, eps)
+  if (yq && y) Q35_RDQ(true, true);
+  else if (yq) Q35_RDQ(true, false);
+  else Q35_RDQ(false, true);
+#undef Q35_RDQ
+  return q35_last_error();
+}
+
+// A8W8 prefill: the SwiGLU of a packed [gate; up] int8 GEMM's accumulators
+// acc[M, 2N] (q35_dequant_swiglu_i32's values) quantised per token into
+// yq[M, N] int8 and s_y[M] (q35_quant_act_i8's rule); N % 8 == 0, N <= 6144.
+int q35_dequant_swiglu_quant(const void* acc, const void* s_x, const void* s_w, void* yq, void* s_y,
+                             int M, int N, hipStream_t stream) {
+  Q35_CHECK_ARG(M > 0 && N > 0 && N % 8 == 0 && N <= 3 * 256 * 8 && acc && s_x && s_w && yq && s_y);
+  Q35_CHECK_ARG(q35_aligned16(acc) && q35_aligned16(s_w) && q35_aligned8(yq));
+  swiglu_quant_rows<<<(unsigned)M, 256, 0, stream>>>((const int*)acc, (const float*)s_x,
+                                                     (const float*)s_w, (int8_t*)yq, (float*)s_y, N);
+  return q35_last_error();
+}
 
 // y[M,N] = bf16(acc * s_x[m] * s_w[n]) for int32 accumulators from any int8 GEMM.
 int q35_dequant_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,

@@ -111,6 +111,18 @@ class _Weight(torch.nn.Module):
             return K.linear(x.contiguous(), self.w)
         return K.prefill_linear(x, self.w)
 
+    def from_int8(self, xq: torch.Tensor, sx: torch.Tensor) -> torch.Tensor:
+        """The A8W8 prefill product of already quantised rows ``xq [..., K]``
+        (scales ``sx``): int32 GEMM, then the dequant, bf16 ``[..., N]``."""
+        acc = K.a8w8_int_gemm(xq, self.w)
+        return K.dequant_linear_i32(acc, sx, self.s, (*xq.shape[:-1], self.out_features))
+
+    def to_int32(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """The A8W8 prefill product left as ``(int32 accumulators [rows, N],
+        activation scales)`` for a consumer that dequantises on load."""
+        xq, sx = K.quantize_act_i8(x.contiguous())
+        return K.a8w8_int_gemm(xq, self.w), sx
+
 
 def _stack_rows(parts: list[torch.Tensor], multiple: int) -> torch.Tensor:
     """Concatenate weights along the output dimension, zero rows appended up
@@ -286,10 +298,14 @@ def _kv_slot(attn, cache, like: torch.Tensor):
 
 
 # ----------------------------------------------------------------- mixers
-def _delta_prefill(mixer, hidden: torch.Tensor, cache, config: FusionConfig) -> torch.Tensor:
-    """DeltaNet mixer on the GPU (reference integration.py:220-274)."""
+def _delta_prefill(mixer, hidden: torch.Tensor, cache, config: FusionConfig, quant=None,
+                   int32_out: bool = False):
+    """DeltaNet mixer on the GPU (reference integration.py:220-274). A8W8
+    prefill: ``quant`` = the input already quantised ``(xq [B, L, K], sx)``
+    (``hidden`` then only gives the shape), and ``int32_out`` leaves the
+    output projection as ``(accumulators, activation scales)``."""
     batch, length, _ = hidden.shape
-    packed = mixer.q35_in(hidden.contiguous())
+    packed = mixer.q35_in(hidden.contiguous()) if quant is None else mixer.q35_in.from_int8(*quant)
     conv_state, rec_state = _delta_state(mixer, cache, batch, hidden.device)
     qkv = K.causal_conv1d_fused(packed, mixer.q35_conv_w, conv_state)
     dv = mixer.head_v_dim
@@ -308,7 +324,8 @@ def _delta_prefill(mixer, hidden: torch.Tensor, cache, config: FusionConfig) -> 
             z = packed[..., mixer.conv_dim : mixer.conv_dim + mixer.value_dim]
             core = K.gated_rms_norm(core, z.reshape(-1, dv).contiguous(), mixer.norm.weight,
                                     mixer.layer_norm_epsilon)
-    return mixer.q35_out(core.reshape(batch, length, mixer.value_dim))
+    core = core.reshape(batch, length, mixer.value_dim)
+    return mixer.q35_out.to_int32(core) if int32_out else mixer.q35_out(core)
 
 
 def _delta_fast(mixer, config: FusionConfig):
@@ -322,12 +339,14 @@ def _delta_fast(mixer, config: FusionConfig):
 
 
 def _attention_prefill(attn, hidden: torch.Tensor, position_embeddings, cache,
-                       config: FusionConfig) -> torch.Tensor:
+                       config: FusionConfig, quant=None, int32_out: bool = False):
     """Attention mixer on the GPU (reference integration.py:277-382): packed
     projection, Q/K norm + RoPE with the static-cache write, decode attention
-    for one token or causal GQA prefill attention, sigmoid gate, o_proj."""
+    for one token or causal GQA prefill attention, sigmoid gate, o_proj.
+    ``quant`` / ``int32_out`` as for ``_delta_prefill``."""
     length = hidden.shape[1]
-    packed = attn.q35_qgkv(hidden.contiguous())
+    packed = (attn.q35_qgkv(hidden.contiguous()) if quant is None
+              else attn.q35_qgkv.from_int8(*quant))
     cos, sin = position_embeddings
     slot = _kv_slot(attn, cache, hidden)
     q, k, v = K.qgkv_norm_rope(
@@ -352,7 +371,7 @@ def _attention_prefill(attn, hidden: torch.Tensor, position_embeddings, cache,
         out = K.gqa_prefill_attention(q, k.contiguous(), v.contiguous(), attn.scaling,
                                       kv_start=kv_start, valid_length=valid)
         out = K.attention_gate_mul(out, packed, attn.head_dim)
-    return attn.q35_o(out)
+    return attn.q35_o.to_int32(out) if int32_out else attn.q35_o(out)
 
 
 def _attention_fast(attn, config: FusionConfig):
@@ -481,6 +500,48 @@ def prefill_layer(stack, index: int, residual: torch.Tensor, normalized: torch.T
     return (residual if last else summed), normalized
 
 
+def prefill_layer_a8w8(stack, index: int, residual: torch.Tensor, shape_of: torch.Tensor, quant,
+                       cache, position_embeddings, config: FusionConfig):
+    """``prefill_layer`` for A8W8 linears with the activations handed between
+    the int8 GEMMs in int8 form: the layer's input arrives quantised
+    (``quant`` = ``(xq, sx)``; ``shape_of`` gives its shape), each output
+    projection's int32 accumulators are dequantised inside the following
+    residual add + RMSNorm, which also quantises its output for the next
+    GEMM, and the MLP's SwiGLU quantises its activation directly. The same
+    bits as ``prefill_layer`` (each fused kernel keeps the separate kernels'
+    arithmetic). Returns ``(residual, normalised or None, quant or None)``:
+    after the last layer the final norm's bf16 output and no quant."""
+    layer = stack.layers[index]
+    if hasattr(layer, "linear_attn"):
+        acc, sx = _delta_prefill(layer.linear_attn, shape_of, cache, config, quant=quant,
+                                 int32_out=True)
+        out_w = layer.linear_attn.q35_out
+    else:
+        acc, sx = _attention_prefill(layer.self_attn, shape_of, position_embeddings, cache, config,
+                                     quant=quant, int32_out=True)
+        out_w = layer.self_attn.q35_o
+    ln = layer.post_attention_layernorm
+    residual, _, mq, ms = K.residual_rmsnorm_dequant_quant(residual, acc, sx, out_w.s, ln.weight, ln.eps)
+    gate_up, down = layer.mlp.q35_gate_up, layer.mlp.q35_down
+    aq, sa = K.dequant_swiglu_quant(K.a8w8_int_gemm(mq, gate_up.w), ms, gate_up.s)
+    acc = K.a8w8_int_gemm(aq, down.w)
+    last = index + 1 == stack.config.num_hidden_layers
+    norm = stack.norm if last else stack.layers[index + 1].input_layernorm
+    summed, normalized, nq, ns = K.residual_rmsnorm_dequant_quant(
+        residual, acc, sa, down.s, norm.weight, norm.eps, normalized=last, quant=not last)
+    if last:
+        return residual, normalized, None
+    return summed, None, (nq.view(shape_of.shape), ns)
+
+
+def _a8w8_prefill_ok(stack, config: FusionConfig, length: int) -> bool:
+    """The int8-handoff prefill applies: A8W8 packed projections on every
+    mixer and MLP, hidden width 2048, SwiGLU width <= 6144, and more than 16
+    tokens (fewer run on the int8 GEMV)."""
+    return (config.a8w8 and config.delta and config.attention and config.swiglu and length > 16
+            and stack.config.hidden_size == 2048 and stack.config.intermediate_size <= 6144)
+
+
 def _rope_positions(position_ids, past_seen: int, batch: int, length: int, device) -> torch.Tensor:
     """Positions the rotary embedding takes: Transformers' Qwen3.5 text model
     accepts ``[B, L]`` text positions, ``[3, B, L]`` rope rows or ``[4, B, L]``
@@ -542,8 +603,16 @@ def _text_fast(stack, config: FusionConfig):
             residual = embeds.contiguous()
             hidden = K.rms_norm(residual, stack.layers[0].input_layernorm.weight,
                                 stack.layers[0].input_layernorm.eps)
-            for i in range(n):
-                residual, hidden = prefill_layer(stack, i, residual, hidden, cache, rope, config)
+            if _a8w8_prefill_ok(stack, config, length):
+                xq, sx = K.quantize_act_i8(hidden)
+                quant = (xq, sx)
+                for i in range(n):
+                    residual, out, quant = prefill_layer_a8w8(stack, i, residual, hidden, quant, cache,
+                                                              rope, config)
+                hidden = out
+            else:
+                for i in range(n):
+                    residual, hidden = prefill_layer(stack, i, residual, hidden, cache, rope, config)
         return qwen_impl.Qwen3_5ModelOutputWithPast(last_hidden_state=hidden, past_key_values=cache)
     return fast
 

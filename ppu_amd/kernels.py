@@ -1156,6 +1156,92 @@ def a8w8_swiglu(x: torch.Tensor, weight_q: torch.Tensor, weight_scale: torch.Ten
     return y
 
 
+@_device_checked
+def a8w8_int_gemm(xq: torch.Tensor, weight_q: torch.Tensor) -> torch.Tensor:
+    """Exact int32 ``xq . Wq^T`` for prefill int8 activations ``[..., K]``
+    (the ROCm library's int8 GEMM): ``[rows, N]`` int32."""
+
+    k = xq.shape[-1]
+    if xq.dtype != torch.int8 or weight_q.dtype != torch.int8 or weight_q.shape[1] != k:
+        raise ValueError("int8 GEMM operands must be int8 [M,K] and [N,K]")
+    return torch._int_mm(xq.reshape(-1, k).contiguous(), weight_q.t())
+
+
+@_device_checked
+def dequant_linear_i32(acc: torch.Tensor, x_scale: torch.Tensor, weight_scale: torch.Tensor,
+                       shape: tuple[int, ...] | None = None) -> torch.Tensor:
+    """``bf16(float(acc) * s_x[m] * s_w[n])`` (the A8W8 dequant of reference
+    explore_runtime_quantization.py:173-180), reshaped to ``shape``."""
+
+    m, n = acc.shape
+    if acc.dtype != torch.int32 or not acc.is_contiguous() or n % 8:
+        raise ValueError("dequant expects contiguous int32 [M, N] accumulators, N % 8 == 0")
+    sx = x_scale.reshape(-1).float().contiguous()
+    sw = weight_scale.reshape(-1).float().contiguous()
+    if sx.numel() != m or sw.numel() != n:
+        raise ValueError("one activation scale per row and one weight scale per column")
+    y = torch.empty((m, n), device=acc.device, dtype=_BF16)
+    _lib.call("q35_dequant_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(), m, n,
+              _stream(acc))
+    return y if shape is None else y.reshape(*shape)
+
+
+@_device_checked
+def residual_rmsnorm_dequant_quant(residual: torch.Tensor, acc: torch.Tensor, x_scale: torch.Tensor,
+                                   weight_scale: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                                   *, normalized: bool = False, quant: bool = True):
+    """A8W8 prefill between two int8 GEMMs: ``residual + dequant(acc)`` (the
+    previous GEMM's output), RMSNorm with ``(1 + w)``, and the normalised rows
+    quantised per token for the next GEMM, in one launch with the separate
+    kernels' arithmetic (reference explore_runtime_quantization.py:167-180,
+    integration.py:456-499). Width 2048. Returns ``(residual_out,
+    normalised bf16 or None, int8 rows or None, fp32 row scales or None)``."""
+
+    rows, width = _rows_and_width(residual)
+    if width != 2048 or not (normalized or quant):
+        raise ValueError("width 2048, and at least one of normalized / quant")
+    if acc.dtype != torch.int32 or acc.shape != (rows, width) or not acc.is_contiguous():
+        raise ValueError("acc must be contiguous int32 [rows, 2048]")
+    _need_bf16(residual)
+    w, wf = _param(norm_weight)
+    sx = x_scale.reshape(-1).float().contiguous()
+    sw = weight_scale.reshape(-1).float().contiguous()
+    if sx.numel() != rows or sw.numel() != width:
+        raise ValueError("one activation scale per row and one weight scale per column")
+    x = residual.contiguous()
+    r_out = torch.empty_like(x)
+    y = torch.empty_like(x) if normalized else None
+    yq = torch.empty(x.shape, device=x.device, dtype=torch.int8) if quant else None
+    sy = torch.empty((rows, 1), device=x.device, dtype=torch.float32) if quant else None
+    _lib.call("q35_residual_rmsnorm_dequant_quant", x.data_ptr(), acc.data_ptr(), sx.data_ptr(),
+              sw.data_ptr(), w.data_ptr(), wf, r_out.data_ptr(), _lib.ptr(y), _lib.ptr(yq),
+              _lib.ptr(sy), rows, width, float(eps), _stream(x))
+    return r_out, y, yq, sy
+
+
+@_device_checked
+def dequant_swiglu_quant(acc: torch.Tensor, x_scale: torch.Tensor,
+                         weight_scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """A8W8 prefill MLP: the SwiGLU of the packed ``[gate; up]`` accumulators
+    ``acc[M, 2N]`` (dequantised as in ``a8w8_swiglu``), quantised per token
+    for the down projection: ``(int8 [M, N], fp32 [M, 1])``; the bf16
+    activation is never written (reference integration.py:183-187)."""
+
+    m, n2 = acc.shape
+    n = n2 // 2
+    if acc.dtype != torch.int32 or not acc.is_contiguous() or n2 % 16 or n > 6144:
+        raise ValueError("acc must be contiguous int32 [M, 2N], N % 8 == 0, N <= 6144")
+    sx = x_scale.reshape(-1).float().contiguous()
+    sw = weight_scale.reshape(-1).float().contiguous()
+    if sx.numel() != m or sw.numel() != n2:
+        raise ValueError("one activation scale per row and one weight scale per column")
+    yq = torch.empty((m, n), device=acc.device, dtype=torch.int8)
+    sy = torch.empty((m, 1), device=acc.device, dtype=torch.float32)
+    _lib.call("q35_dequant_swiglu_quant", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), yq.data_ptr(),
+              sy.data_ptr(), m, n, _stream(acc))
+    return yq, sy
+
+
 def _gemm_a8w8_into(xq, sx, weight_q, sw, y, *, swiglu, plan) -> None:
     m, k = xq.shape
     n = weight_q.shape[0] // 2 if swiglu else weight_q.shape[0]

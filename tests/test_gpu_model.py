@@ -144,6 +144,49 @@ def test_fused_cache_reset_matches_transformers(gpu):
     assert again.meta["cache_reused"] and again.tokens == first.tokens
 
 
+def test_a8w8_int8_handoff_prefill_equals_layer_chain(gpu):
+    """The A8W8 prefill that hands int8 activations and int32 accumulators
+    between the GEMMs (fused dequant / norm / quant kernels) leaves the same
+    bits as the layer-by-layer chain of separate kernels: final hidden state,
+    every conv and recurrent state and every K/V cache row."""
+    from transformers.cache_utils import StaticCache
+
+    from ppu_amd import kernels as K
+    from ppu_amd.integration import FusionConfig, prefill_layer, text_stack
+
+    cfg = synth.config_tiny()
+    model, _, _ = _build(cfg, gpu, FusionConfig(a8w8=True))
+    stack = text_stack(model)
+    g = torch.Generator().manual_seed(13)
+    prompt = torch.randint(0, cfg.vocab_size, (1, 90), generator=g).to(gpu)
+    pos = torch.arange(90, device=gpu).view(1, -1)
+    with torch.inference_mode():
+        c1 = StaticCache(config=model.config, max_cache_len=512)
+        fused = model.model(input_ids=prompt, position_ids=pos, past_key_values=c1,
+                            use_cache=True).last_hidden_state
+        c2 = StaticCache(config=model.config, max_cache_len=512)
+        embeds = stack.embed_tokens(prompt)
+        rope = stack.rotary_emb(embeds, pos)
+        residual = embeds.contiguous()
+        hidden = K.rms_norm(residual, stack.layers[0].input_layernorm.weight,
+                            stack.layers[0].input_layernorm.eps)
+        for i in range(cfg.num_hidden_layers):
+            residual, hidden = prefill_layer(stack, i, residual, hidden, c2, rope,
+                                             model._qwen35_fusion_config)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, hidden)
+    for a, b in zip(c1.layers, c2.layers):
+        for name in ("keys", "values", "conv_states", "recurrent_states"):
+            x, y = getattr(a, name, None), getattr(b, name, None)
+            if isinstance(x, torch.Tensor):
+                assert torch.equal(x, y), name
+            elif isinstance(x, (dict, list, tuple)):
+                keys = x.keys() if isinstance(x, dict) else range(len(x))
+                for key in keys:
+                    if isinstance(x[key], torch.Tensor):
+                        assert torch.equal(x[key], y[key]), name
+
+
 @pytest.mark.parametrize("a8w8", [False, True])
 def test_prefill_graph_matches_eager(gpu, a8w8):
     """A prompt length seen before runs its prefill as one captured graph:

@@ -846,6 +846,52 @@ def test_gemm_a8w8_swiglu(gpu, plan, m, n, k):
         assert torch.equal(K.a8w8_swiglu(x.to(gpu), wq, sw), exp)
 
 
+@pytest.mark.parametrize("rows", [1024, 37])
+@pytest.mark.parametrize("w_f32", [False, True])
+def test_residual_rmsnorm_dequant_quant(gpu, rows, w_f32):
+    """The fused A8W8 prefill row kernel gives the same bits as the separate
+    chain: dequant of the int32 accumulators -> residual add + RMSNorm ->
+    per-token int8 quantisation (and the bf16 rows when asked), a zero row
+    included."""
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 95)
+    acc = torch.randint(-2**20, 2**20, (rows, 2048), device=gpu, dtype=torch.int32, generator=g)
+    sx = torch.rand(rows, 1, device=gpu, generator=g) * 1e-3
+    sw = torch.rand(2048, device=gpu, generator=g) * 1e-3
+    res = torch.randn(rows, 2048, device=gpu, generator=g).to(BF)
+    nw = (torch.randn(2048, device=gpu, generator=g) * 0.05).to(torch.float32 if w_f32 else BF)
+    acc[rows // 2] = 0
+    res[rows // 2] = 0
+    upd = K.dequant_linear_i32(acc, sx, sw)
+    r_exp, y_exp = K.residual_add_rms_norm(res, upd, nw, 1e-6)
+    q_exp, s_exp = K.quantize_act_i8(y_exp)
+    r, y, q, sy = K.residual_rmsnorm_dequant_quant(res, acc, sx, sw, nw, 1e-6, normalized=True)
+    assert torch.equal(r, r_exp) and torch.equal(y, y_exp)
+    assert torch.equal(q, q_exp) and torch.equal(sy, s_exp)
+    r2, y2, q2, s2 = K.residual_rmsnorm_dequant_quant(res, acc, sx, sw, nw, 1e-6)
+    assert y2 is None and torch.equal(r2, r_exp) and torch.equal(q2, q_exp) and torch.equal(s2, s_exp)
+
+
+@pytest.mark.parametrize("m,n", [(1024, 6144), (300, 1024), (17, 200)])
+def test_dequant_swiglu_quant(gpu, m, n):
+    """SwiGLU of the packed gate/up accumulators quantised per token: the same
+    bits as q35_dequant_swiglu_i32 followed by the activation quantiser."""
+    from ppu_amd import _lib
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 96)
+    acc = torch.randint(-2**20, 2**20, (m, 2 * n), device=gpu, dtype=torch.int32, generator=g)
+    sx = torch.rand(m, 1, device=gpu, generator=g) * 1e-3
+    sw = torch.rand(2 * n, device=gpu, generator=g) * 1e-3
+    act = torch.empty((m, n), device=gpu, dtype=BF)
+    _lib.call("q35_dequant_swiglu_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), act.data_ptr(),
+              m, n, torch.cuda.current_stream().cuda_stream)
+    q_exp, s_exp = K.quantize_act_i8(act)
+    q, s = K.dequant_swiglu_quant(acc, sx, sw)
+    assert torch.equal(q, q_exp) and torch.equal(s, s_exp)
+
+
 @pytest.mark.parametrize("m,n,k", [(1024, 6144, 2048), (200, 500, 2048)])
 def test_gemm_swiglu_bf16(gpu, m, n, k):
     """Packed gate/up GEMM with the SwiGLU epilogue vs F.linear + silu_and_mul
