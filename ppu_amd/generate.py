@@ -23,7 +23,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .graph import GreedyDecodeGraph
-from .integration import lm_head_screen
+from .integration import lm_head_screen, text_stack
 from .kernels import lm_head_argmax, zero_tensors
 
 
@@ -112,12 +112,19 @@ class PrefillGraph:
         self.token = torch.zeros((1, 1), device=device, dtype=torch.long)
         saved = _cache_flags(cache)
         screen = lm_head_screen(model)
+        # the rotary table depends only on the (fixed) positions: for a text
+        # model it is computed once, outside the graph, and kept alive with it
+        extra = {}
+        if text_stack(model) is model.model:
+            stack = model.model
+            self.rope = stack.rotary_emb(stack.embed_tokens.weight[:1], self.positions)
+            extra["position_embeddings"] = self.rope
         torch.cuda.synchronize(device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             reset_cache(cache)
             out = model.model(input_ids=self.ids, position_ids=self.positions, past_key_values=cache,
-                              use_cache=True, return_dict=True)
+                              use_cache=True, return_dict=True, **extra)
             lm_head_argmax(out.last_hidden_state[:, -1, :].contiguous(), model.lm_head.weight,
                            out=self.token, screen=screen)
         self.flags = _cache_flags(cache)  # host state after a prefill

@@ -599,7 +599,9 @@ def _text_fast(stack, config: FusionConfig):
             _, hidden = K.residual_add_rms_norm(residual, update, stack.norm.weight, stack.norm.eps)
         else:
             embeds = inputs_embeds if inputs_embeds is not None else stack.embed_tokens(input_ids)
-            rope = stack.rotary_emb(embeds, rope_pos)
+            rope = kwargs.get("position_embeddings")  # (cos, sin) computed by the caller
+            if rope is None:
+                rope = stack.rotary_emb(embeds, rope_pos)
             residual = embeds.contiguous()
             hidden = K.rms_norm(residual, stack.layers[0].input_layernorm.weight,
                                 stack.layers[0].input_layernorm.eps)
