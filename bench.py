@@ -497,7 +497,10 @@ def trace_summary(kind: str, trace_csv: str, bench_json: str) -> None:
             out.append(f"#   {k:72s} n={n:3d} total {t:8.1f} us  avg {t / n:7.2f} us")
         return out
 
-    ends = [i for i, r in enumerate(rows) if "top1_final" in r["Kernel_Name"]]
+    # a greedy token ends with top1_final, or with the rescore of the screened
+    # top-1 (which reduces the candidates itself)
+    ends = [i for i, r in enumerate(rows)
+            if "top1_final" in r["Kernel_Name"] or "lm_head_rescore" in r["Kernel_Name"]]
     v = d.get("variants", {}).get("a8w8", {})
     lines = []
     if kind == "decode":
