@@ -378,6 +378,32 @@ int q35_dequant_swiglu_quant(const void* acc, const void* s_x, const void* s_w, 
 int q35_dequant_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,
                     void* stream);
 
+/* ---------------------------------------------------------- vision encoder */
+/* Vision LayerNorm over rows of `width`: y = bf16((x - mean) * rsqrt(var +
+ * eps) * w + b), mean and variance in fp32; w and b both bf16 or both fp32
+ * (p_f32). Replaces layer_norm (kernels.py:1186-1218). */
+int q35_layernorm(const void* x, const void* w, const void* b, int p_f32, void* y, int rows,
+                  int width, float eps, void* stream);
+/* residual_out = bf16(residual + update); y = q35_layernorm(residual_out).
+ * Replaces residual_add_layer_norm (kernels.py:1221-1280). */
+int q35_residual_layernorm(const void* residual, const void* update, const void* w, const void* b,
+                           int p_f32, void* residual_out, void* y, int rows, int width, float eps,
+                           void* stream);
+/* out[r] = bf16(hidden[r] + bf16(sum_n table[indices[r, n]] * weights[r, n])),
+ * the sum an fp32 FMA chain in neighbour order; indices int64 [rows,
+ * neighbors] (clamped to [0, table_rows)), weights fp32 or bf16 (w_f32).
+ * Replaces position_embed_add (kernels.py:1283-1336). */
+int q35_position_embed_add(const void* hidden, const void* table, int table_rows,
+                           const void* indices, const void* weights, int w_f32, void* out, int rows,
+                           int width, int neighbors, void* stream);
+/* packed [tokens, 3*heads*dim] = [q heads | k heads | v heads] per token ->
+ * q, k, v [1, heads, tokens, dim]; q and k get rotate-half RoPE in fp32
+ * (x*cos + (sign*x_partner)*sin, partner = c +- dim/2), cos/sin [tokens, dim]
+ * fp32 or bf16 (cs_f32); dim even. Replaces vision_qkv_rope
+ * (kernels.py:336-416). */
+int q35_vision_qkv_rope(const void* packed, const void* cos, const void* sin, int cs_f32, void* q,
+                        void* k, void* v, int tokens, int heads, int dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

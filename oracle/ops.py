@@ -22,7 +22,16 @@ Pinning (tests/test_oracle.py):
   gqa_decode_attention, prefill_attention — fp64 textbook softmax attention,
       split invariance;
   lm_head_argmax — brute force F.linear + argmax, the all-zero tie (index 0)
-      and planted duplicate maxima.
+      and planted duplicate maxima;
+  layer_norm, residual_add_layer_norm — against torch's F.layer_norm in fp64
+      on the same inputs (one bf16 rounding of the output apart), constant
+      rows (output = bias) and mean/scale invariance;
+  position_embed_add — against Transformers 5.15.0's weighted
+      pos_embed(indices) sum (Qwen3_5VisionModel.forward; unfused products,
+      so one bf16 ulp of the position term apart) and one-hot weights (an
+      exact table row);
+  vision_qkv_rope — bit-exact against Transformers 5.15.0
+      apply_rotary_pos_emb_vision, and cos = 1, sin = 0 (identity).
 """
 
 from __future__ import annotations
@@ -286,3 +295,54 @@ def rotary_cos_sin(positions: torch.Tensor, rotary_dim: int = 64, theta: float =
     freqs = torch.gather(freqs, 0, row.view(1, 1, 1, -1).expand(1, *freqs.shape[1:]))[0]
     emb = torch.cat((freqs, freqs), dim=-1)
     return _bf(emb.cos()), _bf(emb.sin())
+
+
+# ---------------------------------------------------------------- vision
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+               eps: float = 1e-6) -> torch.Tensor:
+    """reference kernels.py:1186-1218: mean and variance of the fp32 row,
+    bf16((x - mean) * rsqrt(var + eps) * w + b)."""
+    xf = _f(x)
+    mean = xf.sum(-1, keepdim=True) / xf.shape[-1]
+    c = xf - mean
+    var = (c * c).sum(-1, keepdim=True) / xf.shape[-1]
+    return _bf(c * _rsqrt(var + eps) * _f(weight) + _f(bias))
+
+
+def residual_add_layer_norm(residual, update, weight, bias, eps: float = 1e-6):
+    """reference kernels.py:1221-1280: r' = bf16(r + u), then layer_norm(r')."""
+    added = _bf(_f(residual) + _f(update))
+    return added, layer_norm(added, weight, bias, eps)
+
+
+def position_embed_add(hidden, table, indices, weights):
+    """reference kernels.py:1283-1336: p = sum_n table[idx_n] * w_n as an fp32
+    multiply-add chain in neighbour order (the kernel's `position +=
+    embedding * weight`, contracted to one fused multiply-add by Triton's
+    default fp fusion), out = bf16(hidden + bf16(p)). Each fused step is
+    computed in fp64 (the fp32 product is exact there) and rounded to fp32."""
+    pos = torch.zeros(hidden.shape, dtype=torch.float32)
+    for n in range(indices.shape[-1]):
+        e = table[indices[:, n]].to(torch.float64)
+        w = _f(weights[:, n : n + 1]).to(torch.float64)
+        pos = (e * w + pos.to(torch.float64)).to(torch.float32)
+    return _bf(_f(hidden) + _f(_bf(pos)))
+
+
+def vision_qkv_rope(packed, cos, sin, *, heads: int, dim: int):
+    """reference kernels.py:336-416: packed [T, 3*H*D] -> q, k, v [1, H, T, D];
+    q and k get x*cos + rotate_half(x)*sin in fp32 (no fused multiply-add),
+    rounded to bf16; v is copied."""
+    tokens = packed.shape[0]
+    parts = packed.reshape(tokens, 3, heads, dim)
+    c = _f(cos)[:, None, :]
+    s = _f(sin)[:, None, :]
+    half = dim // 2
+
+    def rope(x):
+        xf = _f(x)
+        rot = torch.cat((-xf[..., half:], xf[..., :half]), dim=-1)
+        return _bf(xf * c + rot * s).permute(1, 0, 2).unsqueeze(0).contiguous()
+
+    v = parts[:, 2].permute(1, 0, 2).unsqueeze(0).contiguous()
+    return rope(parts[:, 0]), rope(parts[:, 1]), v

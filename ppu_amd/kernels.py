@@ -1329,21 +1329,120 @@ def stream_read(buf: torch.Tensor) -> torch.Tensor:
     return out[: blocks.value * 256]
 
 
-# ------------------------------------------------------------------ out of scope
-def _vision_out_of_scope(name: str):
-    def fn(*args, **kwargs):
-        raise NotImplementedError(
-            f"{name} belongs to the vision encoder, which this MI355X build does not implement"
-        )
-
-    fn.__name__ = name
-    return fn
+# ------------------------------------------------------------------ vision
+def _param_pair(a: torch.Tensor, b: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, int]:
+    """Two parameter vectors in one dtype (bf16 if both are, else fp32)."""
+    if a.dtype == _BF16 and b.dtype == _BF16:
+        return a.contiguous(), b.contiguous(), 0
+    return a.float().contiguous(), b.float().contiguous(), 1
 
 
-layer_norm = _vision_out_of_scope("layer_norm")
-residual_add_layer_norm = _vision_out_of_scope("residual_add_layer_norm")
-position_embed_add = _vision_out_of_scope("position_embed_add")
-vision_qkv_rope = _vision_out_of_scope("vision_qkv_rope")
+@_device_checked
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+               eps: float = 1e-6) -> torch.Tensor:
+    """Vision LayerNorm ``(x - mean) * rsqrt(var + eps) * w + b`` over the last
+    dimension, fp32 statistics, bf16 output. reference kernels.py:1209-1218."""
+
+    rows, width = _rows_and_width(x)
+    if weight.numel() != width or bias.numel() != width:
+        raise ValueError(f"layer norm parameters must have {width} values")
+    _need_bf16(x)
+    w, b, pf = _param_pair(weight, bias)
+    out = torch.empty_like(x)
+    _lib.call("q35_layernorm", x.data_ptr(), w.data_ptr(), b.data_ptr(), pf, out.data_ptr(), rows,
+              width, float(eps), _stream(x))
+    return out
+
+
+@_device_checked
+def residual_add_layer_norm(
+    residual: torch.Tensor,
+    update: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    eps: float = 1e-6,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``r' = bf16(residual + update)`` and ``layer_norm(r')``; returns
+    ``(r', norm)``. reference kernels.py:1249-1280."""
+
+    if residual.shape != update.shape:
+        raise ValueError("vision residual tensors must have identical shape")
+    rows, width = _rows_and_width(residual)
+    if not update.is_contiguous():
+        raise ValueError("fused kernels require contiguous input")
+    if weight.numel() != width or bias.numel() != width:
+        raise ValueError(f"layer norm parameters must have {width} values")
+    _need_bf16(residual, update)
+    w, b, pf = _param_pair(weight, bias)
+    residual_out = torch.empty_like(residual)
+    norm_out = torch.empty_like(residual)
+    _lib.call("q35_residual_layernorm", residual.data_ptr(), update.data_ptr(), w.data_ptr(),
+              b.data_ptr(), pf, residual_out.data_ptr(), norm_out.data_ptr(), rows, width,
+              float(eps), _stream(residual))
+    return residual_out, norm_out
+
+
+@_device_checked
+def position_embed_add(
+    hidden: torch.Tensor,
+    embedding_table: torch.Tensor,
+    indices: torch.Tensor,
+    interpolation_weight: torch.Tensor,
+) -> torch.Tensor:
+    """``hidden + bf16(sum_n table[indices[:, n]] * weight[:, n])``: the
+    interpolated vision position embedding (fp32 sum over the neighbours).
+    Indices outside the table are clamped to it. reference kernels.py:1309-1336."""
+
+    if hidden.ndim != 2 or not hidden.is_contiguous():
+        raise ValueError("vision hidden tensor must be contiguous [rows,width]")
+    rows, width = hidden.shape
+    neighbors = indices.shape[-1]
+    if indices.shape != interpolation_weight.shape or indices.shape[0] != rows:
+        raise ValueError("position interpolation tensors do not match hidden rows")
+    if embedding_table.ndim != 2 or embedding_table.shape[1] != width:
+        raise ValueError(f"position embedding table must be [positions,{width}]")
+    _need_bf16(hidden, embedding_table)
+    table = embedding_table.contiguous()
+    idx = indices.to(torch.int64).contiguous()
+    wt, wf = _param(interpolation_weight)
+    out = torch.empty_like(hidden)
+    _lib.call("q35_position_embed_add", hidden.data_ptr(), table.data_ptr(), table.shape[0],
+              idx.data_ptr(), wt.data_ptr(), wf, out.data_ptr(), rows, width, neighbors,
+              _stream(hidden))
+    return out
+
+
+@_device_checked
+def vision_qkv_rope(
+    packed_qkv: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    *,
+    heads: int,
+    dim: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Packed vision QKV ``[tokens, 3*heads*dim]`` -> q, k, v ``[1, heads,
+    tokens, dim]`` with rotate-half RoPE (``cos``/``sin`` ``[tokens, dim]``) on
+    q and k in fp32, bf16 out. reference kernels.py:378-416."""
+
+    if packed_qkv.ndim != 2 or not packed_qkv.is_contiguous():
+        raise ValueError("packed Vision QKV must be contiguous [tokens,3*hidden]")
+    tokens, packed_width = packed_qkv.shape
+    if packed_width != 3 * heads * dim:
+        raise ValueError(f"packed Vision QKV width {packed_width}, expected {3 * heads * dim}")
+    if cos.shape != (tokens, dim) or sin.shape != cos.shape:
+        raise ValueError(f"Vision RoPE shape {tuple(cos.shape)}, expected {(tokens, dim)}")
+    if dim % 2:
+        raise ValueError("vision head dim must be even")
+    _need_bf16(packed_qkv)
+    c, s, cf = _param_pair(cos, sin)
+    shape = (1, heads, tokens, dim)
+    q = torch.empty(shape, device=packed_qkv.device, dtype=packed_qkv.dtype)
+    k = torch.empty_like(q)
+    v = torch.empty_like(q)
+    _lib.call("q35_vision_qkv_rope", packed_qkv.data_ptr(), c.data_ptr(), s.data_ptr(), cf,
+              q.data_ptr(), k.data_ptr(), v.data_ptr(), tokens, heads, dim, _stream(packed_qkv))
+    return q, k, v
 
 
 @_device_checked

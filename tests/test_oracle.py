@@ -364,3 +364,79 @@ def test_oracle_reproduces_golden_vectors():
     ulp_close(q, bf("qg_q"))
     ulp_close(k, bf("qg_k"))
     assert int(ref.lm_head_argmax(bf("lm_h"), bf("lm_w"))) == int(data["lm_idx"])
+
+
+# ---------------------------------------------------------------- vision
+@pytest.mark.parametrize("width", [64, 1152])
+def test_layer_norm_matches_fp64_and_invariants(width):
+    g = gen(KERNEL_SEED)
+    x = randn(g, 9, width, scale=2.0, mean=0.5)
+    w = randn(g, width, scale=0.1, mean=1.0)
+    b = randn(g, width, scale=0.1)
+    got = ref.layer_norm(x, w, b)
+    exp = F.layer_norm(x.double(), (width,), w.double(), b.double(), eps=1e-6)
+    # one bf16 rounding of the output apart
+    torch.testing.assert_close(got.double(), exp, rtol=2 ** -8, atol=1e-5)
+    # a constant row normalises to exactly the bias
+    const = torch.full((2, width), 3.0).to(BF)
+    assert torch.equal(ref.layer_norm(const, w, b), b.expand(2, width))
+    # shift invariance: x and x + 1 (exact in bf16 here) give the same output
+    xs = torch.randint(-8, 8, (3, width), generator=g).to(BF)
+    torch.testing.assert_close(ref.layer_norm(xs + 1, w, b).float(), ref.layer_norm(xs, w, b).float(),
+                               rtol=2 ** -7, atol=1e-3)
+
+
+def test_residual_add_layer_norm_is_add_then_norm():
+    g = gen(KERNEL_SEED)
+    r = randn(g, 5, 256)
+    u = randn(g, 5, 256)
+    w = randn(g, 256, scale=0.1, mean=1.0)
+    b = randn(g, 256, scale=0.1)
+    added, normed = ref.residual_add_layer_norm(r, u, w, b)
+    assert torch.equal(added, (r.float() + u.float()).to(BF))
+    exp = F.layer_norm(added.double(), (256,), w.double(), b.double(), eps=1e-6)
+    torch.testing.assert_close(normed.double(), exp, rtol=2 ** -8, atol=1e-5)
+
+
+def test_position_embed_add_matches_transformers_sum():
+    from transformers.vision_utils import get_vision_interpolation_indices_and_weights
+
+    g = gen(KERNEL_SEED)
+    side, width = 8, 64
+    table = randn(g, side * side, width, scale=0.5)
+    grid = torch.tensor([[1, 6, 4]])
+    idx, wts = get_vision_interpolation_indices_and_weights(
+        grid, num_grid_per_side=side, mode="bilinear", align_corners=True, spatial_merge_size=2)
+    hidden = randn(g, idx.shape[0], width)
+    got = ref.position_embed_add(hidden, table, idx, wts)
+    # Qwen3_5VisionModel.forward: (pos_embed(indices) * weights[:, :, None]).sum(1), cast, added
+    emb = torch.nn.functional.embedding(idx, table.float())
+    pos = (emb * wts.float()[:, :, None]).sum(1).to(BF)
+    exp = (hidden.float() + pos.float()).to(BF)
+    ulp_close(got, exp, frac_exact=0.98)
+    # one-hot weights select the table row exactly
+    one = torch.zeros_like(wts)
+    one[:, 2] = 1.0
+    got1 = ref.position_embed_add(torch.zeros_like(hidden), table, idx, one)
+    assert torch.equal(got1, table[idx[:, 2]])
+
+
+def test_vision_qkv_rope_matches_transformers():
+    m = tf_impl()
+    g = gen(KERNEL_SEED)
+    tokens, heads, dim = 10, 4, 72
+    packed = randn(g, tokens, 3 * heads * dim)
+    ang = torch.randn(tokens, dim // 2, generator=g)
+    emb = torch.cat((ang, ang), dim=-1)
+    cos, sin = emb.cos(), emb.sin()
+    q, k, v = ref.vision_qkv_rope(packed, cos, sin, heads=heads, dim=dim)
+    qs, ks, vs = packed.reshape(tokens, 3, heads, dim).permute(1, 0, 2, 3).unbind(0)
+    qe, ke = m.apply_rotary_pos_emb_vision(qs, ks, cos, sin)
+    assert torch.equal(q, qe.transpose(0, 1).unsqueeze(0))
+    assert torch.equal(k, ke.transpose(0, 1).unsqueeze(0))
+    assert torch.equal(v, vs.transpose(0, 1).unsqueeze(0))
+    # cos = 1, sin = 0 is the identity on q and k
+    q1, k1, _ = ref.vision_qkv_rope(packed, torch.ones(tokens, dim), torch.zeros(tokens, dim),
+                                    heads=heads, dim=dim)
+    assert torch.equal(q1, qs.transpose(0, 1).unsqueeze(0))
+    assert torch.equal(k1, ks.transpose(0, 1).unsqueeze(0))
