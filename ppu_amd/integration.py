@@ -619,12 +619,146 @@ def _text_fast(stack, config: FusionConfig):
     return fast
 
 
+# ----------------------------------------------------------------- vision
+def _vision_sdpa(q, k, v, scale: float, segments) -> torch.Tensor:
+    """Non-causal attention of ``[1, H, T, D]`` q/k/v, per image segment
+    (``None``: one image). Only the fused SDPA backends are allowed: the math
+    backend's batched bf16 product with a transposed key is kept off this GPU."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        if segments is None:
+            return sdpa(q, k, v, scale=scale)
+        return torch.cat([sdpa(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], scale=scale)
+                          for a, b in segments], dim=2)
+
+
+def _vision_attention(attn, x: torch.Tensor, cos, sin, segments) -> torch.Tensor:
+    """One vision block's attention (reference integration.py:644-735): the
+    packed QKV projection, the split + RoPE kernel straight into
+    ``[1, heads, tokens, dim]``, non-causal attention, output projection."""
+    tokens = x.shape[0]
+    packed = attn.qkv(x).contiguous()
+    q, k, v = K.vision_qkv_rope(packed, cos, sin, heads=attn.num_heads, dim=attn.head_dim)
+    out = _vision_sdpa(q, k, v, attn.scaling, segments)
+    return attn.proj(out.transpose(1, 2).reshape(tokens, -1).contiguous())
+
+
+def _vision_blocks(visual, patches, interp_indices, interp_weights, position_ids, segments):
+    """Position embedding, rotary table and every vision block for the patch
+    rows of one call (reference integration.py:514-562): the residual stream
+    stays bf16, each block's second norm and the next block's first norm run
+    as residual-add + LayerNorm launches."""
+    hidden = K.position_embed_add(patches, visual.pos_embed.weight, interp_indices, interp_weights)
+    tokens = hidden.shape[0]
+    freqs = visual.rotary_pos_emb(position_ids).reshape(tokens, -1)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    cos, sin = emb.cos(), emb.sin()
+    blocks = visual.blocks
+    n1 = blocks[0].norm1
+    normed = K.layer_norm(hidden, n1.weight, n1.bias, n1.eps)
+    residual = hidden
+    for i, blk in enumerate(blocks):
+        update = _vision_attention(blk.attn, normed, cos, sin, segments)
+        residual, mlp_in = K.residual_add_layer_norm(residual, update.contiguous(), blk.norm2.weight,
+                                                     blk.norm2.bias, blk.norm2.eps)
+        mlp_out = blk.mlp(mlp_in).contiguous()
+        if i + 1 < len(blocks):
+            nxt = blocks[i + 1].norm1
+            residual, normed = K.residual_add_layer_norm(residual, mlp_out, nxt.weight, nxt.bias, nxt.eps)
+        else:
+            residual = residual + mlp_out
+    return residual
+
+
+class _VisionGraph:
+    """The vision blocks for one patch count captured as a graph over static
+    inputs (reference integration.py:587-632): the first call of a size runs
+    eagerly and captures; later calls copy their inputs in and replay."""
+
+    def __init__(self, visual, patches, interp_indices, interp_weights, position_ids) -> None:
+        self.inputs = [t.contiguous().clone() for t in (patches, interp_indices, interp_weights,
+                                                        position_ids)]
+        torch.cuda.synchronize(patches.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = _vision_blocks(visual, *self.inputs, None)
+
+    def run(self, *inputs) -> torch.Tensor:
+        for dst, src in zip(self.inputs, inputs):
+            dst.copy_(src)
+        self.graph.replay()
+        return self.out
+
+
+def _vision_model_fast(visual, config: FusionConfig):
+    graphs: dict[int, _VisionGraph] = {}
+
+    def fast(hidden_states, grid_thw=None, **kwargs):
+        if (grid_thw is None or not hidden_states.is_cuda or not _gpu_bf16(visual.pos_embed.weight)
+                or kwargs.get("output_attentions") or kwargs.get("output_hidden_states")):
+            return NotImplemented
+        kw = dict(kwargs)
+        idx, wts = qwen_impl.get_vision_interpolation_indices_and_weights(
+            grid_thw, num_grid_per_side=visual.num_grid_per_side, mode=visual.interpolation_mode,
+            align_corners=visual.interpolation_align_corners,
+            spatial_merge_size=visual.config.spatial_merge_size, kwargs=kw)
+        position_ids = qwen_impl.get_vision_position_ids(grid_thw, visual.spatial_merge_size, kwargs=kw)
+        cu_seqlens, _ = qwen_impl.get_vision_attention_seqlens(grid_thw, visual.config, kwargs=kw)
+        patches = visual.patch_embed(hidden_states).contiguous()
+        device = patches.device
+        idx, wts, position_ids = idx.to(device), wts.to(device), position_ids.to(device)
+        single = cu_seqlens.numel() == 2
+        segments = None
+        if not single:
+            bounds = cu_seqlens.tolist()
+            segments = list(zip(bounds[:-1], bounds[1:]))
+        entry = graphs.get(patches.shape[0]) if config.vision_graph and single else None
+        if entry is not None:
+            # a copy: the graph's output buffer is overwritten by the next replay
+            hidden = entry.run(patches, idx, wts, position_ids).clone()
+        else:
+            hidden = _vision_blocks(visual, patches, idx.contiguous(), wts.contiguous(),
+                                    position_ids.contiguous(), segments)
+            if (config.vision_graph and single and len(graphs) < config.vision_graph_max_entries
+                    and not torch.cuda.is_current_stream_capturing()):
+                graphs[patches.shape[0]] = _VisionGraph(visual, patches, idx, wts, position_ids)
+        return qwen_impl.BaseModelOutputWithPooling(last_hidden_state=hidden,
+                                                    pooler_output=visual.merger(hidden))
+    return fast
+
+
+def _vision_tower(model: torch.nn.Module):
+    inner = getattr(model, "model", None)
+    return getattr(inner, "visual", None)
+
+
 # ----------------------------------------------------------------- entry points
 def precompute_vision_kwargs(model: torch.nn.Module, inputs: Any) -> Any:
-    """reference integration.py:738-775. The vision encoder is outside this
-    build: for text-only inputs (no ``image_grid_thw``) the mapping is returned
-    unchanged, and image inputs go to Transformers' own vision path, which
-    computes these tensors itself."""
+    """reference integration.py:738-775: for an image input (``image_grid_thw``
+    present), add the vision tower's interpolation indices / weights, rotary
+    position ids and sequence bounds under the ``image_``-prefixed names that
+    Transformers' ``get_image_features`` hands to the vision forward, so they
+    are computed once on the processor output (CPU) and travel with
+    ``inputs.to(device)``. Text-only inputs are returned unchanged."""
+    grid = inputs.get("image_grid_thw")
+    if grid is None:
+        return inputs
+    visual = _vision_tower(model)
+    sink: dict[str, Any] = {}
+    idx, wts = qwen_impl.get_vision_interpolation_indices_and_weights(
+        grid, num_grid_per_side=visual.num_grid_per_side, mode=visual.interpolation_mode,
+        align_corners=visual.interpolation_align_corners,
+        spatial_merge_size=visual.config.spatial_merge_size, kwargs=sink)
+    position_ids = qwen_impl.get_vision_position_ids(grid, visual.spatial_merge_size, kwargs=sink)
+    cu_seqlens, max_seqlen = qwen_impl.get_vision_attention_seqlens(grid, visual.config, kwargs=sink)
+    inputs["image_interp_indices"] = idx
+    inputs["image_interp_weights"] = wts
+    inputs["image_position_ids"] = position_ids
+    inputs["image_cu_seqlens"] = cu_seqlens
+    if max_seqlen is not None:
+        inputs["image_max_seqlen"] = max_seqlen
     return inputs
 
 
@@ -697,6 +831,10 @@ def install(model: torch.nn.Module, config: FusionConfig,
         _take_over(stack.norm, _norm_fast(stack.norm))
     if config.residual_norm:
         _take_over(stack, _text_fast(stack, config))
+    visual = _vision_tower(model)
+    if config.vision and visual is not None:
+        _take_over(visual, _vision_model_fast(visual, config))
+        stats["vision"] = len(visual.blocks)
     model._qwen35_fusion_config = config
     stats["lm_head_screen"] = int(config.lm_head_screen and attach_lm_head_screen(model))
     stats["delta_precompute_factors"] = int(config.delta and config.delta_precompute_factors)

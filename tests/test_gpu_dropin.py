@@ -4,9 +4,9 @@
   reference's fused greedy generation (evaluation_wrapper.py:307-419) on the
   image-text model class, through the ``qwen35_fused`` import names:
   ``apply_fusions``, ``precompute_vision_kwargs``, a bucketed StaticCache,
-  ``model.model(**inputs)`` prefill with an image (Transformers' own vision
-  tower; the text stack receives ``inputs_embeds`` and 3-row multimodal
-  positions), ``lm_head_argmax``, the ``rope_deltas`` position arithmetic, one
+  ``model.model(**inputs)`` prefill with an image (the vision tower on the
+  fused vision path; the text stack receives ``inputs_embeds`` and 3-row
+  multimodal positions), ``lm_head_argmax``, the ``rope_deltas`` position arithmetic, one
   eager decode step and ``GreedyDecodeGraph`` replays. The text path is checked
   against the oracle decoder on the embeddings and positions the text stack
   received.

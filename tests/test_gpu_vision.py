@@ -11,6 +11,8 @@ multiply-add on either side) bit-exact.
 
 from __future__ import annotations
 
+import copy
+
 import pytest
 import torch
 
@@ -133,3 +135,92 @@ def test_vision_ops_reject_bad_shapes(gpu):
                           torch.zeros(4, 8, device=gpu), heads=2, dim=16)
     with pytest.raises(ValueError):
         K.layer_norm(x.cpu(), torch.ones(64), torch.zeros(64))
+
+
+# ------------------------------------------------------------- vision tower
+def _vision_setup(gpu):
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as impl
+
+    from ppu_amd import synth
+
+    vision = dict(depth=2, hidden_size=128, intermediate_size=256, num_heads=4, in_channels=3,
+                  patch_size=16, spatial_merge_size=2, temporal_patch_size=2,
+                  out_hidden_size=64, num_position_embeddings=64)
+    cfg = synth.config_vlm(vision_config=vision)
+    model = synth.build_model(cfg, device=gpu)
+    # fp32 CPU copy of the tower with Transformers' own forward (eager attention)
+    vcfg = copy.deepcopy(model.model.visual.config)
+    vcfg._attn_implementation = "eager"
+    ref_tower = impl.Qwen3_5VisionModel(vcfg).float().eval()
+    ref_tower.load_state_dict({k: v.float().cpu() for k, v in model.model.visual.state_dict().items()})
+    ref_tower.rotary_pos_emb.inv_freq.copy_(model.model.visual.rotary_pos_emb.inv_freq.cpu())
+    return cfg, model, ref_tower
+
+
+def _pixels(cfg, grid, seed):
+    vc = cfg.vision_config
+    g = torch.Generator().manual_seed(seed)
+    n = int(grid.prod(-1).sum())
+    return torch.randn(n, vc.in_channels * vc.temporal_patch_size * vc.patch_size ** 2, generator=g)
+
+
+def _rel(a, b):
+    a, b = a.detach().float().cpu(), b.detach().float().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def test_vision_tower_matches_transformers_and_graph_replays(gpu):
+    """The fused vision forward (our LayerNorm / position-embedding / RoPE
+    kernels, library GEMMs, fused SDPA) against Transformers' fp32 CPU forward
+    of the same weights; the second call of a patch count replays the captured
+    graph and every replay (with eager work in between) equals the eager call."""
+    from qwen35_fused.integration import apply_fusions
+
+    cfg, model, ref_tower = _vision_setup(gpu)
+    stats = apply_fusions(model)
+    assert stats["vision"] == 2
+    grid = torch.tensor([[1, 8, 12]])
+    pix = _pixels(cfg, grid, 11)
+    with torch.inference_mode():
+        exp = ref_tower(pix, grid_thw=grid)
+        first = model.model.visual(pix.to(gpu, torch.bfloat16), grid_thw=grid.to(gpu))
+        # bf16 path against the fp32 reference: relative L2 error of the outputs
+        assert _rel(first.last_hidden_state, exp.last_hidden_state) < 2e-2
+        assert _rel(first.pooler_output, exp.pooler_output) < 2e-2
+        base_h = first.last_hidden_state.clone()
+        base_p = first.pooler_output.clone()
+        for r in range(3):
+            other = model.model.visual(_pixels(cfg, grid, 100 + r).to(gpu, torch.bfloat16),
+                                       grid_thw=grid.to(gpu))
+            torch.cuda.synchronize()
+            again = model.model.visual(pix.to(gpu, torch.bfloat16), grid_thw=grid.to(gpu))
+            assert torch.equal(again.last_hidden_state, base_h)
+            assert torch.equal(again.pooler_output, base_p)
+            assert not torch.equal(other.last_hidden_state, base_h)
+
+
+def test_vision_tower_two_images_and_precomputed_kwargs(gpu):
+    """Two images in one call (attention per image, no graph) and the
+    precomputed tensors of precompute_vision_kwargs give the same output as
+    computing them inside the forward."""
+    from transformers import BatchFeature
+
+    from qwen35_fused.integration import apply_fusions, precompute_vision_kwargs
+
+    cfg, model, ref_tower = _vision_setup(gpu)
+    apply_fusions(model)
+    grid = torch.tensor([[1, 8, 8], [1, 4, 6]])
+    pix = _pixels(cfg, grid, 12)
+    with torch.inference_mode():
+        exp = ref_tower(pix, grid_thw=grid)
+        got = model.model.visual(pix.to(gpu, torch.bfloat16), grid_thw=grid.to(gpu))
+        assert _rel(got.last_hidden_state, exp.last_hidden_state) < 2e-2
+        assert _rel(got.pooler_output, exp.pooler_output) < 2e-2
+        inputs = precompute_vision_kwargs(model, BatchFeature({"image_grid_thw": grid}))
+        for name in ("image_interp_indices", "image_interp_weights", "image_position_ids",
+                     "image_cu_seqlens"):
+            assert name in inputs
+        pre = {k[len("image_"):]: (v.to(gpu) if isinstance(v, torch.Tensor) else v)
+               for k, v in inputs.items() if k.startswith("image_") and k != "image_grid_thw"}
+        got2 = model.model.visual(pix.to(gpu, torch.bfloat16), grid_thw=grid.to(gpu), **pre)
+        assert torch.equal(got2.last_hidden_state, got.last_hidden_state)
