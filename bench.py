@@ -686,6 +686,54 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def vision_tower_timing(dev) -> dict:
+    """The vision tower (Transformers' default Qwen3.5 vision config: 27 blocks,
+    1152 wide, 16 heads) on one 448x448 image (28x28 patches), seeded random
+    bf16 weights: Transformers' own forward against the fused forward (eager
+    first call, then the captured graph), and their output difference."""
+    import torch
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as impl
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5VisionConfig
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from ppu_amd import integration
+
+    cfg = Qwen3_5VisionConfig()
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(20260625)
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        tower = impl.Qwen3_5VisionModel(cfg)
+    finally:
+        torch.set_default_dtype(old)
+    hd = cfg.hidden_size // cfg.num_heads // 2
+    tower.rotary_pos_emb.inv_freq = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    tower = tower.to(dev).eval()
+    grid = torch.tensor([[1, 28, 28]], device=dev)
+    pix = torch.randn(784, cfg.in_channels * cfg.temporal_patch_size * cfg.patch_size ** 2,
+                      device=dev).to(torch.bfloat16)
+
+    def timed(fn, reps=10):
+        fn(); torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            out = fn()
+        e1.record(); e1.synchronize()
+        return e0.elapsed_time(e1) / reps, out
+
+    with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        t_ref, ref = timed(lambda: tower(pix, grid_thw=grid).pooler_output)
+        integration._take_over(tower, integration._vision_model_fast(tower, integration.FusionConfig()))
+        t_fused, got = timed(lambda: tower(pix, grid_thw=grid).pooler_output)
+    rel = ((got.float() - ref.float()).norm() / ref.float().norm()).item()
+    log(f"vision tower 784 patches: Transformers {t_ref:.3f} ms, fused {t_fused:.3f} ms, rel diff {rel:.2e}")
+    return {"workload": "Qwen3.5 vision tower (27 x 1152, 16 heads), one 448x448 image (784 patches), bf16",
+            "transformers_ms": round(t_ref, 3), "fused_graph_ms": round(t_fused, 3),
+            "pooler_rel_l2_vs_transformers": round(rel, 5)}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -699,6 +747,7 @@ def main() -> None:
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     ap.add_argument("--cpu-prompt", type=int, default=PROMPT_LEN, help="prompt length of the CPU sample")
     ap.add_argument("--no-eager", action="store_true", help="skip the Transformers-eager CPU timing")
+    ap.add_argument("--no-vision", action="store_true", help="skip the vision-tower timing")
     ap.add_argument("--trace-summary", nargs=3, metavar=("decode|prefill", "TRACE_CSV", "BENCH_JSON"),
                     help="per-kernel anatomy of a rocprofv3 kernel trace of this bench, then exit")
     ap.add_argument("--gemm-sweep", action="store_true",
@@ -844,6 +893,11 @@ def main() -> None:
         del m2
         torch.cuda.empty_cache()
 
+    vision = None
+    if not args.no_vision:
+        vision = vision_tower_timing(dev)
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         log("CPU baseline ...")
@@ -875,6 +929,7 @@ def main() -> None:
         "roofline_detail": {"swiglu_gemv": roof, "lm_head": lm},
         "step_roofline": main_res["step_roofline"],
         "kernels": kernels,
+        "vision_tower": vision,
         "cpu_baseline": cpu,
         "inputs_sha256": _digest_report(digests),
     }
