@@ -403,6 +403,16 @@ int q35_position_embed_add(const void* hidden, const void* table, int table_rows
  * (kernels.py:336-416). */
 int q35_vision_qkv_rope(const void* packed, const void* cos, const void* sin, int cs_f32, void* q,
                         void* k, void* v, int tokens, int heads, int dim, void* stream);
+/* Non-causal attention of the vision blocks: q, k, v [heads, tokens, dim]
+ * (bf16, 16-byte aligned, dim % 8 == 0, dim <= 128), each query over the keys
+ * of its own image (cu_seqlens: n_images + 1 int32 offsets, or null for one
+ * image), fp32 softmax, P rounded to bf16 for the P.V product; out [tokens,
+ * heads*dim] bf16. No counterpart among the reference's kernels: it replaces
+ * the Transformers attention-interface call of the vision attention
+ * (integration.py:671-731). */
+int q35_vision_attention(const void* q, const void* k, const void* v, void* out,
+                         const void* cu_seqlens, int n_images, int tokens, int heads, int dim,
+                         float scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,7 +31,9 @@ Pinning (tests/test_oracle.py):
       so one bf16 ulp of the position term apart) and one-hot weights (an
       exact table row);
   vision_qkv_rope — bit-exact against Transformers 5.15.0
-      apply_rotary_pos_emb_vision, and cos = 1, sin = 0 (identity).
+      apply_rotary_pos_emb_vision, and cos = 1, sin = 0 (identity);
+  vision_attention — against torch's scaled_dot_product_attention in fp64
+      per image, and a one-key image (output = its value row).
 """
 
 from __future__ import annotations
@@ -346,3 +348,17 @@ def vision_qkv_rope(packed, cos, sin, *, heads: int, dim: int):
 
     v = parts[:, 2].permute(1, 0, 2).unsqueeze(0).contiguous()
     return rope(parts[:, 0]), rope(parts[:, 1]), v
+
+
+def vision_attention(q, k, v, scale: float, cu_seqlens=None):
+    """Non-causal attention per image (the Transformers attention interface
+    the reference's vision attention calls, integration.py:671-731): fp32
+    softmax(q k^T * scale) v over each image's tokens, bf16 out, [T, H*D]."""
+    _, heads, tokens, dim = q.shape
+    bounds = [0, tokens] if cu_seqlens is None else [int(x) for x in cu_seqlens]
+    out = torch.empty(tokens, heads, dim, dtype=torch.float32)
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        qs, ks, vs = (_f(t[0, :, a:b]) for t in (q, k, v))
+        w = torch.softmax(qs @ ks.transpose(-1, -2) * scale, dim=-1)
+        out[a:b] = (w @ vs).permute(1, 0, 2)
+    return _bf(out.reshape(tokens, heads * dim))

@@ -30,6 +30,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_residual_layernorm": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _F, _P]),
     "q35_position_embed_add": (_I, [_P, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P]),
     "q35_vision_qkv_rope": (_I, [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P]),
+    "q35_vision_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
     "q35_rmsnorm": (_I, [_P, _P, _I, _P, _I, _I, _F, _P]),
     "q35_residual_rmsnorm": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P]),
     "q35_gated_rmsnorm": (_I, [_P, _P, _P, _I, _P, _I, _I, _F, _P]),

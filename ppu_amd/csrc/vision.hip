@@ -234,6 +234,296 @@ __global__ __launch_bounds__(256) void vision_qkv_rope_rows(
   }
 }
 
+
+// ------------------------------------------------------ vision attention
+// Non-causal multi-head attention of the vision blocks on the matrix cores
+// (v_mfma_f32_16x16x32_bf16), one workgroup per (64 query rows, head), four
+// waves of 16 rows each; keys in blocks of 64 staged once in LDS for all four
+// waves (double buffered, the next block loaded into registers while the
+// current one is computed). Head dims D (D % 8 == 0, D <= 128) are zero-padded
+// to 32 QT (QT = ceil(D / 32)) in Q's registers and K's LDS rows; O has
+// OT = ceil(D / 16) tiles of 16 dims. Both are template parameters: a tile
+// count known only at run time put O behind branches, and the compiler then
+// copied the whole accumulator array at each one. Per block and
+// wave: S = Q K^T (4 x QT MFMAs), online softmax in fp32 (DPP row
+// reductions), P rounded to bf16 and written transposed to LDS, then O += P V
+// with P and V reaching the MFMA through the gfx950 transpose read
+// ds_read_b64_tr_b16 (the operand layouts and lane mapping of the causal
+// prefill kernel). Queries only see keys of their own image: image i holds
+// tokens [cu[i], cu[i+1]). Output rows go straight to [T, H*D], the layout the
+// output projection reads.
+typedef short q35_i16x4v __attribute__((ext_vector_type(4)));
+Q35_DEV uint2 va_read_tr16(const uint16_t* p) {
+  const q35_i16x4v v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) q35_i16x4v*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+Q35_DEV q35_f32x4 va_mfma(const uint4 a, const uint4 b, q35_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(q35_bf16x8, a),
+                                                 __builtin_bit_cast(q35_bf16x8, b), c, 0, 0, 0);
+}
+
+typedef uint32_t va_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kVaKeys = 64;    // keys per block
+constexpr int kVaRows = 64;    // query rows per workgroup
+constexpr int kVaPt = 16 + 4;  // padded P^T row (16 query rows)
+
+// Image bounds [start, end) of token t (cu: n + 1 ascending offsets; none:
+// one image of T tokens).
+Q35_DEV void va_segment(const int* cu, int n, int T, int t, int& s0, int& s1) {
+  s0 = 0;
+  s1 = T;
+  if (!cu) return;
+  for (int i = 0; i < n; ++i) {
+    const int a = cu[i], b = cu[i + 1];
+    if (t >= a && t < b) {
+      s0 = a;
+      s1 = b;
+    }
+  }
+}
+
+// One key block of one wave: S = Q K^T for its 16 rows x 64 keys, the online
+// softmax in base 2 (c = scale * log2(e) folded into one FMA per score; m is
+// kept in unscaled score units), bf16 P^T through the wave's LDS tile, then
+// O += P V. MASK: some key of the block lies outside a row's image (keys
+// outside get p = 0). lp holds this lane's partial row sums (the row sum is
+// one 16-lane reduction at the end).
+template <int QT, int OT, bool MASK>
+Q35_DEV void va_block(const uint16_t* __restrict__ Ks, const uint16_t* __restrict__ Vs,
+                      uint16_t* __restrict__ pt, const uint4 (&qa)[QT], q35_f32x4 (&o)[OT],
+                      float (&m)[4], float (&lp)[4], int kb, const int (&s0)[4],
+                      const int (&s1)[4], float c, int col, int kg, int te, int tq) {
+  constexpr int RS = 32 * QT + 8;
+  q35_f32x4 s[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    s[st] = {0.f, 0.f, 0.f, 0.f};
+    const uint16_t* krow = Ks + (16 * st + col) * RS + 8 * kg;
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+      s[st] = va_mfma(qa[t], *reinterpret_cast<const uint4*>(krow + 32 * t), s[st]);
+  }
+  float corr[4], p[4][4];
+  bool moved = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float sv[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      sv[st] = s[st][i];
+      if (MASK) {
+        const int key = kb + 16 * st + col;
+        if (key < s0[i] || key >= s1[i]) sv[st] = -INFINITY;
+      }
+    }
+    const float m_new =
+        fmaxf(m[i], row16_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))));
+    // A row with no key of its image so far keeps m = -inf: offset 0 then.
+    const float mc = (MASK && m_new == -INFINITY) ? 0.f : m_new * c;
+    moved |= m_new != m[i];
+    corr[i] = __builtin_amdgcn_exp2f(fmaf(m[i], c, -mc));
+    float ps = 0.f;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      p[st][i] = __builtin_amdgcn_exp2f(fmaf(sv[st], c, -mc));
+      ps += p[st][i];
+    }
+    lp[i] = fmaf(lp[i], corr[i], ps);
+    m[i] = m_new;
+  }
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const int off = (16 * st + col) * kVaPt + 4 * kg;
+    *reinterpret_cast<uint2*>(pt + off) =
+        make_uint2(pack_bf2(p[st][0], p[st][1]), pack_bf2(p[st][2], p[st][3]));
+  }
+  // Rescale O only when some row's maximum moved (corr == 1 otherwise).
+  if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+    for (int d = 0; d < OT; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[d][i] *= corr[i];
+  }
+  // O += P V over the two 32-key halves; the wave's own LDS stores above
+  // complete before its reads (LDS operations of a wave execute in order).
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const uint16_t* pth = pt + 32 * half * kVaPt;
+    const uint2 a0 = va_read_tr16(pth + (8 * kg + te) * kVaPt + 4 * tq);
+    const uint2 a1 = va_read_tr16(pth + (8 * kg + 4 + te) * kVaPt + 4 * tq);
+    const uint4 pa = make_uint4(a0.x, a0.y, a1.x, a1.y);
+    const uint16_t* v0 = Vs + (32 * half + 8 * kg + te) * RS + 4 * tq;
+    const uint16_t* v1 = Vs + (32 * half + 8 * kg + 4 + te) * RS + 4 * tq;
+#pragma unroll
+    for (int d = 0; d < OT; ++d) {
+      const uint2 b0 = va_read_tr16(v0 + 16 * d), b1 = va_read_tr16(v1 + 16 * d);
+      o[d] = va_mfma(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), o[d]);
+    }
+  }
+}
+
+template <int QT, int OT>
+__global__ __launch_bounds__(256) void vision_attn_fa(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    uint16_t* __restrict__ out, const int* __restrict__ cu, int nseg, int T, int H, int D,
+    float scale) {
+  static_assert(QT >= 1 && QT <= 4 && (OT == 2 * QT || OT == 2 * QT - 1), "head dim tiles");
+  constexpr int DP = 32 * QT;          // padded head dim
+  constexpr int RS = DP + 8;           // LDS row stride (elements): rows 16-byte aligned
+  constexpr int NLD = (kVaKeys * DP / 8 + 255) / 256;  // 16-byte K (and V) chunks per thread
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // Workgroup -> (query tile, head): with heads a multiple of 8 the tiles of a
+  // head share one residue mod 8 (one XCD, whose L2 then serves the head's
+  // K/V to all of them); otherwise tiles fastest.
+  const int ntiles = (T + kVaRows - 1) / kVaRows;
+  int h, tile;
+  if (H % 8 == 0) {
+    const int slot = (int)blockIdx.x >> 3;
+    h = ((int)blockIdx.x & 7) + 8 * (slot / ntiles);
+    tile = slot % ntiles;
+  } else {
+    h = (int)blockIdx.x / ntiles;
+    tile = (int)blockIdx.x % ntiles;
+  }
+  const int qwg = tile * kVaRows;
+  const int qw0 = qwg + 16 * wid;
+  const int col = lane & 15, kg = lane >> 4;
+  const int te = (lane & 15) >> 2, tq = lane & 3;
+  const int ch = D / 8;            // 16-byte chunks per row
+  const float c = scale * 1.4426950408889634f;
+  const size_t hb = (size_t)h * T * D;
+
+  // Key range of the workgroup: images are contiguous, so the union of its
+  // rows' images is [image start of its first row, image end of its last).
+  int kbeg, kend, tmp;
+  va_segment(cu, nseg, T, qwg, kbeg, tmp);
+  va_segment(cu, nseg, T, min(qwg + kVaRows, T) - 1, tmp, kend);
+  const int nblk = (kend - kbeg + kVaKeys - 1) / kVaKeys;
+  int s0[4], s1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) va_segment(cu, nseg, T, min(qw0 + 4 * kg + i, T - 1), s0[i], s1[i]);
+  // Keys every row of the wave may see: [latest image start, earliest end).
+  int w0, w1;
+  va_segment(cu, nseg, T, min(qw0 + 15, T - 1), w0, tmp);
+  va_segment(cu, nseg, T, min(qw0, T - 1), tmp, w1);
+
+  uint4 qa[QT];
+  {
+    const uint16_t* qrow = q + hb + (size_t)min(qw0 + col, T - 1) * D;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int d0 = 32 * t + 8 * kg;
+      qa[t] = d0 < D ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  __shared__ alignas(16) uint16_t kv_s[2][2][kVaKeys * RS];  // [buf][K, V][key][dim]
+  __shared__ alignas(16) uint16_t pt_s[4][kVaKeys * kVaPt];  // [wave][key][row]
+  // Zero the padded dims [D, RS) of every K and V row once: they meet the
+  // zero-padded Q dims in S (0 * finite) and only unused output dims in O.
+  const int pad = RS - D;
+  for (int i = tid; i < 2 * 2 * kVaKeys * pad; i += 256) {
+    const int row = i / pad, cc = D + i % pad;
+    (&kv_s[0][0][0])[row * RS + cc] = 0;
+  }
+
+  // This thread's 16-byte chunks of a block: chunk gi = tid + 256 j is key
+  // row gi / ch, dims 8 * (gi % ch); only chunks gi < 64 * ch exist.
+  int lrow[NLD], lcol[NLD];
+  bool lok[NLD];
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) {
+    const int gi = tid + 256 * j;
+    lok[j] = gi < kVaKeys * ch;
+    lrow[j] = lok[j] ? gi / ch : 0;
+    lcol[j] = lok[j] ? 8 * (gi % ch) : 0;
+  }
+  // Native vector registers (a uint4 struct copy between global memory, the
+  // arrays and LDS stays a memory copy and put the arrays in scratch).
+  va_u32x4 kr0[NLD], vr0[NLD], kr1[NLD], vr1[NLD];
+  // Loads are clamped into the workgroup's key range and the head's rows (a
+  // range that malformed image offsets left empty reads row 0, never used).
+  auto va_load = [&](va_u32x4 (&kr)[NLD], va_u32x4 (&vr)[NLD], int b) {
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int key = max(min(min(kbeg + b * kVaKeys + lrow[j], kend - 1), T - 1), 0);
+      const size_t off = hb + (size_t)key * D + lcol[j];
+      kr[j] = *reinterpret_cast<const va_u32x4*>(k + off);
+      vr[j] = *reinterpret_cast<const va_u32x4*>(v + off);
+    }
+  };
+  auto va_store = [&](const va_u32x4 (&kr)[NLD], const va_u32x4 (&vr)[NLD], int buf) {
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      if (lok[j]) {
+        const int off = lrow[j] * RS + lcol[j];
+        *reinterpret_cast<va_u32x4*>(&kv_s[buf][0][off]) = kr[j];
+        *reinterpret_cast<va_u32x4*>(&kv_s[buf][1][off]) = vr[j];
+      }
+    }
+  };
+#define VA_BLOCK(BUF, BLK)                                                                \
+  do {                                                                                    \
+    const int kb = kbeg + (BLK) * kVaKeys;                                                \
+    if (kb >= w0 && kb + kVaKeys <= w1)                                                   \
+      va_block<QT, OT, false>(kv_s[BUF][0], kv_s[BUF][1], pt, qa, o, m, lp, kb, s0, s1,  \
+                              c, col, kg, te, tq);                                        \
+    else                                                                                  \
+      va_block<QT, OT, true>(kv_s[BUF][0], kv_s[BUF][1], pt, qa, o, m, lp, kb, s0, s1,   \
+                             c, col, kg, te, tq);                                         \
+  } while (0)
+
+  q35_f32x4 o[OT];
+#pragma unroll
+  for (int d = 0; d < OT; ++d) o[d] = {0.f, 0.f, 0.f, 0.f};
+  float m[4], lp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    lp[i] = 0.f;
+  }
+  uint16_t* pt = pt_s[wid];
+
+  // Two register sets and two LDS buffers: at the top of an iteration LDS
+  // buffer 0 holds block blk and set 1 block blk + 1; block blk + 2 is
+  // requested into set 0 while blk is computed. Loads past the last block
+  // reload it (unconditional: a conditional load here made the compiler keep
+  // the chunks in scratch memory).
+  va_load(kr0, vr0, 0);
+  va_store(kr0, vr0, 0);
+  va_load(kr1, vr1, min(1, nblk - 1));
+  lds_barrier();
+  int blk = 0;
+  for (; blk + 1 < nblk; blk += 2) {
+    va_load(kr0, vr0, min(blk + 2, nblk - 1));
+    VA_BLOCK(0, blk);
+    va_store(kr1, vr1, 1);
+    lds_barrier();
+    va_load(kr1, vr1, min(blk + 3, nblk - 1));
+    VA_BLOCK(1, blk + 1);
+    va_store(kr0, vr0, 0);
+    lds_barrier();
+  }
+  if (blk < nblk) VA_BLOCK(0, blk);
+#undef VA_BLOCK
+  const size_t ostride = (size_t)H * D;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float l = row16_sum(lp[i]);
+    const int r = qw0 + 4 * kg + i;
+    if (r < T) {
+      const float inv = 1.0f / l;
+      uint16_t* orow = out + (size_t)r * ostride + (size_t)h * D;
+#pragma unroll
+      for (int d = 0; d < OT; ++d) {
+        const int dim = 16 * d + col;
+        if (dim < D) orow[dim] = (uint16_t)f2bf(o[d][i] * inv);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -281,6 +571,35 @@ int q35_vision_qkv_rope(const void* packed, const void* cos, const void* sin, in
   vision_qkv_rope_rows<<<grid, 256, 0, stream>>>((const uint16_t*)packed, cos, sin, cs_f32,
                                                 (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, tokens,
                                                 heads, dim);
+  return q35_last_error();
+}
+
+int q35_vision_attention(const void* q, const void* k, const void* v, void* out,
+                         const void* cu_seqlens, int n_images, int tokens, int heads, int dim,
+                         float scale, hipStream_t stream) {
+  Q35_CHECK_ARG(tokens >= 0 && heads > 0 && dim > 0 && dim % 8 == 0 && dim <= 128);
+  Q35_CHECK_ARG(q && k && v && out && (!cu_seqlens || n_images > 0));
+  Q35_CHECK_ARG(q35_aligned16(q) && q35_aligned16(k) && q35_aligned16(v));
+  Q35_CHECK_ARG((long long)heads * tokens * dim < (1ll << 31));
+  if (tokens == 0) return 0;
+  const unsigned grid = (unsigned)((tokens + kVaRows - 1) / kVaRows) * (unsigned)heads;
+  const int* cu = (const int*)cu_seqlens;
+  const uint16_t *qs = (const uint16_t*)q, *ks = (const uint16_t*)k, *vs = (const uint16_t*)v;
+  uint16_t* os = (uint16_t*)out;
+  const int qt = (dim + 31) / 32, ot = (dim + 15) / 16;
+#define VA_LAUNCH(QT_, OT_) \
+  vision_attn_fa<QT_, OT_><<<grid, 256, 0, stream>>>(qs, ks, vs, os, cu, n_images, tokens, heads, dim, scale)
+  switch (qt * 8 + ot) {
+    case 1 * 8 + 1: VA_LAUNCH(1, 1); break;
+    case 1 * 8 + 2: VA_LAUNCH(1, 2); break;
+    case 2 * 8 + 3: VA_LAUNCH(2, 3); break;
+    case 2 * 8 + 4: VA_LAUNCH(2, 4); break;
+    case 3 * 8 + 5: VA_LAUNCH(3, 5); break;
+    case 3 * 8 + 6: VA_LAUNCH(3, 6); break;
+    case 4 * 8 + 7: VA_LAUNCH(4, 7); break;
+    default: VA_LAUNCH(4, 8); break;
+  }
+#undef VA_LAUNCH
   return q35_last_error();
 }
 

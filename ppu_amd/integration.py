@@ -637,19 +637,50 @@ def _vision_sdpa(q, k, v, scale: float, segments) -> torch.Tensor:
 def _vision_attention(attn, x: torch.Tensor, cos, sin, segments) -> torch.Tensor:
     """One vision block's attention (reference integration.py:644-735): the
     packed QKV projection, the split + RoPE kernel straight into
-    ``[1, heads, tokens, dim]``, non-causal attention, output projection."""
+    ``[1, heads, tokens, dim]``, non-causal attention per image on the
+    matrix-core kernel (``vision_attention``, head dims that are multiples of
+    8 up to 128; PyTorch's fused SDPA otherwise), output projection."""
     tokens = x.shape[0]
     packed = attn.qkv(x).contiguous()
     q, k, v = K.vision_qkv_rope(packed, cos, sin, heads=attn.num_heads, dim=attn.head_dim)
+    if attn.head_dim % 8 == 0 and attn.head_dim <= 128:
+        cu = None if segments is None else torch.tensor([0] + [b for _, b in segments],
+                                                        dtype=torch.int32, device=x.device)
+        return attn.proj(K.vision_attention(q, k, v, attn.scaling, cu))
     out = _vision_sdpa(q, k, v, attn.scaling, segments)
     return attn.proj(out.transpose(1, 2).reshape(tokens, -1).contiguous())
 
 
-def _vision_blocks(visual, patches, interp_indices, interp_weights, position_ids, segments):
-    """Position embedding, rotary table and every vision block for the patch
-    rows of one call (reference integration.py:514-562): the residual stream
-    stays bf16, each block's second norm and the next block's first norm run
-    as residual-add + LayerNorm launches."""
+def _patch_embed(visual, pixels: torch.Tensor) -> torch.Tensor:
+    """The patch embedding as one GEMM: its Conv3d has kernel = stride = one
+    (temporal x patch x patch) block, so each output row is the flattened
+    block times the flattened filter bank (same products, one launch instead
+    of an im2col per patch)."""
+    proj = visual.patch_embed.proj
+    w = proj.weight
+    x = pixels.reshape(-1, w[0].numel()).to(w.dtype)
+    return torch.nn.functional.linear(x, w.reshape(w.shape[0], -1), proj.bias)
+
+
+def _vision_merger(merger, hidden: torch.Tensor) -> torch.Tensor:
+    """Qwen3_5VisionPatchMerger: LayerNorm (before or after the spatial
+    shuffle), then fc1 -> GELU -> fc2 on groups of merged rows."""
+    width = merger.hidden_size
+    if merger.use_postshuffle_norm:
+        x = K.layer_norm(hidden.reshape(-1, width).contiguous(), merger.norm.weight, merger.norm.bias,
+                         merger.norm.eps)
+    else:
+        x = K.layer_norm(hidden, merger.norm.weight, merger.norm.bias, merger.norm.eps).reshape(-1, width)
+    return merger.linear_fc2(merger.act_fn(merger.linear_fc1(x)))
+
+
+def _vision_forward(visual, pixels, interp_indices, interp_weights, position_ids, segments):
+    """The whole tower for the patches of one call (reference
+    integration.py:514-562 plus the patch embedding and the merger): position
+    embedding, rotary table, every block (the residual stream stays bf16; each
+    block's second norm and the next block's first norm run as residual-add +
+    LayerNorm launches), merger. Returns (last hidden state, merged rows)."""
+    patches = _patch_embed(visual, pixels).contiguous()
     hidden = K.position_embed_add(patches, visual.pos_embed.weight, interp_indices, interp_weights)
     tokens = hidden.shape[0]
     freqs = visual.rotary_pos_emb(position_ids).reshape(tokens, -1)
@@ -669,31 +700,32 @@ def _vision_blocks(visual, patches, interp_indices, interp_weights, position_ids
             residual, normed = K.residual_add_layer_norm(residual, mlp_out, nxt.weight, nxt.bias, nxt.eps)
         else:
             residual = residual + mlp_out
-    return residual
+    return residual, _vision_merger(visual.merger, residual)
 
 
 class _VisionGraph:
-    """The vision blocks for one patch count captured as a graph over static
-    inputs (reference integration.py:587-632): the first call of a size runs
-    eagerly and captures; later calls copy their inputs in and replay."""
+    """The tower for one patch count captured as a graph over static inputs
+    (reference integration.py:587-632): the first call of a size runs eagerly
+    and captures; later calls copy their inputs in and replay. Outputs are
+    returned as copies (the next replay overwrites the graph's buffers)."""
 
-    def __init__(self, visual, patches, interp_indices, interp_weights, position_ids) -> None:
-        self.inputs = [t.contiguous().clone() for t in (patches, interp_indices, interp_weights,
+    def __init__(self, visual, pixels, interp_indices, interp_weights, position_ids) -> None:
+        self.inputs = [t.contiguous().clone() for t in (pixels, interp_indices, interp_weights,
                                                         position_ids)]
-        torch.cuda.synchronize(patches.device)
+        torch.cuda.synchronize(pixels.device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.out = _vision_blocks(visual, *self.inputs, None)
+            self.out = _vision_forward(visual, *self.inputs, None)
 
-    def run(self, *inputs) -> torch.Tensor:
+    def run(self, *inputs) -> tuple[torch.Tensor, torch.Tensor]:
         for dst, src in zip(self.inputs, inputs):
             dst.copy_(src)
         self.graph.replay()
-        return self.out
+        return self.out[0].clone(), self.out[1].clone()
 
 
 def _vision_model_fast(visual, config: FusionConfig):
-    graphs: dict[int, _VisionGraph] = {}
+    graphs: dict[tuple, _VisionGraph] = {}
 
     def fast(hidden_states, grid_thw=None, **kwargs):
         if (grid_thw is None or not hidden_states.is_cuda or not _gpu_bf16(visual.pos_embed.weight)
@@ -706,26 +738,26 @@ def _vision_model_fast(visual, config: FusionConfig):
             spatial_merge_size=visual.config.spatial_merge_size, kwargs=kw)
         position_ids = qwen_impl.get_vision_position_ids(grid_thw, visual.spatial_merge_size, kwargs=kw)
         cu_seqlens, _ = qwen_impl.get_vision_attention_seqlens(grid_thw, visual.config, kwargs=kw)
-        patches = visual.patch_embed(hidden_states).contiguous()
-        device = patches.device
-        idx, wts, position_ids = idx.to(device), wts.to(device), position_ids.to(device)
+        device = hidden_states.device
+        pixels = hidden_states.to(visual.patch_embed.proj.weight.dtype).contiguous()
+        idx = idx.to(device).contiguous()
+        wts = wts.to(device).contiguous()
+        position_ids = position_ids.to(device).contiguous()
         single = cu_seqlens.numel() == 2
         segments = None
         if not single:
             bounds = cu_seqlens.tolist()
             segments = list(zip(bounds[:-1], bounds[1:]))
-        entry = graphs.get(patches.shape[0]) if config.vision_graph and single else None
+        key = (tuple(pixels.shape), wts.dtype)
+        entry = graphs.get(key) if config.vision_graph and single else None
         if entry is not None:
-            # a copy: the graph's output buffer is overwritten by the next replay
-            hidden = entry.run(patches, idx, wts, position_ids).clone()
+            hidden, merged = entry.run(pixels, idx, wts, position_ids)
         else:
-            hidden = _vision_blocks(visual, patches, idx.contiguous(), wts.contiguous(),
-                                    position_ids.contiguous(), segments)
+            hidden, merged = _vision_forward(visual, pixels, idx, wts, position_ids, segments)
             if (config.vision_graph and single and len(graphs) < config.vision_graph_max_entries
                     and not torch.cuda.is_current_stream_capturing()):
-                graphs[patches.shape[0]] = _VisionGraph(visual, patches, idx, wts, position_ids)
-        return qwen_impl.BaseModelOutputWithPooling(last_hidden_state=hidden,
-                                                    pooler_output=visual.merger(hidden))
+                graphs[key] = _VisionGraph(visual, pixels, idx, wts, position_ids)
+        return qwen_impl.BaseModelOutputWithPooling(last_hidden_state=hidden, pooler_output=merged)
     return fast
 
 

@@ -1446,6 +1446,36 @@ def vision_qkv_rope(
 
 
 @_device_checked
+def vision_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                     cu_seqlens: torch.Tensor | None = None) -> torch.Tensor:
+    """Non-causal attention of the vision blocks: q, k, v ``[1, heads, tokens,
+    dim]`` (``vision_qkv_rope``'s outputs), each query attending to the keys
+    of its own image (``cu_seqlens``: image offsets ``[n + 1]``; None: one
+    image). Returns ``[tokens, heads*dim]`` bf16, the output projection's
+    input. No counterpart in the reference's kernel API: it replaces the
+    Transformers attention-interface call of reference integration.py:671-731."""
+
+    if q.ndim != 4 or q.shape[0] != 1 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("vision attention expects q, k, v of shape [1, heads, tokens, dim]")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("fused kernels require contiguous input")
+    _, heads, tokens, dim = q.shape
+    if dim % 8 or dim > 128:
+        raise ValueError("vision attention supports head dims that are multiples of 8 up to 128")
+    _need_bf16(q, k, v)
+    cu, n = None, 0
+    if cu_seqlens is not None:
+        cu = cu_seqlens.to(torch.int32).contiguous()
+        n = cu.numel() - 1
+        if n < 1:
+            raise ValueError("cu_seqlens needs at least two offsets")
+    out = torch.empty((tokens, heads * dim), device=q.device, dtype=q.dtype)
+    _lib.call("q35_vision_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+              _lib.ptr(cu), n, tokens, heads, dim, float(scale), _stream(q))
+    return out
+
+
+@_device_checked
 def sigmoid_mul(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
     """``x * bf16(sigmoid(gate))`` (reference kernels.py:266-282; unused by the
     reference integration). Expressed through the attention-gate kernel with a

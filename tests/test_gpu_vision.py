@@ -224,3 +224,34 @@ def test_vision_tower_two_images_and_precomputed_kwargs(gpu):
                for k, v in inputs.items() if k.startswith("image_") and k != "image_grid_thw"}
         got2 = model.model.visual(pix.to(gpu, torch.bfloat16), grid_thw=grid.to(gpu), **pre)
         assert torch.equal(got2.last_hidden_state, got.last_hidden_state)
+
+
+@pytest.mark.parametrize("tokens,heads,dim", [(784, 16, 72), (100, 4, 64), (257, 2, 80), (64, 3, 128),
+                                              (5, 2, 8), (130, 1, 96)])
+def test_vision_attention_one_image(gpu, tokens, heads, dim):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 5)
+    q, k, v = (randn(g, 1, heads, tokens, dim) for _ in range(3))
+    got = K.vision_attention(q.to(gpu), k.to(gpu), v.to(gpu), dim ** -0.5)
+    exp = ref.vision_attention(q, k, v, dim ** -0.5)
+    assert got.shape == (tokens, heads * dim)
+    # P is rounded to bf16 before the P.V product (as fused attention kernels do)
+    torch.testing.assert_close(got.float().cpu(), exp.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("bounds", [[0, 64, 100, 257], [0, 1, 130, 131], [0, 200, 257]])
+def test_vision_attention_per_image(gpu, bounds):
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 6)
+    heads, dim, tokens = 4, 72, bounds[-1]
+    q, k, v = (randn(g, 1, heads, tokens, dim, scale=2.0) for _ in range(3))
+    cu = torch.tensor(bounds, dtype=torch.int32)
+    got = K.vision_attention(q.to(gpu), k.to(gpu), v.to(gpu), dim ** -0.5, cu.to(gpu))
+    exp = ref.vision_attention(q, k, v, dim ** -0.5, cu)
+    torch.testing.assert_close(got.float().cpu(), exp.float(), rtol=1e-2, atol=1e-2)
+    # a one-token image returns its value row exactly
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        if b - a == 1:
+            assert torch.equal(got[a].cpu().reshape(heads, dim), v[0, :, a])

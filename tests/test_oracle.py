@@ -440,3 +440,18 @@ def test_vision_qkv_rope_matches_transformers():
                                     heads=heads, dim=dim)
     assert torch.equal(q1, qs.transpose(0, 1).unsqueeze(0))
     assert torch.equal(k1, ks.transpose(0, 1).unsqueeze(0))
+
+
+def test_vision_attention_matches_sdpa_per_image():
+    g = gen(KERNEL_SEED)
+    heads, tokens, dim = 3, 11, 16
+    q, k, v = (randn(g, 1, heads, tokens, dim) for _ in range(3))
+    cu = torch.tensor([0, 4, 10, 11])
+    got = ref.vision_attention(q, k, v, dim ** -0.5, cu)
+    for a, b in ((0, 4), (4, 10), (10, 11)):
+        exp = F.scaled_dot_product_attention(q[:, :, a:b].double(), k[:, :, a:b].double(),
+                                             v[:, :, a:b].double(), scale=dim ** -0.5)
+        torch.testing.assert_close(got[a:b].double(), exp[0].permute(1, 0, 2).reshape(b - a, -1),
+                                   rtol=2 ** -8, atol=1e-5)
+    # a one-token image attends to itself only
+    assert torch.equal(got[10].reshape(heads, dim), v[0, :, 10])
