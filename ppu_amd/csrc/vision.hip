@@ -41,25 +41,50 @@ Q35_DEV void param8(const void* p, int k, int f32, float* o) {
   }
 }
 
+// Native 16-byte register vector: a uint4 struct held in an array and copied
+// can stay a memory copy (scratch); these stay in registers.
+typedef uint32_t vz_u32x4 __attribute__((ext_vector_type(4)));
+
+Q35_DEV vz_u32x4 ld16(const void* p) { return *reinterpret_cast<const vz_u32x4*>(p); }
+Q35_DEV uint4 as_u4(vz_u32x4 v) { return __builtin_bit_cast(uint4, v); }
+
 // LayerNorm of rows of width <= NJ * 512 (width % 8 == 0): lane l holds the
 // 8-element groups k = 512 j + 8 l. Groups past the width read group 0 of
-// the row (in bounds) and are left out of the sums and the stores.
-template <bool RESIDUAL, int NJ>
+// the row (in bounds) and are left out of the sums and the stores. The
+// weight and bias groups are requested together with the row, so they are in
+// registers when the two reductions end (PF32: fp32 parameters).
+template <bool RESIDUAL, int NJ, bool PF32>
 __global__ __launch_bounds__(256) void layernorm_rows_vec(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ u, const void* __restrict__ w,
-    const void* __restrict__ b, int p_f32, uint16_t* __restrict__ r_out, uint16_t* __restrict__ y,
+    const void* __restrict__ b, uint16_t* __restrict__ r_out, uint16_t* __restrict__ y,
     int rows, int width, float eps) {
+  constexpr int PW = PF32 ? 2 : 1;  // 16-byte parameter loads per group
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const size_t base = (size_t)row * width;
-  uint4 xa[NJ], ua[NJ];
+  vz_u32x4 xa[NJ], ua[NJ], wa[NJ][PW], ba[NJ][PW];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int k = j * 512 + lane * 8;
     const int kk = k < width ? k : 0;
-    xa[j] = *reinterpret_cast<const uint4*>(x + base + kk);
-    if (RESIDUAL) ua[j] = *reinterpret_cast<const uint4*>(u + base + kk);
+    xa[j] = ld16(x + base + kk);
+    if (RESIDUAL) ua[j] = ld16(u + base + kk);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int k = j * 512 + lane * 8;
+    const int kk = k < width ? k : 0;
+#pragma unroll
+    for (int h = 0; h < PW; ++h) {
+      if (PF32) {
+        wa[j][h] = ld16(reinterpret_cast<const float*>(w) + kk + 4 * h);
+        ba[j][h] = ld16(reinterpret_cast<const float*>(b) + kk + 4 * h);
+      } else {
+        wa[j][h] = ld16(reinterpret_cast<const uint16_t*>(w) + kk);
+        ba[j][h] = ld16(reinterpret_cast<const uint16_t*>(b) + kk);
+      }
+    }
   }
   float v[NJ][8];
   float s = 0.f;
@@ -67,10 +92,10 @@ __global__ __launch_bounds__(256) void layernorm_rows_vec(
   for (int j = 0; j < NJ; ++j) {
     const int k = j * 512 + lane * 8;
     const bool ok = k < width;
-    unpack8(xa[j], v[j]);
+    unpack8(as_u4(xa[j]), v[j]);
     if (RESIDUAL) {
       float a[8];
-      unpack8(ua[j], a);
+      unpack8(as_u4(ua[j]), a);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[j][e] = round_bf(v[j][e] + a[e]);
       if (ok) *reinterpret_cast<uint4*>(r_out + base + k) = pack8(v[j]);
@@ -95,8 +120,19 @@ __global__ __launch_bounds__(256) void layernorm_rows_vec(
     const int k = j * 512 + lane * 8;
     if (k < width) {
       float wv[8], bv[8], o[8];
-      param8(w, k, p_f32, wv);
-      param8(b, k, p_f32, bv);
+      if (PF32) {
+        const float4 w0 = __builtin_bit_cast(float4, as_u4(wa[j][0]));
+        const float4 w1 = __builtin_bit_cast(float4, as_u4(wa[j][PW - 1]));
+        const float4 b0 = __builtin_bit_cast(float4, as_u4(ba[j][0]));
+        const float4 b1 = __builtin_bit_cast(float4, as_u4(ba[j][PW - 1]));
+        wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+        wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+        bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
+        bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+      } else {
+        unpack8(as_u4(wa[j][0]), wv);
+        unpack8(as_u4(ba[j][0]), bv);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = v[j][e] * inv * wv[e] + bv[e];
       *reinterpret_cast<uint4*>(y + base + k) = pack8(o);
@@ -151,10 +187,14 @@ int layernorm_launch(const void* x, const void* u, const void* w, const void* b,
   uint16_t *rs = (uint16_t*)r_out, *ys = (uint16_t*)y;
   if (vec) {
     const int nj = (width + 511) / 512;
-    if (nj == 1) layernorm_rows_vec<RESIDUAL, 1><<<grid, 256, 0, stream>>>(xs, us, w, b, p_f32, rs, ys, rows, width, eps);
-    else if (nj == 2) layernorm_rows_vec<RESIDUAL, 2><<<grid, 256, 0, stream>>>(xs, us, w, b, p_f32, rs, ys, rows, width, eps);
-    else if (nj == 3) layernorm_rows_vec<RESIDUAL, 3><<<grid, 256, 0, stream>>>(xs, us, w, b, p_f32, rs, ys, rows, width, eps);
-    else layernorm_rows_vec<RESIDUAL, 4><<<grid, 256, 0, stream>>>(xs, us, w, b, p_f32, rs, ys, rows, width, eps);
+#define LN_VEC(NJ_)                                                                                   \
+  (p_f32 ? layernorm_rows_vec<RESIDUAL, NJ_, true><<<grid, 256, 0, stream>>>(xs, us, w, b, rs, ys, rows, width, eps) \
+         : layernorm_rows_vec<RESIDUAL, NJ_, false><<<grid, 256, 0, stream>>>(xs, us, w, b, rs, ys, rows, width, eps))
+    if (nj == 1) LN_VEC(1);
+    else if (nj == 2) LN_VEC(2);
+    else if (nj == 3) LN_VEC(3);
+    else LN_VEC(4);
+#undef LN_VEC
   } else {
     layernorm_rows_scalar<RESIDUAL><<<grid, 256, 0, stream>>>(xs, us, w, b, p_f32, rs, ys, rows, width, eps);
   }
@@ -234,6 +274,74 @@ __global__ __launch_bounds__(256) void vision_qkv_rope_rows(
   }
 }
 
+
+// Vector form for dim % 8 == 0 (16-byte aligned buffers): per token, thread
+// units are the (head, 4-column group c) of q and of k, each rotating the
+// pairs (c..c+3, c+half..c+half+3) with two 8-byte loads and stores, then the
+// 16-byte chunks of v. Same products and sums as the per-element form
+// (x * cos - partner * sin below half, x * cos + partner * sin above).
+template <bool CS_F32>
+__global__ __launch_bounds__(256) void vision_qkv_rope_vec(
+    const uint16_t* __restrict__ packed, const void* __restrict__ cos, const void* __restrict__ sin,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out,
+    int tokens, int heads, int dim) {
+  const int half = dim / 2, g4 = half / 4, g8 = dim / 8;
+  const int nqk = heads * g4;                 // q (or k) units per token
+  const int units = 2 * nqk + heads * g8;     // + v chunks
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (long long)tokens * units) return;
+  const int token = (int)(gid / units);
+  int u = (int)(gid - (long long)token * units);
+  const uint16_t* row = packed + (size_t)token * 3 * heads * dim;
+  if (u < 2 * nqk) {
+    const int which = u >= nqk;                 // 0: q, 1: k
+    u -= which * nqk;
+    const int head = u / g4, c = 4 * (u - head * g4);
+    const uint16_t* src = row + (size_t)(which * heads + head) * dim;
+    const uint2 xl = *reinterpret_cast<const uint2*>(src + c);
+    const uint2 xh = *reinterpret_cast<const uint2*>(src + c + half);
+    float cl[4], ch[4], sl[4], sh[4];
+    const size_t cs = (size_t)token * dim + c;
+    if (CS_F32) {
+      const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(cos) + cs);
+      const float4 bb = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(cos) + cs + half);
+      const float4 e = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(sin) + cs);
+      const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(sin) + cs + half);
+      cl[0] = a.x; cl[1] = a.y; cl[2] = a.z; cl[3] = a.w;
+      ch[0] = bb.x; ch[1] = bb.y; ch[2] = bb.z; ch[3] = bb.w;
+      sl[0] = e.x; sl[1] = e.y; sl[2] = e.z; sl[3] = e.w;
+      sh[0] = f.x; sh[1] = f.y; sh[2] = f.z; sh[3] = f.w;
+    } else {
+      const uint16_t* c16 = reinterpret_cast<const uint16_t*>(cos);
+      const uint16_t* s16 = reinterpret_cast<const uint16_t*>(sin);
+      const uint2 a = *reinterpret_cast<const uint2*>(c16 + cs);
+      const uint2 bb = *reinterpret_cast<const uint2*>(c16 + cs + half);
+      const uint2 e = *reinterpret_cast<const uint2*>(s16 + cs);
+      const uint2 f = *reinterpret_cast<const uint2*>(s16 + cs + half);
+      cl[0] = bf_lo(a.x); cl[1] = bf_hi(a.x); cl[2] = bf_lo(a.y); cl[3] = bf_hi(a.y);
+      ch[0] = bf_lo(bb.x); ch[1] = bf_hi(bb.x); ch[2] = bf_lo(bb.y); ch[3] = bf_hi(bb.y);
+      sl[0] = bf_lo(e.x); sl[1] = bf_hi(e.x); sl[2] = bf_lo(e.y); sl[3] = bf_hi(e.y);
+      sh[0] = bf_lo(f.x); sh[1] = bf_hi(f.x); sh[2] = bf_lo(f.y); sh[3] = bf_hi(f.y);
+    }
+    const float lo[4] = {bf_lo(xl.x), bf_hi(xl.x), bf_lo(xl.y), bf_hi(xl.y)};
+    const float hi[4] = {bf_lo(xh.x), bf_hi(xh.x), bf_lo(xh.y), bf_hi(xh.y)};
+    float ol[4], oh[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ol[e] = lo[e] * cl[e] + (-hi[e]) * sl[e];
+      oh[e] = hi[e] * ch[e] + lo[e] * sh[e];
+    }
+    uint16_t* dst = (which ? k_out : q_out) + ((size_t)head * tokens + token) * dim;
+    *reinterpret_cast<uint2*>(dst + c) = make_uint2(pack_bf2(ol[0], ol[1]), pack_bf2(ol[2], ol[3]));
+    *reinterpret_cast<uint2*>(dst + c + half) =
+        make_uint2(pack_bf2(oh[0], oh[1]), pack_bf2(oh[2], oh[3]));
+  } else {
+    u -= 2 * nqk;
+    const int head = u / g8, c = 8 * (u - head * g8);
+    *reinterpret_cast<uint4*>(v_out + ((size_t)head * tokens + token) * dim + c) =
+        *reinterpret_cast<const uint4*>(row + (size_t)(2 * heads + head) * dim + c);
+  }
+}
 
 // ------------------------------------------------------ vision attention
 // Non-causal multi-head attention of the vision blocks on the matrix cores
@@ -363,16 +471,21 @@ Q35_DEV void va_block(const uint16_t* __restrict__ Ks, const uint16_t* __restric
   }
 }
 
-template <int QT, int OT>
-__global__ __launch_bounds__(256) void vision_attn_fa(
+template <int QT, int OT, int KS>
+__global__ __launch_bounds__(256 * KS) void vision_attn_fa(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ out, const int* __restrict__ cu, int nseg, int T, int H, int D,
     float scale) {
   static_assert(QT >= 1 && QT <= 4 && (OT == 2 * QT || OT == 2 * QT - 1), "head dim tiles");
+  static_assert(KS == 1 || KS == 2, "key splits");
+  constexpr int NT = 256 * KS;         // threads
+  constexpr int SK = kVaKeys * KS;     // keys per stage (one 64-key block per wave group)
   constexpr int DP = 32 * QT;          // padded head dim
   constexpr int RS = DP + 8;           // LDS row stride (elements): rows 16-byte aligned
-  constexpr int NLD = (kVaKeys * DP / 8 + 255) / 256;  // 16-byte K (and V) chunks per thread
+  constexpr int NLD = (SK * DP / 8 + NT - 1) / NT;  // 16-byte K (and V) chunks per thread
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int rg = wid & 3;              // 16-row group of the tile
+  const int kh = wid >> 2;             // which block of a stage this wave computes
   // Workgroup -> (query tile, head): with heads a multiple of 8 the tiles of a
   // head share one residue mod 8 (one XCD, whose L2 then serves the head's
   // K/V to all of them); otherwise tiles fastest.
@@ -387,7 +500,7 @@ __global__ __launch_bounds__(256) void vision_attn_fa(
     tile = (int)blockIdx.x % ntiles;
   }
   const int qwg = tile * kVaRows;
-  const int qw0 = qwg + 16 * wid;
+  const int qw0 = qwg + 16 * rg;
   const int col = lane & 15, kg = lane >> 4;
   const int te = (lane & 15) >> 2, tq = lane & 3;
   const int ch = D / 8;            // 16-byte chunks per row
@@ -399,7 +512,7 @@ __global__ __launch_bounds__(256) void vision_attn_fa(
   int kbeg, kend, tmp;
   va_segment(cu, nseg, T, qwg, kbeg, tmp);
   va_segment(cu, nseg, T, min(qwg + kVaRows, T) - 1, tmp, kend);
-  const int nblk = (kend - kbeg + kVaKeys - 1) / kVaKeys;
+  const int nst = (kend - kbeg + SK - 1) / SK;
   int s0[4], s1[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) va_segment(cu, nseg, T, min(qw0 + 4 * kg + i, T - 1), s0[i], s1[i]);
@@ -418,24 +531,24 @@ __global__ __launch_bounds__(256) void vision_attn_fa(
     }
   }
 
-  __shared__ alignas(16) uint16_t kv_s[2][2][kVaKeys * RS];  // [buf][K, V][key][dim]
-  __shared__ alignas(16) uint16_t pt_s[4][kVaKeys * kVaPt];  // [wave][key][row]
+  __shared__ alignas(16) uint16_t kv_s[2][2][SK * RS];         // [buf][K, V][key][dim]
+  __shared__ alignas(16) uint16_t pt_s[4 * KS][kVaKeys * kVaPt];  // [wave][key][row]
   // Zero the padded dims [D, RS) of every K and V row once: they meet the
   // zero-padded Q dims in S (0 * finite) and only unused output dims in O.
   const int pad = RS - D;
-  for (int i = tid; i < 2 * 2 * kVaKeys * pad; i += 256) {
+  for (int i = tid; i < 2 * 2 * SK * pad; i += NT) {
     const int row = i / pad, cc = D + i % pad;
     (&kv_s[0][0][0])[row * RS + cc] = 0;
   }
 
-  // This thread's 16-byte chunks of a block: chunk gi = tid + 256 j is key
-  // row gi / ch, dims 8 * (gi % ch); only chunks gi < 64 * ch exist.
+  // This thread's 16-byte chunks of a stage: chunk gi = tid + NT j is key
+  // row gi / ch, dims 8 * (gi % ch); only chunks gi < SK * ch exist.
   int lrow[NLD], lcol[NLD];
   bool lok[NLD];
 #pragma unroll
   for (int j = 0; j < NLD; ++j) {
-    const int gi = tid + 256 * j;
-    lok[j] = gi < kVaKeys * ch;
+    const int gi = tid + NT * j;
+    lok[j] = gi < SK * ch;
     lrow[j] = lok[j] ? gi / ch : 0;
     lcol[j] = lok[j] ? 8 * (gi % ch) : 0;
   }
@@ -444,10 +557,10 @@ __global__ __launch_bounds__(256) void vision_attn_fa(
   va_u32x4 kr0[NLD], vr0[NLD], kr1[NLD], vr1[NLD];
   // Loads are clamped into the workgroup's key range and the head's rows (a
   // range that malformed image offsets left empty reads row 0, never used).
-  auto va_load = [&](va_u32x4 (&kr)[NLD], va_u32x4 (&vr)[NLD], int b) {
+  auto va_load = [&](va_u32x4 (&kr)[NLD], va_u32x4 (&vr)[NLD], int st) {
 #pragma unroll
     for (int j = 0; j < NLD; ++j) {
-      const int key = max(min(min(kbeg + b * kVaKeys + lrow[j], kend - 1), T - 1), 0);
+      const int key = max(min(min(kbeg + st * SK + lrow[j], kend - 1), T - 1), 0);
       const size_t off = hb + (size_t)key * D + lcol[j];
       kr[j] = *reinterpret_cast<const va_u32x4*>(k + off);
       vr[j] = *reinterpret_cast<const va_u32x4*>(v + off);
@@ -463,15 +576,17 @@ __global__ __launch_bounds__(256) void vision_attn_fa(
       }
     }
   };
-#define VA_BLOCK(BUF, BLK)                                                                \
+  // This wave's block of stage ST (keys kb..kb+63 of LDS buffer BUF); the
+  // mask is skipped when the block lies inside every row's image.
+#define VA_BLOCK(BUF, ST)                                                                 \
   do {                                                                                    \
-    const int kb = kbeg + (BLK) * kVaKeys;                                                \
+    const int kb = kbeg + (ST) * SK + kVaKeys * kh;                                       \
+    const uint16_t* Ks = kv_s[BUF][0] + kVaKeys * kh * RS;                                \
+    const uint16_t* Vs = kv_s[BUF][1] + kVaKeys * kh * RS;                                \
     if (kb >= w0 && kb + kVaKeys <= w1)                                                   \
-      va_block<QT, OT, false>(kv_s[BUF][0], kv_s[BUF][1], pt, qa, o, m, lp, kb, s0, s1,  \
-                              c, col, kg, te, tq);                                        \
+      va_block<QT, OT, false>(Ks, Vs, pt, qa, o, m, lp, kb, s0, s1, c, col, kg, te, tq);  \
     else                                                                                  \
-      va_block<QT, OT, true>(kv_s[BUF][0], kv_s[BUF][1], pt, qa, o, m, lp, kb, s0, s1,   \
-                             c, col, kg, te, tq);                                         \
+      va_block<QT, OT, true>(Ks, Vs, pt, qa, o, m, lp, kb, s0, s1, c, col, kg, te, tq);   \
   } while (0)
 
   q35_f32x4 o[OT];
@@ -486,27 +601,62 @@ __global__ __launch_bounds__(256) void vision_attn_fa(
   uint16_t* pt = pt_s[wid];
 
   // Two register sets and two LDS buffers: at the top of an iteration LDS
-  // buffer 0 holds block blk and set 1 block blk + 1; block blk + 2 is
-  // requested into set 0 while blk is computed. Loads past the last block
+  // buffer 0 holds stage st and set 1 stage st + 1; stage st + 2 is
+  // requested into set 0 while st is computed. Loads past the last stage
   // reload it (unconditional: a conditional load here made the compiler keep
-  // the chunks in scratch memory).
+  // the chunks in scratch memory). The barriers order LDS only; the loads
+  // in flight stay in flight across them.
   va_load(kr0, vr0, 0);
   va_store(kr0, vr0, 0);
-  va_load(kr1, vr1, min(1, nblk - 1));
+  va_load(kr1, vr1, min(1, nst - 1));
   lds_barrier();
-  int blk = 0;
-  for (; blk + 1 < nblk; blk += 2) {
-    va_load(kr0, vr0, min(blk + 2, nblk - 1));
-    VA_BLOCK(0, blk);
+  int st = 0;
+  for (; st + 1 < nst; st += 2) {
+    va_load(kr0, vr0, min(st + 2, nst - 1));
+    VA_BLOCK(0, st);
     va_store(kr1, vr1, 1);
     lds_barrier();
-    va_load(kr1, vr1, min(blk + 3, nblk - 1));
-    VA_BLOCK(1, blk + 1);
+    va_load(kr1, vr1, min(st + 3, nst - 1));
+    VA_BLOCK(1, st + 1);
     va_store(kr0, vr0, 0);
     lds_barrier();
   }
-  if (blk < nblk) VA_BLOCK(0, blk);
+  if (st < nst) VA_BLOCK(0, st);
 #undef VA_BLOCK
+
+  if (KS == 2) {
+    // The second wave group hands its (m, partial l, O) to the first through
+    // LDS ([field][row group][lane] floats, conflict-free), which merges
+    // them: both groups hold the same rows and dims lane for lane.
+    constexpr int NF = 4 * OT + 8;
+    static_assert(NF * 4 * 64 * 4 <= (int)sizeof(kv_s), "merge area");
+    float* mg = reinterpret_cast<float*>(&kv_s[0][0][0]);
+    lds_barrier();  // every wave is done with the K/V buffers
+    if (kh == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        mg[((i) * 4 + rg) * 64 + lane] = m[i];
+        mg[((4 + i) * 4 + rg) * 64 + lane] = lp[i];
+#pragma unroll
+        for (int d = 0; d < OT; ++d) mg[((8 + 4 * d + i) * 4 + rg) * 64 + lane] = o[d][i];
+      }
+    }
+    lds_barrier();
+    if (kh == 1) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float m1 = mg[((i) * 4 + rg) * 64 + lane];
+      const float l1 = mg[((4 + i) * 4 + rg) * 64 + lane];
+      const float mm = fmaxf(m[i], m1);
+      const float msub = mm == -INFINITY ? 0.f : mm * c;
+      const float f0 = __builtin_amdgcn_exp2f(fmaf(m[i], c, -msub));
+      const float f1 = __builtin_amdgcn_exp2f(fmaf(m1, c, -msub));
+      lp[i] = lp[i] * f0 + l1 * f1;
+#pragma unroll
+      for (int d = 0; d < OT; ++d)
+        o[d][i] = o[d][i] * f0 + mg[((8 + 4 * d + i) * 4 + rg) * 64 + lane] * f1;
+    }
+  }
   const size_t ostride = (size_t)H * D;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -566,11 +716,22 @@ int q35_vision_qkv_rope(const void* packed, const void* cos, const void* sin, in
   Q35_CHECK_ARG(packed && cos && sin && q && k && v);
   Q35_CHECK_ARG((long long)tokens * 3 * heads * dim < (1ll << 31));
   if (tokens == 0) return 0;
-  const long long waves = (long long)tokens * heads;
-  const unsigned grid = (unsigned)((waves + kRowsPerBlock - 1) / kRowsPerBlock);
-  vision_qkv_rope_rows<<<grid, 256, 0, stream>>>((const uint16_t*)packed, cos, sin, cs_f32,
-                                                (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, tokens,
-                                                heads, dim);
+  const uint16_t* ps = (const uint16_t*)packed;
+  uint16_t *qs = (uint16_t*)q, *ks = (uint16_t*)k, *vs = (uint16_t*)v;
+  if (dim % 8 == 0 && q35_aligned16(packed) && q35_aligned16(cos) && q35_aligned16(sin) &&
+      q35_aligned16(q) && q35_aligned16(k) && q35_aligned16(v)) {
+    const long long threads = (long long)tokens * (2 * heads * (dim / 8) + heads * (dim / 8));
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    if (cs_f32)
+      vision_qkv_rope_vec<true><<<grid, 256, 0, stream>>>(ps, cos, sin, qs, ks, vs, tokens, heads, dim);
+    else
+      vision_qkv_rope_vec<false><<<grid, 256, 0, stream>>>(ps, cos, sin, qs, ks, vs, tokens, heads, dim);
+  } else {
+    const long long waves = (long long)tokens * heads;
+    const unsigned grid = (unsigned)((waves + kRowsPerBlock - 1) / kRowsPerBlock);
+    vision_qkv_rope_rows<<<grid, 256, 0, stream>>>(ps, cos, sin, cs_f32, qs, ks, vs, tokens, heads,
+                                                  dim);
+  }
   return q35_last_error();
 }
 
@@ -587,18 +748,30 @@ int q35_vision_attention(const void* q, const void* k, const void* v, void* out,
   const uint16_t *qs = (const uint16_t*)q, *ks = (const uint16_t*)k, *vs = (const uint16_t*)v;
   uint16_t* os = (uint16_t*)out;
   const int qt = (dim + 31) / 32, ot = (dim + 15) / 16;
-#define VA_LAUNCH(QT_, OT_) \
-  vision_attn_fa<QT_, OT_><<<grid, 256, 0, stream>>>(qs, ks, vs, os, cu, n_images, tokens, heads, dim, scale)
+#define VA_LAUNCH(QT_, OT_, KS_)                                                          \
+  vision_attn_fa<QT_, OT_, KS_><<<grid, 256 * KS_, 0, stream>>>(qs, ks, vs, os, cu, n_images, \
+                                                                tokens, heads, dim, scale)
+  // Two key blocks per stage (8 waves, one workgroup per CU by LDS) while the
+  // grid leaves CUs idle; one block (4 waves, two workgroups per CU) for
+  // larger grids and for the 128-dim tiles, whose registers do not fit two
+  // waves per SIMD.
+  const bool split = grid < 512;
+#define VA_PICK(QT_, OT_)        \
+  if (split)                     \
+    VA_LAUNCH(QT_, OT_, 2);      \
+  else                           \
+    VA_LAUNCH(QT_, OT_, 1);
   switch (qt * 8 + ot) {
-    case 1 * 8 + 1: VA_LAUNCH(1, 1); break;
-    case 1 * 8 + 2: VA_LAUNCH(1, 2); break;
-    case 2 * 8 + 3: VA_LAUNCH(2, 3); break;
-    case 2 * 8 + 4: VA_LAUNCH(2, 4); break;
-    case 3 * 8 + 5: VA_LAUNCH(3, 5); break;
-    case 3 * 8 + 6: VA_LAUNCH(3, 6); break;
-    case 4 * 8 + 7: VA_LAUNCH(4, 7); break;
-    default: VA_LAUNCH(4, 8); break;
+    case 1 * 8 + 1: VA_PICK(1, 1); break;
+    case 1 * 8 + 2: VA_PICK(1, 2); break;
+    case 2 * 8 + 3: VA_PICK(2, 3); break;
+    case 2 * 8 + 4: VA_PICK(2, 4); break;
+    case 3 * 8 + 5: VA_PICK(3, 5); break;
+    case 3 * 8 + 6: VA_PICK(3, 6); break;
+    case 4 * 8 + 7: VA_LAUNCH(4, 7, 1); break;
+    default: VA_LAUNCH(4, 8, 1); break;
   }
+#undef VA_PICK
 #undef VA_LAUNCH
   return q35_last_error();
 }

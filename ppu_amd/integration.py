@@ -34,6 +34,7 @@ from dataclasses import dataclass
 from typing import Any, Callable
 
 import torch
+from transformers.activations import GELUTanh
 from transformers.cache_utils import DynamicCache
 from transformers.models.qwen3_5 import modeling_qwen3_5 as qwen_impl
 
@@ -662,6 +663,20 @@ def _patch_embed(visual, pixels: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(x, w.reshape(w.shape[0], -1), proj.bias)
 
 
+def _vision_mlp(mlp, x: torch.Tensor) -> torch.Tensor:
+    """Qwen3_5VisionMLP (fc1 -> tanh-approximated GELU -> fc2). With the
+    tanh GELU the activation is the library GEMM's epilogue applied to the
+    fp32 accumulator plus bias (one launch and one bf16 rounding fewer than
+    rounding fc1's output and running GELU on it); other activations run as
+    the module wrote them."""
+    fc1, fc2 = mlp.linear_fc1, mlp.linear_fc2
+    if isinstance(mlp.act_fn, GELUTanh) and fc1.bias is not None and x.dim() == 2:
+        h = torch._addmm_activation(fc1.bias, x, fc1.weight.t(), use_gelu=True)
+    else:
+        h = mlp.act_fn(fc1(x))
+    return fc2(h)
+
+
 def _vision_merger(merger, hidden: torch.Tensor) -> torch.Tensor:
     """Qwen3_5VisionPatchMerger: LayerNorm (before or after the spatial
     shuffle), then fc1 -> GELU -> fc2 on groups of merged rows."""
@@ -694,7 +709,7 @@ def _vision_forward(visual, pixels, interp_indices, interp_weights, position_ids
         update = _vision_attention(blk.attn, normed, cos, sin, segments)
         residual, mlp_in = K.residual_add_layer_norm(residual, update.contiguous(), blk.norm2.weight,
                                                      blk.norm2.bias, blk.norm2.eps)
-        mlp_out = blk.mlp(mlp_in).contiguous()
+        mlp_out = _vision_mlp(blk.mlp, mlp_in).contiguous()
         if i + 1 < len(blocks):
             nxt = blocks[i + 1].norm1
             residual, normed = K.residual_add_layer_norm(residual, mlp_out, nxt.weight, nxt.bias, nxt.eps)
@@ -718,40 +733,67 @@ class _VisionGraph:
             self.out = _vision_forward(visual, *self.inputs, None)
 
     def run(self, *inputs) -> tuple[torch.Tensor, torch.Tensor]:
+        """Copy in the pixels and any further inputs given (in capture
+        order), replay, return copies of the outputs."""
         for dst, src in zip(self.inputs, inputs):
             dst.copy_(src)
         self.graph.replay()
         return self.out[0].clone(), self.out[1].clone()
 
 
+_VISION_PRECOMPUTED = ("interp_indices", "interp_weights", "position_ids", "cu_seqlens")
+
+
+def _vision_prep(visual, grid_thw: torch.Tensor, kw: dict, device) -> tuple:
+    """The tower's per-call inputs derived from ``grid_thw`` (Transformers'
+    helpers, which take precomputed values out of ``kw`` when the caller
+    passed them): interpolation indices / weights, rotary position ids and
+    the image segments (None for one image), on ``device``."""
+    idx, wts = qwen_impl.get_vision_interpolation_indices_and_weights(
+        grid_thw, num_grid_per_side=visual.num_grid_per_side, mode=visual.interpolation_mode,
+        align_corners=visual.interpolation_align_corners,
+        spatial_merge_size=visual.config.spatial_merge_size, kwargs=kw)
+    position_ids = qwen_impl.get_vision_position_ids(grid_thw, visual.spatial_merge_size, kwargs=kw)
+    cu_seqlens, _ = qwen_impl.get_vision_attention_seqlens(grid_thw, visual.config, kwargs=kw)
+    segments = None
+    if cu_seqlens.numel() != 2:
+        bounds = cu_seqlens.tolist()
+        segments = list(zip(bounds[:-1], bounds[1:]))
+    return (idx.to(device).contiguous(), wts.to(device).contiguous(),
+            position_ids.to(device).contiguous(), segments)
+
+
 def _vision_model_fast(visual, config: FusionConfig):
     graphs: dict[tuple, _VisionGraph] = {}
+    preps: dict[tuple, tuple] = {}
 
     def fast(hidden_states, grid_thw=None, **kwargs):
         if (grid_thw is None or not hidden_states.is_cuda or not _gpu_bf16(visual.pos_embed.weight)
                 or kwargs.get("output_attentions") or kwargs.get("output_hidden_states")):
             return NotImplemented
         kw = dict(kwargs)
-        idx, wts = qwen_impl.get_vision_interpolation_indices_and_weights(
-            grid_thw, num_grid_per_side=visual.num_grid_per_side, mode=visual.interpolation_mode,
-            align_corners=visual.interpolation_align_corners,
-            spatial_merge_size=visual.config.spatial_merge_size, kwargs=kw)
-        position_ids = qwen_impl.get_vision_position_ids(grid_thw, visual.spatial_merge_size, kwargs=kw)
-        cu_seqlens, _ = qwen_impl.get_vision_attention_seqlens(grid_thw, visual.config, kwargs=kw)
         device = hidden_states.device
+        grid_key = (str(device),) + tuple(int(g) for g in grid_thw.reshape(-1).tolist())
+        given = any(kw.get(name) is not None for name in _VISION_PRECOMPUTED)
+        if given:
+            prep = _vision_prep(visual, grid_thw, kw, device)
+        else:
+            # Pure functions of the grid: computed once per grid (a few dozen
+            # small launches and host syncs fewer per call).
+            prep = preps.get(grid_key)
+            if prep is None:
+                prep = _vision_prep(visual, grid_thw, kw, device)
+                if len(preps) < 64:
+                    preps[grid_key] = prep
+        idx, wts, position_ids, segments = prep
         pixels = hidden_states.to(visual.patch_embed.proj.weight.dtype).contiguous()
-        idx = idx.to(device).contiguous()
-        wts = wts.to(device).contiguous()
-        position_ids = position_ids.to(device).contiguous()
-        single = cu_seqlens.numel() == 2
-        segments = None
-        if not single:
-            bounds = cu_seqlens.tolist()
-            segments = list(zip(bounds[:-1], bounds[1:]))
-        key = (tuple(pixels.shape), wts.dtype)
+        single = segments is None
+        key = (tuple(pixels.shape), wts.dtype, grid_key)
         entry = graphs.get(key) if config.vision_graph and single else None
         if entry is not None:
-            hidden, merged = entry.run(pixels, idx, wts, position_ids)
+            # The captured grid's inputs are already in place unless the
+            # caller handed in its own.
+            hidden, merged = entry.run(pixels, *((idx, wts, position_ids) if given else ()))
         else:
             hidden, merged = _vision_forward(visual, pixels, idx, wts, position_ids, segments)
             if (config.vision_graph and single and len(graphs) < config.vision_graph_max_entries

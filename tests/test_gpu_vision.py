@@ -100,7 +100,8 @@ def test_position_embed_add_clamps_indices(gpu):
     assert torch.equal(got[2], table[15])
 
 
-@pytest.mark.parametrize("tokens,heads,dim", [(10, 16, 72), (257, 16, 64), (33, 12, 80), (5, 2, 128)])
+@pytest.mark.parametrize("tokens,heads,dim", [(10, 16, 72), (257, 16, 64), (33, 12, 80), (5, 2, 128),
+                                               (7, 3, 18), (4, 2, 6)])
 @pytest.mark.parametrize("cs_dtype", [torch.float32, BF])
 def test_vision_qkv_rope(gpu, tokens, heads, dim, cs_dtype):
     from ppu_amd import kernels as K
@@ -227,7 +228,7 @@ def test_vision_tower_two_images_and_precomputed_kwargs(gpu):
 
 
 @pytest.mark.parametrize("tokens,heads,dim", [(784, 16, 72), (100, 4, 64), (257, 2, 80), (64, 3, 128),
-                                              (5, 2, 8), (130, 1, 96)])
+                                              (5, 2, 8), (130, 1, 96), (2048, 16, 72)])
 def test_vision_attention_one_image(gpu, tokens, heads, dim):
     from ppu_amd import kernels as K
 
@@ -240,12 +241,14 @@ def test_vision_attention_one_image(gpu, tokens, heads, dim):
     torch.testing.assert_close(got.float().cpu(), exp.float(), rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("bounds", [[0, 64, 100, 257], [0, 1, 130, 131], [0, 200, 257]])
-def test_vision_attention_per_image(gpu, bounds):
+# (grids of 512 workgroups and more take the one-block-per-stage form)
+@pytest.mark.parametrize("bounds,heads", [([0, 64, 100, 257], 4), ([0, 1, 130, 131], 4), ([0, 200, 257], 4),
+                                          ([0, 1000, 2100], 16)])
+def test_vision_attention_per_image(gpu, bounds, heads):
     from ppu_amd import kernels as K
 
     g = gen(KERNEL_SEED + 6)
-    heads, dim, tokens = 4, 72, bounds[-1]
+    dim, tokens = 72, bounds[-1]
     q, k, v = (randn(g, 1, heads, tokens, dim, scale=2.0) for _ in range(3))
     cu = torch.tensor(bounds, dtype=torch.int32)
     got = K.vision_attention(q.to(gpu), k.to(gpu), v.to(gpu), dim ** -0.5, cu.to(gpu))
@@ -255,3 +258,25 @@ def test_vision_attention_per_image(gpu, bounds):
     for a, b in zip(bounds[:-1], bounds[1:]):
         if b - a == 1:
             assert torch.equal(got[a].cpu().reshape(heads, dim), v[0, :, a])
+
+
+def test_vision_mlp_fused_gelu_matches_module(gpu):
+    """The block MLP with the tanh GELU as the fc1 GEMM's epilogue (one bf16
+    rounding fewer) against the module's own bf16 forward and an fp32 one."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as impl
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5VisionConfig
+    from ppu_amd import integration
+
+    cfg = Qwen3_5VisionConfig(hidden_size=256, intermediate_size=688)
+    torch.manual_seed(KERNEL_SEED + 7)
+    mlp = impl.Qwen3_5VisionMLP(cfg)
+    x = torch.randn(300, 256)
+    exp32 = mlp(x)
+    mlp = mlp.to(gpu, torch.bfloat16)
+    xb = x.to(gpu, torch.bfloat16)
+    with torch.no_grad():
+        got = integration._vision_mlp(mlp, xb).float().cpu()
+        mod = mlp(xb).float().cpu()
+    rel = lambda a, b: ((a - b).norm() / b.norm()).item()
+    assert rel(got, exp32.detach()) <= rel(mod, exp32.detach()) * 1.5 + 1e-3
+    assert rel(got, mod) < 1e-2
