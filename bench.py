@@ -503,6 +503,26 @@ def trace_summary(kind: str, trace_csv: str, bench_json: str) -> None:
             if "top1_final" in r["Kernel_Name"] or "lm_head_rescore" in r["Kernel_Name"]]
     v = d.get("variants", {}).get("a8w8", {})
     lines = []
+    if kind == "vision":
+        # one fused tower call starts with the patch-embedding GEMM right
+        # before its position-embedding add; the last call ends the trace of
+        # `bench.py --vision-only`
+        starts = [i for i, r in enumerate(rows) if "position_embed_add_rows" in r["Kernel_Name"]]
+        gemms = [i for i, r in enumerate(rows) if r["Kernel_Name"].startswith("Cijk")]
+        if starts and gemms:
+            # ... and ends with the merger's second GEMM and the two output copies
+            a, b = max(starts[-1] - 1, 0), gemms[-1] + 1
+            while b < len(rows) and b <= gemms[-1] + 2 and "copyBuffer" in rows[b]["Kernel_Name"]:
+                b += 1
+            lines.append("# fused vision tower, one 784-patch image (the last graph replay in the trace):")
+            lines += table(rows[a:b], True)
+            lines.append("#")
+        vt = d.get("vision_tower", d)
+        lines.append(f"# bench.py JSON given ({Path(bench_json).name}): Transformers forward "
+                     f"{vt.get('transformers_ms')} ms, fused forward {vt.get('fused_graph_ms')} ms per call, "
+                     f"pooled output {vt.get('pooler_rel_l2_vs_transformers')} relative L2 from Transformers.")
+        print("\n".join(lines))
+        return
     if kind == "decode":
         steps = [(a + 1, b + 1) for a, b in zip(ends, ends[1:]) if 60 < b - a < 400]
         for name, pick in (("bf16", False), ("A8W8", True)):
@@ -748,7 +768,9 @@ def main() -> None:
     ap.add_argument("--cpu-prompt", type=int, default=PROMPT_LEN, help="prompt length of the CPU sample")
     ap.add_argument("--no-eager", action="store_true", help="skip the Transformers-eager CPU timing")
     ap.add_argument("--no-vision", action="store_true", help="skip the vision-tower timing")
-    ap.add_argument("--trace-summary", nargs=3, metavar=("decode|prefill", "TRACE_CSV", "BENCH_JSON"),
+    ap.add_argument("--vision-only", action="store_true",
+                    help="only time the vision tower (Transformers vs fused), print its JSON, then exit")
+    ap.add_argument("--trace-summary", nargs=3, metavar=("decode|prefill|vision", "TRACE_CSV", "BENCH_JSON"),
                     help="per-kernel anatomy of a rocprofv3 kernel trace of this bench, then exit")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="prefill GEMM shapes: ROCm library vs the hand-written GEMMs, then exit")
@@ -776,6 +798,9 @@ def main() -> None:
         return
     if args.gemm_sweep:
         gemm_sweep(torch.device("cuda:0"))
+        return
+    if args.vision_only:
+        print(json.dumps({"vision_tower": vision_tower_timing(torch.device("cuda:0"))}), flush=True)
         return
 
     from ppu_amd import synth

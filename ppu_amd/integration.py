@@ -689,18 +689,23 @@ def _vision_merger(merger, hidden: torch.Tensor) -> torch.Tensor:
     return merger.linear_fc2(merger.act_fn(merger.linear_fc1(x)))
 
 
-def _vision_forward(visual, pixels, interp_indices, interp_weights, position_ids, segments):
+def _vision_rotary(visual, position_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin ``[tokens, head_dim]`` of the tower's 2-D rotary embedding
+    for these position ids (Transformers' rotary module, halves repeated)."""
+    freqs = visual.rotary_pos_emb(position_ids).reshape(position_ids.shape[0], -1)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().contiguous(), emb.sin().contiguous()
+
+
+def _vision_forward(visual, pixels, interp_indices, interp_weights, cos, sin, segments):
     """The whole tower for the patches of one call (reference
     integration.py:514-562 plus the patch embedding and the merger): position
-    embedding, rotary table, every block (the residual stream stays bf16; each
-    block's second norm and the next block's first norm run as residual-add +
-    LayerNorm launches), merger. Returns (last hidden state, merged rows)."""
+    embedding, every block with the given rotary table (the residual stream
+    stays bf16; each block's second norm and the next block's first norm run
+    as residual-add + LayerNorm launches), merger. Returns (last hidden
+    state, merged rows)."""
     patches = _patch_embed(visual, pixels).contiguous()
     hidden = K.position_embed_add(patches, visual.pos_embed.weight, interp_indices, interp_weights)
-    tokens = hidden.shape[0]
-    freqs = visual.rotary_pos_emb(position_ids).reshape(tokens, -1)
-    emb = torch.cat((freqs, freqs), dim=-1)
-    cos, sin = emb.cos(), emb.sin()
     blocks = visual.blocks
     n1 = blocks[0].norm1
     normed = K.layer_norm(hidden, n1.weight, n1.bias, n1.eps)
@@ -724,9 +729,8 @@ class _VisionGraph:
     and captures; later calls copy their inputs in and replay. Outputs are
     returned as copies (the next replay overwrites the graph's buffers)."""
 
-    def __init__(self, visual, pixels, interp_indices, interp_weights, position_ids) -> None:
-        self.inputs = [t.contiguous().clone() for t in (pixels, interp_indices, interp_weights,
-                                                        position_ids)]
+    def __init__(self, visual, pixels, interp_indices, interp_weights, cos, sin) -> None:
+        self.inputs = [t.contiguous().clone() for t in (pixels, interp_indices, interp_weights, cos, sin)]
         torch.cuda.synchronize(pixels.device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
@@ -747,8 +751,9 @@ _VISION_PRECOMPUTED = ("interp_indices", "interp_weights", "position_ids", "cu_s
 def _vision_prep(visual, grid_thw: torch.Tensor, kw: dict, device) -> tuple:
     """The tower's per-call inputs derived from ``grid_thw`` (Transformers'
     helpers, which take precomputed values out of ``kw`` when the caller
-    passed them): interpolation indices / weights, rotary position ids and
-    the image segments (None for one image), on ``device``."""
+    passed them): interpolation indices / weights, the image segments (None
+    for one image) and the rotary cos / sin of the position ids, on
+    ``device``."""
     idx, wts = qwen_impl.get_vision_interpolation_indices_and_weights(
         grid_thw, num_grid_per_side=visual.num_grid_per_side, mode=visual.interpolation_mode,
         align_corners=visual.interpolation_align_corners,
@@ -759,8 +764,8 @@ def _vision_prep(visual, grid_thw: torch.Tensor, kw: dict, device) -> tuple:
     if cu_seqlens.numel() != 2:
         bounds = cu_seqlens.tolist()
         segments = list(zip(bounds[:-1], bounds[1:]))
-    return (idx.to(device).contiguous(), wts.to(device).contiguous(),
-            position_ids.to(device).contiguous(), segments)
+    cos, sin = _vision_rotary(visual, position_ids.to(device))
+    return idx.to(device).contiguous(), wts.to(device).contiguous(), segments, cos, sin
 
 
 def _vision_model_fast(visual, config: FusionConfig):
@@ -773,7 +778,9 @@ def _vision_model_fast(visual, config: FusionConfig):
             return NotImplemented
         kw = dict(kwargs)
         device = hidden_states.device
-        grid_key = (str(device),) + tuple(int(g) for g in grid_thw.reshape(-1).tolist())
+        inv_freq = getattr(visual.rotary_pos_emb, "inv_freq", None)
+        rot_key = (inv_freq.data_ptr(), inv_freq._version) if inv_freq is not None else ()
+        grid_key = (str(device), *rot_key) + tuple(int(g) for g in grid_thw.reshape(-1).tolist())
         given = any(kw.get(name) is not None for name in _VISION_PRECOMPUTED)
         if given:
             prep = _vision_prep(visual, grid_thw, kw, device)
@@ -785,7 +792,7 @@ def _vision_model_fast(visual, config: FusionConfig):
                 prep = _vision_prep(visual, grid_thw, kw, device)
                 if len(preps) < 64:
                     preps[grid_key] = prep
-        idx, wts, position_ids, segments = prep
+        idx, wts, segments, cos, sin = prep
         pixels = hidden_states.to(visual.patch_embed.proj.weight.dtype).contiguous()
         single = segments is None
         key = (tuple(pixels.shape), wts.dtype, grid_key)
@@ -793,12 +800,12 @@ def _vision_model_fast(visual, config: FusionConfig):
         if entry is not None:
             # The captured grid's inputs are already in place unless the
             # caller handed in its own.
-            hidden, merged = entry.run(pixels, *((idx, wts, position_ids) if given else ()))
+            hidden, merged = entry.run(pixels, *((idx, wts, cos, sin) if given else ()))
         else:
-            hidden, merged = _vision_forward(visual, pixels, idx, wts, position_ids, segments)
+            hidden, merged = _vision_forward(visual, pixels, idx, wts, cos, sin, segments)
             if (config.vision_graph and single and len(graphs) < config.vision_graph_max_entries
                     and not torch.cuda.is_current_stream_capturing()):
-                graphs[key] = _VisionGraph(visual, pixels, idx, wts, position_ids)
+                graphs[key] = _VisionGraph(visual, pixels, idx, wts, cos, sin)
         return qwen_impl.BaseModelOutputWithPooling(last_hidden_state=hidden, pooler_output=merged)
     return fast
 
