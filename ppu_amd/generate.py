@@ -22,6 +22,7 @@ from dataclasses import dataclass, field
 
 import torch
 
+from .capture import prime_capture_state
 from .graph import GreedyDecodeGraph
 from .integration import lm_head_screen, text_stack
 from .kernels import lm_head_argmax, zero_tensors
@@ -119,6 +120,7 @@ class PrefillGraph:
             stack = model.model
             self.rope = stack.rotary_emb(stack.embed_tokens.weight[:1], self.positions)
             extra["position_embeddings"] = self.rope
+        prime_capture_state(device)
         torch.cuda.synchronize(device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):

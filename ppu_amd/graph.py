@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import torch
 
+from .capture import prime_capture_state
 from .integration import lm_head_screen
 from .kernels import lm_head_argmax
 
@@ -54,6 +55,7 @@ class GreedyDecodeGraph:
         self._ring[-1].copy_(token)
         self._positions = position_ids.clone()
         self.logits = None
+        prime_capture_state(token.device)
         torch.cuda.synchronize(token.device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):

@@ -39,6 +39,7 @@ from transformers.cache_utils import DynamicCache
 from transformers.models.qwen3_5 import modeling_qwen3_5 as qwen_impl
 
 from . import kernels as K
+from .capture import prime_capture_state
 
 
 @dataclass(frozen=True)
@@ -731,6 +732,7 @@ class _VisionGraph:
 
     def __init__(self, visual, pixels, interp_indices, interp_weights, cos, sin) -> None:
         self.inputs = [t.contiguous().clone() for t in (pixels, interp_indices, interp_weights, cos, sin)]
+        prime_capture_state(pixels.device)
         torch.cuda.synchronize(pixels.device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):

@@ -13,6 +13,9 @@
 * ``test_graph_multistep_equals_single_steps``: ``steps=4`` replays continue
   the sequence exactly as single-step replays do.
 * Wrappers reject tensors on the wrong device before any launch.
+* A library capture under inference mode leaves later captures outside
+  inference mode working (the first GPU test of the suite, so in a full run
+  the process has captured nothing before it).
 """
 
 from __future__ import annotations
@@ -58,6 +61,36 @@ def _image_prompt(cfg, gpu):
 
     return BatchFeature(dict(input_ids=ids, attention_mask=torch.ones_like(ids), pixel_values=pixels,
                              image_grid_thw=grid, mm_token_type_ids=types))
+
+
+def test_capture_outside_inference_mode_after_library_capture_inside(gpu):
+    """A decode graph captured under ``torch.inference_mode``, then a plain
+    capture outside it, which must not fail in ``capture_begin`` (the
+    generator's capture state is created at the process's first capture; the
+    library makes that first registration outside inference mode)."""
+    from transformers import StaticCache
+
+    from ppu_amd.graph import GreedyDecodeGraph
+    from ppu_amd.integration import apply_fusions
+
+    cfg = synth.config_tiny()
+    model = synth.build_model(cfg, device=gpu)
+    apply_fusions(model)
+    prompt = synth.prompt_ids(12, cfg.vocab_size, seed=synth.MODEL_SEED + 9).to(gpu)
+    cache = StaticCache(config=model.config, max_cache_len=512)
+    with torch.inference_mode():
+        out = model.model(input_ids=prompt, position_ids=torch.arange(12, device=gpu).view(1, -1),
+                          past_key_values=cache, use_cache=True)
+        tok = out.last_hidden_state[:, -1:, 0].long().abs() % cfg.vocab_size
+        runner = GreedyDecodeGraph(model, cache, tok, torch.full((1, 1), 12, device=gpu))
+        runner.replay()
+    x = torch.zeros(4, device=gpu)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        x.add_(1)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert x.sum().item() == 4.0
 
 
 def test_vlm_generation_call_sequence(gpu):
@@ -254,3 +287,4 @@ def test_checkpoint_loader_generates_like_the_built_model(gpu, tmp_path, a8w8):
     a = FusedGreedyGenerator(built).generate(prompt, max_new_tokens=16).tokens
     b = FusedGreedyGenerator(loaded).generate(prompt, max_new_tokens=16).tokens
     assert a == b
+
