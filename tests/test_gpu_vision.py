@@ -136,6 +136,15 @@ def test_vision_ops_reject_bad_shapes(gpu):
                           torch.zeros(4, 8, device=gpu), heads=2, dim=16)
     with pytest.raises(ValueError):
         K.layer_norm(x.cpu(), torch.ones(64), torch.zeros(64))
+    q = torch.zeros(1, 2, 16, 64, dtype=BF, device=gpu)
+    with pytest.raises(ValueError):  # head dim not a multiple of 8
+        K.vision_attention(*(torch.zeros(1, 2, 16, 12, dtype=BF, device=gpu),) * 3, 0.3)
+    with pytest.raises(ValueError):  # batch of two
+        K.vision_attention(*(torch.zeros(2, 2, 16, 64, dtype=BF, device=gpu),) * 3, 0.125)
+    with pytest.raises(ValueError):  # image offsets on the host
+        K.vision_attention(q, q, q, 0.125, torch.tensor([0, 8, 16], dtype=torch.int32))
+    with pytest.raises(ValueError):  # fewer than two offsets
+        K.vision_attention(q, q, q, 0.125, torch.tensor([0], dtype=torch.int32, device=gpu))
 
 
 # ------------------------------------------------------------- vision tower
