@@ -745,7 +745,7 @@ def vision_tower_timing(dev) -> dict:
 
     with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
         t_ref, ref = timed(lambda: tower(pix, grid_thw=grid).pooler_output)
-        integration._take_over(tower, integration._vision_model_fast(tower, integration.FusionConfig()))
+        integration.install_vision(tower, integration.FusionConfig())
         t_fused, got = timed(lambda: tower(pix, grid_thw=grid).pooler_output)
     rel = ((got.float() - ref.float()).norm() / ref.float().norm()).item()
     log(f"vision tower 784 patches: Transformers {t_ref:.3f} ms, fused {t_fused:.3f} ms, rel diff {rel:.2e}")

@@ -664,18 +664,56 @@ def _patch_embed(visual, pixels: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(x, w.reshape(w.shape[0], -1), proj.bias)
 
 
+def _pad_vision_mlp(mlp, multiple: int = 128) -> None:
+    """Give a vision MLP whose intermediate width is not a multiple of
+    ``multiple`` zero-padded weights: fc1 gets zero rows and zero bias (its
+    extra outputs are act(0)), fc2 zero columns, so the padded product equals
+    the original one and both GEMMs run on the library's whole-tile kernels
+    (Qwen3.5's 4304 -> 4352: fc2 29.4 -> 22.7 µs, fc1 20.4 -> 18.9 µs at 784
+    rows). The module's own weights become views of the padded ones, so no
+    memory is duplicated and its forward is unchanged. Only for GPU bf16
+    weights with a bias on fc1."""
+    fc1, fc2 = mlp.linear_fc1, mlp.linear_fc2
+    w1, b1, w2 = fc1.weight, fc1.bias, fc2.weight
+    if b1 is None or not (_gpu_bf16(w1) and _gpu_bf16(w2) and _gpu_bf16(b1)):
+        return
+    inter = w1.shape[0]
+    padded = -(-inter // multiple) * multiple
+    if padded == inter or w2.shape[1] != inter:
+        return
+    with torch.no_grad():
+        w1p = torch.zeros((padded, w1.shape[1]), dtype=w1.dtype, device=w1.device)
+        w1p[:inter].copy_(w1)
+        b1p = torch.zeros(padded, dtype=b1.dtype, device=b1.device)
+        b1p[:inter].copy_(b1)
+        w2p = torch.zeros((w2.shape[0], padded), dtype=w2.dtype, device=w2.device)
+        w2p[:, :inter].copy_(w2)
+    mlp.register_buffer("q35_fc1_w", w1p, persistent=False)
+    mlp.register_buffer("q35_fc1_b", b1p, persistent=False)
+    mlp.register_buffer("q35_fc2_w", w2p, persistent=False)
+    fc1.weight = torch.nn.Parameter(w1p[:inter], requires_grad=False)
+    fc1.bias = torch.nn.Parameter(b1p[:inter], requires_grad=False)
+    fc2.weight = torch.nn.Parameter(w2p[:, :inter], requires_grad=False)
+
+
 def _vision_mlp(mlp, x: torch.Tensor) -> torch.Tensor:
-    """Qwen3_5VisionMLP (fc1 -> tanh-approximated GELU -> fc2). With the
-    tanh GELU the activation is the library GEMM's epilogue applied to the
-    fp32 accumulator plus bias (one launch and one bf16 rounding fewer than
+    """Qwen3_5VisionMLP (fc1 -> tanh-approximated GELU -> fc2), on the
+    zero-padded weights when ``_pad_vision_mlp`` made them. With the tanh GELU
+    the activation is the library GEMM's epilogue applied to the fp32
+    accumulator plus bias (one launch and one bf16 rounding fewer than
     rounding fc1's output and running GELU on it); other activations run as
     the module wrote them."""
     fc1, fc2 = mlp.linear_fc1, mlp.linear_fc2
-    if isinstance(mlp.act_fn, GELUTanh) and fc1.bias is not None and x.dim() == 2:
-        h = torch._addmm_activation(fc1.bias, x, fc1.weight.t(), use_gelu=True)
+    w1 = getattr(mlp, "q35_fc1_w", None)
+    if w1 is None:
+        w1, b1, w2 = fc1.weight, fc1.bias, fc2.weight
     else:
-        h = mlp.act_fn(fc1(x))
-    return fc2(h)
+        b1, w2 = mlp.q35_fc1_b, mlp.q35_fc2_w
+    if isinstance(mlp.act_fn, GELUTanh) and b1 is not None and x.dim() == 2:
+        h = torch._addmm_activation(b1, x, w1.t(), use_gelu=True)
+    else:
+        h = mlp.act_fn(torch.nn.functional.linear(x, w1, b1))
+    return torch.nn.functional.linear(h, w2, fc2.bias)
 
 
 def _vision_merger(merger, hidden: torch.Tensor) -> torch.Tensor:
@@ -812,6 +850,16 @@ def _vision_model_fast(visual, config: FusionConfig):
     return fast
 
 
+def install_vision(visual, config: FusionConfig) -> int:
+    """Take over a Qwen3.5 vision tower's forward (the fused tower, its graph
+    per image size and grid) after padding its MLP weights; returns the
+    number of blocks."""
+    for blk in visual.blocks:
+        _pad_vision_mlp(blk.mlp)
+    _take_over(visual, _vision_model_fast(visual, config))
+    return len(visual.blocks)
+
+
 def _vision_tower(model: torch.nn.Module):
     inner = getattr(model, "model", None)
     return getattr(inner, "visual", None)
@@ -916,8 +964,7 @@ def install(model: torch.nn.Module, config: FusionConfig,
         _take_over(stack, _text_fast(stack, config))
     visual = _vision_tower(model)
     if config.vision and visual is not None:
-        _take_over(visual, _vision_model_fast(visual, config))
-        stats["vision"] = len(visual.blocks)
+        stats["vision"] = install_vision(visual, config)
     model._qwen35_fusion_config = config
     stats["lm_head_screen"] = int(config.lm_head_screen and attach_lm_head_screen(model))
     stats["delta_precompute_factors"] = int(config.delta and config.delta_precompute_factors)

@@ -271,7 +271,8 @@ def test_vision_attention_per_image(gpu, bounds, heads):
 
 def test_vision_mlp_fused_gelu_matches_module(gpu):
     """The block MLP with the tanh GELU as the fc1 GEMM's epilogue (one bf16
-    rounding fewer) against the module's own bf16 forward and an fp32 one."""
+    rounding fewer) against the module's own bf16 forward and an fp32 one,
+    then on zero-padded weights."""
     from transformers.models.qwen3_5 import modeling_qwen3_5 as impl
     from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5VisionConfig
     from ppu_amd import integration
@@ -284,8 +285,15 @@ def test_vision_mlp_fused_gelu_matches_module(gpu):
     mlp = mlp.to(gpu, torch.bfloat16)
     xb = x.to(gpu, torch.bfloat16)
     with torch.no_grad():
-        got = integration._vision_mlp(mlp, xb).float().cpu()
         mod = mlp(xb).float().cpu()
+        got = integration._vision_mlp(mlp, xb).float().cpu()
+        # zero-padded to 768 intermediate columns: the module's own forward
+        # (on views of the padded weights) is unchanged, the fused one close
+        integration._pad_vision_mlp(mlp)
+        assert mlp.q35_fc1_w.shape == (768, 256) and mlp.linear_fc1.weight.shape == (688, 256)
+        assert torch.equal(mlp(xb).float().cpu(), mod)
+        got_pad = integration._vision_mlp(mlp, xb).float().cpu()
     rel = lambda a, b: ((a - b).norm() / b.norm()).item()
     assert rel(got, exp32.detach()) <= rel(mod, exp32.detach()) * 1.5 + 1e-3
     assert rel(got, mod) < 1e-2
+    assert rel(got_pad, got) < 1e-3
