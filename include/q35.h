@@ -221,6 +221,21 @@ int q35_delta_prefill_gated(const void* qkv, int qkv_stride, const void* packed,
                             int H, int D, const void* norm_w, int norm_w_f32, float eps, void* y,
                             void* stream);
 
+/* q35_delta_prefill_gated with the prefill causal conv folded in: packed is
+ * the raw projection [B, L, packed_stride] (conv channels [0, 3*H*D), then z,
+ * a, b), conv_w the [3*H*D, 4] taps; the chunk prep computes the conv + SiLU
+ * of its rows itself (the bf16 conv output is never stored) and conv_state
+ * [B, 3*H*D, 4] receives the last four input rows, as q35_conv1d_prefill
+ * leaves it. L >= 64 only (the chunked path). Replaces the
+ * causal_conv1d_fused + delta_recurrent_fused + gated_rms_norm chain of
+ * integration.py:244-271 (kernels.py:659, :854, :139) for prefill. */
+int q35_delta_prefill_gated_conv(const void* packed, int packed_stride, const void* conv_w,
+                                 void* conv_state, const void* a_log, const void* dt_bias,
+                                 int params_f32, void* state, void* out, void* workspace,
+                                 long long workspace_floats, int B, int L, int H, int D,
+                                 const void* norm_w, int norm_w_f32, float eps, void* y,
+                                 void* stream);
+
 /* ---- full attention --------------------------------------------------- */
 
 /* qgkv_norm_rope: per-head Q/K RMSNorm (1 + w), partial RoPE, Q to [B,QH,L,D];

@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_delta_prefill": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _P, _P, _L, _I, _I, _I, _I, _P]),
     "q35_delta_prefill_gated": (
         _I, [_P, _I, _P, _I, _P, _P, _I, _P, _P, _P, _L, _I, _I, _I, _I, _P, _I, _F, _P, _P]),
+    "q35_delta_prefill_gated_conv": (
+        _I, [_P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _L, _I, _I, _I, _I, _P, _I, _F, _P, _P]),
     "q35_qgkv_norm_rope": (
         _I,
         [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],

@@ -589,9 +589,18 @@ Q35_DEV void mma4(const float4 a, const float4 bv, q35_f32x4 c0, q35_f32x4 c1, q
   o1 = c1;
 }
 
+// Optional inputs of chunk prep: with CONV, qkv is the raw packed projection
+// and the width-4 causal conv + SiLU of conv1d_prefill_vec4 is applied here
+// (the conv output is never stored); the conv state receives the last four
+// input rows, as conv1d_prefill writes it.
+struct ConvIn {
+  const uint16_t* w;  // [3*H*D, 4] taps
+  uint16_t* state;    // [B, 3*H*D, 4]
+};
+
 // PF32: A_log and dt_bias are fp32 (else bf16); a template parameter, since a
 // run-time branch between two load forms makes the compiler wait for each.
-template <bool PF32>
+template <bool PF32, bool CONV>
 __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restrict__ qkv,
                                                         int qkv_stride,
                                                         const uint16_t* __restrict__ packed,
@@ -600,7 +609,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
                                                         int a_off, int b_off,
                                                         float* __restrict__ ws,
                                                         float* __restrict__ gc_out, int L, int H,
-                                                        int nC) {
+                                                        int nC, ConvIn conv) {
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
@@ -619,23 +628,100 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   //    k_inv = rsqrt(sum of squares + 1e-6) over the head (the 4 threads of a
   //    token hold 32 dims each: quad sum), g = -e^{A_log} softplus(a +
   //    dt_bias), beta = sigmoid(b) [reference kernels.py:713-765].
+  // The token's gate inputs and the head's parameters, requested first (with
+  // CONV they are then in flight during the conv below).
+  const int ti = tid >> 2;
+  const int tcg = min(c * kChunk + ti, L - 1);
+  const uint16_t* prow0 = packed + ((size_t)b * L + tcg) * packed_stride;
+  const float a_raw = bf2f(prow0[a_off + h]), b_raw = bf2f(prow0[b_off + h]);
+  const float alog = ld_param(a_log, h, PF32), dtb = ld_param(dt_bias, h, PF32);
+  if (CONV) {
+    // 0. the conv of this chunk and head into Qh / Kh / Vv (fp32 copies of
+    //    the bf16 conv outputs): thread item = (8-channel group of q, k or v;
+    //    16 tokens), its 19 input rows (16 + 3 before; rows before token 0
+    //    are zero) and 4 x 8 taps loaded before any is used.
+    if (tid < 192) {
+      const int gsel = tid % 48, i0 = (tid / 48) * 16;
+      const int arr = gsel >> 4, d = (gsel & 15) * 8;
+      const int ch = arr * H * kD + h * kD + d;  // conv channel of the group
+      float* dst = arr == 0 ? Qh : (arr == 1 ? Kh : Vv);
+      uint4 raw[19], wr[4];
+#pragma unroll
+      for (int r = 0; r < 19; ++r) {
+        const int tr = min(max(c * kChunk + i0 - 3 + r, 0), L - 1);
+        raw[r] = *reinterpret_cast<const uint4*>(qkv + ((size_t)b * L + tr) * qkv_stride + ch);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wr[q] = *reinterpret_cast<const uint4*>(conv.w + (size_t)ch * 4 + q * 8);
+      float wt[8][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float f[8];
+        unpack8(wr[q], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wt[2 * q + e / 4][e % 4] = f[e];
+      }
+      // every row unpacked once (rows before token 0 as zeros)
+      float xr[19][8];
+#pragma unroll
+      for (int r = 0; r < 19; ++r) {
+        const bool before = c * kChunk + i0 - 3 + r < 0;
+        unpack8(before ? make_uint4(0u, 0u, 0u, 0u) : raw[r], xr[r]);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int t = c * kChunk + i0 + j;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float acc = 0.f;
+#pragma unroll
+          for (int tap = 0; tap < 4; ++tap) acc = fmaf(xr[j + tap][e], wt[e][tap], acc);
+          o[e] = silu_fast(round_bf(acc));
+        }
+        float ob[8];
+        unpack8(pack8(o), ob);  // the conv output is bf16
+        float* dr = dst + (i0 + j) * kCS + d;
+        *reinterpret_cast<float4*>(dr) = make_float4(ob[0], ob[1], ob[2], ob[3]);
+        *reinterpret_cast<float4*>(dr + 4) = make_float4(ob[4], ob[5], ob[6], ob[7]);
+        const int pos = t - (L - 4);
+        if (t < L && pos >= 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            conv.state[((size_t)b * 3 * H * kD + ch + e) * 4 + pos] = (uint16_t)f2bf(xr[j + 3][e]);
+        }
+      }
+    }
+    __syncthreads();
+  }
   {
     const int i = tid >> 2, qq = tid & 3;  // token, 32-dim quarter
     const int t = c * kChunk + i;
     const bool live = t < L;
     const int tc = min(t, L - 1);
     const uint16_t* row = qkv + ((size_t)b * L + tc) * qkv_stride;
-    const uint16_t* prow = packed + ((size_t)b * L + tc) * packed_stride;
-    const float a_raw = bf2f(prow[a_off + h]), b_raw = bf2f(prow[b_off + h]);
-    const float alog = ld_param(a_log, h, PF32), dtb = ld_param(dt_bias, h, PF32);
     float rq[4][8], rk[4][8];
     uint4 rv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int d = qq * 32 + u * 8;
-      unpack8(*reinterpret_cast<const uint4*>(row + h * kD + d), rq[u]);
-      unpack8(*reinterpret_cast<const uint4*>(row + H * kD + h * kD + d), rk[u]);
-      rv[u] = *reinterpret_cast<const uint4*>(row + 2 * H * kD + h * kD + d);
+      if (CONV) {
+        const float* sq = &Qh[i * kCS + d];
+        const float* sk = &Kh[i * kCS + d];
+        const float* sv = &Vv[i * kCS + d];
+        float fv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          rq[u][e] = sq[e];
+          rk[u][e] = sk[e];
+          fv[e] = sv[e];
+        }
+        rv[u] = pack8(fv);  // exact: the values are bf16
+      } else {
+        unpack8(*reinterpret_cast<const uint4*>(row + h * kD + d), rq[u]);
+        unpack8(*reinterpret_cast<const uint4*>(row + H * kD + h * kD + d), rk[u]);
+        rv[u] = *reinterpret_cast<const uint4*>(row + 2 * H * kD + h * kD + d);
+      }
     }
     float qs = 0.f, ks = 0.f;
 #pragma unroll
@@ -1260,7 +1346,7 @@ namespace {
 int delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packed_stride,
                   const void* a_log, const void* dt_bias, int params_f32, void* state, void* out,
                   void* workspace, long long workspace_floats, int B, int L, int H, int D,
-                  const GatedNormArgs* gn, hipStream_t stream) {
+                  const GatedNormArgs* gn, hipStream_t stream, const ConvIn* conv = nullptr) {
   Q35_CHECK_ARG(B >= 0 && L > 0 && H > 0 && D == kD);
   Q35_CHECK_ARG(qkv_stride >= 3 * H * D && qkv_stride % 8 == 0);
   Q35_CHECK_ARG(packed_stride >= 4 * H * D + 2 * H);
@@ -1287,14 +1373,17 @@ int delta_prefill(const void* qkv, int qkv_stride, const void* packed, int packe
   float* gc = chunk_ws + (size_t)B * H * nC * kChunkFloats;
   // Snapshots start 16-byte aligned after the B*H*nC chunk decays.
   float* snap = gc + (((size_t)B * H * nC + 3) & ~(size_t)3);
-  if (params_f32)
-    delta_chunk_prep<true><<<dim3(nC, H, B), 256, 0, stream>>>(
-        (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
-        params_f32, 4 * H * D, 4 * H * D + H, chunk_ws, gc, L, H, nC);
-  else
-    delta_chunk_prep<false><<<dim3(nC, H, B), 256, 0, stream>>>(
-        (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,
-        params_f32, 4 * H * D, 4 * H * D + H, chunk_ws, gc, L, H, nC);
+  const ConvIn cv = conv ? *conv : ConvIn{nullptr, nullptr};
+#define PREP(PF, CV)                                                                              \
+  delta_chunk_prep<PF, CV><<<dim3(nC, H, B), 256, 0, stream>>>(                                   \
+      (const uint16_t*)qkv, qkv_stride, (const uint16_t*)packed, packed_stride, a_log, dt_bias,   \
+      params_f32, 4 * H * D, 4 * H * D + H, chunk_ws, gc, L, H, nC, cv)
+  if (params_f32) {
+    if (conv) PREP(true, true); else PREP(true, false);
+  } else {
+    if (conv) PREP(false, true); else PREP(false, false);
+  }
+#undef PREP
   e = q35_last_error();
   if (e) return e;
   delta_chunk_scan<<<dim3((kD / 16) * H, B), 256, 0, stream>>>(chunk_ws, gc, (float*)state, snap,
@@ -1350,6 +1439,28 @@ int q35_delta_prefill_gated(const void* qkv, int qkv_stride, const void* packed,
   if (e || L >= kChunkMinL) return e;
   return q35_gated_rmsnorm_grouped(out, (const uint16_t*)packed + 3ll * H * D, H, packed_stride,
                                    norm_w, norm_w_f32, y, B * L * H, eps, stream);
+}
+
+
+// q35_delta_prefill_gated with the causal conv folded into the chunk prep:
+// the input is the raw packed projection (conv channels [0, 3*H*D), then z,
+// a, b as for q35_delta_prefill_gated), conv_w the [3*H*D, 4] taps and
+// conv_state receives the last four input rows of every conv channel (what
+// q35_conv1d_prefill writes). Chunked path only: L >= 64 (else error 1).
+int q35_delta_prefill_gated_conv(const void* packed, int packed_stride, const void* conv_w,
+                                 void* conv_state, const void* a_log, const void* dt_bias,
+                                 int params_f32, void* state, void* out, void* workspace,
+                                 long long workspace_floats, int B, int L, int H, int D,
+                                 const void* norm_w, int norm_w_f32, float eps, void* y,
+                                 hipStream_t stream) {
+  Q35_CHECK_ARG(L >= kChunkMinL && conv_w && conv_state && q35_aligned16(conv_w));
+  Q35_CHECK_ARG(norm_w && y && out && D == kD && packed_stride % 8 == 0);
+  Q35_CHECK_ARG(q35_aligned16(norm_w) && q35_aligned16(y) && q35_aligned16(packed));
+  const GatedNormArgs gn{(const uint16_t*)packed + 3ll * H * D, packed_stride, norm_w, norm_w_f32,
+                         eps, (uint16_t*)y};
+  const ConvIn cv{(const uint16_t*)conv_w, (uint16_t*)conv_state};
+  return delta_prefill(packed, packed_stride, packed, packed_stride, a_log, dt_bias, params_f32,
+                       state, out, workspace, workspace_floats, B, L, H, D, &gn, stream, &cv);
 }
 
 }  // extern "C"

@@ -67,6 +67,10 @@ class FusionConfig:
     # recomputation of the rows it cannot exclude (same token, about half the
     # bytes; 0.5 GB more device memory for the 2B vocabulary)
     lm_head_screen: bool = True
+    # prefill of 64+ tokens: the DeltaNet causal conv computed inside the
+    # chunk prep from the raw projection (one launch and one 12 MB
+    # intermediate fewer per layer; same values)
+    delta_conv_in_prep: bool = True
 
 
 def _gpu_bf16(t: Any) -> bool:
@@ -309,8 +313,15 @@ def _delta_prefill(mixer, hidden: torch.Tensor, cache, config: FusionConfig, qua
     batch, length, _ = hidden.shape
     packed = mixer.q35_in(hidden.contiguous()) if quant is None else mixer.q35_in.from_int8(*quant)
     conv_state, rec_state = _delta_state(mixer, cache, batch, hidden.device)
-    qkv = K.causal_conv1d_fused(packed, mixer.q35_conv_w, conv_state)
     dv = mixer.head_v_dim
+    if (config.delta_conv_in_prep and dv == 128 and length >= 64 and mixer.conv_dim == 3 * mixer.value_dim
+            and mixer.q35_conv_w.shape[1] == 4 and conv_state.dtype == torch.bfloat16):
+        core = K.delta_prefill_gated_conv(packed, mixer.q35_conv_w, conv_state, mixer.A_log,
+                                          mixer.dt_bias, rec_state, mixer.norm.weight,
+                                          mixer.layer_norm_epsilon)
+        core = core.reshape(batch, length, mixer.value_dim)
+        return mixer.q35_out.to_int32(core) if int32_out else mixer.q35_out(core)
+    qkv = K.causal_conv1d_fused(packed, mixer.q35_conv_w, conv_state)
     if dv == 128 and length > 1 and mixer.conv_dim == 3 * mixer.value_dim:
         core = K.delta_prefill_gated(qkv, packed, mixer.A_log, mixer.dt_bias, rec_state,
                                      mixer.norm.weight, mixer.layer_norm_epsilon)

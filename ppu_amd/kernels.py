@@ -752,6 +752,56 @@ def delta_prefill_gated(
 
 
 @_device_checked
+def delta_prefill_gated_conv(
+    packed_projection: torch.Tensor,
+    conv_weight: torch.Tensor,
+    conv_state: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    state: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """``causal_conv1d_fused`` (width 4, prefill) + ``delta_prefill_gated`` in
+    one chain whose chunk prep applies the conv itself: the raw packed
+    projection in, ``conv_state`` left as the prefill conv leaves it
+    (reference integration.py:244-271). 64 or more tokens (the chunked path).
+    Returns ``[B, L, H, D]`` bf16; ``state`` and ``conv_state`` updated in
+    place."""
+
+    if packed_projection.ndim != 3 or state.ndim != 4 or conv_weight.ndim != 2 or conv_state.ndim != 3:
+        raise ValueError("invalid delta recurrent tensor rank")
+    if not (packed_projection.is_contiguous() and state.is_contiguous() and conv_weight.is_contiguous()
+            and conv_state.is_contiguous()):
+        raise ValueError("delta recurrent tensors must be contiguous")
+    batch, seq_len, packed_width = packed_projection.shape
+    _, heads, dim, value_dim = state.shape
+    channels = 3 * heads * dim
+    if dim != value_dim or dim != 128 or seq_len < 64:
+        raise ValueError("fused conv prefill needs head dim 128 and at least 64 tokens")
+    if conv_weight.shape != (channels, 4) or conv_state.shape != (batch, channels, 4):
+        raise ValueError("causal conv shapes do not match")
+    if packed_width < channels + heads * dim + 2 * heads or packed_width % 8:
+        raise ValueError("packed projection does not hold [qkv | z | a | b]")
+    if norm_weight.numel() != dim:
+        raise ValueError(f"norm weight has {norm_weight.numel()} values, expected {dim}")
+    if state.dtype != torch.float32:
+        raise ValueError("delta recurrent state must be float32")
+    _need_bf16(packed_projection, conv_weight, conv_state)
+    al, dt, pf = _delta_params(a_log, dt_bias)
+    w, wf = _param(norm_weight)
+    out = torch.empty((batch, seq_len, heads, dim), device=state.device, dtype=torch.bfloat16)
+    y = torch.empty_like(out)
+    floats = _lib.load().q35_delta_prefill_workspace(batch, seq_len, heads)
+    workspace = torch.empty(floats, device=state.device, dtype=torch.float32)
+    _lib.call("q35_delta_prefill_gated_conv", packed_projection.data_ptr(), packed_width,
+              conv_weight.data_ptr(), conv_state.data_ptr(), al.data_ptr(), dt.data_ptr(), pf,
+              state.data_ptr(), out.data_ptr(), workspace.data_ptr(), floats, batch, seq_len, heads,
+              dim, w.data_ptr(), wf, float(eps), y.data_ptr(), _stream(state))
+    return y
+
+
+@_device_checked
 def delta_decode_fused(
     packed_projection: torch.Tensor,
     conv_weight: torch.Tensor,

@@ -402,6 +402,35 @@ def test_delta_prefill_gated(gpu, seq_len):
     torch.testing.assert_close(st.cpu(), st_ref, rtol=1e-3, atol=1e-6)
 
 
+@pytest.mark.parametrize("seq_len", [64, 67, 200, 1024])
+def test_delta_prefill_gated_conv_equals_conv_then_prefill(gpu, seq_len):
+    """The causal conv folded into the chunk prep gives the output, recurrent
+    state and conv state of the separate conv launch followed by the gated
+    prefill, bit for bit (same conv arithmetic, same bf16 conv output), and
+    rejects fewer than 64 tokens."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 15)
+    heads, dim = 16, 128
+    conv_dim = 3 * heads * dim
+    _, packed, a_log, dt_bias, state = _delta_inputs(g, seq_len)
+    conv_w = randn(g, conv_dim, 4, scale=0.3).to(gpu)
+    norm_w = randn(g, dim, scale=0.02, mean=1.0).to(gpu)
+    packed, a_log, dt_bias = packed.to(gpu), a_log.to(gpu), dt_bias.to(gpu)
+    cs_a = torch.full((1, conv_dim, 4), 7.0, dtype=BF, device=gpu)  # prefill ignores the old state
+    cs_b = cs_a.clone()
+    st_a, st_b = state.to(gpu), state.to(gpu)
+    qkv = K.causal_conv1d_fused(packed, conv_w, cs_a)
+    y_a = K.delta_prefill_gated(qkv, packed, a_log, dt_bias, st_a, norm_w, 1e-6)
+    y_b = K.delta_prefill_gated_conv(packed, conv_w, cs_b, a_log, dt_bias, st_b, norm_w, 1e-6)
+    assert torch.equal(y_a, y_b)
+    assert torch.equal(st_a, st_b)
+    assert torch.equal(cs_a, cs_b)
+    with pytest.raises(ValueError):
+        K.delta_prefill_gated_conv(packed[:, :63].contiguous(), conv_w, cs_b, a_log, dt_bias, st_b,
+                                   norm_w, 1e-6)
+
+
 def test_config4_delta_64_steps(gpu):
     """16 heads x 128, S ~N(0,0.1), conv width 4 on q/k/v,
     beta = sigmoid(N(0,1)), g = -softplus(N(0,1)) (A_log = 0, dt_bias = 0),
