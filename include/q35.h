@@ -72,6 +72,14 @@ int q35_gated_rmsnorm_grouped(const void* x, const void* gate, int group_rows,
  * Replaces qwen35_fused/kernels.py:170 (kernel :158-180). */
 int q35_silu_mul(const void* packed, void* out, long long rows, int width, void* stream);
 
+/* q35_silu_mul on the transposed product of a packed [gate; up] projection:
+ * packed_t [2 * width, rows] channel-major (what W @ X^T gives), out [rows,
+ * width] token-major, same arithmetic. width % 64 == 0, rows % 8 == 0. The
+ * prefill MLP computes its gate/up GEMM in that orientation (the library's
+ * kernel for it is faster) and this entry transposes back while it applies
+ * silu_and_mul (reference kernels.py:170, integration.py:183-185). */
+int q35_silu_mul_t(const void* packed_t, void* out, int rows, int width, void* stream);
+
 /* attention_gate_mul: out = bf16(x * bf16(sigmoid(gate))), gate read from the
  * packed QGKV row. Replaces qwen35_fused/kernels.py:312 (kernel :285-333). */
 int q35_attn_gate_mul(const void* x, const void* packed, void* out, long long tokens, int hidden,

@@ -246,6 +246,59 @@ __global__ __launch_bounds__(256) void silu_mul_vec(const uint16_t* __restrict__
   }
 }
 
+// silu_mul on the transposed product of a packed [gate; up] projection:
+// packed_t is [2 * width, rows] (channel-major: gate channels, then up
+// channels, each a row of `rows` tokens), out is [rows, width] token-major,
+// out[m, n] = bf16(bf16(silu(g[n, m])) * u[n, m]) as silu_mul_vec computes
+// it. Tile of 64 channels x 64 tokens per workgroup: thread (n = t/4, q =
+// t%4) loads 16 tokens of gate and up of channel n (16-byte loads along the
+// tokens), computes them, and writes the bf16 results into an LDS tile of
+// stride 33 dwords; thread (m = t/4, q) then reads the 16 channels 16q..16q+15
+// of token m (conflict-free: the four q groups sit 16 banks apart) and
+// stores 32 contiguous bytes. rows % 8 == 0; tokens past rows are skipped.
+constexpr int kSmtS = 66;  // LDS row stride in bf16 (33 dwords)
+__global__ __launch_bounds__(256) void silu_mul_t_tile(const uint16_t* __restrict__ pt,
+                                                       uint16_t* __restrict__ out, int rows,
+                                                       int width) {
+  __shared__ alignas(16) uint16_t os[64 * kSmtS];
+  const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
+  const int t = threadIdx.x, q = t & 3;
+  {
+    const int n = t >> 2;
+    const int m = m0 + 16 * q;
+    const uint16_t* g = pt + (size_t)(n0 + n) * rows;
+    const uint16_t* u = pt + (size_t)(width + n0 + n) * rows;
+    uint4 graw[2], uraw[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int mm = min(m + 8 * h, rows - 8);  // rows % 8 == 0: always a whole 8-token group
+      graw[h] = *reinterpret_cast<const uint4*>(g + mm);
+      uraw[h] = *reinterpret_cast<const uint4*>(u + mm);
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(os + n * kSmtS + 16 * q);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float gf[8], uf[8], o[8];
+      unpack8(graw[h], gf);
+      unpack8(uraw[h], uf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = round_bf(silu_fast(gf[e])) * uf[e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[4 * h + e] = pack_bf2(o[2 * e], o[2 * e + 1]);
+    }
+  }
+  __syncthreads();
+  const int m = t >> 2;
+  if (m0 + m >= rows) return;
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    w[e] = (uint32_t)os[(16 * q + 2 * e) * kSmtS + m] | ((uint32_t)os[(16 * q + 2 * e + 1) * kSmtS + m] << 16);
+  uint16_t* o = out + (size_t)(m0 + m) * width + n0 + 16 * q;
+  *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint4*>(o + 8) = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
 // out = bf16( x * bf16(sigmoid(gate)) ); the gate of head h sits at
 // packed[token, h*2*head_dim + head_dim + col] [reference kernels.py:285-333].
 __global__ __launch_bounds__(256) void attn_gate_elems(const uint16_t* __restrict__ x,
@@ -382,6 +435,15 @@ int q35_silu_mul(const void* packed, void* out, long long rows, int width, hipSt
   Q35_CHECK_ARG(grid < (1ll << 31));
   silu_mul_elems<<<(unsigned)grid, 256, 0, stream>>>((const uint16_t*)packed, (uint16_t*)out, total,
                                                      width);
+  return q35_last_error();
+}
+
+int q35_silu_mul_t(const void* packed_t, void* out, int rows, int width, hipStream_t stream) {
+  Q35_CHECK_ARG(rows >= 0 && width > 0 && width % 64 == 0 && rows % 8 == 0);
+  Q35_CHECK_ARG(q35_aligned16(packed_t) && q35_aligned16(out));
+  if (rows == 0) return 0;
+  const dim3 grid((unsigned)(width / 64), (unsigned)((rows + 63) / 64));
+  silu_mul_t_tile<<<grid, 256, 0, stream>>>((const uint16_t*)packed_t, (uint16_t*)out, rows, width);
   return q35_last_error();
 }
 

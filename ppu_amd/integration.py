@@ -71,6 +71,10 @@ class FusionConfig:
     # chunk prep from the raw projection (one launch and one 12 MB
     # intermediate fewer per layer; same values)
     delta_conv_in_prep: bool = True
+    # prefill of 64+ tokens (a multiple of 8), bf16 linears: the packed gate/up
+    # GEMM as W @ X^T (the library's kernel for that orientation is faster)
+    # and the SiLU-mul transposing back to token-major rows
+    prefill_gate_up_transposed: bool = True
 
 
 def _gpu_bf16(t: Any) -> bool:
@@ -260,7 +264,14 @@ def _mlp_apply(mlp, x: torch.Tensor, config: FusionConfig) -> torch.Tensor:
     elif config.ppu_swiglu_gemv and x.shape[:-1] == (1, 1):
         act = K.ppu_swiglu_gemv(x, gate_up.w, block_n=config.ppu_swiglu_block_n)
     else:
-        act = K.silu_and_mul(gate_up(x))
+        rows = x.numel() // x.shape[-1]
+        width = gate_up.w.shape[0] // 2
+        if (config.prefill_gate_up_transposed and rows >= 64 and rows % 8 == 0 and width % 64 == 0
+                and _gpu_bf16(gate_up.w)):
+            packed_t = torch.mm(gate_up.w, x.reshape(rows, -1).t())
+            act = K.silu_and_mul_t(packed_t).reshape(*x.shape[:-1], width)
+        else:
+            act = K.silu_and_mul(gate_up(x))
     return mlp.q35_down(act)
 
 

@@ -204,6 +204,25 @@ def silu_and_mul(packed: torch.Tensor) -> torch.Tensor:
 
 
 @_device_checked
+def silu_and_mul_t(packed_t: torch.Tensor) -> torch.Tensor:
+    """``silu_and_mul`` of the transposed packed projection ``[2*width,
+    rows]`` (gate rows, then up rows), returned token-major ``[rows, width]``
+    (reference kernels.py:170 on ``packed_t.T``). width % 64 == 0, rows % 8
+    == 0."""
+
+    if packed_t.ndim != 2 or not packed_t.is_contiguous():
+        raise ValueError("transposed packed projection must be a contiguous [2*width, rows] tensor")
+    two_w, rows = packed_t.shape
+    width = two_w // 2
+    if two_w % 2 or width % 64 or rows % 8:
+        raise ValueError("transposed silu_and_mul needs width % 64 == 0 and rows % 8 == 0")
+    _need_bf16(packed_t)
+    out = torch.empty((rows, width), device=packed_t.device, dtype=packed_t.dtype)
+    _lib.call("q35_silu_mul_t", packed_t.data_ptr(), out.data_ptr(), rows, width, _stream(packed_t))
+    return out
+
+
+@_device_checked
 def attention_gate_mul(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int) -> torch.Tensor:
     """Multiply attention output by the gate inside the packed QGKV. reference kernels.py:312."""
 

@@ -104,6 +104,22 @@ def test_silu_and_mul(gpu):
     close(K.silu_and_mul(p.to(gpu)), ref.silu_and_mul(p))
 
 
+@pytest.mark.parametrize("rows,width", [(8, 64), (72, 128), (1024, 6144), (200, 192)])
+def test_silu_and_mul_t_equals_silu_and_mul_of_transpose(gpu, rows, width):
+    """The transposing form on W @ X^T's channel-major product: bit-equal to
+    silu_and_mul of the token-major product (same arithmetic), for token
+    counts that do not fill the last 64-token tile too."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 16)
+    packed = randn(g, rows, 2 * width, scale=2.0).to(gpu)
+    got = K.silu_and_mul_t(packed.t().contiguous())
+    assert torch.equal(got, K.silu_and_mul(packed))
+    with pytest.raises(ValueError):
+        K.silu_and_mul_t(packed.t().contiguous()[:, : rows - 1].contiguous() if rows > 8 else
+                         torch.zeros(2 * width, 7, dtype=BF, device=gpu))
+
+
 def test_attention_gate_mul(gpu):
     from ppu_amd import kernels as K
 
