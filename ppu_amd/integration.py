@@ -697,6 +697,8 @@ def _pad_vision_mlp(mlp, multiple: int = 128) -> None:
     weights with a bias on fc1."""
     fc1, fc2 = mlp.linear_fc1, mlp.linear_fc2
     w1, b1, w2 = fc1.weight, fc1.bias, fc2.weight
+    if getattr(mlp, "q35_fc1_w", None) is not None:
+        return  # already padded
     if b1 is None or not (_gpu_bf16(w1) and _gpu_bf16(w2) and _gpu_bf16(b1)):
         return
     inter = w1.shape[0]

@@ -290,6 +290,9 @@ def test_vision_mlp_fused_gelu_matches_module(gpu):
         # zero-padded to 768 intermediate columns: the module's own forward
         # (on views of the padded weights) is unchanged, the fused one close
         integration._pad_vision_mlp(mlp)
+        padded = mlp.q35_fc1_w
+        integration._pad_vision_mlp(mlp)  # a second call keeps the padded weights
+        assert mlp.q35_fc1_w is padded
         assert mlp.q35_fc1_w.shape == (768, 256) and mlp.linear_fc1.weight.shape == (688, 256)
         assert torch.equal(mlp(xb).float().cpu(), mod)
         got_pad = integration._vision_mlp(mlp, xb).float().cpu()
