@@ -373,6 +373,13 @@ Q35_DEV q35_f32x4 va_mfma(const uint4 a, const uint4 b, q35_f32x4 c) {
 
 typedef uint32_t va_u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kVaKeys = 64;    // keys per block
+// K / V rows in LDS: 128 elements (16 chunks of 16 bytes) per key, chunk c of
+// row r stored at chunk c ^ va_swz(r % 16), a 4 x 4 transpose of the row's
+// low bits. The 16 rows of a K read (one chunk each) then sit on 16 distinct
+// chunks, and the 8 rows {0-3, 8-11} (or {4-7, 12-15}) of a transposed V read
+// (two chunks each) on 16 distinct chunks: both without bank conflicts.
+constexpr int kVaRS = 128;
+Q35_DEV int va_swz(int r15) { return ((r15 & 3) << 2) | ((r15 >> 2) & 3); }
 constexpr int kVaRows = 64;    // query rows per workgroup
 constexpr int kVaPt = 16 + 4;  // padded P^T row (16 query rows)
 
@@ -402,15 +409,16 @@ Q35_DEV void va_block(const uint16_t* __restrict__ Ks, const uint16_t* __restric
                       uint16_t* __restrict__ pt, const uint4 (&qa)[QT], q35_f32x4 (&o)[OT],
                       float (&m)[4], float (&lp)[4], int kb, const int (&s0)[4],
                       const int (&s1)[4], float c, int col, int kg, int te, int tq) {
-  constexpr int RS = 32 * QT + 8;
+  constexpr int RS = kVaRS;
+  const int gk = va_swz(col);  // K rows 16 st + col
   q35_f32x4 s[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     s[st] = {0.f, 0.f, 0.f, 0.f};
-    const uint16_t* krow = Ks + (16 * st + col) * RS + 8 * kg;
+    const uint16_t* krow = Ks + (16 * st + col) * RS;
 #pragma unroll
     for (int t = 0; t < QT; ++t)
-      s[st] = va_mfma(qa[t], *reinterpret_cast<const uint4*>(krow + 32 * t), s[st]);
+      s[st] = va_mfma(qa[t], *reinterpret_cast<const uint4*>(krow + 8 * ((kg + 4 * t) ^ gk)), s[st]);
   }
   float corr[4], p[4][4];
   bool moved = false;
@@ -461,11 +469,15 @@ Q35_DEV void va_block(const uint16_t* __restrict__ Ks, const uint16_t* __restric
     const uint2 a0 = va_read_tr16(pth + (8 * kg + te) * kVaPt + 4 * tq);
     const uint2 a1 = va_read_tr16(pth + (8 * kg + 4 + te) * kVaPt + 4 * tq);
     const uint4 pa = make_uint4(a0.x, a0.y, a1.x, a1.y);
-    const uint16_t* v0 = Vs + (32 * half + 8 * kg + te) * RS + 4 * tq;
-    const uint16_t* v1 = Vs + (32 * half + 8 * kg + 4 + te) * RS + 4 * tq;
+    // dims 16 d + 4 tq .. +3 of rows r0 and r0 + 4: chunk 2 d + tq / 2, half tq % 2
+    const int r0 = 8 * kg + te;
+    const int g0 = va_swz(r0 & 15), g1 = va_swz((r0 + 4) & 15);
+    const uint16_t* v0 = Vs + (32 * half + r0) * RS + 4 * (tq & 1);
+    const uint16_t* v1 = Vs + (32 * half + r0 + 4) * RS + 4 * (tq & 1);
 #pragma unroll
     for (int d = 0; d < OT; ++d) {
-      const uint2 b0 = va_read_tr16(v0 + 16 * d), b1 = va_read_tr16(v1 + 16 * d);
+      const int cv = 2 * d + (tq >> 1);
+      const uint2 b0 = va_read_tr16(v0 + 8 * (cv ^ g0)), b1 = va_read_tr16(v1 + 8 * (cv ^ g1));
       o[d] = va_mfma(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), o[d]);
     }
   }
@@ -481,7 +493,7 @@ __global__ __launch_bounds__(256 * KS) void vision_attn_fa(
   constexpr int NT = 256 * KS;         // threads
   constexpr int SK = kVaKeys * KS;     // keys per stage (one 64-key block per wave group)
   constexpr int DP = 32 * QT;          // padded head dim
-  constexpr int RS = DP + 8;           // LDS row stride (elements): rows 16-byte aligned
+  constexpr int RS = kVaRS;            // LDS row stride (elements), swizzled chunks
   constexpr int NLD = (SK * DP / 8 + NT - 1) / NT;  // 16-byte K (and V) chunks per thread
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int rg = wid & 3;              // 16-row group of the tile
@@ -533,12 +545,16 @@ __global__ __launch_bounds__(256 * KS) void vision_attn_fa(
 
   __shared__ alignas(16) uint16_t kv_s[2][2][SK * RS];         // [buf][K, V][key][dim]
   __shared__ alignas(16) uint16_t pt_s[4 * KS][kVaKeys * kVaPt];  // [wave][key][row]
-  // Zero the padded dims [D, RS) of every K and V row once: they meet the
-  // zero-padded Q dims in S (0 * finite) and only unused output dims in O.
-  const int pad = RS - D;
-  for (int i = tid; i < 2 * 2 * SK * pad; i += NT) {
-    const int row = i / pad, cc = D + i % pad;
-    (&kv_s[0][0][0])[row * RS + cc] = 0;
+  // Zero the padded dims [D, 128) of every K and V row once (whole 16-byte
+  // chunks, at their swizzled places): they meet the zero-padded Q dims in S
+  // (0 * finite) and only unused output dims in O.
+  {
+    const int pc = 16 - D / 8;
+    for (int i = tid; i < 2 * 2 * SK * pc; i += NT) {
+      const int row = i / pc, cc = D / 8 + i % pc;
+      *reinterpret_cast<uint4*>(&(&kv_s[0][0][0])[row * RS + 8 * (cc ^ va_swz(row & 15))]) =
+          make_uint4(0u, 0u, 0u, 0u);
+    }
   }
 
   // This thread's 16-byte chunks of a stage: chunk gi = tid + NT j is key
@@ -570,7 +586,7 @@ __global__ __launch_bounds__(256 * KS) void vision_attn_fa(
 #pragma unroll
     for (int j = 0; j < NLD; ++j) {
       if (lok[j]) {
-        const int off = lrow[j] * RS + lcol[j];
+        const int off = lrow[j] * RS + 8 * ((lcol[j] >> 3) ^ va_swz(lrow[j] & 15));
         *reinterpret_cast<va_u32x4*>(&kv_s[buf][0][off]) = kr[j];
         *reinterpret_cast<va_u32x4*>(&kv_s[buf][1][off]) = vr[j];
       }
