@@ -1,7 +1,9 @@
 // Vision-encoder kernels of the image path (reference kernels.py:336-416 and
 // 1188-1336): LayerNorm with and without the residual add, the interpolated
-// position-embedding add, and the packed-QKV split into [1, heads, tokens,
-// dim] with rotate-half RoPE on q and k.
+// position-embedding add, the packed-QKV split into [1, heads, tokens, dim]
+// with rotate-half RoPE on q and k, and the blocks' non-causal per-image
+// attention on the matrix cores (the attention call of reference
+// integration.py:671-731).
 //
 //   layer_norm              y = bf16((x - mean) * rsqrt(var + eps) * w + b),
 //                           mean and var over the row in fp32
@@ -12,13 +14,15 @@
 //   vision_qkv_rope         o[c] = bf16(x[c] * cos[c] + (sign_c * x[partner c]) * sin[c]),
 //                           partner = c +- dim/2, sign = -1 below dim/2;
 //                           v copied
+//   vision_attention        o = bf16(softmax(q k^T * scale) v) over the keys of
+//                           the query's own image, P rounded to bf16
 //
-// Rows are independent, so every kernel runs one wave64 per row (per (token,
-// head) for the RoPE split) and reduces with the DPP wave sums; widths that
-// are multiples of 8 use 16-byte accesses with the row held in registers
-// between the two LayerNorm passes (one memory round trip per row), other
-// widths a lane-strided scalar form. Builds use -ffp-contract=off, so a*b+c
-// is fused only where fmaf is written.
+// The LayerNorms run one wave64 per row and reduce with the DPP wave sums;
+// widths that are multiples of 8 use 16-byte accesses with the row held in
+// registers between the two passes (one memory round trip per row), other
+// widths a lane-strided scalar form. The RoPE split runs one thread per four
+// rotation pairs (or one wave per (token, head) for other head dims). Builds
+// use -ffp-contract=off, so a*b+c is fused only where fmaf is written.
 #include "q35_common.hpp"
 
 namespace {
