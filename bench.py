@@ -1,6 +1,6 @@
 """Decode tokens/s and TTFT of the synthetic Qwen3.5-2B-shaped decoder on one MI355X.
 
-Workload: the 24-layer 2B-shaped decoder with seeded
+Workload (Benchmark config 5): the 24-layer 2B-shaped decoder with seeded
 random-init bf16 weights (synthetic; no checkpoint), batch 1, a 1024-token
 prompt of uniform-random token ids, then greedy decode. A "step" is one
 greedy decode token: one replay of the captured decode graph (24 layers +
@@ -23,7 +23,7 @@ Printed (one JSON line on stdout):
   step_roofline  the whole decode step: HBM bytes one token needs (packed
                weights, lm_head, recurrent/conv state read + write, K/V read
                at the mean context of the timed steps) / ms_per_step
-  kernels     per-kernel achieved HBM GB/s of the BASELINE configs 1-4
+  kernels     per-kernel achieved HBM GB/s of the Benchmark configs 1-4
                (rotating >= 640 MB of distinct buffers so the 256 MB MALL does
                not serve the weights), in-graph time per launch
   variants     the same decode and TTFT measurement for the other linear
@@ -246,7 +246,7 @@ def step_bytes(model, context: float) -> int:
 
 
 def kernel_table(dev) -> dict:
-    """BASELINE configs 1-4 as individual launches, rotating distinct buffers."""
+    """Benchmark configs 1-4 as individual launches, rotating distinct buffers."""
     import torch
 
     from ppu_amd import kernels as K
@@ -907,7 +907,7 @@ def main() -> None:
     del model
     torch.cuda.empty_cache()
 
-    # The other linear variant of BASELINE config 5 on the same weights.
+    # The other linear variant of Benchmark config 5 on the same weights.
     variants = {}
     if not args.no_other_variant:
         other = "a8w8" if args.variant == "bf16" else "bf16"

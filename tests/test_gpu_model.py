@@ -264,7 +264,7 @@ def test_graph_replay_matches_eager_decode(gpu):
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("variant", ["bf16", "a8w8"])
 def test_2b_prefill_1024_decode_64_vs_oracle(gpu, variant):
-    """the full 2B-shaped decoder, 1024-token uniform-random
+    """Benchmark config 5: the full 2B-shaped decoder, 1024-token uniform-random
     prompt, 64 greedy tokens on the GPU (fused decode graph); the CPU oracle
     decoder is teacher-forced on the same tokens and must agree at every step
     whose top-2 margin exceeds the bf16 rounding noise."""
@@ -316,7 +316,7 @@ def _layer_state_errors(cache, index, states, rows):
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("variant", ["bf16", "a8w8"])
 def test_2b_layerwise_teacher_forced(gpu, variant):
-    """BASELINE config 5, one layer at a time: every GPU layer is run from the
+    """Benchmark config 5, one layer at a time: every GPU layer is run from the
     oracle's own input and cache state, so an error cannot hide in the
     amplification of 24 chaotic random-init layers. Prefill (1024 tokens, the
     product prefill path per layer) and the second decode step (the fused

@@ -142,7 +142,7 @@ def test_linear(gpu, n, k):
 
 
 def test_config1_residual_norm_gemv(gpu):
-    """x, residual ~N(0,1) [1,2048], w ~N(1,0.02), eps 1e-6,
+    """Benchmark config 1: x, residual ~N(0,1) [1,2048], w ~N(1,0.02), eps 1e-6,
     then W[6144,2048] ~N(0,0.02), fused in one launch."""
     from ppu_amd import kernels as K
 
@@ -384,7 +384,7 @@ def test_delta_recurrent(gpu, seq_len):
     got = K.delta_recurrent_fused(qkv.to(gpu), packed.to(gpu), a_log.to(gpu), dt_bias.to(gpu), st,
                                   precompute_factors=True)
     close(got, exp)
-    # state: 1e-3 relative (BASELINE tolerance), plus a tiny absolute floor.
+    # state: 1e-3 relative (the state tolerance of the parity contract), plus a tiny absolute floor.
     torch.testing.assert_close(st.cpu(), st_ref, rtol=1e-3, atol=1e-6)
 
 
@@ -448,7 +448,7 @@ def test_delta_prefill_gated_conv_equals_conv_then_prefill(gpu, seq_len):
 
 
 def test_config4_delta_64_steps(gpu):
-    """16 heads x 128, S ~N(0,0.1), conv width 4 on q/k/v,
+    """Benchmark config 4: 16 heads x 128, S ~N(0,0.1), conv width 4 on q/k/v,
     beta = sigmoid(N(0,1)), g = -softplus(N(0,1)) (A_log = 0, dt_bias = 0),
     64 sequential decode tokens through the fused conv+delta+gated-norm kernel,
     against the oracle chain conv -> delta -> gated norm."""
@@ -483,7 +483,7 @@ def test_config4_delta_64_steps(gpu):
 
 
 def test_config4_delta_64_steps_production_chain(gpu):
-    """BASELINE config 4 through the kernels the model's decode step runs: the
+    """Benchmark config 4 through the kernels the model's decode step runs: the
     single-token conv update (``causal_conv1d_fused``, L = 1) then the
     256-wave delta step (``delta_recurrent_fused``, L = 1) and the packed gated
     norm, 64 sequential tokens. Each step's core output within the bf16
@@ -729,7 +729,7 @@ def test_quantize_weight_bit_exact(gpu, n, k):
 @pytest.mark.parametrize("m", [1, 2, 4, 7, 13, 16, 17])
 @pytest.mark.parametrize("n,k", [(12288, 2048), (2048, 6144), (1000, 2048)])
 def test_a8w8_linear_config2(gpu, m, n, k):
-    """int8 quantisation and int32 accumulators bit-exact,
+    """Benchmark config 2: int8 quantisation and int32 accumulators bit-exact,
     bf16 dequant output within rtol 1e-2 / atol 1e-3."""
     from ppu_amd import kernels as K
 
