@@ -320,12 +320,14 @@ def kernel_table(dev) -> dict:
     return out
 
 
-def gemm_sweep(dev) -> None:
+def gemm_sweep(dev, quick: bool = False) -> None:
     """The prefill GEMM shapes of the 2B decoder at M = 1024: the ROCm library
-    (F.linear bf16; torch._int_mm + the dequant kernel for int8) against the
-    hand-written matrix-core GEMMs for every tile plan, each graph-timed over
-    rotating weights (>= 512 MB, so the MALL does not serve them). Prints one
-    table row per (shape, implementation, plan) on stdout."""
+    (F.linear bf16, + silu_and_mul for the packed gate/up; torch._int_mm + the
+    dequant kernel for int8) against the hand-written matrix-core GEMM
+    (q35_gemm) for its default plan and the other tile plans, each
+    graph-timed over rotating weights (>= 512 MB, so the MALL does not serve
+    them). Prints one table row per (shape, implementation, plan) on stdout.
+    ``quick``: the default plans only."""
     import torch
     import torch.nn.functional as F
 
@@ -335,10 +337,14 @@ def gemm_sweep(dev) -> None:
     g = torch.Generator(device=dev).manual_seed(1)
     m = PROMPT_LEN
     stream = torch.cuda.current_stream().cuda_stream
-    shapes = [(8320, 2048, 18), (2048, 2048, 24), (5120, 2048, 6), (12288, 2048, 24), (2048, 6144, 24)]
+    # (N, K, count per prefill, packed SwiGLU)
+    shapes = [(8320, 2048, 18, False), (2048, 2048, 24, False), (5120, 2048, 6, False),
+              (12288, 2048, 24, True), (2048, 6144, 24, False)]
+    stage = {0: 128, 1: 128, 2: 128, 3: 128, 4: 64, 5: 128, 6: 128}
     print("# N x K (per prefill) | implementation | plan (tile, K splits) | us | TFLOP/s (TOP/s)")
-    for n, k, count in shapes:
+    for n, k, count, swiglu in shapes:
         flops = 2 * m * n * k
+
         nset = max(2, (512 << 20) // (n * k * 2) + 1)
         w = [(torch.randn(n, k, device=dev, generator=g) * 0.02).to(torch.bfloat16) for _ in range(nset)]
         x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
@@ -347,13 +353,19 @@ def gemm_sweep(dev) -> None:
             print(f"{n} x {k} ({count}) | {impl} | {plan} | {us:.2f} | {flops / us / 1e6:.0f}",
                   flush=True)
 
+        if swiglu:
+            row("library bf16 (F.linear) + silu_and_mul", "-",
+                graph_time_us(lambda i: K.silu_and_mul(F.linear(x, w[i % nset])), nset, 5))
         row("library bf16 (F.linear)", "-", graph_time_us(lambda i: F.linear(x, w[i % nset]), nset, 5))
-        plans = [None, (0, 1), (1, 1), (2, 1), (3, 1), (1, 2), (1, 3)]
+        plans = [None] if quick else [None, (0, 1), (5, 1), (1, 1), (6, 1), (2, 1), (3, 1), (1, 2), (6, 2)]
         for plan in plans:
-            if plan and (k // 64) % (2 * plan[1]):
+            if plan and ((2 * k // stage[plan[0]]) % plan[1] or (swiglu and plan[1] > 1)):
                 continue
+            if swiglu and (plan is None or plan[0] not in (5, 6)):
+                us = graph_time_us(lambda i: K.gemm_bf16(x, w[i % nset], swiglu=True, plan=plan), nset, 5)
+                row("own bf16 + SwiGLU epilogue (q35_gemm kind 1)", plan or "default plan", us)
             us = graph_time_us(lambda i: K.gemm_bf16(x, w[i % nset], plan=plan), nset, 5)
-            row("own bf16 (q35_gemm_bf16)", plan or "default plan", us)
+            row("own bf16 (q35_gemm kind 0)", plan or "default plan", us)
         del w
         nset8 = max(2, (512 << 20) // (n * k) + 1)
         wq = [torch.randint(-127, 128, (n, k), device=dev, dtype=torch.int8, generator=g)
@@ -361,18 +373,27 @@ def gemm_sweep(dev) -> None:
         sw = torch.rand(n, device=dev, generator=g) * 1e-3
         xq, sx = K.quantize_act_i8(x)
         y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        acc = torch.empty(m, n, device=dev, dtype=torch.int32)
 
         def lib_i8(i):
-            acc = torch._int_mm(xq, wq[i % nset8].t())
-            _lib.call("q35_dequant_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(),
+            a = torch._int_mm(xq, wq[i % nset8].t())
+            _lib.call("q35_dequant_i32", a.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(),
                       m, n, stream)
 
+        row("library int8 (_int_mm)", "-", graph_time_us(lambda i: torch._int_mm(xq, wq[i % nset8].t()),
+                                                        nset8, 5))
         row("library int8 (_int_mm) + dequant", "-", graph_time_us(lib_i8, nset8, 5))
-        for plan in [None, (0, 1), (1, 1), (2, 1), (1, 2)]:
-            if plan and (k // 128) % (2 * plan[1]):
+        plans = [None] if quick else [None, (0, 1), (5, 1), (1, 1), (6, 1), (2, 1), (3, 1), (1, 2), (6, 2)]
+        for plan in plans:
+            if plan and (k // stage[plan[0]]) % plan[1]:
+                continue
+            us = graph_time_us(lambda i: K.gemm_into(xq, wq[i % nset8], acc, K.GEMM_I32, plan=plan),
+                               nset8, 5)
+            row("own int8 -> int32 (q35_gemm kind 2)", plan or "default plan", us)
+            if plan is not None and plan[0] in (5, 6):
                 continue
             us = graph_time_us(lambda i: K.gemm_a8w8(xq, sx, wq[i % nset8], sw, plan=plan), nset8, 5)
-            row("own int8 + fused dequant (q35_gemm_a8w8)", plan or "default plan", us)
+            row("own int8 + fused dequant (q35_gemm kind 3)", plan or "default plan", us)
         del wq
         torch.cuda.empty_cache()
 
@@ -774,6 +795,7 @@ def main() -> None:
                     help="per-kernel anatomy of a rocprofv3 kernel trace of this bench, then exit")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="prefill GEMM shapes: ROCm library vs the hand-written GEMMs, then exit")
+    ap.add_argument("--quick", action="store_true", help="--gemm-sweep: default plans only")
     ap.add_argument("--counter-probe", action="store_true",
                     help="only run the short workload profiled with rocprofv3 --pmc, then exit")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -797,7 +819,7 @@ def main() -> None:
         counter_probe(torch.device("cuda:0"))
         return
     if args.gemm_sweep:
-        gemm_sweep(torch.device("cuda:0"))
+        gemm_sweep(torch.device("cuda:0"), quick=args.quick)
         return
     if args.vision_only:
         print(json.dumps({"vision_tower": vision_tower_timing(torch.device("cuda:0"))}), flush=True)

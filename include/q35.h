@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; q35_abi_version() must return it. */
-#define Q35_ABI_VERSION 2
+#define Q35_ABI_VERSION 3
 int q35_abi_version(void);
 
 /* Zero n device buffers in one launch: ptrs[i] (16-byte aligned) holds
@@ -326,52 +326,36 @@ int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void
 int q35_dequant_swiglu_i32(const void* acc, const void* s_x, const void* s_w, void* y, int M, int N,
                            void* stream);
 
-/* Workspace bytes q35_gemm_bf16 (swiglu 0) / q35_gemm_swiglu_bf16 (swiglu 1)
- * need for an [M, K] x [N, K]^T product: 0 unless the library's plan for the
- * shape splits K (then fp32 partial tiles). */
-long long q35_gemm_workspace(int M, int N, int K, int swiglu);
-/* Prefill GEMM on the matrix cores: C[M,N] = bf16(A[M,K] . B[N,K]^T), bf16 in,
- * fp32 accumulate. K a multiple of 128, A and B 16-byte aligned, M*K and N*K
- * below 2^32; workspace of q35_gemm_workspace bytes (may be null when that is
- * 0). Narrow outputs run with K split over 2 workgroups per tile, the last
- * one to finish a tile summing the partials in split order (deterministic);
- * its arrival counters live in the library and reset themselves, so split-K
- * GEMMs running at the same time on one GPU (two streams) must not overlap.
- * Replaces F.linear at the prefill sites integration.py:183,245,298. */
-int q35_gemm_bf16(const void* A, const void* B, void* C, int M, int N, int K, void* workspace,
-                  long long workspace_bytes, void* stream);
-/* Packed gate/up projection with SwiGLU in the epilogue: B = [gate; up] is
- * [2N, K]; C[M,N] = bf16(bf16(silu(bf16(A.Bg^T))) * bf16(A.Bu^T)). Replaces
- * F.linear on the packed weight followed by silu_and_mul (integration.py:183-185,
- * kernels.py:158-180) for prefill. Same constraints as q35_gemm_bf16. */
-int q35_gemm_swiglu_bf16(const void* A, const void* B, void* C, int M, int N, int K,
-                         void* workspace, long long workspace_bytes, void* stream);
-/* The same GEMMs with an explicit plan, for measurement and tests: tile 0-3
- * (256x192, 128x128, 256x128, 128x256 outputs per workgroup), K split over
- * `splits` workgroups (K / 64 divisible by 2 * splits; tile 0 unsplit), swiglu
- * 0/1; workspace of q35_gemm_plan_workspace bytes. */
-int q35_gemm_bf16_plan(const void* A, const void* B, void* C, int M, int N, int K, int tile,
-                       int splits, int swiglu, void* workspace, long long workspace_bytes,
-                       void* stream);
-long long q35_gemm_plan_workspace(int M, int N, int tile, int splits, int swiglu);
-
-/* A8W8 prefill GEMM on the int8 matrix cores (v_mfma_i32_32x32x32_i8, exact
- * int32 accumulators) with the dequant in the epilogue: Aq [M,K] int8 with
- * per-token scales s_x [M] fp32, Bq [N,K] int8 with per-channel scales s_w [N]
- * fp32; C[M,N] = bf16(float(acc) * s_x[m] * s_w[n]), the values of
- * q35_dequant_i32 on the exact accumulators. swiglu 1: Bq = [gate; up] is
- * [2N, K] with s_w [2N]; gate and up are dequantised to bf16 and
- * C = bf16(bf16(silu(g)) * u), the values of q35_dequant_swiglu_i32. K a
- * multiple of 256, Aq/Bq 16-byte aligned. tile < 0 lets the library plan
- * (tile and splits are then ignored); otherwise tile 0-3 and splits as for
- * q35_gemm_bf16_plan with K / 128 divisible by 2 * splits. Workspace of
- * q35_gemm_a8w8_workspace bytes for the same (M, N, K, swiglu, tile, splits).
- * Replaces the int8 GEMM + dequant of explore_runtime_quantization.py:173-180
- * (vLLM's cutlass_scaled_mm) at the prefill sites of PPUA8W8Linear. */
-int q35_gemm_a8w8(const void* Aq, const void* s_x, const void* Bq, const void* s_w, void* C, int M,
-                  int N, int K, int swiglu, int tile, int splits, void* workspace,
-                  long long workspace_bytes, void* stream);
-long long q35_gemm_a8w8_workspace(int M, int N, int K, int swiglu, int tile, int splits);
+/* Prefill GEMM on the matrix cores, C = A[M,K] . B[N,K]^T with both operands
+ * K-contiguous, of one kind:
+ *   0  bf16 A, B -> C bf16 = bf16(fp32 sum)                        F.linear at the prefill
+ *      sites integration.py:183,245,272,298,359
+ *   1  bf16, B = [gate; up] [2N, K] -> C[M,N] = bf16(bf16(silu(bf16 g)) * bf16 u)
+ *      F.linear on the packed gate/up weight + silu_and_mul, integration.py:183-185
+ *      and kernels.py:158-180
+ *   2  int8 A, B -> C int32 = exact sum                            the int8 GEMM of
+ *      explore_runtime_quantization.py:173-180 (accumulators for the fused
+ *      dequant kernels below)
+ *   3  int8 -> C bf16 = bf16(float(acc) * s_x[m] * s_w[n])         the same with its
+ *      dequant (q35_dequant_i32's values)
+ *   4  int8, B = [gate; up] -> SwiGLU of the dequantised bf16 gate and up
+ *      (q35_dequant_swiglu_i32's values)
+ * s_x [M] and s_w [N] (kind 4: [2N]) fp32 are used by kinds 3 and 4 only.
+ * K * (element bytes) must be a multiple of the tile's stage width (64 bytes
+ * for tiles 0, 2, 3; 128 for tile 1); A and B 16-byte aligned; each operand
+ * below 2^32 bytes. tile < 0 picks the library's plan (tile and K splits by
+ * output shape); otherwise tile 0-3 (256x192, 128x128, 256x128, 128x192
+ * outputs per workgroup; SwiGLU kinds: half as many output columns) with
+ * `splits` workgroups per tile along K (1-8, dividing the stage count; tiles
+ * 1-3 and kinds 0, 2, 3 only). A plan that splits K needs a workspace of
+ * q35_gemm_workspace bytes (arrival counters + partial tiles), zero-filled
+ * before its first use; each launch leaves the counters at zero again (after
+ * a launch that failed part way, zero it again). Two launches that overlap in
+ * time must not share a workspace. No allocation, no host synchronisation. */
+long long q35_gemm_workspace(int M, int N, int K, int kind, int tile, int splits);
+int q35_gemm(const void* A, const void* B, void* C, int M, int N, int K, int kind, const void* s_x,
+             const void* s_w, int tile, int splits, void* workspace, long long workspace_bytes,
+             void* stream);
 
 /* A8W8 prefill between the int8 GEMMs of a layer: residual add of the
  * dequantised accumulators of the previous GEMM (q35_dequant_i32's values) +

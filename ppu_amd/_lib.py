@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libq35.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -82,13 +82,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_gemv_a8w8": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "q35_dequant_i32": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "q35_dequant_swiglu_i32": (_I, [_P, _P, _P, _P, _I, _I, _P]),
-    "q35_gemm_workspace": (_L, [_I, _I, _I, _I]),
-    "q35_gemm_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P, _L, _P]),
-    "q35_gemm_swiglu_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P, _L, _P]),
-    "q35_gemm_bf16_plan": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
-    "q35_gemm_plan_workspace": (_L, [_I, _I, _I, _I, _I]),
-    "q35_gemm_a8w8": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
-    "q35_gemm_a8w8_workspace": (_L, [_I, _I, _I, _I, _I, _I]),
+    "q35_gemm_workspace": (_L, [_I, _I, _I, _I, _I, _I]),
+    "q35_gemm": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _P, _L, _P]),
     "q35_residual_rmsnorm_dequant_quant": (
         _I, [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P]),
     "q35_dequant_swiglu_quant": (_I, [_P, _P, _P, _P, _P, _I, _I, _P]),

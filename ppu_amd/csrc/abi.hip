@@ -65,7 +65,7 @@ int device_cus() {
 
 extern "C" {
 
-int q35_abi_version(void) { return 2; }
+int q35_abi_version(void) { return 3; }
 
 // Zero n device buffers (host arrays of pointers and byte counts; each
 // pointer 16-byte aligned). Replaces the per-tensor zero_() calls of

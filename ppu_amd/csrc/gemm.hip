@@ -1,521 +1,717 @@
-// Prefill GEMMs on the gfx950 matrix cores: C[M, N] = A[M, K] . B[N, K]^T,
-// bf16 in, fp32 accumulate (v_mfma_f32_32x32x16_bf16), bf16 out, with the
-// SwiGLU of the packed gate/up projection fused into the epilogue; and the
-// same kernel on int8 operands (v_mfma_i32_32x32x32_i8, exact int32
-// accumulators) with the A8W8 dequant bf16(float(acc) * s_x[m] * s_w[n])
-// in the epilogue.
+// Prefill GEMMs on the gfx950 matrix cores: C[M, N] = A[M, K] . B[N, K]^T
+// with both operands K-contiguous (activations x weights^T, as F.linear).
 //
-//   STORE  : C[m, n] = bf16(acc)                                 [F.linear, integration.py:183,245,298]
-//   SWIGLU : B = [gate; up] (2N rows); C[m, n] = bf16(bf16(silu(bf16 g)) * bf16 u)
-//            with g, u the accumulators of rows n and N + n     [integration.py:183-185 + kernels.py:158-180]
+//   kind 0  bf16 A, B -> bf16 C = bf16(acc)                        [F.linear, integration.py:183,245,298]
+//   kind 1  bf16, B = [gate; up] (2N rows) -> C[m, n] = bf16(bf16(silu(bf16 g)) * bf16 u)
+//                                                                   [integration.py:183-185 + kernels.py:158-180]
+//   kind 2  int8 A, B -> int32 C = acc (exact)                     [the int8 GEMM of explore_runtime_quantization.py:173-180]
+//   kind 3  int8 -> bf16 C = bf16(float(acc) * s_x[m] * s_w[n])    [the same with its dequant]
+//   kind 4  int8, B = [gate; up] -> SwiGLU of the dequantised gate and up (kind 1's rounding points)
 //
-// Tiling: a workgroup of 4 waves owns a TM x TN tile of (M rows, B rows);
-// the waves are stacked along M and each holds FM x FN accumulator tiles of
-// 32 x 32 (v_mfma_f32_32x32x16_bf16; SWIGLU: the first FN/2 column tiles are
-// gate rows, the last FN/2 the up rows of the same outputs, so the epilogue
-// pairs them in registers). K runs in stages of 64: each stage of A and B is
-// fetched with 16-byte loads (8 consecutive lanes read one 128-byte row
-// segment) two stages ahead into registers, written to one of two LDS
-// buffers and read back as MFMA fragments (lane l: row l%32, 8 consecutive
-// k at 8*(l/32) of a 16-k step). LDS rows are 128 bytes and the banks span
-// 256 bytes (two rows); 16-byte chunk c of row r is stored at chunk
-// c ^ ((r >> 1) & 7), so the 16 lanes of one 128-bit access phase hit 16
-// different 16-byte bank groups both when reading fragments (16 consecutive
-// rows, same logical chunk) and when storing a stage (two rows, 8 chunks
-// each). (Swizzling by r & 7 alone left rows r and r + 8 on the same banks:
-// measured as SQ_LDS_BANK_CONFLICT.) One barrier per stage.
-// (The 32x32 form keeps each accumulator in place; with 16x16 tiles this
-// compiler rotated the accumulators through copies every iteration.)
+// bf16 runs on v_mfma_f32_32x32x16_bf16 (fp32 accumulators), int8 on
+// v_mfma_i32_32x32x32_i8 (exact int32). Both take 16 bytes per lane and
+// operand: lane l holds row l % 32 of its 32-row block and bytes
+// [16 (l / 32), +16) of a 32-byte k window, so one LDS layout and one
+// fragment read serve both.
 //
-// Status (MI355X, M = 1024, the 2B prefill shapes, graph-timed): correct,
-// but slower than the ROCm library GEMMs, so the prefill path keeps the
-// library. bf16: N x K = 8320x2048 57.8 us vs 48.9, 2048x2048 21.4 vs 18.1,
-// 12288x2048 60 vs 50.6, 2048x6144 41.9 vs 43.3 (split K, the one win);
-// SwiGLU 61 vs ~57 for library GEMM + silu_mul. int8 (vs torch._int_mm +
-// dequant kernel): 46.1 vs 41.3, 21.2 vs 12.0, 30.4 vs 22.6, 52.3 vs 48.1,
-// 36.0 vs 28.3. Measured split of the bf16 12288x2048 time: 34 us with the
-// MFMAs alone, +10 us for the fragment reads from LDS, +17 us for the global
-// fetches (two stages ahead is not enough latency cover at one workgroup per
-// CU; a third register set does not fit beside 192 accumulator registers);
-// the int8 form halves the MFMA share and keeps the rest. Staging the
-// stages straight into LDS (global_load_lds_dwordx4, a 3-4 deep ring) was
-// no faster and was dropped.
+// Workgroup: 4 waves as 2 x 2 over a TM x TN tile; each wave holds FM x FN
+// accumulator blocks of 32 x 32 (tile 0: 256 x 192, the wave 128 x 96, 12
+// blocks = 192 accumulator registers).
 //
-// Tile order: tiles that share B rows (the weights, read once from HBM) run
-// on one XCD: with T tiles and T % 8 == 0, workgroup b (dispatched to XCD
-// b % 8) takes tile (b % 8) * T/8 + b / 8, M-tile index fastest.
+// Operand staging. K advances in stages of RB bytes per row. A stage of the
+// A and B tiles goes straight from memory into LDS with
+// global_load_lds_dwordx4 (each wave instruction writes 1 KiB of LDS: 1024 /
+// RB rows, 16 bytes per lane) into a ring of NS stage buffers, so no register
+// holds a fetched stage and NS - 1 stages are in flight. The loads are issued
+// from inline asm, so the only waits on them are the ring's explicit vmcnt
+// waits. Each lane's global source is chosen so that the LDS image is
+// swizzled: 16-byte chunk c of tile row r sits at slot c ^ swz(r), which
+// makes the fragment reads (16 consecutive rows, one logical chunk, per 16
+// lanes) hit 16 distinct bank groups of the 256-byte LDS bank window.
+// Measured on the 2B prefill shapes (timing copies with parts switched off):
+//  * the operand stream is the bound; stages of 128-byte rows (every request
+//    a whole L2 line) move twice the bytes per second of 64-byte rows, whose
+//    requests each pull a 128-byte line for 64 useful bytes;
+//  * workgroups that share operand rows (the M tiles of one weight tile, the
+//    N tiles of one activation tile) run on one XCD; when they walk K in
+//    lockstep every one of them waits for the same L2 misses, so each
+//    workgroup starts its K walk at its own stage offset (K rotation) and the
+//    later readers of a line find it in L2 (DMA-only time -15 to -30 %);
+//  * a wave issues in order, so a run of fragment reads ahead of the MFMAs
+//    stalls them behind the LDS queue; one read (and one DMA) per MFMA, in
+//    the order the next k step consumes them, hides the reads completely.
+//
+// Ring schedule (one barrier per stage): in stage kt the fragments of k step
+// t + 1 are read under the MFMAs of step t, and the buffer of stage kt - 1
+// (free since the last barrier) is refilled with stage kt + NS - 1 under the
+// MFMAs of the first steps; in the last step, after half of its MFMAs, each
+// wave waits for its part of stage kt + 1 (vmcnt) and all waves meet at
+// s_barrier, then the first fragments of stage kt + 1 are read under the
+// second half.
+//
+// Split K (for outputs with fewer tiles than CUs): `splits` workgroups per
+// tile each take kps stages. Each stores its partial tile (fp32 / int32 bit
+// patterns, in accumulator-register order so every wave store is 512
+// contiguous bytes) with agent-scope stores, every thread waits until its
+// stores have completed (s_waitcnt vmcnt(0)), and one thread counts the
+// workgroup's arrival on the tile's counter (agent-scope atomic add). The
+// workgroup that arrives last resets the counter and sums the partials in
+// split order, its own from registers, so the result does not depend on
+// arrival order; it reads them with agent-scope loads issued only after it
+// has seen the count. Agent-scope stores and loads (sc1) are coherent across
+// the XCDs' L2s by themselves; completed stores before the count and loads
+// after it give the ordering. (Agent-scope release / acquire fences would
+// add an L2 write-back per arriving workgroup and an L2 invalidate per last
+// one, which discards the operands the XCD's other workgroups are streaming:
+// measured 2-3x slower on the split plans.) The counters (a fixed region of
+// kMaxSplitTiles at the start of the workspace) and the partials live in the
+// caller's workspace, which must be zero-filled once before its first use;
+// every launch leaves the counters at zero again (a launch aborted part way
+// can leave them non-zero: zero the workspace again after such an error).
+// Two launches that overlap in time must not share a workspace.
+//
+// Tile order: units (tile, split) are grouped so that the units sharing B
+// rows and a K range (consecutive M tiles) run on one XCD and read the
+// weights into one L2: with U units and U % 8 == 0, workgroup b (XCD b % 8)
+// takes unit (b % 8) * U / 8 + b / 8, M tile fastest.
 #include "q35_common.hpp"
 
 namespace {
 
-enum { GEMM_STORE = 0, GEMM_SWIGLU = 1 };
-constexpr int kBK = 64;        // k per stage: 8 chunks of 16 bytes per row
-constexpr int kRowB = 128;     // LDS bytes per tile row and stage
+enum { KIND_BF16 = 0, KIND_SWIGLU = 1, KIND_I32 = 2, KIND_DEQ = 3, KIND_DEQ_SWIGLU = 4 };
+constexpr int kNumKinds = 5;
+constexpr int kMaxSplitTiles = 8192;  // counters at the start of a split-K workspace
+constexpr int kCounterBytes = kMaxSplitTiles * 4;
 
 struct GemmArgs {
-  const uint16_t* A;  // [M, K]
-  const uint16_t* B;  // [N, K], SWIGLU [2N, K]
-  uint16_t* C;        // [M, N]
-  int M, N, K;
-  // split-K: `splits` workgroups per tile each take `kps` stages of K; their
-  // fp32 partial tiles go to `ws` and the last one to finish a tile sums them.
-  float* ws;
-  int splits, kps;
-  // A8W8: A and B are int8, C = bf16(float(acc) * s_x[m] * s_w[n]).
-  const float* s_x;
-  const float* s_w;
+  const uint8_t* A;  // [M, K]
+  const uint8_t* B;  // [N, K] (SwiGLU kinds: [2N, K])
+  void* C;           // [M, N] bf16 or int32
+  int M, N, K;       // K in elements
+  const float* s_x;  // int8 kinds 3, 4: per-row scales of A
+  const float* s_w;  // per-row scales of B
+  unsigned* cnt;     // split-K arrival counters, one per tile
+  uint8_t* part;     // split-K partial tiles
+  int splits, kps;   // splits per tile, stages per split
 };
 
-// Arrival counters of the split-K tiles (one per output tile, at most
-// kMaxSplitTiles), in the library's device memory: zero at load, and every
-// tile's last workgroup resets its counter, so each launch finds them zero.
-// Split-K launches that run at the same time on one GPU (two streams) would
-// share them: the prefill path issues its GEMMs on one stream.
-constexpr int kMaxSplitTiles = 8192;
-__device__ unsigned split_tile_count[kMaxSplitTiles];
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+Q35_DEV uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)(const lds_u8*)p; }
+
+// One wave instruction of the stage ring: lane i copies the 16 bytes at
+// sbase + voff to LDS bytes [lds + 16 i, +16) (the LDS base goes in m0).
+Q35_DEV void dma16(uint32_t lds, const uint8_t* sbase, uint32_t voff) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// and lgkmcnt at their "no wait" maxima). As a builtin the compiler's wait
+// pass sees it and keeps it; it does not know of the asm loads it waits for.
+template <int N>
+Q35_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// This wave's LDS reads complete (s_waitcnt lgkmcnt(0)).
+Q35_DEV void wait_lds() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14)); }
+// Workgroup barrier; the empty asm statements keep the compiler from moving
+// memory accesses across it (the builtin barrier alone does not order them).
+Q35_DEV void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// Keeps the compiler's scheduler from moving any instruction across it, so
+// the MFMA / read / DMA interleave below is issued as written.
+#define Q35_PIN() __builtin_amdgcn_sched_barrier(0)
 
 typedef float q35_f32x16 __attribute__((ext_vector_type(16)));
 typedef int q35_i32x16 __attribute__((ext_vector_type(16)));
 typedef int q35_i32x4 __attribute__((ext_vector_type(4)));
-Q35_DEV q35_f32x16 mfma32_bf16(const uint4 a, const uint4 b, q35_f32x16 c) {
+Q35_DEV q35_f32x16 mfma32(const q35_u32x4 a, const q35_u32x4 b, q35_f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(q35_bf16x8, a),
                                                  __builtin_bit_cast(q35_bf16x8, b), c, 0, 0, 0);
 }
-// int8 x int8 -> exact int32 (A8W8): 16 bytes per lane and operand, 32 k per
-// instruction, the same lane layout in bytes as the bf16 form.
-Q35_DEV q35_i32x16 mfma32_bf16(const uint4 a, const uint4 b, q35_i32x16 c) {
+Q35_DEV q35_i32x16 mfma32(const q35_u32x4 a, const q35_u32x4 b, q35_i32x16 c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(q35_i32x4, a),
                                                __builtin_bit_cast(q35_i32x4, b), c, 0, 0, 0);
 }
-template <bool I8> struct GemmAcc { using T = q35_f32x16; };
-template <> struct GemmAcc<true> { using T = q35_i32x16; };
+template <bool I8> struct GemmAcc { using T = q35_f32x16; using E = float; };
+template <> struct GemmAcc<true> { using T = q35_i32x16; using E = int; };
 Q35_DEV uint32_t acc_bits(float v) { return __float_as_uint(v); }
 Q35_DEV uint32_t acc_bits(int v) { return (uint32_t)v; }
 Q35_DEV float acc_from(uint32_t b, float) { return __uint_as_float(b); }
 Q35_DEV int acc_from(uint32_t b, int) { return (int)b; }
 
-// Instruction groups of one GEMM stage in issue order (LLVM sched_group_barrier
-// masks: 0x8 MFMA, 0x100 LDS read, 0x200 LDS write, 0x20 global read).
-#define Q35_SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
-template <int FM, int FN>
-Q35_DEV void gemm_stage_schedule() {
-  constexpr int NF = FM + FN, NMF = FM * FN;  // fragment reads and MFMAs per 16-k step
-  Q35_SGB(0x100, NF);                         // step 0 fragments
-  _Pragma("unroll") for (int s = 0; s < 3; ++s) {
-    _Pragma("unroll") for (int i = 0; i < NF; ++i) { Q35_SGB(0x8, 1); Q35_SGB(0x100, 1); }
-    if (s == 0) Q35_SGB(0x8, NMF - NF);
-    if (s == 1) {
-      _Pragma("unroll") for (int i = 0; i < NMF - NF; ++i) Q35_SGB(0x8, 1), Q35_SGB(0x200, 4);
-    }
-    if (s == 2) {
-      _Pragma("unroll") for (int i = 0; i < NMF - NF; ++i) Q35_SGB(0x8, 1), Q35_SGB(0x20, 4);
-    }
-  }
-  Q35_SGB(0x8, NMF);
+constexpr bool kind_i8(int kind) { return kind >= KIND_I32; }
+constexpr bool kind_swiglu(int kind) { return kind == KIND_SWIGLU || kind == KIND_DEQ_SWIGLU; }
+
+template <bool V> struct BoolTag { static constexpr bool value = V; };
+
+// Slot of 16-byte chunk c of tile row r in the swizzled LDS image.
+template <int RB>
+Q35_DEV int swz(int r) {
+  return RB == 64 ? (r >> 2) & 3 : (r >> 1) & 7;
 }
 
-// The end of every GEMM workgroup: (split-K) the partial-tile exchange and
-// sum, then the bf16 (or SwiGLU) store of the tile.
-template <int WM, int FM, int FN, int EPI, bool SPLIT, bool I8 = false>
-Q35_DEV void gemm_finish(const GemmArgs& a, typename GemmAcc<I8>::T (&acc)[FM][FN], int T, int tile,
-                         int ks, int m0, int n0) {
+template <int WM, int WN, int FM, int FN, int RB, int NS, int KIND, bool SPLIT, bool STAGED>
+__global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
+  constexpr bool I8 = kind_i8(KIND);
+  constexpr bool SWIGLU = kind_swiglu(KIND);
+  constexpr int ES = I8 ? 1 : 2;
+  constexpr int TM = WM * FM * 32, TN = WN * FN * 32;
+  constexpr int NC = SWIGLU ? TN / 2 : TN;  // output columns per tile
+  constexpr int RPG = 1024 / RB;             // tile rows per 1 KiB DMA group
+  constexpr int CPR = RB / 16;               // 16-byte chunks per row and stage
+  constexpr int GA = TM / RPG, GB = TN / RPG;
+  constexpr int LPW = (GA + GB) / 4;         // DMA instructions per wave and stage
+  constexpr int STAGE = (TM + TN) * RB;      // LDS bytes per stage
+  constexpr int T = RB / 32;                 // MFMA k steps per stage
+  constexpr int NMF = FM * FN;               // MFMAs per k step
+  constexpr int NR = FM + FN;                // fragment reads per k step
+  constexpr int H = NMF / 2;                 // MFMAs of the last step before the barrier
+  static_assert(WM * WN == 4, "4 waves");
+  static_assert(GA % 4 == 0 && GB % 4 == 0, "every wave issues the same DMA groups of A and B");
+  static_assert(T % 2 == 0, "fragment register sets alternate between k steps");
+  static_assert(!SWIGLU || WN == 2, "SwiGLU pairs the gate waves with the up waves");
+  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "stage ring fits the LDS");
+  static_assert(LPW <= (T - 1) * NMF, "the refill fits the MFMA slots of the first steps");
+  static_assert(STAGED || KIND == KIND_BF16 || KIND == KIND_I32, "direct stores: bf16 and int32 kinds");
+  using AccT = typename GemmAcc<I8>::T;
+  using EltT = typename GemmAcc<I8>::E;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wm = (tid >> 6) % WM, wn = (tid >> 6) / WM;
-  const int l32 = lane & 31, kh = lane >> 5;
-  if (SPLIT) {
-    // Partial tiles are stored in accumulator-register order, so the summing
-    // workgroup reads back exactly the elements of its own registers. Stores and loads are agent-scope (they bypass the non-
-    // coherent per-XCD L2), the stores are complete (vmcnt 0) before the
-    // workgroup's arrival is counted, and the partials are summed in split
-    // order whichever workgroup arrives last, so the result is deterministic.
-    constexpr int NE = FM * FN * 16;
-    constexpr int NP = NE / 2;  // 8-byte pairs per thread
-    // pair p of thread tid sits at p * 256 + tid: every store and load
-    // instruction of a wave covers 512 contiguous bytes
-    uint64_t* mine = reinterpret_cast<uint64_t*>(a.ws) + ((size_t)ks * T + tile) * NP * 256 + tid;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-          const uint64_t v = (uint64_t)acc_bits(acc[i][j][e]) |
-                             ((uint64_t)acc_bits(acc[i][j][e + 1]) << 32);
-          __hip_atomic_store(mine + (size_t)(((i * FN + j) * 16 + e) / 2) * 256, v,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __shared__ unsigned arrived;
-    lds_barrier();
-    if (tid == 0)
-      arrived = __hip_atomic_fetch_add(&split_tile_count[tile], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-    lds_barrier();
-    if (arrived != (unsigned)a.splits - 1) return;  // not the last: done
-    // The last workgroup reads every partial, its own included, in split
-    // order, straight into the accumulators.
-    for (int sp = 0; sp < a.splits; ++sp) {
-      const uint64_t* src = reinterpret_cast<const uint64_t*>(a.ws) + ((size_t)sp * T + tile) * NP * 256 + tid;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int e = 0; e < 16; e += 2) {
-            const uint64_t w = __hip_atomic_load(
-                const_cast<uint64_t*>(src + (size_t)(((i * FN + j) * 16 + e) / 2) * 256),
-                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const auto lo = acc_from((uint32_t)w, acc[i][j][e]);
-            const auto hi = acc_from((uint32_t)(w >> 32), acc[i][j][e]);
-            acc[i][j][e] = sp == 0 ? lo : acc[i][j][e] + lo;
-            acc[i][j][e + 1] = sp == 0 ? hi : acc[i][j][e + 1] + hi;
-          }
-    }
-    if (tid == 0)
-      __hip_atomic_store(&split_tile_count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  const int w = tid >> 6;
+  const int wm = w % WM, wn = w / WM;
 
-  // Epilogue: element r of a 32x32 tile sits at row 8*(r/4) + 4*(lane/32) +
-  // r%4, column lane%32.
-  const int row0 = m0 + wm * FM * 32 + 4 * kh;
+  // ---- unit of this workgroup: (tile, split)
+  const int mt = (a.M + TM - 1) / TM;
+  const int nt = (a.N + NC - 1) / NC;
+  const int ntiles = mt * nt;
+  const int S = SPLIT ? a.splits : 1;
+  const int U = ntiles * S;
+  int u = (int)blockIdx.x;
+  if ((U & 7) == 0) u = (u & 7) * (U >> 3) + (u >> 3);
+  const int tm = u % mt;
+  const int rest = u / mt;
+  const int ks = SPLIT ? rest % S : 0;
+  const int tn = SPLIT ? rest / S : rest;
+  const int tile = tn * mt + tm;
+  const int m0 = tm * TM, n0 = tn * NC;
+  const int nk = a.kps;  // stages of this workgroup
+  // K rotation: the workgroups sharing rows start at different stages
+  const int krot = ((tm % 4) * nk / 4 + (tn & 7) * nk / 32) % nk;
+  const uint32_t rowb = (uint32_t)a.K * ES;
+  // dequant kinds: the tile's row scales s_x[m0 ..] and column scales s_w[..]
+  // (SwiGLU: gate then up columns), loaded now and published through LDS in
+  // the epilogue (NSC <= 512: two per thread)
+  constexpr bool DEQ = KIND == KIND_DEQ || KIND == KIND_DEQ_SWIGLU;
+  constexpr int NSC = DEQ ? TM + (SWIGLU ? 2 * NC : NC) : 0;
+  static_assert(NSC <= 512, "two scales per thread");
+  float scl[2] = {0.f, 0.f};
+  if constexpr (DEQ) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
-      if (row >= a.M) continue;
-      uint16_t* crow = a.C + (size_t)row * a.N;
-      const float sx = I8 ? a.s_x[row] : 1.f;
-      if (EPI == GEMM_SWIGLU) {
-#pragma unroll
-        for (int j = 0; j < FN / 2; ++j) {
-          const int col = n0 + wn * (FN / 2) * 32 + 32 * j + l32;
-          float g, u;
-          if (I8) {  // dequantise gate and up to bf16 first, as the separate kernels do
-            const int cc = min(col, a.N - 1);
-            g = round_bf((float)acc[i][j][r] * sx * a.s_w[cc]);
-            u = round_bf((float)acc[i][j + FN / 2][r] * sx * a.s_w[a.N + cc]);
-          } else {
-            g = round_bf(acc[i][j][r]);
-            u = round_bf(acc[i][j + FN / 2][r]);
-          }
-          if (col < a.N) crow[col] = (uint16_t)f2bf(round_bf(silu_fast(g)) * u);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = n0 + wn * FN * 32 + 32 * j + l32;
-          const float v = I8 ? (float)acc[i][j][r] * sx * a.s_w[min(col, a.N - 1)] : (float)acc[i][j][r];
-          if (col < a.N) crow[col] = (uint16_t)f2bf(v);
-        }
+    for (int q = 0; q < 2; ++q) {
+      const int x = tid + 256 * q;
+      if (x < TM) {
+        scl[q] = a.s_x[min(m0 + x, a.M - 1)];
+      } else if (x < NSC) {
+        const int y = x - TM;
+        scl[q] = y < NC ? a.s_w[min(n0 + y, a.N - 1)] : a.s_w[a.N + min(n0 + y - NC, a.N - 1)];
       }
     }
   }
-}
 
-template <int WM, int FM, int FN, int EPI, bool SPLIT, bool I8>
-__global__ __launch_bounds__(256) void gemm_tn(const GemmArgs a) {
-  constexpr int ES = I8 ? 1 : 2;  // bytes per element; a stage is 128 bytes of every row
-  static_assert(EPI != GEMM_SWIGLU || FN % 2 == 0, "SwiGLU pairs gate and up tiles");
-  static_assert(WM == 1 || WM == 2 || WM == 4, "waves along M");
-  constexpr int WN = 4 / WM;
-  constexpr int TM = WM * FM * 32, TN = WN * FN * 32;
-  constexpr int LA = TM / 32, LB = TN / 32;        // 16-byte chunks per thread and stage
-  constexpr int SA = TM * kRowB, SB = TN * kRowB;  // stage bytes of A and B
-  constexpr int NC = EPI == GEMM_SWIGLU ? TN / 2 : TN;  // output columns per tile
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (SA + SB)];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wm = (tid >> 6) % WM, wn = (tid >> 6) / WM;
-
-  // Tile of this workgroup.
-  const int mtiles = (a.M + TM - 1) / TM;
-  const int ntiles = (a.N + NC - 1) / NC;
-  const int T = mtiles * ntiles;
-  // split s of every tile is the s-th run of T workgroups
-  const int ks = SPLIT ? (int)blockIdx.x / T : 0;
-  int t = SPLIT ? (int)blockIdx.x - ks * T : (int)blockIdx.x;
-  const int tile = t;
-  if (T % 8 == 0) t = (t & 7) * (T >> 3) + (t >> 3);
-  const int m0 = (t % mtiles) * TM;
-  const int n0 = (t / mtiles) * NC;
-  const int K = a.K;
-  const int kbeg = SPLIT ? ks * a.kps : 0;
-  const int nk = SPLIT ? kbeg + a.kps : K * ES / kRowB;  // one past this workgroup's last stage
-
-  // Global chunk sources: thread row r0 + 32i, chunk c (rows past the end
-  // repeat the last row and are never stored).
-  const int r0 = tid >> 3, c = tid & 7;
-  const int st_off = r0 * kRowB + 16 * (c ^ ((r0 >> 1) & 7));
-  uint32_t offA[LA], offB[LB];
+  // ---- DMA sources: wave w issues groups g = w + 4 i (A groups first)
+  uint32_t voff[LPW];
 #pragma unroll
-  for (int i = 0; i < LA; ++i) offA[i] = (uint32_t)min(m0 + r0 + 32 * i, a.M - 1) * (uint32_t)(K * ES) + 16 * c;
-#pragma unroll
-  for (int i = 0; i < LB; ++i) {
-    const int row = r0 + 32 * i;
-    int brow;
-    if (EPI == GEMM_SWIGLU)
-      brow = row < TN / 2 ? min(n0 + row, a.N - 1) : a.N + min(n0 + row - TN / 2, a.N - 1);
-    else
-      brow = min(n0 + row, a.N - 1);
-    offB[i] = (uint32_t)brow * (uint32_t)(K * ES) + 16 * c;
+  for (int i = 0; i < LPW; ++i) {
+    const int g = w + 4 * i;
+    const bool isA = i < GA / 4;
+    const int r = (isA ? g : g - GA) * RPG + lane / CPR;  // tile row
+    const int c = (lane % CPR) ^ swz<RB>(r);
+    int grow;
+    if (isA) {
+      grow = min(m0 + r, a.M - 1);
+    } else if (SWIGLU) {
+      grow = r < TN / 2 ? min(n0 + r, a.N - 1) : a.N + min(n0 + r - TN / 2, a.N - 1);
+    } else {
+      grow = min(n0 + r, a.N - 1);
+    }
+    voff[i] = (uint32_t)grow * rowb + (uint32_t)(ks * nk) * RB + 16u * c;
   }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_offset(lds) + (uint32_t)w * 1024u);
+  // instruction i of the DMA of stage kt into buffer buf
+  auto dma = [&](int kt, int buf, int i) {
+    int ksr = kt + krot;
+    if (ksr >= nk) ksr -= nk;
+    const uint8_t* src = (i < GA / 4 ? a.A : a.B) + (size_t)ksr * RB;
+    dma16(lds0 + (uint32_t)buf * STAGE + 4096u * i, src, voff[i]);
+  };
 
-  // Fragment sources in a stage: lane row l32 of a 32-row tile, logical
-  // chunk 2s + kh of the 16-k step s.
+  // ---- fragment sources: row l32 of each 32-row block, logical chunk 2t + kh
   const int l32 = lane & 31, kh = lane >> 5;
-  int swz[4];
+  uint32_t fa[T], fb[T];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) swz[s] = 16 * ((2 * s + kh) ^ ((l32 >> 1) & 7));
-  const int a_row = (wm * FM * 32 + l32) * kRowB;
-  // B rows of column tile j: STORE, the wave's FN tiles; SWIGLU, its FN/2
-  // gate tiles in the first half of the stage and the matching up tiles in
-  // the second half.
-  int b_row[FN];
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int r = EPI == GEMM_SWIGLU
-                      ? (j < FN / 2 ? wn * (FN / 2) * 32 + 32 * j : TN / 2 + wn * (FN / 2) * 32 + 32 * (j - FN / 2))
-                      : wn * FN * 32 + 32 * j;
-    b_row[j] = SA + (r + l32) * kRowB;
+  for (int t = 0; t < T; ++t) {
+    const uint32_t co = 16u * (uint32_t)((2 * t + kh) ^ swz<RB>(l32));
+    fa[t] = (uint32_t)(wm * FM * 32 + l32) * RB + co;
+    fb[t] = (uint32_t)(TM + wn * FN * 32 + l32) * RB + co;
   }
+  q35_u32x4 ra[2][FM], rb[2][FN];
+  // fragment r of step t in the order the MFMAs consume them: A0, B0 .. B(FN-1), A1 ..
+  auto read1 = [&](int buf, int t, int set, int r) {
+    const uint8_t* base = lds + buf * STAGE;
+    if (r == 0) {
+      ra[set][0] = *reinterpret_cast<const q35_u32x4*>(base + fa[t]);
+    } else if (r <= FN) {
+      rb[set][r - 1] = *reinterpret_cast<const q35_u32x4*>(base + fb[t] + (r - 1) * 32 * RB);
+    } else {
+      ra[set][r - FN] = *reinterpret_cast<const q35_u32x4*>(base + fa[t] + (r - FN) * 32 * RB);
+    }
+  };
 
-  typename GemmAcc<I8>::T acc[FM][FN];
+  AccT acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+  auto mfma = [&](int set, int q) {
+    acc[q / FN][q % FN] = mfma32(ra[set][q / FN], rb[set][q % FN], acc[q / FN][q % FN]);
+  };
 
-  uint4 ra0[LA], rb0[LB], ra1[LA], rb1[LB];
-#define Q35_GLOAD(RA, RB, KT)                                                            \
-  do {                                                                                   \
-    const uint32_t kk = (uint32_t)(KT) * kRowB;                                          \
-    _Pragma("unroll") for (int i = 0; i < LA; ++i) RA[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.A) + offA[i] + kk); \
-    _Pragma("unroll") for (int i = 0; i < LB; ++i) RB[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.B) + offB[i] + kk); \
-  } while (0)
-#define Q35_SSTORE(RA, RB, ST)                                                           \
-  do {                                                                                   \
-    uint8_t* sb = lds + (ST) * (SA + SB) + st_off;                                       \
-    _Pragma("unroll") for (int i = 0; i < LA; ++i) {                                     \
-      const q35_u32x4 v = {RA[i].x, RA[i].y, RA[i].z, RA[i].w};                          \
-      *reinterpret_cast<q35_u32x4*>(sb + i * 32 * kRowB) = v;                            \
-    }                                                                                    \
-    _Pragma("unroll") for (int i = 0; i < LB; ++i) {                                     \
-      const q35_u32x4 v = {RB[i].x, RB[i].y, RB[i].z, RB[i].w};                          \
-      *reinterpret_cast<q35_u32x4*>(sb + SA + i * 32 * kRowB) = v;                       \
-    }                                                                                    \
-  } while (0)
-#define Q35_READ(FA, FB, SB, S)                                                          \
-  do {                                                                                   \
-    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                       \
-      FA[i] = *reinterpret_cast<const uint4*>((SB) + a_row + i * 32 * kRowB + swz[S]);   \
-    _Pragma("unroll") for (int j = 0; j < FN; ++j)                                       \
-      FB[j] = *reinterpret_cast<const uint4*>((SB) + b_row[j] + swz[S]);                 \
-  } while (0)
-#define Q35_MFMA(FA, FB)                                                                 \
-  do {                                                                                   \
-    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                       \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = mfma32_bf16(FA[i], FB[j], acc[i][j]); \
-  } while (0)
-  // One stage: the fragments of 16-k step s + 1 are read while the MFMAs of
-  // step s run, the next stage's registers go to the other LDS buffer after
-  // step 1 and the fetch two stages ahead is issued after step 2; the group
-  // barriers keep the scheduler from clustering the LDS and memory traffic
-  // away from the MFMAs.
-#define Q35_SCHED() gemm_stage_schedule<FM, FN>()
-#define Q35_STAGE(ST, RAS, RBS, NST, RAL, RBL, KTL)                                      \
-  do {                                                                                   \
-    const uint8_t* sb = lds + (ST) * (SA + SB);                                          \
-    uint4 fa0[FM], fb0[FN], fa1[FM], fb1[FN];                                            \
-    Q35_READ(fa0, fb0, sb, 0);                                                           \
-    Q35_READ(fa1, fb1, sb, 1);                                                           \
-    Q35_MFMA(fa0, fb0);                                                                  \
-    Q35_READ(fa0, fb0, sb, 2);                                                           \
-    Q35_MFMA(fa1, fb1);                                                                  \
-    Q35_SSTORE(RAS, RBS, NST);                                                           \
-    Q35_READ(fa1, fb1, sb, 3);                                                           \
-    Q35_MFMA(fa0, fb0);                                                                  \
-    Q35_GLOAD(RAL, RBL, KTL);                                                            \
-    Q35_MFMA(fa1, fb1);                                                                  \
-    Q35_SCHED();                                                                         \
-  } while (0)
+  // ---- prologue: stages 0 .. NS-2 in flight, stage 0 landed, its first fragments read
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) dma(s, s, i);
+  if (nk >= NS - 1) wait_vm<(NS - 2) * LPW>();
+  else wait_vm<0>();
+  ring_barrier();
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read1(0, 0, 0, r);
 
-  // Stage 0 in LDS, stages 1 and 2 in flight; every later stage is fetched
-  // two steps before use. Fetch indices are clamped (the extra fetches at
-  // the end are never used), so no load sits behind a branch.
-  Q35_GLOAD(ra0, rb0, kbeg);
-  Q35_SSTORE(ra0, rb0, 0);
-  Q35_GLOAD(ra1, rb1, min(kbeg + 1, nk - 1));
-  Q35_GLOAD(ra0, rb0, min(kbeg + 2, nk - 1));
-  lds_barrier();
-  for (int kt = kbeg; kt < nk; kt += 2) {
-    Q35_STAGE(0, ra1, rb1, 1, ra1, rb1, min(kt + 3, nk - 1));
-    lds_barrier();
-    Q35_STAGE(1, ra0, rb0, 0, ra0, rb0, min(kt + 4, nk - 1));
-    lds_barrier();
+  // One stage. REFILL: the buffer of stage kt - 1 is refilled with stage
+  // kt + NS - 1 (every stage but the last NS - 1).
+  int buf = 0;
+  auto stage = [&](int kt, auto refill_tag) {
+    constexpr bool REFILL = decltype(refill_tag)::value;
+    const int rbuf = buf == 0 ? NS - 1 : buf - 1;  // buffer of stage kt - 1
+    // steps 0 .. T-2: one MFMA, one fragment read of the next step, and
+    // (first steps) the DMA refill, per slot
+#pragma unroll
+    for (int t = 0; t < T - 1; ++t) {
+#pragma unroll
+      for (int q = 0; q < NMF; ++q) {
+        mfma(t & 1, q);
+        if (q < NR) read1(buf, t + 1, (t + 1) & 1, q);
+        const int slot = t * NMF + q;
+        if (REFILL && slot < LPW) dma(kt + NS - 1, rbuf, slot);
+        Q35_PIN();
+      }
+    }
+    // last step: half the MFMAs, the ring barrier, the other half with the
+    // first fragments of stage kt + 1
+    constexpr int cur = (T - 1) & 1;
+#pragma unroll
+    for (int q = 0; q < H; ++q) {
+      mfma(cur, q);
+      Q35_PIN();
+    }
+    const int nbuf = buf + 1 == NS ? 0 : buf + 1;
+    const bool more = kt + 1 < nk;
+    wait_lds();  // on both paths, so the second half waits for nothing
+    if (more) {
+      // stage kt + 1 landed: this wave's part (vmcnt), then every wave's
+      if (REFILL) wait_vm<(NS - 2) * LPW>();
+      else wait_vm<0>();
+      ring_barrier();
+    }
+    Q35_PIN();
+#pragma unroll
+    for (int q = H; q < NMF; ++q) {
+      mfma(cur, q);
+      if (more) {
+        const int s = q - H;
+#pragma unroll
+        for (int r = s * NR / (NMF - H); r < (s + 1) * NR / (NMF - H); ++r) read1(nbuf, 0, cur ^ 1, r);
+      }
+      Q35_PIN();
+    }
+    buf = nbuf;
+  };
+  int kt = 0;
+  for (; kt + NS - 1 < nk; ++kt) stage(kt, BoolTag<true>{});
+  for (; kt < nk; ++kt) stage(kt, BoolTag<false>{});
+
+  // ---- split K: partial tiles, arrival count, the last workgroup sums
+  if constexpr (SPLIT) {
+    constexpr int NP = NMF * 8;  // 8-byte pairs per thread
+    uint64_t* mine = reinterpret_cast<uint64_t*>(a.part) + ((size_t)ks * ntiles + tile) * NP * 256 + tid;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const uint64_t v = (uint64_t)acc_bits(acc[i][j][e]) | ((uint64_t)acc_bits(acc[i][j][e + 1]) << 32);
+          __hip_atomic_store(mine + (size_t)(((i * FN + j) * 16 + e) / 2) * 256, v, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+    // Every thread waits for its own partial stores to complete (the
+    // workgroup barrier does not wait for memory), then one arrival is counted.
+    wait_vm<0>();
+    // (the count is shared through the first word of the stage ring, which
+    // no wave reads any more after this barrier)
+    unsigned* arrived = reinterpret_cast<unsigned*>(lds);
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned n = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (n == (unsigned)S - 1)
+        __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *arrived = n;
+    }
+    __syncthreads();
+    if (*arrived != (unsigned)S - 1) return;
+    AccT own[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) own[i][j] = acc[i][j];
+    for (int sp = 0; sp < S; ++sp) {
+      const uint64_t* src = reinterpret_cast<const uint64_t*>(a.part) + ((size_t)sp * ntiles + tile) * NP * 256 + tid;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; e += 2) {
+            EltT lo, hi;
+            if (sp == ks) {
+              lo = own[i][j][e];
+              hi = own[i][j][e + 1];
+            } else {
+              const uint64_t v = __hip_atomic_load(
+                  const_cast<uint64_t*>(src + (size_t)(((i * FN + j) * 16 + e) / 2) * 256),
+                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              lo = acc_from((uint32_t)v, EltT{});
+              hi = acc_from((uint32_t)(v >> 32), EltT{});
+            }
+            acc[i][j][e] = sp == 0 ? lo : acc[i][j][e] + lo;
+            acc[i][j][e + 1] = sp == 0 ? hi : acc[i][j][e + 1] + hi;
+          }
+    }
   }
-#undef Q35_READ
-#undef Q35_MFMA
-#undef Q35_STAGE
-#undef Q35_SCHED
-#undef Q35_GLOAD
-#undef Q35_SSTORE
 
-  gemm_finish<WM, FM, FN, EPI, SPLIT, I8>(a, acc, T, tile, ks, m0, n0);
+  // ---- epilogue. Element r of a 32x32 block sits at row 8 (r / 4) + 4 kh +
+  // r % 4, column l32.
+  if constexpr (!STAGED) {
+    // Direct: each lane stores its elements (bf16: 64-byte row segments per
+    // half wave; int32: 128-byte); tiles inside C store without checks.
+    const int rbase = m0 + wm * FM * 32 + 4 * kh;
+    const int cbase = n0 + wn * FN * 32 + l32;
+    const bool full = m0 + TM <= a.M && n0 + TN <= a.N;
+    auto store = [&](int i, int r, int j, bool check) {
+      const int row = rbase + 32 * i + 8 * (r >> 2) + (r & 3);
+      const int col = cbase + 32 * j;
+      if (check && (row >= a.M || col >= a.N)) return;
+      const size_t at = (size_t)row * a.N + col;
+      if constexpr (KIND == KIND_I32) reinterpret_cast<int*>(a.C)[at] = acc[i][j][r];
+      else reinterpret_cast<uint16_t*>(a.C)[at] = (uint16_t)f2bf(acc[i][j][r]);
+    };
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) store(i, r, j, false);
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) store(i, r, j, true);
+    }
+    return;
+  }
+  // Staged through LDS. bf16 kinds stage the whole tile as bf16 (the values
+  // they store, or the rounded gate / up), int8 kinds the int32 accumulators
+  // of one half tile (one wave row) at a time; rows are staged at a stride of
+  // TN elements + 16 bytes (the two halves of each write instruction, rows r
+  // and r + 4, fall on different banks). Then every thread takes ITER chunks
+  // of 16 staged bytes along the rows, all read before any is converted, and
+  // stores each chunk's outputs with one 8- or 16-byte store (bf16 rounding,
+  // dequant with the tile's scales from LDS, or SwiGLU of the gate and up
+  // columns, the two halves of a staged row).
+  {
+    constexpr bool W16 = !I8;                  // staged as bf16
+    constexpr int EB = W16 ? 2 : 4;            // staged bytes per element
+    constexpr int PH = W16 ? 1 : WM;           // phases (half tiles for int8)
+    constexpr int PR = TM / PH;                // staged rows per phase
+    constexpr int SB = TN * EB + 16;           // staged row stride in bytes
+    constexpr int VPC = 16 / EB;               // values per 16-byte chunk
+    constexpr int CPRW = NC / VPC;             // output chunks per row
+    constexpr int ITER = PR * CPRW / 256;      // chunks per thread and phase
+    constexpr int SCO = PR * SB;               // LDS offset of the scales
+    static_assert(PR * CPRW % 256 == 0, "the chunks divide over the workgroup");
+    static_assert(SCO + NSC * 4 <= NS * STAGE, "the staged tile and scales fit the ring");
+    const bool vec = (a.N & 7) == 0;
+    float* sc = reinterpret_cast<float*>(lds + SCO);
+    wait_lds();
+    __syncthreads();  // every wave is done with the stage ring
+    if constexpr (DEQ) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        if (tid + 256 * q < NSC) sc[tid + 256 * q] = scl[q];
+    }
+#pragma unroll
+    for (int h = 0; h < PH; ++h) {
+      if (PH == 1 || wm == h) {
+        const int rb0 = PH == 1 ? wm * FM * 32 : 0;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int off = (rb0 + i * 32 + 8 * (r >> 2) + 4 * kh + (r & 3)) * SB +
+                              (wn * FN * 32 + j * 32 + l32) * EB;
+              if constexpr (W16)
+                *reinterpret_cast<uint16_t*>(lds + off) = (uint16_t)f2bf(acc[i][j][r]);
+              else
+                *reinterpret_cast<uint32_t*>(lds + off) = acc_bits(acc[i][j][r]);
+            }
+      }
+      __syncthreads();
+      q35_u32x4 v[ITER], u[ITER];
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + 256 * it;
+        const uint8_t* src = lds + (c / CPRW) * SB + (c % CPRW) * 16;
+        v[it] = *reinterpret_cast<const q35_u32x4*>(src);
+        if constexpr (SWIGLU) u[it] = *reinterpret_cast<const q35_u32x4*>(src + TN / 2 * EB);
+      }
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int c = tid + 256 * it;
+        const int lrow = h * PR + c / CPRW, lcol = (c % CPRW) * VPC;
+        const int grow = m0 + lrow;
+        const int col = n0 + lcol;
+        if (grow >= a.M || col >= a.N) continue;
+        const int ncol = min(VPC, a.N - col);
+        const size_t at = (size_t)grow * a.N + col;
+        if constexpr (KIND == KIND_I32) {
+          int* C = reinterpret_cast<int*>(a.C) + at;
+          if (vec && ncol == VPC) *reinterpret_cast<q35_u32x4*>(C) = v[it];
+          else for (int e = 0; e < ncol; ++e) C[e] = (int)v[it][e];
+        } else if constexpr (KIND == KIND_BF16) {
+          uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + at;
+          if (vec && ncol == VPC) *reinterpret_cast<q35_u32x4*>(C) = v[it];
+          else for (int e = 0; e < ncol; ++e) C[e] = (uint16_t)(v[it][e >> 1] >> (16 * (e & 1)));
+        } else {
+          float o[VPC];
+          if constexpr (KIND == KIND_SWIGLU) {
+#pragma unroll
+            for (int e = 0; e < VPC; ++e) {
+              const uint32_t gw = v[it][e >> 1], uw = u[it][e >> 1];
+              const float g = (e & 1) ? bf_hi(gw) : bf_lo(gw);
+              const float uu = (e & 1) ? bf_hi(uw) : bf_lo(uw);
+              o[e] = round_bf(silu_fast(g)) * uu;
+            }
+          } else {
+            // scales: s_x of the row at sc[lrow], s_w of column lcol + e at
+            // sc[TM + lcol + e] (SwiGLU up columns NC further)
+            const float sx = sc[lrow];
+            const q35_f32x4 sw = *reinterpret_cast<const q35_f32x4*>(sc + TM + lcol);
+#pragma unroll
+            for (int e = 0; e < VPC; ++e) {
+              if constexpr (KIND == KIND_DEQ) {
+                o[e] = (float)(int)v[it][e] * sx * sw[e];
+              } else {
+                const float g = round_bf((float)(int)v[it][e] * sx * sw[e]);
+                const float uu = round_bf((float)(int)u[it][e] * sx * sc[TM + NC + lcol + e]);
+                o[e] = round_bf(silu_fast(g)) * uu;
+              }
+            }
+          }
+          uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + at;
+          if constexpr (VPC == 8) {
+            if (vec && ncol == 8) *reinterpret_cast<uint4*>(C) = pack8(o);
+            else for (int e = 0; e < ncol; ++e) C[e] = (uint16_t)f2bf(o[e]);
+          } else {
+            if (vec && ncol == 4) *reinterpret_cast<uint2*>(C) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+            else for (int e = 0; e < ncol; ++e) C[e] = (uint16_t)f2bf(o[e]);
+          }
+        }
+      }
+      if (h + 1 < PH) __syncthreads();
+    }
+  }
 }
 
-// Tile shapes (waves along M, 32x32 MFMA tiles per wave along M and N):
-// 0: 256x192 (4x1 waves, 2x6 tiles); 1: 128x128 (2x2 waves, 2x2);
-// 2: 256x128 (4x1 waves, 2x4); 3: 128x256 (2x2 waves, 2x4).
-constexpr int kTiles = 4;
-constexpr int kTileTM[kTiles] = {256, 128, 256, 128};
-constexpr int kTileTN[kTiles] = {192, 128, 128, 256};
-constexpr int kTileRegs[kTiles] = {12 * 16, 4 * 16, 8 * 16, 8 * 16};  // accumulators per thread
+// ---------------------------------------------------------------- plans
+// Tile shapes (waves 2 x 2; FM x FN blocks of 32 x 32 per wave; RB bytes per
+// row and stage; NS stages in the ring; LDS = NS (TM + TN) RB; epilogue
+// staged through LDS, or direct stores for the bf16 / int32 kinds):
+//   0: 256 x 192 (4 x 3), RB 128, NS 2, staged  (112 KiB)
+//   1: 128 x 128 (2 x 2), RB 128, NS 4, staged  (128 KiB)
+//   2: 256 x 128 (4 x 2), RB 128, NS 3, staged  (144 KiB)
+//   3: 128 x 192 (2 x 3), RB 128, NS 4, staged  (160 KiB)
+//   4: 256 x 192 (4 x 3), RB 64,  NS 4, staged  (112 KiB)
+//   5: tile 0 with direct stores; 6: tile 1 with direct stores
+#define Q35_GEMM_TILES(X)           \
+  X(0, 2, 2, 4, 3, 128, 2, true)    \
+  X(1, 2, 2, 2, 2, 128, 4, true)    \
+  X(2, 2, 2, 4, 2, 128, 3, true)    \
+  X(3, 2, 2, 2, 3, 128, 4, true)    \
+  X(4, 2, 2, 4, 3, 64, 4, true)     \
+  X(5, 2, 2, 4, 3, 128, 2, false)   \
+  X(6, 2, 2, 2, 2, 128, 4, false)
+constexpr int kTiles = 7;
+constexpr int kTM[kTiles] = {256, 128, 256, 128, 256, 256, 128};
+constexpr int kTN[kTiles] = {192, 128, 128, 192, 192, 192, 128};
+constexpr int kRB[kTiles] = {128, 128, 128, 128, 64, 128, 128};
+constexpr bool kStaged[kTiles] = {true, true, true, true, true, false, false};
+constexpr bool kSplitOk[kTiles] = {false, true, true, true, false, false, true};  // up to 8 blocks per wave
+constexpr int kMaxSplits = 8;
 
-template <int WM, int FM, int FN, int EPI, bool I8>
-int launch_gemm(const GemmArgs& a, hipStream_t stream) {
-  constexpr int TM = WM * FM * 32, TN = (4 / WM) * FN * 32;
-  constexpr int NC = EPI == GEMM_SWIGLU ? TN / 2 : TN;
-  const long long tiles = (long long)((a.M + TM - 1) / TM) * ((a.N + NC - 1) / NC);
-  Q35_CHECK_ARG(tiles * a.splits < (1ll << 31));
+long long tiles_of(int tile, int M, int N, int kind) {
+  const int nc = kind_swiglu(kind) ? kTN[tile] / 2 : kTN[tile];
+  return (long long)((M + kTM[tile] - 1) / kTM[tile]) * ((N + nc - 1) / nc);
+}
+
+long long workspace_bytes(int tile, int M, int N, int kind, int splits) {
+  if (splits <= 1) return 0;
+  return kCounterBytes + tiles_of(tile, M, N, kind) * splits * kTM[tile] * kTN[tile] * 4ll;
+}
+
+// Default plan by output shape (measured at M = 1024 on the 2B prefill
+// shapes, profiles/prefill_gemm_sweep.txt): the widest tile that still gives
+// most CUs a workgroup, with direct stores for the bf16 / int32 kinds and the
+// staged epilogue for SwiGLU and dequant; outputs with fewer tiles than CUs
+// split K only when each split keeps at least 40 stages (the partial-tile
+// exchange costs more than the idle CUs below that).
+void plan(int M, int N, int K, int kind, int* tile, int* splits) {
+  const int es = kind_i8(kind) ? 1 : 2;
+  const bool direct = kind == KIND_BF16 || kind == KIND_I32;
+  *splits = 1;
+  if (kind_swiglu(kind)) {
+    *tile = tiles_of(0, M, N, kind) >= 192 ? 0 : 3;
+    return;
+  }
+  if (tiles_of(0, M, N, kind) >= 160) {
+    *tile = direct ? 5 : 0;
+  } else if (tiles_of(3, M, N, kind) >= 160) {
+    *tile = 3;
+  } else {
+    *tile = direct ? 6 : 1;
+    const long long t = tiles_of(1, M, N, kind);
+    const int nk = K * es / kRB[1];
+    while (*splits < kMaxSplits && t * *splits * 2 <= 256 && nk % (*splits * 2) == 0 &&
+           nk / (*splits * 2) >= 40 && t <= kMaxSplitTiles)
+      *splits *= 2;
+  }
+}
+
+template <int WM, int WN, int FM, int FN, int RB, int NS, int KIND, bool STAGED>
+int launch_one(const GemmArgs& a, hipStream_t stream) {
+  if constexpr (!STAGED && KIND != KIND_BF16 && KIND != KIND_I32) {
+    return (int)hipErrorInvalidValue;  // direct stores: bf16 and int32 kinds
+  } else {
+  constexpr int TM = WM * FM * 32, TN = WN * FN * 32;
+  constexpr int NC = kind_swiglu(KIND) ? TN / 2 : TN;
+  const long long units = (long long)((a.M + TM - 1) / TM) * ((a.N + NC - 1) / NC) * a.splits;
+  Q35_CHECK_ARG(units < (1ll << 31));
   if (a.splits > 1) {
-    if constexpr (FM * FN <= 8) {
-      Q35_CHECK_ARG(tiles <= kMaxSplitTiles && a.ws);
-      gemm_tn<WM, FM, FN, EPI, true, I8><<<(unsigned)(tiles * a.splits), 256, 0, stream>>>(a);
+    if constexpr (kind_swiglu(KIND) || FM * FN > 8) {
+      return (int)hipErrorInvalidValue;  // split K: tiles of up to 8 blocks per wave, no SwiGLU
     } else {
-      return (int)hipErrorInvalidValue;  // split-K for the tiles of up to 8 MFMA blocks per wave
+      gemm_ring<WM, WN, FM, FN, RB, NS, KIND, true, STAGED><<<(unsigned)units, 256, 0, stream>>>(a);
     }
   } else {
-    gemm_tn<WM, FM, FN, EPI, false, I8><<<(unsigned)tiles, 256, 0, stream>>>(a);
+    gemm_ring<WM, WN, FM, FN, RB, NS, KIND, false, STAGED><<<(unsigned)units, 256, 0, stream>>>(a);
   }
   return q35_last_error();
+  }
 }
 
-template <int EPI, bool I8>
+template <int KIND>
 int launch_tile(int tile, const GemmArgs& a, hipStream_t stream) {
   switch (tile) {
-    case 0: return launch_gemm<4, 2, 6, EPI, I8>(a, stream);
-    case 1: return launch_gemm<2, 2, 2, EPI, I8>(a, stream);
-    case 2: return launch_gemm<4, 2, 4, EPI, I8>(a, stream);
-    case 3: return launch_gemm<2, 2, 4, EPI, I8>(a, stream);
+#define Q35_GEMM_CASE(id, wm, wn, fm, fn, rb, ns, staged) \
+  case id: return launch_one<wm, wn, fm, fn, rb, ns, KIND, staged>(a, stream);
+    Q35_GEMM_TILES(Q35_GEMM_CASE)
+#undef Q35_GEMM_CASE
     default: return (int)hipErrorInvalidValue;
   }
 }
 
-long long tiles_of(int tile, int M, int N, int swiglu) {
-  const int nc = swiglu ? kTileTN[tile] / 2 : kTileTN[tile];
-  return (long long)((M + kTileTM[tile] - 1) / kTileTM[tile]) * ((N + nc - 1) / nc);
-}
-
-// Tile shape and split count by output shape (measured at M = 1024 on the 2B
-// prefill shapes): 128x128 tiles unless the output is wide enough for
-// 256x192 (N >= 12288); outputs that leave fewer tiles than CUs (N = 2048)
-// split K over 2 workgroups per tile.
-void plan(int M, int N, int K, int es, int swiglu, int* tile, int* splits) {
-  *tile = (swiglu ? 2 * N : N) >= 12288 ? 0 : 1;
-  *splits = 1;
-  if (swiglu) return;
-  const int nk = K * es / kRowB;
-  if (*tile == 1 && tiles_of(1, M, N, 0) < 256 && nk % 4 == 0 && tiles_of(1, M, N, 0) <= kMaxSplitTiles)
-    *splits = 2;
-}
-
-long long workspace_bytes(int tile, int M, int N, int splits, int swiglu) {
-  if (splits <= 1) return 0;
-  return tiles_of(tile, M, N, swiglu) * splits * 256ll * kTileRegs[tile] * 4;
-}
-
-int gemm_run(const void* A, const void* B, void* C, int M, int N, int K, int tile, int splits,
-             int swiglu, bool i8, const float* s_x, const float* s_w, void* ws, long long ws_bytes,
-             hipStream_t stream) {
-  const int es = i8 ? 1 : 2;
-  Q35_CHECK_ARG(A && B && C && M > 0 && N > 0 && K > 0 && (K * es) % (2 * kRowB) == 0);
-  Q35_CHECK_ARG(q35_aligned16(A) && q35_aligned16(B));
-  Q35_CHECK_ARG(!i8 || (s_x && s_w));
-  Q35_CHECK_ARG((long long)M * K * es < (1ll << 32) && (swiglu ? 2ll : 1ll) * N * K * es < (1ll << 32));
-  Q35_CHECK_ARG(tile >= 0 && tile < kTiles && splits >= 1 && splits <= 16);
-  const int nk = K * es / kRowB;
-  Q35_CHECK_ARG(nk % (2 * splits) == 0);  // every split runs whole pairs of stages
-  Q35_CHECK_ARG(splits == 1 || ws_bytes >= workspace_bytes(tile, M, N, splits, swiglu));
-  const GemmArgs a{(const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C, M, N, K,
-                   (float*)ws, splits, nk / splits, s_x, s_w};
-  if (i8)
-    return swiglu ? launch_tile<GEMM_SWIGLU, true>(tile, a, stream)
-                  : launch_tile<GEMM_STORE, true>(tile, a, stream);
-  return swiglu ? launch_tile<GEMM_SWIGLU, false>(tile, a, stream)
-                : launch_tile<GEMM_STORE, false>(tile, a, stream);
+int gemm_run(const void* A, const void* B, void* C, int M, int N, int K, int kind, const float* s_x,
+             const float* s_w, int tile, int splits, void* ws, long long ws_bytes, hipStream_t stream) {
+  Q35_CHECK_ARG(kind >= 0 && kind < kNumKinds);
+  if (tile < 0) plan(M, N, K, kind, &tile, &splits);
+  const int es = kind_i8(kind) ? 1 : 2;
+  Q35_CHECK_ARG(A && B && C && M > 0 && N > 0 && K > 0);
+  Q35_CHECK_ARG(tile >= 0 && tile < kTiles && splits >= 1 && splits <= kMaxSplits);
+  Q35_CHECK_ARG(kStaged[tile] || kind == KIND_BF16 || kind == KIND_I32);
+  Q35_CHECK_ARG(q35_aligned16(A) && q35_aligned16(B) && ((long long)K * es) % kRB[tile] == 0);
+  Q35_CHECK_ARG((kind != KIND_DEQ && kind != KIND_DEQ_SWIGLU) || (s_x && s_w));
+  // 32-bit byte offsets of every operand row
+  Q35_CHECK_ARG((long long)M * K * es < (1ll << 32) && (kind_swiglu(kind) ? 2ll : 1ll) * N * K * es < (1ll << 32));
+  const int nk = (int)((long long)K * es / kRB[tile]);
+  Q35_CHECK_ARG(nk % splits == 0);
+  if (splits > 1) {
+    Q35_CHECK_ARG(kSplitOk[tile] && !kind_swiglu(kind) && tiles_of(tile, M, N, kind) <= kMaxSplitTiles);
+    Q35_CHECK_ARG(ws && q35_aligned16(ws) && ws_bytes >= workspace_bytes(tile, M, N, kind, splits));
+  }
+  GemmArgs a{(const uint8_t*)A, (const uint8_t*)B, C, M, N, K, s_x, s_w, nullptr, nullptr, splits, nk / splits};
+  if (splits > 1) {
+    a.cnt = (unsigned*)ws;
+    a.part = (uint8_t*)ws + kCounterBytes;
+  }
+  switch (kind) {
+    case KIND_BF16: return launch_tile<KIND_BF16>(tile, a, stream);
+    case KIND_SWIGLU: return launch_tile<KIND_SWIGLU>(tile, a, stream);
+    case KIND_I32: return launch_tile<KIND_I32>(tile, a, stream);
+    case KIND_DEQ: return launch_tile<KIND_DEQ>(tile, a, stream);
+    default: return launch_tile<KIND_DEQ_SWIGLU>(tile, a, stream);
+  }
 }
 
 }  // namespace
 
 extern "C" {
 
-// Workspace bytes q35_gemm_bf16 / q35_gemm_swiglu_bf16 need for this shape.
-long long q35_gemm_workspace(int M, int N, int K, int swiglu) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  int tile, splits;
-  plan(M, N, K, 2, swiglu, &tile, &splits);
-  return workspace_bytes(tile, M, N, splits, swiglu);
+// Workspace bytes of q35_gemm for (M, N, K, kind) and a plan (tile < 0: the
+// default plan); 0 when the plan does not split K, -1 for an invalid plan.
+long long q35_gemm_workspace(int M, int N, int K, int kind, int tile, int splits) {
+  if (M <= 0 || N <= 0 || K <= 0 || kind < 0 || kind >= kNumKinds) return -1;
+  if (tile < 0) plan(M, N, K, kind, &tile, &splits);
+  if (tile >= kTiles || splits < 1 || splits > kMaxSplits) return -1;
+  if (!kStaged[tile] && kind != KIND_BF16 && kind != KIND_I32) return -1;
+  if (splits > 1 && (!kSplitOk[tile] || kind_swiglu(kind) || tiles_of(tile, M, N, kind) > kMaxSplitTiles))
+    return -1;
+  return workspace_bytes(tile, M, N, kind, splits);
 }
 
-// C[M,N] = bf16(A[M,K] . B[N,K]^T). K a multiple of 128, A/B 16-byte aligned,
-// M*K and N*K below 2^31 elements; workspace of q35_gemm_workspace bytes.
-int q35_gemm_bf16(const void* A, const void* B, void* C, int M, int N, int K, void* workspace,
-                  long long workspace_bytes, hipStream_t stream) {
-  int tile, splits;
-  plan(M, N, K, 2, 0, &tile, &splits);
-  return gemm_run(A, B, C, M, N, K, tile, splits, 0, false, nullptr, nullptr, workspace,
-                  workspace_bytes, stream);
-}
-
-// C[M,N] = bf16(bf16(silu(bf16(A.Bg^T))) * bf16(A.Bu^T)) with B = [Bg; Bu]
-// ([2N, K]): the packed gate/up projection and silu_and_mul in one launch.
-int q35_gemm_swiglu_bf16(const void* A, const void* B, void* C, int M, int N, int K,
-                         void* workspace, long long workspace_bytes, hipStream_t stream) {
-  int tile, splits;
-  plan(M, N, K, 2, 1, &tile, &splits);
-  return gemm_run(A, B, C, M, N, K, tile, splits, 1, false, nullptr, nullptr, workspace,
-                  workspace_bytes, stream);
-}
-
-// Explicit tile shape (0-3) and split count (K / 64 divisible by 2 * splits),
-// for measurement and tests; workspace_bytes as returned for that plan by
-// q35_gemm_plan_workspace.
-int q35_gemm_bf16_plan(const void* A, const void* B, void* C, int M, int N, int K, int tile,
-                       int splits, int swiglu, void* workspace, long long workspace_bytes,
-                       hipStream_t stream) {
-  return gemm_run(A, B, C, M, N, K, tile, splits, swiglu, false, nullptr, nullptr, workspace,
-                  workspace_bytes, stream);
-}
-
-long long q35_gemm_plan_workspace(int M, int N, int tile, int splits, int swiglu) {
-  if (M <= 0 || N <= 0 || tile < 0 || tile >= kTiles || splits < 1) return -1;
-  return workspace_bytes(tile, M, N, splits, swiglu);
-}
-
-// A8W8 prefill GEMM: int8 A[M,K] (per-token quantised, scales s_x[M]) times
-// int8 B[N,K]^T (per-channel, scales s_w[N]; swiglu: B = [gate; up] [2N, K],
-// s_w [2N]) on the int8 matrix cores, exact int32 accumulators, dequantised
-// in the epilogue: C = bf16(float(acc) * s_x[m] * s_w[n]) (swiglu: gate and up
-// dequantised to bf16, then bf16(silu(g)) * u). K a multiple of 256. tile < 0
-// picks the plan; workspace of q35_gemm_a8w8_workspace bytes for that plan.
-long long q35_gemm_a8w8_workspace(int M, int N, int K, int swiglu, int tile, int splits) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  if (tile < 0) plan(M, N, K, 1, swiglu, &tile, &splits);
-  if (tile >= kTiles || splits < 1) return -1;
-  return workspace_bytes(tile, M, N, splits, swiglu);
-}
-
-int q35_gemm_a8w8(const void* Aq, const void* s_x, const void* Bq, const void* s_w, void* C, int M,
-                  int N, int K, int swiglu, int tile, int splits, void* workspace,
-                  long long workspace_bytes, hipStream_t stream) {
-  if (tile < 0) plan(M, N, K, 1, swiglu, &tile, &splits);
-  return gemm_run(Aq, Bq, C, M, N, K, tile, splits, swiglu, true, (const float*)s_x,
-                  (const float*)s_w, workspace, workspace_bytes, stream);
+// Prefill GEMM C = A . B^T of the given kind (0 bf16, 1 bf16 SwiGLU, 2 int8 ->
+// int32, 3 int8 -> bf16 dequant, 4 int8 SwiGLU; see gemm.hip's header).
+// K * element bytes a multiple of the tile's stage width; A and B 16-byte
+// aligned; every operand below 2^32 bytes. tile < 0 picks the default plan,
+// otherwise tile 0-4 with `splits` K splits (the stage count divisible by
+// splits). A split plan needs a workspace of q35_gemm_workspace bytes,
+// zero-filled before its first use.
+int q35_gemm(const void* A, const void* B, void* C, int M, int N, int K, int kind, const void* s_x,
+             const void* s_w, int tile, int splits, void* workspace, long long workspace_bytes,
+             hipStream_t stream) {
+  return gemm_run(A, B, C, M, N, K, kind, (const float*)s_x, (const float*)s_w, tile, splits,
+                  workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -71,10 +71,6 @@ class FusionConfig:
     # chunk prep from the raw projection (one launch and one 12 MB
     # intermediate fewer per layer; same values)
     delta_conv_in_prep: bool = True
-    # prefill of 64+ tokens (a multiple of 8), bf16 linears: the packed gate/up
-    # GEMM as W @ X^T (the library's kernel for that orientation is faster)
-    # and the SiLU-mul transposing back to token-major rows
-    prefill_gate_up_transposed: bool = True
 
 
 def _gpu_bf16(t: Any) -> bool:
@@ -123,9 +119,10 @@ class _Weight(torch.nn.Module):
 
     def from_int8(self, xq: torch.Tensor, sx: torch.Tensor) -> torch.Tensor:
         """The A8W8 prefill product of already quantised rows ``xq [..., K]``
-        (scales ``sx``): int32 GEMM, then the dequant, bf16 ``[..., N]``."""
-        acc = K.a8w8_int_gemm(xq, self.w)
-        return K.dequant_linear_i32(acc, sx, self.s, (*xq.shape[:-1], self.out_features))
+        (scales ``sx``): the int8 GEMM with the dequant in its epilogue, bf16
+        ``[..., N]``."""
+        y = K.gemm_a8w8(xq.reshape(-1, xq.shape[-1]), sx, self.w, self.s)
+        return y.reshape(*xq.shape[:-1], self.out_features)
 
     def to_int32(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """The A8W8 prefill product left as ``(int32 accumulators [rows, N],
@@ -257,21 +254,17 @@ def _mlp_fast(module, config: FusionConfig):
 
 def _mlp_apply(mlp, x: torch.Tensor, config: FusionConfig) -> torch.Tensor:
     """SwiGLU MLP (reference integration.py:169-187): decode one token through
-    the SwiGLU GEMV, prefill through the GEMM and ``silu_and_mul``."""
+    the SwiGLU GEMV, prefill through the matrix-core GEMM with the SwiGLU in
+    its epilogue (the packed gate/up product is never stored)."""
     gate_up = mlp.q35_gate_up
     if gate_up.int8:
         act = K.a8w8_swiglu(x, gate_up.w, gate_up.s)
     elif config.ppu_swiglu_gemv and x.shape[:-1] == (1, 1):
         act = K.ppu_swiglu_gemv(x, gate_up.w, block_n=config.ppu_swiglu_block_n)
+    elif x.numel() > x.shape[-1] and x.shape[-1] % 64 == 0:
+        act = K.gemm_bf16(x, gate_up.w, swiglu=True)  # SwiGLU in the GEMM epilogue
     else:
-        rows = x.numel() // x.shape[-1]
-        width = gate_up.w.shape[0] // 2
-        if (config.prefill_gate_up_transposed and rows >= 64 and rows % 8 == 0 and width % 64 == 0
-                and _gpu_bf16(gate_up.w)):
-            packed_t = torch.mm(gate_up.w, x.reshape(rows, -1).t())
-            act = K.silu_and_mul_t(packed_t).reshape(*x.shape[:-1], width)
-        else:
-            act = K.silu_and_mul(gate_up(x))
+        act = K.silu_and_mul(gate_up(x))
     return mlp.q35_down(act)
 
 

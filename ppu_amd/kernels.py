@@ -465,19 +465,75 @@ def gated_norm_linear(
     return out
 
 
+# ------------------------------------------------------------------ prefill GEMM
+# kinds of q35_gemm (include/q35.h)
+GEMM_BF16, GEMM_SWIGLU, GEMM_I32, GEMM_DEQUANT, GEMM_DEQUANT_SWIGLU = range(5)
+# Split-K workspaces, one per device, zero-filled once and kept for the life of
+# the process: a captured graph holds their address, and every launch leaves
+# the arrival counters at zero again. A larger request allocates a new one and
+# keeps the old. Split-K GEMMs on one device therefore must not overlap in
+# time (the prefill issues its GEMMs one after another).
+_gemm_ws: dict[int, list[torch.Tensor]] = {}
+
+
+def _gemm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    held = _gemm_ws.setdefault(device.index, [])
+    if held and held[-1].numel() * 4 >= nbytes:
+        return held[-1]
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("the split-K GEMM workspace must exist before graph capture: "
+                           "run the same shapes once outside the capture")
+    ws = torch.zeros(max(nbytes, 1 << 24) // 4 + 64, device=device, dtype=torch.int32)
+    held.append(ws)
+    return ws
+
+
+def gemm_into(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, kind: int, *,
+              s_x: torch.Tensor | None = None, s_w: torch.Tensor | None = None,
+              plan: tuple[int, int] | None = None) -> torch.Tensor:
+    """``C = A . B^T`` of one kind on the hand-written matrix-core GEMM
+    (``q35_gemm``): ``a`` [M, K], ``b`` [N, K] (SwiGLU kinds [2N, K]), ``c``
+    [M, N] written in place; all contiguous on the GPU. ``plan`` = (tile 0-3,
+    K splits) overrides the library's choice (for measurement)."""
+
+    m, k = a.shape
+    n = c.shape[-1]
+    tile, splits = plan if plan is not None else (-1, 1)
+    lib = _lib.load()
+    nbytes = lib.q35_gemm_workspace(m, n, k, kind, tile, splits)
+    if nbytes < 0:
+        raise ValueError(f"invalid GEMM plan {plan} for kind {kind}")
+    ws = _gemm_workspace(a.device, nbytes) if nbytes > 0 else None
+    _lib.call("q35_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, kind, _lib.ptr(s_x),
+              _lib.ptr(s_w), tile, splits, _lib.ptr(ws), 0 if ws is None else ws.numel() * 4,
+              _stream(a))
+    return c
+
+
+def _gemm_operands(x: torch.Tensor, weight: torch.Tensor, dtype: torch.dtype, swiglu: bool):
+    k = x.shape[-1]
+    if weight.ndim != 2 or weight.shape[1] != k:
+        raise ValueError("GEMM weight must be [N, K] matching the input")
+    if x.dtype != dtype or weight.dtype != dtype:
+        raise ValueError(f"GEMM operands must be {dtype}")
+    if k % (128 // dtype.itemsize):
+        raise ValueError("the matrix-core GEMM needs K to be a multiple of 128 bytes")
+    if swiglu and weight.shape[0] % 2:
+        raise ValueError("packed SwiGLU weight must have an even number of rows")
+    if not (x.is_cuda and weight.is_cuda and weight.is_contiguous()):
+        raise ValueError("GEMM tensors must be contiguous GPU tensors")
+    x2 = x.reshape(-1, k).contiguous()
+    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    return x2, n
+
+
 @_device_checked
 def prefill_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-    """``F.linear(x, W)`` for M > 1 tokens (prefill), bf16 in/out, fp32 accumulate.
+    """``F.linear(x, W)`` for M > 1 tokens (prefill), bf16 in/out, fp32
+    accumulate, on the hand-written matrix-core GEMM (the reference's prefill
+    ``F.linear`` call sites, integration.py:183,245,272,298,359)."""
 
-    A plain dense GEMM: it runs on the ROCm library GEMM (hipBLASLt/rocBLAS
-    MFMA kernels) behind ``torch.nn.functional.linear`` on the GPU tensor, as
-    the reference's prefill call sites do (integration.py:183,245,298).
-    """
-
-    if not x.is_cuda:
-        raise ValueError("fused kernels require a GPU tensor")
-    _need_bf16(x, weight)
-    return torch.nn.functional.linear(x, weight)
+    return gemm_bf16(x, weight)
 
 
 @_device_checked
@@ -486,41 +542,13 @@ def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
     """The hand-written matrix-core prefill GEMM: ``F.linear(x, W)`` (bf16 in
     and out, fp32 accumulate) or, with ``swiglu``, ``silu_and_mul(F.linear(x,
     W))`` for a packed ``[gate; up]`` weight in one launch (reference
-    integration.py:183-185, kernels.py:158-180). K must be a multiple of 128.
-    ``plan`` = (tile shape 0-3, K splits) overrides the library's choice (for
-    measurement)."""
+    integration.py:183-185, kernels.py:158-180). K must be a multiple of 64.
+    ``plan`` = (tile 0-3, K splits) overrides the library's choice."""
 
-    k = x.shape[-1]
-    if weight.ndim != 2 or weight.shape[1] != k:
-        raise ValueError("GEMM weight must be [N, K] matching the input")
-    if k % 128:
-        raise ValueError("the matrix-core GEMM needs K to be a multiple of 128")
-    if swiglu and weight.shape[0] % 2:
-        raise ValueError("packed SwiGLU weight must have an even number of rows")
-    if not weight.is_contiguous():
-        raise ValueError("GEMM tensors must be contiguous GPU tensors")
-    _need_bf16(x, weight)
-    x2 = x.reshape(-1, k).contiguous()
-    m = x2.shape[0]
-    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    x2, n = _gemm_operands(x, weight, _BF16, swiglu)
     y = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_BF16)
-    if m == 0:
-        return y
-    lib = _lib.load()
-    if plan is None:
-        nbytes = lib.q35_gemm_workspace(m, n, k, int(swiglu))
-    else:
-        nbytes = lib.q35_gemm_plan_workspace(m, n, plan[0], plan[1], int(swiglu))
-        if nbytes < 0:
-            raise ValueError(f"invalid GEMM plan {plan}")
-    ws = torch.empty(nbytes // 4, device=x.device, dtype=torch.float32) if nbytes > 0 else None
-    if plan is None:
-        name = "q35_gemm_swiglu_bf16" if swiglu else "q35_gemm_bf16"
-        _lib.call(name, x2.data_ptr(), weight.data_ptr(), y.data_ptr(), m, n, k, _lib.ptr(ws),
-                  nbytes, _stream(x))
-    else:
-        _lib.call("q35_gemm_bf16_plan", x2.data_ptr(), weight.data_ptr(), y.data_ptr(), m, n, k,
-                  plan[0], plan[1], int(swiglu), _lib.ptr(ws), nbytes, _stream(x))
+    if x2.shape[0]:
+        gemm_into(x2, weight, y.view(-1, n), GEMM_SWIGLU if swiglu else GEMM_BF16, plan=plan)
     return y
 
 
@@ -1146,7 +1174,7 @@ def a8w8_linear(
     against per-channel int8 weights, bf16 dequantised output
     (reference explore_runtime_quantization.py:161-181). Up to 16 tokens run
     on the int8 GEMV (for one token with the quantisation fused into the
-    launch); prefill on the ROCm library's int8 GEMM and the dequant kernel."""
+    launch); prefill on the int8 matrix-core GEMM with the dequant fused."""
 
     k = x.shape[-1]
     if weight_q.ndim != 2 or weight_q.shape[1] != k or weight_q.dtype != torch.int8:
@@ -1164,18 +1192,19 @@ def a8w8_linear(
     xq = torch.empty((m, k), device=x.device, dtype=torch.int8)
     sx = torch.empty((m, 1), device=x.device, dtype=torch.float32)
     y = torch.empty((m, n), device=x.device, dtype=_BF16)
-    if m > _A8W8_GEMV_MAX_M and n % 8 == 0 and k % 8 == 0:
-        # Prefill: per-token quantisation (gfx950 kernel), the int8 GEMM of the
-        # ROCm library (hipBLASLt, exact int32 accumulators), dequant kernel.
-        # (gemm_a8w8, the hand-written int8 GEMM with the dequant in its
-        # epilogue, gives the same bits but measured 8-75% slower at M = 1024
-        # on the 2B shapes, dequant included.)
+    if m > _A8W8_GEMV_MAX_M and k % 128 == 0:
+        # Prefill: per-token quantisation, then the int8 matrix-core GEMM with
+        # the dequant in its epilogue (exact int32 accumulators; with
+        # return_acc the accumulators themselves, then the dequant kernel).
         _lib.call("q35_quant_act_i8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), m, k, _stream(x))
-        acc = torch._int_mm(xq, weight_q.t())
-        _lib.call("q35_dequant_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(), m,
-                  n, _stream(x))
-        if not return_acc:
+        if return_acc:
+            acc = torch.empty((m, n), device=x.device, dtype=torch.int32)
+            gemm_into(xq, weight_q, acc, GEMM_I32)
+            _lib.call("q35_dequant_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(),
+                      m, n, _stream(x))
+        else:
             acc = None
+            gemm_into(xq, weight_q, y, GEMM_DEQUANT, s_x=sx, s_w=sw)
     else:
         acc = torch.empty((m, n), device=x.device, dtype=torch.int32) if return_acc else None
         _lib.call("q35_gemv_a8w8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), weight_q.data_ptr(),
@@ -1206,7 +1235,7 @@ def a8w8_swiglu(x: torch.Tensor, weight_q: torch.Tensor, weight_scale: torch.Ten
         raise ValueError("packed A8W8 SwiGLU weight must be int8 [2N, K] matching the input")
     x2 = x.reshape(-1, k)
     m, n = x2.shape[0], n2 // 2
-    if m <= _A8W8_GEMV_MAX_M or n % 8 or k % 8:
+    if m <= _A8W8_GEMV_MAX_M or k % 128:
         return silu_and_mul(a8w8_linear(x, weight_q, weight_scale))
     if not x.is_cuda or not weight_q.is_contiguous():
         raise ValueError("A8W8 tensors must be contiguous GPU tensors")
@@ -1219,21 +1248,21 @@ def a8w8_swiglu(x: torch.Tensor, weight_q: torch.Tensor, weight_scale: torch.Ten
     sx = torch.empty((m, 1), device=x.device, dtype=torch.float32)
     _lib.call("q35_quant_act_i8", x2.data_ptr(), xq.data_ptr(), sx.data_ptr(), m, k, _stream(x))
     y = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_BF16)
-    acc = torch._int_mm(xq, weight_q.t())
-    _lib.call("q35_dequant_swiglu_i32", acc.data_ptr(), sx.data_ptr(), sw.data_ptr(), y.data_ptr(), m,
-              n, _stream(x))
+    gemm_into(xq, weight_q, y.view(m, n), GEMM_DEQUANT_SWIGLU, s_x=sx, s_w=sw)
     return y
 
 
 @_device_checked
 def a8w8_int_gemm(xq: torch.Tensor, weight_q: torch.Tensor) -> torch.Tensor:
-    """Exact int32 ``xq . Wq^T`` for prefill int8 activations ``[..., K]``
-    (the ROCm library's int8 GEMM): ``[rows, N]`` int32."""
+    """Exact int32 ``xq . Wq^T`` for prefill int8 activations ``[..., K]`` on
+    the int8 matrix-core GEMM: ``[rows, N]`` int32 (the int8 GEMM of reference
+    explore_runtime_quantization.py:173-180)."""
 
-    k = xq.shape[-1]
-    if xq.dtype != torch.int8 or weight_q.dtype != torch.int8 or weight_q.shape[1] != k:
-        raise ValueError("int8 GEMM operands must be int8 [M,K] and [N,K]")
-    return torch._int_mm(xq.reshape(-1, k).contiguous(), weight_q.t())
+    x2, n = _gemm_operands(xq, weight_q, torch.int8, False)
+    acc = torch.empty((x2.shape[0], n), device=xq.device, dtype=torch.int32)
+    if x2.shape[0]:
+        gemm_into(x2, weight_q, acc, GEMM_I32)
+    return acc
 
 
 @_device_checked
@@ -1311,19 +1340,6 @@ def dequant_swiglu_quant(acc: torch.Tensor, x_scale: torch.Tensor,
     return yq, sy
 
 
-def _gemm_a8w8_into(xq, sx, weight_q, sw, y, *, swiglu, plan) -> None:
-    m, k = xq.shape
-    n = weight_q.shape[0] // 2 if swiglu else weight_q.shape[0]
-    tile, splits = plan if plan is not None else (-1, 1)
-    lib = _lib.load()
-    nbytes = lib.q35_gemm_a8w8_workspace(m, n, k, int(swiglu), tile, splits)
-    if nbytes < 0:
-        raise ValueError(f"invalid GEMM plan {plan}")
-    ws = torch.empty(nbytes // 4, device=xq.device, dtype=torch.float32) if nbytes > 0 else None
-    _lib.call("q35_gemm_a8w8", xq.data_ptr(), sx.data_ptr(), weight_q.data_ptr(), sw.data_ptr(),
-              y.data_ptr(), m, n, k, int(swiglu), tile, splits, _lib.ptr(ws), nbytes, _stream(xq))
-
-
 @_device_checked
 def gemm_a8w8(xq: torch.Tensor, x_scale: torch.Tensor, weight_q: torch.Tensor,
               weight_scale: torch.Tensor, *, swiglu: bool = False,
@@ -1332,26 +1348,21 @@ def gemm_a8w8(xq: torch.Tensor, x_scale: torch.Tensor, weight_q: torch.Tensor,
     ``bf16(float(xq . Wq^T) * s_x[m] * s_w[n])`` (exact int32 accumulators,
     the dequant of reference explore_runtime_quantization.py:173-180), or with
     ``swiglu`` the SwiGLU of a packed ``[gate; up]`` int8 weight on the
-    dequantised bf16 gate and up. K must be a multiple of 256. ``plan`` =
-    (tile shape 0-3, K splits) overrides the library's choice."""
+    dequantised bf16 gate and up. K must be a multiple of 128. ``plan`` =
+    (tile 0-3, K splits) overrides the library's choice."""
 
-    if xq.dtype != torch.int8 or weight_q.dtype != torch.int8 or xq.ndim != 2 or weight_q.ndim != 2:
-        raise ValueError("int8 GEMM operands must be int8 [M,K] and [N,K]")
-    m, k = xq.shape
-    if weight_q.shape[1] != k or k % 256:
-        raise ValueError("int8 GEMM needs matching K, a multiple of 256")
-    if swiglu and weight_q.shape[0] % 2:
-        raise ValueError("packed SwiGLU weight must have an even number of rows")
-    if not (xq.is_contiguous() and weight_q.is_contiguous()):
-        raise ValueError("int8 GEMM operands must be contiguous")
+    if xq.ndim != 2:
+        raise ValueError("int8 GEMM activations must be [M, K]")
+    x2, n = _gemm_operands(xq, weight_q, torch.int8, swiglu)
+    m = x2.shape[0]
     sx = x_scale.reshape(-1).float().contiguous()
     sw = weight_scale.reshape(-1).float().contiguous()
     if sx.numel() != m or sw.numel() != weight_q.shape[0]:
         raise ValueError("int8 GEMM scales: one per token row and one per weight row")
-    n = weight_q.shape[0] // 2 if swiglu else weight_q.shape[0]
     y = torch.empty((m, n), device=xq.device, dtype=_BF16)
     if m:
-        _gemm_a8w8_into(xq, sx, weight_q, sw, y, swiglu=swiglu, plan=plan)
+        gemm_into(x2, weight_q, y, GEMM_DEQUANT_SWIGLU if swiglu else GEMM_DEQUANT, s_x=sx, s_w=sw,
+                  plan=plan)
     return y
 
 

@@ -799,19 +799,22 @@ def test_gemm_bf16(gpu, m, n, k):
     close(y, (x.float() @ w.float().t()).to(BF))
 
 
-@pytest.mark.parametrize("tile,splits", [(0, 1), (1, 1), (1, 2), (1, 3), (2, 1), (2, 2), (3, 1),
-                                         (3, 4), (1, 6)])
+_STAGE_BYTES = {0: 128, 1: 128, 2: 128, 3: 128, 4: 64, 5: 128, 6: 128}
+
+
+@pytest.mark.parametrize("tile,splits", [(0, 1), (4, 1), (5, 1), (1, 1), (1, 2), (1, 3), (1, 8),
+                                         (2, 1), (2, 2), (2, 4), (3, 1), (3, 3), (6, 1), (6, 2)])
 @pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (300, 700, 1536)])
 def test_gemm_bf16_split_plans(gpu, tile, splits, m, n, k):
     """Every tile shape with K split over workgroups (the last one to finish a
     tile sums the partials): the fp32 product within the bf16 bar, ragged
     tiles included; the same launch twice in a row and three graph replays
-    give identical bits (the arrival counters reset themselves and the split
-    order of the sum is fixed)."""
+    give identical bits (the arrival counters in the workspace reset
+    themselves and the split order of the sum is fixed)."""
     from ppu_amd import kernels as K
 
-    if (k // 64) % (2 * splits):
-        pytest.skip("K / 64 must split into pairs of stages")
+    if (2 * k // _STAGE_BYTES[tile]) % splits:
+        pytest.skip("the stage count must divide into the splits")
     g = gen(KERNEL_SEED + 92)
     x, w = randn(g, m, k), randn(g, n, k, scale=0.02)
     xg, wg = x.to(gpu), w.to(gpu)
@@ -829,12 +832,36 @@ def test_gemm_bf16_split_plans(gpu, tile, splits, m, n, k):
         assert torch.equal(y3, y1)
 
 
+def test_gemm_rejects_invalid_plans(gpu):
+    """Split K is refused for the 256x192 tiles and for SwiGLU kinds, and for a
+    split that does not divide the stage count; the direct-store tiles refuse
+    the dequant and SwiGLU kinds; a K that is not a multiple of the stage
+    width is refused before any launch."""
+    from ppu_amd import kernels as K
+
+    x = torch.zeros(64, 2048, dtype=BF, device=gpu)
+    w = torch.zeros(256, 2048, dtype=BF, device=gpu)
+    for plan in ((0, 2), (4, 2), (5, 2), (1, 5), (7, 1)):
+        with pytest.raises((ValueError, RuntimeError)):
+            K.gemm_bf16(x, w, plan=plan)
+    with pytest.raises((ValueError, RuntimeError)):
+        K.gemm_bf16(x, w, swiglu=True, plan=(1, 2))
+    with pytest.raises((ValueError, RuntimeError)):
+        K.gemm_bf16(x, w, swiglu=True, plan=(5, 1))
+    with pytest.raises(ValueError):
+        K.gemm_bf16(x[:, :96].contiguous(), w[:, :96].contiguous())
+
+
+_EXACT_CACHE: dict = {}
+
+
 def _exact_i8_product(xq, wq):
     """int8 x int8 dot products summed exactly (|sum| < 2^53 in float64)."""
     return (xq.cpu().double() @ wq.cpu().double().t()).to(torch.int64)
 
 
-@pytest.mark.parametrize("plan", [None, (0, 1), (1, 1), (1, 2), (2, 1), (2, 2), (3, 1), (3, 4)])
+@pytest.mark.parametrize("plan", [None, (0, 1), (4, 1), (1, 1), (1, 2), (1, 4), (2, 1), (2, 2),
+                                  (3, 1), (3, 4)])
 @pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (300, 1000, 2048), (17, 200, 256)])
 def test_gemm_a8w8(gpu, plan, m, n, k):
     """int8 matrix-core GEMM with the dequant epilogue: bit-exact against the
@@ -843,8 +870,8 @@ def test_gemm_a8w8(gpu, plan, m, n, k):
     replays give the same bits."""
     from ppu_amd import kernels as K
 
-    if plan is not None and (k // 128) % (2 * plan[1]):
-        pytest.skip("K / 128 must split into pairs of stages")
+    if plan is not None and (k // _STAGE_BYTES[plan[0]]) % plan[1]:
+        pytest.skip("the stage count must divide into the splits")
     g = gen(KERNEL_SEED + 93)
     w, x = randn(g, n, k, scale=0.02), randn(g, m, k)
     x[m // 2] = 0  # a zero row: scale 0, output 0
@@ -867,7 +894,39 @@ def test_gemm_a8w8(gpu, plan, m, n, k):
         assert torch.equal(y3, y1)
 
 
-@pytest.mark.parametrize("plan", [None, (0, 1), (2, 1), (3, 1)])
+@pytest.mark.parametrize("plan", [None, (0, 1), (4, 1), (5, 1), (1, 2), (2, 3), (3, 8), (6, 2)])
+@pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (1024, 8320, 2048), (33, 520, 1024)])
+def test_int8_gemm_int32_exact(gpu, plan, m, n, k):
+    """The int8 GEMM's int32 accumulators (what the A8W8 prefill hands to the
+    fused dequant kernels) equal the exact integer product, split plans
+    included; graph replays give the same values."""
+    from ppu_amd import kernels as K
+
+    if plan is not None and (k // _STAGE_BYTES[plan[0]]) % plan[1]:
+        pytest.skip("the stage count must divide into the splits")
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 97)
+    xq = torch.randint(-128, 128, (m, k), device=gpu, dtype=torch.int8, generator=g)
+    wq = torch.randint(-127, 128, (n, k), device=gpu, dtype=torch.int8, generator=g)
+    if (m, n, k) not in _EXACT_CACHE:  # the same seeded operands for every plan
+        _EXACT_CACHE[(m, n, k)] = _exact_i8_product(xq, wq)
+    exp = _EXACT_CACHE[(m, n, k)]
+    acc = torch.empty((m, n), device=gpu, dtype=torch.int32)
+    K.gemm_into(xq, wq, acc, K.GEMM_I32, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(acc.cpu().to(torch.int64), exp)
+    if plan is None:
+        assert torch.equal(K.a8w8_int_gemm(xq, wq), acc)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        K.gemm_into(xq, wq, acc, K.GEMM_I32, plan=plan)
+    for _ in range(2):
+        acc.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(acc.cpu().to(torch.int64), exp)
+
+
+@pytest.mark.parametrize("plan", [None, (0, 1), (4, 1), (2, 1), (3, 1)])
 @pytest.mark.parametrize("m,n,k", [(1024, 6144, 2048), (200, 504, 2048)])
 def test_gemm_a8w8_swiglu(gpu, plan, m, n, k):
     """Packed gate/up int8 GEMM with dequant + SwiGLU in the epilogue: the same
