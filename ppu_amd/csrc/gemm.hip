@@ -153,7 +153,7 @@ Q35_DEV int swz(int r) {
   return RB == 64 ? (r >> 2) & 3 : (r >> 1) & 7;
 }
 
-template <int WM, int WN, int FM, int FN, int RB, int NS, int KIND, bool SPLIT, bool STAGED>
+template <int WM, int WN, int FM, int FN, int RB, int NSA, int NSB, bool ROT, int KIND, bool SPLIT, bool STAGED>
 __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
   constexpr bool I8 = kind_i8(KIND);
   constexpr bool SWIGLU = kind_swiglu(KIND);
@@ -163,8 +163,11 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
   constexpr int RPG = 1024 / RB;             // tile rows per 1 KiB DMA group
   constexpr int CPR = RB / 16;               // 16-byte chunks per row and stage
   constexpr int GA = TM / RPG, GB = TN / RPG;
-  constexpr int LPW = (GA + GB) / 4;         // DMA instructions per wave and stage
-  constexpr int STAGE = (TM + TN) * RB;      // LDS bytes per stage
+  constexpr int LA = GA / 4, LB = GB / 4;    // DMA instructions per wave and stage (A, B)
+  constexpr int LPW = LA + LB;
+  constexpr int ASTAGE = TM * RB, BSTAGE = TN * RB;  // LDS bytes per stage of A and of B
+  constexpr int ABYTES = NSA * ASTAGE;       // the A ring, then the B ring
+  constexpr int LDSB = ABYTES + NSB * BSTAGE;
   constexpr int T = RB / 32;                 // MFMA k steps per stage
   constexpr int NMF = FM * FN;               // MFMAs per k step
   constexpr int NR = FM + FN;                // fragment reads per k step
@@ -173,12 +176,12 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
   static_assert(GA % 4 == 0 && GB % 4 == 0, "every wave issues the same DMA groups of A and B");
   static_assert(T % 2 == 0, "fragment register sets alternate between k steps");
   static_assert(!SWIGLU || WN == 2, "SwiGLU pairs the gate waves with the up waves");
-  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "stage ring fits the LDS");
+  static_assert(NSA >= 2 && NSB >= NSA && LDSB <= 160 * 1024, "the stage rings fit the LDS");
   static_assert(LPW <= (T - 1) * NMF, "the refill fits the MFMA slots of the first steps");
   static_assert(STAGED || KIND == KIND_BF16 || KIND == KIND_I32, "direct stores: bf16 and int32 kinds");
   using AccT = typename GemmAcc<I8>::T;
   using EltT = typename GemmAcc<I8>::E;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -200,8 +203,8 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
   const int tile = tn * mt + tm;
   const int m0 = tm * TM, n0 = tn * NC;
   const int nk = a.kps;  // stages of this workgroup
-  // K rotation: the workgroups sharing rows start at different stages
-  const int krot = ((tm % 4) * nk / 4 + (tn & 7) * nk / 32) % nk;
+  // K rotation (ROT): the workgroups sharing rows start at different stages
+  const int krot = ROT ? ((tm % 4) * nk / 4 + (tn & 7) * nk / 32) % nk : 0;
   const uint32_t rowb = (uint32_t)a.K * ES;
   // dequant kinds: the tile's row scales s_x[m0 ..] and column scales s_w[..]
   // (SwiGLU: gate then up columns), loaded now and published through LDS in
@@ -242,12 +245,14 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
     voff[i] = (uint32_t)grow * rowb + (uint32_t)(ks * nk) * RB + 16u * c;
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_offset(lds) + (uint32_t)w * 1024u);
-  // instruction i of the DMA of stage kt into buffer buf
-  auto dma = [&](int kt, int buf, int i) {
+  // instruction i of the DMA of stage kt: A (i < LA) into A buffer abuf, B into B buffer bbuf
+  auto dma = [&](int kt, int abuf, int bbuf, int i) {
     int ksr = kt + krot;
     if (ksr >= nk) ksr -= nk;
-    const uint8_t* src = (i < GA / 4 ? a.A : a.B) + (size_t)ksr * RB;
-    dma16(lds0 + (uint32_t)buf * STAGE + 4096u * i, src, voff[i]);
+    if (i < LA)
+      dma16(lds0 + (uint32_t)abuf * ASTAGE + 4096u * i, a.A + (size_t)ksr * RB, voff[i]);
+    else
+      dma16(lds0 + ABYTES + (uint32_t)bbuf * BSTAGE + 4096u * (i - LA), a.B + (size_t)ksr * RB, voff[i]);
   };
 
   // ---- fragment sources: row l32 of each 32-row block, logical chunk 2t + kh
@@ -257,18 +262,19 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
   for (int t = 0; t < T; ++t) {
     const uint32_t co = 16u * (uint32_t)((2 * t + kh) ^ swz<RB>(l32));
     fa[t] = (uint32_t)(wm * FM * 32 + l32) * RB + co;
-    fb[t] = (uint32_t)(TM + wn * FN * 32 + l32) * RB + co;
+    fb[t] = (uint32_t)(wn * FN * 32 + l32) * RB + co;
   }
   q35_u32x4 ra[2][FM], rb[2][FN];
   // fragment r of step t in the order the MFMAs consume them: A0, B0 .. B(FN-1), A1 ..
-  auto read1 = [&](int buf, int t, int set, int r) {
-    const uint8_t* base = lds + buf * STAGE;
+  auto read1 = [&](int abuf, int bbuf, int t, int set, int r) {
+    const uint8_t* pa = lds + abuf * ASTAGE;
+    const uint8_t* pb = lds + ABYTES + bbuf * BSTAGE;
     if (r == 0) {
-      ra[set][0] = *reinterpret_cast<const q35_u32x4*>(base + fa[t]);
+      ra[set][0] = *reinterpret_cast<const q35_u32x4*>(pa + fa[t]);
     } else if (r <= FN) {
-      rb[set][r - 1] = *reinterpret_cast<const q35_u32x4*>(base + fb[t] + (r - 1) * 32 * RB);
+      rb[set][r - 1] = *reinterpret_cast<const q35_u32x4*>(pb + fb[t] + (r - 1) * 32 * RB);
     } else {
-      ra[set][r - FN] = *reinterpret_cast<const q35_u32x4*>(base + fa[t] + (r - FN) * 32 * RB);
+      ra[set][r - FN] = *reinterpret_cast<const q35_u32x4*>(pa + fa[t] + (r - FN) * 32 * RB);
     }
   };
 
@@ -283,34 +289,48 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
     acc[q / FN][q % FN] = mfma32(ra[set][q / FN], rb[set][q % FN], acc[q / FN][q % FN]);
   };
 
-  // ---- prologue: stages 0 .. NS-2 in flight, stage 0 landed, its first fragments read
+  // ---- prologue: A stages 0 .. NSA-2 and B stages 0 .. NSB-2 in flight (A
+  // before B of the same stage, as in the loop), stage 0 landed, its first
+  // fragments read
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
+  for (int s = 0; s < NSB - 1; ++s) {
+    if (s < NSA - 1 && s < nk)
+#pragma unroll
+      for (int i = 0; i < LA; ++i) dma(s, s, 0, i);
     if (s < nk)
 #pragma unroll
-      for (int i = 0; i < LPW; ++i) dma(s, s, i);
-  if (nk >= NS - 1) wait_vm<(NS - 2) * LPW>();
+      for (int i = LA; i < LPW; ++i) dma(s, 0, s, i);
+  }
+  // issued after stage 0's B: (NSB - 2) later B stages and (NSA - 2) later A stages
+  if (nk >= NSB - 1) wait_vm<(NSB - 2) * LB + (NSA - 2) * LA>();
   else wait_vm<0>();
   ring_barrier();
 #pragma unroll
-  for (int r = 0; r < NR; ++r) read1(0, 0, 0, r);
+  for (int r = 0; r < NR; ++r) read1(0, 0, 0, 0, r);
 
-  // One stage. REFILL: the buffer of stage kt - 1 is refilled with stage
-  // kt + NS - 1 (every stage but the last NS - 1).
-  int buf = 0;
-  auto stage = [&](int kt, auto refill_tag) {
-    constexpr bool REFILL = decltype(refill_tag)::value;
-    const int rbuf = buf == 0 ? NS - 1 : buf - 1;  // buffer of stage kt - 1
+  // One stage. RA / RB: the A / B buffer of stage kt - 1 is refilled with
+  // stage kt + NSA - 1 / kt + NSB - 1 (A refills stop NSA - 1 stages before
+  // the end, B refills NSB - 1).
+  // Wait before the barrier, steady state: stage kt + 1's last load is its A
+  // (issued at stage kt + 2 - NSA) when NSA < NSB, else its B; the loads
+  // issued after it are then LB + (NSA - 2) (LA + LB), or (NSA - 2) (LA + LB).
+  constexpr int WAITN = (NSA < NSB ? LB : 0) + (NSA - 2) * LPW;
+  int abuf = 0, bbuf = 0;
+  auto stage = [&](int kt, auto ra_tag, auto rb_tag) {
+    constexpr bool RA = decltype(ra_tag)::value, RB_ = decltype(rb_tag)::value;
+    const int rabuf = abuf == 0 ? NSA - 1 : abuf - 1;  // buffers of stage kt - 1
+    const int rbbuf = bbuf == 0 ? NSB - 1 : bbuf - 1;
     // steps 0 .. T-2: one MFMA, one fragment read of the next step, and
-    // (first steps) the DMA refill, per slot
+    // (first steps) the DMA refills, per slot
 #pragma unroll
     for (int t = 0; t < T - 1; ++t) {
 #pragma unroll
       for (int q = 0; q < NMF; ++q) {
         mfma(t & 1, q);
-        if (q < NR) read1(buf, t + 1, (t + 1) & 1, q);
+        if (q < NR) read1(abuf, bbuf, t + 1, (t + 1) & 1, q);
         const int slot = t * NMF + q;
-        if (REFILL && slot < LPW) dma(kt + NS - 1, rbuf, slot);
+        if (RA && slot < LA) dma(kt + NSA - 1, rabuf, 0, slot);
+        if (RB_ && slot >= LA && slot < LPW) dma(kt + NSB - 1, 0, rbbuf, slot);
         Q35_PIN();
       }
     }
@@ -322,12 +342,13 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
       mfma(cur, q);
       Q35_PIN();
     }
-    const int nbuf = buf + 1 == NS ? 0 : buf + 1;
+    const int nabuf = abuf + 1 == NSA ? 0 : abuf + 1;
+    const int nbbuf = bbuf + 1 == NSB ? 0 : bbuf + 1;
     const bool more = kt + 1 < nk;
     wait_lds();  // on both paths, so the second half waits for nothing
     if (more) {
       // stage kt + 1 landed: this wave's part (vmcnt), then every wave's
-      if (REFILL) wait_vm<(NS - 2) * LPW>();
+      if (RA && RB_) wait_vm<WAITN>();
       else wait_vm<0>();
       ring_barrier();
     }
@@ -338,15 +359,17 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
       if (more) {
         const int s = q - H;
 #pragma unroll
-        for (int r = s * NR / (NMF - H); r < (s + 1) * NR / (NMF - H); ++r) read1(nbuf, 0, cur ^ 1, r);
+        for (int r = s * NR / (NMF - H); r < (s + 1) * NR / (NMF - H); ++r) read1(nabuf, nbbuf, 0, cur ^ 1, r);
       }
       Q35_PIN();
     }
-    buf = nbuf;
+    abuf = nabuf;
+    bbuf = nbbuf;
   };
   int kt = 0;
-  for (; kt + NS - 1 < nk; ++kt) stage(kt, BoolTag<true>{});
-  for (; kt < nk; ++kt) stage(kt, BoolTag<false>{});
+  for (; kt + NSB - 1 < nk; ++kt) stage(kt, BoolTag<true>{}, BoolTag<true>{});
+  for (; kt + NSA - 1 < nk; ++kt) stage(kt, BoolTag<true>{}, BoolTag<false>{});
+  for (; kt < nk; ++kt) stage(kt, BoolTag<false>{}, BoolTag<false>{});
 
   // ---- split K: partial tiles, arrival count, the last workgroup sums
   if constexpr (SPLIT) {
@@ -460,7 +483,7 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
     constexpr int ITER = PR * CPRW / 256;      // chunks per thread and phase
     constexpr int SCO = PR * SB;               // LDS offset of the scales
     static_assert(PR * CPRW % 256 == 0, "the chunks divide over the workgroup");
-    static_assert(SCO + NSC * 4 <= NS * STAGE, "the staged tile and scales fit the ring");
+    static_assert(SCO + NSC * 4 <= LDSB, "the staged tile and scales fit the rings");
     const bool vec = (a.N & 7) == 0;
     float* sc = reinterpret_cast<float*>(lds + SCO);
     wait_lds();
@@ -557,28 +580,31 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
 
 // ---------------------------------------------------------------- plans
 // Tile shapes (waves 2 x 2; FM x FN blocks of 32 x 32 per wave; RB bytes per
-// row and stage; NS stages in the ring; LDS = NS (TM + TN) RB; epilogue
-// staged through LDS, or direct stores for the bf16 / int32 kinds):
-//   0: 256 x 192 (4 x 3), RB 128, NS 2, staged  (112 KiB)
-//   1: 128 x 128 (2 x 2), RB 128, NS 4, staged  (128 KiB)
-//   2: 256 x 128 (4 x 2), RB 128, NS 3, staged  (144 KiB)
-//   3: 128 x 192 (2 x 3), RB 128, NS 4, staged  (160 KiB)
-//   4: 256 x 192 (4 x 3), RB 64,  NS 4, staged  (112 KiB)
-//   5: tile 0 with direct stores; 6: tile 1 with direct stores
-#define Q35_GEMM_TILES(X)           \
-  X(0, 2, 2, 4, 3, 128, 2, true)    \
-  X(1, 2, 2, 2, 2, 128, 4, true)    \
-  X(2, 2, 2, 4, 2, 128, 3, true)    \
-  X(3, 2, 2, 2, 3, 128, 4, true)    \
-  X(4, 2, 2, 4, 3, 64, 4, true)     \
-  X(5, 2, 2, 4, 3, 128, 2, false)   \
-  X(6, 2, 2, 2, 2, 128, 4, false)
-constexpr int kTiles = 7;
-constexpr int kTM[kTiles] = {256, 128, 256, 128, 256, 256, 128};
-constexpr int kTN[kTiles] = {192, 128, 128, 192, 192, 192, 128};
-constexpr int kRB[kTiles] = {128, 128, 128, 128, 64, 128, 128};
-constexpr bool kStaged[kTiles] = {true, true, true, true, true, false, false};
-constexpr bool kSplitOk[kTiles] = {false, true, true, true, false, false, true};  // up to 8 blocks per wave
+// row and stage; NSA / NSB stages in the A / B rings; LDS = NSA TM RB + NSB
+// TN RB; K rotation; epilogue staged through LDS, or direct stores for the
+// bf16 / int32 kinds):
+//   0: 256 x 192 (4 x 3), RB 128, NSA 2, NSB 4,       staged  (160 KiB)
+//   1: 128 x 128 (2 x 2), RB 128, NSA 4, NSB 6, rot,  staged  (160 KiB)
+//   2: 256 x 128 (4 x 2), RB 128, NSA 2, NSB 4,       staged  (128 KiB)
+//   3: 128 x 192 (2 x 3), RB 128, NSA 4, NSB 4, rot,  staged  (160 KiB)
+//   4: 256 x 192 (4 x 3), RB 128, NSA 2, NSB 2,       staged  (112 KiB)
+//   5: tile 0 with direct stores; 6: tile 1 with direct stores; 7: tile 6
+//   without K rotation
+#define Q35_GEMM_TILES(X)                     \
+  X(0, 2, 2, 4, 3, 128, 2, 4, false, true)    \
+  X(1, 2, 2, 2, 2, 128, 4, 6, true, true)     \
+  X(2, 2, 2, 4, 2, 128, 2, 4, false, true)    \
+  X(3, 2, 2, 2, 3, 128, 4, 4, true, true)     \
+  X(4, 2, 2, 4, 3, 128, 2, 2, false, true)    \
+  X(5, 2, 2, 4, 3, 128, 2, 4, false, false)   \
+  X(6, 2, 2, 2, 2, 128, 4, 6, true, false)    \
+  X(7, 2, 2, 2, 2, 128, 4, 6, false, false)
+constexpr int kTiles = 8;
+constexpr int kTM[kTiles] = {256, 128, 256, 128, 256, 256, 128, 128};
+constexpr int kTN[kTiles] = {192, 128, 128, 192, 192, 192, 128, 128};
+constexpr int kRB[kTiles] = {128, 128, 128, 128, 128, 128, 128, 128};
+constexpr bool kStaged[kTiles] = {true, true, true, true, true, false, false, false};
+constexpr bool kSplitOk[kTiles] = {false, true, true, true, false, false, true, true};  // up to 8 blocks per wave
 constexpr int kMaxSplits = 8;
 
 long long tiles_of(int tile, int M, int N, int kind) {
@@ -619,7 +645,7 @@ void plan(int M, int N, int K, int kind, int* tile, int* splits) {
   }
 }
 
-template <int WM, int WN, int FM, int FN, int RB, int NS, int KIND, bool STAGED>
+template <int WM, int WN, int FM, int FN, int RB, int NSA, int NSB, bool ROT, int KIND, bool STAGED>
 int launch_one(const GemmArgs& a, hipStream_t stream) {
   if constexpr (!STAGED && KIND != KIND_BF16 && KIND != KIND_I32) {
     return (int)hipErrorInvalidValue;  // direct stores: bf16 and int32 kinds
@@ -632,10 +658,10 @@ int launch_one(const GemmArgs& a, hipStream_t stream) {
     if constexpr (kind_swiglu(KIND) || FM * FN > 8) {
       return (int)hipErrorInvalidValue;  // split K: tiles of up to 8 blocks per wave, no SwiGLU
     } else {
-      gemm_ring<WM, WN, FM, FN, RB, NS, KIND, true, STAGED><<<(unsigned)units, 256, 0, stream>>>(a);
+      gemm_ring<WM, WN, FM, FN, RB, NSA, NSB, ROT, KIND, true, STAGED><<<(unsigned)units, 256, 0, stream>>>(a);
     }
   } else {
-    gemm_ring<WM, WN, FM, FN, RB, NS, KIND, false, STAGED><<<(unsigned)units, 256, 0, stream>>>(a);
+    gemm_ring<WM, WN, FM, FN, RB, NSA, NSB, ROT, KIND, false, STAGED><<<(unsigned)units, 256, 0, stream>>>(a);
   }
   return q35_last_error();
   }
@@ -644,8 +670,8 @@ int launch_one(const GemmArgs& a, hipStream_t stream) {
 template <int KIND>
 int launch_tile(int tile, const GemmArgs& a, hipStream_t stream) {
   switch (tile) {
-#define Q35_GEMM_CASE(id, wm, wn, fm, fn, rb, ns, staged) \
-  case id: return launch_one<wm, wn, fm, fn, rb, ns, KIND, staged>(a, stream);
+#define Q35_GEMM_CASE(id, wm, wn, fm, fn, rb, nsa, nsb, rot, staged) \
+  case id: return launch_one<wm, wn, fm, fn, rb, nsa, nsb, rot, KIND, staged>(a, stream);
     Q35_GEMM_TILES(Q35_GEMM_CASE)
 #undef Q35_GEMM_CASE
     default: return (int)hipErrorInvalidValue;

@@ -799,11 +799,11 @@ def test_gemm_bf16(gpu, m, n, k):
     close(y, (x.float() @ w.float().t()).to(BF))
 
 
-_STAGE_BYTES = {0: 128, 1: 128, 2: 128, 3: 128, 4: 64, 5: 128, 6: 128}
+_STAGE_BYTES = {t: 128 for t in range(8)}
 
 
 @pytest.mark.parametrize("tile,splits", [(0, 1), (4, 1), (5, 1), (1, 1), (1, 2), (1, 3), (1, 8),
-                                         (2, 1), (2, 2), (2, 4), (3, 1), (3, 3), (6, 1), (6, 2)])
+                                         (2, 1), (2, 2), (2, 4), (3, 1), (3, 3), (6, 1), (6, 2), (7, 4)])
 @pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (300, 700, 1536)])
 def test_gemm_bf16_split_plans(gpu, tile, splits, m, n, k):
     """Every tile shape with K split over workgroups (the last one to finish a
@@ -841,7 +841,7 @@ def test_gemm_rejects_invalid_plans(gpu):
 
     x = torch.zeros(64, 2048, dtype=BF, device=gpu)
     w = torch.zeros(256, 2048, dtype=BF, device=gpu)
-    for plan in ((0, 2), (4, 2), (5, 2), (1, 5), (7, 1)):
+    for plan in ((0, 2), (4, 2), (5, 2), (1, 5), (8, 1)):
         with pytest.raises((ValueError, RuntimeError)):
             K.gemm_bf16(x, w, plan=plan)
     with pytest.raises((ValueError, RuntimeError)):
