@@ -166,6 +166,12 @@ int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace
  * streams at once) race. */
 int q35_lm_head_top1_noalloc(const void* W, const void* x, int V, int K, void* out,
                              void* advance, int n_advance, void* stream);
+/* Set-up of the current device for q35_lm_head_top1_noalloc: resolves this
+ * GPU's address of its fixed array (a runtime query). Call once per device,
+ * with that device current, before the first no-alloc call made under graph
+ * capture (otherwise the first call on a device resolves it). No counterpart
+ * in the reference. */
+int q35_init(void);
 /* The same index as q35_lm_head_top1 (replaces the same reference call,
  * qwen35_fused/kernels.py:1146), found with half the weight bytes: an int8
  * copy of W screens every row with a rigorous bound on the difference to the
@@ -181,6 +187,11 @@ int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, cons
                               const void* x, int V, int K, void* workspace,
                               long long workspace_bytes, void* out, void* advance, int n_advance,
                               void* stream);
+/* Where a screened top-1 workspace for vocabulary V keeps the number of rows
+ * each workgroup recomputed exactly (uint32 each, written by every call):
+ * returns the byte offset, *n the count. Their sum is the call's bf16 row
+ * reads beyond the int8 screen (for monitoring; no reference counterpart). */
+long long q35_lm_head_screened_counts(int V, int* n);
 
 /* ---- DeltaNet --------------------------------------------------------- */
 
@@ -341,13 +352,14 @@ int q35_dequant_swiglu_i32(const void* acc, const void* s_x, const void* s_w, vo
  *   4  int8, B = [gate; up] -> SwiGLU of the dequantised bf16 gate and up
  *      (q35_dequant_swiglu_i32's values)
  * s_x [M] and s_w [N] (kind 4: [2N]) fp32 are used by kinds 3 and 4 only.
- * K * (element bytes) must be a multiple of the tile's stage width (64 bytes
- * for tiles 0, 2, 3; 128 for tile 1); A and B 16-byte aligned; each operand
- * below 2^32 bytes. tile < 0 picks the library's plan (tile and K splits by
- * output shape); otherwise tile 0-3 (256x192, 128x128, 256x128, 128x192
- * outputs per workgroup; SwiGLU kinds: half as many output columns) with
- * `splits` workgroups per tile along K (1-8, dividing the stage count; tiles
- * 1-3 and kinds 0, 2, 3 only). A plan that splits K needs a workspace of
+ * K * (element bytes) must be a multiple of 128 (the stage width); A and B
+ * 16-byte aligned; each operand below 2^32 bytes (bf16: 2^31 elements).
+ * tile < 0 picks the library's plan (tile and K splits by output shape);
+ * otherwise tile 0-7 (outputs per workgroup: 0, 4, 5 256x192; 1, 6, 7
+ * 128x128; 2 256x128; 3 128x192; SwiGLU kinds: half as many output columns;
+ * 5-7 store from registers and take kinds 0 and 2 only) with `splits`
+ * workgroups per tile along K (1-8, dividing the stage count; tiles 1, 2,
+ * 3, 6, 7 and kinds 0, 2, 3 only). A plan that splits K needs a workspace of
  * q35_gemm_workspace bytes (arrival counters + partial tiles), zero-filled
  * before its first use; each launch leaves the counters at zero again (after
  * a launch that failed part way, zero it again). Two launches that overlap in

@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_lm_head_top1_workspace": (_L, [_I, _I]),
     "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),
     "q35_lm_head_top1_noalloc": (_I, [_P, _P, _I, _I, _P, _P, _I, _P]),
+    "q35_init": (_I, []),
     "q35_conv1d_update": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "q35_conv1d_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "q35_delta_decode": (
@@ -89,6 +90,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_dequant_swiglu_quant": (_I, [_P, _P, _P, _P, _P, _I, _I, _P]),
     "q35_lm_head_screen_prep": (_I, [_P, _I, _I, _P, _P, _P, _P]),
     "q35_lm_head_top1_screened_workspace": (_L, [_I, _I]),
+    "q35_lm_head_screened_counts": (_L, [_I, ctypes.POINTER(_I)]),
     "q35_lm_head_top1_screened": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),
 }
 
@@ -115,6 +117,10 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     version = lib.q35_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"libq35 ABI version {version}, expected {ABI_VERSION}")
+    if torch.cuda.is_available():
+        # per-device set-up (the no-alloc top-1's scratch address) before any
+        # call can be made under graph capture
+        check(lib.q35_init(), "q35_init")
     if path is None:
         _lib = lib
     return lib

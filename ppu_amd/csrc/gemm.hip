@@ -728,9 +728,9 @@ long long q35_gemm_workspace(int M, int N, int K, int kind, int tile, int splits
 
 // Prefill GEMM C = A . B^T of the given kind (0 bf16, 1 bf16 SwiGLU, 2 int8 ->
 // int32, 3 int8 -> bf16 dequant, 4 int8 SwiGLU; see gemm.hip's header).
-// K * element bytes a multiple of the tile's stage width; A and B 16-byte
+// K * element bytes a multiple of 128 (the stage width); A and B 16-byte
 // aligned; every operand below 2^32 bytes. tile < 0 picks the default plan,
-// otherwise tile 0-4 with `splits` K splits (the stage count divisible by
+// otherwise tile 0-7 with `splits` K splits (the stage count divisible by
 // splits). A split plan needs a workspace of q35_gemm_workspace bytes,
 // zero-filled before its first use.
 int q35_gemm(const void* A, const void* B, void* C, int M, int N, int K, int kind, const void* s_x,

@@ -824,9 +824,11 @@ __global__ __launch_bounds__(WV * 64) void lm_head_rescore(const uint16_t* __res
                                                            const float* __restrict__ U,
                                                            const float* __restrict__ lpart,
                                                            int nparts, int V,
-                                                           unsigned long long* __restrict__ cand) {
+                                                           unsigned long long* __restrict__ cand,
+                                                           unsigned* __restrict__ ncand) {
   constexpr int NCH = 4, K = 2048;
   __shared__ unsigned long long best_s[WV];
+  __shared__ unsigned count_s[WV];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   float xf[NCH][8];
 #pragma unroll
@@ -839,11 +841,13 @@ __global__ __launch_bounds__(WV * 64) void lm_head_rescore(const uint16_t* __res
   const int per = (V + nw - 1) / nw;
   const int r0 = min(V, w * per), r1 = min(V, r0 + per);
   uint64_t best = 0;
+  unsigned count = 0;  // rows this wave recomputes (wave-uniform)
   const uint8_t* wbase = reinterpret_cast<const uint8_t*>(W) + lane * 16;
   for (int base = r0; base < r1; base += 64) {
     const int row = base + lane;
     const bool is_cand = row < r1 && !(U[min(row, V - 1)] < lstar);
     uint64_t mask = __ballot(is_cand);
+    count += (unsigned)__builtin_popcountll(mask);
     while (mask) {
       int rows[4];
       int last = base;
@@ -876,24 +880,33 @@ __global__ __launch_bounds__(WV * 64) void lm_head_rescore(const uint16_t* __res
       }
     }
   }
-  if (lane == 0) best_s[wid] = best;
+  if (lane == 0) {
+    best_s[wid] = best;
+    count_s[wid] = count;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
     uint64_t b = best_s[0];
+    unsigned n = count_s[0];
 #pragma unroll
-    for (int v = 1; v < WV; ++v) b = u64_max(b, best_s[v]);
+    for (int v = 1; v < WV; ++v) {
+      b = u64_max(b, best_s[v]);
+      n += count_s[v];
+    }
     cand[blockIdx.x] = b;
+    ncand[blockIdx.x] = n;  // every workgroup writes its slot on every call
   }
 }
 
 constexpr int kScWV = 4, kScR = 2;
 // Workspace of the screened top-1: U [V] floats, then per workgroup one
-// float (max lower bound) and one 64-bit key, 256-byte aligned sections.
+// float (max lower bound), one 64-bit key and the number of rows it
+// recomputed (uint32), 256-byte aligned sections.
 long long screened_parts() { return (long long)lm_device_cus() * kLmBlocksPerCU; }
 long long align256(long long b) { return (b + 255) / 256 * 256; }
 long long screened_bytes(int V) {
   const long long nb = screened_parts();
-  return align256((long long)V * 4) + align256(nb * 4) + nb * 8;
+  return align256((long long)V * 4) + align256(nb * 4) + align256(nb * 8) + nb * 4;
 }
 
 // Scratch of q35_lm_head_top1_noalloc: the candidate keys of one top-1 call
@@ -1094,9 +1107,20 @@ long long q35_lm_head_top1_screened_workspace(int V, int K) {
   return screened_bytes(V);
 }
 
+// Byte offset and count of the per-workgroup recomputed-row counts (uint32)
+// in a screened top-1 workspace for vocabulary V: offset in the return
+// value, count in *n.
+long long q35_lm_head_screened_counts(int V, int* n) {
+  const long long nb = screened_parts();
+  if (n) *n = (int)nb;
+  return align256((long long)V * 4) + align256(nb * 4) + align256(nb * 8);
+}
+
 // out[0] = the index q35_lm_head_top1 returns for (W, x), found through the
 // int8 screen (Wq, s, c from q35_lm_head_screen_prep of this W) and the exact
-// recomputation of the rows it cannot exclude; `advance` as there.
+// recomputation of the rows it cannot exclude; `advance` as there. The
+// workspace's last section holds, per workgroup, how many rows it
+// recomputed (q35_lm_head_screened_candidates sums them).
 int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, const void* c,
                               const void* x, int V, int K, void* workspace,
                               long long workspace_bytes, void* out, void* advance, int n_advance,
@@ -1110,17 +1134,28 @@ int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, cons
   float* lpart = (float*)((char*)workspace + align256((long long)V * 4));
   unsigned long long* cand =
       (unsigned long long*)((char*)workspace + align256((long long)V * 4) + align256(nb * 4));
+  unsigned* ncand = (unsigned*)((char*)cand + align256(nb * 8));
   lm_head_screen<kScWV, kScR, 2><<<(unsigned)nb, kScWV * 64, 0, stream>>>(
       (const int8_t*)Wq, (const float*)s, (const float*)c, (const uint16_t*)x, V, U, lpart);
   int e = q35_last_error();
   if (e) return e;
   lm_head_rescore<kScWV><<<(unsigned)nb, kScWV * 64, 0, stream>>>(
-      (const uint16_t*)W, (const uint16_t*)x, U, lpart, (int)nb, V, cand);
+      (const uint16_t*)W, (const uint16_t*)x, U, lpart, (int)nb, V, cand, ncand);
   e = q35_last_error();
   if (e) return e;
   top1_final<<<1, 1024, 0, stream>>>(cand, (int)nb, (long long*)out, (long long*)advance,
                                      advance ? n_advance : 0);
   return q35_last_error();
+}
+
+// Set-up for the current device: resolves this GPU's address of `scratch`
+// (top1_scratch), so that no later call needs a runtime query. Once per
+// device, with that device current, before the first
+// q35_lm_head_top1_noalloc made under graph capture; the ppu_amd loader calls
+// it for the current device.
+int q35_init(void) {
+  void* p = nullptr;
+  return top1_scratch(&p);
 }
 
 // q35_lm_head_top1 without a workspace argument: the candidate keys go to

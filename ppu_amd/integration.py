@@ -65,7 +65,11 @@ class FusionConfig:
     a8w8: bool = False
     # greedy top-1 through an int8 screen of the lm_head plus an exact
     # recomputation of the rows it cannot exclude (same token, about half the
-    # bytes; 0.5 GB more device memory for the 2B vocabulary)
+    # bytes; 0.5 GB more device memory for the 2B vocabulary). Its cost grows
+    # with the rows the bound cannot exclude: lm_head_screen_candidates()
+    # counts them for a hidden state; past about V/4 (a quarter of the
+    # vocabulary) the screen reads more than 3/4 of the plain top-1's bytes
+    # and gains little, so switch it off for such weights
     lm_head_screen: bool = True
     # prefill of 64+ tokens: the DeltaNet causal conv computed inside the
     # chunk prep from the raw projection (one launch and one 12 MB
@@ -637,35 +641,20 @@ def _text_fast(stack, config: FusionConfig):
 
 
 # ----------------------------------------------------------------- vision
-def _vision_sdpa(q, k, v, scale: float, segments) -> torch.Tensor:
-    """Non-causal attention of ``[1, H, T, D]`` q/k/v, per image segment
-    (``None``: one image). Only the fused SDPA backends are allowed: the math
-    backend's batched bf16 product with a transposed key is kept off this GPU."""
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-
-    sdpa = torch.nn.functional.scaled_dot_product_attention
-    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-        if segments is None:
-            return sdpa(q, k, v, scale=scale)
-        return torch.cat([sdpa(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], scale=scale)
-                          for a, b in segments], dim=2)
-
-
-def _vision_attention(attn, x: torch.Tensor, cos, sin, segments) -> torch.Tensor:
+def _vision_attention(attn, x: torch.Tensor, cos, sin, cu) -> torch.Tensor:
     """One vision block's attention (reference integration.py:644-735): the
     packed QKV projection, the split + RoPE kernel straight into
     ``[1, heads, tokens, dim]``, non-causal attention per image on the
-    matrix-core kernel (``vision_attention``, head dims that are multiples of
-    8 up to 128; PyTorch's fused SDPA otherwise), output projection."""
-    tokens = x.shape[0]
+    matrix-core kernel (``vision_attention``: head dims that are multiples of
+    8 up to 128, Qwen3.5's 72 included; other head dims raise), output
+    projection. ``cu``: the images' int32 row bounds on the device (None for
+    one image), built once per call."""
+    if attn.head_dim % 8 or attn.head_dim > 128:
+        raise ValueError(f"the fused vision attention supports head dims that are multiples of 8 "
+                         f"up to 128, not {attn.head_dim}")
     packed = attn.qkv(x).contiguous()
     q, k, v = K.vision_qkv_rope(packed, cos, sin, heads=attn.num_heads, dim=attn.head_dim)
-    if attn.head_dim % 8 == 0 and attn.head_dim <= 128:
-        cu = None if segments is None else torch.tensor([0] + [b for _, b in segments],
-                                                        dtype=torch.int32, device=x.device)
-        return attn.proj(K.vision_attention(q, k, v, attn.scaling, cu))
-    out = _vision_sdpa(q, k, v, attn.scaling, segments)
-    return attn.proj(out.transpose(1, 2).reshape(tokens, -1).contiguous())
+    return attn.proj(K.vision_attention(q, k, v, attn.scaling, cu))
 
 
 def _patch_embed(visual, pixels: torch.Tensor) -> torch.Tensor:
@@ -753,7 +742,7 @@ def _vision_rotary(visual, position_ids: torch.Tensor) -> tuple[torch.Tensor, to
     return emb.cos().contiguous(), emb.sin().contiguous()
 
 
-def _vision_forward(visual, pixels, interp_indices, interp_weights, cos, sin, segments):
+def _vision_forward(visual, pixels, interp_indices, interp_weights, cos, sin, cu):
     """The whole tower for the patches of one call (reference
     integration.py:514-562 plus the patch embedding and the merger): position
     embedding, every block with the given rotary table (the residual stream
@@ -767,7 +756,7 @@ def _vision_forward(visual, pixels, interp_indices, interp_weights, cos, sin, se
     normed = K.layer_norm(hidden, n1.weight, n1.bias, n1.eps)
     residual = hidden
     for i, blk in enumerate(blocks):
-        update = _vision_attention(blk.attn, normed, cos, sin, segments)
+        update = _vision_attention(blk.attn, normed, cos, sin, cu)
         residual, mlp_in = K.residual_add_layer_norm(residual, update.contiguous(), blk.norm2.weight,
                                                      blk.norm2.bias, blk.norm2.eps)
         mlp_out = _vision_mlp(blk.mlp, mlp_in).contiguous()
@@ -808,21 +797,20 @@ _VISION_PRECOMPUTED = ("interp_indices", "interp_weights", "position_ids", "cu_s
 def _vision_prep(visual, grid_thw: torch.Tensor, kw: dict, device) -> tuple:
     """The tower's per-call inputs derived from ``grid_thw`` (Transformers'
     helpers, which take precomputed values out of ``kw`` when the caller
-    passed them): interpolation indices / weights, the image segments (None
-    for one image) and the rotary cos / sin of the position ids, on
-    ``device``."""
+    passed them): interpolation indices / weights, the images' int32 row
+    bounds (None for one image) and the rotary cos / sin of the position ids,
+    on ``device``."""
     idx, wts = qwen_impl.get_vision_interpolation_indices_and_weights(
         grid_thw, num_grid_per_side=visual.num_grid_per_side, mode=visual.interpolation_mode,
         align_corners=visual.interpolation_align_corners,
         spatial_merge_size=visual.config.spatial_merge_size, kwargs=kw)
     position_ids = qwen_impl.get_vision_position_ids(grid_thw, visual.spatial_merge_size, kwargs=kw)
     cu_seqlens, _ = qwen_impl.get_vision_attention_seqlens(grid_thw, visual.config, kwargs=kw)
-    segments = None
+    cu = None
     if cu_seqlens.numel() != 2:
-        bounds = cu_seqlens.tolist()
-        segments = list(zip(bounds[:-1], bounds[1:]))
+        cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
     cos, sin = _vision_rotary(visual, position_ids.to(device))
-    return idx.to(device).contiguous(), wts.to(device).contiguous(), segments, cos, sin
+    return idx.to(device).contiguous(), wts.to(device).contiguous(), cu, cos, sin
 
 
 def _vision_model_fast(visual, config: FusionConfig):
@@ -849,9 +837,9 @@ def _vision_model_fast(visual, config: FusionConfig):
                 prep = _vision_prep(visual, grid_thw, kw, device)
                 if len(preps) < 64:
                     preps[grid_key] = prep
-        idx, wts, segments, cos, sin = prep
+        idx, wts, cu, cos, sin = prep
         pixels = hidden_states.to(visual.patch_embed.proj.weight.dtype).contiguous()
-        single = segments is None
+        single = cu is None
         key = (tuple(pixels.shape), wts.dtype, grid_key)
         entry = graphs.get(key) if config.vision_graph and single else None
         if entry is not None:
@@ -859,7 +847,7 @@ def _vision_model_fast(visual, config: FusionConfig):
             # caller handed in its own.
             hidden, merged = entry.run(pixels, *((idx, wts, cos, sin) if given else ()))
         else:
-            hidden, merged = _vision_forward(visual, pixels, idx, wts, cos, sin, segments)
+            hidden, merged = _vision_forward(visual, pixels, idx, wts, cos, sin, cu)
             if (config.vision_graph and single and len(graphs) < config.vision_graph_max_entries
                     and not torch.cuda.is_current_stream_capturing()):
                 graphs[key] = _VisionGraph(visual, pixels, idx, wts, cos, sin)
@@ -939,6 +927,19 @@ def lm_head_screen(model: torch.nn.Module):
     if (w.data_ptr(), w._version) != getattr(lm, "_q35_screen_of", None) or wq.device != w.device:
         return None
     return wq, lm.q35_screen_s, lm.q35_screen_c
+
+
+def lm_head_screen_candidates(model: torch.nn.Module, hidden: torch.Tensor) -> int | None:
+    """How many lm_head rows the screened top-1 recomputes in bf16 for the
+    final hidden state ``hidden`` ([1, 2048] or [2048]) of ``model``: the
+    bytes it reads are the int8 copy plus 4 KB per such row. None without
+    installed screen operands."""
+    screen = lm_head_screen(model)
+    if screen is None:
+        return None
+    _, n = K.lm_head_argmax(hidden.reshape(1, -1), model.lm_head.weight, screen=screen,
+                            return_candidates=True)
+    return int(n)
 
 
 def apply_fusions(model: torch.nn.Module, config: FusionConfig | None = None) -> dict[str, int]:

@@ -591,7 +591,8 @@ def lm_head_argmax(
     out: torch.Tensor | None = None,
     advance: torch.Tensor | None = None,
     screen: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
-) -> torch.Tensor:
+    return_candidates: bool = False,
+):
     """Greedy token id without materialising logits. reference kernels.py:1146.
 
     ``out`` (int64, one element) receives the token instead of a new tensor;
@@ -600,7 +601,9 @@ def lm_head_argmax(
     reference graph.py:78-79 without extra kernels. ``screen`` (the tensors
     ``lm_head_screen_prep`` made from this ``weight``) finds the same index
     through an int8 copy of the weight and an exact recomputation of the rows
-    the screen cannot exclude (about half the bytes read).
+    the screen cannot exclude (about half the bytes read); with
+    ``return_candidates`` it returns ``(token, rows recomputed)``, the second
+    an int64 device scalar (the bf16 rows read beyond the int8 screen).
     """
 
     if hidden.shape != (1, weight.shape[1]) or hidden.dtype != torch.bfloat16:
@@ -635,10 +638,19 @@ def lm_head_argmax(
         if advance.dtype != torch.int64 or not advance.is_contiguous() or advance.numel() > 64:
             raise ValueError("advance must be a contiguous int64 tensor of at most 64 elements")
         n_adv = advance.numel()
+    if return_candidates and screen is None:
+        raise ValueError("return_candidates needs the screened top-1")
     if screen is not None:
         _lib.call("q35_lm_head_top1_screened", weight.data_ptr(), wq.data_ptr(), sw.data_ptr(),
                   cr.data_ptr(), hidden.data_ptr(), vocab, k, workspace.data_ptr(), nbytes,
                   output.data_ptr(), _lib.ptr(advance), n_adv, _stream(hidden))
+        if return_candidates:
+            import ctypes
+
+            n = ctypes.c_int(0)
+            off = _lib.load().q35_lm_head_screened_counts(vocab, ctypes.byref(n))
+            counts = workspace[off: off + 4 * n.value].view(torch.int32)
+            return output, counts.to(torch.int64).sum()
     else:
         _lib.call("q35_lm_head_top1", weight.data_ptr(), hidden.data_ptr(), vocab, k,
                   workspace.data_ptr(), slots, output.data_ptr(), _lib.ptr(advance), n_adv,

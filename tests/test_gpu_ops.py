@@ -267,6 +267,8 @@ def test_lm_head_screened_ties_and_adversarial(gpu):
     assert int(_screened(gpu, hg, w2g)) == int(K.lm_head_argmax(hg, w2g))
     same = w[5].expand(3000, 2048).contiguous().to(gpu)
     assert int(_screened(gpu, hg, same)) == 0 == int(K.lm_head_argmax(hg, same))
+    _, n_same = _screened(gpu, hg, same, return_candidates=True)
+    assert int(n_same) == 3000  # no row can be excluded
     zero_h = torch.zeros(1, 2048, dtype=BF, device=gpu)
     assert int(_screened(gpu, zero_h, wg)) == 0 == int(K.lm_head_argmax(zero_h, wg))
     w3 = w.clone()
@@ -312,6 +314,16 @@ def test_lm_head_screen_bound_holds(gpu):
     print(f"candidate fraction {frac:.4f}")
     assert frac < 0.2
     assert int(out) == int(K.lm_head_argmax(h, w))
+    # the per-workgroup recomputed-row counts add up to exactly those rows
+    import ctypes
+
+    n = ctypes.c_int(0)
+    off = _lib.load().q35_lm_head_screened_counts(v, ctypes.byref(n))
+    assert n.value == nb and off + 4 * nb <= nbytes
+    counts = ws[off : off + 4 * nb].view(torch.int32).long().cpu()
+    assert int(counts.sum()) == int((upper >= lower_max).sum())
+    _, total = K.lm_head_argmax(h, w, screen=(wq, sw, cr), return_candidates=True)
+    assert int(total) == int(counts.sum())
 
 
 def test_lm_head_screened_in_graph_with_feedback(gpu):

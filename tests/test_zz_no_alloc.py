@@ -1,7 +1,9 @@
 """q35_lm_head_top1_noalloc (the entry point that allocates nothing) against
 q35_lm_head_top1, called through the C ABI.
 
-Two calls in a row, the second with a smaller vocabulary, on the persistent
+The process's first no-alloc call is made under graph capture and the
+graph's replays give the eager entry point's token and advance. Then two
+calls in a row, the second with a smaller vocabulary, on the persistent
 K = 2048 path and on the generic path (K = 256, which needs (V + 3) / 4
 scratch slots): the token index equals the workspace entry point's bit for
 bit, the ``advance`` tensor is incremented the same way, and a generic-path
@@ -34,6 +36,36 @@ def _call_both(lib, stream, W, h):
                "q35_lm_head_top1_noalloc")
     torch.cuda.synchronize()
     return int(out_ws), int(out_na), int(adv_ws), int(adv_na)
+
+
+def test_noalloc_top1_under_graph_capture(gpu):
+    """First in this file, so the first no-alloc call of a run that starts
+    here happens inside torch.cuda.graph capture; three replays, with eager
+    work between them, each give the workspace entry point's token and
+    advance the position the same way."""
+    from ppu_amd import _lib
+
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(20260819)
+    V, K = 248320, 2048
+    W = (torch.randn(V, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    h = torch.randn(1, K, generator=g).to(torch.bfloat16).to(gpu)
+    out = torch.full((1, 1), -1, device=gpu, dtype=torch.int64)
+    adv = torch.tensor([[100]], device=gpu, dtype=torch.int64)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.check(lib.q35_lm_head_top1_noalloc(W.data_ptr(), h.data_ptr(), V, K, out.data_ptr(),
+                                                adv.data_ptr(), 1,
+                                                torch.cuda.current_stream().cuda_stream),
+                   "q35_lm_head_top1_noalloc")
+    stream = torch.cuda.current_stream().cuda_stream
+    for rep in range(3):
+        out.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        ws_tok, _, _, _ = _call_both(lib, stream, W, h)  # eager work between the replays
+        assert int(out) == ws_tok
+        assert int(adv) == 101 + rep
 
 
 @pytest.mark.parametrize("K", [2048, 256])
