@@ -167,11 +167,14 @@ struct RopeLoads {
   long long pt, ph, pw;
 };
 Q35_DEV RopeLoads load_rope(const FusedQ& f, int lane) {
+  // The positions are vector loads (nontemporal): issued in program order
+  // with the other prologue loads, they return before the K/V stream instead
+  // of waiting on the scalar cache.
   RopeLoads r;
   r.invf = f.inv_freq[lane % (f.rot / 2)];
-  r.pt = f.pos_t[0];
-  r.ph = f.pos_h[0];
-  r.pw = f.pos_w[0];
+  r.pt = __builtin_nontemporal_load(f.pos_t);
+  r.ph = __builtin_nontemporal_load(f.pos_h);
+  r.pw = __builtin_nontemporal_load(f.pos_w);
   return r;
 }
 
@@ -346,13 +349,16 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
 
   // 2. K/V rows of the first iteration. Group gi of a wave holds tokens
   //    tb + 4*gi + row (K, the lane's 16 dims), V rows tb + i (dims 4*lane..).
-  //    Rows past the valid end are read at the last valid row (in bounds,
-  //    already cached) and masked out of the softmax.
+  //    The row indices do not depend on the valid length (a device scalar
+  //    whose load would otherwise delay every K/V request by a round trip):
+  //    they are clamped to the chunk's last row inside the cache capacity,
+  //    and rows at or past the valid end (whatever bits they hold) are
+  //    masked out of the softmax and their V values replaced by zeros.
   const uint16_t* Kh = Kc + (size_t)kvh * cache_len * kAD;
   const uint16_t* Vh = Vc + (size_t)kvh * cache_len * kAD;
   const int rw = lane >> 4;
   const int ds = lane & 15;
-  const int tmax = max(end - 1, 0);
+  const int tmax = min(start + chunk, cache_len) - 1;
   uint4 kr[2][2];
   uint2 vr[kWaveTok];
   auto load_kv = [&](int it, uint4 (&kd)[2][2], uint2 (&vd)[kWaveTok]) {
@@ -430,10 +436,11 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
     const int tb = start + (IT) * kIterTok + wid * kWaveTok;                                    \
     float vf[kWaveTok][4];                                                                      \
     _Pragma("unroll") for (int i = 0; i < kWaveTok; ++i) {                                      \
-      vf[i][0] = bf_lo(VR[i].x);                                                                \
-      vf[i][1] = bf_hi(VR[i].x);                                                                \
-      vf[i][2] = bf_lo(VR[i].y);                                                                \
-      vf[i][3] = bf_hi(VR[i].y);                                                                \
+      const bool in = tb + i < end;                                                             \
+      vf[i][0] = in ? bf_lo(VR[i].x) : 0.f;                                                     \
+      vf[i][1] = in ? bf_hi(VR[i].x) : 0.f;                                                     \
+      vf[i][2] = in ? bf_lo(VR[i].y) : 0.f;                                                     \
+      vf[i][3] = in ? bf_hi(VR[i].y) : 0.f;                                                     \
     }                                                                                           \
     _Pragma("unroll") for (int g = 0; g < G; ++g) {                                             \
       float s[2];                                                                               \
@@ -484,12 +491,14 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
   if (it < n_iter) Q35_ATT_STEP(kr, vr, it);
 #undef Q35_ATT_STEP
 
-  // The new token (FUSED): wave KW of the owning workgroup folds it in.
-  if (owns_new && wid == KW) {
+  // The new token (FUSED): the owning workgroup folds it in, head g by wave
+  // g % NW (into that wave's state), so the heads are folded in parallel.
+  if (owns_new) {
     const float4 kv = *reinterpret_cast<const float4*>(&kn_s[4 * lane]);
     const float4 vv = *reinterpret_cast<const float4*>(&vn_s[4 * lane]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+      if (g % NW != wid) continue;
       const uint2 qv = q_s[g][lane];
       float sdot = bf_lo(qv.x) * kv.x;
       sdot = fmaf(bf_hi(qv.x), kv.y, sdot);
@@ -508,8 +517,10 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
     }
   }
 
-  // 5. merge the waves in LDS; write this split's (acc, m, l) per head.
-  __shared__ float m_s[NW][G], l_s[NW][G], f_s[NW][G];
+  // 5. merge the waves in LDS (one barrier: every thread derives the wave
+  //    factors e^(m_w - max_w m_w), 0 for a wave without tokens, of its
+  //    head itself); write this split's (acc, m, l) per head.
+  __shared__ float m_s[NW][G], l_s[NW][G];
   __shared__ float a_s[NW][G][kAD];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -520,38 +531,31 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
     *reinterpret_cast<float4*>(&a_s[wid][g][4 * lane]) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
   }
   __syncthreads();
-  // Per (wave, head) factor e^(m_w - max_w m_w), 0 for a wave without tokens.
-  if (threadIdx.x < NW * G) {
-    const int w = threadIdx.x / G, g = threadIdx.x % G;
+  for (int idx = threadIdx.x; idx < G * kAD / 4; idx += NW * 64) {
+    const int g = idx / (kAD / 4), d = (idx % (kAD / 4)) * 4;
     float mm = -INFINITY;
 #pragma unroll
     for (int v = 0; v < NW; ++v) mm = fmaxf(mm, m_s[v][g]);
-    f_s[w][g] = m_s[w][g] == -INFINITY ? 0.f : expf(m_s[w][g] - mm);
-    if (w == 0) {
-      float ll = 0.f;
+    float f[NW];
 #pragma unroll
-      for (int v = 0; v < NW; ++v)
-        ll += l_s[v][g] * (m_s[v][g] == -INFINITY ? 0.f : expf(m_s[v][g] - mm));
-      const int slot = (kvh * G + g) * splits + split;
-      ml_out[slot * 2] = mm;
-      ml_out[slot * 2 + 1] = ll;
-    }
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * kAD / 4; idx += NW * 64) {
-    const int g = idx / (kAD / 4), d = (idx % (kAD / 4)) * 4;
+    for (int w = 0; w < NW; ++w) f[w] = m_s[w][g] == -INFINITY ? 0.f : expf(m_s[w][g] - mm);
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float f = f_s[w][g];
       const float4 v = *reinterpret_cast<const float4*>(&a_s[w][g][d]);
-      a.x += v.x * f;
-      a.y += v.y * f;
-      a.z += v.z * f;
-      a.w += v.w * f;
+      a.x += v.x * f[w];
+      a.y += v.y * f[w];
+      a.z += v.z * f[w];
+      a.w += v.w * f[w];
     }
     const int slot = (kvh * G + g) * splits + split;
     *reinterpret_cast<float4*>(acc_out + (size_t)slot * kAD + d) = a;
+    if (d == 0) {
+      float ll = 0.f;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) ll += l_s[v][g] * f[v];
+      *reinterpret_cast<float2*>(ml_out + slot * 2) = make_float2(mm, ll);
+    }
   }
 }
 

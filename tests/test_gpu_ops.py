@@ -620,6 +620,49 @@ def test_gqa_decode_attention(gpu, cache_len, n_valid):
     close(got, exp)
 
 
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("cache_len,n_valid", [(1152, 1040), (512, 5), (8192, 6000)])
+def test_gqa_decode_rows_past_valid_end_ignored(gpu, fused, cache_len, n_valid):
+    """Cache rows at and past the valid length hold NaN / inf (a static
+    cache's unwritten tail may hold any bits): the kernels request those rows
+    before they know the length, so they must mask their scores and zero
+    their V values. The output equals the oracle over the valid rows."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 21)
+    kc = randn(g, 1, 2, cache_len, 256)
+    vc = randn(g, 1, 2, cache_len, 256)
+    kc[:, :, n_valid:] = float("nan")
+    vc[:, :, n_valid:] = float("inf")
+    vc[:, 1, n_valid + 1 :: 3] = float("nan")
+    if not fused:
+        q = randn(g, 1, 8, 1, 256)
+        length = torch.tensor(n_valid, dtype=torch.int64)
+        exp = ref.gqa_decode_attention(q, kc, vc, length, 0.0625)
+        got = K.gqa_decode_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), length.to(gpu), 0.0625)
+        close(got, exp)
+        return
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding
+
+    from ppu_amd import synth
+
+    packed = randn(g, 1, 1, 5120)
+    qw, kw = randn(g, 256, scale=0.1), randn(g, 256, scale=0.1)
+    rot = Qwen3_5TextRotaryEmbedding(synth.config_tiny())
+    pos = torch.tensor((n_valid,) * 3, dtype=torch.int64).view(3, 1, 1)
+    cos, sin = rot(torch.zeros(1, 1, 8, dtype=BF), pos)
+    kr, vr = kc.clone(), vc.clone()
+    q, _, _ = ref.qgkv_norm_rope(packed, qw, kw, cos, sin, q_heads=8, kv_heads=2, dim=256,
+                                 rotary_dim=64, cache_key=kr, cache_value=vr, cache_start=n_valid)
+    att = ref.gqa_decode_attention(q, kr, vr, n_valid + 1, 0.0625)
+    exp = ref.attention_gate_mul(att, packed, 256)
+    length = torch.tensor(n_valid, dtype=torch.int64, device=gpu)
+    got = K.gqa_decode_fused(packed.to(gpu), qw.to(gpu), kw.to(gpu), rot.inv_freq.to(gpu),
+                             pos.to(gpu), kc.to(gpu), vc.to(gpu), length, 0.0625, q_heads=8)
+    assert bool(torch.isfinite(got).all())
+    close(got, exp)
+
+
 @pytest.mark.parametrize("q_heads,kv_heads", [(2, 2), (4, 2), (16, 2), (4, 4), (8, 1)])
 def test_gqa_decode_back_to_back(gpu, q_heads, kv_heads):
     """Head groupings G = 1, 2, 4, 8 and several launches queued without a host
