@@ -414,15 +414,19 @@ def counter_probe(dev) -> None:
     * 5 calibration launches of a plain elementwise kernel (``neg``) that reads
       exactly 1 GiB and writes exactly 1 GiB, the yardstick that turns the
       FETCH_SIZE / WRITE_SIZE counters into bytes;
-    * 5 launches of the lm_head GEMV + top-1 on a [248320, 2048] bf16 weight;
+    * 5 launches of the lm_head GEMV + top-1 on a [248320, 2048] bf16 weight,
+      then 5 of the screened top-1 (int8 screen + exact rescore) on it;
     * 4 replays of the captured decode step of the seeded 2B decoder (bf16
       linears, 1024-token context): every decode kernel with its real
       weights, 129 dispatches per replay;
-    * 3 launches of each prefill GEMM shape (M = 1024 tokens), for MFMA
-      counters.
+    * 16 standalone launches of the delta-rule decode step over rotating
+      states, as config 4 times it (fp32 gate parameters, so the kernel is
+      the ``<true>`` instance and its rows stay apart from the step's);
+    * 3 launches of each prefill GEMM of the product path (M = 1024 tokens,
+      the hand-written matrix-core kernels: bf16 plain and SwiGLU, int8 with
+      the dequant epilogue), for MFMA counters.
     """
     import torch
-    import torch.nn.functional as F
 
     from ppu_amd import kernels as K
     from ppu_amd import synth
@@ -441,8 +445,13 @@ def counter_probe(dev) -> None:
     h = torch.randn(1, 2048, device=dev, generator=g).to(bf)
     for _ in range(5):
         K.lm_head_argmax(h, w)
+    screen = K.lm_head_screen_prep(w)
+    for _ in range(5):
+        K.lm_head_argmax(h, w, screen=screen)
     torch.cuda.synchronize()
-    del w
+    _, rows = K.lm_head_argmax(h, w, screen=screen, return_candidates=True)
+    log(f"counter probe: the screened top-1 rescored {int(rows)} rows")
+    del w, screen
     log("counter probe: calibration + lm_head done; decode step ...")
     cfg = synth.config_2b()
     model = synth.build_model(cfg, device=dev)
@@ -462,12 +471,26 @@ def counter_probe(dev) -> None:
         torch.cuda.synchronize()
     del graph, cache, model
     torch.cuda.empty_cache()
-    log("counter probe: decode step done; prefill GEMMs ...")
-    for (n, k) in ((8320, 2048), (2048, 2048), (5120, 2048), (12288, 2048), (2048, 6144)):
+    log("counter probe: decode step done; standalone delta step ...")
+    states = [torch.randn(1, 16, 128, 128, device=dev, generator=g) * 0.1 for _ in range(16)]
+    packed = torch.randn(1, 1, 8320, device=dev, generator=g).to(bf)
+    qkv = torch.randn(1, 1, 6144, device=dev, generator=g).to(bf)
+    z16 = torch.zeros(16, device=dev)
+    for st in states:
+        K.delta_recurrent_fused(qkv, packed, z16, z16, st)
+    torch.cuda.synchronize()
+    del states
+    log("counter probe: delta step done; prefill GEMMs ...")
+    for (n, k, swiglu) in ((8320, 2048, False), (2048, 2048, False), (5120, 2048, False),
+                           (12288, 2048, True), (2048, 6144, False)):
         x = torch.randn(1024, k, device=dev, generator=g).to(bf)
         wt = (torch.randn(n, k, device=dev, generator=g) * 0.02).to(bf)
+        xq, sx = K.quantize_act_i8(x)
+        wq, sw = K.quantize_weight_i8(wt)
         for _ in range(3):
-            F.linear(x, wt)
+            K.gemm_bf16(x, wt, swiglu=swiglu)
+        for _ in range(3):
+            K.gemm_a8w8(xq, sx, wq, sw.reshape(-1), swiglu=swiglu)
     torch.cuda.synchronize()
     log("counter probe done")
 
@@ -483,8 +506,19 @@ DECODE_ALGO_BYTES = {
     "gemv_fused<4, 2, 4, 2, 0, false>": 5120 * 2048 * 2 + 4 * 2048 * 2 + 5120 * 2,
     "gemv_fused<4, 2, 4, 0, 0, false>": 2048 * 2048 * 2 + 2 * 2048 * 2,
     "delta_decode_wave<false>": 2 * 16 * 128 * 128 * 4 + 6144 * 2 + 64 + 16 * 128 * 2,
+    "delta_decode_wave<true>": 2 * 16 * 128 * 128 * 4 + 6144 * 2 + 64 * 2 + 16 * 128 * 2,
     "lm_head_top1_persist<4, 1, 4>": 248320 * 2048 * 2 + 2048 * 2 + 8,
+    # int8 copy, per-row scale and bound factor read, per-row upper bound written
+    "lm_head_screen<4, 2, 2>": 248320 * 2048 + 248320 * 12 + 2048 * 2,
+    # K/V over the ~1026 cached tokens of the probe's replays, the packed row,
+    # the new K/V cache row (the per-split partials are the design's overhead)
+    "gqa_decode_split<4, true>": 2 * 2 * 1026 * 256 * 2 + 5120 * 2 + 2 * 2 * 256 * 2,
+    # 8 heads x 36 splits of (acc[256], m, l), the gate row, the bf16 output
+    "gqa_decode_combine<4>": 8 * 36 * 258 * 4 + 2048 * 2 + 2048 * 2,
 }
+# The rescore reads the per-row upper bounds and the bf16 rows of its
+# candidates (4 KiB each): its algorithmic bytes need the candidate count.
+RESCORE_NAME = "lm_head_rescore<4>"
 
 
 def trace_summary(kind: str, trace_csv: str, bench_json: str) -> None:
@@ -594,7 +628,7 @@ def trace_summary(kind: str, trace_csv: str, bench_json: str) -> None:
     print("\n".join(lines))
 
 
-def pmc_summary(fetch_csv: str, write_csv: str) -> None:
+def pmc_summary(fetch_csv: str, write_csv: str, rescore_rows: int | None = None) -> None:
     """Print the HBM-traffic summary of two ``rocprofv3 --pmc`` runs of
     ``--counter-probe`` (FETCH_SIZE, then WRITE_SIZE; their
     ``*_counter_collection.csv`` files): mean KiB per dispatch per kernel,
@@ -631,8 +665,47 @@ def pmc_summary(fetch_csv: str, write_csv: str) -> None:
             continue
         traffic = int((fetch[name] * f_scale + write[name] * w_scale) * 1024)
         algo = DECODE_ALGO_BYTES.get(name)
+        if name == RESCORE_NAME and rescore_rows is not None:
+            algo = 248320 * 4 + rescore_rows * 2048 * 2 + 2048 * 2
         ratio = f"{traffic / algo:.4f}" if algo else "-"
         print(f"{name} | {fetch[name]:.1f} | {write[name]:.1f} | {traffic} | {algo or '-'} | {ratio}")
+
+
+def mfma_summary(pmc_csv: str, trace_csv: str) -> None:
+    """Print the matrix-core use of the prefill GEMMs of a ``--counter-probe``
+    run: one ``rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16
+    SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE`` pass
+    and one ``--kernel-trace`` pass, matched by kernel name and grid size:
+    operations = MOPS x 512, MFMA busy = busy cycles / (GRBM_GUI_ACTIVE / 8
+    XCDs x 1024 SIMDs)."""
+    import csv
+    from collections import defaultdict
+
+    def key(row):
+        n = row["Kernel_Name"].replace("(anonymous namespace)::", "")
+        return (n[5:] if n.startswith("void ") else n).split("(")[0].strip(), row.get("Grid_Size", "")
+
+    cnt = defaultdict(lambda: defaultdict(list))
+    with open(pmc_csv) as f:
+        for row in csv.DictReader(f):
+            if "gemm_ring" in row["Kernel_Name"]:
+                cnt[key(row)][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    dur = defaultdict(list)
+    with open(trace_csv) as f:
+        for row in csv.DictReader(f):
+            if "gemm_ring" in row["Kernel_Name"]:
+                dur[key(row)].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    print("kernel | grid | T(FL)OPs per launch | us | T(FL)OP/s | of dense peak | MFMA busy")
+    for k, c in cnt.items():
+        mean = {n: sum(v) / len(v) for n, v in c.items()}
+        i8 = mean.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) > mean.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        ops = 512 * mean.get("SQ_INSTS_VALU_MFMA_MOPS_I8" if i8 else "SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        us = sum(dur[k]) / len(dur[k]) if dur.get(k) else float("nan")
+        peak = 5000.0 if i8 else 2500.0
+        active = mean.get("GRBM_GUI_ACTIVE", 0.0) / 8
+        busy = mean.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (active * 1024) if active else float("nan")
+        rate = ops / us / 1e6
+        print(f"{k[0]} | {k[1]} | {ops / 1e12:.4f} | {us:.2f} | {rate:.1f} | {rate / peak:.3f} | {busy:.3f}")
 
 
 def cpu_baseline(state, cfg, prompt, decode_steps: int, eager: bool = True) -> dict:
@@ -811,11 +884,19 @@ def main() -> None:
     ap.add_argument("--quick", action="store_true", help="--gemm-sweep: default plans only")
     ap.add_argument("--counter-probe", action="store_true",
                     help="only run the short workload profiled with rocprofv3 --pmc, then exit")
-    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="print the HBM-traffic table of two --counter-probe pmc runs, then exit")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="FETCH_CSV WRITE_CSV [RESCORE_ROWS]: print the HBM-traffic table of two "
+                         "--counter-probe pmc runs, then exit")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_CSV", "TRACE_CSV"),
+                    help="print the prefill GEMMs' matrix-core use from a --counter-probe pmc run "
+                         "and a kernel trace of it, then exit")
     args = ap.parse_args()
     if args.pmc_summary:
-        pmc_summary(*args.pmc_summary)
+        fetch, write, *rows = args.pmc_summary
+        pmc_summary(fetch, write, int(rows[0]) if rows else None)
+        return
+    if args.mfma_summary:
+        mfma_summary(*args.mfma_summary)
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary)

@@ -219,15 +219,22 @@ __global__ __launch_bounds__(256) void delta_decode(const DeltaArgs p) {
 // head = xcd + 8*(slot / 16), tile = slot % 16.
 constexpr int kWT = 8;  // v columns per wave
 
-Q35_DEV float4 xor_sum_rows(float4 v) {
-#pragma unroll
-  for (int off = 2; off < 64; off <<= 1) {
-    v.x += __shfl_xor(v.x, off);
-    v.y += __shfl_xor(v.y, off);
-    v.z += __shfl_xor(v.z, off);
-    v.w += __shfl_xor(v.w, off);
-  }
+// Sum over the 32 lanes of equal lane % 2 (every lane gets its class's sum):
+// inside each 16-lane row by DPP (xor 2, then rotations by 4 and 8, which
+// keep the parity and together cover the row's 8 lanes of one parity), then
+// across rows by a swizzle (lane ^ 16) and one permute (lane ^ 32): two LDS-
+// unit exchanges per value instead of five.
+constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+Q35_DEV float parity_sum(float v) {
+  v += dpp_f<Q35_DPP_QUAD_XOR2>(v);
+  v += dpp_f<kDppRowRor4>(v);
+  v += dpp_f<kDppRowRor8>(v);
+  v += swz_xor16_f(v);
+  v += __shfl_xor(v, 32);
   return v;
+}
+Q35_DEV float4 xor_sum_rows(float4 v) {
+  return make_float4(parity_sum(v.x), parity_sum(v.y), parity_sum(v.z), parity_sum(v.w));
 }
 
 template <bool PF32>  // gate parameters (A_log, dt_bias) fp32, else bf16

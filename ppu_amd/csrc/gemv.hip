@@ -100,9 +100,14 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
   const int wid = tid >> 6;
   const int n0 = (blockIdx.x * WV + wid) * P;
   const bool writer = blockIdx.x == 0;
+  // HALF: a gated-norm prologue on a workgroup of twice as many threads as
+  // 8-element groups; each thread takes half a group (4 elements), so the
+  // prologue's per-thread arithmetic, which sits between the activation
+  // loads and the first dot product, is halved.
+  constexpr bool HALF = PRO == PRO_GATEDNORM && NT == 2 * NV;
   // Threads past NV (when the workgroup is wider than the vector) own no
   // activation group; the test is uniform per wave (NV is a multiple of 64).
-  const bool act = NV % NT == 0 || tid < NV;
+  const bool act = HALF || NV % NT == 0 || tid < NV;
 
   // 1. activation, update and norm-weight loads, issued before the weight
   //    stream so that the in-order vmcnt lets the prologue start while the
@@ -115,6 +120,21 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
     xsrc += (size_t)r * a.K;
   }
   uint4 xa[PER], ua[PER], wa[PER], wb[PER];
+  if constexpr (HALF) {
+    // element offset of the thread's half group
+    const int e0 = tid * 4;
+    const uint2 xv = *reinterpret_cast<const uint2*>(xsrc + e0);
+    const uint2 uv = *reinterpret_cast<const uint2*>(a.u + e0);
+    xa[0] = make_uint4(xv.x, xv.y, 0u, 0u);
+    ua[0] = make_uint4(uv.x, uv.y, 0u, 0u);
+    const int kn = e0 % kGatedHead;
+    if (a.nw_f32) {
+      wa[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.nw) + kn);
+    } else {
+      const uint2 wv = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.nw) + kn);
+      wa[0] = make_uint4(wv.x, wv.y, 0u, 0u);
+    }
+  } else
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = act ? tid + j * NT : 0;
@@ -188,6 +208,32 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[j][e] = act ? o[j][e] : 0.f;
     }
+  } else if (HALF) {
+    // Thread t holds elements 4t..4t+3: a 128-wide head is 32 consecutive
+    // lanes (two DPP rows, joined by the lane ^ 16 swizzle).
+    const float s4[4] = {bf_lo(xa[0].x), bf_hi(xa[0].x), bf_lo(xa[0].y), bf_hi(xa[0].y)};
+    const float z4[4] = {bf_lo(ua[0].x), bf_hi(ua[0].x), bf_lo(ua[0].y), bf_hi(ua[0].y)};
+    float wn[4];
+    if (a.nw_f32) {
+      wn[0] = __uint_as_float(wa[0].x); wn[1] = __uint_as_float(wa[0].y);
+      wn[2] = __uint_as_float(wa[0].z); wn[3] = __uint_as_float(wa[0].w);
+    } else {
+      wn[0] = bf_lo(wa[0].x); wn[1] = bf_hi(wa[0].x); wn[2] = bf_lo(wa[0].y); wn[3] = bf_hi(wa[0].y);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += s4[e] * s4[e];
+    ss = row16_sum(ss);
+    ss += swz_xor16_f(ss);
+    const float inv = rsqrt_cr(ss * (1.0f / (float)kGatedHead) + a.eps);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float nb = round_bf(s4[e] * inv);
+      const float weighted = round_bf(nb * round_bf(wn[e]));
+      const float v = weighted * silu_fast(z4[e]);
+      o[0][e] = I8 ? round_bf(v) : v;
+      o[0][e + 4] = 0.f;
+    }
   } else if (PRO == PRO_GATEDNORM) {
     // Group i holds elements 8i..8i+7, so head = i/16: the 16 groups of a head
     // sit on the 16 lanes of one DPP row (NT is a multiple of 16).
@@ -201,13 +247,14 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += s[e] * s[e];
       ss = row16_sum(ss);
-      const float inv = rsqrt_cr(ss / (float)kGatedHead + a.eps);
+      // (the mean over the 128-wide head: an exact scaling by 2^-7)
+      const float inv = rsqrt_cr(ss * (1.0f / (float)kGatedHead) + a.eps);
       nw8_from(a, wa[j], wb[j], wn);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float nb = round_bf(s[e] * inv);
         const float weighted = round_bf(nb * round_bf(wn[e]));
-        const float v = weighted * silu_f(z[e]);
+        const float v = weighted * silu_fast(z[e]);
         o[j][e] = act ? (I8 ? round_bf(v) : v) : 0.f;
       }
     }
@@ -248,14 +295,21 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
     }
   }
   if (PRO != PRO_NONE && writer && a.xn_out && act) {
+    if constexpr (HALF) {
+      *reinterpret_cast<uint2*>(a.xn_out + tid * 4) =
+          make_uint2(pack_bf2(o[0][0], o[0][1]), pack_bf2(o[0][2], o[0][3]));
+    } else {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) *reinterpret_cast<uint4*>(a.xn_out + (tid + j * NT) * 8) = pack8(o[j]);
+      for (int j = 0; j < PER; ++j) *reinterpret_cast<uint4*>(a.xn_out + (tid + j * NT) * 8) = pack8(o[j]);
+    }
   }
 
   // 4. stage the activation in LDS: bf16, or (int8 weights) per-token int8
   //    with s_x = absmax/127, q = sat(rint(x * 127/absmax)) over the whole row.
   float sx = 0.f;
-  if (!I8) {
+  if (HALF && !I8) {
+    reinterpret_cast<uint2*>(xs)[tid] = make_uint2(pack_bf2(o[0][0], o[0][1]), pack_bf2(o[0][2], o[0][3]));
+  } else if (!I8) {
 #pragma unroll
     for (int j = 0; j < PER; ++j)
       if (act) xs[tid + j * NT] = pack8(o[j]);
@@ -273,13 +327,20 @@ __global__ __launch_bounds__(WV * 64) void gemv_fused(const GemvArgs a) {
     for (int v = 1; v < WV; ++v) mx = fmaxf(mx, redm[v]);
     const float inv = 127.0f / mx;
     sx = mx / 127.0f;
+    if constexpr (HALF) {
+      // the thread's 4 elements: one 32-bit word of the int8 row
+      const uint32_t v = quant4_i8(o[0][0], o[0][1], o[0][2], o[0][3], inv);
+      reinterpret_cast<uint32_t*>(xq_s)[tid] = v;
+      if (writer && a.xq_out) *reinterpret_cast<uint32_t*>(a.xq_out + tid * 4) = v;
+    } else {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = tid + j * NT;
-      const uint2 v = quant8_i8(o[j], inv);
-      if (act) {
-        xq_s[i] = v;
-        if (writer && a.xq_out) *reinterpret_cast<uint2*>(a.xq_out + i * 8) = v;
+      for (int j = 0; j < PER; ++j) {
+        const int i = tid + j * NT;
+        const uint2 v = quant8_i8(o[j], inv);
+        if (act) {
+          xq_s[i] = v;
+          if (writer && a.xq_out) *reinterpret_cast<uint2*>(a.xq_out + i * 8) = v;
+        }
       }
     }
     if (writer && tid == 0 && a.sx_out) a.sx_out[0] = sx;
@@ -568,6 +629,7 @@ int dispatch(const GemvArgs& a, hipStream_t stream) {
       if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI>(a, stream); return q35_last_error(); }
       if (nch == 12) { launch_fast<4, 2, 12, PRO, EPI>(a, stream); return q35_last_error(); }
     } else {
+      if (PRO == PRO_GATEDNORM && nch == 4) { launch_fast<8, 1, 4, PRO, EPI>(a, stream); return q35_last_error(); }
       if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI>(a, stream); return q35_last_error(); }
       if (nch == 12) { launch_fast<4, 1, 12, PRO, EPI>(a, stream); return q35_last_error(); }
       if (nch == 1) { launch_fast<4, 2, 1, PRO, EPI>(a, stream); return q35_last_error(); }
@@ -601,6 +663,7 @@ int dispatch_i8(const GemvArgs& a, hipStream_t stream) {
     if (nch == 6) { launch_fast<4, 2, 6, PRO, EPI, true>(a, stream); return q35_last_error(); }
   } else {
     if (nch == 1) { launch_fast<4, 4, 1, PRO, EPI, true>(a, stream); return q35_last_error(); }
+    if (PRO == PRO_GATEDNORM && nch == 2) { launch_fast<8, 1, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
     if (nch == 2) { launch_fast<4, 2, 2, PRO, EPI, true>(a, stream); return q35_last_error(); }
     if (nch == 4) { launch_fast<4, 2, 4, PRO, EPI, true>(a, stream); return q35_last_error(); }
     if (nch == 6) { launch_fast<4, 2, 6, PRO, EPI, true>(a, stream); return q35_last_error(); }

@@ -71,7 +71,6 @@ Q35_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
 // a few ulp of a bf16 rounding boundary.
 Q35_DEV float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 Q35_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
-
 // ---------------------------------------------------------------- DPP moves
 template <int CTRL>
 Q35_DEV float dpp_f(float v) {
