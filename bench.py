@@ -196,6 +196,29 @@ def swiglu_roofline(model, variant: str) -> dict:
                                "gemv_frac_of_read_rate": round(achieved / read_gbs, 4)}}
 
 
+def profile_frac(roof: dict) -> dict:
+    """The roofline fraction of the dominant kernel from its average duration
+    in the committed decode-step profile (profiles/decode_step_2b.txt, the
+    in-step kernel under rocprofv3), beside the bench's own graph-timed one."""
+    import re
+
+    name = re.search(r"\((gemv_fused<[^>]*>)\)", roof["kernel"])
+    try:
+        text = (ROOT / "profiles" / "decode_step_2b.txt").read_text()
+    except OSError:
+        return {}
+    if not name:
+        return {}
+    m = re.search(re.escape(name.group(1)) + r" g\d+\s+n=\s*\d+ total\s+[\d.]+ us\s+avg\s+([\d.]+) us", text)
+    if not m:
+        return {}
+    us = float(m.group(1))
+    ach = roof["algorithmic_bytes"] / us / 1e3
+    return {"frac_bench": roof["frac"], "us_bench": roof["us_per_launch"],
+            "frac_profile": round(ach / roof["peak"], 4), "us_profile": us,
+            "profile": "profiles/decode_step_2b.txt (first decode-step table)"}
+
+
 def step_bytes(model, context: float) -> int:
     """HBM bytes one decode token needs: every packed weight (and int8 scale)
     once, the lm_head (tied embedding) once (with the screened top-1
@@ -743,9 +766,14 @@ def cpu_baseline(state, cfg, prompt, decode_steps: int, eager: bool = True) -> d
            "cpu_model": _cpu_model()}
     log(f"CPU oracle: TTFT {ttft * 1e3:.0f} ms, decode {decode_steps / dt:.2f} tok/s on "
         f"{threads} threads; tokens {tokens[:6]}")
-    if eager:
-        out["transformers_eager"] = _eager_cpu(state, cfg, prompt, decode_steps)
-    return out
+    if not eager:
+        return out
+    # The headline CPU figure is the reference's own CPU path, Transformers'
+    # eager forward (integration.py:51-52 runs it for CPU tensors); the
+    # oracle port is kept beside it.
+    ref = _eager_cpu(state, cfg, prompt, decode_steps)
+    ref.update(kind="reference", cpu_model=out["cpu_model"], port=out)
+    return ref
 
 
 def _eager_cpu(state, cfg, prompt, decode_steps: int) -> dict:
@@ -958,6 +986,12 @@ def main() -> None:
         assert all(r.tokens == first.tokens for r in warm), "greedy decode is not deterministic"
         log(f"[{variant}] TTFT {ttft_ms:.2f} ms (cold {first.ttft_seconds * 1e3:.1f} ms); "
             f"generate-loop decode {loop_tps:.1f} tok/s; first tokens {first.tokens[:8]}")
+        # TTFT of prompt lengths this warmed process has not seen: the eager
+        # prefill (the prefill graph of a length is captured after that
+        # call's first token, outside its timed region); median of 3 lengths.
+        fresh = [runner.generate(prompt[:, : PROMPT_LEN - 8 * (i + 1)], 2).ttft_seconds for i in range(3)]
+        ttft_eager_ms = statistics.median(fresh) * 1e3
+        log(f"[{variant}] TTFT of a first-seen prompt length (eager prefill): {ttft_eager_ms:.2f} ms")
         del runner
 
         # Timed decode steps: W warmup + K timed replays of the decode graph.
@@ -1001,7 +1035,8 @@ def main() -> None:
         nbytes = step_bytes(model, context)
         gbs = nbytes / (ms_per_step * 1e-3) / 1e9
         res = {"value": round(args.steps / elapsed, 2), "ms_per_step": round(ms_per_step, 4),
-               "ttft_ms": round(ttft_ms, 3), "graph_replay_ms": round(replay_ms, 4),
+               "ttft_ms": round(ttft_ms, 3), "ttft_eager_ms": round(ttft_eager_ms, 3),
+               "graph_replay_ms": round(replay_ms, 4),
                "generate_loop_tokens_per_s": round(loop_tps, 2),
                "weights_gb_per_token": round(weight_bytes / 1e9, 4), "cache_bucket": bucket,
                "step_roofline": {"bytes_per_token": nbytes, "mean_context": context,
@@ -1062,11 +1097,13 @@ def main() -> None:
                                f"{PROMPT_LEN}-token prefill then greedy decode, batch 1, "
                                f"{args.variant} linears", "cache_bucket": bucket},
         "ttft_ms": main_res["ttft_ms"],
+        "ttft_eager_ms": main_res["ttft_eager_ms"],
         "graph_replay_ms": main_res["graph_replay_ms"],
         "generate_loop_tokens_per_s": main_res["generate_loop_tokens_per_s"],
         "weights_gb_per_token": main_res["weights_gb_per_token"],
         "variants": variants,
-        "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "roofline": {**{k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+                     **profile_frac(roof)},
         "roofline_detail": {"swiglu_gemv": roof, "lm_head": lm},
         "step_roofline": main_res["step_roofline"],
         "kernels": kernels,

@@ -40,3 +40,54 @@ def check_steps(oracle, tokens, ref, gpu_hidden, ref_hidden, bounds):
     assert mean <= mean_bound, f"mean hidden error {mean:.3e} above {mean_bound}"
 
 
+
+
+def eager_greedy(state, cfg, prompt, steps: int):
+    """Greedy tokens of Transformers' own eager Qwen3.5 forward on the CPU
+    (bf16, DynamicCache; the path the reference runs for CPU tensors,
+    integration.py:51-52) on the same weights: ``steps`` tokens (the prefill's
+    token first) and, per token, the top-2 logit margin."""
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5ForCausalLM
+
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("meta"):
+            model = Qwen3_5ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(old)
+    model.load_state_dict(state, assign=True, strict=False)
+    model.tie_weights()
+    rot = model.model.rotary_emb
+    inv_freq, _ = rot.compute_default_rope_parameters(cfg, "cpu")
+    rot.inv_freq = inv_freq
+    rot.original_inv_freq = inv_freq
+    model.eval()
+    tokens, margins = [], []
+    with torch.inference_mode():
+        cache = DynamicCache(config=cfg)
+        ids = prompt
+        for _ in range(steps):
+            logits = model(input_ids=ids, past_key_values=cache, use_cache=True,
+                           logits_to_keep=1).logits[0, -1].float()
+            top = torch.topk(logits, 2)
+            tokens.append(int(top.indices[0]))
+            margins.append(float(top.values[0] - top.values[1]))
+            ids = torch.tensor([[tokens[-1]]])
+    return tokens, margins
+
+
+def report_eager_agreement(gpu_tokens, eager_tokens, eager_margins) -> int | None:
+    """Print how many greedy tokens the GPU and Transformers eager share and
+    the first divergence with eager's top-2 margin there; returns its step."""
+    same = sum(a == b for a, b in zip(gpu_tokens, eager_tokens))
+    first = next((i for i, (a, b) in enumerate(zip(gpu_tokens, eager_tokens)) if a != b), None)
+    prefix = first if first is not None else len(gpu_tokens)
+    msg = (f"GPU vs Transformers eager (CPU): {same}/{len(gpu_tokens)} identical tokens, "
+           f"identical prefix {prefix}")
+    if first is not None:
+        msg += (f"; first divergence at step {first}: gpu {gpu_tokens[first]} eager "
+                f"{eager_tokens[first]}, eager top-2 margin {eager_margins[first]:.4f}")
+    print(msg, flush=True)
+    return first

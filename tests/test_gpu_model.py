@@ -18,7 +18,7 @@ import torch
 
 from oracle.model import OracleDecoder
 from ppu_amd import synth
-from tests._parity import check_steps
+from tests._parity import check_steps, eager_greedy, report_eager_agreement
 
 pytestmark = pytest.mark.gpu
 
@@ -34,11 +34,17 @@ pytestmark = pytest.mark.gpu
 # tests/test_oracle_model.py::_variance_order_noise run once at the 2B shape).
 # The GPU perturbs every reduction, not one: mean bounds are about twice the
 # floor mean, per-step bounds about 2.4x (bf16) and 3x (A8W8) the floor max.
-HIDDEN_BOUNDS = {"tiny": (0.03, 0.03), "2b": (0.05, 0.07), "2b-a8w8": (0.16, 0.30)}
+# The 2B bounds are about 1.5x what the GPU path measures (bf16 mean 0.032 /
+# max 0.044, A8W8 0.083 / 0.094 over the 64 steps), so a data-flow change in
+# a late decode step that moves the state by a few percent fails them.
+HIDDEN_BOUNDS = {"tiny": (0.03, 0.03), "2b": (0.045, 0.06), "2b-a8w8": (0.12, 0.14)}
 
 # Relative L2 error of one layer's outputs and written states, the layer run
 # from the oracle's own input and state (test_2b_layerwise_teacher_forced).
 LAYER_BOUND = {"bf16": 0.01, "a8w8": 0.01}
+# The late decode step the layer-wise test also checks (the states then hold
+# 63 decode tokens on top of the 1024-token prefill).
+LATE = 64
 
 
 def _build(cfg, gpu, fusion):
@@ -282,6 +288,14 @@ def test_2b_prefill_1024_decode_64_vs_oracle(gpu, variant):
     hidden = _gpu_hidden_states(model, prompt.to(gpu), res.tokens, res.meta["cache_bucket"])
     del model
     torch.cuda.empty_cache()
+    # Transformers' own eager forward on the CPU (the reference's fallback
+    # path, bf16) on the same weights, free-running for all 64 tokens: the
+    # streams may part only where eager's own top-2 margin is within bf16
+    # noise (A8W8 is compared with the bf16 eager model: printed only).
+    eager, margins = eager_greedy(state, cfg, prompt, len(res.tokens))
+    first = report_eager_agreement(res.tokens, eager, margins)
+    if variant == "bf16" and first is not None:
+        assert margins[first] <= 0.25, (first, margins[first])
     oracle = OracleDecoder(state, cfg, a8w8=variant == "a8w8")
     _check_teacher_forced(oracle, prompt, res.tokens, res.meta["cache_bucket"], hidden,
                           HIDDEN_BOUNDS["2b" if variant == "bf16" else "2b-a8w8"])
@@ -320,7 +334,9 @@ def test_2b_layerwise_teacher_forced(gpu, variant):
     oracle's own input and cache state, so an error cannot hide in the
     amplification of 24 chaotic random-init layers. Prefill (1024 tokens, the
     product prefill path per layer) and the second decode step (the fused
-    decode launches per layer, state from prefill + one decode step): the
+    decode launches per layer, state from prefill + one decode step) and a
+    late decode step (step LATE = 64, states from the oracle's own greedy
+    continuation): the
     layer's mixer output and stream after the mixer add,
     the MLP output, the next normed input and every cache state it writes,
     each within LAYER_BOUND relative L2 of the oracle's. (The mixer output
@@ -346,7 +362,17 @@ def test_2b_layerwise_teacher_forced(gpu, variant):
     t1 = oracle.top1(h[:, -1])[0]
     h = oracle.forward(torch.tensor([[t1]]), ocache, d1)
     t2 = oracle.top1(h[:, -1])[0]
-    oracle.forward(torch.tensor([[t2]]), ocache, d2)
+    h = oracle.forward(torch.tensor([[t2]]), ocache, d2)
+    # A late decode step (LATE): the oracle continues greedily; the states
+    # after step LATE - 1 and the trace of step LATE are kept.
+    tok = oracle.top1(h[:, -1])[0]
+    for _ in range(3, LATE - 1):
+        h = oracle.forward(torch.tensor([[tok]]), ocache)
+        tok = oracle.top1(h[:, -1])[0]
+    dprev, dlate = [], []
+    h = oracle.forward(torch.tensor([[tok]]), ocache, dprev)
+    t_late = oracle.top1(h[:, -1])[0]
+    oracle.forward(torch.tensor([[t_late]]), ocache, dlate)
 
     worst: dict[str, float] = {}
     fails = []
@@ -377,21 +403,26 @@ def test_2b_layerwise_teacher_forced(gpu, variant):
             errs.update(_layer_state_errors(cache, i, t["states"], 1024))
             record(f"prefill layer {i}", errs)
             print(f"prefill layer {i:2d} " + " ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
-        ctx = DecodeContext(cache, torch.tensor([[1025]], device=gpu), True)
-        token = torch.tensor([t2], device=gpu, dtype=torch.long)
-        for i in range(n):
-            t = d2[i]
-            _set_layer_state(cache, i, d1[i]["states"], 1025)
-            residual = update = None
-            if i:
-                residual, update = d2[i - 1]["residual_mid"].to(gpu), d2[i - 1]["mlp_out"].to(gpu)
-            got = {}
-            r, u = decode_layer(stack, i, residual, update, ctx, token, trace=got)
-            errs = {"update": _rel(got["update"], t["update"]),
-                    "residual_mid": _rel(r, t["residual_mid"]),
-                    "mlp_out": _rel(u, t["mlp_out"])}
-            errs.update(_layer_state_errors(cache, i, t["states"], 1026))
-            record(f"decode layer {i}", errs)
-            print(f"decode layer {i:2d} " + " ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+        # decode step s consumes its token at position 1024 + s - 1, from the
+        # states after step s - 1
+        for step, prev, cur, tok_in in ((2, d1, d2, t2), (LATE, dprev, dlate, t_late)):
+            at = 1024 + step - 1
+            ctx = DecodeContext(cache, torch.tensor([[at]], device=gpu), True)
+            token = torch.tensor([tok_in], device=gpu, dtype=torch.long)
+            for i in range(n):
+                t = cur[i]
+                _set_layer_state(cache, i, prev[i]["states"], at)
+                residual = update = None
+                if i:
+                    residual, update = cur[i - 1]["residual_mid"].to(gpu), cur[i - 1]["mlp_out"].to(gpu)
+                got = {}
+                r, u = decode_layer(stack, i, residual, update, ctx, token, trace=got)
+                errs = {"update": _rel(got["update"], t["update"]),
+                        "residual_mid": _rel(r, t["residual_mid"]),
+                        "mlp_out": _rel(u, t["mlp_out"])}
+                errs.update(_layer_state_errors(cache, i, t["states"], at + 1))
+                record(f"decode step {step} layer {i}", errs)
+                print(f"decode step {step} layer {i:2d} " + " ".join(f"{k} {v:.2e}" for k, v in errs.items()),
+                      flush=True)
     print(f"{variant}: worst per quantity " + " ".join(f"{k} {v:.2e}" for k, v in worst.items()), flush=True)
     assert not fails, fails
