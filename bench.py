@@ -504,8 +504,7 @@ def counter_probe(dev) -> None:
     torch.cuda.synchronize()
     del states
     log("counter probe: delta step done; prefill GEMMs ...")
-    for (n, k, swiglu) in ((8320, 2048, False), (2048, 2048, False), (5120, 2048, False),
-                           (12288, 2048, True), (2048, 6144, False)):
+    for (n, k, swiglu) in PROBE_GEMMS:
         x = torch.randn(1024, k, device=dev, generator=g).to(bf)
         wt = (torch.randn(n, k, device=dev, generator=g) * 0.02).to(bf)
         xq, sx = K.quantize_act_i8(x)
@@ -694,41 +693,58 @@ def pmc_summary(fetch_csv: str, write_csv: str, rescore_rows: int | None = None)
         print(f"{name} | {fetch[name]:.1f} | {write[name]:.1f} | {traffic} | {algo or '-'} | {ratio}")
 
 
+# The prefill GEMM launches of --counter-probe, in program order: per shape
+# (N, K, SwiGLU), 3 bf16 launches then 3 int8 launches.
+PROBE_GEMMS = ((8320, 2048, False), (2048, 2048, False), (5120, 2048, False), (12288, 2048, True),
+               (2048, 6144, False))
+
+
 def mfma_summary(pmc_csv: str, trace_csv: str) -> None:
     """Print the matrix-core use of the prefill GEMMs of a ``--counter-probe``
     run: one ``rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16
     SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE`` pass
-    and one ``--kernel-trace`` pass, matched by kernel name and grid size:
+    and one ``--kernel-trace`` pass. The GEMM dispatches of both runs are taken
+    in program order and labelled with the probe's shapes (PROBE_GEMMS):
     operations = MOPS x 512, MFMA busy = busy cycles / (GRBM_GUI_ACTIVE / 8
     XCDs x 1024 SIMDs)."""
     import csv
     from collections import defaultdict
 
-    def key(row):
-        n = row["Kernel_Name"].replace("(anonymous namespace)::", "")
-        return (n[5:] if n.startswith("void ") else n).split("(")[0].strip(), row.get("Grid_Size", "")
+    def short(name):
+        n = name.replace("(anonymous namespace)::", "")
+        return (n[5:] if n.startswith("void ") else n).split("(")[0].strip()
 
-    cnt = defaultdict(lambda: defaultdict(list))
+    per = defaultdict(dict)
+    names = {}
     with open(pmc_csv) as f:
         for row in csv.DictReader(f):
             if "gemm_ring" in row["Kernel_Name"]:
-                cnt[key(row)][row["Counter_Name"]].append(float(row["Counter_Value"]))
-    dur = defaultdict(list)
+                d = int(row["Dispatch_Id"])
+                per[d][row["Counter_Name"]] = float(row["Counter_Value"])
+                names[d] = short(row["Kernel_Name"])
+    cnt = [(names[d], per[d]) for d in sorted(per)]
     with open(trace_csv) as f:
-        for row in csv.DictReader(f):
-            if "gemm_ring" in row["Kernel_Name"]:
-                dur[key(row)].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
-    print("kernel | grid | T(FL)OPs per launch | us | T(FL)OP/s | of dense peak | MFMA busy")
-    for k, c in cnt.items():
-        mean = {n: sum(v) / len(v) for n, v in c.items()}
-        i8 = mean.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) > mean.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        rows = [r for r in csv.DictReader(f) if "gemm_ring" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows]
+    labels = [f"{n}x{k}{' SwiGLU' if sw else ''} {kind}" for n, k, sw in PROBE_GEMMS
+              for kind in ("bf16", "int8") for _ in range(3)]
+    # the probe's GEMM phase comes last (the model's own prefill GEMMs before it)
+    if len(cnt) < len(labels) or len(dur) < len(labels):
+        raise SystemExit(f"expected {len(labels)} GEMM dispatches, got {len(cnt)} counted / {len(dur)} traced")
+    cnt, dur = cnt[-len(labels):], dur[-len(labels):]
+    print("shape (M = 1024) | kernel | T(FL)OPs per launch | us | T(FL)OP/s | of dense peak | MFMA busy")
+    for i in range(0, len(labels), 3):
+        name = cnt[i][0]
+        mean = {c: sum(cnt[j][1].get(c, 0.0) for j in range(i, i + 3)) / 3 for c in cnt[i][1]}
+        i8 = "int8" in labels[i]
         ops = 512 * mean.get("SQ_INSTS_VALU_MFMA_MOPS_I8" if i8 else "SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
-        us = sum(dur[k]) / len(dur[k]) if dur.get(k) else float("nan")
+        us = sum(dur[i:i + 3]) / 3
         peak = 5000.0 if i8 else 2500.0
         active = mean.get("GRBM_GUI_ACTIVE", 0.0) / 8
         busy = mean.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (active * 1024) if active else float("nan")
         rate = ops / us / 1e6
-        print(f"{k[0]} | {k[1]} | {ops / 1e12:.4f} | {us:.2f} | {rate:.1f} | {rate / peak:.3f} | {busy:.3f}")
+        print(f"{labels[i]} | {name} | {ops / 1e12:.4f} | {us:.2f} | {rate:.1f} | {rate / peak:.3f} | {busy:.3f}")
 
 
 def cpu_baseline(state, cfg, prompt, decode_steps: int, eager: bool = True) -> dict:
