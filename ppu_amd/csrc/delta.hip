@@ -539,44 +539,71 @@ __global__ __launch_bounds__(64) void delta_scan(const uint16_t* __restrict__ qk
 // ------------------------------------------------------- chunked prefill
 // The recurrence over a chunk of C = 64 tokens in closed form (the UT / WY
 // representation of the delta rule), so that the sequential dependence is
-// over L/64 chunks instead of L tokens and the work is matrix products on
-// the fp32 matrix cores (v_mfma_f32_16x16x4f32). Per head, with k and q the
-// scaled vectors of the recurrence (k*k_inv, q*q_inv/sqrt(D)), G_i the
-// cumulative log-decay inside the chunk and gamma_i = e^{G_i}:
-//   A[i][j] = beta_i e^{G_i-G_j} (k_i . k_j)  (j < i),   T = (I + A)^{-1}
+// over L/64 chunks instead of L tokens and the work is matrix products. Per
+// head, with q, k, v the raw (bf16) conv outputs of the chunk, q_inv, k_inv
+// their norm factors, K = diag(k_inv) k and Q = diag(q_inv / sqrt(D)) q the
+// scaled vectors of the recurrence, G_i the cumulative log-decay inside the
+// chunk and gamma_i = e^{G_i}:
+//   A[i][j] = beta_i e^{G_i-G_j} (K_i . K_j)  (j < i),   T = (I + A)^{-1}
 //   W = T diag(beta gamma) K,   U0 = T diag(beta) V      (independent of S)
 //   U = U0 - W S                                           (the delta vectors)
-//   O = diag(gamma) Q S + P U,  P[i][j] = e^{G_i-G_j} (q_i . k_j)  (j <= i)
-//   S <- gamma_C S + K''^T U,   K''[j] = e^{G_C-G_j} k_j
+//   O = diag(gamma) Q S + P U,  P[i][j] = e^{G_i-G_j} (Q_i . K_j)  (j <= i)
+//   S <- gamma_C S + K''^T U,   K''[j] = e^{G_C-G_j} K_j
 // which is the token loop unrolled exactly (every decay factor is e^{a-b}
-// with a <= b, so nothing overflows). Padding tokens past L carry k = q = v =
+// with a <= b, so nothing overflows). Padding tokens past L carry q = k = v =
 // 0, g = 0, beta = 0 and leave S unchanged.
-//   delta_chunk_prep : one workgroup per (chunk, head): A and P from K K^T and
-//     K Q^T, T by 16 x 16 blocks (diagonal blocks by forward substitution,
-//     the rest as MFMA products), W^T and U0, and Q' = diag(gamma) Q, K''^T,
-//     all written in the per-lane order of the MFMA operands that
-//     delta_chunk_scan consumes (coalesced float4 loads).
+//
+// The products run on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16, fp32
+// accumulation). q, k and v are bf16 values, so a product with one of them
+// as an operand is exact in the MFMA; the scale factors are applied outside:
+// K K^T and Q K^T are products of the raw rows, W = (T diag(beta gamma
+// k_inv)) k, U0 = (T diag(beta)) v, diag(gamma) Q S = diag(sc) (q S) with sc =
+// gamma q_inv / sqrt(D), and K''^T U = k^T (diag(f) U) with f_j = e^{G_C-G_j}
+// k_inv_j. An fp32 operand x is split into x_hi = bf16(x) and x_lo = bf16(x -
+// x_hi), |x - x_hi - x_lo| <= 2^-18 |x|: its product with a bf16 operand b is
+// x_hi b + x_lo b (two MFMAs), a product of two fp32 operands x_hi y_hi +
+// x_hi y_lo + x_lo y_hi (three; the dropped x_lo y_lo is below 2^-16 of the
+// product). The operands whose rounding reaches the state directly, the
+// scaled rows of T (into W and U0) and diag(f) U (into S), are split in three
+// (x_mid = bf16(x - x_hi), x_lo = bf16(x - x_hi - x_mid), within 2^-27 |x|):
+// with that the state stays within the fp32 token loop's own rounding of an
+// exact evaluation, where two-part splits of these operands left errors ~40x
+// larger. The triangular solve for T stays in fp32 (v_mfma_f32_16x16x4f32).
+//   delta_chunk_prep : one workgroup per (chunk, head): conv, factors, A and
+//     P, T by 16 x 16 blocks (diagonal blocks by forward substitution, the
+//     rest as MFMA products), W and U0, and every operand of the two later
+//     kernels, written in their per-lane MFMA operand order (coalesced 1 KiB
+//     rows of 16-byte lane entries).
 //   delta_chunk_scan : one workgroup per (16-column v tile, head): the
 //     [128 x 16] state tile in LDS and only the recurrence (U = U0 - W S,
 //     S <- gamma_C S + K''^T U) per chunk; the state entering each chunk and
-//     U are stored as snapshots.
+//     U are stored as split operands of the output kernel.
 //   delta_chunk_out  : one workgroup per (chunk, head), all in parallel:
-//     O = Q' S + P U from the snapshots (the output products do not feed
-//     the next chunk, so they leave the sequential loop).
-// MFMA 16x16x4 f32 (wave64): A[16x4]: lane l holds row l%16, k l/16;
-// B[4x16]: k l/16, column l%16; C: rows 4*(l/16) + e, column l%16.
+//     O = diag(sc) (q S) + P U from the snapshots.
+// MFMA 16x16x32 bf16 (wave64): A[16 x 32]: lane l holds row l%16, 8
+// consecutive k at 8*(l/16); B[32 x 16]: column l%16, the same 8 k; C[16 x
+// 16]: rows 4*(l/16) + e (e < 4) of column l%16. The fp32 16x16x4 form has
+// A: row l%16, k l/16; B: k l/16, column l%16; the same C.
 constexpr int kChunk = 64;
-constexpr int kCS = 132;  // fp32 row stride of the K / Q / V chunk tiles in LDS
+constexpr int kRS = 136;  // bf16 row stride of the raw q / k / v tiles in LDS
 constexpr int kAS = 68;   // fp32 row stride of A and of T
-constexpr int kSS = 17;   // fp32 row stride of the state and U tiles in LDS
-// Workspace floats per (batch, head, chunk): W^T, Q', K''^T, P, U0.
-constexpr int kOffWT = 0, kOffQP = 8192, kOffKT = 16384, kOffPQ = 24576, kOffU0 = 28672;
-constexpr int kChunkFloats = 36864;
-// Snapshot floats per (batch, head, chunk), in the B-operand order of the
-// output kernel's MFMAs (lane (col, g4) of 16x16x4 step group s reads the
-// float4 of rows 16s + 4g4 .. +3, column col): the state entering the chunk
-// as [v tile][k tile][lane] float4 (2048 floats per v tile), then U as
-// [v tile][token tile][lane] float4 (1024 floats per v tile) from kSnapU.
+constexpr int kXS = 36;   // fp32 row stride of the per-wave transpose tiles
+constexpr float kQScale = 0.08838834764831845f;  // 1 / sqrt(D)
+// Workspace floats per (batch, head, chunk); every operand is a row of 64
+// lane entries of 16 bytes (8 bf16, or a float4 for U0):
+//   W   [row tile 4][k step 4][hi, lo]   A operand of W S
+//   U0  [row tile 4][v tile 8]           C layout
+//   kT  [k tile 8][t step 2]             A operand of k^T (diag(f) U)
+//   q   [row tile 4][k step 4]           A operand of q S
+//   P   [row tile 4][t step 2][hi, lo]   A operand of P U (zero above the diagonal)
+//   f [64], sc [64]
+constexpr int kOffW = 0, kOffU0 = 8192, kOffKT = 16384, kOffQ = 20480, kOffP = 24576,
+              kOffF = 28672, kOffSc = 28736;
+constexpr int kChunkFloats = 28800;
+// Snapshot floats per (batch, head, chunk): the state entering the chunk as
+// the B operand of q S, [v tile][k step 4][hi, lo] (2048 floats per v tile),
+// then U as the B operand of P U, [v tile][t step 2][hi, lo] (1024 floats per
+// v tile) from kSnapU.
 constexpr int kSnapSTile = 2048, kSnapU = 8 * kSnapSTile, kSnapUTile = 1024;
 constexpr int kSnapFloats = kSnapU + 8 * kSnapUTile;
 
@@ -584,16 +611,47 @@ Q35_DEV q35_f32x4 mfma4(float a, float b, q35_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Four consecutive 4-k MFMA steps with the lane's float4 operands, alternating
-// between two accumulators (c0 takes steps 0 and 2, c1 steps 1 and 3).
-Q35_DEV void mma4(const float4 a, const float4 bv, q35_f32x4 c0, q35_f32x4 c1, q35_f32x4& o0,
-                  q35_f32x4& o1) {
-  c0 = mfma4(a.x, bv.x, c0);
-  c1 = mfma4(a.y, bv.y, c1);
-  c0 = mfma4(a.z, bv.z, c0);
-  c1 = mfma4(a.w, bv.w, c1);
-  o0 = c0;
-  o1 = c1;
+Q35_DEV q35_f32x4 mfma_bf(const uint4 a, const uint4 b, q35_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(q35_bf16x8, a),
+                                                 __builtin_bit_cast(q35_bf16x8, b), c, 0, 0, 0);
+}
+
+// x = hi + lo (+ a remainder below 2^-18 |x|) for 8 fp32 values: hi = bf16(x)
+// (round to nearest even), lo = bf16(x - hi) (x - hi is exact in fp32).
+struct Split8 {
+  uint4 hi, lo;
+};
+Q35_DEV Split8 split8(const float4 a, const float4 b) {
+  const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    h[p] = pack_bf2(x[2 * p], x[2 * p + 1]);
+    l[p] = pack_bf2(x[2 * p] - bf_lo(h[p]), x[2 * p + 1] - bf_hi(h[p]));
+  }
+  return Split8{make_uint4(h[0], h[1], h[2], h[3]), make_uint4(l[0], l[1], l[2], l[3])};
+}
+
+// The same in three parts: x = hi + mid + lo within 2^-27 |x|.
+struct Split8x3 {
+  uint4 hi, mid, lo;
+};
+Q35_DEV Split8x3 split8x3(const float4 a, const float4 b) {
+  const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[4], m[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    h[p] = pack_bf2(x[2 * p], x[2 * p + 1]);
+    const float r0 = x[2 * p] - bf_lo(h[p]), r1 = x[2 * p + 1] - bf_hi(h[p]);
+    m[p] = pack_bf2(r0, r1);
+    l[p] = pack_bf2(r0 - bf_lo(m[p]), r1 - bf_hi(m[p]));
+  }
+  return Split8x3{make_uint4(h[0], h[1], h[2], h[3]), make_uint4(m[0], m[1], m[2], m[3]),
+                  make_uint4(l[0], l[1], l[2], l[3])};
+}
+
+Q35_DEV float4 mul4(const float4 a, const float4 b) {
+  return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
 }
 
 // Optional inputs of chunk prep: with CONV, qkv is the raw packed projection
@@ -622,19 +680,15 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   const int lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g4 = lane >> 4;
   const size_t bhc = ((size_t)b * H + h) * nC + c;
-  __shared__ alignas(16) float Kh[kChunk * kCS];
-  __shared__ alignas(16) float Qh[kChunk * kCS];
-  __shared__ alignas(16) float Vv[kChunk * kCS];
-  __shared__ alignas(16) float Am[kChunk * kAS];  // A (strictly lower)
-  __shared__ alignas(16) float Tm[kChunk * kAS];  // T = (I + A)^{-1} (lower)
-  __shared__ alignas(16) float Xs[4][16 * 17];     // per-wave 16 x 16 scratch
-  __shared__ float G_s[kChunk], gam_s[kChunk], kf_s[kChunk], bg_s[kChunk], b_s[kChunk];
+  float* wsb = ws + bhc * kChunkFloats;
+  __shared__ alignas(16) uint16_t Qr[kChunk * kRS];  // raw q, k, v rows (bf16)
+  __shared__ alignas(16) uint16_t Kr[kChunk * kRS];
+  __shared__ alignas(16) uint16_t Vr[kChunk * kRS];
+  __shared__ alignas(16) float Am[kChunk * kAS];     // A (strictly lower)
+  __shared__ alignas(16) float Tm[kChunk * kAS];     // T = (I + A)^{-1} (lower)
+  __shared__ alignas(16) float Xs[4][kChunk * kXS];  // per-wave transpose tiles
+  __shared__ alignas(16) float G_s[kChunk], b_s[kChunk], qinv_s[kChunk], kinv_s[kChunk], wsc_s[kChunk];
 
-  // 1. the chunk's k, q (scaled as the recurrence scales them) and v in fp32,
-  //    with the per-token factors of the token loop computed here: q_inv,
-  //    k_inv = rsqrt(sum of squares + 1e-6) over the head (the 4 threads of a
-  //    token hold 32 dims each: quad sum), g = -e^{A_log} softplus(a +
-  //    dt_bias), beta = sigmoid(b) [reference kernels.py:713-765].
   // The token's gate inputs and the head's parameters, requested first (with
   // CONV they are then in flight during the conv below).
   const int ti = tid >> 2;
@@ -643,15 +697,15 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   const float a_raw = bf2f(prow0[a_off + h]), b_raw = bf2f(prow0[b_off + h]);
   const float alog = ld_param(a_log, h, PF32), dtb = ld_param(dt_bias, h, PF32);
   if (CONV) {
-    // 0. the conv of this chunk and head into Qh / Kh / Vv (fp32 copies of
-    //    the bf16 conv outputs): thread item = (8-channel group of q, k or v;
-    //    16 tokens), its 19 input rows (16 + 3 before; rows before token 0
-    //    are zero) and 4 x 8 taps loaded before any is used.
+    // 0. the conv of this chunk and head into Qr / Kr / Vr: thread item =
+    //    (8-channel group of q, k or v; 16 tokens), its 19 input rows (16 + 3
+    //    before; rows before token 0 are zero) and 4 x 8 taps loaded before
+    //    any is used.
     if (tid < 192) {
       const int gsel = tid % 48, i0 = (tid / 48) * 16;
       const int arr = gsel >> 4, d = (gsel & 15) * 8;
       const int ch = arr * H * kD + h * kD + d;  // conv channel of the group
-      float* dst = arr == 0 ? Qh : (arr == 1 ? Kh : Vv);
+      uint16_t* dst = arr == 0 ? Qr : (arr == 1 ? Kr : Vr);
       uint4 raw[19], wr[4];
 #pragma unroll
       for (int r = 0; r < 19; ++r) {
@@ -686,11 +740,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
           for (int tap = 0; tap < 4; ++tap) acc = fmaf(xr[j + tap][e], wt[e][tap], acc);
           o[e] = silu_fast(round_bf(acc));
         }
-        float ob[8];
-        unpack8(pack8(o), ob);  // the conv output is bf16
-        float* dr = dst + (i0 + j) * kCS + d;
-        *reinterpret_cast<float4*>(dr) = make_float4(ob[0], ob[1], ob[2], ob[3]);
-        *reinterpret_cast<float4*>(dr + 4) = make_float4(ob[4], ob[5], ob[6], ob[7]);
+        *reinterpret_cast<uint4*>(dst + (i0 + j) * kRS + d) = pack8(o);  // the conv output is bf16
         const int pos = t - (L - 4);
         if (t < L && pos >= 0) {
 #pragma unroll
@@ -701,79 +751,75 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
     }
     __syncthreads();
   }
+
+  // 1. per token (4 threads, 32 dims each): q_inv, k_inv = rsqrt(sum of
+  //    squares + 1e-6) over the head (quad sum), g = -e^{A_log} softplus(a +
+  //    dt_bias), beta = sigmoid(b) [reference kernels.py:713-765]. The raw
+  //    rows of tokens past L become zeros; the q rows are also the output
+  //    kernel's A operand (row tile i/16, k step = the thread's quarter,
+  //    lane (i%16) + 16u for its 8-dim group u).
   {
-    const int i = tid >> 2, qq = tid & 3;  // token, 32-dim quarter
+    const int i = tid >> 2, qq = tid & 3;
     const int t = c * kChunk + i;
     const bool live = t < L;
-    const int tc = min(t, L - 1);
-    const uint16_t* row = qkv + ((size_t)b * L + tc) * qkv_stride;
-    float rq[4][8], rk[4][8];
-    uint4 rv[4];
+    uint4 rq[4], rk[4], rv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int d = qq * 32 + u * 8;
       if (CONV) {
-        const float* sq = &Qh[i * kCS + d];
-        const float* sk = &Kh[i * kCS + d];
-        const float* sv = &Vv[i * kCS + d];
-        float fv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          rq[u][e] = sq[e];
-          rk[u][e] = sk[e];
-          fv[e] = sv[e];
-        }
-        rv[u] = pack8(fv);  // exact: the values are bf16
+        rq[u] = *reinterpret_cast<const uint4*>(&Qr[i * kRS + d]);
+        rk[u] = *reinterpret_cast<const uint4*>(&Kr[i * kRS + d]);
+        rv[u] = *reinterpret_cast<const uint4*>(&Vr[i * kRS + d]);
       } else {
-        unpack8(*reinterpret_cast<const uint4*>(row + h * kD + d), rq[u]);
-        unpack8(*reinterpret_cast<const uint4*>(row + H * kD + h * kD + d), rk[u]);
+        const uint16_t* row = qkv + ((size_t)b * L + min(t, L - 1)) * qkv_stride;
+        rq[u] = *reinterpret_cast<const uint4*>(row + h * kD + d);
+        rk[u] = *reinterpret_cast<const uint4*>(row + H * kD + h * kD + d);
         rv[u] = *reinterpret_cast<const uint4*>(row + 2 * H * kD + h * kD + d);
       }
     }
     float qs = 0.f, ks = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < 4; ++u) {
+      float fq[8], fk[8];
+      unpack8(rq[u], fq);
+      unpack8(rk[u], fk);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        qs += rq[u][e] * rq[u][e];
-        ks += rk[u][e] * rk[u][e];
+        qs += fq[e] * fq[e];
+        ks += fk[e] * fk[e];
       }
+    }
     qs += __shfl_xor(qs, 1, 64);
     ks += __shfl_xor(ks, 1, 64);
     qs += __shfl_xor(qs, 2, 64);
     ks += __shfl_xor(ks, 2, 64);
-    const float4 f = make_float4(rsqrt_cr(qs + 1e-6f), rsqrt_cr(ks + 1e-6f),
-                                 -expf(alog) * softplus20(a_raw + dtb), 1.0f / (1.0f + expf(-b_raw)));
-    const float qscale = 0.08838834764831845f;
+    if (!live) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int d = qq * 32 + u * 8;
-      float fq[8], fk[8], fv[8];
-      unpack8(rv[u], fv);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fq[e] = live ? rq[u][e] * f.x * qscale : 0.f;
-        fk[e] = live ? rk[u][e] * f.y : 0.f;
-        fv[e] = live ? fv[e] : 0.f;
-      }
-      float* qd = &Qh[i * kCS + d];
-      float* kd = &Kh[i * kCS + d];
-      float* vd = &Vv[i * kCS + d];
-      *reinterpret_cast<float4*>(qd) = make_float4(fq[0], fq[1], fq[2], fq[3]);
-      *reinterpret_cast<float4*>(qd + 4) = make_float4(fq[4], fq[5], fq[6], fq[7]);
-      *reinterpret_cast<float4*>(kd) = make_float4(fk[0], fk[1], fk[2], fk[3]);
-      *reinterpret_cast<float4*>(kd + 4) = make_float4(fk[4], fk[5], fk[6], fk[7]);
-      *reinterpret_cast<float4*>(vd) = make_float4(fv[0], fv[1], fv[2], fv[3]);
-      *reinterpret_cast<float4*>(vd + 4) = make_float4(fv[4], fv[5], fv[6], fv[7]);
+      for (int u = 0; u < 4; ++u) rq[u] = rk[u] = rv[u] = make_uint4(0u, 0u, 0u, 0u);
     }
+    if (!CONV || !live) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int d = qq * 32 + u * 8;
+        *reinterpret_cast<uint4*>(&Qr[i * kRS + d]) = rq[u];
+        *reinterpret_cast<uint4*>(&Kr[i * kRS + d]) = rk[u];
+        *reinterpret_cast<uint4*>(&Vr[i * kRS + d]) = rv[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      *reinterpret_cast<uint4*>(wsb + kOffQ + (((i >> 4) * 4 + qq) * 64 + (i & 15) + 16 * u) * 4) = rq[u];
     if (qq == 0) {
-      G_s[i] = live ? f.z : 0.f;  // g = log alpha, summed below
-      b_s[i] = live ? f.w : 0.f;
+      qinv_s[i] = rsqrt_cr(qs + 1e-6f);
+      kinv_s[i] = rsqrt_cr(ks + 1e-6f);
+      G_s[i] = live ? -expf(alog) * softplus20(a_raw + dtb) : 0.f;  // g = log alpha, summed below
+      b_s[i] = live ? 1.0f / (1.0f + expf(-b_raw)) : 0.f;
     }
   }
   __syncthreads();
 
-  // 2. cumulative log-decay G (inclusive scan over the chunk, wave 0).
+  // 2. cumulative log-decay G (inclusive scan over the chunk, wave 0) and the
+  //    per-token scales: f, sc (to the workspace) and beta gamma k_inv (W).
   if (wid == 0) {
     float gs = G_s[lane];
 #pragma unroll
@@ -782,61 +828,60 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
       if (lane >= o) gs += up;
     }
     const float glast = __shfl(gs, 63, 64);
+    const float gam = expf(gs), ki = kinv_s[lane];
     G_s[lane] = gs;
-    gam_s[lane] = expf(gs);
-    kf_s[lane] = expf(glast - gs);
-    bg_s[lane] = b_s[lane] * expf(gs);
+    wsc_s[lane] = b_s[lane] * gam * ki;
+    wsb[kOffF + lane] = expf(glast - gs) * ki;
+    wsb[kOffSc + lane] = gam * qinv_s[lane] * kQScale;
     if (lane == 0) gc_out[bhc] = expf(glast);
   }
   __syncthreads();
 
-  float* wsb = ws + bhc * kChunkFloats;
-  // 3. A (into LDS) and P (to the workspace) on the 10 tiles (rt, jt <= rt)
-  //    of the lower block triangle, 3/3/2/2 tiles per wave. Operands are
-  //    float4 reads of 4 consecutive dims: lane (col, g4) feeds dims
-  //    16s + 4g4 + e to MFMA e of step s, for both operands.
+  // 3. A (into LDS) and P (split, to the workspace) on the lower block
+  //    triangle. P is exported by (row tile rt, t step s) groups of two tiles
+  //    (jt = 2s, 2s + 1; a tile above the diagonal is zero), each group on one
+  //    wave, so its transpose goes through the wave's own tile: wave 0 takes
+  //    (3, 0) and (0, 0), wave 1 (3, 1) and (2, 1), wave 2 (1, 0), wave 3
+  //    (2, 0): 3/3/2/2 tiles. Operands are raw rows of 16 bytes.
   {
-    const unsigned packed = wid == 0 ? 0x540u : (wid == 1 ? 0xA98u : (wid == 2 ? 0x0DCu : 0x0FEu));
-    const int count = wid < 2 ? 3 : 2;
-    for (int n = 0; n < count; ++n) {
-      const int tj = (packed >> (4 * n)) & 15;
-      const int rt = tj >> 2, jt = tj & 3;
-      q35_f32x4 kk0 = {0.f, 0.f, 0.f, 0.f}, kk1 = kk0, kq0 = kk0, kq1 = kk0;
-      const float* ki = &Kh[(16 * rt + col) * kCS + 4 * g4];
-      const float* kj = &Kh[(16 * jt + col) * kCS + 4 * g4];
-      const float* qi = &Qh[(16 * rt + col) * kCS + 4 * g4];
-#pragma unroll 4
-      for (int st = 0; st < 8; ++st) {
-        const float4 x = *reinterpret_cast<const float4*>(ki + 16 * st);
-        const float4 y = *reinterpret_cast<const float4*>(kj + 16 * st);
-        const float4 z = *reinterpret_cast<const float4*>(qi + 16 * st);
-        kk0 = mfma4(x.x, y.x, kk0);  // (K K^T)[i][j]
-        kq0 = mfma4(y.x, z.x, kq0);  // (K Q^T)[j][i]
-        kk1 = mfma4(x.y, y.y, kk1);
-        kq1 = mfma4(y.y, z.y, kq1);
-        kk0 = mfma4(x.z, y.z, kk0);
-        kq0 = mfma4(y.z, z.z, kq0);
-        kk1 = mfma4(x.w, y.w, kk1);
-        kq1 = mfma4(y.w, z.w, kq1);
-      }
-      const q35_f32x4 kk = kk0 + kk1, kq = kq0 + kq1;
+    const unsigned groups = wid == 0 ? 0x0300u : (wid == 1 ? 0x0607u : (wid == 2 ? 0x01u : 0x02u));
+    const int ng = wid < 2 ? 2 : 1;
+    float* xs = Xs[wid];
+    for (int n = 0; n < ng; ++n) {
+      const int gi = (groups >> (8 * n)) & 0xff;
+      const int rt = gi & 3, s = gi >> 2;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 16 * rt + 4 * g4 + e, j = 16 * jt + col;
-        Am[i * kAS + j] = j < i ? b_s[i] * expf(G_s[i] - G_s[j]) * kk[e] : 0.f;
-      }
-      float4 pq;
-      {
-        const int i = 16 * rt + col;
-        float v[4];
+      for (int jj = 0; jj < 2; ++jj) {
+        const int jt = 2 * s + jj;
+        q35_f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
+        if (jt <= rt) {
+          const uint16_t* ki = &Kr[(16 * rt + col) * kRS + 8 * g4];
+          const uint16_t* kj = &Kr[(16 * jt + col) * kRS + 8 * g4];
+          const uint16_t* qi = &Qr[(16 * rt + col) * kRS + 8 * g4];
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            const uint4 x = *reinterpret_cast<const uint4*>(ki + 32 * st);
+            const uint4 y = *reinterpret_cast<const uint4*>(kj + 32 * st);
+            const uint4 z = *reinterpret_cast<const uint4*>(qi + 32 * st);
+            kk = mfma_bf(x, y, kk);  // (k k^T)[i][j]
+            qk = mfma_bf(z, y, qk);  // (q k^T)[i][j]
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int j = 16 * jt + 4 * g4 + e;
-          v[e] = j <= i ? expf(G_s[i] - G_s[j]) * kq[e] : 0.f;
+          const int i = 16 * rt + 4 * g4 + e, j = 16 * jt + col;
+          const float dec = j <= i ? expf(G_s[i] - G_s[j]) : 0.f;
+          if (jt <= rt) Am[i * kAS + j] = j < i ? b_s[i] * (kinv_s[i] * kinv_s[j]) * dec * kk[e] : 0.f;
+          xs[(4 * g4 + e) * kXS + 16 * jj + col] = qinv_s[i] * kQScale * kinv_s[j] * dec * qk[e];
         }
-        pq = make_float4(v[0], v[1], v[2], v[3]);
       }
-      *reinterpret_cast<float4*>(wsb + kOffPQ + ((rt * 4 + jt) * 64 + lane) * 4) = pq;
+      // the group as the A operand (row 16 rt + l%16, columns 32 s + 8(l/16)
+      // .. +7); the wave's own LDS stores complete before its later reads
+      const float* pr = &xs[col * kXS + 8 * g4];
+      const Split8 sp = split8(*reinterpret_cast<const float4*>(pr), *reinterpret_cast<const float4*>(pr + 4));
+      uint4* dp = reinterpret_cast<uint4*>(wsb + kOffP) + (rt * 2 + s) * 128 + lane;
+      dp[0] = sp.hi;
+      dp[64] = sp.lo;
     }
   }
   __syncthreads();
@@ -844,7 +889,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   // 4. T = (I + A)^{-1} by 16 x 16 blocks (A strictly lower triangular):
   //    T_II = (I + A_II)^{-1} by forward substitution (wave I, lane = column),
   //    then T_IJ = -T_II sum_{K=J}^{I-1} A_IK T_KJ level by level (I - J =
-  //    1, 2, 3) as 16 x 16 x 16 MFMA products, one block per wave.
+  //    1, 2, 3) as 16 x 16 x 16 fp32 MFMA products, one block per wave.
   {
     const int I = wid, j = lane & 15;
     float t[16];
@@ -887,58 +932,101 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
     __syncthreads();
   }
 
-  // 5. W^T = K^T diag(beta gamma) T^T and U0 = T diag(beta) V on the matrix
-  //    cores for every (row tile rt, dim tile dt), wave w taking dt = 2w and
-  //    2w + 1 (T is lower triangular: only j < 16(rt + 1) contribute, so the
-  //    work per wave is equal); Q' and K''^T elementwise.
+  // 5. W = (T diag(beta gamma k_inv)) k and U0 = (T diag(beta)) v for the
+  //    wave's two dim (v) tiles dt = 2 wid + dd and every row tile: the T rows
+  //    are split, the k / v columns (8 consecutive tokens of one dim; the kT
+  //    operand of the scan) are exact. T is lower triangular: row tile rt
+  //    needs the t steps s <= rt/2, and the lane's 8 columns of block
+  //    2s + (l/16)/2 are zero when that block is above the diagonal.
   {
+    uint4 kop[2][2], vop[2][2];
 #pragma unroll
-    for (int dd = 0; dd < 2; ++dd) {
-      const int dt = 2 * wid + dd;
+    for (int dd = 0; dd < 2; ++dd)
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        q35_f32x4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = w0, u0 = w0, u1 = w0;
+      for (int s = 0; s < 2; ++s) {
+        const int dim = 16 * (2 * wid + dd) + col;
+        const uint16_t* kc = &Kr[(32 * s + 8 * g4) * kRS + dim];
+        const uint16_t* vc = &Vr[(32 * s + 8 * g4) * kRS + dim];
+        uint32_t kw[4], vw[4];
 #pragma unroll
-        for (int st = 0; st < 4 * (rt + 1); st += 2) {
-          const int j0 = 4 * st + g4, j1 = j0 + 4;
-          const float t0 = Tm[(16 * rt + col) * kAS + j0];
-          const float t1 = Tm[(16 * rt + col) * kAS + j1];
-          w0 = mfma4(bg_s[j0] * Kh[j0 * kCS + 16 * dt + col], t0, w0);
-          u0 = mfma4(t0, b_s[j0] * Vv[j0 * kCS + 16 * dt + col], u0);
-          w1 = mfma4(bg_s[j1] * Kh[j1 * kCS + 16 * dt + col], t1, w1);
-          u1 = mfma4(t1, b_s[j1] * Vv[j1 * kCS + 16 * dt + col], u1);
+        for (int p = 0; p < 4; ++p) {
+          kw[p] = (uint32_t)kc[2 * p * kRS] | ((uint32_t)kc[(2 * p + 1) * kRS] << 16);
+          vw[p] = (uint32_t)vc[2 * p * kRS] | ((uint32_t)vc[(2 * p + 1) * kRS] << 16);
         }
-        const q35_f32x4 w = w0 + w1, u = u0 + u1;
-        *reinterpret_cast<float4*>(wsb + kOffWT + ((rt * 8 + dt) * 64 + lane) * 4) =
-            make_float4(w[0], w[1], w[2], w[3]);
-        *reinterpret_cast<float4*>(wsb + kOffU0 + ((rt * 8 + dt) * 64 + lane) * 4) =
-            make_float4(u[0], u[1], u[2], u[3]);
-        const int i = 16 * rt + col;
-        const float gi = gam_s[i];
-        const float* qrow = &Qh[i * kCS + 16 * dt + 4 * g4];
-        *reinterpret_cast<float4*>(wsb + kOffQP + ((rt * 8 + dt) * 64 + lane) * 4) =
-            make_float4(qrow[0] * gi, qrow[1] * gi, qrow[2] * gi, qrow[3] * gi);
+        kop[dd][s] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+        vop[dd][s] = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+        *reinterpret_cast<uint4*>(wsb + kOffKT + (((2 * wid + dd) * 2 + s) * 64 + lane) * 4) = kop[dd][s];
+      }
+    float* xw = Xs[wid];  // W rows 0..63, columns 32 wid .. +31
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      q35_f32x4 w[2], u[2];
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd) w[dd] = u[dd] = q35_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s <= rt / 2; ++s) {
+        const int j0 = 32 * s + 8 * g4;
+        float4 t0 = make_float4(0.f, 0.f, 0.f, 0.f), t1 = t0;
+        if (2 * s + (g4 >> 1) <= rt) {
+          t0 = *reinterpret_cast<const float4*>(&Tm[(16 * rt + col) * kAS + j0]);
+          t1 = *reinterpret_cast<const float4*>(&Tm[(16 * rt + col) * kAS + j0 + 4]);
+        }
+        const Split8x3 sw = split8x3(mul4(t0, *reinterpret_cast<const float4*>(&wsc_s[j0])),
+                                     mul4(t1, *reinterpret_cast<const float4*>(&wsc_s[j0 + 4])));
+        const Split8x3 su = split8x3(mul4(t0, *reinterpret_cast<const float4*>(&b_s[j0])),
+                                     mul4(t1, *reinterpret_cast<const float4*>(&b_s[j0 + 4])));
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) {
+          w[dd] = mfma_bf(sw.hi, kop[dd][s], w[dd]);
+          u[dd] = mfma_bf(su.hi, vop[dd][s], u[dd]);
+        }
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) {
+          w[dd] = mfma_bf(sw.mid, kop[dd][s], w[dd]);
+          u[dd] = mfma_bf(su.mid, vop[dd][s], u[dd]);
+        }
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) {
+          w[dd] = mfma_bf(sw.lo, kop[dd][s], w[dd]);
+          u[dd] = mfma_bf(su.lo, vop[dd][s], u[dd]);
+        }
       }
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        float v[4];
+      for (int dd = 0; dd < 2; ++dd) {
+        *reinterpret_cast<float4*>(wsb + kOffU0 + ((rt * 8 + 2 * wid + dd) * 64 + lane) * 4) =
+            make_float4(u[dd][0], u[dd][1], u[dd][2], u[dd][3]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int j = 16 * s4 + 4 * g4 + e;
-          v[e] = kf_s[j] * Kh[j * kCS + 16 * dt + col];
-        }
-        *reinterpret_cast<float4*>(wsb + kOffKT + ((dt * 4 + s4) * 64 + lane) * 4) =
-            make_float4(v[0], v[1], v[2], v[3]);
+        for (int e = 0; e < 4; ++e) xw[(16 * rt + 4 * g4 + e) * kXS + 16 * dd + col] = w[dd][e];
       }
+    }
+    // W as the scan's A operand: row 16 rt + l%16, dims 32 wid + 8(l/16) .. +7
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const float* wr = &xw[(16 * rt + col) * kXS + 8 * g4];
+      const Split8 sp = split8(*reinterpret_cast<const float4*>(wr), *reinterpret_cast<const float4*>(wr + 4));
+      uint4* dp = reinterpret_cast<uint4*>(wsb + kOffW) + (rt * 4 + wid) * 128 + lane;
+      dp[0] = sp.hi;
+      dp[64] = sp.lo;
     }
   }
 }
 
-// State and U tiles are kept transposed in LDS ([column][row]) so that the
-// four k values a lane feeds to four consecutive MFMAs are one float4 read;
-// MFMA chains alternate between two accumulators.
-constexpr int kST = kD + 4;      // fp32 per transposed state column
-constexpr int kUT = kChunk + 4;  // fp32 per transposed U column
+// The fp32 state tile lives in registers, in the C layout of the state update
+// (wave w owns k tiles 2w and 2w + 1: rows 16 kt + 4(l/16) + e of column
+// l%16). LDS holds only its bf16 hi / lo parts, transposed ([column][k]) and
+// double-buffered, as the B operand of W S (8 consecutive k of one column:
+// one 16-byte read per part); each wave splits only its own rows. U likewise:
+// the wave that computes rows of U splits them (diag(f) U in three parts for
+// the state update, U in two for the snapshot) into transposed LDS tiles.
+constexpr int kSB = kD + 8;      // bf16 per transposed state column
+constexpr int kUB = kChunk + 8;  // bf16 per transposed U column
+
+// hi / lo (two parts) of 4 values as bf16 pairs
+Q35_DEV void split4(const float* x, uint2& hi, uint2& lo) {
+  const uint32_t h0 = pack_bf2(x[0], x[1]), h1 = pack_bf2(x[2], x[3]);
+  hi = make_uint2(h0, h1);
+  lo = make_uint2(pack_bf2(x[0] - bf_lo(h0), x[1] - bf_hi(h0)), pack_bf2(x[2] - bf_lo(h1), x[3] - bf_hi(h1)));
+}
 
 __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict__ ws,
                                                         const float* __restrict__ gc,
@@ -961,133 +1049,137 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   const int lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g4 = lane >> 4;
   const size_t bh = (size_t)b * H + h;
-  // The state tile is double-buffered (chunk c reads St[c & 1] and writes the
-  // new state into the other half), so a chunk needs two barriers: after U is
-  // written and after the new state is written.
-  __shared__ alignas(16) float St2[2][16 * kST];
-  __shared__ alignas(16) float Ut[16 * kUT];
-  // The state tile (128 rows x 16 columns): float4 q = (row q / 4, columns
-  // 4(q % 4) .. +3), two per thread, both loads issued before the transposed
-  // LDS writes.
+  __shared__ alignas(16) uint16_t Sp[2][2][16 * kSB];  // [buffer][hi, lo][column][k]
+  // diag(f) U hi, mid, lo and U hi, lo, each [column][t]
+  __shared__ alignas(16) uint16_t Up[5][16 * kUB];
   float* Sg = state + bh * kD * kD + tile * 16;
-  {
-    float4 sv[2];
+  float sr[2][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int q = tid + 256 * i;
-      sv[i] = *reinterpret_cast<const float4*>(Sg + (size_t)(q >> 2) * kD + 4 * (q & 3));
-    }
+  for (int dd = 0; dd < 2; ++dd)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int q = tid + 256 * i, r = q >> 2, c0 = 4 * (q & 3);
-      St2[0][(c0 + 0) * kST + r] = sv[i].x;
-      St2[0][(c0 + 1) * kST + r] = sv[i].y;
-      St2[0][(c0 + 2) * kST + r] = sv[i].z;
-      St2[0][(c0 + 3) * kST + r] = sv[i].w;
+    for (int e = 0; e < 4; ++e) sr[dd][e] = Sg[(size_t)(16 * (2 * wid + dd) + 4 * g4 + e) * kD + col];
+  auto split_state = [&](int buf) {
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+      uint2 hi, lo;
+      split4(sr[dd], hi, lo);
+      const int k0 = 16 * (2 * wid + dd) + 4 * g4;
+      *reinterpret_cast<uint2*>(&Sp[buf][0][col * kSB + k0]) = hi;
+      *reinterpret_cast<uint2*>(&Sp[buf][1][col * kSB + k0]) = lo;
     }
-  }
-  // This wave's operands of one chunk: row tile wid of W^T and U0, dk tiles
-  // 2*wid and 2*wid+1 of K''^T. Chunk c + 1 is requested before chunk c is
-  // computed.
+  };
+  // This wave's operands of one chunk: row tile wid of W (4 k steps, hi and
+  // lo) and of U0, f of the lane's 4 rows of U, k tiles 2 wid and 2 wid + 1
+  // of kT (2 t steps). Chunk c + 1 is requested in two halves between the
+  // MFMAs of chunk c (the kT half during the U phase, the W half during the
+  // state update).
   struct ChunkOps {
-    float4 wt[8], kt[2][4], u0;
+    uint4 w[4][2], kt[2][2];
+    float4 f, u0;
     float gC;
   };
-  auto load_ops = [&](int c, ChunkOps& op) {
-    const float* wsb = ws + (bh * nC + c) * kChunkFloats;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      op.wt[dt] = *reinterpret_cast<const float4*>(wsb + kOffWT + ((wid * 8 + dt) * 64 + lane) * 4);
-#pragma unroll
-    for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-        op.kt[dd][s4] =
-            *reinterpret_cast<const float4*>(wsb + kOffKT + (((2 * wid + dd) * 4 + s4) * 64 + lane) * 4);
-    op.u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
-    op.gC = gc[bh * nC + c];
-  };
-  // The same loads in two halves, issued between the MFMAs of the two phases
-  // of the previous chunk (the K''^T half during the U phase, the W^T half
-  // during the state update): 17 back-to-back 1 KiB loads per wave otherwise
-  // hold the wave ~0.5 us in the texture unit between chunks.
   auto load_k = [&](int c, ChunkOps& op) {
     const float* wsb = ws + (bh * nC + c) * kChunkFloats;
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd)
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-        op.kt[dd][s4] =
-            *reinterpret_cast<const float4*>(wsb + kOffKT + (((2 * wid + dd) * 4 + s4) * 64 + lane) * 4);
+      for (int s = 0; s < 2; ++s)
+        op.kt[dd][s] = *reinterpret_cast<const uint4*>(wsb + kOffKT + (((2 * wid + dd) * 2 + s) * 64 + lane) * 4);
     op.gC = gc[bh * nC + c];
   };
   auto load_w = [&](int c, ChunkOps& op) {
     const float* wsb = ws + (bh * nC + c) * kChunkFloats;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      op.wt[dt] = *reinterpret_cast<const float4*>(wsb + kOffWT + ((wid * 8 + dt) * 64 + lane) * 4);
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+        op.w[s][hl] = *reinterpret_cast<const uint4*>(wsb + kOffW + (((wid * 4 + s) * 2 + hl) * 64 + lane) * 4);
     op.u0 = *reinterpret_cast<const float4*>(wsb + kOffU0 + ((wid * 8 + tile) * 64 + lane) * 4);
+    op.f = *reinterpret_cast<const float4*>(wsb + kOffF + 16 * wid + 4 * g4);
   };
   // Two operand sets alternate (chunk c computes from one while chunk c + 1
   // loads into the other): copying a set whose loads are still in flight
   // would wait for them.
   ChunkOps opa, opb;
-  load_ops(0, opa);
+  load_k(0, opa);
+  load_w(0, opa);
+  split_state(0);
   __syncthreads();
-  float* ucol = &Ut[col * kUT + 4 * g4];
 #define Q35_SCAN_CHUNK(CUR, NXT, C)                                                           \
   do {                                                                                        \
     const int ci = (C); /* not named c: the argument is an expression in the loop's c */     \
     const int cn = min(ci + 1, nC - 1);                                                       \
-    float* St = St2[ci & 1];                                                                   \
-    float* Sn = St2[(ci & 1) ^ 1];                                                             \
-    const float* scol = &St[col * kST + 4 * g4];                                              \
+    const uint16_t* sh = Sp[ci & 1][0];                                                       \
+    const uint16_t* sl = Sp[ci & 1][1];                                                       \
     float* sp = snap + (bh * nC + ci) * kSnapFloats;                                          \
-    /* Snapshot of the state entering the chunk in operand order (2 float4 per thread): */    \
-    /* float4 q = (k tile q / 64, lane q % 64) holds rows 16(q/64) + 4(lane/16) .. +3 of */   \
-    /* column lane % 16. */                                                                   \
-    _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                           \
-      const int q = tid + 256 * i, ln = q & 63;                                               \
-      *reinterpret_cast<float4*>(sp + tile * kSnapSTile + q * 4) = *reinterpret_cast<const float4*>( \
-          &St[(ln & 15) * kST + 16 * (q >> 6) + 4 * (ln >> 4)]);                              \
+    /* snapshot of the entering state: wave wid stores k step wid (hi, lo) */                \
+    {                                                                                         \
+      uint4* dp = reinterpret_cast<uint4*>(sp + tile * kSnapSTile) + wid * 128 + lane;        \
+      dp[0] = *reinterpret_cast<const uint4*>(&sh[col * kSB + 32 * wid + 8 * g4]);            \
+      dp[64] = *reinterpret_cast<const uint4*>(&sl[col * kSB + 32 * wid + 8 * g4]);           \
     }                                                                                         \
-    /* U = U0 - W S (rows 16*wid.., this v tile) */                                           \
-    q35_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};                           \
-    _Pragma("unroll") for (int dt = 0; dt < 8; ++dt) {                                        \
-      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);                     \
-      mma4(CUR.wt[dt], sv, a0, a1, a0, a1);                                                   \
+    /* U = U0 - W S (rows 16 wid .., this v tile): W_hi S_hi, W_hi S_lo, W_lo S_hi */        \
+    q35_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;                                    \
+    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                                           \
+      const uint4 bh_ = *reinterpret_cast<const uint4*>(&sh[col * kSB + 32 * s + 8 * g4]);    \
+      const uint4 bl_ = *reinterpret_cast<const uint4*>(&sl[col * kSB + 32 * s + 8 * g4]);    \
+      a0 = mfma_bf(CUR.w[s][0], bh_, a0);                                                     \
+      a1 = mfma_bf(CUR.w[s][0], bl_, a1);                                                     \
+      a2 = mfma_bf(CUR.w[s][1], bh_, a2);                                                     \
     }                                                                                         \
-    const float4 uo = make_float4(CUR.u0.x - (a0[0] + a1[0]), CUR.u0.y - (a0[1] + a1[1]),     \
-                                  CUR.u0.z - (a0[2] + a1[2]), CUR.u0.w - (a0[3] + a1[3]));    \
-    *reinterpret_cast<float4*>(ucol + 16 * wid) = uo;                                         \
-    *reinterpret_cast<float4*>(sp + kSnapU + tile * kSnapUTile + (wid * 64 + lane) * 4) = uo;  \
-    load_k(cn, NXT);                                                                          \
-    _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                           \
-      __builtin_amdgcn_sched_group_barrier(0x8, 2, 0);                                        \
-      __builtin_amdgcn_sched_group_barrier(0x20, 1, 0);                                       \
-    }                                                                                         \
-    __syncthreads();                                                                          \
-    /* S <- gamma_C S + K''^T U (dk tiles 2*wid, 2*wid + 1) */                                \
-    q35_f32x4 sn[2];                                                                          \
-    _Pragma("unroll") for (int dd = 0; dd < 2; ++dd) {                                        \
-      const int dt = 2 * wid + dd;                                                            \
-      const float4 sv = *reinterpret_cast<const float4*>(scol + 16 * dt);                     \
-      q35_f32x4 s0 = {CUR.gC * sv.x, CUR.gC * sv.y, CUR.gC * sv.z, CUR.gC * sv.w};            \
-      q35_f32x4 s1 = {0.f, 0.f, 0.f, 0.f};                                                    \
-      _Pragma("unroll") for (int s4 = 0; s4 < 4; ++s4) {                                      \
-        const float4 uv = *reinterpret_cast<const float4*>(ucol + 16 * s4);                   \
-        mma4(CUR.kt[dd][s4], uv, s0, s1, s0, s1);                                             \
+    {                                                                                         \
+      const float u0v[4] = {CUR.u0.x, CUR.u0.y, CUR.u0.z, CUR.u0.w};                          \
+      const float fv[4] = {CUR.f.x, CUR.f.y, CUR.f.z, CUR.f.w};                               \
+      float u[4], fu[4];                                                                      \
+      _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                         \
+        u[e] = u0v[e] - ((a0[e] + a1[e]) + a2[e]);                                            \
+        fu[e] = u[e] * fv[e];                                                                 \
       }                                                                                       \
-      sn[dd] = s0 + s1;                                                                       \
+      /* diag(f) U in three parts, U in two, into the transposed tiles */                    \
+      uint2 h3, m3, l3, h2, l2;                                                               \
+      split4(fu, h3, m3);                                                                     \
+      {                                                                                       \
+        const float r[4] = {fu[0] - bf_lo(h3.x) - bf_lo(m3.x), fu[1] - bf_hi(h3.x) - bf_hi(m3.x), \
+                            fu[2] - bf_lo(h3.y) - bf_lo(m3.y), fu[3] - bf_hi(h3.y) - bf_hi(m3.y)}; \
+        l3 = make_uint2(pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]));                          \
+      }                                                                                       \
+      split4(u, h2, l2);                                                                      \
+      const int o = col * kUB + 16 * wid + 4 * g4;                                            \
+      *reinterpret_cast<uint2*>(&Up[0][o]) = h3;                                              \
+      *reinterpret_cast<uint2*>(&Up[1][o]) = m3;                                              \
+      *reinterpret_cast<uint2*>(&Up[2][o]) = l3;                                              \
+      *reinterpret_cast<uint2*>(&Up[3][o]) = h2;                                              \
+      *reinterpret_cast<uint2*>(&Up[4][o]) = l2;                                              \
+    }                                                                                         \
+    load_k(cn, NXT);                                                                          \
+    __syncthreads();                                                                          \
+    /* snapshot of U: waves 0 and 1 store t step wid (hi, lo) */                             \
+    if (wid < 2) {                                                                            \
+      uint4* dp = reinterpret_cast<uint4*>(sp + kSnapU + tile * kSnapUTile) + wid * 128 + lane; \
+      dp[0] = *reinterpret_cast<const uint4*>(&Up[3][col * kUB + 32 * wid + 8 * g4]);         \
+      dp[64] = *reinterpret_cast<const uint4*>(&Up[4][col * kUB + 32 * wid + 8 * g4]);        \
+    }                                                                                         \
+    /* S <- gamma_C S + k^T (diag(f) U) (k tiles 2 wid, 2 wid + 1) */                        \
+    q35_f32x4 ah[2], am[2], al[2];                                                            \
+    _Pragma("unroll") for (int dd = 0; dd < 2; ++dd) {                                        \
+      ah[dd] = q35_f32x4{CUR.gC * sr[dd][0], CUR.gC * sr[dd][1], CUR.gC * sr[dd][2], CUR.gC * sr[dd][3]}; \
+      am[dd] = al[dd] = q35_f32x4{0.f, 0.f, 0.f, 0.f};                                        \
+    }                                                                                         \
+    _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                           \
+      const int o = col * kUB + 32 * s + 8 * g4;                                              \
+      const uint4 bh_ = *reinterpret_cast<const uint4*>(&Up[0][o]);                           \
+      const uint4 bm_ = *reinterpret_cast<const uint4*>(&Up[1][o]);                           \
+      const uint4 bl_ = *reinterpret_cast<const uint4*>(&Up[2][o]);                           \
+      _Pragma("unroll") for (int dd = 0; dd < 2; ++dd) {                                      \
+        ah[dd] = mfma_bf(CUR.kt[dd][s], bh_, ah[dd]);                                         \
+        am[dd] = mfma_bf(CUR.kt[dd][s], bm_, am[dd]);                                         \
+        al[dd] = mfma_bf(CUR.kt[dd][s], bl_, al[dd]);                                         \
+      }                                                                                       \
     }                                                                                         \
     _Pragma("unroll") for (int dd = 0; dd < 2; ++dd)                                          \
-      *reinterpret_cast<float4*>(&Sn[col * kST + 16 * (2 * wid + dd) + 4 * g4]) =             \
-          make_float4(sn[dd][0], sn[dd][1], sn[dd][2], sn[dd][3]);                            \
+      _Pragma("unroll") for (int e = 0; e < 4; ++e) sr[dd][e] = ah[dd][e] + (am[dd][e] + al[dd][e]); \
+    split_state((ci & 1) ^ 1);                                                                \
     load_w(cn, NXT);                                                                          \
-    _Pragma("unroll") for (int i = 0; i < 9; ++i) {                                           \
-      __builtin_amdgcn_sched_group_barrier(0x8, 2, 0);                                        \
-      __builtin_amdgcn_sched_group_barrier(0x20, 1, 0);                                       \
-    }                                                                                         \
     __syncthreads(); /* the new state is complete; U and the old state are free */            \
   } while (0)
   // Pairs of chunks with no branch between them (a conditional second half
@@ -1099,13 +1191,10 @@ __global__ __launch_bounds__(256) void delta_chunk_scan(const float* __restrict_
   }
   if (c < nC) Q35_SCAN_CHUNK(opa, opb, c);
 #undef Q35_SCAN_CHUNK
-  const float* Sf = St2[nC & 1];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = tid + 256 * i, r = q >> 2, c0 = 4 * (q & 3);
-    *reinterpret_cast<float4*>(Sg + (size_t)r * kD + c0) =
-        make_float4(Sf[c0 * kST + r], Sf[(c0 + 1) * kST + r], Sf[(c0 + 2) * kST + r], Sf[(c0 + 3) * kST + r]);
-  }
+  for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Sg[(size_t)(16 * (2 * wid + dd) + 4 * g4 + e) * kD + col] = sr[dd][e];
 }
 
 // Gated RMSNorm fused into the output kernel (optional): with the core row
@@ -1121,19 +1210,18 @@ struct GatedNormArgs {
   uint16_t* y;         // [B, L, H, 128]
 };
 
-// O = Q' S + P U for one (chunk, head) from the snapshots, which the scan
-// stores in this kernel's B-operand order: nothing is staged in LDS, every
-// operand is one coalesced 1 KiB float4 read per wave. Wave w (8 per
+// O = diag(sc) (q S) + P U for one (chunk, head) from the snapshots, which
+// the scan stores in this kernel's B-operand order: nothing is staged in LDS,
+// every operand is one coalesced 1 KiB read per wave. Wave w (8 per
 // workgroup, two per SIMD) takes a row tile of 16 tokens (w for w < 4, 7 - w
-// above) and column tiles 4 (w / 4) .. +3, with Q' and P loaded once; the S
+// above) and column tiles 4 (w / 4) .. +3, with q and P loaded once; the S
 // and U operands of column tile t + 1 are requested before tile t is
-// computed (two register sets alternate), so the snapshot stream overlaps the
-// MFMA chains (two alternating accumulators, Q' S first, then the causal
-// P U tiles) of the recurrence kernel's layout: O is the token loop's output
-// in closed form. GN: the gated RMSNorm of each token row is applied before
-// the store (the two column halves of a row meet in LDS for the sum of
-// squares; WF32: the norm weight is fp32, else bf16); otherwise the core
-// output is stored.
+// computed (two register sets alternate). q S is exact in the bf16 products
+// (q_hi S_hi... : q S_hi + q S_lo), P U takes P_hi U_hi + P_hi U_lo + P_lo
+// U_hi over the t steps at or below the diagonal. GN: the gated RMSNorm of
+// each token row is applied before the store (the two column halves of a
+// row meet in LDS for the sum of squares; WF32: the norm weight is fp32, else
+// bf16); otherwise the core output is stored.
 template <bool GN, bool WF32>
 __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__ ws,
                                                        const float* __restrict__ snap,
@@ -1146,30 +1234,39 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
   // wave-uniform (readfirstlane): the causal P U tests below are scalar
   // branches, not exec-mask branches that would drain the loads in flight
   const int wid = __builtin_amdgcn_readfirstlane(half ? 3 - ((tid >> 6) & 3) : (tid >> 6) & 3);
+  const int ns = wid / 2 + 1;  // t steps of P U at or below the diagonal
   const int col = lane & 15, g4 = lane >> 4;
   const size_t bhc = ((size_t)b * H + h) * nC + c;
   const float* wsb = ws + bhc * kChunkFloats;
   const float* sp = snap + bhc * kSnapFloats;
   __shared__ float ss_s[GN ? 2 : 1][kChunk];
   struct TileOps {
-    float4 s[8], u[4];
+    uint4 s[4][2], u[2][2];
   };
-  // U tiles above the diagonal are never used: they re-read tile wid.
+  // U steps past the diagonal are never used: they re-read step 0.
   auto load_tile = [&](int tile, TileOps& t) {
-    const float* st = sp + tile * kSnapSTile + lane * 4;
+    const uint4* st = reinterpret_cast<const uint4*>(sp + tile * kSnapSTile) + lane;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) t.s[dt] = *reinterpret_cast<const float4*>(st + dt * 256);
-    const float* ut = sp + kSnapU + tile * kSnapUTile + lane * 4;
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) t.u[jt] = *reinterpret_cast<const float4*>(ut + min(jt, wid) * 256);
+      for (int hl = 0; hl < 2; ++hl) t.s[s][hl] = st[(2 * s + hl) * 64];
+    const uint4* ut = reinterpret_cast<const uint4*>(sp + kSnapU + tile * kSnapUTile) + lane;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl) t.u[s][hl] = ut[(2 * (s < ns ? s : 0) + hl) * 64];
   };
-  float4 qp[8], pq[4];
+  uint4 qo[4], po[2][2];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-    qp[dt] = *reinterpret_cast<const float4*>(wsb + kOffQP + ((wid * 8 + dt) * 64 + lane) * 4);
+  for (int s = 0; s < 4; ++s)
+    qo[s] = *reinterpret_cast<const uint4*>(wsb + kOffQ + ((wid * 4 + s) * 64 + lane) * 4);
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-    pq[jt] = *reinterpret_cast<const float4*>(wsb + kOffPQ + ((wid * 4 + min(jt, wid)) * 64 + lane) * 4);
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+      po[s][hl] = *reinterpret_cast<const uint4*>(
+          wsb + kOffP + (((wid * 2 + (s < ns ? s : 0)) * 2 + hl) * 64 + lane) * 4);
+  const float4 scv = *reinterpret_cast<const float4*>(wsb + kOffSc + 16 * wid + 4 * g4);
   TileOps ta, tb;
   load_tile(4 * half, ta);
   load_tile(4 * half + 1, tb);
@@ -1196,20 +1293,28 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
   __builtin_amdgcn_sched_barrier(0);
   float ob[4][4];
   auto compute = [&](int tt, const TileOps& t) {
-    q35_f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
+    q35_f32x4 qa = {0.f, 0.f, 0.f, 0.f}, qb = qa, pa = qa, pb = qa, pc = qa;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) mma4(qp[dt], t.s[dt], o0, o1, o0, o1);
+    for (int s = 0; s < 4; ++s) {
+      qa = mfma_bf(qo[s], t.s[s][0], qa);
+      qb = mfma_bf(qo[s], t.s[s][1], qb);
+    }
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-      if (jt <= wid) mma4(pq[jt], t.u[jt], o0, o1, o0, o1);
+    for (int s = 0; s < 2; ++s)
+      if (s < ns) {
+        pa = mfma_bf(po[s][0], t.u[s][0], pa);
+        pb = mfma_bf(po[s][0], t.u[s][1], pb);
+        pc = mfma_bf(po[s][1], t.u[s][0], pc);
+      }
+    const float sc[4] = {scv.x, scv.y, scv.z, scv.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+      const float o = sc[e] * (qa[e] + qb[e]) + ((pa[e] + pb[e]) + pc[e]);
       if (GN) {
-        ob[tt][e] = round_bf(o0[e] + o1[e]);
+        ob[tt][e] = round_bf(o);
       } else {
         const int tok = c * kChunk + 16 * wid + 4 * g4 + e;
-        if (tok < L)
-          out[(((size_t)b * L + tok) * H + h) * kD + (4 * half + tt) * 16 + col] = (uint16_t)f2bf(o0[e] + o1[e]);
+        if (tok < L) out[(((size_t)b * L + tok) * H + h) * kD + (4 * half + tt) * 16 + col] = (uint16_t)f2bf(o);
       }
     }
   };
@@ -1246,7 +1351,6 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
     }
   }
 }
-
 }  // namespace
 
 extern "C" {
@@ -1335,7 +1439,7 @@ int q35_delta_decode(const void* src, int src_stride, const void* packed, int pa
 constexpr int kChunkMinL = 64;
 
 // Floats of workspace q35_delta_prefill needs: 4 factors per (batch, token,
-// head), and for the chunked form 36864 operand floats, 1 decay and 24576
+// head), and for the chunked form 28800 operand floats, 1 decay and 24576
 // snapshot floats per (batch, head, chunk).
 long long q35_delta_prefill_workspace(int B, int L, int H) {
   long long n = 4ll * B * L * H;

@@ -51,10 +51,10 @@ def test_abi_version_and_host_queries():
     assert lib.q35_abi_version() == _lib.ABI_VERSION
     assert lib.q35_lm_head_top1_workspace(248320, 2048) >= 248320 // 16
     # factors (4 floats per token and head), plus for L >= 64 the chunked form's
-    # 36864 operand + 1 decay + 24576 snapshot floats per (head, 64-token chunk)
+    # 28800 operand + 1 decay + 24576 snapshot floats per (head, 64-token chunk)
     # and 3 floats of alignment slack
     assert lib.q35_delta_prefill_workspace(1, 63, 16) == 4 * 63 * 16
-    assert lib.q35_delta_prefill_workspace(1, 1024, 16) == 4 * 1024 * 16 + 16 * 16 * 61441 + 3
+    assert lib.q35_delta_prefill_workspace(1, 1024, 16) == 4 * 1024 * 16 + 16 * 16 * 53377 + 3
     splits = lib.q35_gqa_decode_splits(8192, 2, None)
     assert 1 <= splits <= 1024
     assert lib.q35_gqa_decode_workspace(8192, 8, 2, 256) == 8 * splits * 258
