@@ -697,55 +697,72 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(const uint16_t* __restri
   const float a_raw = bf2f(prow0[a_off + h]), b_raw = bf2f(prow0[b_off + h]);
   const float alog = ld_param(a_log, h, PF32), dtb = ld_param(dt_bias, h, PF32);
   if (CONV) {
-    // 0. the conv of this chunk and head into Qr / Kr / Vr: thread item =
-    //    (8-channel group of q, k or v; 16 tokens), its 19 input rows (16 + 3
-    //    before; rows before token 0 are zero) and 4 x 8 taps loaded before
-    //    any is used.
-    if (tid < 192) {
-      const int gsel = tid % 48, i0 = (tid / 48) * 16;
-      const int arr = gsel >> 4, d = (gsel & 15) * 8;
-      const int ch = arr * H * kD + h * kD + d;  // conv channel of the group
-      uint16_t* dst = arr == 0 ? Qr : (arr == 1 ? Kr : Vr);
-      uint4 raw[19], wr[4];
+    // 0. the conv of this chunk and head into Qr / Kr / Vr. Thread items are
+    //    (8-channel group g of q, k or v; 4 tokens), 768 of them (48 groups x
+    //    16 token blocks), three per thread, each with its 7 input rows (4 + 3
+    //    before; rows before token 0 are zero) and 4 x 8 taps; every load of
+    //    the three items is issued before any is used. The bf16 rounding of
+    //    the conv sums takes one conversion per pair of values.
+    {
+      constexpr int NI = 3;
+      uint4 raw[NI][7], wr[NI][4];
 #pragma unroll
-      for (int r = 0; r < 19; ++r) {
-        const int tr = min(max(c * kChunk + i0 - 3 + r, 0), L - 1);
-        raw[r] = *reinterpret_cast<const uint4*>(qkv + ((size_t)b * L + tr) * qkv_stride + ch);
-      }
+      for (int it = 0; it < NI; ++it) {
+        const int item = tid + 256 * it;
+        const int g = item % 48, t0 = (item / 48) * 4;
+        const int ch = (g >> 4) * H * kD + h * kD + (g & 15) * 8;  // conv channel of the group
 #pragma unroll
-      for (int q = 0; q < 4; ++q) wr[q] = *reinterpret_cast<const uint4*>(conv.w + (size_t)ch * 4 + q * 8);
-      float wt[8][4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float f[8];
-        unpack8(wr[q], f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wt[2 * q + e / 4][e % 4] = f[e];
-      }
-      // every row unpacked once (rows before token 0 as zeros)
-      float xr[19][8];
-#pragma unroll
-      for (int r = 0; r < 19; ++r) {
-        const bool before = c * kChunk + i0 - 3 + r < 0;
-        unpack8(before ? make_uint4(0u, 0u, 0u, 0u) : raw[r], xr[r]);
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int t = c * kChunk + i0 + j;
-        float o[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float acc = 0.f;
-#pragma unroll
-          for (int tap = 0; tap < 4; ++tap) acc = fmaf(xr[j + tap][e], wt[e][tap], acc);
-          o[e] = silu_fast(round_bf(acc));
+        for (int r = 0; r < 7; ++r) {
+          const int tr = min(max(c * kChunk + t0 - 3 + r, 0), L - 1);
+          raw[it][r] = *reinterpret_cast<const uint4*>(qkv + ((size_t)b * L + tr) * qkv_stride + ch);
         }
-        *reinterpret_cast<uint4*>(dst + (i0 + j) * kRS + d) = pack8(o);  // the conv output is bf16
-        const int pos = t - (L - 4);
-        if (t < L && pos >= 0) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            conv.state[((size_t)b * 3 * H * kD + ch + e) * 4 + pos] = (uint16_t)f2bf(xr[j + 3][e]);
+        for (int q = 0; q < 4; ++q) wr[it][q] = *reinterpret_cast<const uint4*>(conv.w + (size_t)ch * 4 + q * 8);
+      }
+#pragma unroll
+      for (int it = 0; it < NI; ++it) {
+        const int item = tid + 256 * it;
+        const int g = item % 48, t0 = (item / 48) * 4;
+        const int arr = g >> 4, d = (g & 15) * 8;
+        const int ch = arr * H * kD + h * kD + d;
+        uint16_t* dst = arr == 0 ? Qr : (arr == 1 ? Kr : Vr);
+        float wt[8][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float f[8];
+          unpack8(wr[it][q], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) wt[2 * q + e / 4][e % 4] = f[e];
+        }
+        float xr[7][8];
+#pragma unroll
+        for (int r = 0; r < 7; ++r) {
+          const bool before = c * kChunk + t0 - 3 + r < 0;
+          unpack8(before ? make_uint4(0u, 0u, 0u, 0u) : raw[it][r], xr[r]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = c * kChunk + t0 + j;
+          float acc[8], o[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            acc[e] = 0.f;
+#pragma unroll
+            for (int tap = 0; tap < 4; ++tap) acc[e] = fmaf(xr[j + tap][e], wt[e][tap], acc[e]);
+          }
+#pragma unroll
+          for (int p2 = 0; p2 < 4; ++p2) {
+            const uint32_t hb = pack_bf2(acc[2 * p2], acc[2 * p2 + 1]);
+            o[2 * p2] = silu_fast(bf_lo(hb));
+            o[2 * p2 + 1] = silu_fast(bf_hi(hb));
+          }
+          *reinterpret_cast<uint4*>(dst + (t0 + j) * kRS + d) = pack8(o);  // the conv output is bf16
+          const int pos = t - (L - 4);
+          if (t < L && pos >= 0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              conv.state[((size_t)b * 3 * H * kD + ch + e) * 4 + pos] = (uint16_t)f2bf(xr[j + 3][e]);
+          }
         }
       }
     }
