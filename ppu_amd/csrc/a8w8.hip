@@ -164,8 +164,12 @@ __global__ __launch_bounds__(256) void a8w8_gemv_mt(const A8Args a, int m0) {
 // int8 rows and s_x are inputs. Rows past M read row M-1 and are never
 // stored; B columns past MT repeat a staged row and are dropped. The KS
 // partial tiles are summed in LDS, then one thread per output dequantises.
-template <int MT, int RT, int KS, int K, bool QUANT>
+// R8: tiles of 8 weight rows (A rows 8..15 repeat rows 0..7 and their outputs
+// are dropped), for N = 2048: 256 workgroups instead of 128, so twice the CUs
+// stream the weights (the matrix-core time of the wasted half is small).
+template <int MT, int RT, int KS, int K, bool QUANT, bool R8 = false>
 __global__ __launch_bounds__(RT * KS * 64) void a8w8_skinny_mfma(const A8Args a) {
+  constexpr int TR = R8 ? 8 : 16;  // weight rows per tile
   constexpr int NW = RT * KS;
   constexpr int KB = K / (KS * 64);          // MFMAs (16-byte loads) per lane
   constexpr int XS = K + 16;                 // LDS row stride: rows 16 bytes apart in the banks
@@ -181,7 +185,7 @@ __global__ __launch_bounds__(RT * KS * 64) void a8w8_skinny_mfma(const A8Args a)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = tid >> 6;
-  const int nb = blockIdx.x * RT * 16;
+  const int nb = blockIdx.x * RT * TR;
 
   // 1. activation rows (bf16 or int8), the output thread's weight scale, then
   //    the weight stream (unpredicated: rows past N read row N-1).
@@ -198,12 +202,12 @@ __global__ __launch_bounds__(RT * KS * 64) void a8w8_skinny_mfma(const A8Args a)
   }
   // Output thread t < RT*256: tile t/256, token m = (t%256)/16, row n = t%16.
   const int o_rt = tid >> 8, o_m = (tid >> 4) & 15, o_n = tid & 15;
-  const int o_row = nb + o_rt * 16 + o_n;
+  const int o_row = nb + o_rt * TR + o_n;
   const float sw = a.s_w[min(o_row, a.N - 1)];
   const float sx_in = QUANT ? 0.f : a.s_x[min(o_m, a.M - 1)];
   __builtin_amdgcn_sched_barrier(0);
   const int rt = wid / KS, ks = wid % KS;
-  const int wrow = min(nb + rt * 16 + (lane & 15), a.N - 1);
+  const int wrow = min(nb + rt * TR + (lane & (TR - 1)), a.N - 1);
   const int8_t* wp = a.Wq + (size_t)wrow * K + ks * (K / KS) + 16 * (lane >> 4);
   uint4 w[KB];
 #pragma unroll
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(RT * KS * 64) void a8w8_skinny_mfma(const A8Args a)
     int s = 0;
 #pragma unroll
     for (int k2 = 0; k2 < KS; ++k2) s += rp[k2 * 256];
-    if (o_m < a.M && o_row < a.N) {
+    if (o_m < a.M && o_n < TR && o_row < a.N) {
       const size_t o = (size_t)o_m * a.N + o_row;
       const float sx = QUANT ? sx_s[o_m] : sx_in;
       a.y[o] = (uint16_t)f2bf((float)s * sx * sw);
@@ -301,12 +305,13 @@ __global__ __launch_bounds__(256) void dequant_rows(const int* __restrict__ acc,
   }
 }
 
-template <int MT, int RT, int KS, int K, bool QUANT>
+template <int MT, int RT, int KS, int K, bool QUANT, bool R8 = false>
 int launch_skinny(const A8Args& a, hipStream_t stream) {
   // QUANT needs the bf16 rows; otherwise the int8 rows and their scales.
   if (QUANT ? !a.x : (!a.xq || !a.s_x)) return (int)hipErrorInvalidValue;
-  const unsigned grid = (unsigned)((a.N + 16 * RT - 1) / (16 * RT));
-  a8w8_skinny_mfma<MT, RT, KS, K, QUANT><<<grid, RT * KS * 64, 0, stream>>>(a);
+  constexpr int TR = R8 ? 8 : 16;
+  const unsigned grid = (unsigned)((a.N + TR * RT - 1) / (TR * RT));
+  a8w8_skinny_mfma<MT, RT, KS, K, QUANT, R8><<<grid, RT * KS * 64, 0, stream>>>(a);
   return q35_last_error();
 }
 
@@ -613,6 +618,14 @@ int q35_gemv_a8w8(const void* x, void* xq, void* s_x, const void* Wq, const void
                                : launch_skinny<8, 3, 4, 2048, false>(a, stream);
       return fuse ? launch_skinny<16, 3, 4, 2048, true>(a, stream)
                   : launch_skinny<16, 3, 4, 2048, false>(a, stream);
+    }
+    // K = 6 KiB: 8-row tiles when N leaves fewer than 256 workgroups of 16 rows
+    if (a.N <= 2048) {
+      if (mt == 4) return fuse ? launch_skinny<4, 1, 4, 6144, true, true>(a, stream)
+                               : launch_skinny<4, 1, 4, 6144, false, true>(a, stream);
+      if (mt == 8) return fuse ? launch_skinny<8, 1, 8, 6144, true, true>(a, stream)
+                               : launch_skinny<8, 1, 8, 6144, false, true>(a, stream);
+      return launch_skinny<16, 1, 4, 6144, false, true>(a, stream);
     }
     if (mt == 4) return fuse ? launch_skinny<4, 1, 4, 6144, true>(a, stream)
                              : launch_skinny<4, 1, 4, 6144, false>(a, stream);

@@ -782,7 +782,7 @@ def test_quantize_weight_bit_exact(gpu, n, k):
 
 
 @pytest.mark.parametrize("m", [1, 2, 4, 7, 13, 16, 17])
-@pytest.mark.parametrize("n,k", [(12288, 2048), (2048, 6144), (1000, 2048)])
+@pytest.mark.parametrize("n,k", [(12288, 2048), (2048, 6144), (1000, 2048), (1000, 6144)])
 def test_a8w8_linear_config2(gpu, m, n, k):
     """Benchmark config 2: int8 quantisation and int32 accumulators bit-exact,
     bf16 dequant output within rtol 1e-2 / atol 1e-3."""
