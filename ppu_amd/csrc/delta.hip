@@ -1257,6 +1257,8 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
   const float* wsb = ws + bhc * kChunkFloats;
   const float* sp = snap + bhc * kSnapFloats;
   __shared__ float ss_s[GN ? 2 : 1][kChunk];
+  constexpr int kYS = kD + 8;  // bf16 row stride of the gated norm's output tile
+  __shared__ alignas(16) uint16_t yt[GN ? kChunk * kYS : 8];
   struct TileOps {
     uint4 s[4][2], u[2][2];
   };
@@ -1287,22 +1289,28 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
   TileOps ta, tb;
   load_tile(4 * half, ta);
   load_tile(4 * half + 1, tb);
-  // GN: the lane's gate values and norm weights (4 tiles x 4 rows).
-  uint16_t zr[4][4];
-  float wn[4];
+  // GN: this thread's part of the gated norm, by 16-byte rows: token row
+  // tid / 8 of the chunk, columns 16 (tid % 8) .. +15 (its gate values and
+  // norm weights, requested with the operands).
+  const int gr = tid >> 3, gc0 = 16 * (tid & 7);
+  uint4 zv[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+  float wv[16];
   if (GN) {
+    const int t = min(c * kChunk + gr, L - 1);
+    const uint16_t* zp = gn.z + ((size_t)b * L + t) * gn.z_stride + (size_t)h * kD + gc0;
+    zv[0] = *reinterpret_cast<const uint4*>(zp);
+    zv[1] = *reinterpret_cast<const uint4*>(zp + 8);
+    // The weight type is a template parameter: a run-time branch between
+    // two load forms would make the compiler drain every load in flight.
+    if (WF32) {
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int cabs = (4 * half + tt) * 16 + col;
-      // The weight type is a template parameter: a run-time branch between
-      // two load forms would make the compiler drain every load in flight.
-      wn[tt] = WF32 ? reinterpret_cast<const float*>(gn.w)[cabs]
-                    : bf2f(reinterpret_cast<const uint16_t*>(gn.w)[cabs]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = min(c * kChunk + 16 * wid + 4 * g4 + e, L - 1);
-        zr[tt][e] = gn.z[((size_t)b * L + t) * gn.z_stride + (size_t)h * kD + cabs];
+      for (int q = 0; q < 4; ++q) {
+        const float4 w4 = reinterpret_cast<const float4*>(gn.w)[gc0 / 4 + q];
+        wv[4 * q] = w4.x; wv[4 * q + 1] = w4.y; wv[4 * q + 2] = w4.z; wv[4 * q + 3] = w4.w;
       }
+    } else {
+      unpack8(reinterpret_cast<const uint4*>(gn.w)[gc0 / 8], wv);
+      unpack8(reinterpret_cast<const uint4*>(gn.w)[gc0 / 8 + 1], wv + 8);
     }
   }
   // Every load above the first MFMA (the scheduler would otherwise start the
@@ -1353,18 +1361,27 @@ __global__ __launch_bounds__(512) void delta_chunk_out(const float* __restrict__
       if (col == 0) ss_s[half][16 * wid + 4 * g4 + e] = ss;
     }
     __syncthreads();
+    // the normalised core (bf16) into the chunk's [64 x 128] output tile
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 16 * wid + 4 * g4 + e;
-      const int t = c * kChunk + r;
       const float inv = rsqrt_cr((ss_s[0][r] + ss_s[1][r]) / (float)kD + gn.eps);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const float nb = round_bf(ob[tt][e] * inv);
-        const float weighted = round_bf(nb * round_bf(wn[tt]));
-        const float v = weighted * silu_f(bf2f(zr[tt][e]));
-        if (t < L) gn.y[(((size_t)b * L + t) * H + h) * kD + (4 * half + tt) * 16 + col] = (uint16_t)f2bf(v);
-      }
+      for (int tt = 0; tt < 4; ++tt) yt[r * kYS + (4 * half + tt) * 16 + col] = (uint16_t)f2bf(ob[tt][e] * inv);
+    }
+    __syncthreads();
+    const int t = c * kChunk + gr;
+    if (t < L) {
+      float nb[16], zf[16], v[16];
+      unpack8(*reinterpret_cast<const uint4*>(&yt[gr * kYS + gc0]), nb);
+      unpack8(*reinterpret_cast<const uint4*>(&yt[gr * kYS + gc0 + 8]), nb + 8);
+      unpack8(zv[0], zf);
+      unpack8(zv[1], zf + 8);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = round_bf(nb[e] * round_bf(wv[e])) * silu_f(zf[e]);
+      uint16_t* yp = gn.y + (((size_t)b * L + t) * H + h) * kD + gc0;
+      *reinterpret_cast<uint4*>(yp) = pack8(v);
+      *reinterpret_cast<uint4*>(yp + 8) = pack8(v + 8);
     }
   }
 }

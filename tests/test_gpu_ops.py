@@ -400,6 +400,39 @@ def test_delta_recurrent(gpu, seq_len):
     torch.testing.assert_close(st.cpu(), st_ref, rtol=1e-3, atol=1e-6)
 
 
+@pytest.mark.parametrize("batch,heads,seq_len", [(2, 8, 130), (2, 6, 64), (1, 6, 257)])
+def test_delta_chunked_batch_and_head_counts(gpu, batch, heads, seq_len):
+    """The chunked form with several sequences and head counts that do and do
+    not fill the 8-XCD placement of the chunk scan (H % 8 == 0 or not), ragged
+    last chunks included: output and state against the oracle token loop, the
+    gated form against the oracle norm of the same core."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 16)
+    dim = 128
+    qkv_w = 3 * heads * dim
+    qkv = randn(g, batch, seq_len, qkv_w)
+    width = qkv_w + heads * dim + 2 * heads
+    packed = randn(g, batch, seq_len, (width + 7) // 8 * 8)  # rows padded to 16 bytes, as the model packs them
+    packed[..., :qkv_w] = qkv
+    a_log, dt_bias = randn(g, heads), randn(g, heads)
+    state = torch.randn(batch, heads, dim, dim, generator=g) * 0.01
+    norm_w = randn(g, dim, scale=0.02, mean=1.0)
+    st_ref = state.clone()
+    core_ref = ref.delta_recurrent(qkv, packed, a_log, dt_bias, st_ref)
+    args = (qkv.to(gpu), packed.to(gpu), a_log.to(gpu), dt_bias.to(gpu))
+    st = state.to(gpu)
+    core = K.delta_recurrent_fused(*args, st)
+    close(core, core_ref)
+    torch.testing.assert_close(st.cpu(), st_ref, rtol=1e-3, atol=1e-6)
+    st2 = state.to(gpu)
+    got = K.delta_prefill_gated(*args, st2, norm_w.to(gpu), 1e-6)
+    z = packed[..., 3 * heads * dim : 4 * heads * dim].reshape(-1, dim)
+    exp = ref.gated_rms_norm(core.cpu().reshape(-1, dim), z, norm_w).reshape(batch, seq_len, heads, dim)
+    close(got, exp)
+    assert torch.equal(st2, st)
+
+
 @pytest.mark.parametrize("seq_len", [3, 63, 200, 1024])
 def test_delta_prefill_gated(gpu, seq_len):
     """Prefill recurrence + gated RMSNorm in one call (the norm is fused into
