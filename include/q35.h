@@ -216,7 +216,8 @@ int q35_delta_decode(const void* src, int src_stride, const void* packed, int pa
                      int fuse_conv, int fuse_gnorm, void* stream);
 
 /* Workspace floats for q35_delta_prefill: 4 per (batch, token, head), plus for
- * L >= 64 36865 per (batch, head, 64-token chunk). */
+ * L >= 64 53377 per (batch, head, 64-token chunk) (28800 chunk operands, 1
+ * decay, 24576 state / delta snapshots) and 3 of alignment. */
 long long q35_delta_prefill_workspace(int B, int L, int H);
 /* Gated delta rule over L tokens (per-token factors precomputed): a token scan
  * below 64 tokens, the closed form over 64-token chunks on the matrix cores
