@@ -278,7 +278,16 @@ def step_bytes(model, context: float) -> int:
 
 
 def kernel_table(dev) -> dict:
-    """Benchmark configs 1-4 as individual launches, rotating distinct buffers."""
+    """Benchmark configs 1-4 as individual launches, rotating distinct buffers.
+
+    Every record also carries its latency floor: ``read_floor_us``, a plain
+    streaming read of the record's algorithmic bytes (the faster of
+    ``stream_read``'s persistent grid and its one-round grid, which requests
+    every byte at once), graph-timed over rotating buffers the same way;
+    ``launch_floor_us``, a launch of an empty-work kernel in a graph (one
+    16-byte zero fill); ``floor_us`` = the read plus one empty launch for
+    every further dependent launch of the record; ``frac_of_floor`` =
+    floor_us / us."""
     import torch
 
     from ppu_amd import kernels as K
@@ -290,10 +299,32 @@ def kernel_table(dev) -> dict:
     def nbuf(nbytes):
         return max(2, (640 << 20) // nbytes + 1)
 
-    def rec(name, us, nbytes):
+    tiny = torch.zeros(4, device=dev, dtype=torch.int32)
+    launch_us = graph_time_us(lambda i: K.zero_tensors([tiny]), calls=64, reps=10)
+    floors: dict[int, float] = {}
+
+    def read_floor(nbytes):
+        nbytes = (nbytes + 15) // 16 * 16
+        if nbytes not in floors:
+            n = nbuf(nbytes)
+            bufs = [torch.empty(nbytes, device=dev, dtype=torch.uint8) for _ in range(n)]
+            floors[nbytes] = min(
+                graph_time_us(lambda i: K.stream_read(bufs[i % n], one_round=r), calls=n, reps=4)
+                for r in (False, True))
+            del bufs
+        return floors[nbytes]
+
+    def rec(name, us, nbytes, launches=1):
         gbs = nbytes / us / 1e3
-        out[name] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 3)}
-        log(f"  {name}: {us:.2f} us  {gbs:.0f} GB/s  ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
+        rf = read_floor(nbytes)
+        floor = rf + (launches - 1) * launch_us
+        out[name] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 3),
+                     "launches": launches, "read_floor_us": round(rf, 2),
+                     "launch_floor_us": round(launch_us, 2), "floor_us": round(floor, 2),
+                     "frac_of_floor": round(floor / us, 3)}
+        log(f"  {name}: {us:.2f} us  {gbs:.0f} GB/s  ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s); "
+            f"floor {floor:.2f} us ({launches} launch(es): read {rf:.2f} + empty launch "
+            f"{launch_us:.2f}) = {100 * floor / us:.0f}% of the time")
 
     # config 1: residual add + RMSNorm + GEMV [6144, 2048]
     n = nbuf(6144 * 2048 * 2)
@@ -324,7 +355,7 @@ def kernel_table(dev) -> dict:
         ln = torch.tensor(ctx, device=dev, dtype=torch.int64)
         us = graph_time_us(lambda i: K.gqa_decode_attention(q, Kc[i % n], Vc[i % n], ln, 1 / 16),
                            calls=n, reps=4)
-        rec(f"cfg3_gqa_decode_L{ctx}", us, 2048 * ctx + 8192)
+        rec(f"cfg3_gqa_decode_L{ctx}", us, 2048 * ctx + 8192, launches=2)
         del Kc, Vc
     # config 4: one decode token of a DeltaNet layer through the kernels the
     # model runs (conv update, the 256-wave delta step, packed gated norm),
@@ -343,7 +374,7 @@ def kernel_table(dev) -> dict:
         return K.gated_rms_norm_packed(core.reshape(-1, 128), packed, 6144, 16, gw, 1e-6)
 
     us = graph_time_us(chain, calls=n, reps=4)
-    rec("cfg4_delta_decode_chain_3_launches", us, 2_265_216)
+    rec("cfg4_delta_decode_chain_3_launches", us, 2_265_216, launches=3)
     qkv = K.causal_conv1d_fused(packed, cw, cs)
     us = graph_time_us(lambda i: K.delta_recurrent_fused(qkv, packed, z16, z16, St[i % n]),
                        calls=n, reps=4)

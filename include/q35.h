@@ -42,6 +42,15 @@ int q35_zero_buffers(void* const* ptrs, const long long* nbytes, int n, void* st
 int q35_stream_read(const void* p, long long nbytes, void* out, long long out_words, int* workgroups_out,
                     void* stream);
 
+/* Measurement utility with no counterpart in the reference: the same read as
+ * one round of requests (workgroups = max(ceil(nbytes / 32 KiB),
+ * min(CUs, ceil(nbytes / 4 KiB))), so no lane issues more than 8 loads and
+ * every byte is requested at once); out_words >= 256 * that count, which
+ * goes to *workgroups_out when not null. Timing it gives the read floor of a
+ * small kernel that must fetch nbytes in one launch. */
+int q35_stream_read_round(const void* p, long long nbytes, void* out, long long out_words,
+                          int* workgroups_out, void* stream);
+
 /* ---- norms and elementwise ------------------------------------------- */
 
 /* rms_norm: y = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)), rows x width.

@@ -26,6 +26,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_abi_version": (_I, []),
     "q35_zero_buffers": (_I, [_P, _P, _I, _P]),
     "q35_stream_read": (_I, [_P, _L, _P, _L, _P, _P]),
+    "q35_stream_read_round": (_I, [_P, _L, _P, _L, _P, _P]),
     "q35_layernorm": (_I, [_P, _P, _P, _I, _P, _I, _I, _F, _P]),
     "q35_residual_layernorm": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _F, _P]),
     "q35_position_embed_add": (_I, [_P, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P]),

@@ -37,18 +37,20 @@ constexpr int kReadU = 8;
 __global__ __launch_bounds__(256) void stream_read(const uint8_t* __restrict__ p, long long n16,
                                                    uint32_t* __restrict__ out) {
   const long long stride = (long long)gridDim.x * 256;
-  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   uint32_t acc = 0;
-  for (; i + (kReadU - 1) * stride < n16; i += kReadU * stride) {
+  // The last sweep issues its loads together too: an index past the end
+  // reads the lane's own first group of the sweep again (clamped, no branch
+  // to split the batch, no line every lane hits) and is not folded in.
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += kReadU * stride) {
     uint4 v[kReadU];
 #pragma unroll
-    for (int u = 0; u < kReadU; ++u) v[u] = ld_stream16(p + (i + u * stride) * 16);
+    for (int u = 0; u < kReadU; ++u) {
+      const long long j = i + u * stride;
+      v[u] = ld_stream16(p + (j < n16 ? j : i) * 16);
+    }
 #pragma unroll
-    for (int u = 0; u < kReadU; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-  }
-  for (; i < n16; i += stride) {
-    const uint4 v = ld_stream16(p + i * 16);
-    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    for (int u = 0; u < kReadU; ++u)
+      acc ^= i + u * stride < n16 ? v[u].x ^ v[u].y ^ v[u].z ^ v[u].w : 0u;
   }
   out[blockIdx.x * 256 + threadIdx.x] = acc;
 }
@@ -103,6 +105,24 @@ int q35_stream_read(const void* p, long long nbytes, void* out, long long out_wo
   Q35_CHECK_ARG(out_words >= (long long)blocks * 256);
   if (workgroups_out) *workgroups_out = blocks;
   stream_read<<<blocks, 256, 0, stream>>>((const uint8_t*)p, nbytes / 16, (uint32_t*)out);
+  return q35_last_error();
+}
+
+// The same probe as one round of requests: enough workgroups that no lane
+// issues more than kReadU loads (at least one workgroup per CU while the
+// buffer gives every lane a load), so every byte is requested at once. The
+// read floor of a small kernel: one launch that must fetch nbytes.
+int q35_stream_read_round(const void* p, long long nbytes, void* out, long long out_words,
+                          int* workgroups_out, hipStream_t stream) {
+  Q35_CHECK_ARG(p && out && nbytes > 0 && nbytes % 16 == 0 && q35_aligned16(p));
+  const long long n16 = nbytes / 16;
+  const long long one_round = (n16 + 256ll * kReadU - 1) / (256ll * kReadU);
+  const long long per_cu = (n16 + 255) / 256;
+  const long long spread = per_cu < device_cus() ? per_cu : device_cus();
+  const long long blocks = one_round > spread ? one_round : spread;
+  Q35_CHECK_ARG(blocks < (1ll << 31) / 256 && out_words >= blocks * 256);
+  if (workgroups_out) *workgroups_out = (int)blocks;
+  stream_read<<<(unsigned)blocks, 256, 0, stream>>>((const uint8_t*)p, n16, (uint32_t*)out);
   return q35_last_error();
 }
 

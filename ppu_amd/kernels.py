@@ -1400,11 +1400,13 @@ def zero_tensors(tensors) -> None:
 
 
 @_device_checked
-def stream_read(buf: torch.Tensor) -> torch.Tensor:
+def stream_read(buf: torch.Tensor, one_round: bool = False) -> torch.Tensor:
     """Read every byte of a contiguous GPU tensor once with the GEMV weight
     stream's loads (one workgroup per CU) and return one int32 XOR word per
     thread. A measurement utility (no counterpart in the reference): timing
-    it gives the achievable HBM read rate the decode GEMVs are compared to."""
+    it gives the achievable HBM read rate the decode GEMVs are compared to.
+    ``one_round``: as many workgroups as request every byte at once (at most
+    8 loads per lane), the read floor of a small single-launch kernel."""
 
     import ctypes
 
@@ -1414,10 +1416,13 @@ def stream_read(buf: torch.Tensor) -> torch.Tensor:
     if nbytes == 0 or nbytes % 16 or buf.data_ptr() % 16:
         raise ValueError("stream_read needs a 16-byte aligned size and address")
     props = torch.cuda.get_device_properties(buf.device)
-    out = torch.empty(props.multi_processor_count * 256, device=buf.device, dtype=torch.int32)
+    words = props.multi_processor_count * 256
+    if one_round:
+        words = max(words, -(-nbytes // (16 * 8)) + 256)
+    out = torch.empty(words, device=buf.device, dtype=torch.int32)
     blocks = ctypes.c_int(0)
-    _lib.call("q35_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), out.numel(),
-              ctypes.addressof(blocks), _stream(buf))
+    _lib.call("q35_stream_read_round" if one_round else "q35_stream_read", buf.data_ptr(), nbytes,
+              out.data_ptr(), out.numel(), ctypes.addressof(blocks), _stream(buf))
     return out[: blocks.value * 256]
 
 

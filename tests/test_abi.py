@@ -70,6 +70,7 @@ def test_invalid_sizes_rejected_before_launch():
     assert lib.q35_delta_decode(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, 0.0,
                                 None, 1, 16, 64, 0, 0, None) == 1
     assert lib.q35_stream_read(None, 16, None, 1 << 20, None, None) == 1
+    assert lib.q35_stream_read_round(None, 16, None, 1 << 20, None, None) == 1
 
 
 def test_wrappers_reject_cpu_tensors():

@@ -1102,18 +1102,20 @@ def test_gemm_swiglu_bf16(gpu, m, n, k):
     assert outside <= 1e-5 * exp.numel()
 
 
+@pytest.mark.parametrize("one_round", [False, True])
 @pytest.mark.parametrize("nbytes", [16, 1 << 20, (9 << 20) + 48])
-def test_stream_read(gpu, nbytes):
+def test_stream_read(gpu, nbytes, one_round):
     """The read-rate probe reads every 16-byte group exactly once: the XOR of
     its per-thread words is the XOR of all words of the buffer (sizes below,
-    above and past one full 8-load sweep of the grid, with a tail)."""
+    above and past one full 8-load sweep of the grid, with a tail), for the
+    persistent grid and the one-round grid."""
     import numpy as np
 
     from ppu_amd import kernels as K
 
     g = gen(KERNEL_SEED + 15)
     words = torch.randint(-(2**31), 2**31 - 1, (nbytes // 4,), generator=g, dtype=torch.int32)
-    out = K.stream_read(words.to(gpu))
+    out = K.stream_read(words.to(gpu), one_round=one_round)
     torch.cuda.synchronize()
     got = np.bitwise_xor.reduce(out.cpu().numpy())
     assert got == np.bitwise_xor.reduce(words.numpy())

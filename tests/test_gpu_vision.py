@@ -181,7 +181,7 @@ def _rel(a, b):
 
 def test_vision_tower_matches_transformers_and_graph_replays(gpu):
     """The fused vision forward (our LayerNorm / position-embedding / RoPE
-    kernels, library GEMMs, fused SDPA) against Transformers' fp32 CPU forward
+    kernels, library GEMMs, the vision_attn_fa flash kernel) against Transformers' fp32 CPU forward
     of the same weights; the second call of a patch count replays the captured
     graph and every replay (with eager work in between) equals the eager call."""
     from qwen35_fused.integration import apply_fusions
