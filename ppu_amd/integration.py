@@ -528,7 +528,8 @@ def prefill_layer_a8w8(stack, index: int, residual: torch.Tensor, shape_of: torc
     (``quant`` = ``(xq, sx)``; ``shape_of`` gives its shape), each output
     projection's int32 accumulators are dequantised inside the following
     residual add + RMSNorm, which also quantises its output for the next
-    GEMM, and the MLP's SwiGLU quantises its activation directly. The same
+    GEMM, and the gate/up GEMM's SwiGLU epilogue output is quantised per
+    token for the down projection. The same
     bits as ``prefill_layer`` (each fused kernel keeps the separate kernels'
     arithmetic). Returns ``(residual, normalised or None, quant or None)``:
     after the last layer the final norm's bf16 output and no quant."""
@@ -544,7 +545,11 @@ def prefill_layer_a8w8(stack, index: int, residual: torch.Tensor, shape_of: torc
     ln = layer.post_attention_layernorm
     residual, _, mq, ms = K.residual_rmsnorm_dequant_quant(residual, acc, sx, out_w.s, ln.weight, ln.eps)
     gate_up, down = layer.mlp.q35_gate_up, layer.mlp.q35_down
-    aq, sa = K.dequant_swiglu_quant(K.a8w8_int_gemm(mq, gate_up.w), ms, gate_up.s)
+    # SwiGLU in the int8 GEMM's epilogue (bf16 [M, I]), then the per-token
+    # quantiser: the same bits as dequant_swiglu_quant on the int32 [M, 2I]
+    # accumulators, without writing and re-reading them (~2 us per layer)
+    aq, sa = K.quantize_act_i8(K.gemm_a8w8(mq.reshape(-1, mq.shape[-1]), ms, gate_up.w, gate_up.s,
+                                           swiglu=True))
     acc = K.a8w8_int_gemm(aq, down.w)
     last = index + 1 == stack.config.num_hidden_layers
     norm = stack.norm if last else stack.layers[index + 1].input_layernorm

@@ -1084,6 +1084,23 @@ def test_dequant_swiglu_quant(gpu, m, n):
     assert torch.equal(q, q_exp) and torch.equal(s, s_exp)
 
 
+@pytest.mark.parametrize("m", [1024, 90])
+def test_gemm_i8_swiglu_then_quant_equals_dequant_swiglu_quant(gpu, m):
+    """The A8W8 prefill MLP runs the SwiGLU in the int8 GEMM's epilogue and
+    quantises its bf16 output per token: the same int8 rows and scales as
+    quantising the SwiGLU of the int32 [gate; up] accumulators."""
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 97)
+    w = torch.randint(-127, 128, (2 * 6144, 2048), device=gpu, dtype=torch.int8, generator=g)
+    sw = torch.rand(2 * 6144, device=gpu, generator=g) * 1e-3
+    x = torch.randn(m, 2048, device=gpu, generator=g).to(BF)
+    xq, sx = K.quantize_act_i8(x)
+    q_exp, s_exp = K.dequant_swiglu_quant(K.a8w8_int_gemm(xq, w), sx, sw)
+    q, s = K.quantize_act_i8(K.gemm_a8w8(xq, sx, w, sw, swiglu=True))
+    assert torch.equal(q, q_exp) and torch.equal(s.reshape(-1), s_exp.reshape(-1))
+
+
 @pytest.mark.parametrize("m,n,k", [(1024, 6144, 2048), (200, 500, 2048)])
 def test_gemm_swiglu_bf16(gpu, m, n, k):
     """Packed gate/up GEMM with the SwiGLU epilogue vs F.linear + silu_and_mul
