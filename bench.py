@@ -403,7 +403,7 @@ def gemm_sweep(dev, quick: bool = False) -> None:
     # (N, K, count per prefill, packed SwiGLU)
     shapes = [(8320, 2048, 18, False), (2048, 2048, 24, False), (5120, 2048, 6, False),
               (12288, 2048, 24, True), (2048, 6144, 24, False)]
-    stage = {t: 128 for t in range(8)}
+    stage = {t: 128 for t in range(9)}
     print("# N x K (per prefill) | implementation | plan (tile, K splits) | us | TFLOP/s (TOP/s)")
     for n, k, count, swiglu in shapes:
         flops = 2 * m * n * k
@@ -420,11 +420,11 @@ def gemm_sweep(dev, quick: bool = False) -> None:
             row("library bf16 (F.linear) + silu_and_mul", "-",
                 graph_time_us(lambda i: K.silu_and_mul(F.linear(x, w[i % nset])), nset, 5))
         row("library bf16 (F.linear)", "-", graph_time_us(lambda i: F.linear(x, w[i % nset]), nset, 5))
-        plans = [None] if quick else [None, (0, 1), (5, 1), (1, 1), (6, 1), (7, 1), (2, 1), (3, 1), (6, 2), (7, 2)]
+        plans = [None] if quick else [None, (0, 1), (5, 1), (1, 1), (6, 1), (7, 1), (8, 1), (2, 1), (3, 1), (6, 2), (7, 2)]
         for plan in plans:
             if plan and ((2 * k // stage[plan[0]]) % plan[1] or (swiglu and plan[1] > 1)):
                 continue
-            if swiglu and (plan is None or plan[0] not in (5, 6, 7)):
+            if swiglu and (plan is None or plan[0] not in (5, 6, 7, 8)):
                 us = graph_time_us(lambda i: K.gemm_bf16(x, w[i % nset], swiglu=True, plan=plan), nset, 5)
                 row("own bf16 + SwiGLU epilogue (q35_gemm kind 1)", plan or "default plan", us)
             us = graph_time_us(lambda i: K.gemm_bf16(x, w[i % nset], plan=plan), nset, 5)
@@ -446,14 +446,14 @@ def gemm_sweep(dev, quick: bool = False) -> None:
         row("library int8 (_int_mm)", "-", graph_time_us(lambda i: torch._int_mm(xq, wq[i % nset8].t()),
                                                         nset8, 5))
         row("library int8 (_int_mm) + dequant", "-", graph_time_us(lib_i8, nset8, 5))
-        plans = [None] if quick else [None, (0, 1), (5, 1), (1, 1), (6, 1), (7, 1), (2, 1), (3, 1), (6, 2), (7, 2)]
+        plans = [None] if quick else [None, (0, 1), (5, 1), (1, 1), (6, 1), (7, 1), (8, 1), (2, 1), (3, 1), (6, 2), (7, 2)]
         for plan in plans:
             if plan and (k // stage[plan[0]]) % plan[1]:
                 continue
             us = graph_time_us(lambda i: K.gemm_into(xq, wq[i % nset8], acc, K.GEMM_I32, plan=plan),
                                nset8, 5)
             row("own int8 -> int32 (q35_gemm kind 2)", plan or "default plan", us)
-            if plan is not None and plan[0] in (5, 6, 7):
+            if plan is not None and plan[0] in (5, 6, 7, 8):
                 continue
             us = graph_time_us(lambda i: K.gemm_a8w8(xq, sx, wq[i % nset8], sw, plan=plan), nset8, 5)
             row("own int8 + fused dequant (q35_gemm kind 3)", plan or "default plan", us)

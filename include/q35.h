@@ -365,11 +365,11 @@ int q35_dequant_swiglu_i32(const void* acc, const void* s_x, const void* s_w, vo
  * K * (element bytes) must be a multiple of 128 (the stage width); A and B
  * 16-byte aligned; each operand below 2^32 bytes (bf16: 2^31 elements).
  * tile < 0 picks the library's plan (tile and K splits by output shape);
- * otherwise tile 0-7 (outputs per workgroup: 0, 4, 5 256x192; 1, 6, 7
- * 128x128; 2 256x128; 3 128x192; SwiGLU kinds: half as many output columns;
- * 5-7 store from registers and take kinds 0 and 2 only) with `splits`
- * workgroups per tile along K (1-8, dividing the stage count; tiles 1, 2,
- * 3, 6, 7 and kinds 0, 2, 3 only). A plan that splits K needs a workspace of
+ * otherwise tile 0-8 (outputs per workgroup: 0, 4, 5 256x192; 1, 6, 7
+ * 128x128; 2 256x128; 3 128x192; 8 128x64; SwiGLU kinds: half as many
+ * output columns; 5-8 store from registers and take kinds 0 and 2 only)
+ * with `splits` workgroups per tile along K (1-8, dividing the stage count;
+ * tiles 1, 2, 3, 6, 7, 8 and kinds 0, 2, 3 only). A plan that splits K needs a workspace of
  * q35_gemm_workspace bytes (arrival counters + partial tiles), zero-filled
  * before its first use; each launch leaves the counters at zero again (after
  * a launch that failed part way, zero it again). Two launches that overlap in

@@ -327,7 +327,12 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
 #pragma unroll
       for (int q = 0; q < NMF; ++q) {
         mfma(t & 1, q);
-        if (q < NR) read1(abuf, bbuf, t + 1, (t + 1) & 1, q);
+        if constexpr (NR <= NMF) {
+          if (q < NR) read1(abuf, bbuf, t + 1, (t + 1) & 1, q);
+        } else {  // more fragments than MFMAs per step: spread them over the slots
+#pragma unroll
+          for (int r = q * NR / NMF; r < (q + 1) * NR / NMF; ++r) read1(abuf, bbuf, t + 1, (t + 1) & 1, r);
+        }
         const int slot = t * NMF + q;
         if (RA && slot < LA) dma(kt + NSA - 1, rabuf, 0, slot);
         if (RB_ && slot >= LA && slot < LPW) dma(kt + NSB - 1, 0, rbbuf, slot);
@@ -593,6 +598,7 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
 //   4: 256 x 192 (4 x 3), RB 128, NSA 2, NSB 2,       staged  (112 KiB)
 //   5: tile 0 with direct stores; 6: tile 1 with direct stores; 7: tile 6
 //   without K rotation
+//   8: 128 x 64 (2 x 1), RB 128, NSA 6, NSB 8, rot, direct   (160 KiB)
 #define Q35_GEMM_TILES(X)                     \
   X(0, 2, 2, 4, 3, 128, 2, 4, false, true)    \
   X(1, 2, 2, 2, 2, 128, 4, 6, true, true)     \
@@ -601,13 +607,14 @@ __global__ __launch_bounds__(256, 1) void gemm_ring(const GemmArgs a) {
   X(4, 2, 2, 4, 3, 128, 2, 2, false, true)    \
   X(5, 2, 2, 4, 3, 128, 2, 4, false, false)   \
   X(6, 2, 2, 2, 2, 128, 4, 6, true, false)    \
-  X(7, 2, 2, 2, 2, 128, 4, 6, false, false)
-constexpr int kTiles = 8;
-constexpr int kTM[kTiles] = {256, 128, 256, 128, 256, 256, 128, 128};
-constexpr int kTN[kTiles] = {192, 128, 128, 192, 192, 192, 128, 128};
-constexpr int kRB[kTiles] = {128, 128, 128, 128, 128, 128, 128, 128};
-constexpr bool kStaged[kTiles] = {true, true, true, true, true, false, false, false};
-constexpr bool kSplitOk[kTiles] = {false, true, true, true, false, false, true, true};  // up to 8 blocks per wave
+  X(7, 2, 2, 2, 2, 128, 4, 6, false, false)   \
+  X(8, 2, 2, 2, 1, 128, 6, 8, true, false)
+constexpr int kTiles = 9;
+constexpr int kTM[kTiles] = {256, 128, 256, 128, 256, 256, 128, 128, 128};
+constexpr int kTN[kTiles] = {192, 128, 128, 192, 192, 192, 128, 128, 64};
+constexpr int kRB[kTiles] = {128, 128, 128, 128, 128, 128, 128, 128, 128};
+constexpr bool kStaged[kTiles] = {true, true, true, true, true, false, false, false, false};
+constexpr bool kSplitOk[kTiles] = {false, true, true, true, false, false, true, true, true};  // up to 8 blocks per wave
 constexpr int kMaxSplits = 8;
 
 long long tiles_of(int tile, int M, int N, int kind) {
@@ -638,6 +645,11 @@ void plan(int M, int N, int K, int kind, int* tile, int* splits) {
     *tile = direct ? 5 : 0;
   } else if (tiles_of(3, M, N, kind) >= 160) {
     *tile = 3;
+  } else if (direct && tiles_of(8, M, N, kind) <= 256) {
+    // one round of 128x64 tiles: at M = 1024, N = 2048 all 256 CUs without a
+    // K split (o_proj 18.4 -> 14.8 us, down 44.9 -> 37.9 us against 128x128
+    // tiles on 128 CUs, split 2 for the down projection)
+    *tile = 8;
   } else {
     *tile = direct ? 6 : 1;
     const long long t = tiles_of(1, M, N, kind);
@@ -733,7 +745,7 @@ long long q35_gemm_workspace(int M, int N, int K, int kind, int tile, int splits
 // int32, 3 int8 -> bf16 dequant, 4 int8 SwiGLU; see gemm.hip's header).
 // K * element bytes a multiple of 128 (the stage width); A and B 16-byte
 // aligned; every operand below 2^32 bytes. tile < 0 picks the default plan,
-// otherwise tile 0-7 with `splits` K splits (the stage count divisible by
+// otherwise tile 0-8 with `splits` K splits (the stage count divisible by
 // splits). A split plan needs a workspace of q35_gemm_workspace bytes,
 // zero-filled before its first use.
 int q35_gemm(const void* A, const void* B, void* C, int M, int N, int K, int kind, const void* s_x,

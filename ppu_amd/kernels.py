@@ -493,7 +493,7 @@ def gemm_into(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, kind: int, *,
               plan: tuple[int, int] | None = None) -> torch.Tensor:
     """``C = A . B^T`` of one kind on the hand-written matrix-core GEMM
     (``q35_gemm``): ``a`` [M, K], ``b`` [N, K] (SwiGLU kinds [2N, K]), ``c``
-    [M, N] written in place; all contiguous on the GPU. ``plan`` = (tile 0-3,
+    [M, N] written in place; all contiguous on the GPU. ``plan`` = (tile 0-8,
     K splits) overrides the library's choice (for measurement)."""
 
     m, k = a.shape
@@ -543,7 +543,7 @@ def gemm_bf16(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
     and out, fp32 accumulate) or, with ``swiglu``, ``silu_and_mul(F.linear(x,
     W))`` for a packed ``[gate; up]`` weight in one launch (reference
     integration.py:183-185, kernels.py:158-180). K must be a multiple of 64.
-    ``plan`` = (tile 0-3, K splits) overrides the library's choice."""
+    ``plan`` = (tile 0-8, K splits) overrides the library's choice."""
 
     x2, n = _gemm_operands(x, weight, _BF16, swiglu)
     y = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_BF16)
@@ -1361,7 +1361,7 @@ def gemm_a8w8(xq: torch.Tensor, x_scale: torch.Tensor, weight_q: torch.Tensor,
     the dequant of reference explore_runtime_quantization.py:173-180), or with
     ``swiglu`` the SwiGLU of a packed ``[gate; up]`` int8 weight on the
     dequantised bf16 gate and up. K must be a multiple of 128. ``plan`` =
-    (tile 0-3, K splits) overrides the library's choice."""
+    (tile 0-8, K splits) overrides the library's choice."""
 
     if xq.ndim != 2:
         raise ValueError("int8 GEMM activations must be [M, K]")

@@ -887,11 +887,12 @@ def test_gemm_bf16(gpu, m, n, k):
     close(y, (x.float() @ w.float().t()).to(BF))
 
 
-_STAGE_BYTES = {t: 128 for t in range(8)}
+_STAGE_BYTES = {t: 128 for t in range(9)}
 
 
 @pytest.mark.parametrize("tile,splits", [(0, 1), (4, 1), (5, 1), (1, 1), (1, 2), (1, 3), (1, 8),
-                                         (2, 1), (2, 2), (2, 4), (3, 1), (3, 3), (6, 1), (6, 2), (7, 4)])
+                                         (2, 1), (2, 2), (2, 4), (3, 1), (3, 3), (6, 1), (6, 2), (7, 4),
+                                         (8, 1), (8, 2)])
 @pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (300, 700, 1536)])
 def test_gemm_bf16_split_plans(gpu, tile, splits, m, n, k):
     """Every tile shape with K split over workgroups (the last one to finish a
@@ -929,7 +930,7 @@ def test_gemm_rejects_invalid_plans(gpu):
 
     x = torch.zeros(64, 2048, dtype=BF, device=gpu)
     w = torch.zeros(256, 2048, dtype=BF, device=gpu)
-    for plan in ((0, 2), (4, 2), (5, 2), (1, 5), (8, 1)):
+    for plan in ((0, 2), (4, 2), (5, 2), (1, 5), (9, 1)):
         with pytest.raises((ValueError, RuntimeError)):
             K.gemm_bf16(x, w, plan=plan)
     with pytest.raises((ValueError, RuntimeError)):
@@ -982,7 +983,8 @@ def test_gemm_a8w8(gpu, plan, m, n, k):
         assert torch.equal(y3, y1)
 
 
-@pytest.mark.parametrize("plan", [None, (0, 1), (4, 1), (5, 1), (1, 2), (2, 3), (3, 8), (6, 2)])
+@pytest.mark.parametrize("plan", [None, (0, 1), (4, 1), (5, 1), (1, 2), (2, 3), (3, 8), (6, 2), (8, 1),
+                                  (8, 4)])
 @pytest.mark.parametrize("m,n,k", [(1024, 2048, 6144), (1024, 8320, 2048), (33, 520, 1024)])
 def test_int8_gemm_int32_exact(gpu, plan, m, n, k):
     """The int8 GEMM's int32 accumulators (what the A8W8 prefill hands to the
