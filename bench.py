@@ -827,6 +827,73 @@ def cpu_baseline(state, cfg, prompt, decode_steps: int, eager: bool = True) -> d
     return ref
 
 
+def cpu_kernel_table() -> dict:
+    """Benchmark configs 1-4 on the host cores through the oracle's
+    restatement of the reference's CPU arithmetic (torch / numpy on the same
+    threads as the config-5 leg): the median time per call over a few calls
+    and the algorithmic bytes of the GPU table over it. Config 2's int8
+    product is numpy's exact int64 matmul; config 4 is one token of the
+    model's chain (conv update, delta step, gated norm), timed over 64
+    sequential tokens."""
+    import statistics
+
+    import numpy as np
+    import torch
+
+    from oracle import a8w8 as oa
+    from oracle import ops as oo
+
+    g = torch.Generator().manual_seed(20260819)
+    bf = torch.bfloat16
+    out = {}
+
+    def timed(fn, reps):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts) * 1e6
+
+    def rec(name, us, nbytes):
+        out[name] = {"us": round(us, 1), "GB/s": round(nbytes / us / 1e3, 2)}
+
+    w = (torch.randn(6144, 2048, generator=g) * 0.02).to(bf)
+    x, r = torch.randn(1, 2048, generator=g).to(bf), torch.randn(1, 2048, generator=g).to(bf)
+    nw = (torch.randn(2048, generator=g) * 0.02 + 1).to(bf)
+    rec("cfg1_resnorm_gemv_6144x2048",
+        timed(lambda: oo.linear(oo.residual_add_rms_norm(r, x, nw, 1e-6)[1], w), 5), 25_198_592)
+    for nn, kk in ((12288, 2048), (2048, 6144)):
+        wq, sw = oa.quantize_weight((torch.randn(nn, kk, generator=g) * 0.02).to(bf))
+        for m in (1, 4, 16):
+            xm = torch.randn(m, kk, generator=g).to(bf)
+            rec(f"cfg2_a8w8_{nn}x{kk}_m{m}", timed(lambda: oa.a8w8_linear(xm, wq, sw), 3),
+                nn * kk + 4 * nn + 2 * kk * m + 2 * nn * m)
+    for ctx in (512, 2048, 8192):
+        kc = torch.randn(1, 2, ctx, 256, generator=g).to(bf)
+        vc = torch.randn(1, 2, ctx, 256, generator=g).to(bf)
+        q = torch.randn(1, 8, 1, 256, generator=g).to(bf)
+        rec(f"cfg3_gqa_decode_L{ctx}", timed(lambda: oo.gqa_decode_attention(q, kc, vc, ctx, 1 / 16), 3),
+            2048 * ctx + 8192)
+    state = torch.randn(1, 16, 128, 128, generator=g) * 0.1
+    cw = (torch.randn(6144, 4, generator=g) * 0.02).to(bf)
+    cs = torch.zeros(1, 6144, 4, dtype=bf)
+    z16 = torch.zeros(16, dtype=bf)
+    gw = torch.ones(128, dtype=bf)
+    toks = [torch.randn(1, 1, 8320, generator=g).to(bf) for _ in range(64)]
+
+    def chain():
+        for packed in toks:
+            qkv = oo.causal_conv1d(packed, cw, cs)
+            core = oo.delta_recurrent(qkv, packed, z16, z16, state)
+            z = packed[..., 6144:8192].reshape(16, 128)
+            oo.gated_rms_norm(core.reshape(16, 128), z, gw, 1e-6)
+
+    rec("cfg4_delta_decode_chain_per_token", timed(chain, 1) / 64, 2_265_216)
+    log("CPU configs 1-4 (oracle ops): " + ", ".join(f"{k} {v['us']} us" for k, v in out.items()))
+    return out
+
+
 def _eager_cpu(state, cfg, prompt, decode_steps: int) -> dict:
     import torch
     from transformers.cache_utils import DynamicCache
@@ -1130,6 +1197,7 @@ def main() -> None:
         log("CPU baseline ...")
         cpu = cpu_baseline(state, cfg, prompt_cpu[:, : args.cpu_prompt], args.cpu_decode_steps,
                            eager=not args.no_eager)
+        cpu["per_config"] = cpu_kernel_table()
 
     result = {
         "metric": "decode tokens/s (batch 1, greedy) + TTFT, 1 GPU",
