@@ -122,8 +122,10 @@ __global__ __launch_bounds__(256) void qgkv_norm_rope_k(
 // split; gqa_decode_combine merges the splits.
 constexpr int kAD = 256;
 constexpr int kMaxG = 8;
-constexpr int kSplitWaves = 4;             // waves per split workgroup
-constexpr int kWaveTok = 8;                // tokens per wave per iteration
+constexpr int kSplitWaves = 4;                // waves per split workgroup
+constexpr int kWaveTok = 32 / kSplitWaves;    // tokens per wave per iteration
+constexpr int kWaveGroups = kWaveTok / 4;     // K row groups of 4 tokens per wave
+static_assert(kWaveTok % 4 == 0 && kWaveGroups >= 1, "4-token K row groups per wave");
 constexpr int kIterTok = kSplitWaves * kWaveTok;  // tokens per workgroup iteration
 constexpr int kMaxSplits = 128;            // splits per KV head
 
@@ -359,12 +361,12 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
   const int rw = lane >> 4;
   const int ds = lane & 15;
   const int tmax = min(start + chunk, cache_len) - 1;
-  uint4 kr[2][2];
+  uint4 kr[kWaveGroups][2];
   uint2 vr[kWaveTok];
-  auto load_kv = [&](int it, uint4 (&kd)[2][2], uint2 (&vd)[kWaveTok]) {
+  auto load_kv = [&](int it, uint4 (&kd)[kWaveGroups][2], uint2 (&vd)[kWaveTok]) {
     const int tb = start + it * kIterTok + wid * kWaveTok;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < kWaveGroups; ++gi) {
       const int t = min(tb + 4 * gi + rw, tmax);
       kd[gi][0] = *reinterpret_cast<const uint4*>(Kh + (size_t)t * kAD + ds * 8);
       kd[gi][1] = *reinterpret_cast<const uint4*>(Kh + (size_t)t * kAD + 128 + ds * 8);
@@ -443,8 +445,8 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
       vf[i][3] = in ? bf_hi(VR[i].y) : 0.f;                                                     \
     }                                                                                           \
     _Pragma("unroll") for (int g = 0; g < G; ++g) {                                             \
-      float s[2];                                                                               \
-      _Pragma("unroll") for (int gi = 0; gi < 2; ++gi) {                                        \
+      float s[kWaveGroups];                                                                     \
+      _Pragma("unroll") for (int gi = 0; gi < kWaveGroups; ++gi) {                              \
         const uint4 k0 = KR[gi][0], k1 = KR[gi][1];                                             \
         float d = dot2_bf16(qp[g][0], k0.x, 0.f);                                               \
         d = dot2_bf16(qp[g][1], k0.y, d);                                                       \
@@ -457,17 +459,20 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
         d = row16_sum(d) * scale;                                                               \
         s[gi] = tb + 4 * gi + rw < end ? d : -INFINITY;                                         \
       }                                                                                         \
-      const float m_new = fmaxf(m[g], rows4_max(fmaxf(s[0], s[1])));                           \
+      float smax = s[0];                                                                        \
+      _Pragma("unroll") for (int gi = 1; gi < kWaveGroups; ++gi) smax = fmaxf(smax, s[gi]);     \
+      const float m_new = fmaxf(m[g], rows4_max(smax));                                         \
       /* A wave whose tokens so far all lie past the valid end keeps m = -inf:              */  \
       /* subtract 0 then, so that corr and p are 0 instead of NaN.                          */  \
       const float m_sub = m_new == -INFINITY ? 0.f : m_new;                                     \
       const float corr = expf(m[g] - m_sub);                                                    \
-      const float p0 = expf(s[0] - m_sub), p1 = expf(s[1] - m_sub);                             \
+      float pg[kWaveGroups];                                                                    \
+      _Pragma("unroll") for (int gi = 0; gi < kWaveGroups; ++gi) pg[gi] = expf(s[gi] - m_sub);  \
       _Pragma("unroll") for (int e = 0; e < 4; ++e) acc[g][e] *= corr;                          \
       float psum = 0.f;                                                                         \
       _Pragma("unroll") for (int i = 0; i < kWaveTok; ++i) {                                    \
         const float pi = __int_as_float(                                                        \
-            __builtin_amdgcn_readlane(__float_as_int(i < 4 ? p0 : p1), 16 * (i & 3)));          \
+            __builtin_amdgcn_readlane(__float_as_int(pg[i / 4]), 16 * (i & 3)));                \
         psum += pi;                                                                             \
         _Pragma("unroll") for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]); \
       }                                                                                         \
@@ -479,7 +484,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gqa_decode_split(
   // requested before the current one is reduced; nothing copies a set whose
   // loads are in flight, and a single step (the decode shape) issues no
   // prefetch at all.
-  uint4 kb[2][2];
+  uint4 kb[kWaveGroups][2];
   uint2 vb[kWaveTok];
   int it = 0;
   for (; it + 1 < n_iter; it += 2) {
