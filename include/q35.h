@@ -24,10 +24,10 @@ extern "C" {
 #endif
 
 /* ABI version of this header; q35_abi_version() must return it. */
-#define Q35_ABI_VERSION 3
+#define Q35_ABI_VERSION 4
 int q35_abi_version(void);
 
-/* Zero n device buffers in one launch: ptrs[i] (16-byte aligned) holds
+/* Zero n device buffers in one launch per 128: ptrs[i] (16-byte aligned) holds
  * nbytes[i] bytes; ptrs and nbytes are host arrays. Replaces the per-tensor
  * zero_() calls of Transformers' Cache.reset() on a reused generation cache
  * (evaluation_wrapper.py:350-352). */
@@ -90,9 +90,13 @@ int q35_silu_mul(const void* packed, void* out, long long rows, int width, void*
 int q35_silu_mul_t(const void* packed_t, void* out, int rows, int width, void* stream);
 
 /* attention_gate_mul: out = bf16(x * bf16(sigmoid(gate))), gate read from the
- * packed QGKV row. Replaces qwen35_fused/kernels.py:312 (kernel :285-333). */
+ * packed QGKV row. Replaces qwen35_fused/kernels.py:312 (kernel :285-333).
+ * advance (optional int64 device scalar): *advance += amount in the same
+ * launch, the static cache's cumulative_length.add_ of a prefill
+ * (integration.py:338) moved after the attention that reads the start. */
 int q35_attn_gate_mul(const void* x, const void* packed, void* out, long long tokens, int hidden,
-                      int packed_stride, int head_dim, void* stream);
+                      int packed_stride, int head_dim, void* advance, long long amount,
+                      void* stream);
 
 /* ---- bf16 GEMV (M = 1) ------------------------------------------------- */
 
@@ -308,8 +312,9 @@ int q35_gqa_decode_fused(const void* packed, const void* q_w, const void* k_w, i
 
 /* Causal GQA prefill attention: q [B,QH,L,D], K/V [B,KVH,cache_len,D] holding
  * the L prompt tokens from position start; query row i attends to keys
- * [0, start + i]. start = *valid_len - L when valid_len (int64 device scalar,
- * already including the L tokens) is given, else kv_start. out [B,L,QH*D].
+ * [0, start + i]. start = *valid_len - L + kv_start when valid_len (int64
+ * device scalar) is given (kv_start = 0 when it already counts the L tokens,
+ * L when it still holds the start), else kv_start. out [B,L,QH*D].
  * Replaces the prefill ALL_ATTENTION_FUNCTIONS call of
  * qwen35_fused/integration.py:360-372. */
 int q35_gqa_prefill(const void* q, const void* K, const void* V, void* out, int B, int QH, int KVH,

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libq35.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -38,7 +38,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_gated_rmsnorm_grouped": (_I, [_P, _P, _I, _L, _P, _I, _P, _I, _F, _P]),
     "q35_silu_mul": (_I, [_P, _P, _L, _I, _P]),
     "q35_silu_mul_t": (_I, [_P, _P, _I, _I, _P]),
-    "q35_attn_gate_mul": (_I, [_P, _P, _P, _L, _I, _I, _I, _P]),
+    "q35_attn_gate_mul": (_I, [_P, _P, _P, _L, _I, _I, _I, _P, _L, _P]),
     "q35_gemv_bf16": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _I, _I, _P]),
     "q35_swiglu_gemv": (_I, [_P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _I, _I, _P]),
     "q35_gemv_conv": (

@@ -6,7 +6,7 @@
 
 namespace {
 
-constexpr int kZeroMax = 32;  // buffers per launch (kernel argument struct)
+constexpr int kZeroMax = 128;  // buffers per launch (kernel argument struct, 2 KiB)
 
 struct ZeroArgs {
   uint8_t* p[kZeroMax];
@@ -67,7 +67,7 @@ int device_cus() {
 
 extern "C" {
 
-int q35_abi_version(void) { return 3; }
+int q35_abi_version(void) { return 4; }
 
 // Zero n device buffers (host arrays of pointers and byte counts; each
 // pointer 16-byte aligned). Replaces the per-tensor zero_() calls of

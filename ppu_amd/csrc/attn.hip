@@ -697,7 +697,7 @@ __global__ __launch_bounds__(G * 64) void gqa_prefill_mfma(
   const int b = blockIdx.z;
   const int h = kvh * G + wid;
   const int q0 = tile * 16;
-  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  long long ks = valid_len ? valid_len[0] - L + kv_start_host : (long long)kv_start_host;
   if (ks < 0) ks = 0;
   if (ks + L > cache_len) ks = cache_len - L;
   const int kv_start = (int)ks;
@@ -886,7 +886,7 @@ __global__ __launch_bounds__(2 * G * 64) void gqa_prefill_fa(
   const int b = blockIdx.z;
   const int h = kvh * G + g;
   const int q0 = tile * 16;
-  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  long long ks = valid_len ? valid_len[0] - L + kv_start_host : (long long)kv_start_host;
   if (ks < 0) ks = 0;
   if (ks + L > cache_len) ks = cache_len - L;
   const int kv_start = (int)ks;
@@ -1093,7 +1093,7 @@ __global__ __launch_bounds__(G * 256) void gqa_prefill_merge(
   const int tile = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int ntiles = gridDim.x;
   const int q0 = tile * 16;
-  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  long long ks = valid_len ? valid_len[0] - L + kv_start_host : (long long)kv_start_host;
   if (ks < 0) ks = 0;
   if (ks + L > cache_len) ks = cache_len - L;
   const int n_keys = min((int)ks + min(q0 + 16, L), cache_len);
@@ -1144,9 +1144,10 @@ __global__ __launch_bounds__(256) void gqa_prefill_rows(
   const int lane = threadIdx.x & 63;
   const long long wv = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wv >= (long long)B * QH * L) return;
-  // With a device length (static cache, already including these L tokens)
-  // the prompt starts at valid_len - L; the bound keeps reads in the cache.
-  long long ks = valid_len ? valid_len[0] - L : (long long)kv_start_host;
+  // With a device length the prompt starts at valid_len - L + kv_start
+  // (kv_start = 0 when the length already counts these L tokens, L when it
+  // holds the start); the bound keeps reads in the cache.
+  long long ks = valid_len ? valid_len[0] - L + kv_start_host : (long long)kv_start_host;
   if (ks < 0) ks = 0;
   if (ks + L > cache_len) ks = cache_len - L;
   const int kv_start = (int)ks;

@@ -305,8 +305,10 @@ __global__ __launch_bounds__(256) void attn_gate_elems(const uint16_t* __restric
                                                        const uint16_t* __restrict__ packed,
                                                        uint16_t* __restrict__ out, long long total,
                                                        int hidden, int packed_stride,
-                                                       int head_dim) {
+                                                       int head_dim, long long* advance,
+                                                       long long amount) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (advance && i == 0) advance[0] += amount;
   if (i >= total) return;
   const long long token = i / hidden;
   const int col = (int)(i - token * hidden);
@@ -319,11 +321,16 @@ __global__ __launch_bounds__(256) void attn_gate_elems(const uint16_t* __restric
 
 // attn_gate_elems with 8 columns per thread (16-byte loads; head_dim,
 // hidden and packed_stride multiples of 8), grid (column blocks, tokens).
+// Both forms add `amount` to the int64 counter `advance` (when given) from
+// one thread: the prefill's cache-length advance, which no kernel after the
+// attention reads before this one ends.
 __global__ __launch_bounds__(256) void attn_gate_vec(const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ packed,
                                                      uint16_t* __restrict__ out, long long tokens,
-                                                     int hidden, int packed_stride, int head_dim) {
+                                                     int hidden, int packed_stride, int head_dim,
+                                                     long long* advance, long long amount) {
   const int col = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (advance && col == 0 && blockIdx.y == 0) advance[0] += amount;
   if (col >= hidden) return;
   const int head = col / head_dim;
   const int hc = col - head * head_dim;
@@ -448,23 +455,25 @@ int q35_silu_mul_t(const void* packed_t, void* out, int rows, int width, hipStre
 }
 
 int q35_attn_gate_mul(const void* x, const void* packed, void* out, long long tokens, int hidden,
-                      int packed_stride, int head_dim, hipStream_t stream) {
+                      int packed_stride, int head_dim, void* advance, long long amount,
+                      hipStream_t stream) {
   Q35_CHECK_ARG(tokens >= 0 && hidden > 0 && head_dim > 0 && hidden % head_dim == 0);
   Q35_CHECK_ARG(packed_stride >= 2 * hidden);
   const long long total = tokens * (long long)hidden;
-  if (total == 0) return 0;
+  if (total == 0 && (!advance || amount == 0)) return 0;
   if (head_dim % 8 == 0 && packed_stride % 8 == 0 && q35_aligned16(x) && q35_aligned16(packed) &&
       q35_aligned16(out)) {
-    const dim3 vgrid((unsigned)((hidden / 8 + 255) / 256), (unsigned)min(tokens, 65535ll));
+    const dim3 vgrid((unsigned)((hidden / 8 + 255) / 256), (unsigned)max(1ll, min(tokens, 65535ll)));
     attn_gate_vec<<<vgrid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)packed,
-                                             (uint16_t*)out, tokens, hidden, packed_stride, head_dim);
+                                             (uint16_t*)out, tokens, hidden, packed_stride, head_dim,
+                                             (long long*)advance, amount);
     return q35_last_error();
   }
-  const long long grid = (total + 255) / 256;
+  const long long grid = max(1ll, (total + 255) / 256);
   Q35_CHECK_ARG(grid < (1ll << 31));
   attn_gate_elems<<<(unsigned)grid, 256, 0, stream>>>((const uint16_t*)x, (const uint16_t*)packed,
                                                       (uint16_t*)out, total, hidden, packed_stride,
-                                                      head_dim);
+                                                      head_dim, (long long*)advance, amount);
   return q35_last_error();
 }
 

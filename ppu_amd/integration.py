@@ -379,19 +379,26 @@ def _attention_prefill(attn, hidden: torch.Tensor, position_embeddings, cache,
         cache_start=None if slot is None else slot.cumulative_length,
     )
     kv_start, valid = 0, None
-    if slot is not None:
+    decode = slot is not None and length == 1 and config.gqa_decode_attention
+    if decode:
         slot.cumulative_length.add_(length)
+        valid = slot.cumulative_length
+    elif slot is not None:
+        # the cache length still holds the start here: the attention reads it
+        # as such and the gate kernel advances it by `length` (one launch
+        # fewer than the reference's add_ before the attention)
         valid = slot.cumulative_length
     elif cache is not None:
         k, v = cache.update(k, v, attn.layer_idx)
         kv_start = k.shape[2] - length
-    if slot is not None and length == 1 and config.gqa_decode_attention:
+    if decode:
         out = K.gqa_decode_attention(q, slot.keys, slot.values, valid, attn.scaling,
                                      packed_gate=packed)
     else:
         out = K.gqa_prefill_attention(q, k.contiguous(), v.contiguous(), attn.scaling,
-                                      kv_start=kv_start, valid_length=valid)
-        out = K.attention_gate_mul(out, packed, attn.head_dim)
+                                      kv_start=kv_start, valid_length=valid,
+                                      length_is_start=valid is not None)
+        out = K.attention_gate_mul(out, packed, attn.head_dim, advance=valid, amount=length)
     return attn.q35_o.to_int32(out) if int32_out else attn.q35_o(out)
 
 

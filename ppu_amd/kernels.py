@@ -223,8 +223,14 @@ def silu_and_mul_t(packed_t: torch.Tensor) -> torch.Tensor:
 
 
 @_device_checked
-def attention_gate_mul(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int) -> torch.Tensor:
-    """Multiply attention output by the gate inside the packed QGKV. reference kernels.py:312."""
+def attention_gate_mul(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int, *,
+                       advance: torch.Tensor | None = None, amount: int = 0) -> torch.Tensor:
+    """Multiply attention output by the gate inside the packed QGKV. reference kernels.py:312.
+
+    ``advance`` (an int64 GPU scalar, e.g. a static cache's cumulative length)
+    is incremented by ``amount`` in the same launch: the prefill's
+    ``cumulative_length.add_`` (reference integration.py:338), deferred to
+    the end of the attention so that no separate launch carries it."""
 
     if not x.is_contiguous() or not packed_qgkv.is_contiguous():
         raise ValueError("attention gate tensors must be contiguous")
@@ -236,10 +242,13 @@ def attention_gate_mul(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int
     if hidden % head_dim or packed_qgkv.shape[-1] < 2 * hidden:
         raise ValueError("attention gate layout does not match the packed projection")
     _need_bf16(x, packed_qgkv)
+    if advance is not None and (advance.dtype != torch.int64 or advance.numel() != 1
+                                or advance.device != x.device):
+        raise ValueError("advance must be an int64 scalar tensor on the attention output's GPU")
     out = torch.empty_like(x)
     tokens = x.numel() // hidden
     _lib.call("q35_attn_gate_mul", x.data_ptr(), packed_qgkv.data_ptr(), out.data_ptr(), tokens,
-              hidden, packed_qgkv.shape[-1], head_dim, _stream(x))
+              hidden, packed_qgkv.shape[-1], head_dim, _lib.ptr(advance), int(amount), _stream(x))
     return out
 
 
@@ -1101,13 +1110,16 @@ def gqa_prefill_attention(
     *,
     kv_start: int = 0,
     valid_length: torch.Tensor | None = None,
+    length_is_start: bool = False,
 ) -> torch.Tensor:
     """Causal GQA prefill attention: ``q [B,QH,L,D]`` row i attends to
     ``keys/values [B,KVH,C,D]`` positions ``[0, start + i]``, with
     ``start = valid_length - L`` when the device scalar ``valid_length``
     (already including the L tokens, as a static cache's length) is given,
-    else ``kv_start``. Returns ``[B, L, QH*D]`` bf16. Replaces the prefill
-    attention interface call of reference integration.py:360-372."""
+    ``start = valid_length`` with ``length_is_start`` (the length before the
+    L tokens, when its advance comes later), else ``kv_start``. Returns
+    ``[B, L, QH*D]`` bf16. Replaces the prefill attention interface call of
+    reference integration.py:360-372."""
 
     if q.ndim != 4 or keys.ndim != 4 or keys.shape != values.shape:
         raise ValueError("prefill attention expects q[B,QH,L,D] and K/V[B,KVH,C,D]")
@@ -1127,12 +1139,19 @@ def gqa_prefill_attention(
         raise ValueError("MI355X prefill attention kernels are built for head_dim 256")
     if valid_length is not None and (valid_length.dtype != torch.int64 or valid_length.device != q.device):
         raise ValueError("valid_length must be an int64 tensor on the GPU")
+    if valid_length is not None and kv_start:
+        raise ValueError("kv_start and valid_length are exclusive")
+    if length_is_start and valid_length is None:
+        raise ValueError("length_is_start needs valid_length")
     _need_bf16(q, keys, values)
     out = torch.empty((batch, seq_len, heads * dim), device=q.device, dtype=q.dtype)
     floats = _lib.load().q35_gqa_prefill_workspace(batch, heads, kv_heads, seq_len, cache_len)
     ws = torch.empty(max(floats, 1), device=q.device, dtype=torch.float32) if floats > 0 else None
+    # with a device length, the entry's kv_start is added to it: start = *valid_len - L + kv_start
+    offset = seq_len if length_is_start else 0
     _lib.call("q35_gqa_prefill", q.data_ptr(), keys.data_ptr(), values.data_ptr(), out.data_ptr(),
-              batch, heads, kv_heads, dim, seq_len, cache_len, kv_start, _lib.ptr(valid_length),
+              batch, heads, kv_heads, dim, seq_len, cache_len,
+              offset if valid_length is not None else kv_start, _lib.ptr(valid_length),
               float(scale), _lib.ptr(ws), floats, _stream(q))
     return out
 

@@ -129,6 +129,54 @@ def test_attention_gate_mul(gpu):
     close(K.attention_gate_mul(x.to(gpu), packed.to(gpu), 256), ref.attention_gate_mul(x, packed, 256))
 
 
+@pytest.mark.parametrize("tokens,hidden,head_dim", [(70, 2048, 256), (9, 36, 12), (0, 2048, 256)])
+def test_attention_gate_mul_advance(gpu, tokens, hidden, head_dim):
+    """The gate kernel's counter advance (the prefill's cache-length add_ moved
+    into it): the counter grows by `amount` exactly once whatever the grid
+    (16-byte form over 70 tokens, element form at head_dim 12, no tokens), and
+    the output bits are those of the call without it."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 6)
+    packed = randn(g, 1, tokens, 2 * hidden + 8).to(gpu)
+    x = randn(g, 1, tokens, hidden).to(gpu)
+    counter = torch.tensor(37, dtype=torch.int64, device=gpu)
+    plain = K.attention_gate_mul(x, packed, head_dim)
+    got = K.attention_gate_mul(x, packed, head_dim, advance=counter, amount=tokens + 5)
+    torch.cuda.synchronize()
+    assert int(counter) == 37 + tokens + 5
+    assert torch.equal(got, plain)
+    if tokens:
+        close(got.cpu(), ref.attention_gate_mul(x.cpu(), packed.cpu(), head_dim))
+    with pytest.raises(ValueError):
+        K.attention_gate_mul(x, packed, head_dim, advance=counter.to(torch.int32), amount=1)
+
+
+def test_zero_tensors_many(gpu):
+    """zero_tensors over 300 buffers (three launches of at most 128): every
+    buffer is cleared, odd byte counts and empty ones included, and the bytes
+    between the buffers are left as they were."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 7)
+    sizes = torch.randint(0, 5000, (300,), generator=g).tolist()
+    sizes[3], sizes[4], sizes[200] = 0, 1, 15
+    starts, at = [], 0
+    for n in sizes:
+        starts.append(at)
+        at += -(-n // 16) * 16 + 32  # a 16-byte aligned start and a gap after each buffer
+    pool = torch.full((at,), 0xAB, dtype=torch.uint8, device=gpu)
+    views = [pool[st : st + n] for st, n in zip(starts, sizes)]
+    K.zero_tensors(views)
+    torch.cuda.synchronize()
+    mask = torch.zeros(at, dtype=torch.bool)
+    for st, n in zip(starts, sizes):
+        mask[st : st + n] = True
+    host = pool.cpu()
+    assert not host[mask].any()
+    assert bool((host[~mask] == 0xAB).all())
+
+
 # ------------------------------------------------------------------ GEMV
 @pytest.mark.parametrize("n,k", [(6144, 2048), (8320, 2048), (5120, 2048), (2048, 2048),
                                  (2048, 6144), (257, 128), (100, 40)])
@@ -769,6 +817,11 @@ def test_prefill_attention_groupings(gpu, q_heads, kv_heads):
     valid = torch.tensor(start + seq_len, dtype=torch.int64, device=gpu)
     got = K.gqa_prefill_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), 0.0625, valid_length=valid)
     close(got, exp)
+    # the length before the prompt (its advance deferred to the gate kernel): same bits
+    before = torch.tensor(start, dtype=torch.int64, device=gpu)
+    got_s = K.gqa_prefill_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), 0.0625, valid_length=before,
+                                    length_is_start=True)
+    assert torch.equal(got_s, got)
 
 
 @pytest.mark.parametrize("q_heads,kv_heads", [(8, 2), (4, 2)])
@@ -793,6 +846,9 @@ def test_prefill_attention_split_keys(gpu, q_heads, kv_heads):
     assert _lib.load().q35_gqa_prefill_workspace(1, q_heads, kv_heads, seq_len, cache) > 0
     got = K.gqa_prefill_attention(qg, kg, vg, 0.0625, valid_length=valid)
     close(got, exp)
+    before = torch.tensor(start, dtype=torch.int64, device=gpu)
+    assert torch.equal(K.gqa_prefill_attention(qg, kg, vg, 0.0625, valid_length=before,
+                                               length_is_start=True), got)
     unsplit = torch.empty_like(got)
     _lib.call("q35_gqa_prefill", qg.data_ptr(), kg.data_ptr(), vg.data_ptr(), unsplit.data_ptr(),
               1, q_heads, kv_heads, 256, seq_len, cache, 0, valid.data_ptr(), 0.0625, None, 0,
