@@ -1076,7 +1076,7 @@ def main() -> None:
 
     from ppu_amd import synth
     from ppu_amd.generate import FusedGreedyGenerator, cache_bucket
-    from ppu_amd.graph import GreedyDecodeGraph
+    from ppu_amd.graph import GreedyDecodeGraph, decode_tokens
     from ppu_amd.integration import FusionConfig, apply_fusions
     from ppu_amd.kernels import lm_head_argmax
 
@@ -1132,15 +1132,16 @@ def main() -> None:
                               use_cache=True)
             tok = lm_head_argmax(out.last_hidden_state[:, -1].contiguous(), model.lm_head.weight)
             graph = GreedyDecodeGraph(model, cache, tok, torch.full((1, 1), PROMPT_LEN, device=dev,
-                                                                    dtype=torch.long))
-            for _ in range(args.warmup):
-                int(graph.replay().reshape(-1)[0].item())
+                                                                    dtype=torch.long), pipelined=True)
+            # the generation loop's host side: every token read on the host,
+            # the next step queued before the previous token is read
+            decode_tokens(graph, args.warmup)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
-            for _ in range(args.steps):
-                int(graph.replay().reshape(-1)[0].item())
+            timed_tokens = decode_tokens(graph, args.steps)
             torch.cuda.synchronize()
             elapsed = time.perf_counter() - t1
+            assert len(timed_tokens) == args.steps
             # pure device time per replay (no host read between replays)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             cache.reset()

@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; q35_abi_version() must return it. */
-#define Q35_ABI_VERSION 4
+#define Q35_ABI_VERSION 5
 int q35_abi_version(void);
 
 /* Zero n device buffers in one launch per 128: ptrs[i] (16-byte aligned) holds
@@ -161,12 +161,21 @@ int q35_swiglu_gemv_i8(const void* Wq, const void* s_w, const void* x, const voi
 /* Workspace slots (8 bytes each) for q35_lm_head_top1. */
 long long q35_lm_head_top1_workspace(int V, int K);
 /* out[0] (int64) = argmax_v bf16(W[v] . x), lowest index on ties; no logits stored.
- * With advance (int64 device array of n_advance <= 64) every element is incremented
- * after the token is written (the token feedback and position += 1 of graph.py:78-79).
+ * mirror (optional, 8-byte aligned, device-addressable: device memory or the
+ * q35_host_device_ptr address of pinned host memory) receives the same index
+ * from the same launch, so a host loop reads a captured step's token without a
+ * copy after it. With advance (int64 device array of n_advance <= 64) every
+ * element is incremented after the token is written (the token feedback and
+ * position += 1 of graph.py:78-79).
  * Replaces qwen35_fused/kernels.py:1146 (lm_head_argmax, kernels :1093-1143). */
 int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace,
-                     long long workspace_slots, void* out, void* advance, int n_advance,
-                     void* stream);
+                     long long workspace_slots, void* out, void* mirror, void* advance,
+                     int n_advance, void* stream);
+/* *dev = the address kernels use for the pinned, device-mapped host memory at
+ * `host` (hipHostMalloc / torch pin_memory); hipErrorInvalidValue for any
+ * other pointer. For the mirror argument of the top-1 entries; no
+ * counterpart in the reference (its loop copies the token to the host). */
+int q35_host_device_ptr(const void* host, void** dev);
 /* No counterpart in the reference: q35_lm_head_top1 for callers that cannot
  * allocate device memory (code under hipGraph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same result and arguments minus the
@@ -193,13 +202,14 @@ int q35_init(void);
  * the number of recomputed rows sets the cost). K = 2048; W, Wq, x and the
  * workspace 16-byte aligned. q35_lm_head_screen_prep makes Wq [V, K] int8 and
  * s, c [V] fp32 from W once; workspace of
- * q35_lm_head_top1_screened_workspace(V, K) bytes. */
+ * q35_lm_head_top1_screened_workspace(V, K) bytes; out, mirror and advance as
+ * for q35_lm_head_top1. */
 int q35_lm_head_screen_prep(const void* W, int V, int K, void* Wq, void* s, void* c, void* stream);
 long long q35_lm_head_top1_screened_workspace(int V, int K);
 int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, const void* c,
                               const void* x, int V, int K, void* workspace,
-                              long long workspace_bytes, void* out, void* advance, int n_advance,
-                              void* stream);
+                              long long workspace_bytes, void* out, void* mirror, void* advance,
+                              int n_advance, void* stream);
 /* Where a screened top-1 workspace for vocabulary V keeps the number of rows
  * each workgroup recomputed exactly (uint32 each, written by every call):
  * returns the byte offset, *n the count. Their sum is the call's bf16 row

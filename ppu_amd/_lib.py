@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libq35.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -50,7 +50,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_swiglu_gemv_i8": (
         _I, [_P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _P, _I, _I, _I, _P]),
     "q35_lm_head_top1_workspace": (_L, [_I, _I]),
-    "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),
+    "q35_lm_head_top1": (_I, [_P, _P, _I, _I, _P, _L, _P, _P, _P, _I, _P]),
     "q35_lm_head_top1_noalloc": (_I, [_P, _P, _I, _I, _P, _P, _I, _P]),
     "q35_init": (_I, []),
     "q35_conv1d_update": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
@@ -92,7 +92,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_lm_head_screen_prep": (_I, [_P, _I, _I, _P, _P, _P, _P]),
     "q35_lm_head_top1_screened_workspace": (_L, [_I, _I]),
     "q35_lm_head_screened_counts": (_L, [_I, ctypes.POINTER(_I)]),
-    "q35_lm_head_top1_screened": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _L, _P, _P, _I, _P]),
+    "q35_lm_head_top1_screened": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _L, _P, _P, _P, _I, _P]),
+    "q35_host_device_ptr": (_I, [_P, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

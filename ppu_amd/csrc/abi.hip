@@ -67,7 +67,7 @@ int device_cus() {
 
 extern "C" {
 
-int q35_abi_version(void) { return 4; }
+int q35_abi_version(void) { return 5; }
 
 // Zero n device buffers (host arrays of pointers and byte counts; each
 // pointer 16-byte aligned). Replaces the per-tensor zero_() calls of

@@ -515,9 +515,12 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(const GemvArgs a) {
   }
 }
 
+// out[0] = the index of the largest candidate key; `mirror` (may be null)
+// receives the same index (a second destination the caller reads, e.g. the
+// device address of pinned host memory); every advance[i] += 1 after.
 __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __restrict__ cand,
-                                                   int n, long long* out, long long* advance,
-                                                   int n_advance) {
+                                                   int n, long long* out, long long* mirror,
+                                                   long long* advance, int n_advance) {
   __shared__ unsigned long long s[16];
   uint64_t b = 0;
 #pragma unroll 8
@@ -528,7 +531,9 @@ __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __r
   if (threadIdx.x == 0) {
     uint64_t m = s[0];
     for (int i = 1; i < 16; ++i) m = u64_max(m, s[i]);
-    out[0] = (long long)top1_index(m);
+    const long long token = (long long)top1_index(m);
+    out[0] = token;
+    if (mirror) mirror[0] = token;
     for (int i = 0; i < n_advance; ++i) advance[i] += 1;
   }
 }
@@ -694,8 +699,8 @@ static int lm_device_cus() {
 // them. Every slot the final reduction reads is written by the same call, so
 // the workspace needs no clearing.
 int lm_head_top1_launch(const void* W, const void* x, int V, int K, void* workspace,
-                        long long workspace_slots, void* out, void* advance, int n_advance,
-                        hipStream_t stream) {
+                        long long workspace_slots, void* out, void* mirror, void* advance,
+                        int n_advance, hipStream_t stream) {
   GemvArgs a{(const uint16_t*)W, (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, nullptr,
              (unsigned long long*)workspace, V, K, 0, 0.f, nullptr, nullptr, nullptr, 0, 0,
              nullptr, 0};
@@ -710,7 +715,8 @@ int lm_head_top1_launch(const void* W, const void* x, int V, int K, void* worksp
   const int e = q35_last_error();
   if (e) return e;
   top1_final<<<1, 1024, 0, stream>>>((const unsigned long long*)workspace, (int)nc, (long long*)out,
-                                     (long long*)advance, advance ? n_advance : 0);
+                                     (long long*)mirror, (long long*)advance,
+                                     advance ? n_advance : 0);
   return q35_last_error();
 }
 
@@ -1143,15 +1149,33 @@ long long q35_lm_head_top1_workspace(int V, int K) {
   return (V + 3) / 4;  // enough for the one-row-per-wave fallback as well
 }
 
-// out[0] (int64) = argmax_v bf16(W[v].x), lowest index on ties.
+// out[0] (int64) = argmax_v bf16(W[v].x), lowest index on ties; mirror[0]
+// (optional) the same.
 int q35_lm_head_top1(const void* W, const void* x, int V, int K, void* workspace,
-                     long long workspace_slots, void* out, void* advance, int n_advance,
-                     hipStream_t stream) {
+                     long long workspace_slots, void* out, void* mirror, void* advance,
+                     int n_advance, hipStream_t stream) {
   Q35_CHECK_ARG(!advance || (n_advance >= 0 && n_advance <= 64));
   Q35_CHECK_ARG(V > 0 && K > 0 && W && x && workspace && out);
   Q35_CHECK_ARG(workspace_slots >= q35_lm_head_top1_workspace(V, K) && V < (1 << 30));
-  return lm_head_top1_launch(W, x, V, K, workspace, workspace_slots, out, advance, n_advance,
-                             stream);
+  Q35_CHECK_ARG(q35_aligned8(mirror));
+  return lm_head_top1_launch(W, x, V, K, workspace, workspace_slots, out, mirror, advance,
+                             n_advance, stream);
+}
+
+// The device address of pinned, device-mapped host memory (hipHostMalloc):
+// *dev = where a kernel stores to reach `host`. Anything else (pageable host
+// memory, device memory, null) returns hipErrorInvalidValue.
+int q35_host_device_ptr(const void* host, void** dev) {
+  Q35_CHECK_ARG(host && dev);
+  *dev = nullptr;
+  hipPointerAttribute_t attr{};
+  if (hipPointerGetAttributes(&attr, host) != hipSuccess) {
+    (void)hipGetLastError();  // an unregistered pointer leaves an error behind
+    return (int)hipErrorInvalidValue;
+  }
+  if (attr.type != hipMemoryTypeHost || !attr.devicePointer) return (int)hipErrorInvalidValue;
+  *dev = attr.devicePointer;
+  return 0;
 }
 
 // Screen operands of an lm_head weight W [V, K] (bf16, K = 2048): the int8
@@ -1181,15 +1205,16 @@ long long q35_lm_head_screened_counts(int V, int* n) {
 
 // out[0] = the index q35_lm_head_top1 returns for (W, x), found through the
 // int8 screen (Wq, s, c from q35_lm_head_screen_prep of this W) and the exact
-// recomputation of the rows it cannot exclude; `advance` as there. The
+// recomputation of the rows it cannot exclude; `mirror` and `advance` as there. The
 // workspace's last section holds, per workgroup, how many rows it
 // recomputed (q35_lm_head_screened_candidates sums them).
 int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, const void* c,
                               const void* x, int V, int K, void* workspace,
-                              long long workspace_bytes, void* out, void* advance, int n_advance,
-                              hipStream_t stream) {
+                              long long workspace_bytes, void* out, void* mirror, void* advance,
+                              int n_advance, hipStream_t stream) {
   Q35_CHECK_ARG(!advance || (n_advance >= 0 && n_advance <= 64));
   Q35_CHECK_ARG(W && Wq && s && c && x && workspace && out && V > 0 && K == 2048 && V < (1 << 30));
+  Q35_CHECK_ARG(q35_aligned8(mirror));
   Q35_CHECK_ARG(q35_aligned16(W) && q35_aligned16(Wq) && q35_aligned16(x) && q35_aligned16(workspace));
   Q35_CHECK_ARG(workspace_bytes >= screened_bytes(V));
   const long long nb = screened_parts();
@@ -1206,8 +1231,8 @@ int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, cons
       (const uint16_t*)W, (const uint16_t*)x, U, lpart, (int)nb, V, cand, ncand);
   e = q35_last_error();
   if (e) return e;
-  top1_final<<<1, 1024, 0, stream>>>(cand, (int)nb, (long long*)out, (long long*)advance,
-                                     advance ? n_advance : 0);
+  top1_final<<<1, 1024, 0, stream>>>(cand, (int)nb, (long long*)out, (long long*)mirror,
+                                     (long long*)advance, advance ? n_advance : 0);
   return q35_last_error();
 }
 
@@ -1235,8 +1260,8 @@ int q35_lm_head_top1_noalloc(const void* W, const void* x, int V, int K, void* o
   void* scratch = nullptr;
   const int e = top1_scratch(&scratch);
   if (e) return e;
-  return lm_head_top1_launch(W, x, V, K, scratch, kTop1ScratchSlots, out, advance, n_advance,
-                             stream);
+  return lm_head_top1_launch(W, x, V, K, scratch, kTop1ScratchSlots, out, nullptr, advance,
+                             n_advance, stream);
 }
 
 }  // extern "C"

@@ -18,9 +18,20 @@ of separate input/output buffers:
 
 Everything the captured kernels read between replays (token, position, cache
 length) lives in device memory, so ``replay`` is one graph launch.
+
+With ``pipelined`` (one step per replay, fused lm_head) the step is captured
+twice, and capture ``i``'s top-1 launch also stores the token into pinned host
+slot ``i`` (``lm_head_argmax(..., mirror=)``). ``launch`` replays the two
+captures alternately and ``result`` waits for one and reads its slot, so a
+host loop keeps the next step queued while it reads the previous token
+(``decode_tokens``): the GPU never waits for the host's read, and no copy runs
+between steps. At most two launches are outstanding and results are read in
+launch order, so a slot is rewritten only after its token was read.
 """
 
 from __future__ import annotations
+
+from collections import deque
 
 import torch
 
@@ -39,7 +50,7 @@ class GreedyDecodeGraph:
     """
 
     def __init__(self, model, cache, token, position_ids, *, fused_lm_head: bool = True,
-                 steps: int = 1) -> None:
+                 steps: int = 1, pipelined: bool = False) -> None:
         if not (isinstance(token, torch.Tensor) and token.is_cuda and token.dtype == torch.long
                 and token.shape[-1] == 1):
             raise ValueError("token must be an int64 GPU tensor whose last dimension is 1")
@@ -47,28 +58,41 @@ class GreedyDecodeGraph:
             raise ValueError("position_ids must be a GPU tensor")
         if int(steps) < 1:
             raise ValueError("steps must be at least 1")
+        if pipelined and (int(steps) != 1 or not fused_lm_head):
+            raise ValueError("pipelined decode needs one step per replay and the fused lm_head")
         self.model = model
         self.cache = cache
         self.fused_lm_head = bool(fused_lm_head)
         self.steps = int(steps)
+        self.pipelined = bool(pipelined)
         self._ring = torch.empty((self.steps, *token.shape), dtype=torch.long, device=token.device)
         self._ring[-1].copy_(token)
         self._positions = position_ids.clone()
         self.logits = None
+        self._host = ([torch.zeros(1, dtype=torch.long, pin_memory=True) for _ in range(2)]
+                      if self.pipelined else [None])
+        self._events = [torch.cuda.Event() for _ in self._host]
+        self._pending: deque[int] = deque()
+        self._next = 0
         prime_capture_state(token.device)
         torch.cuda.synchronize(token.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            for s in range(self.steps):
-                self._record_step(self._ring[s - 1], self._ring[s])
+        self._graphs = []
+        for host in self._host:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for s in range(self.steps):
+                    self._record_step(self._ring[s - 1], self._ring[s], host)
+            self._graphs.append(graph)
+        self.graph = self._graphs[0]
 
-    def _record_step(self, token_in: torch.Tensor, token_out: torch.Tensor) -> None:
+    def _record_step(self, token_in: torch.Tensor, token_out: torch.Tensor,
+                     host: torch.Tensor | None = None) -> None:
         model, positions = self.model, self._positions
         if self.fused_lm_head:
             state = model.model(input_ids=token_in, attention_mask=None, position_ids=positions,
                                 past_key_values=self.cache, use_cache=True, return_dict=True)
             last = state.last_hidden_state[:, -1, :].contiguous()
-            lm_head_argmax(last, model.lm_head.weight, out=token_out, advance=positions,
+            lm_head_argmax(last, model.lm_head.weight, out=token_out, mirror=host, advance=positions,
                            screen=lm_head_screen(model))
             return
         state = model(input_ids=token_in, attention_mask=None, position_ids=positions,
@@ -96,11 +120,64 @@ class GreedyDecodeGraph:
         """Start the next replay from ``token`` at ``position_ids``."""
         if tuple(token.shape) != tuple(self._ring.shape[1:]) or position_ids.shape != self._positions.shape:
             raise ValueError("graph input shapes do not match the captured buffers")
+        if self._pending:
+            raise RuntimeError("read the outstanding tokens (result) before setting new inputs")
         self._ring[-1].copy_(token)
         self._positions.copy_(position_ids)
 
     def replay(self) -> torch.Tensor:
         """Run the captured steps; the token ``[1, 1]`` (one step) or the
         ``[steps, 1, 1]`` tokens of this replay, in order."""
+        if self._pending:
+            raise RuntimeError("read the outstanding tokens (result) before a plain replay")
         self.graph.replay()
         return self._ring[0] if self.steps == 1 else self._ring
+
+    def launch(self) -> int:
+        """Queue one decode step (pipelined graphs) and return its slot; the
+        token is read with ``result(slot)``, in launch order. At most two
+        launches may be outstanding."""
+        if not self.pipelined:
+            raise RuntimeError("launch needs a pipelined GreedyDecodeGraph")
+        if len(self._pending) >= 2:
+            raise RuntimeError("read a token (result) before a third launch")
+        i = self._next
+        self._graphs[i].replay()
+        self._events[i].record()
+        self._pending.append(i)
+        self._next = 1 - i
+        return i
+
+    def result(self, slot: int) -> int:
+        """Wait for the oldest outstanding launch (``slot``) and return its
+        token, read from that capture's pinned host slot."""
+        if not self._pending or self._pending[0] != slot:
+            raise RuntimeError("results must be read in launch order")
+        self._events[slot].synchronize()
+        self._pending.popleft()
+        return int(self._host[slot][0])
+
+
+def decode_tokens(runner: GreedyDecodeGraph, count: int, eos_ids=()) -> list[int]:
+    """Up to ``count`` greedy tokens from a pipelined ``runner`` (inputs set):
+    the next step is queued before the previous token is read, and no step
+    past ``count`` is queued. After an EOS token the one step already queued
+    behind it is waited for (its token dropped), so the caller's clock covers
+    all the GPU work of the call."""
+    tokens: list[int] = []
+    launched = 0
+    pending: deque[int] = deque()
+    if count > 0:
+        pending.append(runner.launch())
+        launched = 1
+    while pending:
+        if launched < count:
+            pending.append(runner.launch())
+            launched += 1
+        token = runner.result(pending.popleft())
+        tokens.append(token)
+        if token in eos_ids:
+            break
+    while pending:
+        runner.result(pending.popleft())
+    return tokens

@@ -33,6 +33,8 @@ def _device_checked(fn):
     of them (inputs, weights, states, ``out``/``advance`` targets, positions)
     must be GPU tensors on one device; a CPU tensor would otherwise become a
     host address inside a kernel. Raises ``ValueError`` before any launch.
+    The one exception is a ``mirror`` argument in host memory, which the
+    wrapper itself accepts only when it is pinned and device-mapped.
     """
 
     code = fn.__code__
@@ -50,6 +52,8 @@ def _device_checked(fn):
         for name, value in flat:
             if not isinstance(value, torch.Tensor):
                 continue
+            if name == "mirror" and not value.is_cuda:
+                continue  # checked by the wrapper (host_device_address)
             if not value.is_cuda:
                 raise ValueError(f"fused kernels require GPU tensors: {name} is on {value.device}")
             if device is None:
@@ -598,6 +602,7 @@ def lm_head_argmax(
     block_n: int = 16,
     block_k: int = 128,
     out: torch.Tensor | None = None,
+    mirror: torch.Tensor | None = None,
     advance: torch.Tensor | None = None,
     screen: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     return_candidates: bool = False,
@@ -605,7 +610,10 @@ def lm_head_argmax(
     """Greedy token id without materialising logits. reference kernels.py:1146.
 
     ``out`` (int64, one element) receives the token instead of a new tensor;
-    ``advance`` (an int64 tensor, e.g. the decode position ids) is incremented
+    ``mirror`` (int64, one element: a GPU tensor or pinned host memory) also
+    receives it from the same launch, so a host loop can read the token of a
+    captured step without a copy after it; ``advance`` (an int64 tensor, e.g.
+    the decode position ids) is incremented
     by one in the same launch — the token feedback and ``position_ids += 1`` of
     reference graph.py:78-79 without extra kernels. ``screen`` (the tensors
     ``lm_head_screen_prep`` made from this ``weight``) finds the same index
@@ -647,12 +655,22 @@ def lm_head_argmax(
         if advance.dtype != torch.int64 or not advance.is_contiguous() or advance.numel() > 64:
             raise ValueError("advance must be a contiguous int64 tensor of at most 64 elements")
         n_adv = advance.numel()
+    mirror_at = None
+    if mirror is not None:
+        if mirror.numel() != 1 or mirror.dtype != torch.int64 or not mirror.is_contiguous():
+            raise ValueError("mirror must be a contiguous one-element int64 tensor")
+        if mirror.is_cuda:
+            if mirror.device != hidden.device:
+                raise ValueError("mirror must be on the hidden vector's GPU or in pinned host memory")
+            mirror_at = mirror.data_ptr()
+        else:
+            mirror_at = host_device_address(mirror)
     if return_candidates and screen is None:
         raise ValueError("return_candidates needs the screened top-1")
     if screen is not None:
         _lib.call("q35_lm_head_top1_screened", weight.data_ptr(), wq.data_ptr(), sw.data_ptr(),
                   cr.data_ptr(), hidden.data_ptr(), vocab, k, workspace.data_ptr(), nbytes,
-                  output.data_ptr(), _lib.ptr(advance), n_adv, _stream(hidden))
+                  output.data_ptr(), mirror_at, _lib.ptr(advance), n_adv, _stream(hidden))
         if return_candidates:
             import ctypes
 
@@ -662,9 +680,24 @@ def lm_head_argmax(
             return output, counts.to(torch.int64).sum()
     else:
         _lib.call("q35_lm_head_top1", weight.data_ptr(), hidden.data_ptr(), vocab, k,
-                  workspace.data_ptr(), slots, output.data_ptr(), _lib.ptr(advance), n_adv,
-                  _stream(hidden))
+                  workspace.data_ptr(), slots, output.data_ptr(), mirror_at, _lib.ptr(advance),
+                  n_adv, _stream(hidden))
     return output
+
+
+def host_device_address(t: torch.Tensor) -> int:
+    """The address a kernel stores to in order to reach the pinned host
+    tensor ``t`` (memory from ``pin_memory``); raises ValueError for pageable
+    host memory or anything else the device cannot address."""
+
+    import ctypes
+
+    if t.is_cuda:
+        raise ValueError("host_device_address takes a host tensor")
+    dev = ctypes.c_void_p(0)
+    if t.numel() == 0 or _lib.load().q35_host_device_ptr(ctypes.c_void_p(t.data_ptr()), ctypes.byref(dev)) != 0:
+        raise ValueError("the tensor is not in pinned, device-mapped host memory")
+    return int(dev.value)
 
 
 @_device_checked

@@ -236,6 +236,67 @@ def test_graph_multistep_equals_single_steps(gpu):
     assert len(s1) == len(s4) and all(torch.equal(a, b) for a, b in zip(s1, s4))
 
 
+def test_pipelined_graph_equals_single_steps(gpu):
+    """The pipelined decode loop (two captures alternating, the token read from
+    pinned host memory the top-1 launch writes, the next step queued before the
+    previous token is read) gives the tokens, the position and the cache state
+    of plain one-step replays; an EOS stops it after that token with nothing
+    left outstanding; misuse is refused before any launch."""
+    from ppu_amd.graph import GreedyDecodeGraph, decode_tokens
+    from ppu_amd.integration import apply_fusions
+    from ppu_amd.kernels import lm_head_argmax
+
+    cfg = synth.config_tiny()
+    model = synth.build_model(cfg, device=gpu)
+    apply_fusions(model)
+    prompt = synth.prompt_ids(45, cfg.vocab_size, seed=synth.MODEL_SEED + 5).to(gpu)
+    start = torch.full((1, 1), 45, device=gpu, dtype=torch.long)
+    results = {}
+    with torch.inference_mode():
+        def restart(runner, cache):
+            cache.reset()
+            pos = torch.arange(45, device=gpu).view(1, -1)
+            out = model.model(input_ids=prompt, position_ids=pos, past_key_values=cache, use_cache=True)
+            tok = lm_head_argmax(out.last_hidden_state[:, -1].contiguous(), model.lm_head.weight)
+            runner.set_inputs(tok, start)
+
+        for pipelined in (False, True):
+            cache, tok = _prefilled(model, cfg, gpu, prompt)
+            runner = GreedyDecodeGraph(model, cache, tok, start, pipelined=pipelined)
+            restart(runner, cache)
+            if pipelined:
+                tokens = decode_tokens(runner, 9)
+            else:
+                tokens = [int(runner.replay()) for _ in range(9)]
+            torch.cuda.synchronize()
+            results[pipelined] = (tokens, int(runner.position_ids), _state_tensors(cache))
+        (t0, p0, s0), (t1, p1, s1) = results[False], results[True]
+        assert t0 == t1 and len(t1) == 9
+        assert p0 == p1 == 45 + 9
+        assert len(s0) == len(s1) and all(torch.equal(a, b) for a, b in zip(s0, s1))
+
+        # an EOS at the fourth token: four tokens back, the queued fifth step drained
+        restart(runner, cache)
+        assert decode_tokens(runner, 9, eos_ids={t0[3]}) == t0[: t0.index(t0[3]) + 1]
+        assert int(runner.position_ids) == 45 + t0.index(t0[3]) + 2
+        # misuse: a third launch, an out-of-order read, new inputs or a plain
+        # replay while launches are outstanding
+        restart(runner, cache)
+        a = runner.launch()
+        b = runner.launch()
+        with pytest.raises(RuntimeError):
+            runner.launch()
+        with pytest.raises(RuntimeError):
+            runner.result(b)
+        with pytest.raises(RuntimeError):
+            runner.set_inputs(t0[0] * torch.ones((1, 1), device=gpu, dtype=torch.long), start)
+        with pytest.raises(RuntimeError):
+            runner.replay()
+        assert [runner.result(a), runner.result(b)] == t0[:2]
+        with pytest.raises(ValueError):
+            GreedyDecodeGraph(model, cache, tok, start, pipelined=True, steps=2)
+
+
 def test_wrappers_reject_wrong_device_before_launch(gpu):
     """A CPU ``out``/``advance``/``positions`` tensor, or mis-shaped state,
     raises ValueError on the host (no kernel sees a host address)."""

@@ -152,6 +152,32 @@ def test_attention_gate_mul_advance(gpu, tokens, hidden, head_dim):
         K.attention_gate_mul(x, packed, head_dim, advance=counter.to(torch.int32), amount=1)
 
 
+@pytest.mark.parametrize("screened", [False, True])
+def test_lm_head_top1_mirror(gpu, screened):
+    """The top-1 launch also stores the token into a mirror: pinned host
+    memory (through its device address) or a second GPU tensor; pageable host
+    memory is refused before any launch."""
+    from ppu_amd import kernels as K
+
+    g = torch.Generator(device=gpu).manual_seed(KERNEL_SEED + 63)
+    v = 50000
+    w = (torch.randn(v, 2048, device=gpu, generator=g) * 0.02).to(BF)
+    h = torch.randn(1, 2048, device=gpu, generator=g).to(BF)
+    screen = K.lm_head_screen_prep(w) if screened else None
+    plain = int(K.lm_head_argmax(h, w, screen=screen))
+    host = torch.full((1,), -1, dtype=torch.int64, pin_memory=True)
+    dev2 = torch.full((1, 1), -1, device=gpu, dtype=torch.int64)
+    out = torch.full((1, 1), -1, device=gpu, dtype=torch.int64)
+    K.lm_head_argmax(h, w, out=out, mirror=host, screen=screen)
+    K.lm_head_argmax(h, w, mirror=dev2, screen=screen)
+    torch.cuda.synchronize()
+    assert int(out) == int(host[0]) == int(dev2) == plain
+    with pytest.raises(ValueError):
+        K.lm_head_argmax(h, w, mirror=torch.zeros(1, dtype=torch.int64), screen=screen)
+    with pytest.raises(ValueError):
+        K.host_device_address(torch.zeros(1, dtype=torch.int64))
+
+
 def test_zero_tensors_many(gpu):
     """zero_tensors over 300 buffers (three launches of at most 128): every
     buffer is cleared, odd byte counts and empty ones included, and the bytes
@@ -345,7 +371,7 @@ def test_lm_head_screen_bound_holds(gpu):
     ws = torch.empty(nbytes, device=gpu, dtype=torch.uint8)
     out = torch.empty(1, 1, device=gpu, dtype=torch.int64)
     _lib.call("q35_lm_head_top1_screened", w.data_ptr(), wq.data_ptr(), sw.data_ptr(), cr.data_ptr(),
-              h.data_ptr(), v, 2048, ws.data_ptr(), nbytes, out.data_ptr(), None, 0,
+              h.data_ptr(), v, 2048, ws.data_ptr(), nbytes, out.data_ptr(), None, None, 0,
               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     upper = ws[: v * 4].view(torch.float32).double().cpu()

@@ -29,7 +29,7 @@ def _call_both(lib, stream, W, h):
     adv_ws = torch.tensor([[7]], device=W.device, dtype=torch.int64)
     adv_na = adv_ws.clone()
     _lib.check(lib.q35_lm_head_top1(W.data_ptr(), h.data_ptr(), V, K, ws.data_ptr(), slots,
-                                    out_ws.data_ptr(), adv_ws.data_ptr(), 1, stream),
+                                    out_ws.data_ptr(), None, adv_ws.data_ptr(), 1, stream),
                "q35_lm_head_top1")
     _lib.check(lib.q35_lm_head_top1_noalloc(W.data_ptr(), h.data_ptr(), V, K, out_na.data_ptr(),
                                             adv_na.data_ptr(), 1, stream),
