@@ -516,8 +516,9 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(const GemvArgs a) {
 }
 
 // out[0] = the index of the largest candidate key; `mirror` (may be null)
-// receives the same index (a second destination the caller reads, e.g. the
-// device address of pinned host memory); every advance[i] += 1 after.
+// receives the same index with a system-scope store (a second destination
+// the caller reads, e.g. the device address of pinned host memory that a
+// host loop polls); every advance[i] += 1 after.
 __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __restrict__ cand,
                                                    int n, long long* out, long long* mirror,
                                                    long long* advance, int n_advance) {
@@ -533,7 +534,9 @@ __global__ __launch_bounds__(1024) void top1_final(const unsigned long long* __r
     for (int i = 1; i < 16; ++i) m = u64_max(m, s[i]);
     const long long token = (long long)top1_index(m);
     out[0] = token;
-    if (mirror) mirror[0] = token;
+    // system scope: the store is written through to memory, so a host that
+    // polls a pinned mirror sees it without a release after the kernel
+    if (mirror) __hip_atomic_store(mirror, token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     for (int i = 0; i < n_advance; ++i) advance[i] += 1;
   }
 }

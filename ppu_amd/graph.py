@@ -21,16 +21,19 @@ length) lives in device memory, so ``replay`` is one graph launch.
 
 With ``pipelined`` (one step per replay, fused lm_head) the step is captured
 twice, and capture ``i``'s top-1 launch also stores the token into pinned host
-slot ``i`` (``lm_head_argmax(..., mirror=)``). ``launch`` replays the two
-captures alternately and ``result`` waits for one and reads its slot, so a
+slot ``i`` (``lm_head_argmax(..., mirror=)``, a store written through to
+memory). ``launch`` sets the slot to -1 and replays the two captures
+alternately; ``result`` polls the slot until the token replaces the -1, so a
 host loop keeps the next step queued while it reads the previous token
-(``decode_tokens``): the GPU never waits for the host's read, and no copy runs
-between steps. At most two launches are outstanding and results are read in
+(``decode_tokens``): the GPU never waits for the host's read, and nothing runs
+on the stream between steps (an event recorded after each replay cost 5 µs
+per step). At most two launches are outstanding and results are read in
 launch order, so a slot is rewritten only after its token was read.
 """
 
 from __future__ import annotations
 
+import time
 from collections import deque
 
 import torch
@@ -71,7 +74,8 @@ class GreedyDecodeGraph:
         self.logits = None
         self._host = ([torch.zeros(1, dtype=torch.long, pin_memory=True) for _ in range(2)]
                       if self.pipelined else [None])
-        self._events = [torch.cuda.Event() for _ in self._host]
+        self._host_view = [None if t is None else t.numpy() for t in self._host]
+        self._streams = [None for _ in self._host]
         self._pending: deque[int] = deque()
         self._next = 0
         prime_capture_state(token.device)
@@ -142,20 +146,33 @@ class GreedyDecodeGraph:
         if len(self._pending) >= 2:
             raise RuntimeError("read a token (result) before a third launch")
         i = self._next
+        self._host_view[i][0] = -1  # token ids are >= 0: -1 marks "not written yet"
+        self._streams[i] = torch.cuda.current_stream()
         self._graphs[i].replay()
-        self._events[i].record()
         self._pending.append(i)
         self._next = 1 - i
         return i
 
     def result(self, slot: int) -> int:
         """Wait for the oldest outstanding launch (``slot``) and return its
-        token, read from that capture's pinned host slot."""
+        token: polls that capture's pinned host slot. Should the stream run
+        dry with the slot still unwritten, raises RuntimeError instead of
+        waiting forever."""
         if not self._pending or self._pending[0] != slot:
             raise RuntimeError("results must be read in launch order")
-        self._events[slot].synchronize()
+        view, spins, since = self._host_view[slot], 0, None
+        while view[0] < 0:
+            spins += 1
+            if spins % 1024 == 0:
+                # a stream query is not free on the GPU side (it can put a
+                # marker in the queue): only after 20 ms of polling, far
+                # beyond a step's time, is the stream asked whether it ran dry
+                now = time.perf_counter()
+                since = now if since is None else since
+                if now - since > 0.02 and self._streams[slot].query() and view[0] < 0:
+                    raise RuntimeError("the decode step ended without its token reaching the host slot")
         self._pending.popleft()
-        return int(self._host[slot][0])
+        return int(view[0])
 
 
 def decode_tokens(runner: GreedyDecodeGraph, count: int, eos_ids=()) -> list[int]:
