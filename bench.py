@@ -1115,8 +1115,9 @@ def main() -> None:
             f"generate-loop decode {loop_tps:.1f} tok/s; first tokens {first.tokens[:8]}")
         # TTFT of prompt lengths this warmed process has not seen: the eager
         # prefill (the prefill graph of a length is captured after that
-        # call's first token, outside its timed region); median of 3 lengths.
-        fresh = [runner.generate(prompt[:, : PROMPT_LEN - 8 * (i + 1)], 2).ttft_seconds for i in range(3)]
+        # call's first token, outside its timed region); median of 5 lengths
+        # (the first also allocates the new bucket's cache)
+        fresh = [runner.generate(prompt[:, : PROMPT_LEN - 8 * (i + 1)], 2).ttft_seconds for i in range(5)]
         ttft_eager_ms = statistics.median(fresh) * 1e3
         log(f"[{variant}] TTFT of a first-seen prompt length (eager prefill): {ttft_eager_ms:.2f} ms")
         del runner
