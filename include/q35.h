@@ -345,6 +345,15 @@ int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, void
  * one workgroup per row: K a multiple of 8 and at most 8192, x 16-byte and xq
  * 8-byte aligned. Replaces the call at explore_runtime_quantization.py:167-172. */
 int q35_quant_act_i8(const void* x, void* xq, void* scale, int M, int K, void* stream);
+/* attention_gate_mul (qwen35_fused/kernels.py:312) followed by the per-token
+ * int8 quantisation of the o_proj input that the A8W8 linear applies
+ * (explore_runtime_quantization.py:167-172), in one launch: the same bits as
+ * q35_attn_gate_mul -> q35_quant_act_i8; the gated bf16 rows are never
+ * stored. hidden and head_dim multiples of 8, hidden <= 8192, packed_stride a
+ * multiple of 8; advance / amount as for q35_attn_gate_mul. */
+int q35_attn_gate_quant(const void* x, const void* packed, void* xq, void* scale, long long tokens,
+                        int hidden, int packed_stride, int head_dim, void* advance, long long amount,
+                        void* stream);
 /* y[M,N] = bf16(int32(xq . Wq) * s_x[m] * s_w[n]). With x (bf16) the per-token
  * quantisation is done here and xq/s_x receive it (fused into the GEMV launch
  * for M == 1 and for small M*K at K = 2048/6144, where they are optional);

@@ -48,25 +48,56 @@ __global__ __launch_bounds__(256) void quant_weight_rows(const uint16_t* __restr
   if (lane == 0) scale[n] = s;
 }
 
+// The attention output gate applied before the quantisation (GATE): the
+// row's values become bf16(x * bf16(sigmoid(gate))) with the gate of head h
+// at packed[token, h*2*head_dim + head_dim + c] (attn_gate_vec's arithmetic),
+// and block 0 adds `amount` to the int64 counter `advance` when given.
+struct GateIn {
+  const uint16_t* packed;
+  int stride, head_dim;
+  long long* advance;
+  long long amount;
+};
+
 // One workgroup per token row: 16-byte loads (PER groups of 8 per thread,
 // K <= PER * 2048), block absmax, then q = sat(rint(x * 127/absmax)) written
 // as 8-byte groups (K % 8 == 0).
-template <int PER>
+template <int PER, bool GATE = false>
 __global__ __launch_bounds__(256) void quant_act_rows(const uint16_t* __restrict__ x,
                                                       int8_t* __restrict__ xq,
-                                                      float* __restrict__ scale, int M, int K) {
+                                                      float* __restrict__ scale, int M, int K,
+                                                      const GateIn gt = GateIn{}) {
   const int m = blockIdx.x;
   const int tid = threadIdx.x;
   const uint16_t* row = x + (size_t)m * K;
   const int groups = K / 8;
   __shared__ float red[4];
+  if (GATE && gt.advance && m == 0 && tid == 0) gt.advance[0] += gt.amount;
+  if (m >= M) return;  // the advance-only launch (no rows): nothing is read
   float v[PER][8];
   float mx = 0.f;
+  uint4 graw[PER];
+  if (GATE) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int col = min(tid + j * 256, groups - 1) * 8;
+      const int head = col / gt.head_dim;
+      graw[j] = *reinterpret_cast<const uint4*>(gt.packed + (size_t)m * gt.stride +
+                                                (size_t)head * 2 * gt.head_dim + gt.head_dim +
+                                                (col - head * gt.head_dim));
+    }
+  }
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int gidx = tid + j * 256;
     const uint4 raw = *reinterpret_cast<const uint4*>(row + (size_t)min(gidx, groups - 1) * 8);
     unpack8(raw, v[j]);
+    if (GATE) {
+      float gv[8];
+      unpack8(graw[j], gv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = round_bf(v[j][e] * round_bf(sigmoid_f(gv[e])));
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx = gidx < groups ? fmaxf(mx, fabsf(v[j][e])) : mx;
   }
@@ -561,6 +592,40 @@ int q35_quant_weight_i8(const void* W, void* Wq, void* scale, int N, int K, hipS
   Q35_CHECK_ARG(N > 0 && K > 0 && W && Wq && scale);
   quant_weight_rows<<<(N + 3) / 4, 256, 0, stream>>>((const uint16_t*)W, (int8_t*)Wq,
                                                     (float*)scale, N, K);
+  return q35_last_error();
+}
+
+// attention_gate_mul then the per-token int8 quantisation in one launch; the
+// same bits as q35_attn_gate_mul -> q35_quant_act_i8, the gated bf16 rows
+// never stored. advance / amount as for q35_attn_gate_mul.
+int q35_attn_gate_quant(const void* x, const void* packed, void* xq, void* scale, long long tokens,
+                        int hidden, int packed_stride, int head_dim, void* advance, long long amount,
+                        hipStream_t stream) {
+  Q35_CHECK_ARG(tokens >= 0 && tokens < (1ll << 31) && hidden > 0 && hidden % 8 == 0 && hidden <= 8192);
+  Q35_CHECK_ARG(head_dim > 0 && head_dim % 8 == 0 && hidden % head_dim == 0);
+  Q35_CHECK_ARG(packed_stride >= 2 * hidden && packed_stride % 8 == 0);
+  Q35_CHECK_ARG(tokens == 0 || (x && packed && xq && scale));  // empty tensors may be null
+  Q35_CHECK_ARG(q35_aligned16(x) && q35_aligned16(packed) && q35_aligned8(xq));
+  if (tokens == 0 && (!advance || amount == 0)) return 0;
+  const GateIn gt{(const uint16_t*)packed, packed_stride, head_dim, (long long*)advance, amount};
+  const unsigned grid = (unsigned)(tokens > 0 ? tokens : 1);
+  const int M = (int)tokens;
+  const int per = (hidden / 8 + 255) / 256;
+  if (tokens == 0) {
+    // only the advance: one workgroup whose rows are all past the end
+    quant_act_rows<1, true><<<1, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale,
+                                                   0, hidden, GateIn{nullptr, 0, head_dim,
+                                                                     (long long*)advance, amount});
+    return q35_last_error();
+  }
+#define Q35_GQ(P)                                                                                  \
+  quant_act_rows<P, true><<<grid, 256, 0, stream>>>((const uint16_t*)x, (int8_t*)xq, (float*)scale, \
+                                                    M, hidden, gt)
+  if (per == 1) Q35_GQ(1);
+  else if (per == 2) Q35_GQ(2);
+  else if (per == 3) Q35_GQ(3);
+  else Q35_GQ(4);
+#undef Q35_GQ
   return q35_last_error();
 }
 

@@ -398,6 +398,12 @@ def _attention_prefill(attn, hidden: torch.Tensor, position_embeddings, cache,
         out = K.gqa_prefill_attention(q, k.contiguous(), v.contiguous(), attn.scaling,
                                       kv_start=kv_start, valid_length=valid,
                                       length_is_start=valid is not None)
+        hidden = out.shape[-1]
+        if (int32_out and attn.q35_o.int8 and hidden % 8 == 0 and attn.head_dim % 8 == 0
+                and hidden <= 8192 and packed.shape[-1] % 8 == 0):
+            # the gate and the o_proj input's quantisation in one launch
+            aq, sa = K.attention_gate_quant(out, packed, attn.head_dim, advance=valid, amount=length)
+            return K.a8w8_int_gemm(aq, attn.q35_o.w), sa
         out = K.attention_gate_mul(out, packed, attn.head_dim, advance=valid, amount=length)
     return attn.q35_o.to_int32(out) if int32_out else attn.q35_o(out)
 

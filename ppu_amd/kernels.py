@@ -1212,6 +1212,36 @@ def quantize_weight_i8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor
 
 
 @_device_checked
+def attention_gate_quant(x: torch.Tensor, packed_qgkv: torch.Tensor, head_dim: int, *,
+                         advance: torch.Tensor | None = None,
+                         amount: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """``quantize_act_i8(attention_gate_mul(x, packed_qgkv, head_dim))`` in
+    one launch (the same bits; the gated bf16 rows are never stored): the A8W8
+    o_proj input of reference kernels.py:312 + explore_runtime_quantization.py:167-172.
+    ``advance`` / ``amount`` as for ``attention_gate_mul``."""
+
+    hidden = x.shape[-1]
+    if not x.is_contiguous() or not packed_qgkv.is_contiguous():
+        raise ValueError("attention gate tensors must be contiguous")
+    if packed_qgkv.shape[:-1] != x.shape[:-1]:
+        raise ValueError("attention output and packed projection rows do not match")
+    if hidden % head_dim or hidden % 8 or head_dim % 8 or hidden > 8192 or packed_qgkv.shape[-1] < 2 * hidden \
+            or packed_qgkv.shape[-1] % 8:
+        raise ValueError("the fused gate + quantisation needs hidden, head_dim and the packed width "
+                         "multiples of 8 (hidden <= 8192) and the gate inside the packed row")
+    _need_bf16(x, packed_qgkv)
+    if advance is not None and (advance.dtype != torch.int64 or advance.numel() != 1):
+        raise ValueError("advance must be an int64 scalar tensor")
+    tokens = x.numel() // hidden
+    xq = torch.empty(x.shape, device=x.device, dtype=torch.int8)
+    scale = torch.empty((tokens, 1), device=x.device, dtype=torch.float32)
+    _lib.call("q35_attn_gate_quant", x.data_ptr(), packed_qgkv.data_ptr(), xq.data_ptr(),
+              scale.data_ptr(), tokens, hidden, packed_qgkv.shape[-1], head_dim, _lib.ptr(advance),
+              int(amount), _stream(x))
+    return xq, scale
+
+
+@_device_checked
 def quantize_act_i8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-token dynamic symmetric int8 activations and fp32 ``[M,1]`` scales
     (the scaled_int8_quant call of reference explore_runtime_quantization.py:167-172)."""

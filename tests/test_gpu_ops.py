@@ -178,6 +178,29 @@ def test_lm_head_top1_mirror(gpu, screened):
         K.host_device_address(torch.zeros(1, dtype=torch.int64))
 
 
+@pytest.mark.parametrize("tokens,hidden,head_dim", [(70, 2048, 256), (9, 4096, 128), (0, 2048, 256)])
+def test_attention_gate_quant_equals_gate_then_quant(gpu, tokens, hidden, head_dim):
+    """The gate + per-token quantisation launch gives the bits of the gate
+    kernel followed by the quantiser (int8 rows and scales), and advances the
+    counter once; all-zero gated rows keep the quantiser's zero rule."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 8)
+    packed = randn(g, 1, tokens, 2 * hidden + 16).to(gpu)
+    x = randn(g, 1, tokens, hidden).to(gpu)
+    if tokens:
+        x[0, 3] = 0.0  # a row whose gated values are all zero
+    counter = torch.tensor(5, dtype=torch.int64, device=gpu)
+    xq, sx = K.attention_gate_quant(x, packed, head_dim, advance=counter, amount=tokens + 1)
+    eq, es = K.quantize_act_i8(K.attention_gate_mul(x, packed, head_dim))
+    torch.cuda.synchronize()
+    assert int(counter) == 5 + tokens + 1
+    assert xq.shape == eq.shape and sx.shape == es.shape
+    assert torch.equal(xq, eq) and torch.equal(sx, es)
+    with pytest.raises(ValueError):
+        K.attention_gate_quant(x, packed, 12)
+
+
 def test_zero_tensors_many(gpu):
     """zero_tensors over 300 buffers (three launches of at most 128): every
     buffer is cleared, odd byte counts and empty ones included, and the bytes
