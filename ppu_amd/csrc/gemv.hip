@@ -970,7 +970,11 @@ __global__ __launch_bounds__(WV * 64) void lm_head_rescore(const uint16_t* __res
   }
 }
 
-constexpr int kScWV = 4, kScR = 2;
+// Screen: one workgroup of 8 waves per CU, 2 rows per group (the fastest of
+// 24 shapes of waves x rows x workgroups per CU over the 248320-row int8
+// copy: 75.5 us against 79.1 for two 4-wave workgroups per CU). Rescore: two
+// 4-wave workgroups per CU.
+constexpr int kScWV = 4, kScScreenWV = 8, kScR = 2;
 // Workspace of the screened top-1: U [V] floats, then per workgroup one
 // float (max lower bound), one 64-bit key and the number of rows it
 // recomputed (uint32), 256-byte aligned sections.
@@ -1226,12 +1230,13 @@ int q35_lm_head_top1_screened(const void* W, const void* Wq, const void* s, cons
   unsigned long long* cand =
       (unsigned long long*)((char*)workspace + align256((long long)V * 4) + align256(nb * 4));
   unsigned* ncand = (unsigned*)((char*)cand + align256(nb * 8));
-  lm_head_screen<kScWV, kScR, 2><<<(unsigned)nb, kScWV * 64, 0, stream>>>(
+  const long long nbs = lm_device_cus();  // screen workgroups (<= nb lower-bound slots)
+  lm_head_screen<kScScreenWV, kScR, 2><<<(unsigned)nbs, kScScreenWV * 64, 0, stream>>>(
       (const int8_t*)Wq, (const float*)s, (const float*)c, (const uint16_t*)x, V, U, lpart);
   int e = q35_last_error();
   if (e) return e;
   lm_head_rescore<kScWV><<<(unsigned)nb, kScWV * 64, 0, stream>>>(
-      (const uint16_t*)W, (const uint16_t*)x, U, lpart, (int)nb, V, cand, ncand);
+      (const uint16_t*)W, (const uint16_t*)x, U, lpart, (int)nbs, V, cand, ncand);
   e = q35_last_error();
   if (e) return e;
   top1_final<<<1, 1024, 0, stream>>>(cand, (int)nb, (long long*)out, (long long*)mirror,

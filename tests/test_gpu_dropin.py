@@ -275,6 +275,10 @@ def test_pipelined_graph_equals_single_steps(gpu):
         assert p0 == p1 == 45 + 9
         assert len(s0) == len(s1) and all(torch.equal(a, b) for a, b in zip(s0, s1))
 
+        # no step asked: nothing launched; one step: one token, nothing queued past it
+        restart(runner, cache)
+        assert decode_tokens(runner, 0) == [] and int(runner.position_ids) == 45
+        assert decode_tokens(runner, 1) == t0[:1] and int(runner.position_ids) == 46
         # an EOS at the fourth token: four tokens back, the queued fifth step drained
         restart(runner, cache)
         assert decode_tokens(runner, 9, eos_ids={t0[3]}) == t0[: t0.index(t0[3]) + 1]

@@ -401,8 +401,8 @@ def test_lm_head_screen_bound_holds(gpu):
     exact = (w.double() @ h.double().t()).reshape(-1).cpu()
     assert bool((upper >= exact + exact.abs() * 2.0**-8).all())
     # per-workgroup largest lower bounds follow U (256-byte aligned), one per
-    # workgroup of the persistent grid (2 per CU)
-    nb = 2 * torch.cuda.get_device_properties(gpu).multi_processor_count
+    # workgroup of the screen's persistent grid (1 per CU)
+    nb = torch.cuda.get_device_properties(gpu).multi_processor_count
     at = (v * 4 + 255) // 256 * 256
     lower_max = float(ws[at : at + 4 * nb].view(torch.float32).max())
     assert lower_max <= float(exact.max()) * (1 - 2.0**-8 * (1 if exact.max() > 0 else -1))
@@ -416,8 +416,9 @@ def test_lm_head_screen_bound_holds(gpu):
 
     n = ctypes.c_int(0)
     off = _lib.load().q35_lm_head_screened_counts(v, ctypes.byref(n))
-    assert n.value == nb and off + 4 * nb <= nbytes
-    counts = ws[off : off + 4 * nb].view(torch.int32).long().cpu()
+    nr = 2 * nb  # rescore workgroups (2 per CU) each count their rows
+    assert n.value == nr and off + 4 * nr <= nbytes
+    counts = ws[off : off + 4 * nr].view(torch.int32).long().cpu()
     assert int(counts.sum()) == int((upper >= lower_max).sum())
     _, total = K.lm_head_argmax(h, w, screen=(wq, sw, cr), return_candidates=True)
     assert int(total) == int(counts.sum())
