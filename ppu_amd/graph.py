@@ -78,6 +78,7 @@ class GreedyDecodeGraph:
         self._streams = [None for _ in self._host]
         self._pending: deque[int] = deque()
         self._next = 0
+        self._plain_unsynced = False  # a plain replay's mirror store may still be in flight
         prime_capture_state(token.device)
         torch.cuda.synchronize(token.device)
         self._graphs = []
@@ -135,6 +136,7 @@ class GreedyDecodeGraph:
         if self._pending:
             raise RuntimeError("read the outstanding tokens (result) before a plain replay")
         self.graph.replay()
+        self._plain_unsynced = self.pipelined
         return self._ring[0] if self.steps == 1 else self._ring
 
     def launch(self) -> int:
@@ -145,6 +147,11 @@ class GreedyDecodeGraph:
             raise RuntimeError("launch needs a pipelined GreedyDecodeGraph")
         if len(self._pending) >= 2:
             raise RuntimeError("read a token (result) before a third launch")
+        if self._plain_unsynced:
+            # capture 0 also stores into host slot 0: let a plain replay's
+            # store land before the slot is reset
+            torch.cuda.current_stream().synchronize()
+            self._plain_unsynced = False
         i = self._next
         self._host_view[i][0] = -1  # token ids are >= 0: -1 marks "not written yet"
         self._streams[i] = torch.cuda.current_stream()

@@ -279,6 +279,11 @@ def test_pipelined_graph_equals_single_steps(gpu):
         restart(runner, cache)
         assert decode_tokens(runner, 0) == [] and int(runner.position_ids) == 45
         assert decode_tokens(runner, 1) == t0[:1] and int(runner.position_ids) == 46
+        # a plain replay (capture 0, whose top-1 also writes host slot 0), not
+        # waited for, then the pipelined loop: it continues with the next tokens
+        restart(runner, cache)
+        runner.replay()
+        assert decode_tokens(runner, 3) == t0[1:4]
         # an EOS at the fourth token: four tokens back, the queued fifth step drained
         restart(runner, cache)
         assert decode_tokens(runner, 9, eos_ids={t0[3]}) == t0[: t0.index(t0[3]) + 1]
