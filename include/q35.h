@@ -58,6 +58,15 @@ int q35_stream_read_round(const void* p, long long nbytes, void* out, long long 
 int q35_rmsnorm(const void* x, const void* w, int w_f32, void* y, int rows, int width, float eps,
                 void* stream);
 
+/* The prefill's embedding lookup and the first layer's input RMSNorm in one
+ * launch: r_out[r] = table[ids[r]] (ids int64, clamped to [0, table_rows) as
+ * the decode step's gather), y[r] = rms_norm(r_out[r]) with q35_rmsnorm's
+ * arithmetic. Replaces embed_tokens(input_ids) (qwen35_fused/integration.py:403)
+ * followed by the first layer's rms_norm (kernels.py:44). r_out may be null;
+ * widths 512, 1024, 2048, 4096. */
+int q35_embed_rmsnorm(const void* table, int table_rows, const void* ids, const void* w, int w_f32,
+                      void* r_out, void* y, int rows, int width, float eps, void* stream);
+
 /* residual_add_rms_norm: r' = bf16(residual + update); y = rms_norm(r').
  * Replaces qwen35_fused/kernels.py:85 (kernel :56-112). */
 int q35_residual_rmsnorm(const void* residual, const void* update, const void* w, int w_f32,

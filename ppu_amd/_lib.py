@@ -95,6 +95,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "q35_lm_head_top1_screened": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _L, _P, _P, _P, _I, _P]),
     "q35_host_device_ptr": (_I, [_P, _P]),
     "q35_attn_gate_quant": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _P, _L, _P]),
+    "q35_embed_rmsnorm": (_I, [_P, _I, _P, _P, _I, _P, _P, _I, _I, _F, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -85,22 +85,34 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const uint16_t* __restrict__
 // rmsnorm_rows for widths of NPER * 512: the row stays in registers between
 // the two passes (lane l holds elements 512*j + 8*l .. +7), and every load
 // (x, u, w) is issued before the reduction, so a row costs one round trip.
-template <bool RESIDUAL, int NPER>
+// GATHER (no RESIDUAL): x is a [table_rows, width] table and row r reads
+// table row ids[r] (clamped to [0, table_rows), as the decode GEMV's gather
+// does); the raw row is also stored to r_out (the embedding lookup that
+// starts the residual stream).
+template <bool RESIDUAL, int NPER, bool GATHER = false>
 __global__ __launch_bounds__(256) void rmsnorm_rows_reg(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ u,
                                                         const void* __restrict__ w, int w_f32,
                                                         uint16_t* __restrict__ r_out,
-                                                        uint16_t* __restrict__ y, int rows, float eps) {
+                                                        uint16_t* __restrict__ y, int rows, float eps,
+                                                        const long long* __restrict__ ids = nullptr,
+                                                        int table_rows = 0) {
   constexpr int width = NPER * 512;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
   const size_t base = (size_t)row * width;
+  size_t xbase = base;
+  if (GATHER) {
+    long long r = ids[row];
+    r = r < 0 ? 0 : (r >= table_rows ? table_rows - 1 : r);
+    xbase = (size_t)r * width;
+  }
   uint4 xa[NPER], ua[NPER], wa[NPER], wb[NPER];
 #pragma unroll
   for (int j = 0; j < NPER; ++j) {
     const int k = j * 512 + lane * 8;
-    xa[j] = *reinterpret_cast<const uint4*>(x + base + k);
+    xa[j] = *reinterpret_cast<const uint4*>(x + xbase + k);
     if (RESIDUAL) ua[j] = *reinterpret_cast<const uint4*>(u + base + k);
     if (w_f32) {
       wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + k);
@@ -108,6 +120,10 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_reg(const uint16_t* __restri
     } else {
       wa[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + k);
     }
+  }
+  if (GATHER && r_out) {
+#pragma unroll
+    for (int j = 0; j < NPER; ++j) *reinterpret_cast<uint4*>(r_out + base + j * 512 + lane * 8) = xa[j];
   }
   float a[NPER][8];
   float ss = 0.f;
@@ -368,6 +384,29 @@ int q35_rmsnorm(const void* x, const void* w, int w_f32, void* y, int rows, int 
   }
   rmsnorm_rows<false><<<grid, 256, 0, stream>>>((const uint16_t*)x, nullptr, w, w_f32, nullptr,
                                                 (uint16_t*)y, rows, width, eps, vec);
+  return q35_last_error();
+}
+
+// The embedding lookup of the prefill and the first layer's input RMSNorm
+// in one launch: r_out[r] = table[clamp(ids[r])], y[r] = rms_norm(r_out[r]),
+// the bits of a gather followed by q35_rmsnorm. Widths 512, 1024, 2048, 4096.
+int q35_embed_rmsnorm(const void* table, int table_rows, const void* ids, const void* w, int w_f32,
+                      void* r_out, void* y, int rows, int width, float eps, hipStream_t stream) {
+  Q35_CHECK_ARG(rows >= 0 && table_rows > 0 && table && w && y && (rows == 0 || ids));
+  Q35_CHECK_ARG(width == 512 || width == 1024 || width == 2048 || width == 4096);
+  Q35_CHECK_ARG(q35_aligned16(table) && q35_aligned16(y) && q35_aligned16(w) && q35_aligned16(r_out) &&
+                q35_aligned8(ids));
+  if (rows == 0) return 0;
+  const int grid = (rows + kWaves - 1) / kWaves;
+#define Q35_ERMS(NP)                                                                              \
+  rmsnorm_rows_reg<false, NP, true><<<grid, 256, 0, stream>>>(                                     \
+      (const uint16_t*)table, nullptr, w, w_f32, (uint16_t*)r_out, (uint16_t*)y, rows, eps,       \
+      (const long long*)ids, table_rows)
+  if (width == 512) Q35_ERMS(1);
+  else if (width == 1024) Q35_ERMS(2);
+  else if (width == 2048) Q35_ERMS(4);
+  else Q35_ERMS(8);
+#undef Q35_ERMS
   return q35_last_error();
 }
 

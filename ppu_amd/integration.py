@@ -637,13 +637,19 @@ def _text_fast(stack, config: FusionConfig):
                 residual, update = decode_layer(stack, i, residual, update, ctx, token)
             _, hidden = K.residual_add_rms_norm(residual, update, stack.norm.weight, stack.norm.eps)
         else:
-            embeds = inputs_embeds if inputs_embeds is not None else stack.embed_tokens(input_ids)
+            ln0 = stack.layers[0].input_layernorm
+            table = stack.embed_tokens.weight
+            if (inputs_embeds is None and table.shape[1] in (512, 1024, 2048, 4096)
+                    and table.is_contiguous() and input_ids.dtype == torch.int64):
+                # the embedding lookup and the first input norm in one launch
+                residual, hidden = K.embed_rms_norm(table, input_ids, ln0.weight, ln0.eps)
+            else:
+                embeds = inputs_embeds if inputs_embeds is not None else stack.embed_tokens(input_ids)
+                residual = embeds.contiguous()
+                hidden = K.rms_norm(residual, ln0.weight, ln0.eps)
             rope = kwargs.get("position_embeddings")  # (cos, sin) computed by the caller
             if rope is None:
-                rope = stack.rotary_emb(embeds, rope_pos)
-            residual = embeds.contiguous()
-            hidden = K.rms_norm(residual, stack.layers[0].input_layernorm.weight,
-                                stack.layers[0].input_layernorm.eps)
+                rope = stack.rotary_emb(residual, rope_pos)
             if _a8w8_prefill_ok(stack, config, length):
                 xq, sx = K.quantize_act_i8(hidden)
                 quant = (xq, sx)

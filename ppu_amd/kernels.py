@@ -110,6 +110,31 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
 
 
 @_device_checked
+def embed_rms_norm(table: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor,
+                   eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(table[ids], rms_norm(table[ids]))`` in one launch: the embedding
+    lookup (reference integration.py:403, ids clamped to the table as the
+    decode step's gather does) and the first layer's input norm (reference
+    kernels.py:44). ``table [V, D]`` bf16, ``ids`` int64 of any shape; returns
+    two ``[*ids.shape, D]`` bf16 tensors. D in 512, 1024, 2048, 4096."""
+
+    if table.ndim != 2 or not table.is_contiguous() or ids.dtype != torch.int64:
+        raise ValueError("embed_rms_norm takes a contiguous [V, D] table and int64 ids")
+    vocab, width = table.shape
+    if width not in (512, 1024, 2048, 4096) or weight.numel() != width:
+        raise ValueError("embed_rms_norm supports widths 512, 1024, 2048 and 4096 with a matching weight")
+    _need_bf16(table)
+    w, wf = _param(weight)
+    idx = ids.contiguous()
+    rows = idx.numel()
+    residual = torch.empty((*ids.shape, width), device=table.device, dtype=table.dtype)
+    normed = torch.empty_like(residual)
+    _lib.call("q35_embed_rmsnorm", table.data_ptr(), vocab, idx.data_ptr(), w.data_ptr(), wf,
+              residual.data_ptr(), normed.data_ptr(), rows, width, float(eps), _stream(table))
+    return residual, normed
+
+
+@_device_checked
 def residual_add_rms_norm(
     residual: torch.Tensor,
     update: torch.Tensor,

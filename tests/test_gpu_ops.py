@@ -178,6 +178,30 @@ def test_lm_head_top1_mirror(gpu, screened):
         K.host_device_address(torch.zeros(1, dtype=torch.int64))
 
 
+@pytest.mark.parametrize("width", [512, 2048, 4096])
+def test_embed_rms_norm_equals_gather_then_norm(gpu, width):
+    """The embedding lookup + first input norm launch gives the bits of the
+    table gather followed by rms_norm (ids of any shape, repeats included);
+    ids outside the table read its nearest end row, as the decode gather."""
+    from ppu_amd import kernels as K
+
+    g = gen(KERNEL_SEED + 9)
+    table = randn(g, 300, width).to(gpu)
+    w = randn(g, width, scale=0.02, mean=1.0).to(gpu)
+    ids = torch.randint(0, 300, (2, 37), generator=g).to(gpu)
+    ids[0, 5] = ids[1, 7]
+    res, y = K.embed_rms_norm(table, ids, w, 1e-6)
+    ref_res = table[ids]
+    torch.cuda.synchronize()
+    assert torch.equal(res, ref_res)
+    assert torch.equal(y, K.rms_norm(ref_res, w, 1e-6))
+    oob = torch.tensor([[-4, 300, 10**9]], device=gpu)
+    r2, _ = K.embed_rms_norm(table, oob, w)
+    assert torch.equal(r2[0], table[[0, 299, 299]])
+    with pytest.raises(ValueError):
+        K.embed_rms_norm(table[:, :100].contiguous(), ids, w[:100])
+
+
 @pytest.mark.parametrize("tokens,hidden,head_dim", [(70, 2048, 256), (9, 4096, 128), (0, 2048, 256)])
 def test_attention_gate_quant_equals_gate_then_quant(gpu, tokens, hidden, head_dim):
     """The gate + per-token quantisation launch gives the bits of the gate
